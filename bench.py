@@ -1,0 +1,256 @@
+#!/usr/bin/env python
+"""Headline benchmark: torch.ops.st.bloom_index_search_batch on one MI355X.
+
+Workload ("cfg2"): 10M docs, 8 features, per-doc
+value count uniform in [1, 4], values Zipf(1.1) over a 100k vocabulary, index
+built with K=3, B_MULTIPLIER=5.0; 256 flat AND/OR queries of 2-6 terms,
+HASH_K=7; packed int64 output.  A step is one full op call (plan compile on
+the host, plan upload, search kernel) with the index, bundle offsets and
+query plans resident in HBM.
+
+Prints ONE JSON line with the throughput (doc-queries/s), the roofline of
+the search kernel (algorithmic bytes per launch / kernel time from HIP
+events on the launching stream) and the reference's own CPU search timed on
+a bounded sample on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "bloom search doc-queries/sec at 10M docs; achieved HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "search_cfg2_traffic.json"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--config", default="cfg2")
+    p.add_argument("--bool-mask", action="store_true", help="bool output instead of packed")
+    p.add_argument("--cpu-queries", type=int, default=256,
+                   help="queries of the batch the reference CPU search is timed on")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+def cpu_baseline(index, bbo, queries, k, hash_k, num_docs, n_queries):
+    """Times the reference's CPU search (oracle/_ref, compiled from the
+    reference sources) in a child process; falls back to the C oracle."""
+    import numpy as np
+
+    ref_so = ROOT / "oracle" / "_ref" / "libst_ref.so"
+    sample = queries[:n_queries]
+    with tempfile.TemporaryDirectory() as td:
+        np.save(Path(td) / "index.npy", index)
+        np.save(Path(td) / "bbo.npy", bbo)
+        Path(td, "queries.json").write_text(json.dumps(sample))
+        if ref_so.exists():
+            kind = "reference"
+            code = f"""
+import json, time, numpy as np, torch
+torch.set_num_threads(1)
+torch.ops.load_library({str(ref_so)!r})
+st = torch.ops.st
+idx = torch.from_numpy(np.load({td!r} + '/index.npy'))
+bbo = torch.from_numpy(np.load({td!r} + '/bbo.npy'))
+qs = json.load(open({td!r} + '/queries.json'))
+_, (pd, po) = st.parse_expression_query_batch(qs, torch.ones(1, dtype=torch.long), {hash_k}, True, 5)
+st.bloom_index_search_batch(idx, bbo, pd[:0], po[:0], {k}, {hash_k}, False)
+t = time.perf_counter()
+st.bloom_index_search_batch(idx, bbo, pd, po, {k}, {hash_k}, False)
+print(json.dumps({{"seconds": time.perf_counter() - t}}))
+"""
+        else:
+            kind = "port"
+            code = f"""
+import json, sys, time, numpy as np
+sys.path.insert(0, {str(ROOT)!r})
+from oracle import oracle as O, parser_oracle as P
+idx = np.load({td!r} + '/index.npy'); bbo = np.load({td!r} + '/bbo.npy')
+qs = json.load(open({td!r} + '/queries.json'))
+_, data, offs = P.parse_batch(qs, {hash_k})
+t = time.perf_counter()
+O.search_packed(idx, bbo, np.frombuffer(data, np.int8), np.array(offs), {k}, {hash_k})
+print(json.dumps({{"seconds": time.perf_counter() - t}}))
+"""
+        env = dict(os.environ, OMP_NUM_THREADS="1")
+        out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=900)
+        if out.returncode != 0:
+            log("cpu baseline failed: " + out.stderr[-2000:])
+            return None
+        secs = json.loads(out.stdout.strip().splitlines()[-1])["seconds"]
+    return {
+        "value": len(sample) * num_docs / secs,
+        "unit": "doc-queries/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": f"{len(sample)} of the {len(queries)} queries over all {num_docs} docs, packed output, "
+                  f"{secs:.2f} s single-threaded ({'reference CPU op compiled from its sources' if kind == 'reference' else 'C oracle'})",
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import silvertorch_amd.ops._load_ops  # noqa: F401
+    from silvertorch_amd import capi
+    from silvertorch_amd import synthetic as S
+
+    st = torch.ops.st
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cspec, qspec = S.CONFIGS[args.config]
+    t0 = time.time()
+    corp = S.make_corpus(cspec, seed=0)
+    queries = S.make_queries(cspec, qspec, seed=0)
+    log(f"generated {args.config}: {cspec.num_docs} docs, {corp.feature_values.size} values, "
+        f"{len(queries)} queries in {time.time() - t0:.1f}s")
+
+    ids = torch.from_numpy(corp.feature_ids).to(dev)
+    offs = torch.from_numpy(corp.feature_offsets).to(dev)
+    vals = torch.from_numpy(corp.feature_values).to(dev)
+    bi, bo = st.bloom_index_build(ids, offs, vals, cspec.b_multiplier, cspec.k)  # warm
+    torch.cuda.synchronize()
+    tb = time.perf_counter()
+    bi, bo = st.bloom_index_build(ids, offs, vals, cspec.b_multiplier, cspec.k)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - tb
+    log(f"index built on GPU: {bi.numel() * 8 / 1e6:.1f} MB, {bo.numel() - 1} bundles, {build_s * 1e3:.2f} ms")
+    del ids, offs, vals
+
+    _, (pd, po) = st.parse_expression_query_batch(queries, torch.ones(1, dtype=torch.long), cspec.hash_k, True, 5)
+    pd_d, po_d = pd.to(dev), po.to(dev)
+    k, hk = cspec.k, cspec.hash_k
+    Q, N = len(queries), cspec.num_docs
+    nb = bo.numel() - 1
+
+    def step():
+        return st.bloom_index_search_batch(bi, bo, pd_d, po_d, k, hk, args.bool_mask)
+
+    for _ in range(args.warmup):
+        out = step()
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    ms_per_step = elapsed * 1e3 / args.steps
+    log(f"{args.steps} steps: {ms_per_step:.4f} ms/step")
+
+    # Sampled parity: a few bundles against the C oracle (the tests cover the rest).
+    from oracle import oracle as O
+
+    packed = out if not args.bool_mask else None
+    if packed is not None:
+        bbo_h = bo.cpu().numpy()
+        ok = True
+        for bnd in (0, nb // 3, nb - 1):
+            s, e = int(bbo_h[bnd]), int(bbo_h[bnd + 1])
+            want = O.search_packed(bi[s * 32:e * 32].cpu().numpy(), np.array([0, e - s], np.int64),
+                                   pd.numpy(), po.numpy(), k, hk)
+            ok &= bool(np.array_equal(packed[:, bnd * 32:(bnd + 1) * 32].cpu().numpy(), want))
+        log(f"sampled bundles bit-exact vs oracle: {ok}")
+        if not ok:
+            sys.exit("parity failure in sampled bundles")
+
+    # Kernel-only timing through the C ABI: HIP events recorded on the stream
+    # the search kernel is launched on, bracketing only the launch.
+    L = capi.lib()
+    plan = capi.SearchPlan(pd.numpy().tobytes(), po.numpy(), k, hk)
+    blob = torch.frombuffer(bytearray(plan.blob()), dtype=torch.uint8).to(dev)
+    kout = torch.empty_like(out)
+    stream = torch.cuda.current_stream()
+    reps = max(args.steps, 20)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    for i in range(reps + 3):
+        j = i - 3
+        if j >= 0:
+            starts[j].record(stream)
+        capi.check(L.st_bloom_index_search_batch(bi.data_ptr(), bi.numel(), bo.data_ptr(), nb, plan.handle,
+                                                 blob.data_ptr(), int(args.bool_mask), kout.data_ptr(),
+                                                 stream.cuda_stream))
+        if j >= 0:
+            ends[j].record(stream)
+    torch.cuda.synchronize()
+    kernel_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / reps
+    assert torch.equal(kout, out)
+
+    out_bytes = out.numel() * out.element_size()
+    alg_bytes = bi.numel() * 8 + bo.numel() * 8 + pd.numel() + po.numel() * 8 + out_bytes
+    achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        t = json.loads(TRAFFIC_FILE.read_text())
+        if t.get("config") == args.config and t.get("bool_mask", False) == args.bool_mask:
+            traffic = t.get("hbm_bytes_per_launch")
+    log(f"search kernel {kernel_ms * 1e3:.1f} us, {alg_bytes / 1e6:.1f} MB algorithmic, {achieved:.0f} GB/s")
+
+    baseline = None
+    if not args.no_cpu_baseline:
+        baseline = cpu_baseline(bi.cpu().numpy(), bo.cpu().numpy(), queries, k, hk, N, args.cpu_queries)
+
+    result = {
+        "metric": METRIC,
+        "value": Q * N / (ms_per_step * 1e-3),
+        "unit": "doc-queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int64",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.config}: bloom_index_search_batch, {N} docs x {Q} queries, "
+                        f"{'bool' if args.bool_mask else 'packed int64'} output",
+            "docs": N, "queries": Q, "features": cspec.num_features, "k": k, "hash_k": hk,
+            "b_multiplier": cspec.b_multiplier, "bundles": nb, "index_bytes": bi.numel() * 8,
+            "output_bytes": out_bytes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": traffic,
+            "kernel": "bloom_search_kernel",
+            "kernel_us": kernel_ms * 1e3,
+            "algorithmic_bytes": alg_bytes,
+        },
+        "cpu_baseline": baseline,
+        "build": {"ms": build_s * 1e3, "docs_per_s": N / build_s},
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,211 @@
+/*
+ * silvertorch_hip.h -- C ABI of the MI355X (gfx950) bloom-index retrieval path.
+ *
+ * Plain pointers and sizes only; no torch types.  Every device pointer is a
+ * HIP device allocation on the current device, and every `stream` argument is
+ * a hipStream_t passed as void* (NULL = the legacy default stream).  Work is
+ * enqueued on that stream and ordered with the caller's other work on it.
+ *
+ * Status convention: every function returning int returns 0 on success and a
+ * negative code on failure; st_last_error() then returns a message for the
+ * calling thread (valid until that thread's next call into this library).
+ *
+ * Reference interfaces replaced (paths relative to the reference tree
+ * silvertorch/ops/csrc/):
+ *   st::bloom_index_build             bloom_indexer.cpp:115-125 (schema),
+ *                                     bloom_indexer.cpp:26-113 (CPU impl),
+ *                                     bloom_indexer_cuda.cu:880-904 (CUDA impl)
+ *   st::bloom_index_search_batch      bloom_index_search.cpp:549-558 (schema),
+ *                                     bloom_index_search.cpp:378-395 (CPU impl),
+ *                                     bloom_index_search_cuda.cu:1031-1109 (CUDA)
+ *   st::parse_expression_query_batch  expression_query_parser.cpp:456-472
+ *   st::generate_column_info_for_clusters
+ *                                     bloom_index_search.cpp:489-540, :543-547
+ */
+#ifndef SILVERTORCH_HIP_H_
+#define SILVERTORCH_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ST_OK 0
+#define ST_ERR_INVALID_ARGUMENT (-1)
+#define ST_ERR_HIP (-2)
+#define ST_ERR_UNSUPPORTED (-3)
+
+/* Geometry of the bloom index (bloom_index_util.h:41-45 of the reference). */
+#define ST_BITS_PER_COLUMN 64
+#define ST_COLUMNS_PER_BUNDLE 32
+#define ST_DOCS_PER_BUNDLE 2048
+/* Largest number of distinct positions a search term may resolve
+ * (MAX_K_V2, bloom_index_util.h:45). */
+#define ST_MAX_SEARCH_K 10
+/* Largest k the build accepts (MAX_K, bloom_index_util.h:39). */
+#define ST_MAX_BUILD_K 64
+
+/* Message describing the last failure on the calling thread. */
+const char* st_last_error(void);
+
+/* Library version string. */
+const char* st_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Hash.  MurmurHash3_x64_128 of the 16-byte key LE(x)||LE(y) with both lanes
+ * seeded by `seed`, folded as h1 ^ h2.  Host-side twin of the device routine
+ * the kernels use; replaces murmur_hash3_2x64 (bloom_index_util.cuh:59-106).
+ * ------------------------------------------------------------------------- */
+uint64_t st_murmur_hash3_2x64(uint64_t x, uint64_t y, uint64_t seed);
+
+/* ---------------------------------------------------------------------------
+ * Build, step 1 of 2: per-bundle bloom widths.
+ *
+ * Replaces the width pass of bloom_index_build (bloom_indexer.cpp:43-70 and
+ * bloom_indexer_cuda.cu:253-389):
+ *   b_i = (int64)((double)(max_{doc in bundle i} terms(doc) * k) * b_multiplier)
+ *   bundle_b_offsets[0] = 0, bundle_b_offsets[i+1] = bundle_b_offsets[i] + b_i
+ *
+ *   feature_offsets   device int64[num_docs * num_features + 1]
+ *   bundle_b_offsets  device int64[ceil(num_docs / 2048) + 1]      (output)
+ *   stats             device int64[6]                              (output)
+ *                     stats[0] = total rows (bundle_b_offsets[last]),
+ *                     stats[1] = largest single-bundle width,
+ *                     stats[2] = 1 if feature_offsets ever decreases, else 0,
+ *                     stats[3] = feature_offsets[0],
+ *                     stats[4] = feature_offsets[num_docs * num_features],
+ *                     stats[5] = 0 (reserved).
+ * The caller must check stats[2] == 0 and 0 <= stats[3] <= stats[4] <=
+ * num_values before st_bloom_index_build; values outside [0, num_values) are
+ * never read.
+ * Requires num_features >= 1, num_docs >= 0, 0 <= k <= ST_MAX_BUILD_K and
+ * b_multiplier > 1.0.
+ * ------------------------------------------------------------------------- */
+int st_bloom_build_bundle_offsets(const int64_t* feature_offsets,
+                                  int64_t num_docs, int64_t num_features,
+                                  int64_t k, double b_multiplier,
+                                  int64_t* bundle_b_offsets, int64_t* stats,
+                                  void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Build, step 2 of 2: set the bloom bits.
+ *
+ * Replaces the scatter of bloom_index_build (bloom_indexer.cpp:72-110 and
+ * bloom_indexer_cuda.cu:137-251 / :506-711).  For every doc d, feature slot f
+ * and value v of that slot, the first k distinct murmur(feature_ids[f], v,
+ * seed = 0, 1, 2, ...) % b positions p set bit (63 - d % 64) of
+ *   bloom_index[(bundle_b_offsets[d / 2048] + p) * 32 + (d % 2048) / 64].
+ *
+ *   feature_ids       device int32[num_features]
+ *   feature_offsets   device int64[num_docs * num_features + 1]
+ *   feature_values    device int64[num_values]
+ *   bundle_b_offsets  device int64[nb + 1] from st_bloom_build_bundle_offsets
+ *   max_b             stats[1] of that call (host value)
+ *   bloom_index       device int64[bloom_index_numel] (output, fully written;
+ *                     bloom_index_numel must equal total rows * 32)
+ * ------------------------------------------------------------------------- */
+int st_bloom_index_build(const int32_t* feature_ids,
+                         const int64_t* feature_offsets,
+                         const int64_t* feature_values, int64_t num_features,
+                         int64_t num_docs, int64_t num_values, int64_t k,
+                         const int64_t* bundle_b_offsets, int64_t max_b,
+                         int64_t* bloom_index, int64_t bloom_index_numel,
+                         void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Search plan: a host-side compilation of a batch of encoded query plans
+ * (the plans_data / plans_offsets pair produced by
+ * st::parse_expression_query_batch; format of bloom_index_util.cpp:81-124)
+ * into the flat accumulator programs the search kernel runs.
+ *
+ * st_search_plan_create validates the plans exactly where the reference CPU
+ * search would fail or read out of bounds (bloom_index_search.cpp:72-171):
+ * unknown operators, NOT with a child count other than 1, stack underflow,
+ * empty programs and hash reads past the plan's hash array are errors.
+ *
+ *   plans_data     host int8[plans_data_len]
+ *   plans_offsets  host int64[plans_offsets_len], 8 per query
+ *   k, hash_k      as passed to bloom_index_search_batch
+ *
+ * The blob (st_search_plan_blob, st_search_plan_blob_bytes bytes) must be
+ * copied verbatim to device memory, which is then passed to
+ * st_bloom_index_search_batch together with the plan.
+ * ------------------------------------------------------------------------- */
+typedef struct st_search_plan st_search_plan;
+
+int st_search_plan_create(const int8_t* plans_data, int64_t plans_data_len,
+                          const int64_t* plans_offsets,
+                          int64_t plans_offsets_len, int64_t k, int64_t hash_k,
+                          st_search_plan** out);
+int64_t st_search_plan_num_queries(const st_search_plan* plan);
+int64_t st_search_plan_blob_bytes(const st_search_plan* plan);
+const void* st_search_plan_blob(const st_search_plan* plan);
+void st_search_plan_destroy(st_search_plan* plan);
+
+/* ---------------------------------------------------------------------------
+ * Batched boolean search.  Replaces bloom_index_search_batch
+ * (bloom_index_search.cpp:173-243, bloom_index_search_cuda.cu:575-615,
+ * :940-1029).  With C = num_bundles * 32 columns:
+ *   return_bool_mask == 0: out is device int64[Q, C], out[q, c] = the 64-bit
+ *                          match word of column c (doc 64c+i is bit 63-i);
+ *   return_bool_mask != 0: out is device bool (uint8)[Q, C * 64],
+ *                          out[q, 64c + i] = bit (63 - i) of that word.
+ * Docs past the real doc count are included, as in the reference.
+ *
+ *   bloom_index        device int64[bloom_index_numel]
+ *   bundle_b_offsets   device int64[num_bundles + 1]
+ *   plan_blob_device   device copy of st_search_plan_blob(plan)
+ * ------------------------------------------------------------------------- */
+int st_bloom_index_search_batch(const int64_t* bloom_index,
+                                int64_t bloom_index_numel,
+                                const int64_t* bundle_b_offsets,
+                                int64_t num_bundles,
+                                const st_search_plan* plan,
+                                const void* plan_blob_device,
+                                int return_bool_mask, void* out,
+                                void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Expression parser (host).  Replaces parse_expression_query_batch
+ * (expression_query_parser.cpp:30-430): grammar of EXPRESSION_SYNTAX.md,
+ * precedence NOT > AND > OR, runs of more than max_sub_queries operands
+ * folded into nested operators, every term carrying hash_k murmur hashes
+ * (seeds 0..hash_k-1), "" compiling to a single EMPTY operator.  The encoded
+ * bytes are identical to the reference's.
+ * ------------------------------------------------------------------------- */
+typedef struct st_parsed_plans st_parsed_plans;
+
+int st_parse_expression_query_batch(const char* const* expressions,
+                                    int64_t num_expressions, int64_t hash_k,
+                                    int return_query_plan,
+                                    int64_t max_sub_queries,
+                                    st_parsed_plans** out);
+int64_t st_parsed_plans_max_stack(const st_parsed_plans* plans);
+int64_t st_parsed_plans_data_bytes(const st_parsed_plans* plans);
+const int8_t* st_parsed_plans_data(const st_parsed_plans* plans);
+int64_t st_parsed_plans_offsets_len(const st_parsed_plans* plans);
+const int64_t* st_parsed_plans_offsets(const st_parsed_plans* plans);
+void st_parsed_plans_destroy(st_parsed_plans* plans);
+
+/* ---------------------------------------------------------------------------
+ * Cluster column geometry (companion op of the same operator surface).
+ * Replaces generate_column_info_for_clusters (bloom_index_search.cpp:489-540,
+ * bloom_index_search_cuda.cu:617-645).  For cluster i with first doc
+ * offsets[i] and length lengths[i]:
+ *   start_columns[i] = offsets[i] / 64, first_offsets[i] = offsets[i] % 64,
+ *   column_counts[i] = lengths[i] > 0
+ *       ? (lengths[i] + first_offsets[i] + 63) / 64 : 0.
+ * All pointers are device pointers; n entries each.
+ * ------------------------------------------------------------------------- */
+int st_generate_column_info_for_clusters(const int64_t* offsets,
+                                         const int64_t* lengths, int64_t n,
+                                         int32_t* column_counts,
+                                         int32_t* start_columns,
+                                         int8_t* first_offsets, void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* SILVERTORCH_HIP_H_ */

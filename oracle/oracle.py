@@ -1,0 +1,158 @@
+"""ctypes front end of the C oracle (bloom_oracle.c) -- TEST INFRASTRUCTURE ONLY.
+
+Each wrapper names the reference code it restates; see bloom_oracle.c for the
+full citation list and for how each function is pinned.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "_build" / "liboracle.so"
+
+_lib = None
+
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE), "all"], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.or_murmur3_pair.restype = ctypes.c_uint64
+        L.or_murmur3_pair.argtypes = [ctypes.c_uint64] * 3
+        L.or_build_positions.restype = ctypes.c_int
+        L.or_build_positions.argtypes = [ctypes.c_int64] * 4 + [ctypes.POINTER(ctypes.c_int32)]
+        L.or_bundle_b_offsets.restype = None
+        L.or_bundle_b_offsets.argtypes = [_i64p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_double, _i64p]
+        L.or_bloom_build.restype = ctypes.c_int
+        L.or_bloom_build.argtypes = [ctypes.POINTER(ctypes.c_int32), _i64p, _i64p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _i64p, _i64p]
+        L.or_search_batch.restype = ctypes.c_int
+        L.or_search_batch.argtypes = [_i64p, ctypes.c_int64, _i64p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int8), ctypes.c_int64, _i64p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _i64p]
+        L.or_unpack_bool.restype = None
+        L.or_unpack_bool.argtypes = [_i64p, ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(ctypes.c_uint8)]
+        L.or_compact.restype = None
+        L.or_compact.argtypes = [_i64p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _i64p, _i64p]
+        L.or_filtered_topk.restype = ctypes.c_int
+        L.or_filtered_topk.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(ctypes.c_float), ctypes.c_int64, _i64p, ctypes.c_int64, ctypes.c_int64, _i64p, ctypes.POINTER(ctypes.c_float)]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray, ct):
+    return a.ctypes.data_as(ctypes.POINTER(ct))
+
+
+def murmur3_pair(x: int, y: int, seed: int) -> int:
+    """murmur_hash3_2x64 (bloom_index_util.cuh:59-106)."""
+    m = (1 << 64) - 1
+    return int(lib().or_murmur3_pair(x & m, y & m, seed & m))
+
+
+def build_positions(fid: int, value: int, b: int, k: int) -> list[int]:
+    """assign_one_bits_position (bloom_index_util.cuh:183-207)."""
+    out = np.zeros(max(k, 1), dtype=np.int32)
+    rc = lib().or_build_positions(fid, value, b, k, _p(out, ctypes.c_int32))
+    if rc != 0:
+        raise ValueError("no k distinct positions exist for this b")
+    return out[:k].tolist()
+
+
+def bundle_b_offsets(offsets: np.ndarray, num_features: int, k: int, b_multiplier: float) -> np.ndarray:
+    """Per-bundle width pass (bloom_indexer.cpp:43-70)."""
+    offsets = np.ascontiguousarray(offsets, dtype=np.int64)
+    n = (offsets.size - 1) // num_features
+    nb = (n + 2047) // 2048
+    out = np.zeros(nb + 1, dtype=np.int64)
+    lib().or_bundle_b_offsets(_p(offsets, ctypes.c_int64), n, num_features, k, b_multiplier, _p(out, ctypes.c_int64))
+    return out
+
+
+def bloom_build(feature_ids, offsets, values, b_multiplier: float, k: int):
+    """bloom_index_build_cpu (bloom_indexer.cpp:26-113) -> (index, bundle_b_offsets)."""
+    ids = np.ascontiguousarray(feature_ids, dtype=np.int32)
+    offsets = np.ascontiguousarray(offsets, dtype=np.int64)
+    values = np.ascontiguousarray(values, dtype=np.int64)
+    F = ids.size
+    n = (offsets.size - 1) // F
+    bbo = bundle_b_offsets(offsets, F, k, b_multiplier)
+    index = np.zeros(max(int(bbo[-1]) * 32, 1), dtype=np.int64)
+    if values.size == 0:
+        values = np.zeros(1, dtype=np.int64)
+    rc = lib().or_bloom_build(_p(ids, ctypes.c_int32), _p(offsets, ctypes.c_int64), _p(values, ctypes.c_int64),
+                              F, n, k, _p(bbo, ctypes.c_int64), _p(index, ctypes.c_int64))
+    if rc != 0:
+        raise ValueError("oracle build rejected its arguments")
+    return index[: int(bbo[-1]) * 32], bbo
+
+
+def search_packed(index, bbo, plans_data, plans_offsets, k: int, hash_k: int) -> np.ndarray:
+    """bloom_index_search_batch_cpu with return_bool_mask=False
+    (bloom_index_search.cpp:27-243) -> int64[Q, nb*32]."""
+    index = np.ascontiguousarray(index, dtype=np.int64)
+    bbo = np.ascontiguousarray(bbo, dtype=np.int64)
+    pdata = np.ascontiguousarray(plans_data, dtype=np.int8)
+    poffs = np.ascontiguousarray(plans_offsets, dtype=np.int64)
+    q = poffs.size // 8
+    nb = bbo.size - 1
+    out = np.zeros((q, nb * 32), dtype=np.int64)
+    idx = index if index.size else np.zeros(1, dtype=np.int64)
+    pd = pdata if pdata.size else np.zeros(1, dtype=np.int8)
+    po = poffs if poffs.size else np.zeros(1, dtype=np.int64)
+    rc = lib().or_search_batch(_p(idx, ctypes.c_int64), index.size, _p(bbo, ctypes.c_int64), nb,
+                               _p(pd, ctypes.c_int8), pdata.size, _p(po, ctypes.c_int64), q, k, hash_k,
+                               _p(out, ctypes.c_int64))
+    if rc != 0:
+        raise ValueError(f"oracle search rejected plan {-rc - 1}")
+    return out
+
+
+def unpack_bool(packed: np.ndarray) -> np.ndarray:
+    """bool mask layout of bloom_index_search.cpp:231-236."""
+    packed = np.ascontiguousarray(packed, dtype=np.int64)
+    rows, cols = packed.shape
+    out = np.zeros((rows, cols * 64), dtype=np.uint8)
+    if packed.size:
+        lib().or_unpack_bool(_p(packed, ctypes.c_int64), rows, cols, _p(out, ctypes.c_uint8))
+    return out.astype(bool)
+
+
+def compact(packed: np.ndarray, num_docs: int):
+    """Matching ids below num_docs per query (README.md:191) -> (ids, row_offsets)."""
+    packed = np.ascontiguousarray(packed, dtype=np.int64)
+    rows, cols = packed.shape
+    ro = np.zeros(rows + 1, dtype=np.int64)
+    src = packed if packed.size else np.zeros(1, dtype=np.int64)
+    lib().or_compact(_p(src, ctypes.c_int64), rows, cols, num_docs, _p(ro, ctypes.c_int64), None)
+    ids = np.zeros(max(int(ro[-1]), 1), dtype=np.int64)
+    lib().or_compact(_p(src, ctypes.c_int64), rows, cols, num_docs, _p(ro, ctypes.c_int64), _p(ids, ctypes.c_int64))
+    return ids[: int(ro[-1])], ro
+
+
+def filtered_topk(emb: np.ndarray, qv: np.ndarray, packed: np.ndarray, topk: int):
+    """Top-k by (fp64 score desc, id asc) over filter-passing docs."""
+    emb = np.ascontiguousarray(emb, dtype=np.float32)
+    qv = np.ascontiguousarray(qv, dtype=np.float32)
+    packed = np.ascontiguousarray(packed, dtype=np.int64)
+    n, dim = emb.shape
+    q = qv.shape[0]
+    ids = np.zeros((q, topk), dtype=np.int64)
+    scores = np.zeros((q, topk), dtype=np.float32)
+    rc = lib().or_filtered_topk(_p(emb, ctypes.c_float), n, dim, _p(qv, ctypes.c_float), q,
+                                _p(packed, ctypes.c_int64), packed.shape[1], topk,
+                                _p(ids, ctypes.c_int64), _p(scores, ctypes.c_float))
+    if rc != 0:
+        raise MemoryError("oracle top-k allocation failed")
+    return ids, scores

@@ -1,0 +1,375 @@
+// Bloom index build for gfx950.
+//
+// Replaces bloom_index_build (bloom_indexer.cpp:26-113 on CPU,
+// bloom_indexer_cuda.cu:253-389 and :137-251 / :506-711 on CUDA) with three
+// kernels:
+//   widths_kernel   one workgroup per bundle of 2048 docs: per-doc term count
+//                   (feature_offsets[(d+1)F] - feature_offsets[dF]), bundle
+//                   max, b = (int64)((double)(max * k) * b_multiplier); also
+//                   checks that feature_offsets never decreases.
+//   scan_kernel     one workgroup: exclusive prefix sum of the widths into
+//                   bundle_b_offsets, plus the totals the host needs.
+//   scatter_kernel  one workgroup per bundle: zeroes a b x 32-word tile in
+//                   LDS, hashes every (doc, feature, value) term of the bundle
+//                   (one thread per value, the owning slot found by binary
+//                   search over an LDS copy of the offsets), ORs its k bits
+//                   into the tile with LDS atomics and writes the tile out with
+//                   coalesced stores.  Bundles wider than the tile OR straight
+//                   into global memory.
+// The reference's per-doc byte signatures and 64-way transpose
+// (bloom_indexer_cuda.cu:137-251, ~N*b/8 bytes of scratch) are not needed.
+#include <hip/hip_runtime.h>
+
+#include "st_common.hpp"
+#include "st_errors.hpp"
+
+namespace st {
+int cu_count();
+
+namespace {
+
+constexpr int kWidthThreads = 256;
+constexpr int kScanThreads = 1024;
+constexpr int kBuildThreads = 1024;
+constexpr int kBuildTileRows = 512;
+constexpr int kBuildTileWords = kBuildTileRows * 32;
+constexpr int kBuildOffsetCap = 4096;  // int64 slot offsets staged per chunk
+
+// stats layout (device int64[6]):
+//   [0] total rows  [1] max bundle width  [2] non-decreasing violation flag
+//   [3] feature_offsets[0]  [4] feature_offsets[N*F]  [5] reserved
+constexpr int kStatsLen = 6;
+
+__global__ void init_stats_kernel(int64_t* __restrict__ stats) {
+  if (threadIdx.x < kStatsLen) stats[threadIdx.x] = 0;
+}
+
+__device__ __forceinline__ int64_t wave_max(int64_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const int64_t o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__global__ __launch_bounds__(kWidthThreads) void widths_kernel(
+    const int64_t* __restrict__ offsets, int64_t num_docs, int64_t num_features,
+    int64_t k, double b_multiplier, int64_t* __restrict__ bundle_b_offsets,
+    int64_t* __restrict__ stats) {
+  __shared__ int64_t red[kWidthThreads / 64];
+  const int64_t bundle = blockIdx.x;
+  const int64_t doc0 = bundle * kDocsPerBundle;
+  const int64_t doc1 = min(doc0 + kDocsPerBundle, num_docs);
+  // Every offset of the bundle's slots is read once: the slot boundaries
+  // give the monotonicity check, the per-doc differences the counts.
+  const int64_t s0 = doc0 * num_features;
+  const int64_t s1 = doc1 * num_features;
+  int bad = 0;
+  for (int64_t s = s0 + threadIdx.x; s < s1; s += kWidthThreads)
+    bad |= offsets[s + 1] < offsets[s];
+  int64_t best = 0;
+  for (int64_t d = doc0 + threadIdx.x; d < doc1; d += kWidthThreads) {
+    const int64_t cnt = offsets[(d + 1) * num_features] - offsets[d * num_features];
+    best = cnt > best ? cnt : best;
+  }
+  best = wave_max(best);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+  if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(reinterpret_cast<unsigned long long*>(stats + 2), 1ull);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t m = red[0];
+    for (int i = 1; i < kWidthThreads / 64; ++i) m = red[i] > m ? red[i] : m;
+    const int64_t b = static_cast<int64_t>(static_cast<double>(m * k) * b_multiplier);
+    bundle_b_offsets[bundle + 1] = b;
+    atomicMax(reinterpret_cast<unsigned long long*>(stats + 1),
+              static_cast<unsigned long long>(b < 0 ? 0 : b));
+  }
+}
+
+// In-place exclusive scan: on entry bundle_b_offsets[i+1] holds width i.
+__global__ __launch_bounds__(kScanThreads) void scan_kernel(
+    const int64_t* __restrict__ offsets, int64_t num_slots, int64_t nb,
+    int64_t* __restrict__ bundle_b_offsets, int64_t* __restrict__ stats) {
+  __shared__ int64_t part[kScanThreads];
+  const int t = threadIdx.x;
+  const int64_t per = (nb + kScanThreads - 1) / kScanThreads;
+  const int64_t lo = min<int64_t>(t * per, nb);
+  const int64_t hi = min<int64_t>(lo + per, nb);
+  int64_t sum = 0;
+  for (int64_t i = lo; i < hi; ++i) sum += bundle_b_offsets[i + 1];
+  part[t] = sum;
+  __syncthreads();
+  for (int off = 1; off < kScanThreads; off <<= 1) {
+    const int64_t v = t >= off ? part[t - off] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  int64_t run = t == 0 ? 0 : part[t - 1];
+  for (int64_t i = lo; i < hi; ++i) {
+    run += bundle_b_offsets[i + 1];
+    bundle_b_offsets[i + 1] = run;
+  }
+  if (t == 0) {
+    bundle_b_offsets[0] = 0;
+    stats[0] = part[kScanThreads - 1];
+    stats[3] = offsets[0];
+    stats[4] = offsets[num_slots];
+  }
+}
+
+// First K distinct positions murmur(fid, value, seed) % b over seeds
+// 0, 1, 2, ... (assign_one_bits_position, bloom_index_util.cuh:183-207).
+// b >= K always holds for bundles that have terms (b >= floor(K *
+// b_multiplier) >= K), so the loop ends.
+template <int K>
+__device__ __forceinline__ void build_positions(uint64_t mx, uint64_t my,
+                                                const FastMod64& fm,
+                                                uint32_t (&found)[K]) {
+  int cnt = 0;
+  uint64_t seed = 0;
+  while (cnt < K) {
+    const uint32_t p = static_cast<uint32_t>(fast_mod(murmur_finish(mx, my, seed++), fm));
+    bool dup = false;
+#pragma unroll
+    for (int j = 0; j < K; ++j) dup |= (j < cnt) && (found[j] == p);
+    if (!dup) {
+#pragma unroll
+      for (int j = 0; j < K; ++j)
+        if (j == cnt) found[j] = p;
+      ++cnt;
+    }
+  }
+}
+
+struct ScatterArgs {
+  const int32_t* feature_ids;
+  const int64_t* offsets;
+  const int64_t* values;
+  int64_t num_values;
+  int64_t num_features;
+  int64_t num_docs;
+  int64_t k;
+  const int64_t* bundle_b_offsets;
+  unsigned long long* index;
+};
+
+// Swizzled LDS word of tile (row p, column c): spreads the 64 lanes of a
+// wave, which mostly share a column, over the LDS banks.
+__device__ __forceinline__ int tile_word(uint32_t p, uint32_t c) {
+  return static_cast<int>(p * 32 + (c ^ (p & 31)));
+}
+
+// Sets the term's bits either in the LDS tile or in global memory.
+template <int K>
+__device__ __forceinline__ void scatter_term(const ScatterArgs& a, bool staged,
+                                             unsigned long long* tile,
+                                             unsigned long long* gbase,
+                                             const FastMod64& fm, uint64_t mx,
+                                             uint64_t my, uint32_t col,
+                                             unsigned long long bit) {
+  uint32_t found[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) found[j] = 0;
+  build_positions<K>(mx, my, fm, found);
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    if (staged) {
+      atomicOr(tile + tile_word(found[j], col), bit);
+    } else {
+      atomicOr(gbase + static_cast<uint64_t>(found[j]) * 32 + col, bit);
+    }
+  }
+}
+
+// Runtime-k variant for k above the templated range (k <= 64).
+__device__ void scatter_term_generic(const ScatterArgs& a, bool staged,
+                                     unsigned long long* tile,
+                                     unsigned long long* gbase,
+                                     const FastMod64& fm, uint64_t mx,
+                                     uint64_t my, uint32_t col,
+                                     unsigned long long bit) {
+  uint32_t found[kMaxBuildK];
+  const int k = static_cast<int>(a.k);
+  int cnt = 0;
+  uint64_t seed = 0;
+  while (cnt < k) {
+    const uint32_t p = static_cast<uint32_t>(fast_mod(murmur_finish(mx, my, seed++), fm));
+    bool dup = false;
+    for (int j = 0; j < cnt; ++j) dup |= found[j] == p;
+    if (!dup) found[cnt++] = p;
+  }
+  for (int j = 0; j < k; ++j) {
+    if (staged) {
+      atomicOr(tile + tile_word(found[j], col), bit);
+    } else {
+      atomicOr(gbase + static_cast<uint64_t>(found[j]) * 32 + col, bit);
+    }
+  }
+}
+
+template <int K>
+__global__ __launch_bounds__(kBuildThreads) void scatter_kernel(ScatterArgs a) {
+  __shared__ unsigned long long tile[kBuildTileWords];
+  __shared__ int64_t soff[kBuildOffsetCap];
+
+  const int tid = threadIdx.x;
+  const int64_t bundle = blockIdx.x;
+  const int64_t start = a.bundle_b_offsets[bundle];
+  const int64_t b = a.bundle_b_offsets[bundle + 1] - start;
+  const bool staged = b <= kBuildTileRows;
+  unsigned long long* gbase = a.index + start * 32;
+  const int64_t words = b * 32;
+
+  if (staged) {
+    for (int64_t w = tid; w < words; w += kBuildThreads) tile[w] = 0;
+  } else {
+    for (int64_t w = tid; w < words; w += kBuildThreads) gbase[w] = 0;
+    __threadfence();
+  }
+  __syncthreads();
+
+  if (b > 0) {
+    const FastMod64 fm = make_fastmod(static_cast<uint64_t>(b));
+    const int64_t doc0 = bundle * kDocsPerBundle;
+    const int64_t doc1 = min(doc0 + kDocsPerBundle, a.num_docs);
+    const int64_t F = a.num_features;
+    // Slot chunks: slots [c0, c1) with their c1 - c0 + 1 offsets in LDS.
+    for (int64_t c0 = doc0 * F; c0 < doc1 * F; c0 += kBuildOffsetCap - 1) {
+      const int64_t c1 = min(c0 + kBuildOffsetCap - 1, doc1 * F);
+      const int n = static_cast<int>(c1 - c0);
+      __syncthreads();  // previous chunk's readers are done with soff
+      for (int i = tid; i <= n; i += kBuildThreads) soff[i] = a.offsets[c0 + i];
+      __syncthreads();
+      // Values outside [0, num_values) are never read (the host rejects
+      // offsets that would point there before launching).
+      const int64_t v0 = max<int64_t>(soff[0], 0);
+      const int64_t v1 = min<int64_t>(soff[n], a.num_values);
+      for (int64_t j = v0 + tid; j < v1; j += kBuildThreads) {
+        // Largest slot i with soff[i] <= j (offsets are non-decreasing).
+        int lo = 0, hi = n - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (soff[mid] <= j) lo = mid; else hi = mid - 1;
+        }
+        const int64_t slot = c0 + lo;
+        const int64_t doc = slot / F;
+        const int64_t f = slot - doc * F;
+        const int64_t in_bundle = doc - doc0;
+        const uint32_t col = static_cast<uint32_t>(in_bundle >> 6);
+        const unsigned long long bit = 1ull << (63 - (in_bundle & 63));
+        const uint64_t mx = murmur_mix_x(static_cast<uint64_t>(static_cast<int64_t>(a.feature_ids[f])));
+        const uint64_t my = murmur_mix_y(static_cast<uint64_t>(a.values[j]));
+        if constexpr (K > 0) {
+          scatter_term<K>(a, staged, tile, gbase, fm, mx, my, col, bit);
+        } else {
+          scatter_term_generic(a, staged, tile, gbase, fm, mx, my, col, bit);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (staged) {
+    for (int64_t w = tid; w < words; w += kBuildThreads) {
+      const uint32_t p = static_cast<uint32_t>(w >> 5);
+      const uint32_t c = static_cast<uint32_t>(w & 31);
+      __builtin_nontemporal_store(tile[tile_word(p, c)], gbase + w);
+    }
+  }
+}
+
+using ScatterFn = void (*)(ScatterArgs);
+
+ScatterFn select_scatter(int64_t k) {
+  switch (k) {
+    case 1: return scatter_kernel<1>;
+    case 2: return scatter_kernel<2>;
+    case 3: return scatter_kernel<3>;
+    case 4: return scatter_kernel<4>;
+    case 5: return scatter_kernel<5>;
+    case 6: return scatter_kernel<6>;
+    case 7: return scatter_kernel<7>;
+    case 8: return scatter_kernel<8>;
+    case 9: return scatter_kernel<9>;
+    case 10: return scatter_kernel<10>;
+    default: return scatter_kernel<0>;
+  }
+}
+
+void check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    throw Error(ST_ERR_HIP, cat(what, " launch failed: ", hipGetErrorString(e)));
+}
+
+}  // namespace
+}  // namespace st
+
+extern "C" int st_bloom_build_bundle_offsets(const int64_t* feature_offsets,
+                                             int64_t num_docs,
+                                             int64_t num_features, int64_t k,
+                                             double b_multiplier,
+                                             int64_t* bundle_b_offsets,
+                                             int64_t* stats, void* stream) {
+  using namespace st;
+  return guarded([&] {
+    ST_CHECK(num_features >= 1, "feature_ids must not be empty");
+    ST_CHECK(num_docs >= 0, "negative document count");
+    ST_CHECK(k >= 0 && k <= kMaxBuildK, "k must be in [0, ", kMaxBuildK,
+             "], got ", k);
+    ST_CHECK(b_multiplier > 1.0, "b_multiplier must be greater than 1.0");
+    ST_CHECK(feature_offsets && bundle_b_offsets && stats, "null device pointer");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t nb = (num_docs + kDocsPerBundle - 1) / kDocsPerBundle;
+    hipLaunchKernelGGL(init_stats_kernel, dim3(1), dim3(64), 0, s, stats);
+    check_launch("init_stats_kernel");
+    if (nb > 0) {
+      hipLaunchKernelGGL(widths_kernel, dim3(static_cast<unsigned>(nb)),
+                         dim3(kWidthThreads), 0, s, feature_offsets, num_docs,
+                         num_features, k, b_multiplier, bundle_b_offsets, stats);
+      check_launch("widths_kernel");
+    }
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, s,
+                       feature_offsets, num_docs * num_features, nb,
+                       bundle_b_offsets, stats);
+    check_launch("scan_kernel");
+  });
+}
+
+extern "C" int st_bloom_index_build(const int32_t* feature_ids,
+                                    const int64_t* feature_offsets,
+                                    const int64_t* feature_values,
+                                    int64_t num_features, int64_t num_docs,
+                                    int64_t num_values, int64_t k,
+                                    const int64_t* bundle_b_offsets,
+                                    int64_t max_b, int64_t* bloom_index,
+                                    int64_t bloom_index_numel, void* stream) {
+  using namespace st;
+  return guarded([&] {
+    ST_CHECK(num_features >= 1, "feature_ids must not be empty");
+    ST_CHECK(num_docs >= 0 && num_values >= 0, "negative sizes");
+    ST_CHECK(k >= 0 && k <= kMaxBuildK, "k must be in [0, ", kMaxBuildK,
+             "], got ", k);
+    const int64_t nb = (num_docs + kDocsPerBundle - 1) / kDocsPerBundle;
+    if (nb == 0 || bloom_index_numel == 0) return;
+    ST_CHECK(feature_ids && feature_offsets && bundle_b_offsets && bloom_index,
+             "null device pointer");
+    ST_CHECK(num_values == 0 || feature_values, "feature_values is null");
+    (void)max_b;
+    ScatterArgs a;
+    a.feature_ids = feature_ids;
+    a.offsets = feature_offsets;
+    a.values = feature_values;
+    a.num_values = num_values;
+    a.num_features = num_features;
+    a.num_docs = num_docs;
+    a.k = k;
+    a.bundle_b_offsets = bundle_b_offsets;
+    a.index = reinterpret_cast<unsigned long long*>(bloom_index);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(select_scatter(k), dim3(static_cast<unsigned>(nb)),
+                       dim3(kBuildThreads), 0, s, a);
+    check_launch("scatter_kernel");
+  });
+}

@@ -1,0 +1,83 @@
+// Compiled form of a batch of encoded query plans, shared by the host plan
+// compiler (search_plan.cpp) and the search kernels (bloom_search.hip).
+//
+// Each query plan arrives as the postfix operator list of
+// bloom_index_util.h:70-93 (ops, child counts via offsets, hash_k hashes per
+// TERM).  The compiler rebuilds the expression tree, flattens nested
+// AND/AND and OR/OR, removes double negation, deduplicates terms across the
+// batch, and emits a straight-line program for a one-accumulator machine
+// with a small push/pop stack.  All of that preserves the bitwise result of
+// the reference's stack evaluation (bloom_index_search.cpp:72-171) exactly,
+// since AND and OR over 64-bit words are associative, commutative and
+// idempotent.
+#pragma once
+
+#include <climits>
+#include <cstdint>
+#include <vector>
+
+namespace st {
+
+// Search kernel geometry.
+constexpr int kSearchWaves = 16;                 // waves per workgroup
+constexpr int kSearchThreads = kSearchWaves * 64;
+constexpr int kSearchTileRows = 512;             // bundle rows staged in LDS
+constexpr int kSearchOnesRow = kSearchTileRows;  // virtual all-ones row
+constexpr int kSearchZerosRow = kSearchTileRows + 1;  // virtual all-zeros row
+constexpr int kSearchTileBytes = (kSearchTileRows + 2) * 256;
+constexpr int kSearchLdsBytes = 160 * 1024;
+constexpr int kSearchPosSlots = (kSearchLdsBytes - kSearchTileBytes) / 4;
+constexpr int kSearchMaxStack = 16;
+
+// Position codes of the global-memory path (bundles wider than the tile).
+constexpr int32_t kPosOnes = INT32_MIN;
+constexpr int32_t kPosZeros = INT32_MIN + 1;
+
+// Instruction word: [2:0] opcode, [4:3] combine mode, [5] negate, [31:6] arg.
+enum InsnOp : uint32_t {
+  kInsTerm = 0,   // acc = mode(acc, [~]term(arg))
+  kInsConst = 1,  // acc = mode(acc, [~]all_ones)
+  kInsPush = 2,   // stack[sp++] = acc
+  kInsPop = 3,    // acc = mode(stack[--sp], acc)
+  kInsNot = 4,    // acc = ~acc
+};
+enum InsnMode : uint32_t { kModeSet = 0, kModeAnd = 1, kModeOr = 2 };
+
+constexpr uint32_t kInsnArgBits = 26;
+constexpr uint32_t kInsnMaxArg = (1u << kInsnArgBits) - 1;
+
+inline uint32_t encode_insn(uint32_t op, uint32_t mode, bool neg,
+                            uint32_t arg) {
+  return op | (mode << 3) | (static_cast<uint32_t>(neg) << 5) | (arg << 6);
+}
+
+// Positions stored per term in LDS, padded so a term's list is read with
+// 16-byte loads.
+inline int positions_per_term(int k_eff) {
+  return k_eff <= 4 ? 4 : (k_eff <= 8 ? 8 : 12);
+}
+
+// One kernel launch worth of queries.  Offsets are byte offsets into the
+// plan blob.
+struct SearchBatch {
+  uint32_t num_slots = 0;   // queries in this batch
+  uint32_t num_terms = 0;   // distinct terms in this batch
+  uint64_t off_wave = 0;    // uint32[kSearchWaves + 1]: slot range per wave
+  uint64_t off_row = 0;     // uint32[num_slots]: output row of each slot
+  uint64_t off_insn_start = 0;  // uint32[num_slots + 1]: program ranges
+  uint64_t off_insns = 0;   // uint32[...]: instruction words
+  uint64_t off_hashes = 0;  // uint64[num_terms * hash_k]
+};
+
+}  // namespace st
+
+// Host object behind the opaque st_search_plan handle.
+struct st_search_plan {
+  int64_t num_queries = 0;
+  int64_t hash_k = 0;
+  int k_eff = 0;        // distinct positions resolved per term
+  int kp = 4;           // padded positions per term in LDS
+  int max_stack = 0;    // deepest push in any program
+  std::vector<st::SearchBatch> batches;
+  std::vector<uint8_t> blob;
+};

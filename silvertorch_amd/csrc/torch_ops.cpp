@@ -1,0 +1,316 @@
+// torch.ops.st.* registration for the MI355X build.
+//
+// Registers the same schemas as the reference (bloom_indexer.cpp:115-125,
+// bloom_index_search.cpp:542-558, expression_query_parser.cpp:456-465) and
+// binds both dispatch keys to the HIP implementation behind the C ABI in
+// include/silvertorch_hip.h:
+//   CUDA key (HIP tensors under ROCm torch): runs on the tensors' device.
+//   CPU key: the inputs are copied to the current GPU, the same HIP kernels
+//            run, and the results are copied back; without a visible GPU the
+//            call raises.  No CPU implementation of the path exists here.
+// The parser is host code on both keys, as in the reference
+// (expression_query_parser_cuda.cu:27-44).
+#include <ATen/ATen.h>
+#include <c10/hip/HIPFunctions.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <Python.h>
+#include <torch/library.h>
+
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/silvertorch_hip.h"
+
+namespace {
+
+using at::Tensor;
+
+void check_st(int rc, const char* what) {
+  TORCH_CHECK(rc == ST_OK, what, ": ", st_last_error());
+}
+
+void* current_stream(const Tensor& t) {
+  return static_cast<void*>(
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream());
+}
+
+at::Device gpu_for_cpu_call() {
+  TORCH_CHECK(c10::hip::device_count() > 0,
+              "silvertorch_amd computes the bloom path with HIP kernels on an "
+              "MI355X; no GPU is visible to this process");
+  return at::Device(at::kCUDA, c10::hip::current_device());
+}
+
+// ---------------------------------------------------------------- build
+
+// Argument checks shared by both dispatch keys (the reference's CPU op checks
+// dtypes and b_multiplier first, bloom_indexer.cpp:33-36; the shape check is
+// the CUDA op's, bloom_indexer_cuda.cu:114-119).
+void check_build_args(const Tensor& feature_ids, const Tensor& feature_offsets,
+                      const Tensor& feature_values, double b_multiplier,
+                      int64_t k) {
+  TORCH_CHECK(feature_ids.scalar_type() == at::kInt, "feature_ids must be int32");
+  TORCH_CHECK(feature_offsets.scalar_type() == at::kLong,
+              "feature_offsets must be int64");
+  TORCH_CHECK(feature_values.scalar_type() == at::kLong,
+              "feature_values must be int64");
+  TORCH_CHECK(b_multiplier > 1.0, "b_multiplier must be greater than 1.0");
+  const int64_t F = feature_ids.numel();
+  TORCH_CHECK(F > 0, "feature_ids must not be empty");
+  TORCH_CHECK(feature_offsets.numel() >= 1,
+              "feature_offsets must hold at least one entry");
+  TORCH_CHECK((feature_offsets.numel() - 1) % F == 0, "Feature offsets size ",
+              feature_offsets.numel(),
+              " must be a multiple of the feature ids size ", F, " plus one");
+  TORCH_CHECK(k >= 0 && k <= ST_MAX_BUILD_K, "k must be in [0, ",
+              ST_MAX_BUILD_K, "], got ", k);
+}
+
+std::tuple<Tensor, Tensor> build_gpu(const Tensor& feature_ids_in,
+                                     const Tensor& feature_offsets_in,
+                                     const Tensor& feature_values_in,
+                                     double b_multiplier, int64_t k,
+                                     bool /*fast_build*/) {
+  check_build_args(feature_ids_in, feature_offsets_in, feature_values_in,
+                   b_multiplier, k);
+  TORCH_CHECK(feature_ids_in.is_cuda() && feature_offsets_in.is_cuda() &&
+                  feature_values_in.is_cuda(),
+              "bloom_index_build inputs must all be GPU tensors");
+  const auto dev = feature_ids_in.device();
+  TORCH_CHECK(feature_offsets_in.device() == dev &&
+                  feature_values_in.device() == dev,
+              "bloom_index_build inputs must be on one device");
+  const int64_t F = feature_ids_in.numel();
+
+  c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(dev);
+  const Tensor ids = feature_ids_in.contiguous();
+  const Tensor offsets = feature_offsets_in.contiguous();
+  const Tensor values = feature_values_in.contiguous();
+  const int64_t N = (offsets.numel() - 1) / F;
+  const int64_t nb = (N + ST_DOCS_PER_BUNDLE - 1) / ST_DOCS_PER_BUNDLE;
+  void* stream = current_stream(ids);
+
+  auto lopts = at::TensorOptions().dtype(at::kLong).device(dev);
+  Tensor bundle_b_offsets = at::empty({nb + 1}, lopts);
+  Tensor stats = at::empty({6}, lopts);
+  check_st(st_bloom_build_bundle_offsets(offsets.data_ptr<int64_t>(), N, F, k,
+                                         b_multiplier,
+                                         bundle_b_offsets.data_ptr<int64_t>(),
+                                         stats.data_ptr<int64_t>(), stream),
+           "bloom_index_build");
+  const Tensor st = stats.cpu();  // the index size is data dependent
+  const int64_t* s = st.data_ptr<int64_t>();
+  TORCH_CHECK(s[2] == 0, "feature_offsets must be non-decreasing");
+  TORCH_CHECK(s[3] >= 0 && s[4] <= values.numel(), "feature_offsets range [",
+              s[3], ", ", s[4], ") lies outside feature_values (",
+              values.numel(), " values)");
+  TORCH_CHECK(s[1] <= INT32_MAX, "bundle width ", s[1],
+              " exceeds the int32 position range");
+  Tensor bloom_index = at::empty({s[0] * ST_COLUMNS_PER_BUNDLE}, lopts);
+  check_st(st_bloom_index_build(ids.data_ptr<int32_t>(),
+                                offsets.data_ptr<int64_t>(),
+                                values.numel() ? values.data_ptr<int64_t>() : nullptr,
+                                F, N, values.numel(), k,
+                                bundle_b_offsets.data_ptr<int64_t>(), s[1],
+                                bloom_index.data_ptr<int64_t>(),
+                                bloom_index.numel(), stream),
+           "bloom_index_build");
+  return {bloom_index, bundle_b_offsets};
+}
+
+std::tuple<Tensor, Tensor> build_cpu_tensors(const Tensor& feature_ids,
+                                             const Tensor& feature_offsets,
+                                             const Tensor& feature_values,
+                                             double b_multiplier, int64_t k,
+                                             bool fast_build) {
+  check_build_args(feature_ids, feature_offsets, feature_values, b_multiplier, k);
+  const at::Device gpu = gpu_for_cpu_call();
+  auto [index, offsets] =
+      build_gpu(feature_ids.to(gpu), feature_offsets.to(gpu),
+                feature_values.to(gpu), b_multiplier, k, fast_build);
+  return {index.cpu(), offsets.cpu()};
+}
+
+// ---------------------------------------------------------------- search
+
+struct PlanHolder {
+  st_search_plan* p = nullptr;
+  ~PlanHolder() { st_search_plan_destroy(p); }
+};
+
+Tensor search_gpu(const Tensor& bloom_index_in, const Tensor& bundle_b_offsets_in,
+                  const Tensor& plans_data, const Tensor& plans_offsets,
+                  int64_t k, int64_t hash_k, bool return_bool_mask) {
+  TORCH_CHECK(bloom_index_in.is_cuda(), "bloom_index must be a GPU tensor");
+  TORCH_CHECK(bloom_index_in.dim() == 1, "bloom_index must be 1-D");
+  TORCH_CHECK(bloom_index_in.scalar_type() == at::kLong, "bloom_index must be int64");
+  TORCH_CHECK(bundle_b_offsets_in.scalar_type() == at::kLong,
+              "bloom_bundle_b_offsets must be int64");
+  TORCH_CHECK(bundle_b_offsets_in.device() == bloom_index_in.device(),
+              "bloom_bundle_b_offsets must be on the device of bloom_index");
+  TORCH_CHECK(bundle_b_offsets_in.numel() >= 1,
+              "bloom_bundle_b_offsets must hold at least one entry");
+  TORCH_CHECK(plans_data.scalar_type() == at::kChar ||
+                  plans_data.scalar_type() == at::kByte,
+              "bloom_query_plans_data must be int8");
+  TORCH_CHECK(plans_offsets.scalar_type() == at::kLong,
+              "bloom_query_plans_offsets must be int64");
+  const auto dev = bloom_index_in.device();
+  c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(dev);
+  const Tensor index = bloom_index_in.contiguous();
+  const Tensor bbo = bundle_b_offsets_in.contiguous();
+  // Plans are compiled on the host, as the reference decodes them there
+  // (bloom_index_search_cuda.cu:1043-1098).
+  const Tensor pd = plans_data.to(at::kCPU).contiguous();
+  const Tensor po = plans_offsets.to(at::kCPU).contiguous();
+
+  PlanHolder plan;
+  check_st(st_search_plan_create(
+               reinterpret_cast<const int8_t*>(pd.data_ptr()), pd.numel(),
+               po.data_ptr<int64_t>(), po.numel(), k, hash_k, &plan.p),
+           "bloom_index_search_batch");
+  const int64_t Q = st_search_plan_num_queries(plan.p);
+  const int64_t nb = bbo.numel() - 1;
+  const int64_t C = nb * ST_COLUMNS_PER_BUNDLE;
+  Tensor out = return_bool_mask
+                   ? at::empty({Q, C * ST_BITS_PER_COLUMN},
+                               at::TensorOptions().dtype(at::kBool).device(dev))
+                   : at::empty({Q, C}, at::TensorOptions().dtype(at::kLong).device(dev));
+  if (Q == 0 || nb == 0) return out;
+
+  const int64_t blob_bytes = st_search_plan_blob_bytes(plan.p);
+  Tensor host = at::empty({blob_bytes}, at::TensorOptions().dtype(at::kByte).pinned_memory(true));
+  std::memcpy(host.data_ptr(), st_search_plan_blob(plan.p), blob_bytes);
+  Tensor blob = host.to(dev, /*non_blocking=*/true);
+  check_st(st_bloom_index_search_batch(index.data_ptr<int64_t>(), index.numel(),
+                                       bbo.data_ptr<int64_t>(), nb, plan.p,
+                                       blob.data_ptr(), return_bool_mask ? 1 : 0,
+                                       out.data_ptr(), current_stream(index)),
+           "bloom_index_search_batch");
+  return out;
+}
+
+Tensor search_cpu_tensors(const Tensor& bloom_index, const Tensor& bundle_b_offsets,
+                          const Tensor& plans_data, const Tensor& plans_offsets,
+                          int64_t k, int64_t hash_k, bool return_bool_mask) {
+  TORCH_CHECK(bloom_index.dim() == 1, "bloom_index must be 1-D");
+  {  // plan errors surface before any device work, as on the reference CPU op
+    const Tensor pd = plans_data.contiguous(), po = plans_offsets.contiguous();
+    TORCH_CHECK(po.scalar_type() == at::kLong, "bloom_query_plans_offsets must be int64");
+    PlanHolder probe;
+    check_st(st_search_plan_create(reinterpret_cast<const int8_t*>(pd.data_ptr()),
+                                   pd.numel(), po.data_ptr<int64_t>(), po.numel(),
+                                   k, hash_k, &probe.p),
+             "bloom_index_search_batch");
+  }
+  const at::Device gpu = gpu_for_cpu_call();
+  return search_gpu(bloom_index.to(gpu), bundle_b_offsets.to(gpu), plans_data,
+                    plans_offsets, k, hash_k, return_bool_mask)
+      .cpu();
+}
+
+// ---------------------------------------------------------------- parser
+
+std::tuple<int64_t, std::vector<Tensor>> parse_batch(
+    const c10::List<std::string>& expressions, const Tensor& /*silvertorch_ks*/,
+    int64_t bloom_hash_k, bool return_query_plan, int64_t max_sub_queries) {
+  std::vector<std::string> owned;
+  owned.reserve(expressions.size());
+  for (size_t i = 0; i < expressions.size(); ++i) owned.push_back(expressions.get(i));
+  std::vector<const char*> ptrs;
+  for (const auto& s : owned) ptrs.push_back(s.c_str());
+  st_parsed_plans* res = nullptr;
+  const int rc = st_parse_expression_query_batch(
+      ptrs.data(), static_cast<int64_t>(ptrs.size()), bloom_hash_k,
+      return_query_plan ? 1 : 0, max_sub_queries, &res);
+  check_st(rc, "parse_expression_query_batch");
+  const int64_t nbytes = st_parsed_plans_data_bytes(res);
+  const int64_t noff = st_parsed_plans_offsets_len(res);
+  Tensor data = at::empty({nbytes}, at::kChar);
+  Tensor offs = at::empty({noff}, at::kLong);
+  if (nbytes) std::memcpy(data.data_ptr(), st_parsed_plans_data(res), nbytes);
+  if (noff) std::memcpy(offs.data_ptr(), st_parsed_plans_offsets(res), noff * 8);
+  const int64_t max_stack = st_parsed_plans_max_stack(res);
+  st_parsed_plans_destroy(res);
+  return {max_stack, {data, offs}};
+}
+
+// ------------------------------------------ generate_column_info_for_clusters
+
+std::tuple<Tensor, Tensor, Tensor> column_info(const Tensor& offsets_in,
+                                               const Tensor& lengths_in) {
+  TORCH_CHECK(offsets_in.sizes() == lengths_in.sizes(),
+              "selected_cluster_offsets and selected_cluster_lengths must have "
+              "the same shape");
+  TORCH_CHECK(offsets_in.dim() == 1 || offsets_in.dim() == 2,
+              "selected_cluster_offsets must be 1D or 2D, got ", offsets_in.dim(), "D");
+  TORCH_CHECK(offsets_in.scalar_type() == at::kLong &&
+                  lengths_in.scalar_type() == at::kLong,
+              "cluster offsets and lengths must be int64");
+  TORCH_CHECK(offsets_in.device() == lengths_in.device(),
+              "cluster offsets and lengths must be on one device");
+  const auto dev = offsets_in.device();
+  const int64_t n = lengths_in.numel();
+  auto opts = at::TensorOptions().device(dev);
+  Tensor counts = at::empty({n}, opts.dtype(at::kInt));
+  Tensor starts = at::empty({n}, opts.dtype(at::kInt));
+  Tensor firsts = at::empty({n}, opts.dtype(at::kChar));
+  if (n == 0) return {counts, starts, firsts};
+  if (dev.is_cuda()) {
+    c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(dev);
+    const Tensor o = offsets_in.contiguous(), l = lengths_in.contiguous();
+    check_st(st_generate_column_info_for_clusters(
+                 o.data_ptr<int64_t>(), l.data_ptr<int64_t>(), n,
+                 counts.data_ptr<int32_t>(), starts.data_ptr<int32_t>(),
+                 firsts.data_ptr<int8_t>(), current_stream(o)),
+             "generate_column_info_for_clusters");
+  } else {
+    const at::Device gpu = gpu_for_cpu_call();
+    auto [c, s, f] = column_info(offsets_in.to(gpu), lengths_in.to(gpu));
+    return {c.cpu(), s.cpu(), f.cpu()};
+  }
+  return {counts, starts, firsts};
+}
+
+}  // namespace
+
+TORCH_LIBRARY_FRAGMENT(st, m) {
+  m.def(
+      "bloom_index_build(Tensor feature_ids, Tensor feature_offsets, "
+      "Tensor feature_values, float b_multiplier, int k, "
+      "bool fast_build=False) -> (Tensor, Tensor)");
+  m.def(
+      "bloom_index_search_batch(Tensor bloom_index, "
+      "Tensor bloom_bundle_b_offsets, Tensor bloom_query_plans_data, "
+      "Tensor bloom_query_plans_offsets, int k, int hash_k, "
+      "bool return_bool_mask=True)-> Tensor");
+  m.def(
+      "parse_expression_query_batch(str[] expressions, Tensor silvertorch_ks, "
+      "int bloom_hash_k, bool return_query_plan=True, "
+      "int max_sub_queries=5)-> (int, Tensor[])");
+  m.def(
+      "generate_column_info_for_clusters(Tensor selected_cluster_offsets, "
+      "Tensor selected_cluster_lengths) -> (Tensor, Tensor, Tensor)");
+}
+
+TORCH_LIBRARY_IMPL(st, CUDA, m) {
+  m.impl("bloom_index_build", TORCH_FN(build_gpu));
+  m.impl("bloom_index_search_batch", TORCH_FN(search_gpu));
+  m.impl("parse_expression_query_batch", TORCH_FN(parse_batch));
+  m.impl("generate_column_info_for_clusters", TORCH_FN(column_info));
+}
+
+TORCH_LIBRARY_IMPL(st, CPU, m) {
+  m.impl("bloom_index_build", TORCH_FN(build_cpu_tensors));
+  m.impl("bloom_index_search_batch", TORCH_FN(search_cpu_tensors));
+  m.impl("parse_expression_query_batch", TORCH_FN(parse_batch));
+  m.impl("generate_column_info_for_clusters", TORCH_FN(column_info));
+}
+
+// Python module entry point: importing silvertorch_amd._C loads this library,
+// whose static initialisers above register torch.ops.st.*.
+static PyModuleDef st_module = {PyModuleDef_HEAD_INIT, "_C",
+                                "torch.ops.st.* on MI355X (HIP)", -1, nullptr};
+PyMODINIT_FUNC PyInit__C(void) { return PyModule_Create(&st_module); }

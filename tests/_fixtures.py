@@ -1,0 +1,61 @@
+"""Loaders for the committed golden fixtures (tests/golden/)."""
+
+from __future__ import annotations
+
+import hashlib
+import json
+from functools import lru_cache
+from pathlib import Path
+
+import numpy as np
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+@lru_cache(None)
+def murmur_vectors() -> list[tuple[int, int, int, int]]:
+    d = json.loads((GOLDEN / "murmur_x64_128.json").read_text())
+    return [tuple(int(v) for v in row) for row in d["vectors"]]
+
+
+@lru_cache(None)
+def parser_golden() -> dict:
+    return json.loads((GOLDEN / "ref_parser.json").read_text())
+
+
+@lru_cache(None)
+def digests() -> dict:
+    return json.loads((GOLDEN / "ref_digests.json").read_text())
+
+
+@lru_cache(None)
+def _cases_npz():
+    return dict(np.load(GOLDEN / "ref_cases.npz", allow_pickle=False))
+
+
+def case_names() -> list[str]:
+    return sorted({k.split("/")[0] for k in _cases_npz()})
+
+
+def case(name: str) -> dict:
+    z = _cases_npz()
+    c = {k.split("/", 1)[1]: v for k, v in z.items() if k.startswith(name + "/")}
+    bm, kb, ks, hk, ms, phk = c["params"].tolist()
+    c.update(b_multiplier=bm, build_k=int(kb), k=int(ks), hash_k=int(hk), max_sub=int(ms), parse_hash_k=int(phk))
+    c["queries"] = [str(q) for q in c["queries"]]
+    return c
+
+
+def sha(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def wide_corpus():
+    w = digests()["wide_bundles"]
+    n = 2048 + 16
+    cnt = np.ones(n, dtype=np.int64)
+    cnt[0] = w["doc0_terms"]
+    cnt[2048] = w["doc2048_terms"]
+    offs = np.concatenate([[0], np.cumsum(cnt)]).astype(np.int64)
+    vals = (np.arange(int(offs[-1]), dtype=np.int64) * 7919) % 100003
+    return np.array([5], dtype=np.int32), offs, vals, w

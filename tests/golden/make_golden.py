@@ -1,0 +1,227 @@
+"""Writes the golden fixtures under tests/golden/ (run in the build container).
+
+Sources of truth, neither of which is this repository's code:
+  * MurmurHash3_x64_128 vectors from scikit-learn's independent public-domain
+    source (sklearn/utils/src/MurmurHash3.cpp), compiled into a temporary
+    directory: murmur_x64_128.json.  Keys are LE(x)||LE(y), 16 bytes; the
+    fixture stores h1 ^ h2 of the 128-bit output.
+  * The reference's own CPU ops (bloom_index_build, bloom_index_search_batch,
+    parse_expression_query_batch), compiled from its sources by
+    ``make -C oracle ref`` into oracle/_ref/libst_ref.so:
+      ref_parser.json   plan bytes / offsets / max stack per expression batch,
+                        and which expressions raise;
+      ref_cases.npz     small build + search cases stored in full;
+      ref_digests.json  sha256 digests of larger cases (cfg1 and a case with
+                        bundles wider than 32767 rows) plus generator params.
+
+Usage:  python tests/golden/make_golden.py
+The reference library registers torch.ops.st.*, so this script never imports
+silvertorch_amd.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import json
+import subprocess
+import sys
+import tempfile
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parents[1]
+sys.path.insert(0, str(ROOT))
+
+
+
+def _sklearn_murmur_source() -> Path:
+    import sklearn
+
+    return Path(sklearn.__file__).parent / "utils" / "src" / "MurmurHash3.cpp"
+
+
+def murmur_vectors() -> dict:
+    src = _sklearn_murmur_source()
+    with tempfile.TemporaryDirectory() as td:
+        so = Path(td) / "libmm.so"
+        subprocess.run(["g++", "-O2", "-shared", "-fPIC", str(src), "-I", str(src.parent), "-o", str(so)], check=True)
+        L = ctypes.CDLL(str(so))
+        fn = L.MurmurHash3_x64_128  # (const void* key, int len, uint32_t seed, void* out)
+        fn.restype = None
+        rng = np.random.default_rng(2024)
+        rows = []
+        specials = [(0, 0, 0), (1, 100, 0), (2, 200, 6), ((1 << 64) - 1, (1 << 63), 3),
+                    (1, (1 << 64) - 200, 1), (42, 100, 4294967295)]
+        for _ in range(200):
+            x, y = (int(v) for v in rng.integers(0, 1 << 63, 2, dtype=np.int64))
+            if rng.random() < 0.5:
+                x = int(rng.integers(-5, 20)) & ((1 << 64) - 1)
+            seed = int(rng.integers(0, 64))
+            specials.append((x, y, seed))
+        for x, y, seed in specials:
+            key = (ctypes.c_uint64 * 2)(x, y)
+            out = (ctypes.c_uint64 * 2)()
+            fn(key, 16, ctypes.c_uint32(seed), out)
+            rows.append([str(x), str(y), str(seed), str(out[0] ^ out[1])])
+    return {"source": "sklearn/utils/src/MurmurHash3.cpp MurmurHash3_x64_128, h1^h2", "vectors": rows}
+
+
+def main() -> None:
+    import torch
+
+    ref = ROOT / "oracle" / "_ref" / "libst_ref.so"
+    if not ref.exists():
+        subprocess.run(["make", "-C", str(ROOT / "oracle"), "ref"], check=True)
+    torch.ops.load_library(str(ref))
+    st = torch.ops.st
+    from silvertorch_amd import synthetic as S
+
+    (HERE / "murmur_x64_128.json").write_text(json.dumps(murmur_vectors(), indent=0))
+
+    # ---------------- parser
+    exprs = ["1:100", "1:100 AND NOT 2:201", "1:102 OR 2:203", "", "-1:-200", "NOT NOT 1:10",
+             "(1:100 & 2:200) | !(3:300 & 4:400:0.8)", "1:10 | 2:20 | 3:30 | 4:40 | 5:50",
+             "(1:10 | 2:20 | 3:30 | 4:40) & 5:50", "1:10 OR 2:20 AND NOT 3:30", "42:100:0.5",
+             "1:1:2", "((((1:1))))", "1:1 & 2:2 & 3:3 & 4:4 & 5:5 & 6:6 & 7:7 | 8:8", "  7:7  ",
+             "NOT (1:1 OR 2:2 OR 3:3) AND NOT 4:4", "9223372036854775807:-9223372036854775808"]
+    batches = []
+    for hk in (1, 3, 7):
+        for ms in (1, 2, 3, 5, 0):
+            m, (pd, po) = st.parse_expression_query_batch(exprs, torch.ones(1, dtype=torch.long), hk, True, ms)
+            batches.append({"hash_k": hk, "max_sub_queries": ms, "max_stack": int(m),
+                            "data_hex": pd.numpy().tobytes().hex(), "offsets": po.tolist()})
+    m, (pd, po) = st.parse_expression_query_batch(exprs, torch.ones(1, dtype=torch.long), 7, False, 5)
+    no_plan = {"max_stack": int(m), "data_len": int(pd.numel()), "offsets_len": int(po.numel())}
+    errors = {}
+    for e in ["42", "(1:10 AND 2:20", "1:10 XOR 2:20", "1:10 AND", "1:10 2:20", "1:10 $", "1.5:3", "1:", "1:2:",
+              "()", "AND 1:1", "1:1 OR", "NOT", "1:1)", "1:-", "--1:1"]:
+        try:
+            st.parse_expression_query_batch([e], torch.ones(1, dtype=torch.long), 7, True, 5)
+            errors[e] = None
+        except RuntimeError as ex:
+            errors[e] = str(ex).splitlines()[0]
+    (HERE / "ref_parser.json").write_text(json.dumps(
+        {"expressions": exprs, "batches": batches, "no_plan": no_plan, "errors": errors}, indent=0))
+
+    # ---------------- small build + search cases (stored in full)
+    cases = {}
+    readme_ids = np.array([1, 2], dtype=np.int32)
+    readme_vals = np.array([100, 200, 201, 100, 101, 200, 102, 202, 100, 200, 203], dtype=np.int64)
+    readme_offs = np.array([0, 1, 3, 5, 6, 7, 8, 9, 11], dtype=np.int64)
+    rng = np.random.default_rng(7)
+
+    def add_case(name, ids, offs, vals, bm, kb, queries, ks, hk, ms=5, parse_hk=None):
+        parse_hk = hk if parse_hk is None else parse_hk
+        bi, bo = st.bloom_index_build(torch.from_numpy(ids), torch.from_numpy(offs), torch.from_numpy(vals), bm, kb)
+        _, (pd, po) = st.parse_expression_query_batch(queries, torch.ones(1, dtype=torch.long), parse_hk, True, ms)
+        packed = st.bloom_index_search_batch(bi, bo, pd, po, ks, hk, False)
+        boolm = st.bloom_index_search_batch(bi, bo, pd, po, ks, hk, True)
+        assert np.array_equal(np.packbits(boolm.numpy(), axis=1).view(">u8").astype(np.int64).reshape(packed.shape),
+                              packed.numpy())
+        cases[f"{name}/ids"] = ids
+        cases[f"{name}/offsets"] = offs
+        cases[f"{name}/values"] = vals
+        cases[f"{name}/params"] = np.array([bm, kb, ks, hk, ms, parse_hk], dtype=np.float64)
+        cases[f"{name}/queries"] = np.array(queries, dtype=object).astype(str)
+        cases[f"{name}/plans_data"] = pd.numpy()
+        cases[f"{name}/plans_offsets"] = po.numpy()
+        cases[f"{name}/index"] = bi.numpy()
+        cases[f"{name}/bundle_b_offsets"] = bo.numpy()
+        cases[f"{name}/packed"] = packed.numpy()
+
+    readme_q = ["1:100", "1:100 AND NOT 2:201", "1:102 OR 2:203", "1:100 AND 2:200", "1:102"]
+    add_case("readme", readme_ids, readme_offs, readme_vals, 5.0, 3, readme_q, 3, 7)
+
+    def make_features(n, F):  # test_bloom_index_search.py:41-53 fixture shape
+        ids = np.arange(F, dtype=np.int32)
+        vals = np.array([d * 100 + f for d in range(n) for f in range(F)], dtype=np.int64)
+        offs = np.arange(n * F + 1, dtype=np.int64)
+        return ids, offs, vals
+
+    ids, offs, vals = make_features(10, 3)
+    add_case("features10x3", ids, offs, vals, 2.0, 7, ["0:0", "1:1", "0:0 AND 1:1", "0:0 OR 1:1", "NOT 0:0", ""], 3, 7)
+    n = 32 * 64 * 2 + 10  # test_bloom_indexer.py:123-145 multi-bundle shape
+    add_case("multibundle", np.array([0], dtype=np.int32), np.arange(n + 1, dtype=np.int64),
+             np.arange(n, dtype=np.int64), 2.0, 3, ["0:5", "0:4100 OR 0:4101", "NOT 0:7", "0:1 AND 0:2"], 3, 3)
+
+    for i, (kb, ks, hk, bm) in enumerate([(3, 3, 7, 5.0), (7, 3, 7, 2.0), (1, 1, 1, 1.5), (10, 10, 10, 3.0),
+                                          (4, 4, 2, 2.0), (3, 0, 7, 5.0), (3, 3, 0, 5.0), (5, 8, 8, 4.0)]):
+        ndoc = int(rng.integers(1, 7000))
+        F = int(rng.integers(1, 5))
+        cnt = rng.integers(0, 5, (ndoc, F))
+        offs = np.concatenate([[0], np.cumsum(cnt.reshape(-1))]).astype(np.int64)
+        vals = rng.integers(-3, 40, int(offs[-1])).astype(np.int64)
+        ids = (np.arange(F, dtype=np.int32) * 7 - 3).astype(np.int32)
+        qs = []
+        for _ in range(12):
+            t = int(rng.integers(1, 7))
+            parts = []
+            for j in range(t):
+                term = f"{int(ids[rng.integers(0, F)])}:{int(rng.integers(-3, 40))}"
+                if rng.random() < 0.25:
+                    term = "NOT " + term
+                if rng.random() < 0.15:
+                    term = f"({term} OR {int(ids[rng.integers(0, F)])}:{int(rng.integers(-3, 40))})"
+                parts.append(term)
+                if j < t - 1:
+                    parts.append(str(rng.choice(["AND", "OR"])))
+            qs.append(" ".join(parts))
+        qs.append("")
+        # hash_k 0 at search time: plans parsed with hash_k 7 (the reference
+        # parser divides by hash_k), searched with hash_k 0.
+        add_case(f"random{i}", ids, offs, vals, bm, kb, qs, ks, hk, int(rng.integers(1, 6)),
+                 parse_hk=hk if hk > 0 else 7)
+    np.savez_compressed(HERE / "ref_cases.npz", **cases)
+
+    # ---------------- digests of larger cases
+    digests = {}
+
+    def h(a: np.ndarray) -> str:
+        return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+    cspec, qspec = S.CONFIGS["cfg1"]
+    corp = S.make_corpus(cspec, seed=0)
+    queries = S.make_queries(cspec, qspec, seed=0)
+    bi, bo = st.bloom_index_build(torch.from_numpy(corp.feature_ids), torch.from_numpy(corp.feature_offsets),
+                                  torch.from_numpy(corp.feature_values), cspec.b_multiplier, cspec.k)
+    _, (pd, po) = st.parse_expression_query_batch(queries, torch.ones(1, dtype=torch.long), cspec.hash_k, True, 5)
+    packed = st.bloom_index_search_batch(bi, bo, pd, po, cspec.k, cspec.hash_k, False).numpy()
+    digests["cfg1"] = {
+        "inputs": {"offsets": h(corp.feature_offsets), "values": h(corp.feature_values)},
+        "queries_sha256": hashlib.sha256("\n".join(queries).encode()).hexdigest(),
+        "plans_data": h(pd.numpy()), "plans_offsets": h(po.numpy()),
+        "index": h(bi.numpy()), "bundle_b_offsets": h(bo.numpy()), "packed": h(packed),
+        "index_len": int(bi.numel()), "bundle_b_offsets_head": bo.numpy()[:4].tolist(),
+        "packed_row0_head": packed[0, :8].tolist(),
+        "match_counts": [int(np.unpackbits(packed[q].astype(">i8").view(np.uint8))[:cspec.num_docs].sum())
+                         for q in range(packed.shape[0])],
+    }
+
+    # Two bundles: bundle 0 exactly 32768 rows wide, bundle 1 wider than
+    # 32767 rows, so the reference's int16 position cast wraps into bundle 0.
+    wide = {"k": 4, "b_multiplier": 2.0, "doc0_terms": 4096, "doc2048_terms": 5000}
+    n = 2048 + 16
+    cnt = np.ones(n, dtype=np.int64)
+    cnt[0] = wide["doc0_terms"]
+    cnt[2048] = wide["doc2048_terms"]
+    offs = np.concatenate([[0], np.cumsum(cnt)]).astype(np.int64)
+    vals = (np.arange(int(offs[-1]), dtype=np.int64) * 7919) % 100003
+    ids = np.array([5], dtype=np.int32)
+    bi, bo = st.bloom_index_build(torch.from_numpy(ids), torch.from_numpy(offs), torch.from_numpy(vals),
+                                  wide["b_multiplier"], wide["k"])
+    qs = [f"5:{int(v)}" for v in vals[[0, 5, 4095, 4097, 6000, 9000, 9100]]] + \
+         ["5:1 OR 5:2", "NOT 5:3", f"5:{int(vals[4200])} AND NOT 5:{int(vals[10])}"]
+    _, (pd, po) = st.parse_expression_query_batch(qs, torch.ones(1, dtype=torch.long), 7, True, 5)
+    packed = st.bloom_index_search_batch(bi, bo, pd, po, 4, 7, False).numpy()
+    wide.update({"queries": qs, "bundle_b_offsets": bo.tolist(), "index": h(bi.numpy()), "packed": h(packed),
+                 "value_rule": "values[i] = (i * 7919) % 100003; doc 0 and doc 2048 carry the wide counts"})
+    digests["wide_bundles"] = wide
+    (HERE / "ref_digests.json").write_text(json.dumps(digests, indent=1))
+    print("golden fixtures written to", HERE)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,65 @@
+"""Drives the C ABI (include/silvertorch_hip.h) with torch device tensors."""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import torch
+
+from silvertorch_amd import capi
+
+
+def note(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def build(ids, offsets, values, b_multiplier: float, k: int):
+    """C-ABI build -> (index, bundle_b_offsets) as numpy arrays."""
+    L = capi.lib()
+    ids_d = torch.as_tensor(np.ascontiguousarray(ids, dtype=np.int32)).cuda()
+    off_d = torch.as_tensor(np.ascontiguousarray(offsets, dtype=np.int64)).cuda()
+    val_d = torch.as_tensor(np.ascontiguousarray(values, dtype=np.int64)).cuda()
+    F = ids_d.numel()
+    n = (off_d.numel() - 1) // F
+    nb = (n + 2047) // 2048
+    bbo = torch.empty(nb + 1, dtype=torch.long, device="cuda")
+    stats = torch.empty(6, dtype=torch.long, device="cuda")
+    capi.check(L.st_bloom_build_bundle_offsets(off_d.data_ptr(), n, F, k, b_multiplier, bbo.data_ptr(),
+                                               stats.data_ptr(), _stream()))
+    s = stats.cpu().tolist()
+    assert s[2] == 0 and 0 <= s[3] <= s[4] <= val_d.numel(), s
+    index = torch.empty(s[0] * 32, dtype=torch.long, device="cuda")
+    capi.check(L.st_bloom_index_build(ids_d.data_ptr(), off_d.data_ptr(),
+                                      val_d.data_ptr() if val_d.numel() else None, F, n, val_d.numel(), k,
+                                      bbo.data_ptr(), s[1], index.data_ptr() if index.numel() else None,
+                                      index.numel(), _stream()))
+    torch.cuda.synchronize()
+    return index.cpu().numpy(), bbo.cpu().numpy()
+
+
+def search(index, bbo, plans_data, plans_offsets, k: int, hash_k: int, bool_mask: bool = False):
+    """C-ABI search; index / bbo may be numpy arrays or cuda tensors."""
+    L = capi.lib()
+    idx_d = index if isinstance(index, torch.Tensor) else torch.as_tensor(np.ascontiguousarray(index, np.int64)).cuda()
+    bbo_d = bbo if isinstance(bbo, torch.Tensor) else torch.as_tensor(np.ascontiguousarray(bbo, np.int64)).cuda()
+    plan = capi.SearchPlan(bytes(np.asarray(plans_data, dtype=np.int8).tobytes()), plans_offsets, k, hash_k)
+    blob = plan.blob()
+    blob_d = torch.frombuffer(bytearray(blob), dtype=torch.uint8).cuda() if blob else None
+    q = plan.num_queries
+    nb = bbo_d.numel() - 1
+    if bool_mask:
+        out = torch.empty((q, nb * 2048), dtype=torch.bool, device="cuda")
+    else:
+        out = torch.empty((q, nb * 32), dtype=torch.long, device="cuda")
+    capi.check(L.st_bloom_index_search_batch(idx_d.data_ptr() if idx_d.numel() else None, idx_d.numel(),
+                                             bbo_d.data_ptr(), nb, plan.handle,
+                                             blob_d.data_ptr() if blob_d is not None else None,
+                                             int(bool_mask), out.data_ptr() if out.numel() else None, _stream()))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()

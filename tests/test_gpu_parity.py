@@ -1,0 +1,256 @@
+"""GPU parity: the HIP path against the reference's outputs and the oracle.
+
+Integer work is compared bit-exactly:
+  * golden fixtures of the reference's CPU ops (tests/golden/ref_cases.npz,
+    ref_digests.json), through the C ABI;
+  * the C oracle (oracle/) on seeded random corpora and query batches,
+    including bundles wider than the LDS tile, int16 position wrap-around,
+    k / hash_k variants and batches large enough to need several passes;
+  * the reference's own test shapes through torch.ops.st (the drop-in path),
+    after test_bloom_index_search.py:41-269 and test_bloom_indexer.py:31-150.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from oracle import parser_oracle as P
+from tests import _fixtures as G
+from tests import gpu_helpers as H
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a HIP device")
+    import silvertorch_amd.ops._load_ops  # noqa: F401
+
+
+def _plans(queries, hash_k, max_sub=5):
+    _, data, offs = P.parse_batch(queries, hash_k, True, max_sub)
+    return np.frombuffer(data, dtype=np.int8).copy(), np.array(offs, dtype=np.int64)
+
+
+@pytest.mark.parametrize("name", G.case_names())
+def test_build_matches_reference(name):
+    c = G.case(name)
+    H.note(f"[build] case={name} docs={(len(c['offsets']) - 1) // len(c['ids'])} k={c['build_k']}")
+    index, bbo = H.build(c["ids"], c["offsets"], c["values"], c["b_multiplier"], c["build_k"])
+    np.testing.assert_array_equal(bbo, c["bundle_b_offsets"])
+    np.testing.assert_array_equal(index, c["index"])
+
+
+@pytest.mark.parametrize("name", G.case_names())
+@pytest.mark.parametrize("bool_mask", [False, True])
+def test_search_matches_reference(name, bool_mask):
+    c = G.case(name)
+    H.note(f"[search] case={name} k={c['k']} hash_k={c['hash_k']} bool={bool_mask}")
+    out = H.search(c["index"], c["bundle_b_offsets"], c["plans_data"], c["plans_offsets"], c["k"], c["hash_k"], bool_mask)
+    want = O.unpack_bool(c["packed"]) if bool_mask else c["packed"]
+    np.testing.assert_array_equal(out, want)
+
+
+def test_cfg1_digest():
+    from silvertorch_amd import synthetic as S
+
+    d = G.digests()["cfg1"]
+    cspec, qspec = S.CONFIGS["cfg1"]
+    corp = S.make_corpus(cspec, seed=0)
+    H.note("[cfg1] build + search on GPU")
+    index, bbo = H.build(corp.feature_ids, corp.feature_offsets, corp.feature_values, cspec.b_multiplier, cspec.k)
+    assert G.sha(index) == d["index"] and G.sha(bbo) == d["bundle_b_offsets"]
+    pd, po = _plans(S.make_queries(cspec, qspec, seed=0), cspec.hash_k)
+    packed = H.search(index, bbo, pd, po, cspec.k, cspec.hash_k)
+    assert G.sha(packed) == d["packed"]
+
+
+def test_wide_bundles_global_path_and_int16_wrap():
+    ids, offs, vals, w = G.wide_corpus()
+    H.note("[wide] bundles of 32768 and 40000 rows")
+    index, bbo = H.build(ids, offs, vals, w["b_multiplier"], w["k"])
+    assert bbo.tolist() == w["bundle_b_offsets"]
+    assert G.sha(index) == w["index"]
+    pd, po = _plans(w["queries"], 7)
+    assert G.sha(H.search(index, bbo, pd, po, w["k"], 7)) == w["packed"]
+
+
+def _random_corpus(rng, n, F, lo, hi, vocab):
+    cnt = rng.integers(lo, hi + 1, (n, F))
+    offs = np.concatenate([[0], np.cumsum(cnt.reshape(-1))]).astype(np.int64)
+    vals = rng.integers(-vocab // 4, vocab, int(offs[-1])).astype(np.int64)
+    ids = (rng.permutation(50)[:F] - 10).astype(np.int32)
+    return ids, offs, vals
+
+
+def _random_queries(rng, ids, vocab, n, max_terms, deep=False):
+    out = []
+    for _ in range(n):
+        def leaf():
+            t = f"{int(rng.choice(ids))}:{int(rng.integers(-vocab // 4, vocab))}"
+            return ("NOT " + t) if rng.random() < 0.2 else t
+
+        def tree(d):
+            if d == 0 or rng.random() < 0.3:
+                return leaf()
+            parts = [tree(d - 1) for _ in range(int(rng.integers(1, max_terms + 1)))]
+            s = (" AND " if rng.random() < 0.5 else " OR ").join(parts)
+            s = f"({s})"
+            return ("NOT " + s) if rng.random() < 0.15 else s
+
+        q = tree(4 if deep else 2)
+        out.append("" if rng.random() < 0.03 else q)
+    return out
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_vs_oracle(seed):
+    rng = np.random.default_rng(1000 + seed)
+    n = int(rng.integers(1, 20000))
+    F = int(rng.integers(1, 6))
+    hi = [3, 6, 40, 3, 8, 2][seed]  # seed 2 gives bundles wider than the LDS tile
+    vocab = int(rng.integers(10, 5000))
+    ids, offs, vals = _random_corpus(rng, n, F, 0, hi, vocab)
+    kb = int(rng.integers(1, 11))
+    bm = float(rng.choice([1.1, 2.0, 5.0, 9.5]))
+    H.note(f"[random] seed={seed} docs={n} F={F} max_cnt={hi} k={kb} bm={bm}")
+    index, bbo = H.build(ids, offs, vals, bm, kb)
+    want_index, want_bbo = O.bloom_build(ids, offs, vals, bm, kb)
+    np.testing.assert_array_equal(bbo, want_bbo)
+    np.testing.assert_array_equal(index, want_index)
+    queries = _random_queries(rng, ids, vocab, int(rng.integers(1, 300)), 5, deep=seed % 2 == 1)
+    hk = int(rng.integers(1, 11))
+    ks = int(rng.integers(0, 12))
+    pd, po = _plans(queries, hk, int(rng.integers(1, 6)))
+    if min(ks, hk) > 10:
+        ks = 10
+    H.note(f"[random] seed={seed} queries={len(queries)} k={ks} hash_k={hk}")
+    got = H.search(index, bbo, pd, po, ks, hk)
+    np.testing.assert_array_equal(got, O.search_packed(index, bbo, pd, po, ks, hk))
+
+
+def test_many_terms_split_into_passes():
+    """More distinct terms than one LDS position area holds -> several passes."""
+    rng = np.random.default_rng(77)
+    ids, offs, vals = _random_corpus(rng, 5000, 3, 1, 3, 100000)
+    index, bbo = H.build(ids, offs, vals, 3.0, 3)
+    queries = [" OR ".join(f"{int(rng.choice(ids))}:{int(rng.integers(0, 100000))}" for _ in range(40))
+               for _ in range(120)]
+    pd, po = _plans(queries, 7, 64)
+    H.note("[passes] 4800 terms")
+    np.testing.assert_array_equal(H.search(index, bbo, pd, po, 3, 7), O.search_packed(index, bbo, pd, po, 3, 7))
+
+
+def test_edge_cases():
+    c = G.case("features10x3")
+    # no queries
+    out = H.search(c["index"], c["bundle_b_offsets"], np.zeros(0, np.int8), np.zeros(0, np.int64), 3, 7)
+    assert out.shape == (0, 32)
+    # zero docs
+    ids = np.array([1], dtype=np.int32)
+    index, bbo = H.build(ids, np.zeros(1, np.int64), np.zeros(0, np.int64), 2.0, 3)
+    assert index.size == 0 and bbo.tolist() == [0]
+    pd, po = _plans(["1:1", ""], 7)
+    assert H.search(index, bbo, pd, po, 3, 7).shape == (2, 0)
+    # docs without terms: width-0 bundles, terms match nothing, NOT / EMPTY match all
+    index, bbo = H.build(ids, np.zeros(3001, np.int64), np.zeros(0, np.int64), 2.0, 3)
+    assert bbo.tolist() == [0, 0, 0]
+    pd, po = _plans(["1:1", "NOT 1:1", ""], 7)
+    got = H.search(index, bbo, pd, po, 3, 7)
+    np.testing.assert_array_equal(got, O.search_packed(index, bbo, pd, po, 3, 7))
+    assert (got[0] == 0).all() and (got[1] == -1).all() and (got[2] == -1).all()
+
+
+# ------------------------------------------------ drop-in path (torch.ops.st)
+
+def _make_features(num_docs, num_features):  # test_bloom_index_search.py:41-53
+    ids = torch.arange(num_features, dtype=torch.int32)
+    vals, offs = [], [0]
+    for d in range(num_docs):
+        for f in range(num_features):
+            vals.append(d * 100 + f)
+            offs.append(len(vals))
+    return ids, torch.tensor(offs, dtype=torch.long), torch.tensor(vals, dtype=torch.long)
+
+
+def _oracle_for(ids, offs, vals, bm, kb, exprs, k, hk):
+    index, bbo = O.bloom_build(ids.numpy(), offs.numpy(), vals.numpy(), bm, kb)
+    pd, po = _plans(exprs, hk)
+    return index, bbo, O.search_packed(index, bbo, pd, po, k, hk)
+
+
+@pytest.mark.parametrize("exprs", [["0:0"], ["0:0 AND 1:1"], ["0:0 OR 1:1"], ["NOT 0:0"], ["0:0", "1:1", "0:0 AND 1:1"]])
+@pytest.mark.parametrize("bool_mask", [True, False])
+def test_ops_search_like_reference_tests(exprs, bool_mask):
+    st = torch.ops.st
+    ids, offs, vals = _make_features(10, 3)
+    bi, bo = st.bloom_index_build(ids.cuda(), offs.cuda(), vals.cuda(), 2.0, 7)
+    _, (pd, po) = st.parse_expression_query_batch(exprs, torch.ones(1, dtype=torch.long), 7, True, 5)
+    res = st.bloom_index_search_batch(bi, bo, pd.cuda(), po.cuda(), 3, 7, bool_mask)
+    assert res.is_cuda and res.size(0) == len(exprs)
+    assert res.dtype == (torch.bool if bool_mask else torch.long)
+    _, _, want = _oracle_for(ids, offs, vals, 2.0, 7, exprs, 3, 7)
+    want = O.unpack_bool(want) if bool_mask else want
+    np.testing.assert_array_equal(res.cpu().numpy(), want)
+    # CPU tensors go through the same HIP path (copied to the GPU and back)
+    res_cpu = st.bloom_index_search_batch(bi.cpu(), bo.cpu(), pd, po, 3, 7, bool_mask)
+    assert not res_cpu.is_cuda
+    np.testing.assert_array_equal(res_cpu.numpy(), want)
+
+
+@pytest.mark.parametrize("shape", ["basic", "single_doc", "many_docs"] + [f"k{k}" for k in (1, 3, 7, 10)])
+def test_ops_build_like_reference_tests(shape):  # test_bloom_indexer.py:112-150
+    st = torch.ops.st
+    k, bm = 7, 2.0
+    if shape == "basic":
+        ids, offs, vals = _make_features(10, 3)
+    elif shape == "single_doc":
+        ids, offs, vals = torch.tensor([0], dtype=torch.int32), torch.tensor([0, 1]), torch.tensor([42])
+        k = 3
+    elif shape == "many_docs":
+        n = 32 * 64 * 2 + 10
+        ids, offs, vals = torch.tensor([0], dtype=torch.int32), torch.arange(n + 1), torch.arange(n)
+        k = 3
+    else:
+        ids, offs, vals = _make_features(5, 2)
+        k = int(shape[1:])
+    bi, bo = st.bloom_index_build(ids.cuda(), offs.cuda(), vals.cuda(), bm, k)
+    assert bi.dtype == torch.long and bi.dim() == 1 and bi.numel() > 0
+    assert bo[0].item() == 0 and bo[-1].item() > 0
+    want_i, want_b = O.bloom_build(ids.numpy(), offs.numpy(), vals.numpy(), bm, k)
+    np.testing.assert_array_equal(bi.cpu().numpy(), want_i)
+    np.testing.assert_array_equal(bo.cpu().numpy(), want_b)
+    if shape == "many_docs":
+        assert bo.numel() > 2
+    bi2, bo2 = st.bloom_index_build(ids, offs, vals, bm, k)  # CPU tensors, same HIP path
+    assert torch.equal(bi2, bi.cpu()) and torch.equal(bo2, bo.cpu())
+
+
+def test_ops_readme_example():
+    """README.md:118-196 with CPU tensors, as the README writes it."""
+    st = torch.ops.st
+    ids = torch.tensor([1, 2], dtype=torch.int32)
+    vals = torch.tensor([100, 200, 201, 100, 101, 200, 102, 202, 100, 200, 203], dtype=torch.long)
+    offs = torch.tensor([0, 1, 3, 5, 6, 7, 8, 9, 11], dtype=torch.long)
+    bi, bo = st.bloom_index_build(ids, offs, vals, 5.0, 3)
+    queries = ["1:100", "1:100 AND NOT 2:201", "1:102 OR 2:203"]
+    _, (pd, po) = st.parse_expression_query_batch(queries, torch.full((3,), 3, dtype=torch.long), 7, True, 5)
+    mask = st.bloom_index_search_batch(bi.cuda(), bo.cuda(), pd.cuda(), po.cuda(), 3, 7, True)
+    hits = [m.nonzero().flatten().tolist() for m in mask[:, :4].cpu()]
+    assert hits == [[0, 1, 3], [1, 3], [2, 3]]
+    assert mask.shape == (3, 2048)
+
+
+def test_ops_column_info():  # test_bloom_index_search.py:216-241
+    st = torch.ops.st
+    offsets = torch.tensor([0, 100, 200, 63, 64], dtype=torch.long)
+    lengths = torch.tensor([100, 50, 80, 0, 1], dtype=torch.long)
+    counts, starts, firsts = st.generate_column_info_for_clusters(offsets.cuda(), lengths.cuda())
+    assert counts.is_cuda and counts.dtype == torch.int32 and starts.dtype == torch.int32
+    assert firsts.dtype == torch.int8
+    want_s = (offsets // 64).tolist()
+    want_f = (offsets % 64).tolist()
+    want_c = [(l + f + 63) // 64 if l > 0 else 0 for l, f in zip(lengths.tolist(), want_f)]
+    assert counts.cpu().tolist() == want_c and starts.cpu().tolist() == want_s and firsts.cpu().tolist() == want_f

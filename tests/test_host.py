@@ -1,0 +1,181 @@
+"""CPU tests of the product's host side and of the C ABI boundary.
+
+* the C-ABI library loads and exports every function include/*.h declares;
+* the product parser (C++, behind the C ABI and torch.ops.st) emits the
+  reference's plan bytes (tests/golden/ref_parser.json) and raises with the
+  reference's messages;
+* the plan compiler accepts every reference-produced plan and rejects the
+  malformed ones where the reference CPU search fails or reads out of bounds
+  (bloom_index_search.cpp:72-171);
+* the torch.ops.st schemas match the reference's (bloom_indexer.cpp:117-124,
+  bloom_index_search.cpp:549-558, expression_query_parser.cpp:457-464).
+No compute kernel is launched here.
+"""
+
+import re
+import struct
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import parser_oracle as P
+from silvertorch_amd import capi
+from tests import _fixtures as G
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions() -> list[str]:
+    text = "\n".join(p.read_text() for p in (ROOT / "include").glob("*.h"))
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(st_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = capi.lib()
+    names = declared_functions()
+    assert len(names) >= 19
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(capi.SIGNATURES)
+    assert b"gfx950" in lib.st_version()
+
+
+def test_host_murmur_matches_independent_vectors():
+    lib = capi.lib()
+    for x, y, seed, want in G.murmur_vectors():
+        assert lib.st_murmur_hash3_2x64(x, y, seed) == want
+
+
+def test_parser_matches_reference_bytes():
+    g = G.parser_golden()
+    for b in g["batches"]:
+        m, data, offs = capi.parse_expression_query_batch(g["expressions"], b["hash_k"], True, b["max_sub_queries"])
+        assert m == b["max_stack"]
+        assert data.hex() == b["data_hex"]
+        assert offs == b["offsets"]
+    m, data, offs = capi.parse_expression_query_batch(g["expressions"], 7, False, 5)
+    assert (m, len(data), len(offs)) == tuple(g["no_plan"].values())
+
+
+def test_parser_errors_match_reference():
+    for expr, msg in G.parser_golden()["errors"].items():
+        if msg is None:
+            capi.parse_expression_query_batch([expr], 7)
+            continue
+        with pytest.raises(capi.StError) as ei:
+            capi.parse_expression_query_batch([expr], 7)
+        assert str(ei.value) == msg
+
+
+def _random_expr(rng, depth=0):
+    if depth > 2 or rng.random() < 0.35:
+        t = f"{int(rng.integers(-3, 20))}:{int(rng.integers(-50, 50))}"
+        if rng.random() < 0.2:
+            t += ":0.5" if rng.random() < 0.5 else ":3"
+        return t
+    n = int(rng.integers(1, 7))
+    sep = [" AND ", " OR ", " & ", " | "][int(rng.integers(0, 4))]
+    body = sep.join(_random_expr(rng, depth + 1) for _ in range(n))
+    if rng.random() < 0.5:
+        body = f"({body})"
+    if rng.random() < 0.2:
+        body = ("NOT " if rng.random() < 0.5 else "!") + body
+    return body
+
+
+def test_parser_matches_oracle_on_random_expressions():
+    rng = np.random.default_rng(99)
+    for _ in range(60):
+        exprs = [_random_expr(rng) for _ in range(int(rng.integers(1, 8)))]
+        hk = int(rng.integers(1, 9))
+        ms = int(rng.integers(-1, 7))
+        assert capi.parse_expression_query_batch(exprs, hk, True, ms) == P.parse_batch(exprs, hk, True, ms)
+
+
+def _plan(ops, offsets, hashes, params=()):
+    """Encodes one plan in the reference's layout (bloom_index_util.cpp:81-124)."""
+    buf, offs = bytearray(), []
+    for raw in (bytes(ops), struct.pack(f"<{len(offsets)}i", *offsets),
+                struct.pack(f"<{len(params)}i", *params), struct.pack(f"<{len(hashes)}Q", *hashes)):
+        start = len(buf)
+        buf += raw + b"\0" * ((-len(raw)) % 8)
+        offs += [start, start + len(raw)]
+    return bytes(buf), offs
+
+
+def test_plan_compiler_accepts_reference_plans():
+    for name in G.case_names():
+        c = G.case(name)
+        plan = capi.SearchPlan(c["plans_data"].tobytes(), c["plans_offsets"], c["k"], c["hash_k"])
+        assert plan.num_queries == len(c["plans_offsets"]) // 8
+        assert len(plan.blob()) > 0
+
+
+@pytest.mark.parametrize("ops,offsets,nh,msg", [
+    ([9], [0, 0], 0, "unknown operator: 9"),
+    ([4, 4, 3], [0, 1, 2, 4], 14, "NOT query should have 1 parameter, but got 2"),
+    ([4, 1], [0, 1, 4], 7, "pops 3 values from a shorter stack"),
+    ([], [0], 0, "has no operators"),
+    ([4, 4, 1], [0, 1, 2, 4], 7, "needs hashes [7, 14)"),
+    ([4, 1], [0, 1], 7, "has no child count"),
+])
+def test_plan_compiler_rejects_malformed_plans(ops, offsets, nh, msg):
+    data, offs = _plan(ops, offsets, list(range(nh)))
+    with pytest.raises(capi.StError, match=re.escape(msg)):
+        capi.SearchPlan(data, offs, 3, 7)
+
+
+def test_plan_compiler_limits():
+    data, offs = _plan([4], [0, 1], list(range(11)))
+    with pytest.raises(capi.StError, match="at most 10"):
+        capi.SearchPlan(data, offs, 11, 11)
+    capi.SearchPlan(data, offs, 11, 10)  # k_eff = min(k, hash_k) = 10
+    capi.SearchPlan(data, offs, 0, 7)  # every term is all ones
+    with pytest.raises(capi.StError, match="outside plans_data"):
+        capi.SearchPlan(data, [0, 1, 8, 12, 16, 16, 16, 10_000], 3, 7)
+
+
+def test_torch_ops_schemas_and_cpu_parser():
+    import torch
+
+    import silvertorch_amd.ops._load_ops  # noqa: F401
+
+    st = torch.ops.st
+    schemas = {s.name: str(s) for s in torch._C._jit_get_all_schemas() if s.name.startswith("st::")}
+    assert set(schemas) >= {"st::bloom_index_build", "st::bloom_index_search_batch",
+                            "st::parse_expression_query_batch", "st::generate_column_info_for_clusters"}
+    assert "bool fast_build=False" in schemas["st::bloom_index_build"]
+    assert "bool return_bool_mask=True" in schemas["st::bloom_index_search_batch"]
+    assert "int max_sub_queries=5" in schemas["st::parse_expression_query_batch"]
+    g = G.parser_golden()
+    m, (pd, po) = st.parse_expression_query_batch(g["expressions"], torch.ones(1, dtype=torch.long), 7, True, 5)
+    want = next(b for b in g["batches"] if b["hash_k"] == 7 and b["max_sub_queries"] == 5)
+    assert m == want["max_stack"]
+    assert pd.dtype == torch.int8 and po.dtype == torch.int64
+    assert pd.numpy().tobytes().hex() == want["data_hex"]
+    with pytest.raises(RuntimeError, match="Unknown keyword"):
+        st.parse_expression_query_batch(["1:1 XOR 2:2"], torch.ones(1, dtype=torch.long), 7)
+
+
+def test_cpu_tensor_calls_fail_loudly_without_gpu():
+    import torch
+
+    import silvertorch_amd.ops._load_ops  # noqa: F401
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible; CPU-tensor calls run on it")
+    c = G.case("readme")
+    with pytest.raises(RuntimeError, match="no GPU is visible"):
+        torch.ops.st.bloom_index_build(torch.from_numpy(c["ids"]), torch.from_numpy(c["offsets"]),
+                                       torch.from_numpy(c["values"]), 5.0, 3)
+    # argument errors come first, as in the reference CPU op (bloom_indexer.cpp:33-36)
+    with pytest.raises(RuntimeError, match="b_multiplier must be greater than 1.0"):
+        torch.ops.st.bloom_index_build(torch.from_numpy(c["ids"]), torch.from_numpy(c["offsets"]),
+                                       torch.from_numpy(c["values"]), 1.0, 3)
+    with pytest.raises(RuntimeError, match="unknown operator"):
+        data, offs = _plan([9], [0, 0], [])
+        torch.ops.st.bloom_index_search_batch(torch.from_numpy(c["index"]), torch.from_numpy(c["bundle_b_offsets"]),
+                                              torch.frombuffer(bytearray(data), dtype=torch.int8),
+                                              torch.tensor(offs, dtype=torch.long), 3, 7, False)

@@ -1,0 +1,182 @@
+"""Pins the CPU oracle before it is trusted as the parity checker.
+
+Every oracle function is checked against data the oracle did not produce:
+sklearn's independent MurmurHash3 vectors, the reference's own CPU ops
+(compiled from its sources into oracle/_ref, fixtures in tests/golden/), the
+README known answers (README.md:163-196, :255-268), brute force and
+closed-form invariants.  The last test plants mistakes in a copy of the
+oracle logic and shows the checks catch them.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from oracle import parser_oracle as P
+from tests import _fixtures as G
+
+
+def test_murmur_matches_independent_vectors():
+    for x, y, seed, want in G.murmur_vectors():
+        assert O.murmur3_pair(x, y, seed) == want
+        assert P.murmur3_pair(x, y, seed) == want
+
+
+def test_build_positions_brute_force():
+    rng = np.random.default_rng(3)
+    for _ in range(300):
+        fid, val = int(rng.integers(-50, 50)), int(rng.integers(-(1 << 40), 1 << 40))
+        k = int(rng.integers(1, 12))
+        b = int(rng.integers(k, 3 * k + 40))
+        want, seed = [], 0
+        while len(want) < k:  # first k distinct residues over seeds 0, 1, ...
+            p = P.murmur3_pair(fid, val, seed) % b
+            seed += 1
+            if p not in want:
+                want.append(p)
+        assert O.build_positions(fid, val, b, k) == want
+
+
+@pytest.mark.parametrize("name", G.case_names())
+def test_oracle_build_matches_reference(name):
+    c = G.case(name)
+    index, bbo = O.bloom_build(c["ids"], c["offsets"], c["values"], c["b_multiplier"], c["build_k"])
+    np.testing.assert_array_equal(bbo, c["bundle_b_offsets"])
+    np.testing.assert_array_equal(index, c["index"])
+
+
+@pytest.mark.parametrize("name", G.case_names())
+def test_oracle_search_matches_reference(name):
+    c = G.case(name)
+    packed = O.search_packed(c["index"], c["bundle_b_offsets"], c["plans_data"], c["plans_offsets"], c["k"], c["hash_k"])
+    np.testing.assert_array_equal(packed, c["packed"])
+
+
+def test_readme_known_answers():
+    c = G.case("readme")
+    index, bbo = O.bloom_build(c["ids"], c["offsets"], c["values"], 5.0, 3)
+    _, data, offs = P.parse_batch(c["queries"], 7)
+    packed = O.search_packed(index, bbo, np.frombuffer(data, np.int8), np.array(offs), 3, 7)
+    ids, ro = O.compact(packed, 4)
+    got = [ids[ro[q]:ro[q + 1]].tolist() for q in range(len(ro) - 1)]
+    assert got == [[0, 1, 3], [1, 3], [2, 3], [0, 1, 3], [2]]
+    assert O.unpack_bool(packed).shape == (5, 2048)  # README.md:260
+
+
+def test_parser_oracle_matches_reference_bytes():
+    g = G.parser_golden()
+    for b in g["batches"]:
+        m, data, offs = P.parse_batch(g["expressions"], b["hash_k"], True, b["max_sub_queries"])
+        assert m == b["max_stack"]
+        assert data.hex() == b["data_hex"]
+        assert offs == b["offsets"]
+    m, data, offs = P.parse_batch(g["expressions"], 7, False, 5)
+    assert (m, len(data), len(offs)) == tuple(g["no_plan"].values())
+
+
+def test_parser_oracle_errors_match_reference():
+    for expr, msg in G.parser_golden()["errors"].items():
+        if msg is None:
+            P.parse_batch([expr], 7)
+        else:
+            with pytest.raises(P.ParseError) as ei:
+                P.parse_batch([expr], 7)
+            assert str(ei.value) == msg
+
+
+def test_parser_precedence_rules():
+    # test_expression_query_parser.py:98-117
+    same = [("NOT 1:10 AND 2:20", "(NOT 1:10) AND 2:20"), ("1:10 OR 2:20 AND 3:30", "1:10 OR (2:20 AND 3:30)")]
+    for a, b in same:
+        assert P.parse_batch([a], 7) == P.parse_batch([b], 7)
+    assert P.parse_batch(["(1:10 OR 2:20) AND 3:30"], 7) != P.parse_batch(["1:10 OR 2:20 AND 3:30"], 7)
+    assert P.parse_batch(["42:100"], 7)[0] == 1
+
+
+def test_cfg1_digest():
+    from silvertorch_amd import synthetic as S
+
+    d = G.digests()["cfg1"]
+    cspec, qspec = S.CONFIGS["cfg1"]
+    corp = S.make_corpus(cspec, seed=0)
+    assert G.sha(corp.feature_offsets) == d["inputs"]["offsets"]
+    assert G.sha(corp.feature_values) == d["inputs"]["values"]
+    index, bbo = O.bloom_build(corp.feature_ids, corp.feature_offsets, corp.feature_values, cspec.b_multiplier, cspec.k)
+    assert G.sha(index) == d["index"] and G.sha(bbo) == d["bundle_b_offsets"]
+    queries = S.make_queries(cspec, qspec, seed=0)
+    _, data, offs = P.parse_batch(queries, cspec.hash_k)
+    pd, po = np.frombuffer(data, np.int8), np.array(offs, dtype=np.int64)
+    assert G.sha(pd) == d["plans_data"] and G.sha(po) == d["plans_offsets"]
+    packed = O.search_packed(index, bbo, pd, po, cspec.k, cspec.hash_k)
+    assert G.sha(packed) == d["packed"]
+    _, ro = O.compact(packed, cspec.num_docs)
+    assert np.diff(ro).tolist() == d["match_counts"]
+
+
+def test_wide_bundles_int16_wrap_digest():
+    ids, offs, vals, w = G.wide_corpus()
+    index, bbo = O.bloom_build(ids, offs, vals, w["b_multiplier"], w["k"])
+    assert bbo.tolist() == w["bundle_b_offsets"]
+    assert G.sha(index) == w["index"]
+    _, data, po = P.parse_batch(w["queries"], 7)
+    packed = O.search_packed(index, bbo, np.frombuffer(data, np.int8), np.array(po), w["k"], 7)
+    assert G.sha(packed) == w["packed"]
+
+
+def test_build_invariants():
+    rng = np.random.default_rng(11)
+    n, F, k = 5000, 2, 4
+    cnt = rng.integers(0, 3, (n, F))
+    offs = np.concatenate([[0], np.cumsum(cnt.reshape(-1))]).astype(np.int64)
+    vals = rng.integers(0, 1 << 40, int(offs[-1])).astype(np.int64)
+    ids = np.array([3, 9], dtype=np.int32)
+    index, bbo = O.bloom_build(ids, offs, vals, 2.5, k)
+    # closed form of the widths
+    per_doc = cnt.sum(1)
+    for i in range(len(bbo) - 1):
+        m = per_doc[i * 2048:(i + 1) * 2048].max()
+        assert bbo[i + 1] - bbo[i] == int(float(m * k) * 2.5)
+    # a doc's bits are the union of its terms' positions (no false negatives,
+    # nothing extra)
+    words = index.view(np.uint64)
+    for d in rng.choice(n, 60, replace=False):
+        bnd, col, bit = d // 2048, (d % 2048) // 64, np.uint64(1) << np.uint64(63 - d % 64)
+        b = int(bbo[bnd + 1] - bbo[bnd])
+        want = set()
+        for f in range(F):
+            for j in range(offs[d * F + f], offs[d * F + f + 1]):
+                want |= set(O.build_positions(int(ids[f]), int(vals[j]), b, k))
+        have = {p for p in range(b) if words[(bbo[bnd] + p) * 32 + col] & bit}
+        assert have == want
+
+
+def test_search_identities():
+    c = G.case("random0")
+    base = ["1:1", "1:2", "4:5"]
+    exprs = [f"NOT ({base[0]} AND {base[1]})", f"NOT {base[0]} OR NOT {base[1]}", "", f"{base[2]} OR NOT {base[2]}"]
+    _, data, offs = P.parse_batch(exprs, c["hash_k"])
+    packed = O.search_packed(c["index"], c["bundle_b_offsets"], np.frombuffer(data, np.int8), np.array(offs), c["k"], c["hash_k"])
+    np.testing.assert_array_equal(packed[0], packed[1])  # De Morgan
+    assert (packed[2] == -1).all() and (packed[3] == -1).all()  # EMPTY, x | ~x
+
+
+def test_planted_mistakes_are_caught():
+    """Variants of the oracle logic with a plausible bug must fail the pins."""
+    x, y, seed, want = G.murmur_vectors()[10]
+    # (1) swapped key halves, (2) seed off by one
+    assert P.murmur3_pair(y, x, seed) != want
+    assert P.murmur3_pair(x, y, seed + 1) != want
+    # (3) LSB-first doc order in the words, (4) transposed [column][row] layout
+    c = G.case("readme")
+    index, _ = O.bloom_build(c["ids"], c["offsets"], c["values"], 5.0, 3)
+    w = index.view(np.uint64)
+    rev = np.array([int(f"{int(v):064b}"[::-1], 2) for v in w], dtype=np.uint64)
+    assert not np.array_equal(rev.view(np.int64), c["index"])
+    rows = len(index) // 32
+    assert not np.array_equal(index.reshape(rows, 32).T.reshape(-1), c["index"])
+    # (5) evaluating with the int32 cast of the CUDA path instead of int16
+    ids, offs, vals, wd = G.wide_corpus()
+    idx, bbo = O.bloom_build(ids, offs, vals, wd["b_multiplier"], wd["k"])
+    h = P.murmur3_pair(5, int(vals[4200]), 0)
+    b1 = int(bbo[2] - bbo[1])
+    assert np.int16(np.int64(h % b1).astype(np.int16)) != h % b1 or h % b1 < 32768
