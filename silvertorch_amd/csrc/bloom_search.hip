@@ -46,7 +46,6 @@ struct SearchArgs {
   const int64_t* bundle_offsets;
   int64_t num_bundles;
   const uint32_t* wave_off;
-  const uint32_t* rows;
   const uint32_t* insn_start;
   const uint32_t* insns;
   const uint64_t* hashes;
@@ -125,10 +124,274 @@ __device__ __forceinline__ void store_bool32(uint8_t* dst, uint32_t bits) {
   __builtin_nontemporal_store(u32x4{w[4], w[5], w[6], w[7]}, d + 1);
 }
 
+// Executes one non-TERM operation on the accumulator machine.
+__device__ __forceinline__ void exec_op(uint32_t op, uint32_t& acc,
+                                        uint32_t (&stk)[kSearchMaxStack],
+                                        uint32_t& sp) {
+  const uint32_t code = op & 7u;
+  uint32_t v;
+  if (code == kInsConst) {
+    v = ~0u;
+  } else if (code == kInsPush) {
+    stk[sp++] = acc;
+    return;
+  } else if (code == kInsPop) {
+    v = acc;
+    acc = stk[--sp];
+  } else {  // kInsNot
+    acc = ~acc;
+    return;
+  }
+  if (op & 32u) v = ~v;
+  const uint32_t mode = (op >> 3) & 3u;
+  acc = mode == kModeSet ? v : (mode == kModeAnd ? (acc & v) : (acc | v));
+}
+
+__device__ __forceinline__ uint32_t combine(uint32_t op, uint32_t acc, uint32_t v) {
+  if (op & 32u) v = ~v;
+  const uint32_t mode = (op >> 3) & 3u;
+  return mode == kModeSet ? v : (mode == kModeAnd ? (acc & v) : (acc | v));
+}
+
+// Where the rows of the current bundle are read from.
+struct RowSource {
+  const uint32_t* pos;    // LDS position lists
+  const char* tile_lane;  // LDS tile + this lane's byte offset
+  const uint32_t* index32;
+  int64_t index_numel;
+  int64_t start;          // first row of the bundle
+  int lane;
+  bool staged;            // rows in the LDS tile (else global memory)
+};
+
+// Position list of the term whose list starts at byte `off` of the LDS
+// position area.
+template <int KP>
+__device__ __forceinline__ void load_positions(const RowSource& rs, uint32_t off,
+                                               uint32_t (&p)[KP]) {
+  const uint32_t* pp = reinterpret_cast<const uint32_t*>(
+      reinterpret_cast<const char*>(rs.pos) + off);
+#pragma unroll
+  for (int r = 0; r < KP; r += 4) {
+    const u32x4 q4 = *reinterpret_cast<const u32x4*>(pp + r);
+    p[r] = q4.x;
+    p[r + 1] = q4.y;
+    p[r + 2] = q4.z;
+    p[r + 3] = q4.w;
+  }
+}
+
+// Word of one term for this lane's 32-bit half column: AND of its K rows.
+// STAGED selects the LDS tile or global memory at compile time, so the row
+// reads of several terms form one straight-line block.
+template <int K, int KP, bool STAGED>
+__device__ __forceinline__ uint32_t term_word(const RowSource& rs, const uint32_t (&p)[KP]) {
+  uint32_t v = ~0u;
+  if constexpr (STAGED) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) v &= *reinterpret_cast<const uint32_t*>(rs.tile_lane + p[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const int32_t r = static_cast<int32_t>(p[j]);
+      uint32_t word = 0;
+      if (r != kPosZeros) {
+        const int64_t row = rs.start + r;
+        if (row >= 0 && (row * 32 + (rs.lane >> 1)) < rs.index_numel)
+          word = rs.index32[row * 64 + rs.lane];
+      }
+      v &= word;
+    }
+  }
+  return v;
+}
+
+// Flat-form query with exactly T literals: every position list, then every
+// row word, then the branch-free OR-of-ANDs fold.
+template <int K, int KP, bool STAGED, int T>
+__device__ __forceinline__ uint32_t eval_flat_fixed(const RowSource& rs, const u32x4* lit) {
+  uint32_t p[T > 0 ? T : 1][KP];
+#pragma unroll
+  for (int j = 0; j < T; ++j) load_positions<KP>(rs, lit[j].x, p[j]);
+  uint32_t w[T > 0 ? T : 1];
+#pragma unroll
+  for (int j = 0; j < T; ++j) w[j] = term_word<K, KP, STAGED>(rs, p[j]);
+  uint32_t res = 0, acc = 0;
+#pragma unroll
+  for (int j = 0; j < T; ++j) {
+    const u32x4 L = lit[j];
+    res |= acc & L.z;
+    acc = (acc | L.z) & (w[j] ^ L.y);
+  }
+  return res | acc;
+}
+
+// Flat-form query of any length, in groups of G literals.
+template <int K, int KP, bool STAGED, int G>
+__device__ __forceinline__ uint32_t eval_flat_loop(const RowSource& rs, const u32x4* lit,
+                                                   uint32_t T) {
+  uint32_t res = 0, acc = 0;
+  for (uint32_t base = 0; base < T; base += G) {
+    const uint32_t n = min(static_cast<uint32_t>(G), T - base);
+    uint32_t p[G][KP];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (j < n) load_positions<KP>(rs, lit[base + j].x, p[j]);
+    uint32_t w[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (j < n) w[j] = term_word<K, KP, STAGED>(rs, p[j]);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if (j < n) {
+        const u32x4 L = lit[base + j];
+        res |= acc & L.z;
+        acc = (acc | L.z) & (w[j] ^ L.y);
+      }
+    }
+  }
+  return res | acc;
+}
+
+// Flat query dispatch: fully unrolled blocks for short queries (T * KP
+// position registers bounded), the grouped loop otherwise.
+template <int K, int KP, bool STAGED, int G, int T>
+__device__ __forceinline__ uint32_t eval_flat_t(const RowSource& rs, const u32x4* lit, uint32_t n) {
+  if constexpr (T * KP <= 24) {
+    return eval_flat_fixed<K, KP, STAGED, T>(rs, lit);
+  } else {
+    return eval_flat_loop<K, KP, STAGED, G>(rs, lit, n);
+  }
+}
+
+template <int K, int KP, bool STAGED, int G>
+__device__ __forceinline__ uint32_t eval_flat(const RowSource& rs, const u32x4* lit, uint32_t T) {
+  switch (T) {
+    case 0: return 0;
+    case 1: return eval_flat_t<K, KP, STAGED, G, 1>(rs, lit, T);
+    case 2: return eval_flat_t<K, KP, STAGED, G, 2>(rs, lit, T);
+    case 3: return eval_flat_t<K, KP, STAGED, G, 3>(rs, lit, T);
+    case 4: return eval_flat_t<K, KP, STAGED, G, 4>(rs, lit, T);
+    case 5: return eval_flat_t<K, KP, STAGED, G, 5>(rs, lit, T);
+    case 6: return eval_flat_t<K, KP, STAGED, G, 6>(rs, lit, T);
+    default: return eval_flat_loop<K, KP, STAGED, G>(rs, lit, T);
+  }
+}
+
+// Stack-form query: term words in groups of G, operations walked in order.
+template <int K, int KP, bool STAGED, int G>
+__device__ __forceinline__ uint32_t eval_stack(const RowSource& rs, const uint32_t* prog,
+                                               uint32_t T, uint32_t nops) {
+  const uint32_t* tref = prog + kProgHeaderWords;
+  const uint32_t* ops = tref + T;
+  uint32_t acc = 0;
+  uint32_t stk[kSearchMaxStack];
+  uint32_t sp = 0;
+  uint32_t i = 0;
+  for (uint32_t base = 0; base < T; base += G) {
+    const uint32_t n = min(static_cast<uint32_t>(G), T - base);
+    uint32_t p[G][KP];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (j < n) load_positions<KP>(rs, tref[base + j], p[j]);
+    uint32_t w[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (j < n) w[j] = term_word<K, KP, STAGED>(rs, p[j]);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if (j < n) {
+        for (;;) {
+          const uint32_t op = ops[i++];
+          if ((op & 7u) == kInsTerm) {
+            acc = combine(op, acc, w[j]);
+            break;
+          }
+          exec_op(op, acc, stk, sp);
+        }
+      }
+    }
+  }
+  for (; i < nops; ++i) exec_op(ops[i], acc, stk, sp);
+  return acc;
+}
+
+// FastMod64 for a divisor below 2^32 with 32-bit divides only:
+// (2^64-1)/d = ((2^32-1)/d) * 2^32 + (((2^32-1) % d) * 2^32 + 2^32-1) / d.
+__device__ __forceinline__ FastMod64 make_fastmod_dev(uint64_t d) {
+  if (d == 0 || (d >> 32)) return make_fastmod(d);
+  const uint32_t d32 = static_cast<uint32_t>(d);
+  const uint32_t qh = 0xFFFFFFFFu / d32;
+  const uint32_t rh = 0xFFFFFFFFu % d32;
+  const uint64_t n = (static_cast<uint64_t>(rh) << 32) | 0xFFFFFFFFull;  // < d * 2^32
+  uint64_t ql = static_cast<uint64_t>(static_cast<double>(n) / static_cast<double>(d32));
+  // the double quotient is within one of the true one; fix it exactly
+  while (ql * d32 > n) --ql;
+  while (n - ql * d32 >= d32) ++ql;
+  FastMod64 f;
+  f.d = d;
+  f.magic = (static_cast<uint64_t>(qh) << 32) + ql;
+  return f;
+}
+
+// Evaluates this wave's queries [s_begin, s_end) on one bundle and stores
+// their 32-bit halves of the bundle's 32 output words.
+template <int K, int KP, bool STAGED, int G, bool kBoolOut>
+__device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSource& rs,
+                                             uint32_t s_begin, uint32_t s_end,
+                                             int64_t bundle) {
+  const int lane = rs.lane;
+  for (uint32_t s = s_begin; s < s_end; ++s) {
+    const uint32_t* prog = a.insns + a.insn_start[s];
+    const uint32_t hdr = prog[0];
+    const uint32_t row = prog[1];
+    const uint32_t T = hdr & 0xFFFFu;
+    uint32_t acc;
+    if (hdr & kFlatForm) {
+      acc = eval_flat<K, KP, STAGED, G>(rs, reinterpret_cast<const u32x4*>(prog + kProgHeaderWords), T);
+      if (hdr & kFlatComplement) acc = ~acc;
+    } else {
+      acc = eval_stack<K, KP, STAGED, G>(rs, prog, T, prog[2]);
+    }
+
+    const int64_t col0 = static_cast<int64_t>(row) * a.out_cols + bundle * 32;
+    if constexpr (kBoolOut) {
+      uint8_t* dst = static_cast<uint8_t*>(a.out) + (col0 + (lane >> 1)) * 64 +
+                     ((lane & 1) ? 0 : 32);
+      store_bool32(dst, acc);
+    } else {
+      uint32_t* dst = static_cast<uint32_t*>(a.out) + col0 * 2 + lane;
+      __builtin_nontemporal_store(acc, dst);
+    }
+  }
+}
+
+// The arrays arrive as separate __restrict__ parameters (not inside
+// SearchArgs) so the compiler can prove the output stores never alias the
+// program and offset arrays and fetch those with scalar loads.
 template <int K, bool kBoolOut>
 __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
-    SearchArgs a) {
+    const int64_t* __restrict__ index, int64_t index_numel,
+    const int64_t* __restrict__ bundle_offsets, int64_t num_bundles,
+    const uint32_t* __restrict__ wave_off,
+    const uint32_t* __restrict__ insn_start, const uint32_t* __restrict__ insns,
+    const uint64_t* __restrict__ hashes, uint32_t num_terms, int32_t hash_k,
+    int64_t out_cols, void* __restrict__ out) {
+  SearchArgs a;
+  a.index = index;
+  a.index_numel = index_numel;
+  a.bundle_offsets = bundle_offsets;
+  a.num_bundles = num_bundles;
+  a.wave_off = wave_off;
+  a.insn_start = insn_start;
+  a.insns = insns;
+  a.hashes = hashes;
+  a.num_terms = num_terms;
+  a.hash_k = hash_k;
+  a.out_cols = out_cols;
+  a.out = out;
   constexpr int KP = K <= 4 ? 4 : (K <= 8 ? 8 : 12);
+  constexpr int G = KP == 4 ? 4 : (KP == 8 ? 2 : 1);  // terms fetched together
   __shared__ u32x4 tile[(kSearchTileRows + 2) * 16];
   __shared__ uint32_t pos[kSearchPosSlots];
 
@@ -166,7 +429,7 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
       }
     }
     if (b != prev_b) {
-      const FastMod64 fm = make_fastmod(static_cast<uint64_t>(b));
+      const FastMod64 fm = make_fastmod_dev(static_cast<uint64_t>(b));
       for (uint32_t u = tid; u < a.num_terms; u += kSearchThreads) {
         int16_t found[K];
 #pragma unroll
@@ -196,76 +459,26 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     if (next < a.num_bundles) prefetch_tile(a, next, pre);
 
     // Evaluate this wave's queries on the bundle.
-    for (uint32_t s = s_begin; s < s_end; ++s) {
-      const uint32_t i0 = a.insn_start[s];
-      const uint32_t i1 = a.insn_start[s + 1];
-      uint32_t acc = 0;
-      uint32_t stk[kSearchMaxStack];
-      uint32_t sp = 0;
-      for (uint32_t i = i0; i < i1; ++i) {
-        const uint32_t w = a.insns[i];
-        const uint32_t op = w & 7u;
-        const uint32_t mode = (w >> 3) & 3u;
-        uint32_t v;
-        if (op == kInsTerm) {
-          const uint32_t* pp = pos + (w >> 6) * KP;
-          uint32_t p[KP];
-#pragma unroll
-          for (int j = 0; j < KP; j += 4) {
-            const u32x4 q4 = *reinterpret_cast<const u32x4*>(pp + j);
-            p[j] = q4.x;
-            p[j + 1] = q4.y;
-            p[j + 2] = q4.z;
-            p[j + 3] = q4.w;
-          }
-          v = ~0u;
-          if (staged) {
-#pragma unroll
-            for (int j = 0; j < K; ++j)
-              v &= *reinterpret_cast<const uint32_t*>(tile_lane + p[j]);
-          } else {
-#pragma unroll
-            for (int j = 0; j < K; ++j) {
-              const int32_t r = static_cast<int32_t>(p[j]);
-              uint32_t word = 0;
-              if (r != kPosZeros) {
-                const int64_t row = start + r;
-                if (row >= 0 && (row * 32 + (lane >> 1)) < a.index_numel)
-                  word = index32[row * 64 + lane];
-              }
-              v &= word;
-            }
-          }
-        } else if (op == kInsConst) {
-          v = ~0u;
-        } else if (op == kInsPush) {
-          stk[sp++] = acc;
-          continue;
-        } else if (op == kInsPop) {
-          v = acc;
-          acc = stk[--sp];
-        } else {  // kInsNot
-          acc = ~acc;
-          continue;
-        }
-        if (w & 32u) v = ~v;
-        acc = mode == kModeSet ? v : (mode == kModeAnd ? (acc & v) : (acc | v));
-      }
-
-      const int64_t col0 = static_cast<int64_t>(a.rows[s]) * a.out_cols + bundle * 32;
-      if constexpr (kBoolOut) {
-        uint8_t* dst = static_cast<uint8_t*>(a.out) + (col0 + (lane >> 1)) * 64 +
-                       ((lane & 1) ? 0 : 32);
-        store_bool32(dst, acc);
-      } else {
-        uint32_t* dst = static_cast<uint32_t*>(a.out) + col0 * 2 + lane;
-        __builtin_nontemporal_store(acc, dst);
-      }
+    RowSource rs;
+    rs.pos = pos;
+    rs.tile_lane = tile_lane;
+    rs.index32 = index32;
+    rs.index_numel = a.index_numel;
+    rs.start = start;
+    rs.lane = lane;
+    rs.staged = staged;
+    if (staged) {
+      eval_queries<K, KP, true, G, kBoolOut>(a, rs, s_begin, s_end, bundle);
+    } else {
+      eval_queries<K, KP, false, G, kBoolOut>(a, rs, s_begin, s_end, bundle);
     }
   }
 }
 
-using KernelFn = void (*)(SearchArgs);
+using KernelFn = void (*)(const int64_t*, int64_t, const int64_t*, int64_t,
+                          const uint32_t*, const uint32_t*,
+                          const uint32_t*, const uint64_t*, uint32_t, int32_t,
+                          int64_t, void*);
 
 template <int K>
 KernelFn pick(bool bool_out) {
@@ -339,7 +552,6 @@ extern "C" int st_bloom_index_search_batch(
       a.bundle_offsets = bundle_b_offsets;
       a.num_bundles = num_bundles;
       a.wave_off = reinterpret_cast<const uint32_t*>(blob + bt.off_wave);
-      a.rows = reinterpret_cast<const uint32_t*>(blob + bt.off_row);
       a.insn_start = reinterpret_cast<const uint32_t*>(blob + bt.off_insn_start);
       a.insns = reinterpret_cast<const uint32_t*>(blob + bt.off_insns);
       a.hashes = reinterpret_cast<const uint64_t*>(blob + bt.off_hashes);
@@ -348,7 +560,10 @@ extern "C" int st_bloom_index_search_batch(
       a.out_cols = num_bundles * 32;
       a.out = out;
       hipLaunchKernelGGL(fn, dim3(grid), dim3(kSearchThreads), 0,
-                         static_cast<hipStream_t>(stream), a);
+                         static_cast<hipStream_t>(stream), a.index, a.index_numel,
+                         a.bundle_offsets, a.num_bundles, a.wave_off,
+                         a.insn_start, a.insns, a.hashes, a.num_terms, a.hash_k,
+                         a.out_cols, a.out);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess)
         throw Error(ST_ERR_HIP, cat("search kernel launch failed: ",

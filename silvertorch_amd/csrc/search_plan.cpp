@@ -145,7 +145,139 @@ int normalize(Tree& t, int id) {
   return id;
 }
 
-void emit_leaf(const Tree& t, int id, uint32_t mode, std::vector<uint32_t>& out) {
+struct CompiledQuery {
+  std::vector<uint32_t> terms;  // stack form: term ids in consumption order
+  std::vector<uint32_t> ops;    // stack form: operations
+  int need = 0;
+  bool flat = false;            // flat form: OR of AND-groups
+  bool complement = false;
+  struct FlatLit {
+    uint32_t term;
+    bool neg;
+    bool first;
+  };
+  std::vector<FlatLit> lits;    // flat form: literals, group by group
+};
+
+// ---------------------------------------------------------------- flat form
+// Disjunctive normal form of a (sub)tree or of its complement, with the
+// negations pushed onto the terms (De Morgan).  Exact for 64-bit words since
+// every bit obeys Boolean algebra independently.  Groups holding a term and
+// its negation are dropped (their AND is 0), repeated literals are merged.
+
+struct Lit {
+  uint32_t term;
+  bool neg;
+  bool operator<(const Lit& o) const {
+    return term != o.term ? term < o.term : neg < o.neg;
+  }
+  bool operator==(const Lit& o) const { return term == o.term && neg == o.neg; }
+};
+
+struct Dnf {
+  bool is_true = false;             // the constant all-ones
+  std::vector<std::vector<Lit>> groups;  // empty and !is_true: constant zero
+  size_t literals() const {
+    size_t n = 0;
+    for (const auto& g : groups) n += g.size();
+    return n;
+  }
+};
+
+Dnf dnf_true() {
+  Dnf d;
+  d.is_true = true;
+  return d;
+}
+
+// Conjunction of two DNFs by distribution; false when the result exceeds cap.
+bool dnf_and(const Dnf& a, const Dnf& b, size_t cap, Dnf& out) {
+  if (a.is_true) { out = b; return true; }
+  if (b.is_true) { out = a; return true; }
+  Dnf r;
+  for (const auto& ga : a.groups) {
+    for (const auto& gb : b.groups) {
+      std::vector<Lit> g(ga);
+      g.insert(g.end(), gb.begin(), gb.end());
+      std::sort(g.begin(), g.end());
+      g.erase(std::unique(g.begin(), g.end()), g.end());
+      bool contradiction = false;
+      for (size_t i = 1; i < g.size(); ++i)
+        contradiction |= g[i].term == g[i - 1].term;  // t and ~t
+      if (contradiction) continue;
+      r.groups.push_back(std::move(g));
+      if (r.literals() > cap) return false;
+    }
+  }
+  out = std::move(r);
+  return true;
+}
+
+bool to_dnf(const Tree& t, int id, bool negated, size_t cap, Dnf& out) {
+  const Node& n = t.nodes[id];
+  switch (n.kind) {
+    case NodeKind::kTerm:
+      out = Dnf();
+      out.groups.push_back({Lit{n.term, negated}});
+      return true;
+    case NodeKind::kConst:
+      out = (n.ones != negated) ? dnf_true() : Dnf();
+      return true;
+    case NodeKind::kNot:
+      return to_dnf(t, n.kids[0], !negated, cap, out);
+    case NodeKind::kAnd:
+    case NodeKind::kOr: {
+      const bool conj = (n.kind == NodeKind::kAnd) != negated;
+      Dnf acc = conj ? dnf_true() : Dnf();
+      for (int c : n.kids) {
+        Dnf d;
+        if (!to_dnf(t, c, negated, cap, d)) return false;
+        if (conj) {
+          Dnf next;
+          if (!dnf_and(acc, d, cap, next)) return false;
+          acc = std::move(next);
+        } else {
+          if (acc.is_true) continue;
+          if (d.is_true) {
+            acc = dnf_true();
+            continue;
+          }
+          for (auto& g : d.groups) acc.groups.push_back(std::move(g));
+          if (acc.literals() > cap) return false;
+        }
+      }
+      out = std::move(acc);
+      return true;
+    }
+  }
+  return false;
+}
+
+// Fills cq's flat form when the query (or its complement) has a DNF of at
+// most kFlatMaxLiterals literals.
+bool try_flat(const Tree& t, int root, CompiledQuery& cq) {
+  Dnf direct, inverse;
+  const bool ok_d = to_dnf(t, root, false, kFlatMaxLiterals, direct);
+  const bool ok_i = to_dnf(t, root, true, kFlatMaxLiterals, inverse);
+  if (!ok_d && !ok_i) return false;
+  const bool use_inverse =
+      !ok_d || (ok_i && inverse.literals() < direct.literals());
+  const Dnf& d = use_inverse ? inverse : direct;
+  cq.flat = true;
+  cq.lits.clear();
+  if (d.is_true) {
+    cq.complement = !use_inverse;  // empty OR is zero; complement gives ones
+    return true;
+  }
+  cq.complement = use_inverse;
+  for (const auto& g : d.groups) {
+    for (size_t i = 0; i < g.size(); ++i)
+      cq.lits.push_back(CompiledQuery::FlatLit{g[i].term, g[i].neg, i == 0});
+  }
+  return true;
+}
+
+void emit_leaf(const Tree& t, int id, uint32_t mode, CompiledQuery& out) {
   const Node& n = t.nodes[id];
   bool neg = false;
   const Node* leaf = &n;
@@ -154,13 +286,14 @@ void emit_leaf(const Tree& t, int id, uint32_t mode, std::vector<uint32_t>& out)
     leaf = &t.nodes[n.kids[0]];
   }
   if (leaf->kind == NodeKind::kTerm) {
-    out.push_back(encode_insn(kInsTerm, mode, neg, leaf->term));
+    out.terms.push_back(leaf->term);
+    out.ops.push_back(encode_insn(kInsTerm, mode, neg));
   } else {
-    out.push_back(encode_insn(kInsConst, mode, neg != !leaf->ones, 0));
+    out.ops.push_back(encode_insn(kInsConst, mode, neg != !leaf->ones));
   }
 }
 
-void emit(const Tree& t, int id, std::vector<uint32_t>& out) {
+void emit(const Tree& t, int id, CompiledQuery& out) {
   if (is_leaf(t, id)) {
     emit_leaf(t, id, kModeSet, out);
     return;
@@ -168,7 +301,7 @@ void emit(const Tree& t, int id, std::vector<uint32_t>& out) {
   const Node& n = t.nodes[id];
   if (n.kind == NodeKind::kNot) {
     emit(t, n.kids[0], out);
-    out.push_back(encode_insn(kInsNot, 0, false, 0));
+    out.ops.push_back(encode_insn(kInsNot, 0, false));
     return;
   }
   const uint32_t mode = n.kind == NodeKind::kAnd ? kModeAnd : kModeOr;
@@ -178,18 +311,12 @@ void emit(const Tree& t, int id, std::vector<uint32_t>& out) {
     if (is_leaf(t, c)) {
       emit_leaf(t, c, mode, out);
     } else {
-      out.push_back(encode_insn(kInsPush, 0, false, 0));
+      out.ops.push_back(encode_insn(kInsPush, 0, false));
       emit(t, c, out);
-      out.push_back(encode_insn(kInsPop, mode, false, 0));
+      out.ops.push_back(encode_insn(kInsPop, mode, false));
     }
   }
 }
-
-struct CompiledQuery {
-  std::vector<uint32_t> insns;
-  int need = 0;
-  int term_refs = 0;
-};
 
 // Decodes query q, builds its tree and returns its program.  Terms are
 // interned in `terms` (ids are batch-local).
@@ -237,7 +364,6 @@ CompiledQuery compile_query(const int8_t* data, int64_t data_len,
                    ") but the plan holds ", n_hashes);
           n.kind = NodeKind::kTerm;
           n.term = terms.intern(hashes + 8 * term_counter * hash_k);
-          ST_CHECK(n.term <= kInsnMaxArg, "too many distinct terms");
         }
         ++term_counter;
         stack.push_back(tree.add(n));
@@ -284,11 +410,14 @@ CompiledQuery compile_query(const int8_t* data, int64_t data_len,
   ST_CHECK(!stack.empty(), "query plan ", q, " leaves an empty stack");
   int root = normalize(tree, stack.back());
   CompiledQuery cq;
-  emit(tree, root, cq.insns);
+  if (try_flat(tree, root, cq)) return cq;
+  emit(tree, root, cq);
   cq.need = tree.nodes[root].need;
-  for (uint32_t w : cq.insns) cq.term_refs += ((w & 7u) == kInsTerm);
   ST_CHECK(cq.need <= kSearchMaxStack, "query plan ", q, " needs ", cq.need,
            " stack slots; this build evaluates at most ", kSearchMaxStack);
+  ST_CHECK(cq.terms.size() <= kMaxTermsPerQuery && cq.ops.size() <= kMaxOpsPerQuery,
+           "query plan ", q, " is too long (", cq.terms.size(), " terms, ",
+           cq.ops.size(), " operations)");
   return cq;
 }
 
@@ -348,8 +477,10 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
       std::vector<int> order(cur.size());
       for (size_t i = 0; i < order.size(); ++i) order[i] = static_cast<int>(i);
       auto cost = [&](int i) {
-        return static_cast<int64_t>(cur[i].cq.insns.size()) +
-               static_cast<int64_t>(cur[i].cq.term_refs) * (k_eff + 1);
+        const CompiledQuery& c = cur[i].cq;
+        if (c.flat) return 4 + static_cast<int64_t>(c.lits.size()) * (k_eff + 3);
+        return 8 + 6 * static_cast<int64_t>(c.ops.size()) +
+               static_cast<int64_t>(c.terms.size()) * (k_eff + 3);
       };
       std::stable_sort(order.begin(), order.end(),
                        [&](int a, int c) { return cost(a) > cost(c); });
@@ -361,23 +492,35 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
         per_wave[w].push_back(i);
         load[w] += cost(i);
       }
-      std::vector<uint32_t> wave_off(kSearchWaves + 1, 0), rows, starts,
-          insns;
+      std::vector<uint32_t> wave_off(kSearchWaves + 1, 0), starts, insns;
+      const uint32_t pos_bytes = static_cast<uint32_t>(plan->kp) * 4;
       for (int w = 0; w < kSearchWaves; ++w) {
         for (int i : per_wave[w]) {
-          rows.push_back(static_cast<uint32_t>(cur[i].row));
+          const CompiledQuery& cq = cur[i].cq;
+          while (insns.size() % 4) insns.push_back(0);  // 16-byte aligned programs
           starts.push_back(static_cast<uint32_t>(insns.size()));
-          insns.insert(insns.end(), cur[i].cq.insns.begin(),
-                       cur[i].cq.insns.end());
+          const uint32_t row = static_cast<uint32_t>(cur[i].row);
+          if (cq.flat) {
+            insns.insert(insns.end(),
+                         {static_cast<uint32_t>(cq.lits.size()) | kFlatForm |
+                              (cq.complement ? kFlatComplement : 0u),
+                          row, 0u, 0u});
+            for (const auto& l : cq.lits) {
+              insns.insert(insns.end(), {l.term * pos_bytes, l.neg ? ~0u : 0u,
+                                         l.first ? ~0u : 0u, 0u});
+            }
+          } else {
+            insns.insert(insns.end(), {static_cast<uint32_t>(cq.terms.size()), row,
+                                       static_cast<uint32_t>(cq.ops.size()), 0u});
+            for (uint32_t t : cq.terms) insns.push_back(t * pos_bytes);
+            insns.insert(insns.end(), cq.ops.begin(), cq.ops.end());
+          }
         }
-        wave_off[w + 1] = static_cast<uint32_t>(rows.size());
+        wave_off[w + 1] = static_cast<uint32_t>(starts.size());
       }
-      starts.push_back(static_cast<uint32_t>(insns.size()));
       auto& blob = plan->blob;
       b.off_wave = blob.size();
       append_bytes(blob, wave_off.data(), wave_off.size() * 4);
-      b.off_row = blob.size();
-      append_bytes(blob, rows.data(), rows.size() * 4);
       b.off_insn_start = blob.size();
       append_bytes(blob, starts.data(), starts.size() * 4);
       b.off_insns = blob.size();

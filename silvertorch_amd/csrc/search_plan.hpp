@@ -27,15 +27,37 @@ constexpr int kSearchZerosRow = kSearchTileRows + 1;  // virtual all-zeros row
 constexpr int kSearchTileBytes = (kSearchTileRows + 2) * 256;
 constexpr int kSearchLdsBytes = 160 * 1024;
 constexpr int kSearchPosSlots = (kSearchLdsBytes - kSearchTileBytes) / 4;
-constexpr int kSearchMaxStack = 16;
+constexpr int kSearchMaxStack = 8;
 
 // Position codes of the global-memory path (bundles wider than the tile).
 constexpr int32_t kPosOnes = INT32_MIN;
 constexpr int32_t kPosZeros = INT32_MIN + 1;
 
-// Instruction word: [2:0] opcode, [4:3] combine mode, [5] negate, [31:6] arg.
+// A query program is a 16-byte aligned run of uint32 words with a 4-word
+// header [form | T, output row, n_ops, 0], in one of two forms.  Term
+// references are byte offsets of the term's position list in the kernel's
+// LDS position area (term id * positions_per_term * 4), so the kernel never
+// decodes them.
+//
+// Flat form (kFlatForm set): the query as an OR of AND-groups of literals,
+// optionally complemented as a whole.  T literal records of 4 words follow:
+//   [position byte offset, negate mask, group mask, 0]
+// (masks are 0 or ~0; the group mask is ~0 on the first literal of each
+// group).  Evaluated with no decoding: per literal w = word ^ negate,
+// res |= acc & group, acc = (acc | group) & w; then res | acc, complemented
+// if kFlatComplement is set.
+//
+// Stack form (kFlatForm clear), for queries whose flat form would be large:
+// T term references (1 word each, in the order the TERM ops consume them)
+// then n_ops operations: [2:0] opcode, [4:3] combine mode, [5] negate.
+constexpr uint32_t kFlatForm = 1u << 31;
+constexpr uint32_t kFlatComplement = 1u << 30;
+constexpr int kFlatMaxLiterals = 64;
+constexpr int kProgHeaderWords = 4;
+constexpr int kFlatLiteralWords = 4;
+
 enum InsnOp : uint32_t {
-  kInsTerm = 0,   // acc = mode(acc, [~]term(arg))
+  kInsTerm = 0,   // acc = mode(acc, [~]next term word)
   kInsConst = 1,  // acc = mode(acc, [~]all_ones)
   kInsPush = 2,   // stack[sp++] = acc
   kInsPop = 3,    // acc = mode(stack[--sp], acc)
@@ -43,13 +65,12 @@ enum InsnOp : uint32_t {
 };
 enum InsnMode : uint32_t { kModeSet = 0, kModeAnd = 1, kModeOr = 2 };
 
-constexpr uint32_t kInsnArgBits = 26;
-constexpr uint32_t kInsnMaxArg = (1u << kInsnArgBits) - 1;
-
-inline uint32_t encode_insn(uint32_t op, uint32_t mode, bool neg,
-                            uint32_t arg) {
-  return op | (mode << 3) | (static_cast<uint32_t>(neg) << 5) | (arg << 6);
+inline uint32_t encode_insn(uint32_t op, uint32_t mode, bool neg) {
+  return op | (mode << 3) | (static_cast<uint32_t>(neg) << 5);
 }
+
+constexpr uint32_t kMaxTermsPerQuery = 0xFFFF;
+constexpr uint32_t kMaxOpsPerQuery = 0x7FFF;
 
 // Positions stored per term in LDS, padded so a term's list is read with
 // 16-byte loads.
@@ -63,9 +84,8 @@ struct SearchBatch {
   uint32_t num_slots = 0;   // queries in this batch
   uint32_t num_terms = 0;   // distinct terms in this batch
   uint64_t off_wave = 0;    // uint32[kSearchWaves + 1]: slot range per wave
-  uint64_t off_row = 0;     // uint32[num_slots]: output row of each slot
-  uint64_t off_insn_start = 0;  // uint32[num_slots + 1]: program ranges
-  uint64_t off_insns = 0;   // uint32[...]: instruction words
+  uint64_t off_insn_start = 0;  // uint32[num_slots]: first word of each program
+  uint64_t off_insns = 0;   // uint32[...]: query programs
   uint64_t off_hashes = 0;  // uint64[num_terms * hash_k]
 };
 

@@ -143,6 +143,34 @@ def test_many_terms_split_into_passes():
     np.testing.assert_array_equal(H.search(index, bbo, pd, po, 3, 7), O.search_packed(index, bbo, pd, po, 3, 7))
 
 
+def test_program_forms():
+    """Queries compiled to each program form: flat OR-of-ANDs, flat
+    complement (AND-of-ORs) and the stack form (both flat forms too large)."""
+    rng = np.random.default_rng(5)
+    ids, offs, vals = _random_corpus(rng, 9000, 4, 1, 4, 60)
+    index, bbo = H.build(ids, offs, vals, 4.0, 3)
+
+    def t():
+        return f"{int(rng.choice(ids))}:{int(rng.integers(-15, 60))}"
+
+    def ors(n):
+        return "(" + " OR ".join(t() for _ in range(n)) + ")"
+
+    block = lambda: "(" + " AND ".join(ors(2) for _ in range(4)) + ")"
+    queries = [
+        " OR ".join(f"{t()} AND NOT {t()}" for _ in range(5)),      # flat
+        " AND ".join(ors(2) for _ in range(8)),                      # flat complement
+        " OR ".join(block() for _ in range(3)),                      # stack form
+        "NOT (" + " OR ".join(block() for _ in range(3)) + ")",      # stack form, negated
+        f"{t()} AND NOT {t()} AND ({t()} OR NOT ({t()} AND {t()}))",
+        f"({t()} OR {t()}) AND NOT ({t()} OR {t()})",
+    ]
+    for hk, k in [(7, 3), (3, 3), (9, 9)]:
+        pd, po = _plans(queries, hk, 3)
+        H.note(f"[forms] hash_k={hk} k={k}")
+        np.testing.assert_array_equal(H.search(index, bbo, pd, po, k, hk), O.search_packed(index, bbo, pd, po, k, hk))
+
+
 def test_edge_cases():
     c = G.case("features10x3")
     # no queries
