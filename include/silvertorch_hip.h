@@ -138,6 +138,16 @@ int st_search_plan_create(const int8_t* plans_data, int64_t plans_data_len,
                           const int64_t* plans_offsets,
                           int64_t plans_offsets_len, int64_t k, int64_t hash_k,
                           st_search_plan** out);
+/* Optional, after create: binds the plan to an index's bundle widths.
+ * bundle_b_offsets is a HOST copy of the index's int64[num_bundles + 1]
+ * offsets.  The most frequent widths (up to 64) get programs whose term
+ * references are replaced by the terms' row positions at that width, which
+ * removes the per-bundle position step from the kernel; bundles of other
+ * widths keep the unbound path.  A bound plan may only be used with an index
+ * of num_bundles bundles.  Call at most once per plan. */
+int st_search_plan_bind_widths(st_search_plan* plan,
+                               const int64_t* bundle_b_offsets,
+                               int64_t num_bundles);
 int64_t st_search_plan_num_queries(const st_search_plan* plan);
 int64_t st_search_plan_blob_bytes(const st_search_plan* plan);
 const void* st_search_plan_blob(const st_search_plan* plan);

@@ -24,6 +24,7 @@ SIGNATURES = {
     "st_bloom_build_bundle_offsets": (ctypes.c_int, [_vp, _i64, _i64, _i64, ctypes.c_double, _vp, _vp, _vp]),
     "st_bloom_index_build": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
     "st_search_plan_create": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, ctypes.POINTER(_vp)]),
+    "st_search_plan_bind_widths": (ctypes.c_int, [_vp, _vp, _i64]),
     "st_search_plan_num_queries": (_i64, [_vp]),
     "st_search_plan_blob_bytes": (_i64, [_vp]),
     "st_search_plan_blob": (_vp, [_vp]),
@@ -99,6 +100,12 @@ class SearchPlan:
             self._offs.ctypes.data if self._offs.size else None, self._offs.size,
             k, hash_k, ctypes.byref(self.handle)))
 
+    def bind_widths(self, bundle_b_offsets) -> None:
+        import numpy as np
+
+        self._bbo = np.ascontiguousarray(bundle_b_offsets, dtype=np.int64)
+        check(lib().st_search_plan_bind_widths(self.handle, self._bbo.ctypes.data, self._bbo.size - 1))
+
     @property
     def num_queries(self) -> int:
         return int(lib().st_search_plan_num_queries(self.handle))
@@ -108,6 +115,7 @@ class SearchPlan:
         return ctypes.string_at(lib().st_search_plan_blob(self.handle), n) if n else b""
 
     def __del__(self):
-        if getattr(self, "handle", None):
-            lib().st_search_plan_destroy(self.handle)
-            self.handle = None
+        h = getattr(self, "handle", None)
+        if h and _lib is not None:
+            _lib.st_search_plan_destroy(h)
+        self.handle = None

@@ -49,6 +49,10 @@ struct SearchArgs {
   const uint32_t* insn_start;
   const uint32_t* insns;
   const uint64_t* hashes;
+  const uint32_t* bundle_slot;   // nullptr when the plan is not width-bound
+  const uint32_t* bound_start;
+  const uint32_t* bound;
+  uint32_t bound_words;
   uint32_t num_terms;
   int32_t hash_k;
   int64_t out_cols;  // columns per output row = num_bundles * 32
@@ -334,24 +338,155 @@ __device__ __forceinline__ FastMod64 make_fastmod_dev(uint64_t d) {
   return f;
 }
 
+// ----------------------------------------------------- width-bound programs
+
+// This lane's 32-bit half of row position p of the current bundle.
+template <bool STAGED>
+__device__ __forceinline__ uint32_t row_word(const RowSource& rs, uint32_t p) {
+  if constexpr (STAGED) {
+    return *reinterpret_cast<const uint32_t*>(rs.tile_lane + p);
+  } else {
+    const int32_t r = static_cast<int32_t>(p);
+    if (r == kPosZeros) return 0;
+    const int64_t row = rs.start + r;
+    if (row < 0 || (row * 32 + (rs.lane >> 1)) >= rs.index_numel) return 0;
+    return rs.index32[row * 64 + rs.lane];
+  }
+}
+
+template <int K, bool STAGED>
+__device__ __forceinline__ uint32_t bound_term_word(const RowSource& rs, const uint32_t* rec) {
+  uint32_t v = ~0u;
+#pragma unroll
+  for (int q = 0; q < K; ++q) v &= row_word<STAGED>(rs, rec[q]);
+  return v;
+}
+
+// Bound flat query with exactly T literals: all row reads of the query are
+// issued before the OR-of-ANDs fold.
+template <int K, bool STAGED, int T>
+__device__ __forceinline__ uint32_t eval_bound_flat_fixed(const RowSource& rs, const uint32_t* recs) {
+  constexpr int RW = ((K + 1 + 3) / 4) * 4;
+  uint32_t w[T > 0 ? T : 1];
+#pragma unroll
+  for (int j = 0; j < T; ++j) w[j] = bound_term_word<K, STAGED>(rs, recs + j * RW);
+  uint32_t res = 0, acc = 0;
+#pragma unroll
+  for (int j = 0; j < T; ++j) {
+    const uint32_t f = recs[j * RW + K];
+    const uint32_t neg = 0u - (f & 1u);
+    const uint32_t grp = 0u - ((f >> 1) & 1u);
+    res |= acc & grp;
+    acc = (acc | grp) & (w[j] ^ neg);
+  }
+  return res | acc;
+}
+
+template <int K, bool STAGED, int G>
+__device__ __forceinline__ uint32_t eval_bound_flat_loop(const RowSource& rs, const uint32_t* recs,
+                                                         uint32_t T) {
+  constexpr int RW = ((K + 1 + 3) / 4) * 4;
+  uint32_t res = 0, acc = 0;
+  for (uint32_t base = 0; base < T; base += G) {
+    const uint32_t n = min(static_cast<uint32_t>(G), T - base);
+    const uint32_t* r0 = recs + base * RW;
+    uint32_t w[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (j < n) w[j] = bound_term_word<K, STAGED>(rs, r0 + j * RW);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if (j < n) {
+        const uint32_t f = r0[j * RW + K];
+        const uint32_t neg = 0u - (f & 1u);
+        const uint32_t grp = 0u - ((f >> 1) & 1u);
+        res |= acc & grp;
+        acc = (acc | grp) & (w[j] ^ neg);
+      }
+    }
+  }
+  return res | acc;
+}
+
+template <int K, bool STAGED, int G>
+__device__ __forceinline__ uint32_t eval_bound_flat(const RowSource& rs, const uint32_t* recs,
+                                                    uint32_t T) {
+  switch (T) {
+    case 0: return 0;
+    case 1: return eval_bound_flat_fixed<K, STAGED, 1>(rs, recs);
+    case 2: return eval_bound_flat_fixed<K, STAGED, 2>(rs, recs);
+    case 3: return eval_bound_flat_fixed<K, STAGED, 3>(rs, recs);
+    case 4: return eval_bound_flat_fixed<K, STAGED, 4>(rs, recs);
+    case 5: return eval_bound_flat_fixed<K, STAGED, 5>(rs, recs);
+    case 6: return eval_bound_flat_fixed<K, STAGED, 6>(rs, recs);
+    case 7: return eval_bound_flat_fixed<K, STAGED, 7>(rs, recs);
+    case 8: return eval_bound_flat_fixed<K, STAGED, 8>(rs, recs);
+    default: return eval_bound_flat_loop<K, STAGED, G>(rs, recs, T);
+  }
+}
+
+// Bound stack query: term position lists of KP words, then the operations.
+template <int K, int KP, bool STAGED, int G>
+__device__ __forceinline__ uint32_t eval_bound_stack(const RowSource& rs, const uint32_t* prog,
+                                                     uint32_t T, uint32_t nops) {
+  const uint32_t* tpos = prog + kProgHeaderWords;
+  const uint32_t* ops = tpos + T * KP;
+  uint32_t acc = 0;
+  uint32_t stk[kSearchMaxStack];
+  uint32_t sp = 0;
+  uint32_t i = 0;
+  for (uint32_t base = 0; base < T; base += G) {
+    const uint32_t n = min(static_cast<uint32_t>(G), T - base);
+    uint32_t w[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (j < n) w[j] = bound_term_word<K, STAGED>(rs, tpos + (base + j) * KP);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if (j < n) {
+        for (;;) {
+          const uint32_t op = ops[i++];
+          if ((op & 7u) == kInsTerm) {
+            acc = combine(op, acc, w[j]);
+            break;
+          }
+          exec_op(op, acc, stk, sp);
+        }
+      }
+    }
+  }
+  for (; i < nops; ++i) exec_op(ops[i], acc, stk, sp);
+  return acc;
+}
+
 // Evaluates this wave's queries [s_begin, s_end) on one bundle and stores
 // their 32-bit halves of the bundle's 32 output words.
-template <int K, int KP, bool STAGED, int G, bool kBoolOut>
+template <int K, int KP, bool STAGED, bool BOUND, int G, bool kBoolOut>
 __device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSource& rs,
                                              uint32_t s_begin, uint32_t s_end,
-                                             int64_t bundle) {
+                                             int64_t bundle, uint32_t slot) {
   const int lane = rs.lane;
+  const uint32_t* progs = BOUND ? a.bound + static_cast<uint64_t>(slot) * a.bound_words : a.insns;
+  const uint32_t* starts = BOUND ? a.bound_start : a.insn_start;
   for (uint32_t s = s_begin; s < s_end; ++s) {
-    const uint32_t* prog = a.insns + a.insn_start[s];
+    const uint32_t* prog = progs + starts[s];
     const uint32_t hdr = prog[0];
     const uint32_t row = prog[1];
     const uint32_t T = hdr & 0xFFFFu;
     uint32_t acc;
     if (hdr & kFlatForm) {
-      acc = eval_flat<K, KP, STAGED, G>(rs, reinterpret_cast<const u32x4*>(prog + kProgHeaderWords), T);
+      if constexpr (BOUND) {
+        acc = eval_bound_flat<K, STAGED, G>(rs, prog + kProgHeaderWords, T);
+      } else {
+        acc = eval_flat<K, KP, STAGED, G>(rs, reinterpret_cast<const u32x4*>(prog + kProgHeaderWords), T);
+      }
       if (hdr & kFlatComplement) acc = ~acc;
     } else {
-      acc = eval_stack<K, KP, STAGED, G>(rs, prog, T, prog[2]);
+      if constexpr (BOUND) {
+        acc = eval_bound_stack<K, KP, STAGED, G>(rs, prog, T, prog[2]);
+      } else {
+        acc = eval_stack<K, KP, STAGED, G>(rs, prog, T, prog[2]);
+      }
     }
 
     const int64_t col0 = static_cast<int64_t>(row) * a.out_cols + bundle * 32;
@@ -375,7 +510,9 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     const int64_t* __restrict__ bundle_offsets, int64_t num_bundles,
     const uint32_t* __restrict__ wave_off,
     const uint32_t* __restrict__ insn_start, const uint32_t* __restrict__ insns,
-    const uint64_t* __restrict__ hashes, uint32_t num_terms, int32_t hash_k,
+    const uint64_t* __restrict__ hashes, const uint32_t* __restrict__ bundle_slot,
+    const uint32_t* __restrict__ bound_start, const uint32_t* __restrict__ bound,
+    uint32_t bound_words, uint32_t num_terms, int32_t hash_k,
     int64_t out_cols, void* __restrict__ out) {
   SearchArgs a;
   a.index = index;
@@ -386,6 +523,10 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
   a.insn_start = insn_start;
   a.insns = insns;
   a.hashes = hashes;
+  a.bundle_slot = bundle_slot;
+  a.bound_start = bound_start;
+  a.bound = bound;
+  a.bound_words = bound_words;
   a.num_terms = num_terms;
   a.hash_k = hash_k;
   a.out_cols = out_cols;
@@ -428,7 +569,8 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
         if (c < chunks) tile[c] = pre[i];
       }
     }
-    if (b != prev_b) {
+    const uint32_t slot = a.bundle_slot ? a.bundle_slot[bundle] : kNoWidthSlot;
+    if (slot == kNoWidthSlot && b != prev_b) {
       const FastMod64 fm = make_fastmod_dev(static_cast<uint64_t>(b));
       for (uint32_t u = tid; u < a.num_terms; u += kSearchThreads) {
         int16_t found[K];
@@ -467,17 +609,24 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     rs.start = start;
     rs.lane = lane;
     rs.staged = staged;
-    if (staged) {
-      eval_queries<K, KP, true, G, kBoolOut>(a, rs, s_begin, s_end, bundle);
+    if (slot != kNoWidthSlot) {
+      if (staged) {
+        eval_queries<K, KP, true, true, G, kBoolOut>(a, rs, s_begin, s_end, bundle, slot);
+      } else {
+        eval_queries<K, KP, false, true, G, kBoolOut>(a, rs, s_begin, s_end, bundle, slot);
+      }
+    } else if (staged) {
+      eval_queries<K, KP, true, false, G, kBoolOut>(a, rs, s_begin, s_end, bundle, slot);
     } else {
-      eval_queries<K, KP, false, G, kBoolOut>(a, rs, s_begin, s_end, bundle);
+      eval_queries<K, KP, false, false, G, kBoolOut>(a, rs, s_begin, s_end, bundle, slot);
     }
   }
 }
 
 using KernelFn = void (*)(const int64_t*, int64_t, const int64_t*, int64_t,
                           const uint32_t*, const uint32_t*,
-                          const uint32_t*, const uint64_t*, uint32_t, int32_t,
+                          const uint32_t*, const uint64_t*, const uint32_t*,
+                          const uint32_t*, const uint32_t*, uint32_t, uint32_t, int32_t,
                           int64_t, void*);
 
 template <int K>
@@ -541,6 +690,9 @@ extern "C" int st_bloom_index_search_batch(
              "null device pointer");
     ST_CHECK(bloom_index != nullptr || bloom_index_numel == 0,
              "bloom_index is null");
+    ST_CHECK(plan->bound_bundles < 0 || plan->bound_bundles == num_bundles,
+             "plan was bound to ", plan->bound_bundles, " bundles, the index has ",
+             num_bundles);
     KernelFn fn = select_kernel(plan->k_eff, return_bool_mask != 0);
     const int grid = static_cast<int>(
         std::min<int64_t>(num_bundles, static_cast<int64_t>(device_cu_count())));
@@ -555,6 +707,11 @@ extern "C" int st_bloom_index_search_batch(
       a.insn_start = reinterpret_cast<const uint32_t*>(blob + bt.off_insn_start);
       a.insns = reinterpret_cast<const uint32_t*>(blob + bt.off_insns);
       a.hashes = reinterpret_cast<const uint64_t*>(blob + bt.off_hashes);
+      const bool bound = plan->bound_bundles >= 0;
+      a.bundle_slot = bound ? reinterpret_cast<const uint32_t*>(blob + plan->off_bundle_slot) : nullptr;
+      a.bound_start = bound ? reinterpret_cast<const uint32_t*>(blob + bt.off_bound_start) : nullptr;
+      a.bound = bound ? reinterpret_cast<const uint32_t*>(blob + bt.off_bound) : nullptr;
+      a.bound_words = bound ? bt.bound_words : 0;
       a.num_terms = bt.num_terms;
       a.hash_k = static_cast<int32_t>(plan->hash_k);
       a.out_cols = num_bundles * 32;
@@ -562,7 +719,8 @@ extern "C" int st_bloom_index_search_batch(
       hipLaunchKernelGGL(fn, dim3(grid), dim3(kSearchThreads), 0,
                          static_cast<hipStream_t>(stream), a.index, a.index_numel,
                          a.bundle_offsets, a.num_bundles, a.wave_off,
-                         a.insn_start, a.insns, a.hashes, a.num_terms, a.hash_k,
+                         a.insn_start, a.insns, a.hashes, a.bundle_slot,
+                         a.bound_start, a.bound, a.bound_words, a.num_terms, a.hash_k,
                          a.out_cols, a.out);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess)

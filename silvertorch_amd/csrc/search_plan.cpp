@@ -528,6 +528,9 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
       b.off_hashes = blob.size();
       append_bytes(blob, terms.hashes.data(), terms.hashes.size() * 8);
       plan->batches.push_back(b);
+      plan->batch_insns.push_back(insns);
+      plan->batch_starts.push_back(starts);
+      plan->batch_hashes.push_back(terms.hashes);
       cur.clear();
       terms.clear();
     };
@@ -551,7 +554,155 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
       cur.push_back(Pending{q, std::move(cq)});
     }
     flush();
+    plan->blob.resize(plan->blob.size() + 256, 0);  // slack for scalar loads
     *out = plan.release();
+  });
+}
+
+namespace st {
+namespace {
+
+// Row positions of one term at width b, as the kernel's positions step and
+// signature_match (bloom_index_search.cpp:40-61) resolve them: over hashes
+// p < hash_k, b_p = (int16)(h[p] % b), repeats skipped, at most k_eff kept;
+// unused slots repeat the first.  Staged bundles get LDS byte offsets
+// (row * 256, the all-zeros row when nothing resolves); others get signed
+// rows relative to the bundle start (kPosZeros when nothing resolves).
+void term_positions(const uint64_t* h, int64_t hash_k, int k_eff, int64_t b,
+                    int slots, uint32_t* out) {
+  int16_t found[kMaxSearchK] = {0};
+  int cnt = 0;
+  if (b > 0) {
+    for (int64_t p = 0; p < hash_k && cnt < k_eff; ++p) {
+      const int16_t bp = static_cast<int16_t>(h[p] % static_cast<uint64_t>(b));
+      bool dup = false;
+      for (int j = 0; j < cnt; ++j) dup |= found[j] == bp;
+      if (!dup) found[cnt++] = bp;
+    }
+  }
+  const bool staged = b <= kSearchTileRows;
+  for (int j = 0; j < slots; ++j) {
+    const int16_t r = j < cnt ? found[j] : found[0];
+    if (staged) {
+      out[j] = static_cast<uint32_t>(cnt == 0 ? kSearchZerosRow : r) * 256u;
+    } else {
+      out[j] = cnt == 0 ? static_cast<uint32_t>(kPosZeros)
+                        : static_cast<uint32_t>(static_cast<int32_t>(r));
+    }
+  }
+}
+
+}  // namespace
+}  // namespace st
+
+extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
+                                          const int64_t* bundle_b_offsets,
+                                          int64_t num_bundles) {
+  using namespace st;
+  return guarded([&] {
+    ST_CHECK(plan != nullptr, "plan is null");
+    ST_CHECK(plan->bound_bundles < 0, "plan is already bound to bundle widths");
+    ST_CHECK(num_bundles >= 0, "negative bundle count");
+    ST_CHECK(num_bundles == 0 || bundle_b_offsets != nullptr,
+             "bundle_b_offsets is null");
+    const int k_eff = plan->k_eff;
+    const int kp = plan->kp;
+    const int rw = bound_record_words(k_eff);
+    const uint32_t pos_bytes = static_cast<uint32_t>(kp) * 4;
+
+    // Most frequent widths get slots (ties to the smaller width).
+    std::vector<int64_t> width(num_bundles);
+    std::unordered_map<int64_t, int64_t> freq;
+    for (int64_t i = 0; i < num_bundles; ++i) {
+      width[i] = std::max<int64_t>(bundle_b_offsets[i + 1] - bundle_b_offsets[i], 0);
+      ++freq[width[i]];
+    }
+    std::vector<std::pair<int64_t, int64_t>> by_freq(freq.begin(), freq.end());
+    std::sort(by_freq.begin(), by_freq.end(), [](const auto& a, const auto& c) {
+      return a.second != c.second ? a.second > c.second : a.first < c.first;
+    });
+    if (by_freq.size() > static_cast<size_t>(kMaxWidthSlots)) by_freq.resize(kMaxWidthSlots);
+    std::unordered_map<int64_t, uint32_t> slot_of;
+    plan->slot_width.clear();
+    for (const auto& wf : by_freq) {
+      slot_of[wf.first] = static_cast<uint32_t>(plan->slot_width.size());
+      plan->slot_width.push_back(wf.first);
+    }
+    std::vector<uint32_t> bundle_slot(num_bundles);
+    for (int64_t i = 0; i < num_bundles; ++i) {
+      auto it = slot_of.find(width[i]);
+      bundle_slot[i] = it == slot_of.end() ? kNoWidthSlot : it->second;
+    }
+    auto& blob = plan->blob;
+    plan->off_bundle_slot = blob.size();
+    append_bytes(blob, bundle_slot.data(), bundle_slot.size() * 4);
+
+    const size_t nslots = plan->slot_width.size();
+    for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
+      SearchBatch& bt = plan->batches[bi];
+      const auto& insns = plan->batch_insns[bi];
+      const auto& starts = plan->batch_starts[bi];
+      const auto& hashes = plan->batch_hashes[bi];
+      // positions of every term at every slot width
+      std::vector<uint32_t> pos(nslots * bt.num_terms * kp);
+      for (size_t s = 0; s < nslots; ++s)
+        for (uint32_t u = 0; u < bt.num_terms; ++u)
+          term_positions(hashes.data() + static_cast<size_t>(u) * plan->hash_k,
+                         plan->hash_k, k_eff, plan->slot_width[s], kp,
+                         &pos[(s * bt.num_terms + u) * kp]);
+      // layout of one width block (identical for every slot)
+      std::vector<uint32_t> bstart(bt.num_slots);
+      uint32_t words = 0;
+      for (uint32_t q = 0; q < bt.num_slots; ++q) {
+        bstart[q] = words;
+        const uint32_t hdr = insns[starts[q]];
+        const uint32_t T = hdr & 0xFFFFu;
+        uint32_t n = kProgHeaderWords;
+        if (hdr & kFlatForm) {
+          n += T * rw;
+        } else {
+          n += T * kp + insns[starts[q] + 2];
+        }
+        words += (n + 3) & ~3u;
+      }
+      std::vector<uint32_t> block(nslots * words, 0);
+      for (size_t s = 0; s < nslots; ++s) {
+        uint32_t* base = block.data() + s * words;
+        const uint32_t* spos = pos.data() + s * bt.num_terms * kp;
+        for (uint32_t q = 0; q < bt.num_slots; ++q) {
+          const uint32_t* src = insns.data() + starts[q];
+          uint32_t* dst = base + bstart[q];
+          const uint32_t hdr = src[0];
+          const uint32_t T = hdr & 0xFFFFu;
+          for (int w = 0; w < kProgHeaderWords; ++w) dst[w] = src[w];
+          if (hdr & kFlatForm) {
+            for (uint32_t j = 0; j < T; ++j) {
+              const uint32_t* lit = src + kProgHeaderWords + j * kFlatLiteralWords;
+              const uint32_t* tp = spos + (lit[0] / pos_bytes) * kp;
+              uint32_t* rec = dst + kProgHeaderWords + j * rw;
+              for (int r = 0; r < k_eff; ++r) rec[r] = tp[r];
+              rec[k_eff] = (lit[1] ? 1u : 0u) | (lit[2] ? 2u : 0u);
+            }
+          } else {
+            const uint32_t nops = src[2];
+            for (uint32_t j = 0; j < T; ++j) {
+              const uint32_t* tp = spos + (src[kProgHeaderWords + j] / pos_bytes) * kp;
+              for (int r = 0; r < kp; ++r) dst[kProgHeaderWords + j * kp + r] = tp[r];
+            }
+            for (uint32_t o = 0; o < nops; ++o)
+              dst[kProgHeaderWords + T * kp + o] = src[kProgHeaderWords + T + o];
+          }
+        }
+      }
+      bt.bound_words = words;
+      bt.off_bound_start = blob.size();
+      append_bytes(blob, bstart.data(), bstart.size() * 4);
+      bt.off_bound = blob.size();
+      append_bytes(blob, block.data(), block.size() * 4);
+    }
+    // Scalar loads may read a few words past the last program.
+    blob.resize(blob.size() + 256, 0);
+    plan->bound_bundles = num_bundles;
   });
 }
 

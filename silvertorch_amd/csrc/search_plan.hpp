@@ -78,6 +78,26 @@ inline int positions_per_term(int k_eff) {
   return k_eff <= 4 ? 4 : (k_eff <= 8 ? 8 : 12);
 }
 
+// Width-bound programs.  Once the bundle widths are known on the host
+// (st_search_plan_bind_widths), every distinct width among the most frequent
+// kMaxWidthSlots gets a copy of the batch's programs with each term
+// reference replaced by the term's row positions at that width, so the
+// kernel needs neither the per-bundle positions step nor the LDS position
+// lookup.  Bundles of other widths (bundle_slot == kNoWidthSlot) use the
+// term-reference programs.
+//
+// Bound flat form: header as above, then T records of
+// bound_record_words(K) words: [row position 0 .. K-1, flags, pad...]
+// with flags bit 0 = negate, bit 1 = first of its group.
+// Bound stack form: header, T position lists of positions_per_term(K)
+// words, then the operations.
+// Positions are LDS byte offsets (row * 256) for bundles staged in LDS and
+// signed rows relative to the bundle start otherwise.
+constexpr int kMaxWidthSlots = 64;
+constexpr uint32_t kNoWidthSlot = 0xFFFFFFFFu;
+
+inline int bound_record_words(int k_eff) { return ((k_eff + 1 + 3) / 4) * 4; }
+
 // One kernel launch worth of queries.  Offsets are byte offsets into the
 // plan blob.
 struct SearchBatch {
@@ -87,6 +107,10 @@ struct SearchBatch {
   uint64_t off_insn_start = 0;  // uint32[num_slots]: first word of each program
   uint64_t off_insns = 0;   // uint32[...]: query programs
   uint64_t off_hashes = 0;  // uint64[num_terms * hash_k]
+  // width-bound programs (valid when the plan is bound)
+  uint64_t off_bound_start = 0;  // uint32[num_slots]: first word within a width block
+  uint64_t off_bound = 0;        // uint32[width_slots * bound_words]
+  uint32_t bound_words = 0;      // words per width block
 };
 
 }  // namespace st
@@ -100,4 +124,12 @@ struct st_search_plan {
   int max_stack = 0;    // deepest push in any program
   std::vector<st::SearchBatch> batches;
   std::vector<uint8_t> blob;
+  // term-reference programs and term hashes of each batch, kept for binding
+  std::vector<std::vector<uint32_t>> batch_insns;
+  std::vector<std::vector<uint32_t>> batch_starts;
+  std::vector<std::vector<uint64_t>> batch_hashes;
+  // set by st_search_plan_bind_widths
+  int64_t bound_bundles = -1;        // -1: not bound
+  uint64_t off_bundle_slot = 0;      // uint32[bound_bundles]
+  std::vector<int64_t> slot_width;   // width of each slot
 };

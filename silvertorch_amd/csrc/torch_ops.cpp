@@ -173,6 +173,12 @@ Tensor search_gpu(const Tensor& bloom_index_in, const Tensor& bundle_b_offsets_i
            "bloom_index_search_batch");
   const int64_t Q = st_search_plan_num_queries(plan.p);
   const int64_t nb = bbo.numel() - 1;
+  if (Q > 0 && nb > 0) {
+    // Bundle widths on the host let the plan carry per-width row positions.
+    const Tensor bbo_h = bbo.to(at::kCPU);
+    check_st(st_search_plan_bind_widths(plan.p, bbo_h.data_ptr<int64_t>(), nb),
+             "bloom_index_search_batch");
+  }
   const int64_t C = nb * ST_COLUMNS_PER_BUNDLE;
   Tensor out = return_bool_mask
                    ? at::empty({Q, C * ST_BITS_PER_COLUMN},
