@@ -37,21 +37,33 @@ namespace {
 // Native 4 x u32 vector (usable with the nontemporal builtins).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// The plan arrays and bundle offsets are read-only for the kernel's lifetime.
+// Reading them through the constant address space lets every uniform read
+// become a scalar load: a vector load there would share the in-order vmcnt
+// counter with the next bundle's tile prefetch, and waiting for it would wait
+// for the whole prefetch.
+#define ST_CONST __attribute__((address_space(4)))
+template <typename T>
+__device__ __forceinline__ const ST_CONST T* as_const(const T* p) {
+  return (const ST_CONST T*)(p);  // addrspacecast: only a C-style cast spells it
+}
+
 constexpr int kPrefetch = kSearchTileRows * 16 / kSearchThreads;  // uint4/thread
 static_assert(kPrefetch * kSearchThreads == kSearchTileRows * 16, "tile split");
 
 struct SearchArgs {
   const int64_t* index;
   int64_t index_numel;
-  const int64_t* bundle_offsets;
+  const ST_CONST int64_t* bundle_offsets;
   int64_t num_bundles;
-  const uint32_t* wave_off;
-  const uint32_t* insn_start;
-  const uint32_t* insns;
-  const uint64_t* hashes;
-  const uint32_t* bundle_slot;   // nullptr when the plan is not width-bound
-  const uint32_t* bound_start;
-  const uint32_t* bound;
+  const ST_CONST uint32_t* wave_off;
+  const ST_CONST uint32_t* insn_start;
+  const ST_CONST uint32_t* insns;
+  const ST_CONST uint64_t* hashes;
+  const ST_CONST uint32_t* bundle_slot;   // nullptr when the plan is not width-bound
+  const ST_CONST uint32_t* bundle_order;  // visiting order (nullptr: index order)
+  const ST_CONST uint32_t* bound_start;
+  const ST_CONST uint32_t* bound;
   uint32_t bound_words;
   uint32_t num_terms;
   int32_t hash_k;
@@ -97,7 +109,7 @@ __device__ __forceinline__ void prefetch_tile(const SearchArgs& a, int64_t bnd,
 // are resolved, b_p = (int16)(h[p] % b); repeats of an earlier b_p are
 // skipped.  Unused slots repeat slot 0 (AND is idempotent).
 template <int K>
-__device__ __forceinline__ int resolve_positions(const uint64_t* h, int hash_k,
+__device__ __forceinline__ int resolve_positions(const ST_CONST uint64_t* h, int hash_k,
                                                  const FastMod64& fm,
                                                  int16_t (&found)[K]) {
   int cnt = 0;
@@ -213,7 +225,7 @@ __device__ __forceinline__ uint32_t term_word(const RowSource& rs, const uint32_
 // Flat-form query with exactly T literals: every position list, then every
 // row word, then the branch-free OR-of-ANDs fold.
 template <int K, int KP, bool STAGED, int T>
-__device__ __forceinline__ uint32_t eval_flat_fixed(const RowSource& rs, const u32x4* lit) {
+__device__ __forceinline__ uint32_t eval_flat_fixed(const RowSource& rs, const ST_CONST u32x4* lit) {
   uint32_t p[T > 0 ? T : 1][KP];
 #pragma unroll
   for (int j = 0; j < T; ++j) load_positions<KP>(rs, lit[j].x, p[j]);
@@ -232,7 +244,7 @@ __device__ __forceinline__ uint32_t eval_flat_fixed(const RowSource& rs, const u
 
 // Flat-form query of any length, in groups of G literals.
 template <int K, int KP, bool STAGED, int G>
-__device__ __forceinline__ uint32_t eval_flat_loop(const RowSource& rs, const u32x4* lit,
+__device__ __forceinline__ uint32_t eval_flat_loop(const RowSource& rs, const ST_CONST u32x4* lit,
                                                    uint32_t T) {
   uint32_t res = 0, acc = 0;
   for (uint32_t base = 0; base < T; base += G) {
@@ -260,7 +272,7 @@ __device__ __forceinline__ uint32_t eval_flat_loop(const RowSource& rs, const u3
 // Flat query dispatch: fully unrolled blocks for short queries (T * KP
 // position registers bounded), the grouped loop otherwise.
 template <int K, int KP, bool STAGED, int G, int T>
-__device__ __forceinline__ uint32_t eval_flat_t(const RowSource& rs, const u32x4* lit, uint32_t n) {
+__device__ __forceinline__ uint32_t eval_flat_t(const RowSource& rs, const ST_CONST u32x4* lit, uint32_t n) {
   if constexpr (T * KP <= 24) {
     return eval_flat_fixed<K, KP, STAGED, T>(rs, lit);
   } else {
@@ -269,7 +281,7 @@ __device__ __forceinline__ uint32_t eval_flat_t(const RowSource& rs, const u32x4
 }
 
 template <int K, int KP, bool STAGED, int G>
-__device__ __forceinline__ uint32_t eval_flat(const RowSource& rs, const u32x4* lit, uint32_t T) {
+__device__ __forceinline__ uint32_t eval_flat(const RowSource& rs, const ST_CONST u32x4* lit, uint32_t T) {
   switch (T) {
     case 0: return 0;
     case 1: return eval_flat_t<K, KP, STAGED, G, 1>(rs, lit, T);
@@ -284,10 +296,10 @@ __device__ __forceinline__ uint32_t eval_flat(const RowSource& rs, const u32x4* 
 
 // Stack-form query: term words in groups of G, operations walked in order.
 template <int K, int KP, bool STAGED, int G>
-__device__ __forceinline__ uint32_t eval_stack(const RowSource& rs, const uint32_t* prog,
+__device__ __forceinline__ uint32_t eval_stack(const RowSource& rs, const ST_CONST uint32_t* prog,
                                                uint32_t T, uint32_t nops) {
-  const uint32_t* tref = prog + kProgHeaderWords;
-  const uint32_t* ops = tref + T;
+  const ST_CONST uint32_t* tref = prog + kProgHeaderWords;
+  const ST_CONST uint32_t* ops = tref + T;
   uint32_t acc = 0;
   uint32_t stk[kSearchMaxStack];
   uint32_t sp = 0;
@@ -348,6 +360,7 @@ __device__ __forceinline__ uint32_t row_word(const RowSource& rs, uint32_t p) {
   } else {
     const int32_t r = static_cast<int32_t>(p);
     if (r == kPosZeros) return 0;
+    if (r == kPosOnes) return ~0u;
     const int64_t row = rs.start + r;
     if (row < 0 || (row * 32 + (rs.lane >> 1)) >= rs.index_numel) return 0;
     return rs.index32[row * 64 + rs.lane];
@@ -355,7 +368,7 @@ __device__ __forceinline__ uint32_t row_word(const RowSource& rs, uint32_t p) {
 }
 
 template <int K, bool STAGED>
-__device__ __forceinline__ uint32_t bound_term_word(const RowSource& rs, const uint32_t* rec) {
+__device__ __forceinline__ uint32_t bound_term_word(const RowSource& rs, const ST_CONST uint32_t* rec) {
   uint32_t v = ~0u;
 #pragma unroll
   for (int q = 0; q < K; ++q) v &= row_word<STAGED>(rs, rec[q]);
@@ -365,7 +378,7 @@ __device__ __forceinline__ uint32_t bound_term_word(const RowSource& rs, const u
 // Bound flat query with exactly T literals: all row reads of the query are
 // issued before the OR-of-ANDs fold.
 template <int K, bool STAGED, int T>
-__device__ __forceinline__ uint32_t eval_bound_flat_fixed(const RowSource& rs, const uint32_t* recs) {
+__device__ __forceinline__ uint32_t eval_bound_flat_fixed(const RowSource& rs, const ST_CONST uint32_t* recs) {
   constexpr int RW = ((K + 1 + 3) / 4) * 4;
   uint32_t w[T > 0 ? T : 1];
 #pragma unroll
@@ -382,14 +395,60 @@ __device__ __forceinline__ uint32_t eval_bound_flat_fixed(const RowSource& rs, c
   return res | acc;
 }
 
+// Two bound flat queries with the same literal count T, evaluated together
+// so that both queries' row reads are in flight at once.
+template <int K, bool STAGED, int T>
+__device__ __forceinline__ void eval_bound_pair_fixed(const RowSource& rs, const ST_CONST uint32_t* ra,
+                                                      const ST_CONST uint32_t* rb, uint32_t& out_a,
+                                                      uint32_t& out_b) {
+  constexpr int RW = ((K + 1 + 3) / 4) * 4;
+  uint32_t wa[T], wb[T];
+#pragma unroll
+  for (int j = 0; j < T; ++j) {
+    wa[j] = bound_term_word<K, STAGED>(rs, ra + j * RW);
+    wb[j] = bound_term_word<K, STAGED>(rs, rb + j * RW);
+  }
+  uint32_t res_a = 0, acc_a = 0, res_b = 0, acc_b = 0;
+#pragma unroll
+  for (int j = 0; j < T; ++j) {
+    const uint32_t fa = ra[j * RW + K], fb = rb[j * RW + K];
+    const uint32_t neg_a = 0u - (fa & 1u), grp_a = 0u - ((fa >> 1) & 1u);
+    const uint32_t neg_b = 0u - (fb & 1u), grp_b = 0u - ((fb >> 1) & 1u);
+    res_a |= acc_a & grp_a;
+    acc_a = (acc_a | grp_a) & (wa[j] ^ neg_a);
+    res_b |= acc_b & grp_b;
+    acc_b = (acc_b | grp_b) & (wb[j] ^ neg_b);
+  }
+  out_a = res_a | acc_a;
+  out_b = res_b | acc_b;
+}
+
+// Pair dispatch on the shared literal count; false when T is beyond the
+// unrolled range (the caller then evaluates the two queries one by one).
+template <int K, bool STAGED>
+__device__ __forceinline__ bool eval_bound_pair(const RowSource& rs, const ST_CONST uint32_t* ra,
+                                                const ST_CONST uint32_t* rb, uint32_t T, uint32_t& out_a,
+                                                uint32_t& out_b) {
+  switch (T) {
+    case 0: out_a = 0; out_b = 0; return true;
+    case 1: eval_bound_pair_fixed<K, STAGED, 1>(rs, ra, rb, out_a, out_b); return true;
+    case 2: eval_bound_pair_fixed<K, STAGED, 2>(rs, ra, rb, out_a, out_b); return true;
+    case 3: eval_bound_pair_fixed<K, STAGED, 3>(rs, ra, rb, out_a, out_b); return true;
+    case 4: eval_bound_pair_fixed<K, STAGED, 4>(rs, ra, rb, out_a, out_b); return true;
+    case 5: eval_bound_pair_fixed<K, STAGED, 5>(rs, ra, rb, out_a, out_b); return true;
+    case 6: eval_bound_pair_fixed<K, STAGED, 6>(rs, ra, rb, out_a, out_b); return true;
+    default: return false;
+  }
+}
+
 template <int K, bool STAGED, int G>
-__device__ __forceinline__ uint32_t eval_bound_flat_loop(const RowSource& rs, const uint32_t* recs,
+__device__ __forceinline__ uint32_t eval_bound_flat_loop(const RowSource& rs, const ST_CONST uint32_t* recs,
                                                          uint32_t T) {
   constexpr int RW = ((K + 1 + 3) / 4) * 4;
   uint32_t res = 0, acc = 0;
   for (uint32_t base = 0; base < T; base += G) {
     const uint32_t n = min(static_cast<uint32_t>(G), T - base);
-    const uint32_t* r0 = recs + base * RW;
+    const ST_CONST uint32_t* r0 = recs + base * RW;
     uint32_t w[G];
 #pragma unroll
     for (int j = 0; j < G; ++j)
@@ -409,7 +468,7 @@ __device__ __forceinline__ uint32_t eval_bound_flat_loop(const RowSource& rs, co
 }
 
 template <int K, bool STAGED, int G>
-__device__ __forceinline__ uint32_t eval_bound_flat(const RowSource& rs, const uint32_t* recs,
+__device__ __forceinline__ uint32_t eval_bound_flat(const RowSource& rs, const ST_CONST uint32_t* recs,
                                                     uint32_t T) {
   switch (T) {
     case 0: return 0;
@@ -427,10 +486,10 @@ __device__ __forceinline__ uint32_t eval_bound_flat(const RowSource& rs, const u
 
 // Bound stack query: term position lists of KP words, then the operations.
 template <int K, int KP, bool STAGED, int G>
-__device__ __forceinline__ uint32_t eval_bound_stack(const RowSource& rs, const uint32_t* prog,
+__device__ __forceinline__ uint32_t eval_bound_stack(const RowSource& rs, const ST_CONST uint32_t* prog,
                                                      uint32_t T, uint32_t nops) {
-  const uint32_t* tpos = prog + kProgHeaderWords;
-  const uint32_t* ops = tpos + T * KP;
+  const ST_CONST uint32_t* tpos = prog + kProgHeaderWords;
+  const ST_CONST uint32_t* ops = tpos + T * KP;
   uint32_t acc = 0;
   uint32_t stk[kSearchMaxStack];
   uint32_t sp = 0;
@@ -466,29 +525,7 @@ __device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSourc
                                              uint32_t s_begin, uint32_t s_end,
                                              int64_t bundle, uint32_t slot) {
   const int lane = rs.lane;
-  const uint32_t* progs = BOUND ? a.bound + static_cast<uint64_t>(slot) * a.bound_words : a.insns;
-  const uint32_t* starts = BOUND ? a.bound_start : a.insn_start;
-  for (uint32_t s = s_begin; s < s_end; ++s) {
-    const uint32_t* prog = progs + starts[s];
-    const uint32_t hdr = prog[0];
-    const uint32_t row = prog[1];
-    const uint32_t T = hdr & 0xFFFFu;
-    uint32_t acc;
-    if (hdr & kFlatForm) {
-      if constexpr (BOUND) {
-        acc = eval_bound_flat<K, STAGED, G>(rs, prog + kProgHeaderWords, T);
-      } else {
-        acc = eval_flat<K, KP, STAGED, G>(rs, reinterpret_cast<const u32x4*>(prog + kProgHeaderWords), T);
-      }
-      if (hdr & kFlatComplement) acc = ~acc;
-    } else {
-      if constexpr (BOUND) {
-        acc = eval_bound_stack<K, KP, STAGED, G>(rs, prog, T, prog[2]);
-      } else {
-        acc = eval_stack<K, KP, STAGED, G>(rs, prog, T, prog[2]);
-      }
-    }
-
+  auto store = [&](uint32_t row, uint32_t acc) {
     const int64_t col0 = static_cast<int64_t>(row) * a.out_cols + bundle * 32;
     if constexpr (kBoolOut) {
       uint8_t* dst = static_cast<uint8_t*>(a.out) + (col0 + (lane >> 1)) * 64 +
@@ -498,6 +535,58 @@ __device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSourc
       uint32_t* dst = static_cast<uint32_t*>(a.out) + col0 * 2 + lane;
       __builtin_nontemporal_store(acc, dst);
     }
+  };
+  if constexpr (BOUND) {
+    constexpr int RW = ((K + 1 + 3) / 4) * 4;
+    const ST_CONST uint32_t* progs = a.bound + static_cast<uint64_t>(slot) * a.bound_words;
+    for (uint32_t s = s_begin; s < s_end;) {
+      const ST_CONST uint32_t* prog = progs + a.bound_start[s];
+      const uint32_t hdr = prog[0];
+      const uint32_t T = hdr & 0xFFFFu;
+      if (hdr & kPairedWithNext) {
+        const ST_CONST uint32_t* prog_b = progs + a.bound_start[s + 1];
+        const uint32_t hdr_b = prog_b[0];
+        uint32_t acc_a, acc_b;
+        if (!eval_bound_pair<K, STAGED>(rs, prog + kProgHeaderWords, prog_b + kProgHeaderWords,
+                                        T, acc_a, acc_b)) {
+          acc_a = eval_bound_flat_loop<K, STAGED, G>(rs, prog + kProgHeaderWords, T);
+          acc_b = eval_bound_flat_loop<K, STAGED, G>(rs, prog_b + kProgHeaderWords, T);
+        }
+        if (hdr & kFlatComplement) acc_a = ~acc_a;
+        if (hdr_b & kFlatComplement) acc_b = ~acc_b;
+        store(prog[1], acc_a);
+        store(prog_b[1], acc_b);
+        s += 2;
+        continue;
+      }
+      uint32_t acc;
+      if (hdr & kFlatForm) {
+        acc = eval_bound_flat<K, STAGED, G>(rs, prog + kProgHeaderWords, T);
+        if (hdr & kFlatComplement) acc = ~acc;
+      } else {
+        acc = eval_bound_stack<K, KP, STAGED, G>(rs, prog, T, prog[2]);
+      }
+      store(prog[1], acc);
+      ++s;
+    }
+    (void)RW;
+    return;
+  }
+  const ST_CONST uint32_t* progs = a.insns;
+  const ST_CONST uint32_t* starts = a.insn_start;
+  for (uint32_t s = s_begin; s < s_end; ++s) {
+    const ST_CONST uint32_t* prog = progs + starts[s];
+    const uint32_t hdr = prog[0];
+    const uint32_t row = prog[1];
+    const uint32_t T = hdr & 0xFFFFu;
+    uint32_t acc;
+    if (hdr & kFlatForm) {
+      acc = eval_flat<K, KP, STAGED, G>(rs, reinterpret_cast<const ST_CONST u32x4*>(prog + kProgHeaderWords), T);
+      if (hdr & kFlatComplement) acc = ~acc;
+    } else {
+      acc = eval_stack<K, KP, STAGED, G>(rs, prog, T, prog[2]);
+    }
+    store(row, acc);
   }
 }
 
@@ -511,21 +600,23 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     const uint32_t* __restrict__ wave_off,
     const uint32_t* __restrict__ insn_start, const uint32_t* __restrict__ insns,
     const uint64_t* __restrict__ hashes, const uint32_t* __restrict__ bundle_slot,
+    const uint32_t* __restrict__ bundle_order,
     const uint32_t* __restrict__ bound_start, const uint32_t* __restrict__ bound,
     uint32_t bound_words, uint32_t num_terms, int32_t hash_k,
     int64_t out_cols, void* __restrict__ out) {
   SearchArgs a;
   a.index = index;
   a.index_numel = index_numel;
-  a.bundle_offsets = bundle_offsets;
+  a.bundle_offsets = as_const(bundle_offsets);
   a.num_bundles = num_bundles;
-  a.wave_off = wave_off;
-  a.insn_start = insn_start;
-  a.insns = insns;
-  a.hashes = hashes;
-  a.bundle_slot = bundle_slot;
-  a.bound_start = bound_start;
-  a.bound = bound;
+  a.wave_off = as_const(wave_off);
+  a.insn_start = as_const(insn_start);
+  a.insns = as_const(insns);
+  a.hashes = as_const(hashes);
+  a.bundle_slot = as_const(bundle_slot);
+  a.bundle_order = as_const(bundle_order);
+  a.bound_start = as_const(bound_start);
+  a.bound = as_const(bound);
   a.bound_words = bound_words;
   a.num_terms = num_terms;
   a.hash_k = hash_k;
@@ -545,9 +636,12 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     tile[kSearchOnesRow * 16 + (tid & 15) + (tid & 16)] = u32x4{fill, fill, fill, fill};
   }
 
+  // Bundle visited at step i of the grid-stride walk.
+  auto bundle_at = [&](int64_t i) -> int64_t {
+    return a.bundle_order ? static_cast<int64_t>(a.bundle_order[i]) : i;
+  };
   u32x4 pre[kPrefetch];
-  int64_t bundle = blockIdx.x;
-  if (bundle < a.num_bundles) prefetch_tile(a, bundle, pre);
+  if (blockIdx.x < a.num_bundles) prefetch_tile(a, bundle_at(blockIdx.x), pre);
 
   int64_t prev_b = -1;
   const uint32_t s_begin = uniform(a.wave_off[wave]);
@@ -555,7 +649,8 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
   const char* tile_lane = reinterpret_cast<const char*>(tile) + lane * 4;
   const uint32_t* index32 = reinterpret_cast<const uint32_t*>(a.index);
 
-  for (; bundle < a.num_bundles; bundle += gridDim.x) {
+  for (int64_t step = blockIdx.x; step < a.num_bundles; step += gridDim.x) {
+    const int64_t bundle = bundle_at(step);
     int64_t start, b;
     bundle_extent(a, bundle, start, b);
     const bool staged = b <= kSearchTileRows;
@@ -597,8 +692,8 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     }
     __syncthreads();
 
-    const int64_t next = bundle + gridDim.x;
-    if (next < a.num_bundles) prefetch_tile(a, next, pre);
+    const int64_t next = step + gridDim.x;
+    if (next < a.num_bundles) prefetch_tile(a, bundle_at(next), pre);
 
     // Evaluate this wave's queries on the bundle.
     RowSource rs;
@@ -626,7 +721,8 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
 using KernelFn = void (*)(const int64_t*, int64_t, const int64_t*, int64_t,
                           const uint32_t*, const uint32_t*,
                           const uint32_t*, const uint64_t*, const uint32_t*,
-                          const uint32_t*, const uint32_t*, uint32_t, uint32_t, int32_t,
+                          const uint32_t*, const uint32_t*, const uint32_t*, uint32_t,
+                          uint32_t, int32_t,
                           int64_t, void*);
 
 template <int K>
@@ -697,31 +793,19 @@ extern "C" int st_bloom_index_search_batch(
     const int grid = static_cast<int>(
         std::min<int64_t>(num_bundles, static_cast<int64_t>(device_cu_count())));
     const char* blob = static_cast<const char*>(plan_blob_device);
+    const bool bound = plan->bound_bundles >= 0;
+    auto at = [&](uint64_t off) { return reinterpret_cast<const uint32_t*>(blob + off); };
     for (const SearchBatch& bt : plan->batches) {
-      SearchArgs a;
-      a.index = bloom_index;
-      a.index_numel = bloom_index_numel;
-      a.bundle_offsets = bundle_b_offsets;
-      a.num_bundles = num_bundles;
-      a.wave_off = reinterpret_cast<const uint32_t*>(blob + bt.off_wave);
-      a.insn_start = reinterpret_cast<const uint32_t*>(blob + bt.off_insn_start);
-      a.insns = reinterpret_cast<const uint32_t*>(blob + bt.off_insns);
-      a.hashes = reinterpret_cast<const uint64_t*>(blob + bt.off_hashes);
-      const bool bound = plan->bound_bundles >= 0;
-      a.bundle_slot = bound ? reinterpret_cast<const uint32_t*>(blob + plan->off_bundle_slot) : nullptr;
-      a.bound_start = bound ? reinterpret_cast<const uint32_t*>(blob + bt.off_bound_start) : nullptr;
-      a.bound = bound ? reinterpret_cast<const uint32_t*>(blob + bt.off_bound) : nullptr;
-      a.bound_words = bound ? bt.bound_words : 0;
-      a.num_terms = bt.num_terms;
-      a.hash_k = static_cast<int32_t>(plan->hash_k);
-      a.out_cols = num_bundles * 32;
-      a.out = out;
-      hipLaunchKernelGGL(fn, dim3(grid), dim3(kSearchThreads), 0,
-                         static_cast<hipStream_t>(stream), a.index, a.index_numel,
-                         a.bundle_offsets, a.num_bundles, a.wave_off,
-                         a.insn_start, a.insns, a.hashes, a.bundle_slot,
-                         a.bound_start, a.bound, a.bound_words, a.num_terms, a.hash_k,
-                         a.out_cols, a.out);
+      hipLaunchKernelGGL(
+          fn, dim3(grid), dim3(kSearchThreads), 0, static_cast<hipStream_t>(stream),
+          bloom_index, bloom_index_numel, bundle_b_offsets, num_bundles, at(bt.off_wave),
+          at(bt.off_insn_start), at(bt.off_insns),
+          reinterpret_cast<const uint64_t*>(blob + bt.off_hashes),
+          bound ? at(plan->off_bundle_slot) : nullptr,
+          bound ? at(plan->off_bundle_order) : nullptr,
+          bound ? at(bt.off_bound_start) : nullptr, bound ? at(bt.off_bound) : nullptr,
+          bound ? bt.bound_words : 0u, bt.num_terms, static_cast<int32_t>(plan->hash_k),
+          num_bundles * 32, out);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess)
         throw Error(ST_ERR_HIP, cat("search kernel launch failed: ",

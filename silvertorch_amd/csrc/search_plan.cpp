@@ -495,15 +495,29 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
       std::vector<uint32_t> wave_off(kSearchWaves + 1, 0), starts, insns;
       const uint32_t pos_bytes = static_cast<uint32_t>(plan->kp) * 4;
       for (int w = 0; w < kSearchWaves; ++w) {
-        for (int i : per_wave[w]) {
+        // Within a wave: flat programs by decreasing literal count, paired
+        // neighbour by neighbour, then the stack-form ones.
+        auto& list = per_wave[w];
+        std::stable_sort(list.begin(), list.end(), [&](int x, int y) {
+          const CompiledQuery& a = cur[x].cq;
+          const CompiledQuery& c = cur[y].cq;
+          if (a.flat != c.flat) return a.flat;
+          return a.flat && a.lits.size() > c.lits.size();
+        });
+        size_t n_flat = 0;
+        while (n_flat < list.size() && cur[list[n_flat]].cq.flat) ++n_flat;
+        for (size_t li = 0; li < list.size(); ++li) {
+          const int i = list[li];
           const CompiledQuery& cq = cur[i].cq;
           while (insns.size() % 4) insns.push_back(0);  // 16-byte aligned programs
           starts.push_back(static_cast<uint32_t>(insns.size()));
           const uint32_t row = static_cast<uint32_t>(cur[i].row);
+          const bool paired = cq.flat && li % 2 == 0 && li + 1 < n_flat;
           if (cq.flat) {
             insns.insert(insns.end(),
                          {static_cast<uint32_t>(cq.lits.size()) | kFlatForm |
-                              (cq.complement ? kFlatComplement : 0u),
+                              (cq.complement ? kFlatComplement : 0u) |
+                              (paired ? kPairedWithNext : 0u),
                           row, 0u, 0u});
             for (const auto& l : cq.lits) {
               insns.insert(insns.end(), {l.term * pos_bytes, l.neg ? ~0u : 0u,
@@ -633,9 +647,20 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
       auto it = slot_of.find(width[i]);
       bundle_slot[i] = it == slot_of.end() ? kNoWidthSlot : it->second;
     }
+    // Visiting order: bundles grouped by slot (then by width), so that a
+    // workgroup striding through it meets long runs of one width and reuses
+    // that width's programs from the scalar cache.
+    std::vector<uint32_t> order(num_bundles);
+    for (int64_t i = 0; i < num_bundles; ++i) order[i] = static_cast<uint32_t>(i);
+    std::stable_sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) {
+      if (bundle_slot[x] != bundle_slot[y]) return bundle_slot[x] < bundle_slot[y];
+      return width[x] < width[y];
+    });
     auto& blob = plan->blob;
     plan->off_bundle_slot = blob.size();
     append_bytes(blob, bundle_slot.data(), bundle_slot.size() * 4);
+    plan->off_bundle_order = blob.size();
+    append_bytes(blob, order.data(), order.size() * 4);
 
     const size_t nslots = plan->slot_width.size();
     for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
@@ -650,6 +675,16 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
           term_positions(hashes.data() + static_cast<size_t>(u) * plan->hash_k,
                          plan->hash_k, k_eff, plan->slot_width[s], kp,
                          &pos[(s * bt.num_terms + u) * kp]);
+      // Literal count of each bound program: paired flat programs are padded
+      // to the larger count of the pair.
+      std::vector<uint32_t> bound_T(bt.num_slots);
+      for (uint32_t q = 0; q < bt.num_slots; ++q) bound_T[q] = insns[starts[q]] & 0xFFFFu;
+      for (uint32_t q = 0; q + 1 < bt.num_slots; ++q) {
+        if (insns[starts[q]] & kPairedWithNext) {
+          const uint32_t t = std::max(bound_T[q], bound_T[q + 1]);
+          bound_T[q] = bound_T[q + 1] = t;
+        }
+      }
       // layout of one width block (identical for every slot)
       std::vector<uint32_t> bstart(bt.num_slots);
       uint32_t words = 0;
@@ -659,7 +694,7 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
         const uint32_t T = hdr & 0xFFFFu;
         uint32_t n = kProgHeaderWords;
         if (hdr & kFlatForm) {
-          n += T * rw;
+          n += bound_T[q] * rw;
         } else {
           n += T * kp + insns[starts[q] + 2];
         }
@@ -676,12 +711,22 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
           const uint32_t T = hdr & 0xFFFFu;
           for (int w = 0; w < kProgHeaderWords; ++w) dst[w] = src[w];
           if (hdr & kFlatForm) {
+            dst[0] = (hdr & ~0xFFFFu) | bound_T[q];
             for (uint32_t j = 0; j < T; ++j) {
               const uint32_t* lit = src + kProgHeaderWords + j * kFlatLiteralWords;
               const uint32_t* tp = spos + (lit[0] / pos_bytes) * kp;
               uint32_t* rec = dst + kProgHeaderWords + j * rw;
               for (int r = 0; r < k_eff; ++r) rec[r] = tp[r];
               rec[k_eff] = (lit[1] ? 1u : 0u) | (lit[2] ? 2u : 0u);
+            }
+            // no-op padding: AND with the all-ones row inside the last group
+            const bool staged = plan->slot_width[s] <= kSearchTileRows;
+            const uint32_t ones = staged ? static_cast<uint32_t>(kSearchOnesRow) * 256u
+                                         : static_cast<uint32_t>(kPosOnes);
+            for (uint32_t j = T; j < bound_T[q]; ++j) {
+              uint32_t* rec = dst + kProgHeaderWords + j * rw;
+              for (int r = 0; r < k_eff; ++r) rec[r] = ones;
+              rec[k_eff] = 0;
             }
           } else {
             const uint32_t nops = src[2];

@@ -30,7 +30,7 @@ constexpr int kSearchPosSlots = (kSearchLdsBytes - kSearchTileBytes) / 4;
 constexpr int kSearchMaxStack = 8;
 
 // Position codes of the global-memory path (bundles wider than the tile).
-constexpr int32_t kPosOnes = INT32_MIN;
+constexpr int32_t kPosOnes = INT32_MIN;  // (no-op literals of width-bound pairs)
 constexpr int32_t kPosZeros = INT32_MIN + 1;
 
 // A query program is a 16-byte aligned run of uint32 words with a 4-word
@@ -52,6 +52,10 @@ constexpr int32_t kPosZeros = INT32_MIN + 1;
 // then n_ops operations: [2:0] opcode, [4:3] combine mode, [5] negate.
 constexpr uint32_t kFlatForm = 1u << 31;
 constexpr uint32_t kFlatComplement = 1u << 30;
+// Set on the first of two consecutive flat programs of a wave that the
+// width-bound kernel evaluates together; their bound copies are padded to the
+// same literal count with no-op literals (all-ones row, same group).
+constexpr uint32_t kPairedWithNext = 1u << 29;
 constexpr int kFlatMaxLiterals = 64;
 constexpr int kProgHeaderWords = 4;
 constexpr int kFlatLiteralWords = 4;
@@ -131,5 +135,6 @@ struct st_search_plan {
   // set by st_search_plan_bind_widths
   int64_t bound_bundles = -1;        // -1: not bound
   uint64_t off_bundle_slot = 0;      // uint32[bound_bundles]
+  uint64_t off_bundle_order = 0;     // uint32[bound_bundles]: visiting order
   std::vector<int64_t> slot_width;   // width of each slot
 };
