@@ -4,9 +4,11 @@
 Workload ("cfg2"): 10M docs, 8 features, per-doc
 value count uniform in [1, 4], values Zipf(1.1) over a 100k vocabulary, index
 built with K=3, B_MULTIPLIER=5.0; 256 flat AND/OR queries of 2-6 terms,
-HASH_K=7; packed int64 output.  A step is one full op call (plan compile on
-the host, plan upload, search kernel) with the index, bundle offsets and
-query plans resident in HBM.
+HASH_K=7; packed int64 output.  A step is one full op call with the index
+and bundle offsets resident in HBM and the query plans in host memory, as the
+parser returns them and as the reference's bench and BloomIndexSearchModule
+pass them (bloom_index_bench.py:105-138, bloom_index_search_module.py:48-72):
+plan compile and width binding on the host, plan upload, search kernel.
 
 Prints ONE JSON line with the throughput (doc-queries/s), the roofline of
 the search kernel (algorithmic bytes per launch / kernel time from HIP
@@ -73,9 +75,11 @@ bbo = torch.from_numpy(np.load({td!r} + '/bbo.npy'))
 qs = json.load(open({td!r} + '/queries.json'))
 _, (pd, po) = st.parse_expression_query_batch(qs, torch.ones(1, dtype=torch.long), {hash_k}, True, 5)
 st.bloom_index_search_batch(idx, bbo, pd[:0], po[:0], {k}, {hash_k}, False)
-t = time.perf_counter()
-st.bloom_index_search_batch(idx, bbo, pd, po, {k}, {hash_k}, False)
-print(json.dumps({{"seconds": time.perf_counter() - t}}))
+t, passes = time.perf_counter(), 0
+while passes < 8 and (passes == 0 or time.perf_counter() - t < 10.0):
+    st.bloom_index_search_batch(idx, bbo, pd, po, {k}, {hash_k}, False)
+    passes += 1
+print(json.dumps({{"seconds": (time.perf_counter() - t) / passes, "passes": passes}}))
 """
         else:
             kind = "port"
@@ -86,23 +90,27 @@ from oracle import oracle as O, parser_oracle as P
 idx = np.load({td!r} + '/index.npy'); bbo = np.load({td!r} + '/bbo.npy')
 qs = json.load(open({td!r} + '/queries.json'))
 _, data, offs = P.parse_batch(qs, {hash_k})
-t = time.perf_counter()
-O.search_packed(idx, bbo, np.frombuffer(data, np.int8), np.array(offs), {k}, {hash_k})
-print(json.dumps({{"seconds": time.perf_counter() - t}}))
+t, passes = time.perf_counter(), 0
+while passes < 8 and (passes == 0 or time.perf_counter() - t < 10.0):
+    O.search_packed(idx, bbo, np.frombuffer(data, np.int8), np.array(offs), {k}, {hash_k})
+    passes += 1
+print(json.dumps({{"seconds": (time.perf_counter() - t) / passes, "passes": passes}}))
 """
         env = dict(os.environ, OMP_NUM_THREADS="1")
         out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=900)
         if out.returncode != 0:
             log("cpu baseline failed: " + out.stderr[-2000:])
             return None
-        secs = json.loads(out.stdout.strip().splitlines()[-1])["seconds"]
+        res = json.loads(out.stdout.strip().splitlines()[-1])
+        secs, passes = res["seconds"], res["passes"]
     return {
         "value": len(sample) * num_docs / secs,
         "unit": "doc-queries/s",
         "cores": 1,
         "kind": kind,
         "sample": f"{len(sample)} of the {len(queries)} queries over all {num_docs} docs, packed output, "
-                  f"{secs:.2f} s single-threaded ({'reference CPU op compiled from its sources' if kind == 'reference' else 'C oracle'})",
+                  f"mean of {passes} passes of {secs:.2f} s, single-threaded "
+                  f"({'reference CPU op compiled from its sources' if kind == 'reference' else 'C oracle'})",
     }
 
 
@@ -143,13 +151,12 @@ def main():
     del ids, offs, vals
 
     _, (pd, po) = st.parse_expression_query_batch(queries, torch.ones(1, dtype=torch.long), cspec.hash_k, True, 5)
-    pd_d, po_d = pd.to(dev), po.to(dev)
     k, hk = cspec.k, cspec.hash_k
     Q, N = len(queries), cspec.num_docs
     nb = bo.numel() - 1
 
     def step():
-        return st.bloom_index_search_batch(bi, bo, pd_d, po_d, k, hk, args.bool_mask)
+        return st.bloom_index_search_batch(bi, bo, pd, po, k, hk, args.bool_mask)
 
     for _ in range(args.warmup):
         out = step()
@@ -182,6 +189,7 @@ def main():
     # the search kernel is launched on, bracketing only the launch.
     L = capi.lib()
     plan = capi.SearchPlan(pd.numpy().tobytes(), po.numpy(), k, hk)
+    plan.bind_widths(bo.cpu().numpy())  # the op binds its plans to the bundle widths too
     blob = torch.frombuffer(bytearray(plan.blob()), dtype=torch.uint8).to(dev)
     kout = torch.empty_like(out)
     stream = torch.cuda.current_stream()

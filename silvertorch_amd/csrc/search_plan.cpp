@@ -16,6 +16,7 @@
 #include <climits>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <unordered_map>
 
@@ -28,21 +29,35 @@ namespace {
 
 enum class NodeKind { kTerm, kConst, kAnd, kOr, kNot };
 
+// Expression tree of one query.  Child lists live in one shared pool
+// (kids[kb .. kb+kn)), so building and simplifying a tree allocates nothing
+// once the pools have grown to the largest query seen.
 struct Node {
   NodeKind kind;
   bool ones = true;        // kConst: value is all ones (true) or zero
   uint32_t term = 0;       // kTerm: batch-local term id
-  std::vector<int> kids;   // kAnd / kOr / kNot
+  int kb = 0, kn = 0;      // kAnd / kOr / kNot: children
   int need = 0;            // stack slots needed to evaluate
 };
 
 struct Tree {
   std::vector<Node> nodes;
-  int add(Node n) {
-    nodes.push_back(std::move(n));
+  std::vector<int> kids;
+  void clear() {
+    nodes.clear();
+    kids.clear();
+  }
+  int add(const Node& n) {
+    nodes.push_back(n);
     return static_cast<int>(nodes.size()) - 1;
   }
+  int kid(int id, int j) const { return kids[nodes[id].kb + j]; }
 };
+
+// Deepest nesting a query may have; recursion over the tree is bounded by it.
+constexpr int kMaxPlanDepth = 4096;
+// Deepest subtree the flat-form search descends into.
+constexpr int kMaxFlatDepth = 64;
 
 template <typename T>
 T load_le(const int8_t* p) {
@@ -51,33 +66,59 @@ T load_le(const int8_t* p) {
   return v;
 }
 
-// Interns each distinct hash_k-tuple once per batch.
+// Interns each distinct hash_k-tuple once per batch: open addressing on a
+// 64-bit digest of the tuple, verified against the stored hashes.
 struct TermTable {
   int64_t hash_k = 0;
-  std::unordered_map<std::string, uint32_t> ids;
-  std::vector<uint64_t> hashes;
-  std::vector<std::string> added;  // keys interned since the last commit()
-  uint32_t intern(const int8_t* h) {
-    std::string key(reinterpret_cast<const char*>(h),
-                    static_cast<size_t>(hash_k) * 8);
-    auto it = ids.find(key);
-    if (it != ids.end()) return it->second;
-    uint32_t id = static_cast<uint32_t>(ids.size());
-    ids.emplace(key, id);
-    added.push_back(std::move(key));
-    for (int64_t j = 0; j < hash_k; ++j) hashes.push_back(load_le<uint64_t>(h + 8 * j));
-    return id;
+  std::vector<uint64_t> hashes;  // hash_k words per interned term
+  std::vector<uint32_t> slots;   // id + 1 (0 = empty); power-of-two size
+  uint32_t count = 0, committed = 0;
+
+  uint64_t digest(const int8_t* h) const {
+    uint64_t d = 0x9E3779B97F4A7C15ull;
+    for (int64_t j = 0; j < hash_k; ++j) {
+      d = (d ^ load_le<uint64_t>(h + 8 * j)) * 0xFF51AFD7ED558CCDull;
+      d ^= d >> 29;
+    }
+    return d;
   }
-  void commit() { added.clear(); }
-  void rollback() {
-    for (const auto& key : added) ids.erase(key);
-    hashes.resize(ids.size() * static_cast<size_t>(hash_k));
-    added.clear();
+  void place(uint32_t id) {
+    const size_t mask = slots.size() - 1;
+    size_t i = digest(reinterpret_cast<const int8_t*>(hashes.data() + id * hash_k)) & mask;
+    while (slots[i] != 0) i = (i + 1) & mask;
+    slots[i] = id + 1;
+  }
+  void rehash(size_t n) {
+    slots.assign(n, 0);
+    for (uint32_t id = 0; id < count; ++id) place(id);
+  }
+  uint32_t intern(const int8_t* h) {
+    if ((static_cast<size_t>(count) + 1) * 2 > slots.size())
+      rehash(std::max<size_t>(256, slots.size() * 2));
+    const size_t mask = slots.size() - 1;
+    const size_t bytes = static_cast<size_t>(hash_k) * 8;
+    for (size_t i = digest(h) & mask;; i = (i + 1) & mask) {
+      const uint32_t s = slots[i];
+      if (s == 0) {
+        slots[i] = count + 1;
+        hashes.resize(hashes.size() + hash_k);
+        std::memcpy(hashes.data() + count * hash_k, h, bytes);
+        return count++;
+      }
+      if (std::memcmp(hashes.data() + (s - 1) * hash_k, h, bytes) == 0) return s - 1;
+    }
+  }
+  uint32_t size() const { return count; }
+  void commit() { committed = count; }
+  void rollback() {  // forget the terms interned since the last commit()
+    count = committed;
+    hashes.resize(static_cast<size_t>(count) * hash_k);
+    rehash(slots.size());
   }
   void clear() {
-    ids.clear();
+    count = committed = 0;
     hashes.clear();
-    added.clear();
+    std::fill(slots.begin(), slots.end(), 0u);
   }
 };
 
@@ -85,62 +126,79 @@ bool is_leaf(const Tree& t, int id) {
   const Node& n = t.nodes[id];
   if (n.kind == NodeKind::kTerm || n.kind == NodeKind::kConst) return true;
   if (n.kind == NodeKind::kNot) {
-    const Node& c = t.nodes[n.kids[0]];
+    const Node& c = t.nodes[t.kid(id, 0)];
     return c.kind == NodeKind::kTerm || c.kind == NodeKind::kConst;
   }
   return false;
 }
 
+int add_const(Tree& t, bool ones) {
+  Node k;
+  k.kind = NodeKind::kConst;
+  k.ones = ones;
+  return t.add(k);
+}
+
 // Simplifies in place (flatten same-kind children, drop double negation) and
 // computes `need`.  Returns the id that replaces `id`.
 int normalize(Tree& t, int id) {
-  Node& n0 = t.nodes[id];
-  if (n0.kind == NodeKind::kTerm || n0.kind == NodeKind::kConst) {
+  const NodeKind kind = t.nodes[id].kind;
+  if (kind == NodeKind::kTerm || kind == NodeKind::kConst) {
     t.nodes[id].need = 0;
     return id;
   }
-  if (n0.kind == NodeKind::kNot) {
-    int c = normalize(t, t.nodes[id].kids[0]);
-    if (t.nodes[c].kind == NodeKind::kNot) return t.nodes[c].kids[0];
-    if (t.nodes[c].kind == NodeKind::kConst) {
-      Node k;
-      k.kind = NodeKind::kConst;
-      k.ones = !t.nodes[c].ones;
-      return t.add(k);
-    }
-    t.nodes[id].kids[0] = c;
+  if (kind == NodeKind::kNot) {
+    const int c = normalize(t, t.kid(id, 0));
+    if (t.nodes[c].kind == NodeKind::kNot) return t.kid(c, 0);
+    if (t.nodes[c].kind == NodeKind::kConst) return add_const(t, !t.nodes[c].ones);
+    t.kids[t.nodes[id].kb] = c;
     t.nodes[id].need = t.nodes[c].need;
     return id;
   }
-  const NodeKind kind = n0.kind;
-  std::vector<int> flat;
-  std::vector<int> pending = t.nodes[id].kids;
-  for (int c : pending) {
-    int nc = normalize(t, c);
-    if (t.nodes[nc].kind == kind) {
-      for (int g : t.nodes[nc].kids) flat.push_back(g);
+  const int kb = t.nodes[id].kb, kn = t.nodes[id].kn;
+  for (int j = 0; j < kn; ++j) {
+    const int c = normalize(t, t.kids[kb + j]);
+    t.kids[kb + j] = c;
+  }
+  // Flattened child list, appended to the pool.
+  const int fb = static_cast<int>(t.kids.size());
+  for (int j = 0; j < kn; ++j) {
+    const int c = t.kids[kb + j];
+    if (t.nodes[c].kind == kind) {
+      const int cb = t.nodes[c].kb, cn = t.nodes[c].kn;
+      for (int g = 0; g < cn; ++g) {
+        const int v = t.kids[cb + g];
+        t.kids.push_back(v);
+      }
     } else {
-      flat.push_back(nc);
+      t.kids.push_back(c);
     }
   }
-  if (flat.empty()) {
-    Node k;
-    k.kind = NodeKind::kConst;
-    k.ones = (kind == NodeKind::kAnd);
-    return t.add(k);
-  }
-  // Evaluation order: the most demanding subtree first, the other
-  // subtrees by decreasing demand, leaves last.
-  std::stable_sort(flat.begin(), flat.end(), [&](int a, int b) {
-    bool la = is_leaf(t, a), lb = is_leaf(t, b);
+  const int fn = static_cast<int>(t.kids.size()) - fb;
+  if (fn == 0) return add_const(t, kind == NodeKind::kAnd);
+  // Evaluation order: the most demanding subtree first, the other subtrees
+  // by decreasing demand, leaves last (stable insertion sort: lists are short).
+  auto before = [&](int a, int b) {
+    const bool la = is_leaf(t, a), lb = is_leaf(t, b);
     if (la != lb) return !la;
     return t.nodes[a].need > t.nodes[b].need;
-  });
-  int need = t.nodes[flat[0]].need;
-  for (size_t i = 1; i < flat.size(); ++i) {
-    if (!is_leaf(t, flat[i])) need = std::max(need, 1 + t.nodes[flat[i]].need);
+  };
+  int* f = t.kids.data() + fb;
+  for (int i = 1; i < fn; ++i) {
+    const int v = f[i];
+    int j = i;
+    while (j > 0 && before(v, f[j - 1])) {
+      f[j] = f[j - 1];
+      --j;
+    }
+    f[j] = v;
   }
-  t.nodes[id].kids = std::move(flat);
+  int need = t.nodes[f[0]].need;
+  for (int i = 1; i < fn; ++i) {
+    if (!is_leaf(t, f[i])) need = std::max(need, 1 + t.nodes[f[i]].need);
+  }
+  t.nodes[id].kb = fb;
+  t.nodes[id].kn = fn;
   t.nodes[id].need = need;
   return id;
 }
@@ -174,79 +232,104 @@ struct Lit {
   bool operator==(const Lit& o) const { return term == o.term && neg == o.neg; }
 };
 
+// At most kFlatMaxLiterals literals, hence at most as many groups.  Copies
+// move only the used prefix of the arrays.
 struct Dnf {
-  bool is_true = false;             // the constant all-ones
-  std::vector<std::vector<Lit>> groups;  // empty and !is_true: constant zero
-  size_t literals() const {
-    size_t n = 0;
-    for (const auto& g : groups) n += g.size();
-    return n;
+  bool is_true = false;  // the constant all-ones
+  int nlits = 0, ngroups = 0;  // ngroups == 0 and !is_true: constant zero
+  uint8_t gend[kFlatMaxLiterals];  // end of group g in lits
+  Lit lits[kFlatMaxLiterals];
+
+  Dnf() = default;
+  explicit Dnf(bool ones) : is_true(ones) {}
+  Dnf(const Dnf& o) { *this = o; }
+  Dnf& operator=(const Dnf& o) {
+    is_true = o.is_true;
+    nlits = o.nlits;
+    ngroups = o.ngroups;
+    std::memcpy(gend, o.gend, static_cast<size_t>(ngroups));
+    std::memcpy(lits, o.lits, sizeof(Lit) * static_cast<size_t>(nlits));
+    return *this;
+  }
+  int gbegin(int g) const { return g ? gend[g - 1] : 0; }
+  // Appends a group; false when the literal budget would be exceeded.
+  bool push(const Lit* g, int n) {
+    if (nlits + n > kFlatMaxLiterals) return false;
+    for (int i = 0; i < n; ++i) lits[nlits + i] = g[i];
+    nlits += n;
+    gend[ngroups++] = static_cast<uint8_t>(nlits);
+    return true;
   }
 };
 
-Dnf dnf_true() {
-  Dnf d;
-  d.is_true = true;
-  return d;
-}
-
-// Conjunction of two DNFs by distribution; false when the result exceeds cap.
-bool dnf_and(const Dnf& a, const Dnf& b, size_t cap, Dnf& out) {
+// Conjunction of two DNFs by distribution; false when it exceeds the budget.
+bool dnf_and(const Dnf& a, const Dnf& b, Dnf& out) {
   if (a.is_true) { out = b; return true; }
   if (b.is_true) { out = a; return true; }
   Dnf r;
-  for (const auto& ga : a.groups) {
-    for (const auto& gb : b.groups) {
-      std::vector<Lit> g(ga);
-      g.insert(g.end(), gb.begin(), gb.end());
-      std::sort(g.begin(), g.end());
-      g.erase(std::unique(g.begin(), g.end()), g.end());
+  Lit g[2 * kFlatMaxLiterals];
+  for (int ia = 0; ia < a.ngroups; ++ia) {
+    for (int ib = 0; ib < b.ngroups; ++ib) {
+      int n = 0;
+      for (int i = a.gbegin(ia); i < a.gend[ia]; ++i) g[n++] = a.lits[i];
+      for (int i = b.gbegin(ib); i < b.gend[ib]; ++i) g[n++] = b.lits[i];
+      for (int i = 1; i < n; ++i) {  // sort (insertion: groups are short)
+        const Lit v = g[i];
+        int j = i;
+        while (j > 0 && v < g[j - 1]) {
+          g[j] = g[j - 1];
+          --j;
+        }
+        g[j] = v;
+      }
+      n = static_cast<int>(std::unique(g, g + n) - g);
       bool contradiction = false;
-      for (size_t i = 1; i < g.size(); ++i)
-        contradiction |= g[i].term == g[i - 1].term;  // t and ~t
+      for (int i = 1; i < n; ++i) contradiction |= g[i].term == g[i - 1].term;  // t, ~t
       if (contradiction) continue;
-      r.groups.push_back(std::move(g));
-      if (r.literals() > cap) return false;
+      if (!r.push(g, n)) return false;
     }
   }
-  out = std::move(r);
+  out = r;
   return true;
 }
 
-bool to_dnf(const Tree& t, int id, bool negated, size_t cap, Dnf& out) {
+bool to_dnf(const Tree& t, int id, bool negated, int depth, Dnf& out) {
+  if (depth > kMaxFlatDepth) return false;
   const Node& n = t.nodes[id];
   switch (n.kind) {
-    case NodeKind::kTerm:
-      out = Dnf();
-      out.groups.push_back({Lit{n.term, negated}});
+    case NodeKind::kTerm: {
+      out = Dnf(false);
+      const Lit l{n.term, negated};
+      out.push(&l, 1);
       return true;
+    }
     case NodeKind::kConst:
-      out = (n.ones != negated) ? dnf_true() : Dnf();
+      out = Dnf(n.ones != negated);
       return true;
     case NodeKind::kNot:
-      return to_dnf(t, n.kids[0], !negated, cap, out);
+      return to_dnf(t, t.kid(id, 0), !negated, depth + 1, out);
     case NodeKind::kAnd:
     case NodeKind::kOr: {
       const bool conj = (n.kind == NodeKind::kAnd) != negated;
-      Dnf acc = conj ? dnf_true() : Dnf();
-      for (int c : n.kids) {
+      Dnf acc(conj);
+      for (int j = 0; j < n.kn; ++j) {
         Dnf d;
-        if (!to_dnf(t, c, negated, cap, d)) return false;
+        if (!to_dnf(t, t.kid(id, j), negated, depth + 1, d)) return false;
         if (conj) {
           Dnf next;
-          if (!dnf_and(acc, d, cap, next)) return false;
-          acc = std::move(next);
+          if (!dnf_and(acc, d, next)) return false;
+          acc = next;
         } else {
           if (acc.is_true) continue;
           if (d.is_true) {
-            acc = dnf_true();
+            acc = Dnf(true);
             continue;
           }
-          for (auto& g : d.groups) acc.groups.push_back(std::move(g));
-          if (acc.literals() > cap) return false;
+          for (int g = 0; g < d.ngroups; ++g)
+            if (!acc.push(d.lits + d.gbegin(g), d.gend[g] - d.gbegin(g))) return false;
         }
       }
-      out = std::move(acc);
+      out = acc;
       return true;
     }
   }
@@ -254,14 +337,16 @@ bool to_dnf(const Tree& t, int id, bool negated, size_t cap, Dnf& out) {
 }
 
 // Fills cq's flat form when the query (or its complement) has a DNF of at
-// most kFlatMaxLiterals literals.
-bool try_flat(const Tree& t, int root, CompiledQuery& cq) {
+// most kFlatMaxLiterals literals.  A direct form with no more literals than
+// the query has term leaves repeats no term, and the complement cannot be
+// shorter, so it is not tried then.
+bool try_flat(const Tree& t, int root, int term_leaves, CompiledQuery& cq) {
   Dnf direct, inverse;
-  const bool ok_d = to_dnf(t, root, false, kFlatMaxLiterals, direct);
-  const bool ok_i = to_dnf(t, root, true, kFlatMaxLiterals, inverse);
+  const bool ok_d = to_dnf(t, root, false, 0, direct);
+  const bool ok_i = !(ok_d && direct.nlits <= term_leaves) &&
+                    to_dnf(t, root, true, 0, inverse);
   if (!ok_d && !ok_i) return false;
-  const bool use_inverse =
-      !ok_d || (ok_i && inverse.literals() < direct.literals());
+  const bool use_inverse = !ok_d || (ok_i && inverse.nlits < direct.nlits);
   const Dnf& d = use_inverse ? inverse : direct;
   cq.flat = true;
   cq.lits.clear();
@@ -270,9 +355,11 @@ bool try_flat(const Tree& t, int root, CompiledQuery& cq) {
     return true;
   }
   cq.complement = use_inverse;
-  for (const auto& g : d.groups) {
-    for (size_t i = 0; i < g.size(); ++i)
-      cq.lits.push_back(CompiledQuery::FlatLit{g[i].term, g[i].neg, i == 0});
+  cq.lits.reserve(d.nlits);
+  for (int g = 0; g < d.ngroups; ++g) {
+    for (int i = d.gbegin(g); i < d.gend[g]; ++i)
+      cq.lits.push_back(CompiledQuery::FlatLit{d.lits[i].term, d.lits[i].neg,
+                                               i == d.gbegin(g)});
   }
   return true;
 }
@@ -283,7 +370,7 @@ void emit_leaf(const Tree& t, int id, uint32_t mode, CompiledQuery& out) {
   const Node* leaf = &n;
   if (n.kind == NodeKind::kNot) {
     neg = true;
-    leaf = &t.nodes[n.kids[0]];
+    leaf = &t.nodes[t.kid(id, 0)];
   }
   if (leaf->kind == NodeKind::kTerm) {
     out.terms.push_back(leaf->term);
@@ -300,14 +387,14 @@ void emit(const Tree& t, int id, CompiledQuery& out) {
   }
   const Node& n = t.nodes[id];
   if (n.kind == NodeKind::kNot) {
-    emit(t, n.kids[0], out);
+    emit(t, t.kid(id, 0), out);
     out.ops.push_back(encode_insn(kInsNot, 0, false));
     return;
   }
   const uint32_t mode = n.kind == NodeKind::kAnd ? kModeAnd : kModeOr;
-  emit(t, n.kids[0], out);
-  for (size_t i = 1; i < n.kids.size(); ++i) {
-    int c = n.kids[i];
+  emit(t, t.kid(id, 0), out);
+  for (int i = 1; i < n.kn; ++i) {
+    const int c = t.kid(id, i);
     if (is_leaf(t, c)) {
       emit_leaf(t, c, mode, out);
     } else {
@@ -318,11 +405,19 @@ void emit(const Tree& t, int id, CompiledQuery& out) {
   }
 }
 
+// Per-thread working storage of the compiler, kept between calls so that
+// compiling a batch allocates only its results.
+struct CompileScratch {
+  Tree tree;
+  std::vector<int> stack;
+  std::vector<int> depth;
+};
+
 // Decodes query q, builds its tree and returns its program.  Terms are
 // interned in `terms` (ids are batch-local).
 CompiledQuery compile_query(const int8_t* data, int64_t data_len,
                             const int64_t* offs, int64_t q, int64_t hash_k,
-                            int k_eff, TermTable& terms) {
+                            int k_eff, TermTable& terms, CompileScratch& cs) {
   const int64_t* o = offs + 8 * q;
   for (int j = 0; j < 8; j += 2) {
     ST_CHECK(o[j] >= 0 && o[j] <= o[j + 1] && o[j + 1] <= data_len,
@@ -338,8 +433,12 @@ CompiledQuery compile_query(const int8_t* data, int64_t data_len,
   const int8_t* hashes = data + o[6];
   ST_CHECK(n_ops > 0, "query plan ", q, " has no operators");
 
-  Tree tree;
-  std::vector<int> stack;
+  Tree& tree = cs.tree;
+  std::vector<int>& stack = cs.stack;
+  std::vector<int>& depth = cs.depth;  // nesting depth of each stack entry
+  tree.clear();
+  stack.clear();
+  depth.clear();
   int64_t term_counter = 0;
   auto child_count = [&](int64_t i) -> int32_t {
     ST_CHECK(i + 1 < n_offsets, "query plan ", q, ": operator ", i,
@@ -347,6 +446,12 @@ CompiledQuery compile_query(const int8_t* data, int64_t data_len,
              " entries)");
     return load_le<int32_t>(offsets + 4 * (i + 1)) -
            load_le<int32_t>(offsets + 4 * i);
+  };
+  auto push = [&](const Node& n, int d) {
+    ST_CHECK(d <= kMaxPlanDepth, "query plan ", q, " nests operators more than ",
+             kMaxPlanDepth, " levels deep");
+    stack.push_back(tree.add(n));
+    depth.push_back(d);
   };
   for (int64_t i = 0; i < n_ops; ++i) {
     const uint8_t op = static_cast<uint8_t>(ops[i]);
@@ -366,41 +471,52 @@ CompiledQuery compile_query(const int8_t* data, int64_t data_len,
           n.term = terms.intern(hashes + 8 * term_counter * hash_k);
         }
         ++term_counter;
-        stack.push_back(tree.add(n));
+        push(n, 1);
         break;
       }
       case kOpEmpty: {
         Node n;
         n.kind = NodeKind::kConst;
         n.ones = true;
-        stack.push_back(tree.add(n));
+        push(n, 1);
         break;
       }
       case kOpAnd:
       case kOpOr: {
-        int32_t children = child_count(i);
+        // A count below one pops nothing: the operator's identity results.
+        const int32_t children = std::max<int32_t>(child_count(i), 0);
+        ST_CHECK(static_cast<size_t>(children) <= stack.size(), "query plan ", q,
+                 ": operator ", i, " pops ", child_count(i),
+                 " values from a shorter stack");
         Node n;
         n.kind = op == kOpAnd ? NodeKind::kAnd : NodeKind::kOr;
-        for (int32_t j = 0; j < children; ++j) {
-          ST_CHECK(!stack.empty(), "query plan ", q, ": operator ", i,
-                   " pops ", children, " values from a shorter stack");
-          n.kids.push_back(stack.back());
+        n.kb = static_cast<int>(tree.kids.size());
+        n.kn = children;
+        int d = 0;
+        for (int32_t j = 0; j < children; ++j) {  // top of the stack first
+          tree.kids.push_back(stack.back());
+          d = std::max(d, depth.back());
           stack.pop_back();
+          depth.pop_back();
         }
-        stack.push_back(tree.add(n));
+        push(n, d + 1);
         break;
       }
       case kOpNot: {
-        int32_t children = child_count(i);
+        const int32_t children = child_count(i);
         ST_CHECK(children == 1, "NOT query should have 1 parameter, but got ",
                  children);
         ST_CHECK(!stack.empty(), "query plan ", q, ": NOT operator ", i,
                  " applied to an empty stack");
         Node n;
         n.kind = NodeKind::kNot;
-        n.kids.push_back(stack.back());
+        n.kb = static_cast<int>(tree.kids.size());
+        n.kn = 1;
+        tree.kids.push_back(stack.back());
+        const int d = depth.back();
         stack.pop_back();
-        stack.push_back(tree.add(n));
+        depth.pop_back();
+        push(n, d + 1);
         break;
       }
       default:
@@ -408,9 +524,9 @@ CompiledQuery compile_query(const int8_t* data, int64_t data_len,
     }
   }
   ST_CHECK(!stack.empty(), "query plan ", q, " leaves an empty stack");
-  int root = normalize(tree, stack.back());
+  const int root = normalize(tree, stack.back());
   CompiledQuery cq;
-  if (try_flat(tree, root, cq)) return cq;
+  if (try_flat(tree, root, static_cast<int>(term_counter), cq)) return cq;
   emit(tree, root, cq);
   cq.need = tree.nodes[root].need;
   ST_CHECK(cq.need <= kSearchMaxStack, "query plan ", q, " needs ", cq.need,
@@ -419,6 +535,27 @@ CompiledQuery compile_query(const int8_t* data, int64_t data_len,
            "query plan ", q, " is too long (", cq.terms.size(), " terms, ",
            cq.ops.size(), " operations)");
   return cq;
+}
+
+// Blob buffers of destroyed plans, kept with their capacity: a fresh buffer
+// of a few hundred KB would be mapped anew by the allocator on every call and
+// page-faulted in word by word.
+std::mutex g_blob_pool_mu;
+std::vector<std::vector<uint8_t>> g_blob_pool;
+constexpr size_t kBlobPoolSize = 4;
+
+std::vector<uint8_t> take_blob_buffer() {
+  std::lock_guard<std::mutex> lock(g_blob_pool_mu);
+  if (g_blob_pool.empty()) return {};
+  std::vector<uint8_t> b = std::move(g_blob_pool.back());
+  g_blob_pool.pop_back();
+  b.clear();
+  return b;
+}
+
+void return_blob_buffer(std::vector<uint8_t>&& b) {
+  std::lock_guard<std::mutex> lock(g_blob_pool_mu);
+  if (g_blob_pool.size() < kBlobPoolSize) g_blob_pool.push_back(std::move(b));
 }
 
 void append_bytes(std::vector<uint8_t>& blob, const void* p, size_t n) {
@@ -451,6 +588,7 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
              " positions per term; at most ", kMaxSearchK, " are supported");
 
     auto plan = std::make_unique<st_search_plan>();
+    plan->blob = take_blob_buffer();
     plan->num_queries = num_queries;
     plan->hash_k = hash_k;
     plan->k_eff = static_cast<int>(k_eff);
@@ -464,14 +602,16 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
       CompiledQuery cq;
     };
     std::vector<Pending> cur;
-    TermTable terms;
+    static thread_local TermTable terms;
+    static thread_local CompileScratch scratch;
     terms.hash_k = std::max<int64_t>(hash_k, 0);
+    terms.clear();
 
     auto flush = [&]() {
       if (cur.empty()) return;
       SearchBatch b;
       b.num_slots = static_cast<uint32_t>(cur.size());
-      b.num_terms = static_cast<uint32_t>(terms.ids.size());
+      b.num_terms = terms.size();
       // Longest-processing-time assignment of queries to the waves of a
       // workgroup; cost ~ LDS word reads plus instruction count.
       std::vector<int> order(cur.size());
@@ -552,14 +692,14 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
     for (int64_t q = 0; q < num_queries; ++q) {
       CompiledQuery cq = compile_query(plans_data, plans_data_len,
                                        plans_offsets, q, hash_k,
-                                       plan->k_eff, terms);
-      if (static_cast<int64_t>(terms.ids.size()) > term_capacity) {
+                                       plan->k_eff, terms, scratch);
+      if (static_cast<int64_t>(terms.size()) > term_capacity) {
         terms.rollback();
         flush();
         cq = compile_query(plans_data, plans_data_len, plans_offsets, q,
-                           hash_k, plan->k_eff, terms);
-        ST_CHECK(static_cast<int64_t>(terms.ids.size()) <= term_capacity,
-                 "query plan ", q, " has ", terms.ids.size(),
+                           hash_k, plan->k_eff, terms, scratch);
+        ST_CHECK(static_cast<int64_t>(terms.size()) <= term_capacity,
+                 "query plan ", q, " has ", terms.size(),
                  " distinct terms; at most ", term_capacity,
                  " fit one search pass at k = ", plan->k_eff);
       }
@@ -583,12 +723,12 @@ namespace {
 // (row * 256, the all-zeros row when nothing resolves); others get signed
 // rows relative to the bundle start (kPosZeros when nothing resolves).
 void term_positions(const uint64_t* h, int64_t hash_k, int k_eff, int64_t b,
-                    int slots, uint32_t* out) {
+                    const FastMod64& fm, int slots, uint32_t* out) {
   int16_t found[kMaxSearchK] = {0};
   int cnt = 0;
   if (b > 0) {
     for (int64_t p = 0; p < hash_k && cnt < k_eff; ++p) {
-      const int16_t bp = static_cast<int16_t>(h[p] % static_cast<uint64_t>(b));
+      const int16_t bp = static_cast<int16_t>(fast_mod(h[p], fm));
       bool dup = false;
       for (int j = 0; j < cnt; ++j) dup |= found[j] == bp;
       if (!dup) found[cnt++] = bp;
@@ -624,38 +764,64 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
     const int rw = bound_record_words(k_eff);
     const uint32_t pos_bytes = static_cast<uint32_t>(kp) * 4;
 
-    // Most frequent widths get slots (ties to the smaller width).
+    // Most frequent widths get slots (ties to the smaller width).  Census in
+    // an open-addressed table keyed by width (few distinct widths).
     std::vector<int64_t> width(num_bundles);
-    std::unordered_map<int64_t, int64_t> freq;
+    std::vector<std::pair<int64_t, int64_t>> census;  // (width, bundles)
+    std::vector<int32_t> cell(64, -1);  // index into census
+    auto cell_of = [&](int64_t w) -> int32_t& {
+      size_t m = cell.size() - 1;
+      size_t i = static_cast<size_t>(static_cast<uint64_t>(w) * 0x9E3779B97F4A7C15ull >> 40) & m;
+      while (cell[i] >= 0 && census[cell[i]].first != w) i = (i + 1) & m;
+      return cell[i];
+    };
     for (int64_t i = 0; i < num_bundles; ++i) {
-      width[i] = std::max<int64_t>(bundle_b_offsets[i + 1] - bundle_b_offsets[i], 0);
-      ++freq[width[i]];
+      const int64_t w = std::max<int64_t>(bundle_b_offsets[i + 1] - bundle_b_offsets[i], 0);
+      width[i] = w;
+      int32_t& c = cell_of(w);
+      if (c < 0) {
+        c = static_cast<int32_t>(census.size());
+        census.emplace_back(w, 0);
+        if (census.size() * 2 > cell.size()) {  // grow and re-place
+          cell.assign(cell.size() * 2, -1);
+          for (size_t j = 0; j < census.size(); ++j) cell_of(census[j].first) = static_cast<int32_t>(j);
+        }
+      }
+      ++census[cell_of(w)].second;
     }
-    std::vector<std::pair<int64_t, int64_t>> by_freq(freq.begin(), freq.end());
+    std::vector<std::pair<int64_t, int64_t>> by_freq = census;
     std::sort(by_freq.begin(), by_freq.end(), [](const auto& a, const auto& c) {
       return a.second != c.second ? a.second > c.second : a.first < c.first;
     });
     if (by_freq.size() > static_cast<size_t>(kMaxWidthSlots)) by_freq.resize(kMaxWidthSlots);
-    std::unordered_map<int64_t, uint32_t> slot_of;
+    // slot of each census entry
+    std::vector<uint32_t> census_slot(census.size(), kNoWidthSlot);
     plan->slot_width.clear();
     for (const auto& wf : by_freq) {
-      slot_of[wf.first] = static_cast<uint32_t>(plan->slot_width.size());
+      census_slot[cell_of(wf.first)] = static_cast<uint32_t>(plan->slot_width.size());
       plan->slot_width.push_back(wf.first);
     }
     std::vector<uint32_t> bundle_slot(num_bundles);
-    for (int64_t i = 0; i < num_bundles; ++i) {
-      auto it = slot_of.find(width[i]);
-      bundle_slot[i] = it == slot_of.end() ? kNoWidthSlot : it->second;
-    }
+    for (int64_t i = 0; i < num_bundles; ++i) bundle_slot[i] = census_slot[cell_of(width[i])];
     // Visiting order: bundles grouped by slot (then by width), so that a
     // workgroup striding through it meets long runs of one width and reuses
     // that width's programs from the scalar cache.
+    // A slot fixes the width, so a counting sort by slot does it; bundles
+    // without a slot (kNoWidthSlot) go last, stably sorted by width.
     std::vector<uint32_t> order(num_bundles);
-    for (int64_t i = 0; i < num_bundles; ++i) order[i] = static_cast<uint32_t>(i);
-    std::stable_sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) {
-      if (bundle_slot[x] != bundle_slot[y]) return bundle_slot[x] < bundle_slot[y];
-      return width[x] < width[y];
-    });
+    {
+      const size_t nsl = plan->slot_width.size();
+      std::vector<int64_t> first(nsl + 2, 0);
+      for (int64_t i = 0; i < num_bundles; ++i)
+        ++first[(bundle_slot[i] == kNoWidthSlot ? nsl : bundle_slot[i]) + 1];
+      for (size_t j = 1; j < first.size(); ++j) first[j] += first[j - 1];
+      const int64_t unslotted = first[nsl];  // start of the kNoWidthSlot bucket
+      for (int64_t i = 0; i < num_bundles; ++i)
+        order[first[bundle_slot[i] == kNoWidthSlot ? nsl : bundle_slot[i]]++] =
+            static_cast<uint32_t>(i);
+      std::stable_sort(order.begin() + unslotted, order.end(),
+                       [&](uint32_t x, uint32_t y) { return width[x] < width[y]; });
+    }
     auto& blob = plan->blob;
     plan->off_bundle_slot = blob.size();
     append_bytes(blob, bundle_slot.data(), bundle_slot.size() * 4);
@@ -669,15 +835,18 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
       const auto& starts = plan->batch_starts[bi];
       const auto& hashes = plan->batch_hashes[bi];
       // positions of every term at every slot width
-      std::vector<uint32_t> pos(nslots * bt.num_terms * kp);
-      for (size_t s = 0; s < nslots; ++s)
+      static thread_local std::vector<uint32_t> pos, bound_T, bstart;
+      pos.resize(nslots * bt.num_terms * kp);
+      for (size_t s = 0; s < nslots; ++s) {
+        const FastMod64 fm = make_fastmod(static_cast<uint64_t>(plan->slot_width[s]));
         for (uint32_t u = 0; u < bt.num_terms; ++u)
           term_positions(hashes.data() + static_cast<size_t>(u) * plan->hash_k,
-                         plan->hash_k, k_eff, plan->slot_width[s], kp,
+                         plan->hash_k, k_eff, plan->slot_width[s], fm, kp,
                          &pos[(s * bt.num_terms + u) * kp]);
+      }
       // Literal count of each bound program: paired flat programs are padded
       // to the larger count of the pair.
-      std::vector<uint32_t> bound_T(bt.num_slots);
+      bound_T.resize(bt.num_slots);
       for (uint32_t q = 0; q < bt.num_slots; ++q) bound_T[q] = insns[starts[q]] & 0xFFFFu;
       for (uint32_t q = 0; q + 1 < bt.num_slots; ++q) {
         if (insns[starts[q]] & kPairedWithNext) {
@@ -686,7 +855,7 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
         }
       }
       // layout of one width block (identical for every slot)
-      std::vector<uint32_t> bstart(bt.num_slots);
+      bstart.resize(bt.num_slots);
       uint32_t words = 0;
       for (uint32_t q = 0; q < bt.num_slots; ++q) {
         bstart[q] = words;
@@ -700,9 +869,15 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
         }
         words += (n + 3) & ~3u;
       }
-      std::vector<uint32_t> block(nslots * words, 0);
+      bt.bound_words = words;
+      bt.off_bound_start = blob.size();
+      append_bytes(blob, bstart.data(), bstart.size() * 4);
+      // The width blocks are written in place at the end of the blob.
+      bt.off_bound = blob.size();
+      blob.resize(blob.size() + nslots * words * 4, 0);
+      uint32_t* block = reinterpret_cast<uint32_t*>(blob.data() + bt.off_bound);
       for (size_t s = 0; s < nslots; ++s) {
-        uint32_t* base = block.data() + s * words;
+        uint32_t* base = block + s * words;
         const uint32_t* spos = pos.data() + s * bt.num_terms * kp;
         for (uint32_t q = 0; q < bt.num_slots; ++q) {
           const uint32_t* src = insns.data() + starts[q];
@@ -739,11 +914,6 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
           }
         }
       }
-      bt.bound_words = words;
-      bt.off_bound_start = blob.size();
-      append_bytes(blob, bstart.data(), bstart.size() * 4);
-      bt.off_bound = blob.size();
-      append_bytes(blob, block.data(), block.size() * 4);
     }
     // Scalar loads may read a few words past the last program.
     blob.resize(blob.size() + 256, 0);
@@ -763,4 +933,8 @@ extern "C" const void* st_search_plan_blob(const st_search_plan* plan) {
   return plan ? plan->blob.data() : nullptr;
 }
 
-extern "C" void st_search_plan_destroy(st_search_plan* plan) { delete plan; }
+extern "C" void st_search_plan_destroy(st_search_plan* plan) {
+  if (plan == nullptr) return;
+  st::return_blob_buffer(std::move(plan->blob));
+  delete plan;
+}

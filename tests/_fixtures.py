@@ -4,6 +4,7 @@ from __future__ import annotations
 
 import hashlib
 import json
+import struct
 from functools import lru_cache
 from pathlib import Path
 
@@ -59,3 +60,14 @@ def wide_corpus():
     offs = np.concatenate([[0], np.cumsum(cnt)]).astype(np.int64)
     vals = (np.arange(int(offs[-1]), dtype=np.int64) * 7919) % 100003
     return np.array([5], dtype=np.int32), offs, vals, w
+
+
+def encode_plan(ops, offsets, hashes, params=()):
+    """Encodes one plan in the reference's layout (bloom_index_util.cpp:81-124)."""
+    buf, offs = bytearray(), []
+    for raw in (bytes(ops), struct.pack(f"<{len(offsets)}i", *offsets),
+                struct.pack(f"<{len(params)}i", *params), struct.pack(f"<{len(hashes)}Q", *hashes)):
+        start = len(buf)
+        buf += raw + b"\0" * ((-len(raw)) % 8)
+        offs += [start, start + len(raw)]
+    return bytes(buf), offs

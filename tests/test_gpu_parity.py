@@ -191,6 +191,35 @@ def test_edge_cases():
     assert (got[0] == 0).all() and (got[1] == -1).all() and (got[2] == -1).all()
 
 
+def test_hand_built_plans():
+    """Plans the parser never writes: a negative child count (the operator
+    pops nothing and pushes its identity), 4000 nested NOTs, and a query
+    whose flat form repeats a term."""
+    c = G.case("features10x3")
+    index, bbo = c["index"], c["bundle_b_offsets"]
+    _, data, offs = P.parse_batch(["1:2"], 7)
+    h = list(np.frombuffer(data[offs[6]:offs[7]], dtype="<u8"))
+    plans = [
+        ([4, 1], [0, 1, -2], h),               # TERM, AND(-3 children) -> all ones
+        ([4, 2], [0, 1, -1], h),               # TERM, OR(-2 children) -> zero
+        ([4] + [3] * 4000, list(range(4002)), h),  # NOT^4000 TERM = TERM
+        ([4, 4, 4, 1, 2], [0, 1, 2, 3, 5, 7], h * 3),  # t OR (t AND t)
+    ]
+    pd, po = bytearray(), []
+    for ops, o, hs in plans:
+        d, of = G.encode_plan(ops, o, hs)
+        po += [x + len(pd) for x in of]
+        pd += d
+    pd = np.frombuffer(bytes(pd), dtype=np.int8).copy()
+    po = np.array(po, dtype=np.int64)
+    H.note("[hand-built plans]")
+    got = H.search(index, bbo, pd, po, 3, 7)
+    want = O.search_packed(index, bbo, pd, po, 3, 7)
+    np.testing.assert_array_equal(got, want)
+    assert (got[0] == -1).all() and (got[1] == 0).all()
+    np.testing.assert_array_equal(got[2], got[3])
+
+
 # ------------------------------------------------ drop-in path (torch.ops.st)
 
 def _make_features(num_docs, num_features):  # test_bloom_index_search.py:41-53

@@ -94,15 +94,7 @@ def test_parser_matches_oracle_on_random_expressions():
         assert capi.parse_expression_query_batch(exprs, hk, True, ms) == P.parse_batch(exprs, hk, True, ms)
 
 
-def _plan(ops, offsets, hashes, params=()):
-    """Encodes one plan in the reference's layout (bloom_index_util.cpp:81-124)."""
-    buf, offs = bytearray(), []
-    for raw in (bytes(ops), struct.pack(f"<{len(offsets)}i", *offsets),
-                struct.pack(f"<{len(params)}i", *params), struct.pack(f"<{len(hashes)}Q", *hashes)):
-        start = len(buf)
-        buf += raw + b"\0" * ((-len(raw)) % 8)
-        offs += [start, start + len(raw)]
-    return bytes(buf), offs
+_plan = G.encode_plan
 
 
 def test_plan_compiler_accepts_reference_plans():
@@ -135,6 +127,22 @@ def test_plan_compiler_limits():
     capi.SearchPlan(data, offs, 0, 7)  # every term is all ones
     with pytest.raises(capi.StError, match="outside plans_data"):
         capi.SearchPlan(data, [0, 1, 8, 12, 16, 16, 16, 10_000], 3, 7)
+
+
+def test_plan_compiler_nesting_and_identity_operators():
+    # 5000 nested NOTs around one term: deeper than the compiler's recursion
+    # bound, rejected with an error instead of exhausting the host stack.
+    n = 5000
+    data, offs = _plan([4] + [3] * n, list(range(n + 2)), list(range(7)))
+    with pytest.raises(capi.StError, match="levels deep"):
+        capi.SearchPlan(data, offs, 3, 7)
+    # 4000 levels are accepted (double negations cancel).
+    data, offs = _plan([4] + [3] * 4000, list(range(4002)), list(range(7)))
+    capi.SearchPlan(data, offs, 3, 7)
+    # A negative child count pops nothing, as the reference's pop loop does
+    # not run: AND/OR push their identity.
+    data, offs = _plan([4, 1], [0, 1, -2], list(range(7)))
+    assert capi.SearchPlan(data, offs, 3, 7).num_queries == 1
 
 
 def test_torch_ops_schemas_and_cpu_parser():
