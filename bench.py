@@ -49,7 +49,22 @@ def parse_args():
     p.add_argument("--cpu-queries", type=int, default=256,
                    help="queries of the batch the reference CPU search is timed on")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only run a plain 512 MiB device-to-device copy, 5 times: the known-size "
+                        "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings")
     return p.parse_args()
+
+
+def calibrate_copy():
+    import torch
+
+    n = 512 << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n, "launches": 5}), flush=True)
 
 
 def cpu_baseline(index, bbo, queries, k, hash_k, num_docs, n_queries):
@@ -116,6 +131,9 @@ print(json.dumps({{"seconds": (time.perf_counter() - t) / passes, "passes": pass
 
 def main():
     args = parse_args()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
