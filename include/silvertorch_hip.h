@@ -214,6 +214,29 @@ int st_generate_column_info_for_clusters(const int64_t* offsets,
                                          int32_t* start_columns,
                                          int8_t* first_offsets, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Compaction of matching doc ids.  No reference operator: the reference's
+ * users call mask[:, :num_docs].nonzero() on the search output (README.md:
+ * 191-193, :265-266 of the reference).  `packed` is a packed search output,
+ * int64[num_queries, num_columns] (device).  The ids of query q are the
+ * ascending d < num_docs whose bit is set, stored at
+ * ids[row_offsets[q] .. row_offsets[q+1]).
+ *   1. st_bloom_compact_offsets: counts and scans; writes row_offsets
+ *      (device int64[num_queries + 1]) and the per-chunk output positions into
+ *      `workspace` (device, st_bloom_compact_workspace_bytes bytes).
+ *   2. the caller reads row_offsets[num_queries] (the total) and allocates ids.
+ *   3. st_bloom_compact_ids: writes the ids (int32 unless ids_int64; int32
+ *      requires doc ids below 2^31).  Needs the workspace of step 1 unchanged.
+ * ------------------------------------------------------------------------- */
+int64_t st_bloom_compact_workspace_bytes(int64_t num_queries, int64_t num_columns);
+int st_bloom_compact_offsets(const int64_t* packed, int64_t num_queries,
+                             int64_t num_columns, int64_t num_docs,
+                             void* workspace, int64_t* row_offsets, void* stream);
+int st_bloom_compact_ids(const int64_t* packed, int64_t num_queries,
+                         int64_t num_columns, int64_t num_docs,
+                         const void* workspace, void* ids, int ids_int64,
+                         void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -43,6 +43,7 @@ LIB_SOURCES = [
     "st_runtime.hip",
     "bloom_search.hip",
     "bloom_build.hip",
+    "bloom_compact.hip",
     "search_plan.cpp",
     "expression_parser.cpp",
 ]

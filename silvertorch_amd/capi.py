@@ -38,6 +38,9 @@ SIGNATURES = {
     "st_parsed_plans_offsets": (_vp, [_vp]),
     "st_parsed_plans_destroy": (None, [_vp]),
     "st_generate_column_info_for_clusters": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _vp, _vp]),
+    "st_bloom_compact_workspace_bytes": (_i64, [_i64, _i64]),
+    "st_bloom_compact_offsets": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp]),
+    "st_bloom_compact_ids": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, ctypes.c_int, _vp]),
 }
 
 _lib = None

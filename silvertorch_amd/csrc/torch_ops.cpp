@@ -17,6 +17,7 @@
 #include <Python.h>
 #include <torch/library.h>
 
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -280,6 +281,72 @@ std::tuple<Tensor, Tensor, Tensor> column_info(const Tensor& offsets_in,
   return {counts, starts, firsts};
 }
 
+// ------------------------------------------ compaction of matching ids
+// No reference operator: the reference's users call
+// mask[:, :num_docs].nonzero() on the search output (README.md:191-193).
+
+std::tuple<Tensor, Tensor> mask_to_ids_gpu(const Tensor& packed_in, int64_t num_docs,
+                                           bool int64_ids) {
+  TORCH_CHECK(packed_in.is_cuda(), "packed_mask must be a GPU tensor");
+  TORCH_CHECK(packed_in.dim() == 2 && packed_in.scalar_type() == at::kLong,
+              "packed_mask must be the 2-D int64 packed search output");
+  TORCH_CHECK(num_docs >= 0, "num_docs must be non-negative, got ", num_docs);
+  const auto dev = packed_in.device();
+  c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(dev);
+  const Tensor packed = packed_in.contiguous();
+  const int64_t Q = packed.size(0), C = packed.size(1);
+  TORCH_CHECK(int64_ids || std::min(num_docs, C * ST_BITS_PER_COLUMN) <= INT32_MAX,
+              "int32 ids cannot hold doc ids up to ", num_docs, "; pass int64_ids=True");
+  auto opts = at::TensorOptions().device(dev);
+  Tensor row_offsets = at::empty({Q + 1}, opts.dtype(at::kLong));
+  Tensor ws = at::empty({std::max<int64_t>(st_bloom_compact_workspace_bytes(Q, C), 1)},
+                        opts.dtype(at::kByte));
+  void* stream = current_stream(packed);
+  check_st(st_bloom_compact_offsets(packed.numel() ? packed.data_ptr<int64_t>() : nullptr,
+                                    Q, C, num_docs, ws.data_ptr(),
+                                    row_offsets.data_ptr<int64_t>(), stream),
+           "bloom_mask_to_ids");
+  const int64_t total = row_offsets[Q].item<int64_t>();  // the id count sizes the output
+  Tensor ids = at::empty({total}, opts.dtype(int64_ids ? at::kLong : at::kInt));
+  if (total > 0) {
+    check_st(st_bloom_compact_ids(packed.data_ptr<int64_t>(), Q, C, num_docs, ws.data_ptr(),
+                                  ids.data_ptr(), int64_ids ? 1 : 0, stream),
+             "bloom_mask_to_ids");
+  }
+  return {ids, row_offsets};
+}
+
+std::tuple<Tensor, Tensor> mask_to_ids_cpu(const Tensor& packed, int64_t num_docs,
+                                           bool int64_ids) {
+  TORCH_CHECK(packed.dim() == 2 && packed.scalar_type() == at::kLong,
+              "packed_mask must be the 2-D int64 packed search output");
+  const at::Device gpu = gpu_for_cpu_call();
+  auto [ids, ro] = mask_to_ids_gpu(packed.to(gpu), num_docs, int64_ids);
+  return {ids.cpu(), ro.cpu()};
+}
+
+std::tuple<Tensor, Tensor> search_ids_gpu(const Tensor& bloom_index,
+                                          const Tensor& bundle_b_offsets,
+                                          const Tensor& plans_data,
+                                          const Tensor& plans_offsets, int64_t k,
+                                          int64_t hash_k, int64_t num_docs,
+                                          bool int64_ids) {
+  const Tensor packed = search_gpu(bloom_index, bundle_b_offsets, plans_data,
+                                   plans_offsets, k, hash_k, /*return_bool_mask=*/false);
+  return mask_to_ids_gpu(packed, num_docs, int64_ids);
+}
+
+std::tuple<Tensor, Tensor> search_ids_cpu(const Tensor& bloom_index,
+                                          const Tensor& bundle_b_offsets,
+                                          const Tensor& plans_data,
+                                          const Tensor& plans_offsets, int64_t k,
+                                          int64_t hash_k, int64_t num_docs,
+                                          bool int64_ids) {
+  const Tensor packed = search_cpu_tensors(bloom_index, bundle_b_offsets, plans_data,
+                                           plans_offsets, k, hash_k, false);
+  return mask_to_ids_cpu(packed, num_docs, int64_ids);
+}
+
 }  // namespace
 
 TORCH_LIBRARY_FRAGMENT(st, m) {
@@ -299,6 +366,15 @@ TORCH_LIBRARY_FRAGMENT(st, m) {
   m.def(
       "generate_column_info_for_clusters(Tensor selected_cluster_offsets, "
       "Tensor selected_cluster_lengths) -> (Tensor, Tensor, Tensor)");
+  // Ops of this build without a reference counterpart: matching ids as CSR
+  // (ids, row_offsets) instead of a mask.
+  m.def("bloom_mask_to_ids(Tensor packed_mask, int num_docs, bool int64_ids=False) "
+        "-> (Tensor, Tensor)");
+  m.def(
+      "bloom_index_search_batch_ids(Tensor bloom_index, "
+      "Tensor bloom_bundle_b_offsets, Tensor bloom_query_plans_data, "
+      "Tensor bloom_query_plans_offsets, int k, int hash_k, int num_docs, "
+      "bool int64_ids=False) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(st, CUDA, m) {
@@ -306,6 +382,8 @@ TORCH_LIBRARY_IMPL(st, CUDA, m) {
   m.impl("bloom_index_search_batch", TORCH_FN(search_gpu));
   m.impl("parse_expression_query_batch", TORCH_FN(parse_batch));
   m.impl("generate_column_info_for_clusters", TORCH_FN(column_info));
+  m.impl("bloom_mask_to_ids", TORCH_FN(mask_to_ids_gpu));
+  m.impl("bloom_index_search_batch_ids", TORCH_FN(search_ids_gpu));
 }
 
 TORCH_LIBRARY_IMPL(st, CPU, m) {
@@ -313,6 +391,8 @@ TORCH_LIBRARY_IMPL(st, CPU, m) {
   m.impl("bloom_index_search_batch", TORCH_FN(search_cpu_tensors));
   m.impl("parse_expression_query_batch", TORCH_FN(parse_batch));
   m.impl("generate_column_info_for_clusters", TORCH_FN(column_info));
+  m.impl("bloom_mask_to_ids", TORCH_FN(mask_to_ids_cpu));
+  m.impl("bloom_index_search_batch_ids", TORCH_FN(search_ids_cpu));
 }
 
 // Python module entry point: importing silvertorch_amd._C loads this library,

@@ -72,3 +72,20 @@ def search(index, bbo, plans_data, plans_offsets, k: int, hash_k: int, bool_mask
                                              int(bool_mask), out.data_ptr() if out.numel() else None, _stream()))
     torch.cuda.synchronize()
     return out.cpu().numpy()
+
+
+def compact(packed, num_docs: int, int64_ids: bool = False):
+    """C-ABI compaction of a packed mask -> (ids, row_offsets) as numpy arrays."""
+    L = capi.lib()
+    p = packed if isinstance(packed, torch.Tensor) else torch.as_tensor(np.ascontiguousarray(packed, np.int64)).cuda()
+    q, c = p.shape
+    ro = torch.empty(q + 1, dtype=torch.long, device="cuda")
+    ws = torch.empty(max(L.st_bloom_compact_workspace_bytes(q, c), 1), dtype=torch.uint8, device="cuda")
+    capi.check(L.st_bloom_compact_offsets(p.data_ptr() if p.numel() else None, q, c, num_docs,
+                                          ws.data_ptr(), ro.data_ptr(), _stream()))
+    total = int(ro[q].item())
+    ids = torch.empty(total, dtype=torch.long if int64_ids else torch.int32, device="cuda")
+    capi.check(L.st_bloom_compact_ids(p.data_ptr() if p.numel() else None, q, c, num_docs, ws.data_ptr(),
+                                      ids.data_ptr() if total else None, int(int64_ids), _stream()))
+    torch.cuda.synchronize()
+    return ids.cpu().numpy(), ro.cpu().numpy()

@@ -63,6 +63,29 @@ def test_readme_known_answers():
     assert O.unpack_bool(packed).shape == (5, 2048)  # README.md:260
 
 
+def _nonzero_csr(packed, num_docs):
+    """CSR of mask[:, :num_docs].nonzero() with the mask unpacked MSB-first."""
+    q, c = packed.shape
+    bits = np.unpackbits(packed.astype(">i8").view(np.uint8).reshape(q, c * 8), axis=1)
+    rows, cols = np.nonzero(bits[:, :num_docs])
+    ro = np.zeros(q + 1, dtype=np.int64)
+    np.add.at(ro, rows + 1, 1)
+    return cols.astype(np.int64), np.cumsum(ro)
+
+
+def test_compact_matches_numpy_nonzero():
+    rng = np.random.default_rng(21)
+    for q, c in [(0, 0), (3, 0), (0, 5), (4, 33), (7, 64), (5, 1)]:
+        for density in (0.0, 0.03, 0.5, 1.0):
+            packed = np.packbits(rng.random((q, c * 64)) < density, axis=1).view(">i8").astype(np.int64) \
+                if q and c else np.zeros((q, c), dtype=np.int64)
+            for nd in sorted({0, 1, 37, max(c * 64 - 5, 0), c * 64, c * 64 + 100}):
+                ids, ro = O.compact(packed, nd)
+                want_ids, want_ro = _nonzero_csr(packed, nd)
+                np.testing.assert_array_equal(ro, want_ro)
+                np.testing.assert_array_equal(ids, want_ids)
+
+
 def test_parser_oracle_matches_reference_bytes():
     g = G.parser_golden()
     for b in g["batches"]:
