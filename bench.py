@@ -129,6 +129,73 @@ print(json.dumps({{"seconds": (time.perf_counter() - t) / passes, "passes": pass
     }
 
 
+def measure_ids(st, capi, O, bi, bo, pd, po, k, hk, N, Q, packed, steps, warmup):
+    """Matching ids as CSR (bloom_index_search_batch_ids): op step time, the
+    compaction kernels' time from HIP events on the launching stream, and
+    exactness on sampled queries against the oracle's compaction."""
+    import numpy as np
+    import torch
+
+    def step():
+        return st.bloom_index_search_batch_ids(bi, bo, pd, po, k, hk, N)
+
+    for _ in range(max(warmup // 2, 1)):
+        ids, ro = step()
+    torch.cuda.synchronize()
+    n = max(steps // 2, 5)
+    t0 = time.perf_counter()
+    for _ in range(n):
+        ids, ro = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / n
+    matches = int(ro[-1].item())
+    if packed is None:
+        packed = st.bloom_index_search_batch(bi, bo, pd, po, k, hk, False)
+    ro_h = ro.cpu().numpy()
+    ok = bool(np.all(np.diff(ro_h) >= 0))
+    for q in (0, Q // 2, Q - 1):
+        want, _ = O.compact(packed[q:q + 1].cpu().numpy(), N)
+        ok &= bool(np.array_equal(ids[ro_h[q]:ro_h[q + 1]].cpu().numpy(), want))
+    log(f"ids: {matches} matches, {ms:.3f} ms/step, sampled queries exact: {ok}")
+    if not ok:
+        sys.exit("parity failure in sampled compacted ids")
+    # compaction kernels alone, on the packed output
+    L = capi.lib()
+    Qp, C = packed.shape
+    ws = torch.empty(max(L.st_bloom_compact_workspace_bytes(Qp, C), 1), dtype=torch.uint8, device=packed.device)
+    row = torch.empty(Qp + 1, dtype=torch.long, device=packed.device)
+    kids = torch.empty(matches, dtype=torch.int32, device=packed.device)
+    stream = torch.cuda.current_stream()
+    reps = 10
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(reps)]
+    for r in range(reps + 2):
+        e = ev[r - 2] if r >= 2 else None
+        if e:
+            e[0].record(stream)
+        capi.check(L.st_bloom_compact_offsets(packed.data_ptr(), Qp, C, N, ws.data_ptr(), row.data_ptr(),
+                                              stream.cuda_stream))
+        if e:
+            e[1].record(stream)
+        capi.check(L.st_bloom_compact_ids(packed.data_ptr(), Qp, C, N, ws.data_ptr(),
+                                          kids.data_ptr() if matches else None, 0, stream.cuda_stream))
+        if e:
+            e[2].record(stream)
+    torch.cuda.synchronize()
+    count_us = sum(e[0].elapsed_time(e[1]) for e in ev) / reps * 1e3
+    write_us = sum(e[1].elapsed_time(e[2]) for e in ev) / reps * 1e3
+    assert torch.equal(kids, ids) and torch.equal(row, ro)
+    # algorithmic bytes of compaction: the packed mask read once, ids and row offsets written
+    alg = packed.numel() * 8 + 4 * matches + 8 * (Qp + 1)
+    return {
+        "op": "bloom_index_search_batch_ids (int32 ids, CSR)",
+        "ms_per_step": ms, "matches": matches,
+        "doc_queries_per_s": Q * N / (ms * 1e-3),
+        "compact_count_scan_us": count_us, "compact_write_us": write_us,
+        "compact_algorithmic_bytes": alg,
+        "compact_achieved_gbs": alg / ((count_us + write_us) * 1e-6) / 1e9,
+    }
+
+
 def main():
     args = parse_args()
     if args.calibrate_copy:
@@ -145,6 +212,8 @@ def main():
     import silvertorch_amd.ops._load_ops  # noqa: F401
     from silvertorch_amd import capi
     from silvertorch_amd import synthetic as S
+
+    from oracle import oracle as O  # the checker of the sampled parity legs
 
     st = torch.ops.st
     dev = torch.device("cuda:0")
@@ -188,7 +257,6 @@ def main():
     log(f"{args.steps} steps: {ms_per_step:.4f} ms/step")
 
     # Sampled parity: a few bundles against the C oracle (the tests cover the rest).
-    from oracle import oracle as O
 
     packed = out if not args.bool_mask else None
     if packed is not None:
@@ -237,6 +305,9 @@ def main():
             traffic = t.get("hbm_bytes_per_launch")
     log(f"search kernel {kernel_ms * 1e3:.1f} us, {alg_bytes / 1e6:.1f} MB algorithmic, {achieved:.0f} GB/s")
 
+    ids_report = measure_ids(st, capi, O, bi, bo, pd, po, k, hk, N, Q, out if not args.bool_mask else None,
+                             args.steps, args.warmup)
+
     baseline = None
     if not args.no_cpu_baseline:
         baseline = cpu_baseline(bi.cpu().numpy(), bo.cpu().numpy(), queries, k, hk, N, args.cpu_queries)
@@ -274,6 +345,7 @@ def main():
         },
         "cpu_baseline": baseline,
         "build": {"ms": build_s * 1e3, "docs_per_s": N / build_s},
+        "ids": ids_report,
     }
     print(json.dumps(result), flush=True)
 

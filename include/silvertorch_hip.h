@@ -232,6 +232,21 @@ int64_t st_bloom_compact_workspace_bytes(int64_t num_queries, int64_t num_column
 int st_bloom_compact_offsets(const int64_t* packed, int64_t num_queries,
                              int64_t num_columns, int64_t num_docs,
                              void* workspace, int64_t* row_offsets, void* stream);
+/* Search plus step 1 of the compaction in one pass over the index: writes
+ * the packed output int64[num_queries, 32 * num_bundles] to packed_out, the
+ * per-(query, bundle) match counts of docs < num_docs into the workspace
+ * (st_bloom_compact_workspace_bytes(num_queries, 32 * num_bundles) bytes) and
+ * scans them into row_offsets, as st_bloom_compact_offsets would.  Step 3 is
+ * st_bloom_compact_ids on packed_out with the same workspace. */
+int st_bloom_index_search_batch_counts(const int64_t* bloom_index,
+                                       int64_t bloom_index_numel,
+                                       const int64_t* bundle_b_offsets,
+                                       int64_t num_bundles,
+                                       const st_search_plan* plan,
+                                       const void* plan_blob_device,
+                                       int64_t num_docs, int64_t* packed_out,
+                                       void* workspace, int64_t* row_offsets,
+                                       void* stream);
 int st_bloom_compact_ids(const int64_t* packed, int64_t num_queries,
                          int64_t num_columns, int64_t num_docs,
                          const void* workspace, void* ids, int ids_int64,

@@ -39,9 +39,11 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
+# (source, ST_SEARCH_K) pairs: the search kernel is compiled once per K.
 LIB_SOURCES = [
     "st_runtime.hip",
     "bloom_search.hip",
+    *[("bloom_search_k.hip", k) for k in range(1, 11)],
     "bloom_build.hip",
     "bloom_compact.hip",
     "search_plan.cpp",
@@ -59,13 +61,16 @@ def _run(cmd: list[str]) -> None:
         sys.stderr.write(out + "\n")
 
 
-def _compile_lib_object(src: str) -> Path:
-    obj = OBJ / (src + ".o")
+def _compile_lib_object(spec) -> Path:
+    src, k = spec if isinstance(spec, tuple) else (spec, None)
+    obj = OBJ / (src + ("" if k is None else f".k{k}") + ".o")
     path = CSRC / src
     if src.endswith(".cpp"):  # host-only C++
         cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-c"]
     else:
         cmd = [HIPCC, *HIP_FLAGS, "-c"]
+    if k is not None:
+        cmd.append(f"-DST_SEARCH_K={k}")
     cmd += [str(path), "-o", str(obj)]
     _run(cmd)
     return obj
@@ -80,7 +85,7 @@ def _torch_paths() -> tuple[list[str], list[str]]:
     return inc, [libdir]
 
 
-def build_library(jobs: int = 8) -> Path:
+def build_library(jobs: int = os.cpu_count() or 8) -> Path:
     OBJ.mkdir(exist_ok=True)
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile_lib_object, LIB_SOURCES))
@@ -112,7 +117,7 @@ def build_extension() -> Path:
     return EXT
 
 
-def build(jobs: int = 8) -> None:
+def build(jobs: int = os.cpu_count() or 8) -> None:
     build_library(jobs)
     build_extension()
 

@@ -41,6 +41,7 @@ SIGNATURES = {
     "st_bloom_compact_workspace_bytes": (_i64, [_i64, _i64]),
     "st_bloom_compact_offsets": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp]),
     "st_bloom_compact_ids": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, ctypes.c_int, _vp]),
+    "st_bloom_index_search_batch_counts": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
 }
 
 _lib = None

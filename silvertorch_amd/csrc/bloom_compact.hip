@@ -26,6 +26,7 @@
 
 #include "st_common.hpp"
 #include "st_errors.hpp"
+#include "wave_ops.hpp"
 
 namespace st {
 int cu_count();
@@ -34,67 +35,59 @@ namespace {
 
 constexpr int kCompactThreads = 256;            // 4 waves per workgroup
 constexpr int kCompactWaves = kCompactThreads / 64;
-constexpr int kItemsPerWave = 8;                // row loads in flight per wave
+constexpr int kCountItems = 8;   // row loads in flight per wave, count pass
+constexpr int kWriteItems = 8;   // and write pass (register bound)
 constexpr int kChunkWords = kColumnsPerBundle;  // 32 words = 2048 docs
 
 constexpr int kScanThreads = 1024;
 constexpr int kScanPerThread = 8;
 constexpr int kScanTile = kScanThreads * kScanPerThread;
 
-// The lane's 32 doc bits of item `item`, masked to docs < num_docs; bit 31 is
-// the lane's first doc.  *first_doc receives the doc id of bit 31.
+// The lane's 32 doc bits of item (q, ch), masked to docs < num_docs; bit 31
+// is the lane's first doc, whose offset within the chunk is 32 * lane.
 __device__ __forceinline__ uint32_t lane_bits(const uint32_t* __restrict__ packed32,
-                                              int64_t num_columns, int64_t nch,
-                                              int64_t num_docs, int64_t item, int lane,
-                                              int64_t* first_doc) {
-  const int64_t q = item / nch;
-  const int64_t ch = item - q * nch;
+                                              int64_t num_columns, int64_t num_docs,
+                                              int64_t q, int64_t ch, int lane) {
   const int64_t w = ch * kChunkWords + (lane >> 1);  // column within the row
   const int half = lane & 1;                          // 0: docs 0-31 of the word
   const int64_t base = w * kBitsPerColumn + half * 32;
-  *first_doc = base;
   if (w >= num_columns || base >= num_docs) return 0u;
   // Little-endian words: the high half (docs 0-31) is the second u32.
-  uint32_t bits = __builtin_nontemporal_load(packed32 + 2 * (q * num_columns + w) + 1 - half);
-  const int64_t valid = num_docs - base;
-  if (valid < 32) bits &= ~0u << (32 - static_cast<int>(valid));
-  return bits;
+  const uint32_t bits = __builtin_nontemporal_load(packed32 + 2 * (q * num_columns + w) + 1 - half);
+  return bits & valid_doc_mask(base, num_docs);
 }
 
-__device__ __forceinline__ int64_t wave_sum(int64_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
-__device__ __forceinline__ uint32_t wave_exclusive_prefix(uint32_t v, int lane) {
-  uint32_t x = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
+// Items first .. first+kItemsPerWave-1 as (query, chunk) pairs: one division
+// per group, then increments.
+struct ItemCursor {
+  int64_t q, ch;
+  __device__ ItemCursor(int64_t first, int64_t nch) : q(first / nch), ch(first - (first / nch) * nch) {}
+  __device__ void next(int64_t nch) {
+    if (++ch == nch) {
+      ch = 0;
+      ++q;
+    }
   }
-  return x - v;
-}
+};
 
 __global__ __launch_bounds__(kCompactThreads) void compact_count_kernel(
     const uint32_t* __restrict__ packed32, int64_t num_columns, int64_t nch,
     int64_t num_docs, int64_t n_items, int64_t* __restrict__ counts) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * kCompactWaves + (threadIdx.x >> 6);
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCompactWaves * kItemsPerWave;
-  for (int64_t first = wave * kItemsPerWave; first < n_items; first += stride) {
-    uint32_t bits[kItemsPerWave];
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCompactWaves * kCountItems;
+  for (int64_t first = wave * kCountItems; first < n_items; first += stride) {
+    uint32_t bits[kCountItems];
+    ItemCursor it(first, nch);
 #pragma unroll
-    for (int u = 0; u < kItemsPerWave; ++u) {
-      int64_t doc;
-      bits[u] = first + u < n_items
-                    ? lane_bits(packed32, num_columns, nch, num_docs, first + u, lane, &doc)
-                    : 0u;
+    for (int u = 0; u < kCountItems; ++u) {
+      bits[u] = first + u < n_items ? lane_bits(packed32, num_columns, num_docs, it.q, it.ch, lane)
+                                    : 0u;
+      it.next(nch);
     }
 #pragma unroll
-    for (int u = 0; u < kItemsPerWave; ++u) {
-      const int64_t c = wave_sum(__builtin_popcount(bits[u]));
+    for (int u = 0; u < kCountItems; ++u) {
+      const uint32_t c = wave_total_small(static_cast<uint32_t>(__builtin_popcount(bits[u])));
       if (lane == 0 && first + u < n_items) counts[first + u] = c;
     }
   }
@@ -183,14 +176,19 @@ __global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(
   }
   int64_t total;
   int64_t run = tile_offsets[blockIdx.x] + block_exclusive_scan(s, &total);
+  int64_t q = start / nch, r = start - (start / nch) * nch;
 #pragma unroll
   for (int j = 0; j < kScanPerThread; ++j) {
     const int64_t i = start + j;
     if (i < n) {
       data[i] = run;
-      if (i % nch == 0) row_offsets[i / nch] = run;
+      if (r == 0) row_offsets[q] = run;
     }
     run += v[j];
+    if (++r == nch) {
+      r = 0;
+      ++q;
+    }
   }
 }
 
@@ -199,43 +197,72 @@ __global__ void zero_offsets_kernel(int64_t* __restrict__ row_offsets, int64_t n
   if (i < n) row_offsets[i] = 0;
 }
 
+// Each wave stages an item's ids in LDS as 16-bit offsets within the chunk
+// (lane order is doc order, so the wave prefix of lane popcounts places
+// them), then copies the run out with coalesced stores.
 template <typename Id>
 __global__ __launch_bounds__(kCompactThreads) void compact_write_kernel(
     const uint32_t* __restrict__ packed32, int64_t num_columns, int64_t nch,
     int64_t num_docs, int64_t n_items, const int64_t* __restrict__ item_base,
     Id* __restrict__ ids) {
+  __shared__ uint16_t stage[kCompactWaves][kDocsPerBundle];
   const int lane = threadIdx.x & 63;
+  uint16_t* my = stage[threadIdx.x >> 6];
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * kCompactWaves + (threadIdx.x >> 6);
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCompactWaves * kItemsPerWave;
-  for (int64_t first = wave * kItemsPerWave; first < n_items; first += stride) {
-    uint32_t bits[kItemsPerWave];
-    int64_t doc0[kItemsPerWave];
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCompactWaves * kWriteItems;
+  for (int64_t first = wave * kWriteItems; first < n_items; first += stride) {
+    uint32_t bits[kWriteItems];
+    int64_t pos[kWriteItems];
+    ItemCursor it(first, nch);
+    const int64_t ch0 = it.ch;
 #pragma unroll
-    for (int u = 0; u < kItemsPerWave; ++u) {
-      bits[u] = first + u < n_items
-                    ? lane_bits(packed32, num_columns, nch, num_docs, first + u, lane, &doc0[u])
-                    : 0u;
+    for (int u = 0; u < kWriteItems; ++u) {
+      const bool valid = first + u < n_items;
+      bits[u] = valid ? lane_bits(packed32, num_columns, num_docs, it.q, it.ch, lane) : 0u;
+      pos[u] = valid ? item_base[first + u] : 0;
+      it.next(nch);
     }
+    int64_t ch = ch0;
 #pragma unroll
-    for (int u = 0; u < kItemsPerWave; ++u) {
+    for (int u = 0; u < kWriteItems; ++u) {
       if (first + u >= n_items) break;  // wave-uniform
       uint32_t b = bits[u];
-      int64_t pos = item_base[first + u] +
-                    wave_exclusive_prefix(static_cast<uint32_t>(__builtin_popcount(b)), lane);
+      const WaveScan ws = wave_scan_small(static_cast<uint32_t>(__builtin_popcount(b)));
+      const uint32_t total = ws.total;
+      uint32_t slot = ws.excl;
+      const uint32_t lane_doc = static_cast<uint32_t>(lane) * 32u;
       while (b != 0u) {
         const int lz = __builtin_clz(b);
-        ids[pos++] = static_cast<Id>(doc0[u] + lz);
+        my[slot++] = static_cast<uint16_t>(lane_doc + lz);
         b &= ~(0x80000000u >> lz);
       }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int64_t doc0 = ch * kDocsPerBundle;
+      Id* dst = ids + pos[u];
+      for (uint32_t i = lane; i < total; i += 64) dst[i] = static_cast<Id>(doc0 + my[i]);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (++ch == nch) ch = 0;
     }
   }
 }
 
-int compact_grid(int64_t n_items) {
-  const int64_t per_block = static_cast<int64_t>(kCompactWaves) * kItemsPerWave;
+// As many workgroups as are resident at once (no tail of late workgroups),
+// fewer when there are not enough items.
+template <typename Kernel>
+int compact_grid(Kernel kernel, int64_t n_items, int items_per_wave) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kCompactThreads, 0) !=
+          hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const int64_t per_block = static_cast<int64_t>(kCompactWaves) * items_per_wave;
   const int64_t want = (n_items + per_block - 1) / per_block;
   return static_cast<int>(std::max<int64_t>(
-      1, std::min<int64_t>(want, static_cast<int64_t>(cu_count()) * 8)));
+      1, std::min<int64_t>(want, static_cast<int64_t>(cu_count()) * per_cu)));
 }
 
 int64_t num_chunks(int64_t num_columns) {
@@ -256,6 +283,31 @@ void check_shape(int64_t num_queries, int64_t num_columns, int64_t num_docs) {
 }
 
 }  // namespace
+
+// Turns the per-(query, chunk) match counts at the start of a compaction
+// workspace into output positions, in place, and fills row_offsets.
+void compact_scan_counts(int64_t* counts, int64_t num_queries, int64_t nch,
+                         int64_t* row_offsets, hipStream_t s) {
+  const int64_t items = num_queries * nch;
+  const int64_t tiles = (items + kScanTile - 1) / kScanTile;
+  int64_t* tile_sums = counts + items;
+  hipLaunchKernelGGL(scan_reduce_kernel, dim3(static_cast<unsigned>(tiles)),
+                     dim3(kScanThreads), 0, s, counts, items, tile_sums);
+  check_launch("scan_reduce_kernel");
+  hipLaunchKernelGGL(scan_tiles_kernel, dim3(1), dim3(kScanThreads), 0, s, tile_sums, tiles,
+                     row_offsets, num_queries);
+  check_launch("scan_tiles_kernel");
+  hipLaunchKernelGGL(scan_apply_kernel, dim3(static_cast<unsigned>(tiles)),
+                     dim3(kScanThreads), 0, s, counts, items, tile_sums, nch, row_offsets);
+  check_launch("scan_apply_kernel");
+}
+
+void compact_zero_offsets(int64_t* row_offsets, int64_t n, hipStream_t s) {
+  hipLaunchKernelGGL(zero_offsets_kernel, dim3(static_cast<unsigned>((n + 255) / 256)),
+                     dim3(256), 0, s, row_offsets, n);
+  check_launch("zero_offsets_kernel");
+}
+
 }  // namespace st
 
 extern "C" int64_t st_bloom_compact_workspace_bytes(int64_t num_queries, int64_t num_columns) {
@@ -276,29 +328,18 @@ extern "C" int st_bloom_compact_offsets(const int64_t* packed, int64_t num_queri
     const int64_t nch = num_chunks(num_columns);
     const int64_t items = num_queries * nch;
     if (items == 0) {
-      const int64_t n = num_queries + 1;
-      hipLaunchKernelGGL(zero_offsets_kernel, dim3(static_cast<unsigned>((n + 255) / 256)),
-                         dim3(256), 0, s, row_offsets, n);
-      check_launch("zero_offsets_kernel");
+      compact_zero_offsets(row_offsets, num_queries + 1, s);
       return;
     }
     ST_CHECK(packed != nullptr && workspace != nullptr, "null device pointer");
     int64_t* counts = static_cast<int64_t*>(workspace);
-    const int64_t tiles = (items + kScanTile - 1) / kScanTile;
-    int64_t* tile_sums = counts + items;
     const uint32_t* p32 = reinterpret_cast<const uint32_t*>(packed);
-    hipLaunchKernelGGL(compact_count_kernel, dim3(compact_grid(items)), dim3(kCompactThreads),
-                       0, s, p32, num_columns, nch, num_docs, items, counts);
+    hipLaunchKernelGGL(compact_count_kernel,
+                       dim3(compact_grid(compact_count_kernel, items, kCountItems)),
+                       dim3(kCompactThreads), 0, s, p32, num_columns, nch, num_docs, items,
+                       counts);
     check_launch("compact_count_kernel");
-    hipLaunchKernelGGL(scan_reduce_kernel, dim3(static_cast<unsigned>(tiles)),
-                       dim3(kScanThreads), 0, s, counts, items, tile_sums);
-    check_launch("scan_reduce_kernel");
-    hipLaunchKernelGGL(scan_tiles_kernel, dim3(1), dim3(kScanThreads), 0, s, tile_sums, tiles,
-                       row_offsets, num_queries);
-    check_launch("scan_tiles_kernel");
-    hipLaunchKernelGGL(scan_apply_kernel, dim3(static_cast<unsigned>(tiles)),
-                       dim3(kScanThreads), 0, s, counts, items, tile_sums, nch, row_offsets);
-    check_launch("scan_apply_kernel");
+    compact_scan_counts(counts, num_queries, nch, row_offsets, s);
   });
 }
 
@@ -319,11 +360,13 @@ extern "C" int st_bloom_compact_ids(const int64_t* packed, int64_t num_queries,
     const uint32_t* p32 = reinterpret_cast<const uint32_t*>(packed);
     const int64_t* base = static_cast<const int64_t*>(workspace);
     if (ids_int64) {
-      hipLaunchKernelGGL(compact_write_kernel<int64_t>, dim3(compact_grid(items)),
+      hipLaunchKernelGGL(compact_write_kernel<int64_t>,
+                         dim3(compact_grid(compact_write_kernel<int64_t>, items, kWriteItems)),
                          dim3(kCompactThreads), 0, s, p32, num_columns, nch, num_docs, items,
                          base, static_cast<int64_t*>(ids));
     } else {
-      hipLaunchKernelGGL(compact_write_kernel<int32_t>, dim3(compact_grid(items)),
+      hipLaunchKernelGGL(compact_write_kernel<int32_t>,
+                         dim3(compact_grid(compact_write_kernel<int32_t>, items, kWriteItems)),
                          dim3(kCompactThreads), 0, s, p32, num_columns, nch, num_docs, items,
                          base, static_cast<int32_t*>(ids));
     }

@@ -1,0 +1,769 @@
+// Batched boolean search over the bundled bloom index, for gfx950: device
+// code and the kernel template.  Each K is instantiated in its own
+// translation unit (bloom_search_k.hip); the host side is bloom_search.hip.
+//
+// Replaces process_documents / bloom_index_search_common
+// (bloom_index_search_cuda.cu:575-615, :940-1029) and the CPU loop
+// bloom_index_search_common_cpu (bloom_index_search.cpp:173-243).
+//
+// Layout (unchanged from the reference, bloom_indexer.cpp:72-110): bundle i
+// owns rows [off[i], off[i+1]) of 32 int64 words; word (row, c) holds the
+// bloom bit `row` of the 64 docs of column c, doc 64c+j at bit 63-j.
+//
+// Work decomposition: one 1024-thread workgroup per CU walks bundles
+// blockIdx.x, blockIdx.x + gridDim.x, ...  For each bundle it
+//   1. moves the bundle's rows (prefetched into registers while the previous
+//      bundle was evaluated) into LDS, so the index is read from HBM once per
+//      query batch;
+//   2. resolves every distinct batch term to its k row positions for this
+//      bundle's width b -- once per bundle instead of once per (query,
+//      column) -- skipping the step when b equals the previous bundle's;
+//   3. has each wave run its queries' accumulator programs: lane l owns the
+//      32-bit half (l & 1) of column l >> 1, so one wave covers the 32
+//      columns of the bundle for one query and all control flow is
+//      wave-uniform.
+// Bundles wider than the LDS tile are evaluated from global memory with the
+// same programs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+
+#include "search_plan.hpp"
+#include "st_common.hpp"
+#include "st_errors.hpp"
+#include "wave_ops.hpp"
+
+namespace st {
+namespace {
+
+// Native 4 x u32 vector (usable with the nontemporal builtins).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// The plan arrays and bundle offsets are read-only for the kernel's lifetime.
+// Reading them through the constant address space lets every uniform read
+// become a scalar load: a vector load there would share the in-order vmcnt
+// counter with the next bundle's tile prefetch, and waiting for it would wait
+// for the whole prefetch.
+#define ST_CONST __attribute__((address_space(4)))
+template <typename T>
+__device__ __forceinline__ const ST_CONST T* as_const(const T* p) {
+  return (const ST_CONST T*)(p);  // addrspacecast: only a C-style cast spells it
+}
+
+constexpr int kPrefetch = kSearchTileRows * 16 / kSearchThreads;  // uint4/thread
+static_assert(kPrefetch * kSearchThreads == kSearchTileRows * 16, "tile split");
+
+struct SearchArgs {
+  const int64_t* index;
+  int64_t index_numel;
+  const ST_CONST int64_t* bundle_offsets;
+  int64_t num_bundles;
+  const ST_CONST uint32_t* wave_off;
+  const ST_CONST uint32_t* insn_start;
+  const ST_CONST uint32_t* insns;
+  const ST_CONST uint64_t* hashes;
+  const ST_CONST uint32_t* bundle_slot;   // nullptr when the plan is not width-bound
+  const ST_CONST uint32_t* bundle_order;  // visiting order (nullptr: index order)
+  const ST_CONST uint32_t* bound_start;
+  const ST_CONST uint32_t* bound;
+  uint32_t bound_words;
+  uint32_t num_terms;
+  int32_t hash_k;
+  int64_t out_cols;  // columns per output row = num_bundles * 32
+  void* out;
+  int64_t* counts;   // kOutCounts: matches per (query row, bundle)
+  int64_t num_docs;  // kOutCounts: docs at or past it are not counted
+};
+
+// Output modes of the search kernel.
+constexpr int kOutPacked = 0;  // int64 words
+constexpr int kOutBool = 1;    // one byte per doc
+constexpr int kOutCounts = 2;  // int64 words, plus per-(row, bundle) match counts
+
+__device__ __forceinline__ uint32_t uniform(uint32_t v) {
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+// Width and first row of bundle `bnd`; a negative width (malformed offsets)
+// reads as an empty bundle.
+__device__ __forceinline__ void bundle_extent(const SearchArgs& a, int64_t bnd,
+                                              int64_t& start, int64_t& b) {
+  start = a.bundle_offsets[bnd];
+  b = a.bundle_offsets[bnd + 1] - start;
+  if (b < 0) b = 0;
+}
+
+__device__ __forceinline__ void prefetch_tile(const SearchArgs& a, int64_t bnd,
+                                              u32x4 (&pre)[kPrefetch]) {
+  int64_t start, b;
+  bundle_extent(a, bnd, start, b);
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < kPrefetch; ++i) pre[i] = u32x4{0, 0, 0, 0};
+  if (b > kSearchTileRows) return;
+  const int64_t chunks = b * 16;
+  const u32x4* src = reinterpret_cast<const u32x4*>(a.index + start * 32);
+#pragma unroll
+  for (int i = 0; i < kPrefetch; ++i) {
+    const int c = tid + i * kSearchThreads;
+    // chunk c holds words start*32 + 2c and + 2c + 1
+    if (c < chunks && start * 32 + 2 * c + 1 < a.index_numel) {
+      pre[i] = __builtin_nontemporal_load(src + c);
+    }
+  }
+}
+
+// Resolves term u's positions for width b, as signature_match does
+// (bloom_index_search.cpp:40-61): over hashes p < hash_k, while fewer than K
+// are resolved, b_p = (int16)(h[p] % b); repeats of an earlier b_p are
+// skipped.  Unused slots repeat slot 0 (AND is idempotent).
+template <int K>
+__device__ __forceinline__ int resolve_positions(const ST_CONST uint64_t* h, int hash_k,
+                                                 const FastMod64& fm,
+                                                 int16_t (&found)[K]) {
+  int cnt = 0;
+  for (int p = 0; p < hash_k && cnt < K; ++p) {
+    const int16_t bp = static_cast<int16_t>(fast_mod(h[p], fm));
+    bool dup = false;
+#pragma unroll
+    for (int j = 0; j < K; ++j) dup |= (j < cnt) && (found[j] == bp);
+    if (!dup) {
+#pragma unroll
+      for (int j = 0; j < K; ++j)
+        if (j == cnt) found[j] = bp;
+      ++cnt;
+    }
+  }
+  return cnt;
+}
+
+// Expands a 32-bit match half into 32 bool bytes, most significant bit
+// first (the doc order of bloom_index_search.cpp:231-236).
+__device__ __forceinline__ void store_bool32(uint8_t* dst, uint32_t bits) {
+  const uint32_t y = __builtin_bitreverse32(bits);
+  uint32_t w[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) w[j] = (((y >> (4 * j)) & 0xFu) * 0x00204081u) & 0x01010101u;
+  u32x4* d = reinterpret_cast<u32x4*>(dst);
+  __builtin_nontemporal_store(u32x4{w[0], w[1], w[2], w[3]}, d);
+  __builtin_nontemporal_store(u32x4{w[4], w[5], w[6], w[7]}, d + 1);
+}
+
+// Executes one non-TERM operation on the accumulator machine.
+__device__ __forceinline__ void exec_op(uint32_t op, uint32_t& acc,
+                                        uint32_t (&stk)[kSearchMaxStack],
+                                        uint32_t& sp) {
+  const uint32_t code = op & 7u;
+  uint32_t v;
+  if (code == kInsConst) {
+    v = ~0u;
+  } else if (code == kInsPush) {
+    stk[sp++] = acc;
+    return;
+  } else if (code == kInsPop) {
+    v = acc;
+    acc = stk[--sp];
+  } else {  // kInsNot
+    acc = ~acc;
+    return;
+  }
+  if (op & 32u) v = ~v;
+  const uint32_t mode = (op >> 3) & 3u;
+  acc = mode == kModeSet ? v : (mode == kModeAnd ? (acc & v) : (acc | v));
+}
+
+__device__ __forceinline__ uint32_t combine(uint32_t op, uint32_t acc, uint32_t v) {
+  if (op & 32u) v = ~v;
+  const uint32_t mode = (op >> 3) & 3u;
+  return mode == kModeSet ? v : (mode == kModeAnd ? (acc & v) : (acc | v));
+}
+
+// Where the rows of the current bundle are read from.
+struct RowSource {
+  const uint32_t* pos;    // LDS position lists
+  const char* tile_lane;  // LDS tile + this lane's byte offset
+  const uint32_t* index32;
+  int64_t index_numel;
+  int64_t start;          // first row of the bundle
+  int lane;
+  bool staged;            // rows in the LDS tile (else global memory)
+};
+
+// Position list of the term whose list starts at byte `off` of the LDS
+// position area.
+template <int KP>
+__device__ __forceinline__ void load_positions(const RowSource& rs, uint32_t off,
+                                               uint32_t (&p)[KP]) {
+  const uint32_t* pp = reinterpret_cast<const uint32_t*>(
+      reinterpret_cast<const char*>(rs.pos) + off);
+#pragma unroll
+  for (int r = 0; r < KP; r += 4) {
+    const u32x4 q4 = *reinterpret_cast<const u32x4*>(pp + r);
+    p[r] = q4.x;
+    p[r + 1] = q4.y;
+    p[r + 2] = q4.z;
+    p[r + 3] = q4.w;
+  }
+}
+
+// Word of one term for this lane's 32-bit half column: AND of its K rows.
+// STAGED selects the LDS tile or global memory at compile time, so the row
+// reads of several terms form one straight-line block.
+template <int K, int KP, bool STAGED>
+__device__ __forceinline__ uint32_t term_word(const RowSource& rs, const uint32_t (&p)[KP]) {
+  uint32_t v = ~0u;
+  if constexpr (STAGED) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) v &= *reinterpret_cast<const uint32_t*>(rs.tile_lane + p[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const int32_t r = static_cast<int32_t>(p[j]);
+      uint32_t word = 0;
+      if (r != kPosZeros) {
+        const int64_t row = rs.start + r;
+        if (row >= 0 && (row * 32 + (rs.lane >> 1)) < rs.index_numel)
+          word = rs.index32[row * 64 + rs.lane];
+      }
+      v &= word;
+    }
+  }
+  return v;
+}
+
+// Flat-form query with exactly T literals: every position list, then every
+// row word, then the branch-free OR-of-ANDs fold.
+template <int K, int KP, bool STAGED, int T>
+__device__ __forceinline__ uint32_t eval_flat_fixed(const RowSource& rs, const ST_CONST u32x4* lit) {
+  uint32_t p[T > 0 ? T : 1][KP];
+#pragma unroll
+  for (int j = 0; j < T; ++j) load_positions<KP>(rs, lit[j].x, p[j]);
+  uint32_t w[T > 0 ? T : 1];
+#pragma unroll
+  for (int j = 0; j < T; ++j) w[j] = term_word<K, KP, STAGED>(rs, p[j]);
+  uint32_t res = 0, acc = 0;
+#pragma unroll
+  for (int j = 0; j < T; ++j) {
+    const u32x4 L = lit[j];
+    res |= acc & L.z;
+    acc = (acc | L.z) & (w[j] ^ L.y);
+  }
+  return res | acc;
+}
+
+// Flat-form query of any length, in groups of G literals.
+template <int K, int KP, bool STAGED, int G>
+__device__ __forceinline__ uint32_t eval_flat_loop(const RowSource& rs, const ST_CONST u32x4* lit,
+                                                   uint32_t T) {
+  uint32_t res = 0, acc = 0;
+  for (uint32_t base = 0; base < T; base += G) {
+    const uint32_t n = min(static_cast<uint32_t>(G), T - base);
+    uint32_t p[G][KP];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (j < n) load_positions<KP>(rs, lit[base + j].x, p[j]);
+    uint32_t w[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (j < n) w[j] = term_word<K, KP, STAGED>(rs, p[j]);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if (j < n) {
+        const u32x4 L = lit[base + j];
+        res |= acc & L.z;
+        acc = (acc | L.z) & (w[j] ^ L.y);
+      }
+    }
+  }
+  return res | acc;
+}
+
+// Flat query dispatch: fully unrolled blocks for short queries (T * KP
+// position registers bounded), the grouped loop otherwise.
+template <int K, int KP, bool STAGED, int G, int T>
+__device__ __forceinline__ uint32_t eval_flat_t(const RowSource& rs, const ST_CONST u32x4* lit, uint32_t n) {
+  if constexpr (T * KP <= 24) {
+    return eval_flat_fixed<K, KP, STAGED, T>(rs, lit);
+  } else {
+    return eval_flat_loop<K, KP, STAGED, G>(rs, lit, n);
+  }
+}
+
+template <int K, int KP, bool STAGED, int G>
+__device__ __forceinline__ uint32_t eval_flat(const RowSource& rs, const ST_CONST u32x4* lit, uint32_t T) {
+  switch (T) {
+    case 0: return 0;
+    case 1: return eval_flat_t<K, KP, STAGED, G, 1>(rs, lit, T);
+    case 2: return eval_flat_t<K, KP, STAGED, G, 2>(rs, lit, T);
+    case 3: return eval_flat_t<K, KP, STAGED, G, 3>(rs, lit, T);
+    case 4: return eval_flat_t<K, KP, STAGED, G, 4>(rs, lit, T);
+    case 5: return eval_flat_t<K, KP, STAGED, G, 5>(rs, lit, T);
+    case 6: return eval_flat_t<K, KP, STAGED, G, 6>(rs, lit, T);
+    default: return eval_flat_loop<K, KP, STAGED, G>(rs, lit, T);
+  }
+}
+
+// Stack-form query: term words in groups of G, operations walked in order.
+template <int K, int KP, bool STAGED, int G>
+__device__ __forceinline__ uint32_t eval_stack(const RowSource& rs, const ST_CONST uint32_t* prog,
+                                               uint32_t T, uint32_t nops) {
+  const ST_CONST uint32_t* tref = prog + kProgHeaderWords;
+  const ST_CONST uint32_t* ops = tref + T;
+  uint32_t acc = 0;
+  uint32_t stk[kSearchMaxStack];
+  uint32_t sp = 0;
+  uint32_t i = 0;
+  for (uint32_t base = 0; base < T; base += G) {
+    const uint32_t n = min(static_cast<uint32_t>(G), T - base);
+    uint32_t p[G][KP];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (j < n) load_positions<KP>(rs, tref[base + j], p[j]);
+    uint32_t w[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (j < n) w[j] = term_word<K, KP, STAGED>(rs, p[j]);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if (j < n) {
+        for (;;) {
+          const uint32_t op = ops[i++];
+          if ((op & 7u) == kInsTerm) {
+            acc = combine(op, acc, w[j]);
+            break;
+          }
+          exec_op(op, acc, stk, sp);
+        }
+      }
+    }
+  }
+  for (; i < nops; ++i) exec_op(ops[i], acc, stk, sp);
+  return acc;
+}
+
+// FastMod64 for a divisor below 2^32 with 32-bit divides only:
+// (2^64-1)/d = ((2^32-1)/d) * 2^32 + (((2^32-1) % d) * 2^32 + 2^32-1) / d.
+__device__ __forceinline__ FastMod64 make_fastmod_dev(uint64_t d) {
+  if (d == 0 || (d >> 32)) return make_fastmod(d);
+  const uint32_t d32 = static_cast<uint32_t>(d);
+  const uint32_t qh = 0xFFFFFFFFu / d32;
+  const uint32_t rh = 0xFFFFFFFFu % d32;
+  const uint64_t n = (static_cast<uint64_t>(rh) << 32) | 0xFFFFFFFFull;  // < d * 2^32
+  uint64_t ql = static_cast<uint64_t>(static_cast<double>(n) / static_cast<double>(d32));
+  // the double quotient is within one of the true one; fix it exactly
+  while (ql * d32 > n) --ql;
+  while (n - ql * d32 >= d32) ++ql;
+  FastMod64 f;
+  f.d = d;
+  f.magic = (static_cast<uint64_t>(qh) << 32) + ql;
+  return f;
+}
+
+// ----------------------------------------------------- width-bound programs
+
+// This lane's 32-bit half of row position p of the current bundle.
+template <bool STAGED>
+__device__ __forceinline__ uint32_t row_word(const RowSource& rs, uint32_t p) {
+  if constexpr (STAGED) {
+    return *reinterpret_cast<const uint32_t*>(rs.tile_lane + p);
+  } else {
+    const int32_t r = static_cast<int32_t>(p);
+    if (r == kPosZeros) return 0;
+    if (r == kPosOnes) return ~0u;
+    const int64_t row = rs.start + r;
+    if (row < 0 || (row * 32 + (rs.lane >> 1)) >= rs.index_numel) return 0;
+    return rs.index32[row * 64 + rs.lane];
+  }
+}
+
+template <int K, bool STAGED>
+__device__ __forceinline__ uint32_t bound_term_word(const RowSource& rs, const ST_CONST uint32_t* rec) {
+  uint32_t v = ~0u;
+#pragma unroll
+  for (int q = 0; q < K; ++q) v &= row_word<STAGED>(rs, rec[q]);
+  return v;
+}
+
+// Bound flat query with exactly T literals: all row reads of the query are
+// issued before the OR-of-ANDs fold.
+template <int K, bool STAGED, int T>
+__device__ __forceinline__ uint32_t eval_bound_flat_fixed(const RowSource& rs, const ST_CONST uint32_t* recs) {
+  constexpr int RW = ((K + 1 + 3) / 4) * 4;
+  uint32_t w[T > 0 ? T : 1];
+#pragma unroll
+  for (int j = 0; j < T; ++j) w[j] = bound_term_word<K, STAGED>(rs, recs + j * RW);
+  uint32_t res = 0, acc = 0;
+#pragma unroll
+  for (int j = 0; j < T; ++j) {
+    const uint32_t f = recs[j * RW + K];
+    const uint32_t neg = 0u - (f & 1u);
+    const uint32_t grp = 0u - ((f >> 1) & 1u);
+    res |= acc & grp;
+    acc = (acc | grp) & (w[j] ^ neg);
+  }
+  return res | acc;
+}
+
+// Two bound flat queries with the same literal count T, evaluated together
+// so that both queries' row reads are in flight at once.
+template <int K, bool STAGED, int T>
+__device__ __forceinline__ void eval_bound_pair_fixed(const RowSource& rs, const ST_CONST uint32_t* ra,
+                                                      const ST_CONST uint32_t* rb, uint32_t& out_a,
+                                                      uint32_t& out_b) {
+  constexpr int RW = ((K + 1 + 3) / 4) * 4;
+  uint32_t wa[T], wb[T];
+#pragma unroll
+  for (int j = 0; j < T; ++j) {
+    wa[j] = bound_term_word<K, STAGED>(rs, ra + j * RW);
+    wb[j] = bound_term_word<K, STAGED>(rs, rb + j * RW);
+  }
+  uint32_t res_a = 0, acc_a = 0, res_b = 0, acc_b = 0;
+#pragma unroll
+  for (int j = 0; j < T; ++j) {
+    const uint32_t fa = ra[j * RW + K], fb = rb[j * RW + K];
+    const uint32_t neg_a = 0u - (fa & 1u), grp_a = 0u - ((fa >> 1) & 1u);
+    const uint32_t neg_b = 0u - (fb & 1u), grp_b = 0u - ((fb >> 1) & 1u);
+    res_a |= acc_a & grp_a;
+    acc_a = (acc_a | grp_a) & (wa[j] ^ neg_a);
+    res_b |= acc_b & grp_b;
+    acc_b = (acc_b | grp_b) & (wb[j] ^ neg_b);
+  }
+  out_a = res_a | acc_a;
+  out_b = res_b | acc_b;
+}
+
+// Pair dispatch on the shared literal count; false when T is beyond the
+// unrolled range (the caller then evaluates the two queries one by one).
+template <int K, bool STAGED>
+__device__ __forceinline__ bool eval_bound_pair(const RowSource& rs, const ST_CONST uint32_t* ra,
+                                                const ST_CONST uint32_t* rb, uint32_t T, uint32_t& out_a,
+                                                uint32_t& out_b) {
+  switch (T) {
+    case 0: out_a = 0; out_b = 0; return true;
+    case 1: eval_bound_pair_fixed<K, STAGED, 1>(rs, ra, rb, out_a, out_b); return true;
+    case 2: eval_bound_pair_fixed<K, STAGED, 2>(rs, ra, rb, out_a, out_b); return true;
+    case 3: eval_bound_pair_fixed<K, STAGED, 3>(rs, ra, rb, out_a, out_b); return true;
+    case 4: eval_bound_pair_fixed<K, STAGED, 4>(rs, ra, rb, out_a, out_b); return true;
+    case 5: eval_bound_pair_fixed<K, STAGED, 5>(rs, ra, rb, out_a, out_b); return true;
+    case 6: eval_bound_pair_fixed<K, STAGED, 6>(rs, ra, rb, out_a, out_b); return true;
+    default: return false;
+  }
+}
+
+template <int K, bool STAGED, int G>
+__device__ __forceinline__ uint32_t eval_bound_flat_loop(const RowSource& rs, const ST_CONST uint32_t* recs,
+                                                         uint32_t T) {
+  constexpr int RW = ((K + 1 + 3) / 4) * 4;
+  uint32_t res = 0, acc = 0;
+  for (uint32_t base = 0; base < T; base += G) {
+    const uint32_t n = min(static_cast<uint32_t>(G), T - base);
+    const ST_CONST uint32_t* r0 = recs + base * RW;
+    uint32_t w[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (j < n) w[j] = bound_term_word<K, STAGED>(rs, r0 + j * RW);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if (j < n) {
+        const uint32_t f = r0[j * RW + K];
+        const uint32_t neg = 0u - (f & 1u);
+        const uint32_t grp = 0u - ((f >> 1) & 1u);
+        res |= acc & grp;
+        acc = (acc | grp) & (w[j] ^ neg);
+      }
+    }
+  }
+  return res | acc;
+}
+
+template <int K, bool STAGED, int G>
+__device__ __forceinline__ uint32_t eval_bound_flat(const RowSource& rs, const ST_CONST uint32_t* recs,
+                                                    uint32_t T) {
+  switch (T) {
+    case 0: return 0;
+    case 1: return eval_bound_flat_fixed<K, STAGED, 1>(rs, recs);
+    case 2: return eval_bound_flat_fixed<K, STAGED, 2>(rs, recs);
+    case 3: return eval_bound_flat_fixed<K, STAGED, 3>(rs, recs);
+    case 4: return eval_bound_flat_fixed<K, STAGED, 4>(rs, recs);
+    case 5: return eval_bound_flat_fixed<K, STAGED, 5>(rs, recs);
+    case 6: return eval_bound_flat_fixed<K, STAGED, 6>(rs, recs);
+    case 7: return eval_bound_flat_fixed<K, STAGED, 7>(rs, recs);
+    case 8: return eval_bound_flat_fixed<K, STAGED, 8>(rs, recs);
+    default: return eval_bound_flat_loop<K, STAGED, G>(rs, recs, T);
+  }
+}
+
+// Bound stack query: term position lists of KP words, then the operations.
+template <int K, int KP, bool STAGED, int G>
+__device__ __forceinline__ uint32_t eval_bound_stack(const RowSource& rs, const ST_CONST uint32_t* prog,
+                                                     uint32_t T, uint32_t nops) {
+  const ST_CONST uint32_t* tpos = prog + kProgHeaderWords;
+  const ST_CONST uint32_t* ops = tpos + T * KP;
+  uint32_t acc = 0;
+  uint32_t stk[kSearchMaxStack];
+  uint32_t sp = 0;
+  uint32_t i = 0;
+  for (uint32_t base = 0; base < T; base += G) {
+    const uint32_t n = min(static_cast<uint32_t>(G), T - base);
+    uint32_t w[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (j < n) w[j] = bound_term_word<K, STAGED>(rs, tpos + (base + j) * KP);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if (j < n) {
+        for (;;) {
+          const uint32_t op = ops[i++];
+          if ((op & 7u) == kInsTerm) {
+            acc = combine(op, acc, w[j]);
+            break;
+          }
+          exec_op(op, acc, stk, sp);
+        }
+      }
+    }
+  }
+  for (; i < nops; ++i) exec_op(ops[i], acc, stk, sp);
+  return acc;
+}
+
+// Evaluates this wave's queries [s_begin, s_end) on one bundle and stores
+// their 32-bit halves of the bundle's 32 output words.
+template <int K, int KP, bool STAGED, bool BOUND, int G, int kOut>
+__device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSource& rs,
+                                             uint32_t s_begin, uint32_t s_end,
+                                             int64_t bundle, uint32_t slot) {
+  const int lane = rs.lane;
+  uint32_t count_mask = 0u;
+  if constexpr (kOut == kOutCounts) {
+    // The lane's u32 is half (lane & 1) of little-endian word lane >> 1: odd
+    // lanes hold the word's high half (docs 0-31), even lanes docs 32-63.
+    const int64_t first_doc =
+        bundle * kDocsPerBundle + (lane >> 1) * kBitsPerColumn + ((lane & 1) ? 0 : 32);
+    count_mask = valid_doc_mask(first_doc, a.num_docs);
+  }
+  auto store = [&](uint32_t row, uint32_t acc) {
+    const int64_t col0 = static_cast<int64_t>(row) * a.out_cols + bundle * 32;
+    if constexpr (kOut == kOutBool) {
+      uint8_t* dst = static_cast<uint8_t*>(a.out) + (col0 + (lane >> 1)) * 64 +
+                     ((lane & 1) ? 0 : 32);
+      store_bool32(dst, acc);
+    } else {
+      uint32_t* dst = static_cast<uint32_t*>(a.out) + col0 * 2 + lane;
+      __builtin_nontemporal_store(acc, dst);
+    }
+    if constexpr (kOut == kOutCounts) {
+      const uint32_t c = wave_total_small(static_cast<uint32_t>(__builtin_popcount(acc & count_mask)));
+      if (lane == 0) a.counts[static_cast<int64_t>(row) * a.num_bundles + bundle] = c;
+    }
+  };
+  if constexpr (BOUND) {
+    constexpr int RW = ((K + 1 + 3) / 4) * 4;
+    const ST_CONST uint32_t* progs = a.bound + static_cast<uint64_t>(slot) * a.bound_words;
+    for (uint32_t s = s_begin; s < s_end;) {
+      const ST_CONST uint32_t* prog = progs + a.bound_start[s];
+      const uint32_t hdr = prog[0];
+      const uint32_t T = hdr & 0xFFFFu;
+      if (hdr & kPairedWithNext) {
+        const ST_CONST uint32_t* prog_b = progs + a.bound_start[s + 1];
+        const uint32_t hdr_b = prog_b[0];
+        uint32_t acc_a, acc_b;
+        if (!eval_bound_pair<K, STAGED>(rs, prog + kProgHeaderWords, prog_b + kProgHeaderWords,
+                                        T, acc_a, acc_b)) {
+          acc_a = eval_bound_flat_loop<K, STAGED, G>(rs, prog + kProgHeaderWords, T);
+          acc_b = eval_bound_flat_loop<K, STAGED, G>(rs, prog_b + kProgHeaderWords, T);
+        }
+        if (hdr & kFlatComplement) acc_a = ~acc_a;
+        if (hdr_b & kFlatComplement) acc_b = ~acc_b;
+        store(prog[1], acc_a);
+        store(prog_b[1], acc_b);
+        s += 2;
+        continue;
+      }
+      uint32_t acc;
+      if (hdr & kFlatForm) {
+        acc = eval_bound_flat<K, STAGED, G>(rs, prog + kProgHeaderWords, T);
+        if (hdr & kFlatComplement) acc = ~acc;
+      } else {
+        acc = eval_bound_stack<K, KP, STAGED, G>(rs, prog, T, prog[2]);
+      }
+      store(prog[1], acc);
+      ++s;
+    }
+    (void)RW;
+    return;
+  }
+  const ST_CONST uint32_t* progs = a.insns;
+  const ST_CONST uint32_t* starts = a.insn_start;
+  for (uint32_t s = s_begin; s < s_end; ++s) {
+    const ST_CONST uint32_t* prog = progs + starts[s];
+    const uint32_t hdr = prog[0];
+    const uint32_t row = prog[1];
+    const uint32_t T = hdr & 0xFFFFu;
+    uint32_t acc;
+    if (hdr & kFlatForm) {
+      acc = eval_flat<K, KP, STAGED, G>(rs, reinterpret_cast<const ST_CONST u32x4*>(prog + kProgHeaderWords), T);
+      if (hdr & kFlatComplement) acc = ~acc;
+    } else {
+      acc = eval_stack<K, KP, STAGED, G>(rs, prog, T, prog[2]);
+    }
+    store(row, acc);
+  }
+}
+
+// The arrays arrive as separate __restrict__ parameters (not inside
+// SearchArgs) so the compiler can prove the output stores never alias the
+// program and offset arrays and fetch those with scalar loads.
+template <int K, int kOut>
+__global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
+    const int64_t* __restrict__ index, int64_t index_numel,
+    const int64_t* __restrict__ bundle_offsets, int64_t num_bundles,
+    const uint32_t* __restrict__ wave_off,
+    const uint32_t* __restrict__ insn_start, const uint32_t* __restrict__ insns,
+    const uint64_t* __restrict__ hashes, const uint32_t* __restrict__ bundle_slot,
+    const uint32_t* __restrict__ bundle_order,
+    const uint32_t* __restrict__ bound_start, const uint32_t* __restrict__ bound,
+    uint32_t bound_words, uint32_t num_terms, int32_t hash_k,
+    int64_t out_cols, void* __restrict__ out, int64_t* __restrict__ counts, int64_t num_docs) {
+  SearchArgs a;
+  a.index = index;
+  a.index_numel = index_numel;
+  a.bundle_offsets = as_const(bundle_offsets);
+  a.num_bundles = num_bundles;
+  a.wave_off = as_const(wave_off);
+  a.insn_start = as_const(insn_start);
+  a.insns = as_const(insns);
+  a.hashes = as_const(hashes);
+  a.bundle_slot = as_const(bundle_slot);
+  a.bundle_order = as_const(bundle_order);
+  a.bound_start = as_const(bound_start);
+  a.bound = as_const(bound);
+  a.bound_words = bound_words;
+  a.num_terms = num_terms;
+  a.hash_k = hash_k;
+  a.out_cols = out_cols;
+  a.out = out;
+  a.counts = counts;
+  a.num_docs = num_docs;
+  constexpr int KP = K <= 4 ? 4 : (K <= 8 ? 8 : 12);
+  constexpr int G = KP == 4 ? 4 : (KP == 8 ? 2 : 1);  // terms fetched together
+  __shared__ u32x4 tile[(kSearchTileRows + 2) * 16];
+  __shared__ uint32_t pos[kSearchPosSlots];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const uint32_t wave = uniform(tid >> 6);
+
+  if (tid < 32) {
+    const uint32_t fill = tid < 16 ? ~0u : 0u;
+    tile[kSearchOnesRow * 16 + (tid & 15) + (tid & 16)] = u32x4{fill, fill, fill, fill};
+  }
+
+  // Bundle visited at step i of the grid-stride walk.
+  auto bundle_at = [&](int64_t i) -> int64_t {
+    return a.bundle_order ? static_cast<int64_t>(a.bundle_order[i]) : i;
+  };
+  u32x4 pre[kPrefetch];
+  if (blockIdx.x < a.num_bundles) prefetch_tile(a, bundle_at(blockIdx.x), pre);
+
+  int64_t prev_b = -1;
+  const uint32_t s_begin = uniform(a.wave_off[wave]);
+  const uint32_t s_end = uniform(a.wave_off[wave + 1]);
+  const char* tile_lane = reinterpret_cast<const char*>(tile) + lane * 4;
+  const uint32_t* index32 = reinterpret_cast<const uint32_t*>(a.index);
+
+  for (int64_t step = blockIdx.x; step < a.num_bundles; step += gridDim.x) {
+    const int64_t bundle = bundle_at(step);
+    int64_t start, b;
+    bundle_extent(a, bundle, start, b);
+    const bool staged = b <= kSearchTileRows;
+
+    __syncthreads();  // previous bundle's readers are done with tile and pos
+    if (staged) {
+      const int64_t chunks = b * 16;
+#pragma unroll
+      for (int i = 0; i < kPrefetch; ++i) {
+        const int c = tid + i * kSearchThreads;
+        if (c < chunks) tile[c] = pre[i];
+      }
+    }
+    const uint32_t slot = a.bundle_slot ? a.bundle_slot[bundle] : kNoWidthSlot;
+    if (slot == kNoWidthSlot && b != prev_b) {
+      const FastMod64 fm = make_fastmod_dev(static_cast<uint64_t>(b));
+      for (uint32_t u = tid; u < a.num_terms; u += kSearchThreads) {
+        int16_t found[K];
+#pragma unroll
+        for (int j = 0; j < K; ++j) found[j] = 0;
+        int cnt = 0;
+        if (b > 0) cnt = resolve_positions<K>(a.hashes + static_cast<uint64_t>(u) * a.hash_k,
+                                              a.hash_k, fm, found);
+        uint32_t* dst = pos + u * KP;
+#pragma unroll
+        for (int j = 0; j < KP; ++j) {
+          const int16_t r = (j < K && j < cnt) ? found[j < K ? j : 0] : found[0];
+          uint32_t v;
+          if (staged) {
+            v = (cnt == 0 ? kSearchZerosRow : static_cast<int>(r)) * 256u;
+          } else {
+            v = cnt == 0 ? static_cast<uint32_t>(kPosZeros)
+                         : static_cast<uint32_t>(static_cast<int32_t>(r));
+          }
+          dst[j] = v;
+        }
+      }
+      prev_b = b;
+    }
+    __syncthreads();
+
+    const int64_t next = step + gridDim.x;
+    if (next < a.num_bundles) prefetch_tile(a, bundle_at(next), pre);
+
+    // Evaluate this wave's queries on the bundle.
+    RowSource rs;
+    rs.pos = pos;
+    rs.tile_lane = tile_lane;
+    rs.index32 = index32;
+    rs.index_numel = a.index_numel;
+    rs.start = start;
+    rs.lane = lane;
+    rs.staged = staged;
+    if (slot != kNoWidthSlot) {
+      if (staged) {
+        eval_queries<K, KP, true, true, G, kOut>(a, rs, s_begin, s_end, bundle, slot);
+      } else {
+        eval_queries<K, KP, false, true, G, kOut>(a, rs, s_begin, s_end, bundle, slot);
+      }
+    } else if (staged) {
+      eval_queries<K, KP, true, false, G, kOut>(a, rs, s_begin, s_end, bundle, slot);
+    } else {
+      eval_queries<K, KP, false, false, G, kOut>(a, rs, s_begin, s_end, bundle, slot);
+    }
+  }
+}
+
+}  // namespace
+
+using KernelFn = void (*)(const int64_t*, int64_t, const int64_t*, int64_t,
+                          const uint32_t*, const uint32_t*,
+                          const uint32_t*, const uint64_t*, const uint32_t*,
+                          const uint32_t*, const uint32_t*, const uint32_t*, uint32_t,
+                          uint32_t, int32_t,
+                          int64_t, void*, int64_t*, int64_t);
+
+// The kernels of one K (all output modes), defined in the translation unit
+// compiled with ST_SEARCH_K = K.
+template <int K>
+KernelFn search_kernel_for(int mode);
+template <> KernelFn search_kernel_for<1>(int mode);
+template <> KernelFn search_kernel_for<2>(int mode);
+template <> KernelFn search_kernel_for<3>(int mode);
+template <> KernelFn search_kernel_for<4>(int mode);
+template <> KernelFn search_kernel_for<5>(int mode);
+template <> KernelFn search_kernel_for<6>(int mode);
+template <> KernelFn search_kernel_for<7>(int mode);
+template <> KernelFn search_kernel_for<8>(int mode);
+template <> KernelFn search_kernel_for<9>(int mode);
+template <> KernelFn search_kernel_for<10>(int mode);
+
+}  // namespace st

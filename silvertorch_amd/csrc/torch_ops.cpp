@@ -141,9 +141,17 @@ struct PlanHolder {
   ~PlanHolder() { st_search_plan_destroy(p); }
 };
 
-Tensor search_gpu(const Tensor& bloom_index_in, const Tensor& bundle_b_offsets_in,
-                  const Tensor& plans_data, const Tensor& plans_offsets,
-                  int64_t k, int64_t hash_k, bool return_bool_mask) {
+// Checks, plan compilation, width binding and plan upload shared by the
+// search ops.
+struct PreparedSearch {
+  Tensor index, bbo, blob;
+  PlanHolder plan;
+  int64_t Q = 0, nb = 0;
+};
+
+void prepare_search(PreparedSearch& ps, const Tensor& bloom_index_in,
+                    const Tensor& bundle_b_offsets_in, const Tensor& plans_data,
+                    const Tensor& plans_offsets, int64_t k, int64_t hash_k) {
   TORCH_CHECK(bloom_index_in.is_cuda(), "bloom_index must be a GPU tensor");
   TORCH_CHECK(bloom_index_in.dim() == 1, "bloom_index must be 1-D");
   TORCH_CHECK(bloom_index_in.scalar_type() == at::kLong, "bloom_index must be int64");
@@ -158,43 +166,48 @@ Tensor search_gpu(const Tensor& bloom_index_in, const Tensor& bundle_b_offsets_i
               "bloom_query_plans_data must be int8");
   TORCH_CHECK(plans_offsets.scalar_type() == at::kLong,
               "bloom_query_plans_offsets must be int64");
-  const auto dev = bloom_index_in.device();
-  c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(dev);
-  const Tensor index = bloom_index_in.contiguous();
-  const Tensor bbo = bundle_b_offsets_in.contiguous();
+  ps.index = bloom_index_in.contiguous();
+  ps.bbo = bundle_b_offsets_in.contiguous();
   // Plans are compiled on the host, as the reference decodes them there
   // (bloom_index_search_cuda.cu:1043-1098).
   const Tensor pd = plans_data.to(at::kCPU).contiguous();
   const Tensor po = plans_offsets.to(at::kCPU).contiguous();
-
-  PlanHolder plan;
   check_st(st_search_plan_create(
                reinterpret_cast<const int8_t*>(pd.data_ptr()), pd.numel(),
-               po.data_ptr<int64_t>(), po.numel(), k, hash_k, &plan.p),
+               po.data_ptr<int64_t>(), po.numel(), k, hash_k, &ps.plan.p),
            "bloom_index_search_batch");
-  const int64_t Q = st_search_plan_num_queries(plan.p);
-  const int64_t nb = bbo.numel() - 1;
-  if (Q > 0 && nb > 0) {
-    // Bundle widths on the host let the plan carry per-width row positions.
-    const Tensor bbo_h = bbo.to(at::kCPU);
-    check_st(st_search_plan_bind_widths(plan.p, bbo_h.data_ptr<int64_t>(), nb),
-             "bloom_index_search_batch");
-  }
-  const int64_t C = nb * ST_COLUMNS_PER_BUNDLE;
-  Tensor out = return_bool_mask
-                   ? at::empty({Q, C * ST_BITS_PER_COLUMN},
-                               at::TensorOptions().dtype(at::kBool).device(dev))
-                   : at::empty({Q, C}, at::TensorOptions().dtype(at::kLong).device(dev));
-  if (Q == 0 || nb == 0) return out;
-
-  const int64_t blob_bytes = st_search_plan_blob_bytes(plan.p);
+  ps.Q = st_search_plan_num_queries(ps.plan.p);
+  ps.nb = ps.bbo.numel() - 1;
+  if (ps.Q == 0 || ps.nb == 0) return;
+  // Bundle widths on the host let the plan carry per-width row positions.
+  const Tensor bbo_h = ps.bbo.to(at::kCPU);
+  check_st(st_search_plan_bind_widths(ps.plan.p, bbo_h.data_ptr<int64_t>(), ps.nb),
+           "bloom_index_search_batch");
+  const int64_t blob_bytes = st_search_plan_blob_bytes(ps.plan.p);
   Tensor host = at::empty({blob_bytes}, at::TensorOptions().dtype(at::kByte).pinned_memory(true));
-  std::memcpy(host.data_ptr(), st_search_plan_blob(plan.p), blob_bytes);
-  Tensor blob = host.to(dev, /*non_blocking=*/true);
-  check_st(st_bloom_index_search_batch(index.data_ptr<int64_t>(), index.numel(),
-                                       bbo.data_ptr<int64_t>(), nb, plan.p,
-                                       blob.data_ptr(), return_bool_mask ? 1 : 0,
-                                       out.data_ptr(), current_stream(index)),
+  std::memcpy(host.data_ptr(), st_search_plan_blob(ps.plan.p), blob_bytes);
+  ps.blob = host.to(ps.index.device(), /*non_blocking=*/true);
+}
+
+Tensor search_gpu(const Tensor& bloom_index_in, const Tensor& bundle_b_offsets_in,
+                  const Tensor& plans_data, const Tensor& plans_offsets,
+                  int64_t k, int64_t hash_k, bool return_bool_mask) {
+  TORCH_CHECK(bloom_index_in.is_cuda(), "bloom_index must be a GPU tensor");
+  c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(bloom_index_in.device());
+  PreparedSearch ps;
+  prepare_search(ps, bloom_index_in, bundle_b_offsets_in, plans_data, plans_offsets, k,
+                 hash_k);
+  const auto dev = ps.index.device();
+  const int64_t C = ps.nb * ST_COLUMNS_PER_BUNDLE;
+  Tensor out = return_bool_mask
+                   ? at::empty({ps.Q, C * ST_BITS_PER_COLUMN},
+                               at::TensorOptions().dtype(at::kBool).device(dev))
+                   : at::empty({ps.Q, C}, at::TensorOptions().dtype(at::kLong).device(dev));
+  if (ps.Q == 0 || ps.nb == 0) return out;
+  check_st(st_bloom_index_search_batch(ps.index.data_ptr<int64_t>(), ps.index.numel(),
+                                       ps.bbo.data_ptr<int64_t>(), ps.nb, ps.plan.p,
+                                       ps.blob.data_ptr(), return_bool_mask ? 1 : 0,
+                                       out.data_ptr(), current_stream(ps.index)),
            "bloom_index_search_batch");
   return out;
 }
@@ -325,15 +338,43 @@ std::tuple<Tensor, Tensor> mask_to_ids_cpu(const Tensor& packed, int64_t num_doc
   return {ids.cpu(), ro.cpu()};
 }
 
+// Search and the count step of the compaction in one pass over the index,
+// then the scan, one sync for the id total, and the id writes.
 std::tuple<Tensor, Tensor> search_ids_gpu(const Tensor& bloom_index,
                                           const Tensor& bundle_b_offsets,
                                           const Tensor& plans_data,
                                           const Tensor& plans_offsets, int64_t k,
                                           int64_t hash_k, int64_t num_docs,
                                           bool int64_ids) {
-  const Tensor packed = search_gpu(bloom_index, bundle_b_offsets, plans_data,
-                                   plans_offsets, k, hash_k, /*return_bool_mask=*/false);
-  return mask_to_ids_gpu(packed, num_docs, int64_ids);
+  TORCH_CHECK(num_docs >= 0, "num_docs must be non-negative, got ", num_docs);
+  TORCH_CHECK(bloom_index.is_cuda(), "bloom_index must be a GPU tensor");
+  c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(bloom_index.device());
+  PreparedSearch ps;
+  prepare_search(ps, bloom_index, bundle_b_offsets, plans_data, plans_offsets, k, hash_k);
+  const auto dev = ps.index.device();
+  const int64_t C = ps.nb * ST_COLUMNS_PER_BUNDLE;
+  TORCH_CHECK(int64_ids || std::min(num_docs, C * ST_BITS_PER_COLUMN) <= INT32_MAX,
+              "int32 ids cannot hold doc ids up to ", num_docs, "; pass int64_ids=True");
+  auto opts = at::TensorOptions().device(dev);
+  Tensor row_offsets = at::empty({ps.Q + 1}, opts.dtype(at::kLong));
+  Tensor packed = at::empty({ps.Q, C}, opts.dtype(at::kLong));
+  Tensor ws = at::empty({std::max<int64_t>(st_bloom_compact_workspace_bytes(ps.Q, C), 1)},
+                        opts.dtype(at::kByte));
+  void* stream = current_stream(ps.index);
+  check_st(st_bloom_index_search_batch_counts(
+               ps.index.data_ptr<int64_t>(), ps.index.numel(), ps.bbo.data_ptr<int64_t>(),
+               ps.nb, ps.plan.p, ps.blob.defined() ? ps.blob.data_ptr() : nullptr, num_docs,
+               packed.numel() ? packed.data_ptr<int64_t>() : nullptr, ws.data_ptr(),
+               row_offsets.data_ptr<int64_t>(), stream),
+           "bloom_index_search_batch_ids");
+  const int64_t total = row_offsets[ps.Q].item<int64_t>();
+  Tensor ids = at::empty({total}, opts.dtype(int64_ids ? at::kLong : at::kInt));
+  if (total > 0) {
+    check_st(st_bloom_compact_ids(packed.data_ptr<int64_t>(), ps.Q, C, num_docs, ws.data_ptr(),
+                                  ids.data_ptr(), int64_ids ? 1 : 0, stream),
+             "bloom_index_search_batch_ids");
+  }
+  return {ids, row_offsets};
 }
 
 std::tuple<Tensor, Tensor> search_ids_cpu(const Tensor& bloom_index,

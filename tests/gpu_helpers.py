@@ -89,3 +89,31 @@ def compact(packed, num_docs: int, int64_ids: bool = False):
                                       ids.data_ptr() if total else None, int(int64_ids), _stream()))
     torch.cuda.synchronize()
     return ids.cpu().numpy(), ro.cpu().numpy()
+
+
+def search_ids(index, bbo, plans_data, plans_offsets, k: int, hash_k: int, num_docs: int,
+               int64_ids: bool = False):
+    """Fused search + count (st_bloom_index_search_batch_counts), then the id
+    writes -> (ids, row_offsets, packed) as numpy arrays."""
+    L = capi.lib()
+    idx_d = torch.as_tensor(np.ascontiguousarray(index, np.int64)).cuda()
+    bbo_d = torch.as_tensor(np.ascontiguousarray(bbo, np.int64)).cuda()
+    plan = capi.SearchPlan(bytes(np.asarray(plans_data, dtype=np.int8).tobytes()), plans_offsets, k, hash_k)
+    plan.bind_widths(bbo_d.cpu().numpy())
+    blob = plan.blob()
+    blob_d = torch.frombuffer(bytearray(blob), dtype=torch.uint8).cuda() if blob else None
+    q, nb = plan.num_queries, bbo_d.numel() - 1
+    packed = torch.empty((q, nb * 32), dtype=torch.long, device="cuda")
+    ro = torch.empty(q + 1, dtype=torch.long, device="cuda")
+    ws = torch.empty(max(L.st_bloom_compact_workspace_bytes(q, nb * 32), 1), dtype=torch.uint8, device="cuda")
+    capi.check(L.st_bloom_index_search_batch_counts(
+        idx_d.data_ptr() if idx_d.numel() else None, idx_d.numel(), bbo_d.data_ptr(), nb, plan.handle,
+        blob_d.data_ptr() if blob_d is not None else None, num_docs,
+        packed.data_ptr() if packed.numel() else None, ws.data_ptr(), ro.data_ptr(), _stream()))
+    total = int(ro[q].item())
+    ids = torch.empty(total, dtype=torch.long if int64_ids else torch.int32, device="cuda")
+    if total:
+        capi.check(L.st_bloom_compact_ids(packed.data_ptr(), q, nb * 32, num_docs, ws.data_ptr(),
+                                          ids.data_ptr(), int(int64_ids), _stream()))
+    torch.cuda.synchronize()
+    return ids.cpu().numpy(), ro.cpu().numpy(), packed.cpu().numpy()

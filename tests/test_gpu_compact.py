@@ -61,6 +61,33 @@ def test_compact_cfg1_search_output():
     np.testing.assert_array_equal(ids, want_ids)
 
 
+@pytest.mark.parametrize("seed", range(3))
+def test_fused_search_counts_vs_oracle(seed):
+    """Search with per-(query, bundle) counts in the same pass, then ids:
+    equal to the oracle's search followed by the oracle's compaction, for doc
+    counts that end inside a bundle and inside a half-word."""
+    rng = np.random.default_rng(100 + seed)
+    n = int(rng.integers(3000, 9000))
+    F = 3
+    cnt = rng.integers(0, 4, (n, F))
+    offs = np.concatenate([[0], np.cumsum(cnt.reshape(-1))]).astype(np.int64)
+    vals = rng.integers(0, 40, int(offs[-1])).astype(np.int64)
+    ids_f = np.array([1, 2, 3], dtype=np.int32)
+    index, bbo = H.build(ids_f, offs, vals, 3.0, 3)
+    terms = [f"{int(rng.integers(1, 4))}:{int(rng.integers(0, 40))}" for _ in range(40)]
+    queries = [f"{terms[i]} OR {terms[i + 1]} AND NOT {terms[i + 2]}" for i in range(0, 36)] + ["", "NOT " + terms[0]]
+    _, data, po = P.parse_batch(queries, 7)
+    pd, po = np.frombuffer(data, np.int8).copy(), np.array(po, np.int64)
+    want_packed = O.search_packed(index, bbo, pd, po, 3, 7)
+    for nd in (n, n - 17, 0, (len(bbo) - 1) * 2048):
+        H.note(f"[fused ids] seed={seed} num_docs={nd}")
+        ids, ro, packed = H.search_ids(index, bbo, pd, po, 3, 7, nd)
+        np.testing.assert_array_equal(packed, want_packed)
+        want_ids, want_ro = O.compact(want_packed, nd)
+        np.testing.assert_array_equal(ro, want_ro)
+        np.testing.assert_array_equal(ids.astype(np.int64), want_ids)
+
+
 def test_ops_ids_readme_known_answers():
     """README.md:255-268: ids of the five README queries over four docs,
     through the fused search-to-ids op and through mask -> ids."""
