@@ -252,6 +252,29 @@ int st_bloom_compact_ids(const int64_t* packed, int64_t num_queries,
                          const void* workspace, void* ids, int ids_int64,
                          void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Fused filter + top-k.  No reference operator; relatives are the bloom-
+ * filtered scoring of fused_kmean_ann (fused_kmean_ann_cuda.cu:545-551,
+ * :1797-1926) and at::topk (fresh_index_post_processing.cpp:245-250).
+ * For each query q, among docs d < num_docs whose bit is set in `packed`
+ * (int64[num_queries, num_columns], the packed search output), the `topk`
+ * best by score = sum_j doc_embeddings[d, j] * query_embeddings[q, j]
+ * (bf16 inputs, row-major [*, dim], fp32 accumulation), ordered by score
+ * descending then doc id ascending, into out_ids int64[num_queries, topk]
+ * and out_scores float[num_queries, topk]; missing entries are -1 / -inf.
+ * dim is 64, 128 or 256; 1 <= topk <= 2048; doc ids below 2^32; embeddings
+ * 16-byte aligned with at least num_docs rows.  workspace: device memory of
+ * st_filtered_topk_workspace_bytes(num_queries) bytes.  Synchronises the
+ * stream once (to learn whether a candidate list overflowed; if one did, the
+ * selection is redone with smaller rounds).
+ * ------------------------------------------------------------------------- */
+int64_t st_filtered_topk_workspace_bytes(int64_t num_queries);
+int st_filtered_topk(const int64_t* packed, int64_t num_queries,
+                     int64_t num_columns, int64_t num_docs,
+                     const void* doc_embeddings, const void* query_embeddings,
+                     int64_t dim, int64_t topk, void* workspace,
+                     int64_t* out_ids, float* out_scores, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

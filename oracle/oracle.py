@@ -148,6 +148,8 @@ def filtered_topk(emb: np.ndarray, qv: np.ndarray, packed: np.ndarray, topk: int
     packed = np.ascontiguousarray(packed, dtype=np.int64)
     n, dim = emb.shape
     q = qv.shape[0]
+    if packed.ndim != 2 or packed.shape[0] != q or packed.shape[1] * 64 < n or qv.shape[1] != dim:
+        raise ValueError(f"shapes do not match: emb {emb.shape}, qv {qv.shape}, packed {packed.shape}")
     ids = np.zeros((q, topk), dtype=np.int64)
     scores = np.zeros((q, topk), dtype=np.float32)
     rc = lib().or_filtered_topk(_p(emb, ctypes.c_float), n, dim, _p(qv, ctypes.c_float), q,

@@ -41,6 +41,8 @@ SIGNATURES = {
     "st_bloom_compact_workspace_bytes": (_i64, [_i64, _i64]),
     "st_bloom_compact_offsets": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp]),
     "st_bloom_compact_ids": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, ctypes.c_int, _vp]),
+    "st_filtered_topk_workspace_bytes": (_i64, [_i64]),
+    "st_filtered_topk": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp]),
     "st_bloom_index_search_batch_counts": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
 }
 

@@ -388,6 +388,72 @@ std::tuple<Tensor, Tensor> search_ids_cpu(const Tensor& bloom_index,
   return mask_to_ids_cpu(packed, num_docs, int64_ids);
 }
 
+// ------------------------------------------ fused filter + top-k
+// No reference operator (relatives: fused_kmean_ann's bloom-filtered scoring,
+// fused_kmean_ann_cuda.cu:1797-1926, and at::topk).
+
+std::tuple<Tensor, Tensor> filtered_topk_gpu(const Tensor& packed_in, const Tensor& emb_in,
+                                             const Tensor& qv_in, int64_t num_docs,
+                                             int64_t topk) {
+  TORCH_CHECK(packed_in.is_cuda() && emb_in.is_cuda() && qv_in.is_cuda(),
+              "filtered_topk inputs must be GPU tensors");
+  TORCH_CHECK(packed_in.device() == emb_in.device() && emb_in.device() == qv_in.device(),
+              "filtered_topk inputs must be on one device");
+  TORCH_CHECK(packed_in.dim() == 2 && packed_in.scalar_type() == at::kLong,
+              "packed_mask must be the 2-D int64 packed search output");
+  TORCH_CHECK(emb_in.dim() == 2 && emb_in.scalar_type() == at::kBFloat16,
+              "doc_embeddings must be a 2-D bfloat16 tensor");
+  TORCH_CHECK(qv_in.dim() == 2 && qv_in.scalar_type() == at::kBFloat16,
+              "query_embeddings must be a 2-D bfloat16 tensor");
+  TORCH_CHECK(qv_in.size(0) == packed_in.size(0), "query_embeddings has ", qv_in.size(0),
+              " rows, the mask ", packed_in.size(0), " queries");
+  TORCH_CHECK(qv_in.size(1) == emb_in.size(1), "embedding dimensions differ: ", emb_in.size(1),
+              " vs ", qv_in.size(1));
+  TORCH_CHECK(num_docs >= 0 && num_docs <= emb_in.size(0), "num_docs ", num_docs,
+              " must be in [0, ", emb_in.size(0), "] (rows of doc_embeddings)");
+  c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(packed_in.device());
+  const Tensor packed = packed_in.contiguous(), emb = emb_in.contiguous(),
+               qv = qv_in.contiguous();
+  const int64_t Q = packed.size(0);
+  auto opts = at::TensorOptions().device(packed.device());
+  Tensor ids = at::empty({Q, topk}, opts.dtype(at::kLong));
+  Tensor scores = at::empty({Q, topk}, opts.dtype(at::kFloat));
+  if (Q == 0) return {ids, scores};
+  Tensor ws = at::empty({st_filtered_topk_workspace_bytes(Q)}, opts.dtype(at::kByte));
+  check_st(st_filtered_topk(packed.numel() ? packed.data_ptr<int64_t>() : nullptr, Q,
+                            packed.size(1), num_docs, emb.numel() ? emb.data_ptr() : nullptr,
+                            qv.data_ptr(), emb.size(1), topk, ws.data_ptr(),
+                            ids.data_ptr<int64_t>(), scores.data_ptr<float>(),
+                            current_stream(packed)),
+           "filtered_topk");
+  return {ids, scores};
+}
+
+std::tuple<Tensor, Tensor> filtered_topk_cpu(const Tensor& packed, const Tensor& emb,
+                                             const Tensor& qv, int64_t num_docs, int64_t topk) {
+  const at::Device gpu = gpu_for_cpu_call();
+  auto [ids, scores] = filtered_topk_gpu(packed.to(gpu), emb.to(gpu), qv.to(gpu), num_docs, topk);
+  return {ids.cpu(), scores.cpu()};
+}
+
+std::tuple<Tensor, Tensor> search_topk_gpu(const Tensor& bloom_index, const Tensor& bundle_b_offsets,
+                                           const Tensor& plans_data, const Tensor& plans_offsets,
+                                           int64_t k, int64_t hash_k, const Tensor& emb,
+                                           const Tensor& qv, int64_t num_docs, int64_t topk) {
+  const Tensor packed = search_gpu(bloom_index, bundle_b_offsets, plans_data, plans_offsets, k,
+                                   hash_k, /*return_bool_mask=*/false);
+  return filtered_topk_gpu(packed, emb, qv, num_docs, topk);
+}
+
+std::tuple<Tensor, Tensor> search_topk_cpu(const Tensor& bloom_index, const Tensor& bundle_b_offsets,
+                                           const Tensor& plans_data, const Tensor& plans_offsets,
+                                           int64_t k, int64_t hash_k, const Tensor& emb,
+                                           const Tensor& qv, int64_t num_docs, int64_t topk) {
+  const Tensor packed = search_cpu_tensors(bloom_index, bundle_b_offsets, plans_data,
+                                           plans_offsets, k, hash_k, false);
+  return filtered_topk_cpu(packed, emb, qv, num_docs, topk);
+}
+
 }  // namespace
 
 TORCH_LIBRARY_FRAGMENT(st, m) {
@@ -416,6 +482,15 @@ TORCH_LIBRARY_FRAGMENT(st, m) {
       "Tensor bloom_bundle_b_offsets, Tensor bloom_query_plans_data, "
       "Tensor bloom_query_plans_offsets, int k, int hash_k, int num_docs, "
       "bool int64_ids=False) -> (Tensor, Tensor)");
+  // Fused filter + top-k (no reference counterpart): ids int64[Q, topk] and
+  // scores float32[Q, topk], padded with -1 / -inf.
+  m.def("filtered_topk(Tensor packed_mask, Tensor doc_embeddings, Tensor query_embeddings, "
+        "int num_docs, int topk) -> (Tensor, Tensor)");
+  m.def(
+      "bloom_index_search_topk(Tensor bloom_index, Tensor bloom_bundle_b_offsets, "
+      "Tensor bloom_query_plans_data, Tensor bloom_query_plans_offsets, int k, int hash_k, "
+      "Tensor doc_embeddings, Tensor query_embeddings, int num_docs, int topk) "
+      "-> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(st, CUDA, m) {
@@ -425,6 +500,8 @@ TORCH_LIBRARY_IMPL(st, CUDA, m) {
   m.impl("generate_column_info_for_clusters", TORCH_FN(column_info));
   m.impl("bloom_mask_to_ids", TORCH_FN(mask_to_ids_gpu));
   m.impl("bloom_index_search_batch_ids", TORCH_FN(search_ids_gpu));
+  m.impl("filtered_topk", TORCH_FN(filtered_topk_gpu));
+  m.impl("bloom_index_search_topk", TORCH_FN(search_topk_gpu));
 }
 
 TORCH_LIBRARY_IMPL(st, CPU, m) {
@@ -434,6 +511,8 @@ TORCH_LIBRARY_IMPL(st, CPU, m) {
   m.impl("generate_column_info_for_clusters", TORCH_FN(column_info));
   m.impl("bloom_mask_to_ids", TORCH_FN(mask_to_ids_cpu));
   m.impl("bloom_index_search_batch_ids", TORCH_FN(search_ids_cpu));
+  m.impl("filtered_topk", TORCH_FN(filtered_topk_cpu));
+  m.impl("bloom_index_search_topk", TORCH_FN(search_topk_cpu));
 }
 
 // Python module entry point: importing silvertorch_amd._C loads this library,

@@ -86,6 +86,29 @@ def test_compact_matches_numpy_nonzero():
                 np.testing.assert_array_equal(ids, want_ids)
 
 
+def test_filtered_topk_matches_brute_force():
+    """The oracle's filtered top-k against a numpy restatement on tiny inputs:
+    fp64 scores of filter-passing docs, order (score desc, id asc), -1/-inf
+    padding; includes exact ties (repeated embeddings) and empty filters."""
+    rng = np.random.default_rng(31)
+    for n, dim, q, topk in [(1, 4, 1, 1), (70, 8, 3, 5), (130, 16, 4, 20), (200, 8, 2, 300)]:
+        emb = rng.integers(-3, 4, (n, dim)).astype(np.float32)  # small ints: many exact ties
+        qv = rng.integers(-3, 4, (q, dim)).astype(np.float32)
+        cols = (n + 63) // 64
+        bits = rng.random((q, cols * 64)) < 0.6
+        bits[0, :] = False if q > 1 else bits[0, :]
+        packed = np.packbits(bits, axis=1).view(">i8").astype(np.int64)
+        ids, scores = O.filtered_topk(emb, qv, packed, topk)
+        for qi in range(q):
+            passing = [d for d in range(n) if bits[qi, d]]
+            sc = {d: float(np.dot(emb[d].astype(np.float64), qv[qi].astype(np.float64))) for d in passing}
+            order = sorted(passing, key=lambda d: (-sc[d], d))[:topk]
+            want_ids = order + [-1] * (topk - len(order))
+            want_sc = [sc[d] for d in order] + [-np.inf] * (topk - len(order))
+            assert ids[qi].tolist() == want_ids
+            np.testing.assert_array_equal(scores[qi], np.array(want_sc, dtype=np.float32))
+
+
 def test_parser_oracle_matches_reference_bytes():
     g = G.parser_golden()
     for b in g["batches"]:
