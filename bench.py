@@ -49,6 +49,7 @@ def parse_args():
     p.add_argument("--cpu-queries", type=int, default=256,
                    help="queries of the batch the reference CPU search is timed on")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-topk", action="store_true", help="skip the cfg5 filter + top-k leg")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 512 MiB device-to-device copy, 5 times: the known-size "
                         "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings")
@@ -196,6 +197,109 @@ def measure_ids(st, capi, O, bi, bo, pd, po, k, hk, N, Q, packed, steps, warmup)
     }
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def measure_topk(st, capi, steps):
+    """cfg5: 20M docs built as cfg2, bf16[128]
+    embeddings, 512 queries with 3-term AND/OR filters, top-100.  Op step
+    time, the filter + top-k kernels' time from HIP events on the launching
+    stream, dense-equivalent MFMA rate, and a full-size check of sampled
+    queries against an fp32 torch reference of the same scores."""
+    import numpy as np
+    import torch
+
+    from silvertorch_amd import synthetic as S
+
+    cspec, qspec = S.CONFIGS["cfg5"]
+    N, D, TOPK = cspec.num_docs, 128, 100
+    t0 = time.time()
+    corp = S.make_corpus(cspec, seed=0)
+    queries = S.make_queries(cspec, qspec, seed=0)
+    dev = torch.device("cuda:0")
+    bi, bo = st.bloom_index_build(torch.from_numpy(corp.feature_ids).to(dev),
+                                  torch.from_numpy(corp.feature_offsets).to(dev),
+                                  torch.from_numpy(corp.feature_values).to(dev), cspec.b_multiplier, cspec.k)
+    del corp
+    emb, qv = S.make_embeddings_device(N, D, len(queries), seed=0)
+    _, (pd, po) = st.parse_expression_query_batch(queries, torch.ones(1, dtype=torch.long), cspec.hash_k, True, 5)
+    torch.cuda.synchronize()
+    log(f"cfg5 prepared in {time.time() - t0:.1f}s: {bi.numel() * 8 / 1e9:.2f} GB index, "
+        f"{emb.numel() * 2 / 1e9:.2f} GB embeddings")
+    Q = len(queries)
+
+    def step():
+        return st.bloom_index_search_topk(bi, bo, pd, po, cspec.k, cspec.hash_k, emb, qv, N, TOPK)
+
+    ids, sc = step()
+    torch.cuda.synchronize()
+    n = max(steps // 10, 3)
+    t1 = time.perf_counter()
+    for _ in range(n):
+        ids, sc = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t1) * 1e3 / n
+
+    # filter + top-k alone on the packed mask
+    packed = st.bloom_index_search_batch(bi, bo, pd, po, cspec.k, cspec.hash_k, False)
+    L = capi.lib()
+    stream = torch.cuda.current_stream()
+    ws = torch.empty(L.st_filtered_topk_workspace_bytes(Q), dtype=torch.uint8, device=dev)
+    kids = torch.empty((Q, TOPK), dtype=torch.long, device=dev)
+    ksc = torch.empty((Q, TOPK), dtype=torch.float32, device=dev)
+    reps = 5
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for r in range(reps + 1):
+        if r:
+            evs[r - 1][0].record(stream)
+        capi.check(L.st_filtered_topk(packed.data_ptr(), Q, packed.shape[1], N, emb.data_ptr(), qv.data_ptr(), D,
+                                      TOPK, ws.data_ptr(), kids.data_ptr(), ksc.data_ptr(), stream.cuda_stream))
+        if r:
+            evs[r - 1][1].record(stream)
+    torch.cuda.synchronize()
+    topk_ms = sum(a.elapsed_time(b) for a, b in evs) / reps
+    assert torch.equal(kids, ids) and torch.equal(ksc, sc)
+
+    # filter selectivity from the compaction's counting pass
+    ro = torch.empty(Q + 1, dtype=torch.long, device=dev)
+    cws = torch.empty(max(L.st_bloom_compact_workspace_bytes(Q, packed.shape[1]), 1), dtype=torch.uint8, device=dev)
+    capi.check(L.st_bloom_compact_offsets(packed.data_ptr(), Q, packed.shape[1], N, cws.data_ptr(), ro.data_ptr(),
+                                          stream.cuda_stream))
+    passing = int(ro[-1].item())
+
+    # sampled full-size check against fp32 torch scores of all passing docs
+    ok = True
+    words = packed.view(torch.uint8)  # little-endian bytes of each word
+    for q in (0, Q // 2, Q - 1):
+        row = words[q].view(-1, 8).flip(1).reshape(-1)       # big-endian bytes: doc order
+        bits = ((row.unsqueeze(1) >> torch.arange(7, -1, -1, device=dev, dtype=torch.uint8)) & 1).reshape(-1)[:N]
+        docs = torch.nonzero(bits, as_tuple=True)[0]
+        s_ref = emb[docs].float() @ qv[q].float()
+        k = min(TOPK, docs.numel())
+        top = torch.topk(s_ref, k).values
+        got = sc[q, :k]
+        ok &= bool(torch.allclose(got, top, rtol=1e-3, atol=1e-4))
+        ok &= bool((ids[q, :k] >= 0).all()) and bool((ids[q, k:] == -1).all())
+        ok &= bool(torch.allclose(emb[ids[q, :k]].float() @ qv[q].float(), got, rtol=1e-3, atol=1e-4))
+        ok &= bool(bits[ids[q, :k]].all())
+    log(f"topk: {ms:.3f} ms/step (search + filter + top-k), filter+top-k {topk_ms:.3f} ms, "
+        f"{passing} passing pairs, sampled queries consistent with fp32 torch reference: {ok}")
+    if not ok:
+        sys.exit("parity failure in sampled top-k queries")
+    dense_flop = 2.0 * D * Q * N
+    achieved = dense_flop / (topk_ms * 1e-3) / 1e12
+    return {
+        "workload": f"cfg5: {N} docs x {Q} queries, bf16[{D}] embeddings, 3-term filters, top-{TOPK}",
+        "op": "bloom_index_search_topk", "ms_per_step": ms,
+        "filtered_topk_ms": topk_ms,
+        "passing_pairs": passing, "selectivity": passing / (Q * N),
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / MFMA_BF16_PEAK_TFLOPS,
+                     "note": "dense-equivalent 2*D*Q*N flops; tiles with no passing doc are skipped"},
+        "hbm_gbs": (emb.numel() * 2 + packed.numel() * 8) / (topk_ms * 1e-3) / 1e9,
+    }
+
+
 def main():
     args = parse_args()
     if args.calibrate_copy:
@@ -308,6 +412,8 @@ def main():
     ids_report = measure_ids(st, capi, O, bi, bo, pd, po, k, hk, N, Q, out if not args.bool_mask else None,
                              args.steps, args.warmup)
 
+    topk_report = None if args.no_topk else measure_topk(st, capi, args.steps)
+
     baseline = None
     if not args.no_cpu_baseline:
         baseline = cpu_baseline(bi.cpu().numpy(), bo.cpu().numpy(), queries, k, hk, N, args.cpu_queries)
@@ -346,6 +452,7 @@ def main():
         "cpu_baseline": baseline,
         "build": {"ms": build_s * 1e3, "docs_per_s": N / build_s},
         "ids": ids_report,
+        "topk": topk_report,
     }
     print(json.dumps(result), flush=True)
 

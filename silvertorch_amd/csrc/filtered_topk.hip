@@ -87,96 +87,180 @@ __global__ void topk_reset_kernel(TopkState st, int64_t num_queries) {
   if (i == 0) st.overflow[0] = 0u;
 }
 
+// LDS bytes per query of a chunk: its row (D bf16) plus, per wave, the two
+// u32 filter words of the wave's 64 docs.
+template <int D>
+constexpr int lds_bytes_per_query() {
+  return D * 2 + kScoreWaves * 8;
+}
+
+template <int D>
+constexpr int64_t query_chunk() {
+  return (kLdsBytes / lds_bytes_per_query<D>()) / kQueryTile * kQueryTile;
+}
+
 // Scores docs [lo, hi) against queries [q_begin, q_begin + q_count).
+// LDS: the query rows (16-byte pieces XOR-swizzled by row, so the 32 rows a
+// wave reads at once hit distinct banks), then per wave the filter words of
+// its 64 docs for every query of the chunk.
 template <int D>
 __global__ __launch_bounds__(kScoreThreads) void topk_score_kernel(
     const uint16_t* __restrict__ emb, const uint16_t* __restrict__ qv,
     const uint32_t* __restrict__ mask32, int64_t num_columns, int64_t q_begin,
     int64_t q_count, int64_t lo, int64_t hi, TopkState st) {
-  constexpr int S = D / 16;                  // MFMA k-steps
-  constexpr int kRowBytes = D * 2 + 16;      // padded LDS row: no bank conflicts
+  constexpr int S = D / 16;        // MFMA k-steps
+  constexpr int kPieces = D / 8;   // 16-byte pieces per row
+  // 16 lanes read at once on gfx950 (64 banks): spread 16 rows.
+  constexpr int kSwz = kPieces < 16 ? kPieces - 1 : 15;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t q_tiles = (q_count + kQueryTile - 1) / kQueryTile;
+  const int q_tiles = static_cast<int>((q_count + kQueryTile - 1) / kQueryTile);
+  const int rows = q_tiles * kQueryTile;
+  uint32_t* masks = reinterpret_cast<uint32_t*>(lds + static_cast<int64_t>(rows) * D * 2) +
+                    wave * rows * 2;  // [tile][64]: lanes 0-31 docs 0-31, 32-63 docs 32-63
 
-  // Stage the query chunk (zero rows pad it to whole tiles).
-  {
-    const int64_t rows = q_tiles * kQueryTile;
-    constexpr int kChunks = D / 8;  // 16-byte pieces per row
-    for (int64_t i = threadIdx.x; i < rows * kChunks; i += kScoreThreads) {
-      const int64_t r = i / kChunks;
-      const int c = static_cast<int>(i - r * kChunks);
-      bf16x8 v = {};
-      if (r < q_count)
-        v = *reinterpret_cast<const bf16x8*>(qv + (q_begin + r) * D + c * 8);
-      *reinterpret_cast<bf16x8*>(lds + r * kRowBytes + c * 16) = v;
-    }
+  for (int i = threadIdx.x; i < rows * kPieces; i += kScoreThreads) {
+    const int r = i / kPieces, c = i - r * kPieces;
+    bf16x8 v = {};
+    if (r < q_count) v = *reinterpret_cast<const bf16x8*>(qv + (q_begin + r) * D + c * 8);
+    *reinterpret_cast<bf16x8*>(lds + r * (D * 2) + ((c ^ (r & kSwz)) << 4)) = v;
   }
   __syncthreads();
 
-  const int kofs = (lane >> 5) * 8;  // this lane's k sub-range of a step
   for (int64_t base = lo + static_cast<int64_t>(blockIdx.x) * kDocsPerStep; base < hi;
        base += static_cast<int64_t>(gridDim.x) * kDocsPerStep) {
     const int64_t d0 = base + wave * kDocsPerWave;  // first doc of this wave
     if (d0 >= hi) continue;                         // wave-uniform
-    bf16x8 a0[S], a1[S];
+    // Filter words of the wave's 64 docs for every query: docs 0-31 of a
+    // word are its high half, the second u32 in memory (d0 is a multiple of
+    // 64 within the round).
     {
-      const int64_t da = d0 + (lane & 31), db = da + 32;
+      constexpr int kBatch = 16;  // loads in flight before the LDS stores
+      const int64_t col = d0 >> 6;
+      const int half = lane >> 5;
+      const bool has = half == 0 || d0 + 32 < hi;
+      // docs at or past hi never pass (bit 31 is the half-word's first doc)
+      const int64_t left = hi - (d0 + 32 * half);
+      const uint32_t valid = left >= 32 ? ~0u : (left <= 0 ? 0u : ~0u << (32 - static_cast<int>(left)));
+      for (int t0 = 0; t0 < q_tiles; t0 += kBatch) {
+        uint32_t mv[kBatch];
+        // Unconditional loads from a valid address (selected afterwards), so
+        // that all of them are in flight before the first is waited for.
 #pragma unroll
-      for (int s = 0; s < S; ++s) {
-        a0[s] = da < hi ? *reinterpret_cast<const bf16x8*>(emb + da * D + s * 16 + kofs)
-                        : bf16x8{};
-        a1[s] = db < hi ? *reinterpret_cast<const bf16x8*>(emb + db * D + s * 16 + kofs)
-                        : bf16x8{};
+        for (int u = 0; u < kBatch; ++u) {
+          const int64_t ql = static_cast<int64_t>(t0 + u) * kQueryTile + (lane & 31);
+          const bool ok = t0 + u < q_tiles && ql < q_count && has;
+          const int64_t idx = ok ? (q_begin + ql) * 2 * num_columns + 2 * col + 1 - half : 0;
+          mv[u] = mask32[idx];
+          mv[u] = ok ? mv[u] & valid : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+          if (t0 + u < q_tiles) masks[(t0 + u) * 64 + lane] = mv[u];
       }
     }
-    // u32 of the packed row holding docs d0..d0+31 (and d0+32..d0+63): docs
-    // 0-31 of a word are its high half, the second u32 in memory.
-    const int64_t col = d0 >> 6;  // d0 is a multiple of 64 within the round
-    for (int64_t t = 0; t < q_tiles; ++t) {
-      const int64_t ql = t * kQueryTile + (lane & 31);  // query of this lane's column
+    bf16x8 a0[S], a1[S];
+    {
+      const int kofs = (lane >> 5) * 8;
+      // Rows past hi read row hi - 1 (valid) and are zeroed afterwards.
+      const int64_t da = d0 + (lane & 31), db = da + 32;
+      const int64_t ra = da < hi ? da : hi - 1, rb = db < hi ? db : hi - 1;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        a0[s] = *reinterpret_cast<const bf16x8*>(emb + ra * D + s * 16 + kofs);
+        a1[s] = *reinterpret_cast<const bf16x8*>(emb + rb * D + s * 16 + kofs);
+      }
+      if (da >= hi) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) a0[s] = bf16x8{};
+      }
+      if (db >= hi) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) a1[s] = bf16x8{};
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float th_next = st.thr[q_begin + ((lane & 31) < q_count ? (lane & 31) : 0)];
+    for (int t = 0; t < q_tiles; ++t) {
+      const int ql = t * kQueryTile + (lane & 31);  // query of this lane's column
       const bool qvalid = ql < q_count;
       const int64_t q = q_begin + ql;
-      const uint32_t* mrow = mask32 + q * 2 * num_columns + 2 * col;
-      const uint32_t m0 = qvalid ? mrow[1] : 0u;
-      const uint32_t m1 = (qvalid && d0 + 32 < hi) ? mrow[0] : 0u;
+      const float th = qvalid ? th_next : INFINITY;
+      {  // threshold of the next tile, one tile ahead (clamped address)
+        const int qn = ql + kQueryTile;
+        th_next = st.thr[q_begin + (qn < q_count ? qn : 0)];
+      }
+      // lane's column: docs 0-31 in slot (lane & 31), docs 32-63 in slot 32 + (lane & 31)
+      const uint32_t m0 = masks[t * 64 + (lane & 31)];
+      const uint32_t m1 = masks[t * 64 + 32 + (lane & 31)];
       const bool any0 = __ballot(m0 != 0u) != 0, any1 = __ballot(m1 != 0u) != 0;
       if (!any0 && !any1) continue;
       f32x16 acc0 = {}, acc1 = {};
-      const uint8_t* qrow = lds + (t * kQueryTile + (lane & 31)) * kRowBytes + kofs * 2;
+      const uint8_t* qrow = lds + ql * (D * 2);
+      const int sw = ql & kSwz;
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(qrow + s * 32);
+        const int piece = (2 * s + (lane >> 5)) ^ sw;
+        const bf16x8 b = *reinterpret_cast<const bf16x8*>(qrow + (piece << 4));
         if (any0) acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[s], b, acc0, 0, 0, 0);
         if (any1) acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[s], b, acc1, 0, 0, 0);
       }
-      const float th = qvalid ? st.thr[q] : INFINITY;
       // acc[j] holds doc row 8*(j/4) + 4*(lane/32) + j%4 of the tile, query
       // column lane % 32.
+      {
+        // Gate on the lane maxima (no score of the tile at the threshold),
+        // then per-lane hit bits, one atomic per query per tile for a run of
+        // slots, and the writes.
+        float mx = fmaxf(acc0[0], acc1[0]);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int r = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-        if (((m0 >> (31 - r)) & 1u) && acc0[j] >= th && d0 + r < hi) {
-          const uint32_t slot = atomicAdd(st.counts + q, 1u);
-          if (slot < st.capacity) st.cand[q * st.capacity + slot] = make_key(acc0[j], d0 + r);
-          else atomicOr(st.overflow, 1u);
+        for (int j = 1; j < 16; ++j) mx = fmaxf(mx, fmaxf(acc0[j], acc1[j]));
+        if (__ballot(mx >= th) == 0) continue;
+        uint32_t hits = 0u;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int r = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+          const bool h0 = ((m0 >> (31 - r)) & 1u) && acc0[j] >= th;
+          const bool h1 = ((m1 >> (31 - r)) & 1u) && acc1[j] >= th;
+          hits |= (h0 ? 1u << j : 0u) | (h1 ? 1u << (16 + j) : 0u);
         }
-        if (((m1 >> (31 - r)) & 1u) && acc1[j] >= th && d0 + 32 + r < hi) {
-          const uint32_t slot = atomicAdd(st.counts + q, 1u);
-          if (slot < st.capacity) st.cand[q * st.capacity + slot] = make_key(acc1[j], d0 + 32 + r);
-          else atomicOr(st.overflow, 1u);
+        if (__ballot(hits != 0u) == 0) continue;
+        const uint32_t cnt = __builtin_popcount(hits);
+        const uint32_t cnt_pair = __shfl_xor(cnt, 32, 64);  // lanes l, l ^ 32: same query
+        uint32_t base = 0u;
+        if (lane < 32 && cnt + cnt_pair > 0u) base = atomicAdd(st.counts + q, cnt + cnt_pair);
+        const uint32_t base_pair = __shfl_xor(base, 32, 64);
+        uint32_t slot = lane < 32 ? base : base_pair + cnt_pair;
+        while (__ballot(hits != 0u) != 0) {
+          if (hits != 0u) {
+            const int j = __builtin_ctz(hits);
+            hits &= hits - 1u;
+            const int jj = j & 15;
+            const bool second = j >= 16;
+            float v = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v = jj == i ? (second ? acc1[i] : acc0[i]) : v;
+            const int64_t doc = d0 + (second ? 32 : 0) + 8 * (jj >> 2) + 4 * (lane >> 5) + (jj & 3);
+            if (slot < st.capacity) st.cand[q * st.capacity + slot] = make_key(v, doc);
+            else atomicOr(st.overflow, 1u);
+            ++slot;
+          }
         }
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 }
 
-// Descending bitonic sort of kSelectSlots keys in LDS.
-__device__ void bitonic_sort_desc(uint64_t* keys) {
-  for (int k = 2; k <= kSelectSlots; k <<= 1) {
+// Descending bitonic sort of the first `size` keys in LDS (a power of two).
+__device__ void bitonic_sort_desc(uint64_t* keys, int size) {
+  for (int k = 2; k <= size; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < kSelectSlots / 2; i += kSelectThreads) {
+      for (int i = threadIdx.x; i < size / 2; i += kSelectThreads) {
         // i-th compare pair of this stage: lower index lo, partner lo + j
         const int lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
         const int hi = lo + j;
@@ -201,15 +285,23 @@ __global__ __launch_bounds__(kSelectThreads) void topk_select_kernel(
   const int64_t q = blockIdx.x;
   uint64_t* cand = st.cand + q * st.capacity;
   const uint32_t n = min(st.counts[q], st.capacity);
-  for (int i = threadIdx.x; i < kSelectSlots; i += kSelectThreads) keys[i] = 0ull;
-  __syncthreads();
-  // Keys 0 .. kSelectChunk-1 hold the best so far; each chunk of candidates
-  // is sorted in behind them.
-  for (uint32_t c0 = 0; c0 < n; c0 += kSelectChunk) {
-    for (int i = threadIdx.x; i < kSelectChunk; i += kSelectThreads)
-      keys[kSelectChunk + i] = c0 + i < n ? cand[c0 + i] : 0ull;
+  if (n <= static_cast<uint32_t>(kSelectSlots)) {
+    // One sort of the smallest power of two holding every candidate.
+    int size = 64;
+    while (size < static_cast<int>(n)) size <<= 1;
+    for (int i = threadIdx.x; i < size; i += kSelectThreads) keys[i] = i < static_cast<int>(n) ? cand[i] : 0ull;
     __syncthreads();
-    bitonic_sort_desc(keys);
+    bitonic_sort_desc(keys, size);
+  } else {
+    // Keys 0 .. kSelectChunk-1 hold the best so far; each chunk of
+    // candidates is sorted in behind them.
+    for (int i = threadIdx.x; i < kSelectChunk; i += kSelectThreads) keys[i] = 0ull;
+    for (uint32_t c0 = 0; c0 < n; c0 += kSelectChunk) {
+      for (int i = threadIdx.x; i < kSelectChunk; i += kSelectThreads)
+        keys[kSelectChunk + i] = c0 + i < n ? cand[c0 + i] : 0ull;
+      __syncthreads();
+      bitonic_sort_desc(keys, kSelectSlots);
+    }
   }
   const uint32_t kept = min(n, static_cast<uint32_t>(topk));
   if (final_round) {
@@ -237,14 +329,14 @@ template <int D>
 void launch_score(const uint16_t* emb, const uint16_t* qv, const uint32_t* mask32,
                   int64_t num_columns, int64_t num_queries, int64_t lo, int64_t hi,
                   const TopkState& st, hipStream_t s) {
-  constexpr int kRowBytes = D * 2 + 16;
-  const int64_t q_chunk = (kLdsBytes / kRowBytes) / kQueryTile * kQueryTile;
+  const int64_t q_chunk = query_chunk<D>();
   const int64_t steps = (hi - lo + kDocsPerStep - 1) / kDocsPerStep;
   const int grid = static_cast<int>(std::max<int64_t>(
       1, std::min<int64_t>(steps, static_cast<int64_t>(cu_count()))));
   for (int64_t qb = 0; qb < num_queries; qb += q_chunk) {
     const int64_t qn = std::min(q_chunk, num_queries - qb);
-    const size_t lds = static_cast<size_t>((qn + kQueryTile - 1) / kQueryTile * kQueryTile) * kRowBytes;
+    const size_t lds = static_cast<size_t>((qn + kQueryTile - 1) / kQueryTile * kQueryTile) *
+                       lds_bytes_per_query<D>();
     hipLaunchKernelGGL(topk_score_kernel<D>, dim3(grid), dim3(kScoreThreads), lds, s, emb, qv,
                        mask32, num_columns, qb, qn, lo, hi, st);
     check_launch("topk_score_kernel");
@@ -280,7 +372,7 @@ void set_lds_limits() {
 }
 
 // Doc ranges of the rounds: a first round of 8192 docs, then each round
-// four times everything before it (rounds aligned to bundles), or, in the
+// eight times everything before it (rounds aligned to bundles), or, in the
 // safe schedule, rounds no larger than a candidate list can always hold.
 std::vector<int64_t> round_bounds(int64_t num_docs, int64_t topk, bool safe) {
   std::vector<int64_t> b{0};
@@ -288,7 +380,7 @@ std::vector<int64_t> round_bounds(int64_t num_docs, int64_t topk, bool safe) {
   const int64_t safe_step =
       std::max<int64_t>(kRoundAlign, (static_cast<int64_t>(kCandidateCapacity) - topk) / kRoundAlign * kRoundAlign);
   while (pos < num_docs) {
-    int64_t step = safe ? safe_step : (pos == 0 ? 8192 : 4 * pos);
+    int64_t step = safe ? safe_step : (pos == 0 ? 8192 : 8 * pos);
     step = (step + kRoundAlign - 1) / kRoundAlign * kRoundAlign;
     pos = std::min(num_docs, pos + step);
     b.push_back(pos);

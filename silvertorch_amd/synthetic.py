@@ -177,3 +177,21 @@ def make_embeddings(num_docs: int, dim: int, num_queries: int, seed: int = 0):
     e = _rng(seed, STREAM_EMB).standard_normal((num_docs, dim), dtype=np.float32) / np.sqrt(dim)
     q = _rng(seed, STREAM_QEMB).standard_normal((num_queries, dim), dtype=np.float32)
     return (torch.from_numpy(e).to(torch.bfloat16), torch.from_numpy(q).to(torch.bfloat16))
+
+
+def make_embeddings_device(num_docs: int, dim: int, num_queries: int, seed: int = 0,
+                           device: str = "cuda", chunk: int = 1 << 21):
+    """Large-scale variant of make_embeddings, drawn on the device with a
+    seeded torch generator (docs ~ N(0, 1/dim), queries ~ N(0, 1), stored as
+    bf16), chunk by chunk to bound the fp32 staging."""
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(seed * 1_000_003 + STREAM_EMB)
+    emb = torch.empty((num_docs, dim), dtype=torch.bfloat16, device=device)
+    for r0 in range(0, num_docs, chunk):
+        r1 = min(num_docs, r0 + chunk)
+        emb[r0:r1] = (torch.randn((r1 - r0, dim), generator=g, device=device) / dim ** 0.5).to(torch.bfloat16)
+    g.manual_seed(seed * 1_000_003 + STREAM_QEMB)
+    q = torch.randn((num_queries, dim), generator=g, device=device).to(torch.bfloat16)
+    return emb, q
