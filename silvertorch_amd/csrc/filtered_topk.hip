@@ -196,17 +196,21 @@ __global__ __launch_bounds__(kScoreThreads) void topk_score_kernel(
       // lane's column: docs 0-31 in slot (lane & 31), docs 32-63 in slot 32 + (lane & 31)
       const uint32_t m0 = masks[t * 64 + (lane & 31)];
       const uint32_t m1 = masks[t * 64 + 32 + (lane & 31)];
-      const bool any0 = __ballot(m0 != 0u) != 0, any1 = __ballot(m1 != 0u) != 0;
-      if (!any0 && !any1) continue;
+      if (__ballot((m0 | m1) != 0u) == 0) continue;  // no filter bit in the tile
+      // All query fragments first (one LDS latency per tile), then the two
+      // MFMA chains; a half-tile without filter bits still runs (rare at
+      // useful selectivities, and cheaper than a branch per MFMA).
       f32x16 acc0 = {}, acc1 = {};
       const uint8_t* qrow = lds + ql * (D * 2);
       const int sw = ql & kSwz;
+      bf16x8 b[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+        b[s] = *reinterpret_cast<const bf16x8*>(qrow + (((2 * s + (lane >> 5)) ^ sw) << 4));
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        const int piece = (2 * s + (lane >> 5)) ^ sw;
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(qrow + (piece << 4));
-        if (any0) acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[s], b, acc0, 0, 0, 0);
-        if (any1) acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[s], b, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[s], b[s], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[s], b[s], acc1, 0, 0, 0);
       }
       // acc[j] holds doc row 8*(j/4) + 4*(lane/32) + j%4 of the tile, query
       // column lane % 32.
