@@ -148,6 +148,18 @@ int st_search_plan_create(const int8_t* plans_data, int64_t plans_data_len,
 int st_search_plan_bind_widths(st_search_plan* plan,
                                const int64_t* bundle_b_offsets,
                                int64_t num_bundles);
+/* Width binding on the device instead: the search call itself derives the
+ * slots from the device bundle offsets (a census kernel) and expands
+ * host-built width-independent templates (a fill kernel), so that no copy of
+ * the bundle offsets to the host and no synchronisation is needed.  After
+ * this call the device copy of the plan must hold
+ * st_search_plan_device_bytes(plan) bytes: the first
+ * st_search_plan_blob_bytes(plan) copied from st_search_plan_blob(plan), the
+ * rest written by the search call.  Exclusive with
+ * st_search_plan_bind_widths. */
+int st_search_plan_prepare_device_binding(st_search_plan* plan,
+                                          int64_t num_bundles);
+int64_t st_search_plan_device_bytes(const st_search_plan* plan);
 int64_t st_search_plan_num_queries(const st_search_plan* plan);
 int64_t st_search_plan_blob_bytes(const st_search_plan* plan);
 const void* st_search_plan_blob(const st_search_plan* plan);

@@ -25,6 +25,8 @@ SIGNATURES = {
     "st_bloom_index_build": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
     "st_search_plan_create": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, ctypes.POINTER(_vp)]),
     "st_search_plan_bind_widths": (ctypes.c_int, [_vp, _vp, _i64]),
+    "st_search_plan_prepare_device_binding": (ctypes.c_int, [_vp, _i64]),
+    "st_search_plan_device_bytes": (_i64, [_vp]),
     "st_search_plan_num_queries": (_i64, [_vp]),
     "st_search_plan_blob_bytes": (_i64, [_vp]),
     "st_search_plan_blob": (_vp, [_vp]),
@@ -111,6 +113,13 @@ class SearchPlan:
 
         self._bbo = np.ascontiguousarray(bundle_b_offsets, dtype=np.int64)
         check(lib().st_search_plan_bind_widths(self.handle, self._bbo.ctypes.data, self._bbo.size - 1))
+
+    def prepare_device_binding(self, num_bundles: int) -> None:
+        check(lib().st_search_plan_prepare_device_binding(self.handle, num_bundles))
+
+    @property
+    def device_bytes(self) -> int:
+        return int(lib().st_search_plan_device_bytes(self.handle))
 
     @property
     def num_queries(self) -> int:

@@ -55,6 +55,162 @@ int cu_count() { return device_cu_count(); }
 namespace st {
 namespace {
 
+// ------------------------------------------------- width binding on the device
+// The host-side equivalent is st_search_plan_bind_widths (search_plan.cpp).
+
+constexpr int kCensusThreads = 1024;
+constexpr int kCensusCap = 4096;  // distinct widths tracked; more stay unslotted
+constexpr long long kCensusEmpty = -1;
+
+__device__ __forceinline__ uint32_t census_hash(long long w) {
+  return static_cast<uint32_t>((static_cast<unsigned long long>(w) * 0x9E3779B97F4A7C15ull) >> 52) &
+         (kCensusCap - 1);
+}
+
+// Entry of width w in the table, inserting it when `insert`; -1 when absent
+// (or the table is full).
+__device__ int census_find(long long* keys, long long w, bool insert) {
+  uint32_t h = census_hash(w);
+  for (int probe = 0; probe < kCensusCap; ++probe, h = (h + 1) & (kCensusCap - 1)) {
+    long long k = keys[h];
+    if (k == w) return static_cast<int>(h);
+    if (k == kCensusEmpty) {
+      if (!insert) return -1;
+      k = static_cast<long long>(atomicCAS(reinterpret_cast<unsigned long long*>(keys + h),
+                                           static_cast<unsigned long long>(kCensusEmpty),
+                                           static_cast<unsigned long long>(w)));
+      if (k == kCensusEmpty || k == w) return static_cast<int>(h);
+    }
+  }
+  return -1;
+}
+
+__device__ __forceinline__ long long bundle_width(const int64_t* bbo, int64_t i) {
+  const int64_t w = bbo[i + 1] - bbo[i];
+  return w > 0 ? w : 0;
+}
+
+// One workgroup: the kMaxWidthSlots most frequent widths get slots (ties to
+// the smaller width), every bundle its slot, and the visiting order groups
+// bundles by slot (a counting sort; order within a slot is arbitrary).
+__global__ __launch_bounds__(kCensusThreads) void width_census_kernel(
+    const int64_t* __restrict__ bbo, int64_t nb, uint32_t* __restrict__ num_slots,
+    int64_t* __restrict__ slot_width, uint32_t* __restrict__ bundle_slot,
+    uint32_t* __restrict__ bundle_order) {
+  __shared__ long long keys[kCensusCap];
+  __shared__ uint32_t count[kCensusCap];
+  __shared__ uint32_t slot_of[kCensusCap];
+  __shared__ uint32_t dense[kCensusCap];
+  __shared__ uint32_t n_dense;
+  __shared__ uint32_t cursor[kMaxWidthSlots + 1];
+  for (int e = threadIdx.x; e < kCensusCap; e += kCensusThreads) {
+    keys[e] = kCensusEmpty;
+    count[e] = 0u;
+    slot_of[e] = kNoWidthSlot;
+  }
+  if (threadIdx.x == 0) n_dense = 0u;
+  if (threadIdx.x <= kMaxWidthSlots) cursor[threadIdx.x] = 0u;
+  __syncthreads();
+  for (int64_t i = threadIdx.x; i < nb; i += kCensusThreads) {
+    const int e = census_find(keys, bundle_width(bbo, i), true);
+    if (e >= 0) atomicAdd(count + e, 1u);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < kCensusCap; e += kCensusThreads)
+    if (keys[e] != kCensusEmpty) dense[atomicAdd(&n_dense, 1u)] = static_cast<uint32_t>(e);
+  __syncthreads();
+  const uint32_t n = n_dense;
+  for (uint32_t a = threadIdx.x; a < n; a += kCensusThreads) {
+    const uint32_t e = dense[a];
+    const uint32_t c = count[e];
+    const long long w = keys[e];
+    uint32_t rank = 0;
+    for (uint32_t b = 0; b < n; ++b) {
+      const uint32_t f = dense[b];
+      rank += (count[f] > c || (count[f] == c && keys[f] < w)) ? 1u : 0u;
+    }
+    if (rank < static_cast<uint32_t>(kMaxWidthSlots)) {
+      slot_of[e] = rank;
+      slot_width[rank] = w;
+    }
+  }
+  if (threadIdx.x == 0) *num_slots = n < static_cast<uint32_t>(kMaxWidthSlots) ? n : kMaxWidthSlots;
+  __syncthreads();
+  for (int64_t i = threadIdx.x; i < nb; i += kCensusThreads) {
+    const int e = census_find(keys, bundle_width(bbo, i), false);
+    const uint32_t sl = e >= 0 ? slot_of[e] : kNoWidthSlot;
+    bundle_slot[i] = sl;
+    atomicAdd(cursor + (sl == kNoWidthSlot ? kMaxWidthSlots : sl), 1u);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {  // bucket sizes -> bucket starts
+    uint32_t run = 0;
+    for (int b = 0; b <= kMaxWidthSlots; ++b) {
+      const uint32_t c = cursor[b];
+      cursor[b] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  for (int64_t i = threadIdx.x; i < nb; i += kCensusThreads) {
+    const int e = census_find(keys, bundle_width(bbo, i), false);
+    const uint32_t sl = e >= 0 ? slot_of[e] : kNoWidthSlot;
+    const uint32_t pos = atomicAdd(cursor + (sl == kNoWidthSlot ? kMaxWidthSlots : sl), 1u);
+    bundle_order[pos] = static_cast<uint32_t>(i);
+  }
+}
+
+// Position r of a term at width b, as term_positions (search_plan.cpp) and
+// signature_match (bloom_index_search.cpp:40-61) resolve it: over hashes
+// p < hash_k, b_p = (int16)(h[p] % b), repeats skipped, at most k_eff kept,
+// unused slots repeat the first; LDS byte offsets for staged widths, rows
+// relative to the bundle start otherwise.
+__device__ uint32_t device_term_position(const uint64_t* h, int hash_k, int k_eff, int64_t b,
+                                         int r) {
+  int16_t found[kMaxSearchK];
+  int cnt = 0;
+  if (b > 0) {
+    for (int p = 0; p < hash_k && cnt < k_eff; ++p) {
+      const int16_t bp = static_cast<int16_t>(h[p] % static_cast<uint64_t>(b));
+      bool dup = false;
+      for (int j = 0; j < cnt; ++j) dup |= found[j] == bp;
+      if (!dup) found[cnt++] = bp;
+    }
+  }
+  const int16_t row = cnt == 0 ? 0 : (r < cnt ? found[r] : found[0]);
+  if (b <= kSearchTileRows)
+    return static_cast<uint32_t>(cnt == 0 ? kSearchZerosRow : row) * 256u;
+  return cnt == 0 ? static_cast<uint32_t>(kPosZeros)
+                  : static_cast<uint32_t>(static_cast<int32_t>(row));
+}
+
+// Expands a batch's width-block template for every slot.
+__global__ void bind_fill_kernel(const uint32_t* __restrict__ tmpl,
+                                 const uint32_t* __restrict__ code, uint32_t words,
+                                 const uint64_t* __restrict__ hashes, int hash_k, int k_eff,
+                                 const uint32_t* __restrict__ num_slots,
+                                 const int64_t* __restrict__ slot_width,
+                                 uint32_t* __restrict__ bound) {
+  const uint32_t sl = blockIdx.y;
+  if (sl >= *num_slots) return;
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= words) return;
+  const int64_t b = slot_width[sl];
+  const uint32_t c = code[i];
+  uint32_t v;
+  if (c == kTmplCopy) {
+    v = tmpl[i];
+  } else if (c == kTmplOnes) {
+    v = b <= kSearchTileRows ? static_cast<uint32_t>(kSearchOnesRow) * 256u
+                             : static_cast<uint32_t>(kPosOnes);
+  } else {
+    const uint32_t t = (c >> 4) - 1u;
+    v = device_term_position(hashes + static_cast<uint64_t>(t) * hash_k, hash_k, k_eff, b,
+                             static_cast<int>(c & 15u));
+  }
+  bound[static_cast<uint64_t>(sl) * words + i] = v;
+}
+
 // Validates the arguments and launches the search kernel once per batch.
 void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
                    const int64_t* bundle_b_offsets, int64_t num_bundles,
@@ -72,6 +228,30 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
   const char* blob = static_cast<const char*>(plan_blob_device);
   const bool bound = plan->bound_bundles >= 0;
   auto at = [&](uint64_t off) { return reinterpret_cast<const uint32_t*>(blob + off); };
+  if (plan->device_bind) {
+    // Width binding on the device, ahead of the search on the same stream.
+    char* dev = const_cast<char*>(blob);
+    auto* nsl = reinterpret_cast<uint32_t*>(dev + plan->off_num_slots);
+    auto* sw = reinterpret_cast<int64_t*>(dev + plan->off_slot_width);
+    hipLaunchKernelGGL(width_census_kernel, dim3(1), dim3(kCensusThreads), 0, stream,
+                       bundle_b_offsets, num_bundles, nsl, sw,
+                       reinterpret_cast<uint32_t*>(dev + plan->off_bundle_slot),
+                       reinterpret_cast<uint32_t*>(dev + plan->off_bundle_order));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+      throw Error(ST_ERR_HIP, cat("width census launch failed: ", hipGetErrorString(e)));
+    for (const SearchBatch& bt : plan->batches) {
+      if (bt.bound_words == 0) continue;
+      hipLaunchKernelGGL(bind_fill_kernel, dim3((bt.bound_words + 255) / 256, kMaxWidthSlots),
+                         dim3(256), 0, stream, at(bt.off_tmpl), at(bt.off_tmpl_code),
+                         bt.bound_words, reinterpret_cast<const uint64_t*>(blob + bt.off_hashes),
+                         static_cast<int>(plan->hash_k), plan->k_eff, nsl, sw,
+                         reinterpret_cast<uint32_t*>(dev + bt.off_bound));
+      e = hipGetLastError();
+      if (e != hipSuccess)
+        throw Error(ST_ERR_HIP, cat("bind fill launch failed: ", hipGetErrorString(e)));
+    }
+  }
   for (const SearchBatch& bt : plan->batches) {
     hipLaunchKernelGGL(
         fn, dim3(grid), dim3(kSearchThreads), 0, stream, bloom_index, bloom_index_numel,

@@ -921,6 +921,123 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
   });
 }
 
+namespace st {
+namespace {
+
+uint64_t align_to(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+
+// Template of one batch's width block: the layout of st_search_plan_bind_widths
+// with every position word replaced by a code (term, position index) that the
+// device resolves at each slot width.
+void build_block_template(const st_search_plan& plan, const SearchBatch& bt,
+                          const std::vector<uint32_t>& insns,
+                          const std::vector<uint32_t>& starts, std::vector<uint32_t>& bstart,
+                          std::vector<uint32_t>& tmpl, std::vector<uint32_t>& code) {
+  const int k_eff = plan.k_eff, kp = plan.kp, rw = bound_record_words(k_eff);
+  const uint32_t pos_bytes = static_cast<uint32_t>(kp) * 4;
+  std::vector<uint32_t> bound_T(bt.num_slots);
+  for (uint32_t q = 0; q < bt.num_slots; ++q) bound_T[q] = insns[starts[q]] & 0xFFFFu;
+  for (uint32_t q = 0; q + 1 < bt.num_slots; ++q) {
+    if (insns[starts[q]] & kPairedWithNext) {
+      const uint32_t t = std::max(bound_T[q], bound_T[q + 1]);
+      bound_T[q] = bound_T[q + 1] = t;
+    }
+  }
+  bstart.assign(bt.num_slots, 0);
+  uint32_t words = 0;
+  for (uint32_t q = 0; q < bt.num_slots; ++q) {
+    bstart[q] = words;
+    const uint32_t hdr = insns[starts[q]];
+    uint32_t n = kProgHeaderWords;
+    n += (hdr & kFlatForm) ? bound_T[q] * rw : (hdr & 0xFFFFu) * kp + insns[starts[q] + 2];
+    words += (n + 3) & ~3u;
+  }
+  tmpl.assign(words, 0u);
+  code.assign(words, kTmplCopy);
+  for (uint32_t q = 0; q < bt.num_slots; ++q) {
+    const uint32_t* src = insns.data() + starts[q];
+    uint32_t* dst = tmpl.data() + bstart[q];
+    uint32_t* dc = code.data() + bstart[q];
+    const uint32_t hdr = src[0];
+    const uint32_t T = hdr & 0xFFFFu;
+    for (int w = 0; w < kProgHeaderWords; ++w) dst[w] = src[w];
+    if (hdr & kFlatForm) {
+      dst[0] = (hdr & ~0xFFFFu) | bound_T[q];
+      for (uint32_t j = 0; j < T; ++j) {
+        const uint32_t* lit = src + kProgHeaderWords + j * kFlatLiteralWords;
+        const uint32_t term = lit[0] / pos_bytes;
+        const uint32_t at = kProgHeaderWords + j * rw;
+        for (int r = 0; r < k_eff; ++r) dc[at + r] = tmpl_position_code(term, r);
+        dst[at + k_eff] = (lit[1] ? 1u : 0u) | (lit[2] ? 2u : 0u);
+      }
+      for (uint32_t j = T; j < bound_T[q]; ++j) {  // no-op padding records
+        const uint32_t at = kProgHeaderWords + j * rw;
+        for (int r = 0; r < k_eff; ++r) dc[at + r] = kTmplOnes;
+        dst[at + k_eff] = 0u;
+      }
+    } else {
+      const uint32_t nops = src[2];
+      for (uint32_t j = 0; j < T; ++j) {
+        const uint32_t term = src[kProgHeaderWords + j] / pos_bytes;
+        for (int r = 0; r < kp; ++r)
+          dc[kProgHeaderWords + j * kp + r] = tmpl_position_code(term, r);
+      }
+      for (uint32_t o = 0; o < nops; ++o)
+        dst[kProgHeaderWords + T * kp + o] = src[kProgHeaderWords + T + o];
+    }
+  }
+}
+
+}  // namespace
+}  // namespace st
+
+extern "C" int st_search_plan_prepare_device_binding(st_search_plan* plan,
+                                                     int64_t num_bundles) {
+  using namespace st;
+  return guarded([&] {
+    ST_CHECK(plan != nullptr, "plan is null");
+    ST_CHECK(plan->bound_bundles < 0, "plan is already bound to bundle widths");
+    ST_CHECK(num_bundles >= 0, "negative bundle count");
+    auto& blob = plan->blob;
+    std::vector<uint32_t> bstart, tmpl, code;
+    for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
+      SearchBatch& bt = plan->batches[bi];
+      build_block_template(*plan, bt, plan->batch_insns[bi], plan->batch_starts[bi], bstart,
+                           tmpl, code);
+      bt.bound_words = static_cast<uint32_t>(tmpl.size());
+      bt.off_bound_start = blob.size();
+      append_bytes(blob, bstart.data(), bstart.size() * 4);
+      bt.off_tmpl = blob.size();
+      append_bytes(blob, tmpl.data(), tmpl.size() * 4);
+      bt.off_tmpl_code = blob.size();
+      append_bytes(blob, code.data(), code.size() * 4);
+    }
+    blob.resize(blob.size() + 256, 0);  // slack for scalar loads
+    // The device-written part follows the uploaded bytes.
+    uint64_t d = align_to(blob.size(), 256);
+    plan->off_num_slots = d;
+    d += 256;
+    plan->off_slot_width = d;
+    d = align_to(d + 8 * kMaxWidthSlots, 256);
+    plan->off_bundle_slot = d;
+    d = align_to(d + 4 * static_cast<uint64_t>(num_bundles), 256);
+    plan->off_bundle_order = d;
+    d = align_to(d + 4 * static_cast<uint64_t>(num_bundles), 256);
+    for (SearchBatch& bt : plan->batches) {
+      bt.off_bound = d;
+      d = align_to(d + 4ull * kMaxWidthSlots * bt.bound_words, 256);
+    }
+    plan->device_bytes = d + 256;  // slack after the last width block
+    plan->bound_bundles = num_bundles;
+    plan->device_bind = true;
+  });
+}
+
+extern "C" int64_t st_search_plan_device_bytes(const st_search_plan* plan) {
+  if (plan == nullptr) return 0;
+  return static_cast<int64_t>(plan->device_bind ? plan->device_bytes : plan->blob.size());
+}
+
 extern "C" int64_t st_search_plan_num_queries(const st_search_plan* plan) {
   return plan ? plan->num_queries : 0;
 }

@@ -115,7 +115,17 @@ struct SearchBatch {
   uint64_t off_bound_start = 0;  // uint32[num_slots]: first word within a width block
   uint64_t off_bound = 0;        // uint32[width_slots * bound_words]
   uint32_t bound_words = 0;      // words per width block
+  // device binding: one width block as a template (host-written) whose
+  // position words are codes resolved per slot width on the device
+  uint64_t off_tmpl = 0;         // uint32[bound_words]: words copied as they are
+  uint64_t off_tmpl_code = 0;    // uint32[bound_words]: kTmplCopy / kTmplOnes / term code
 };
+
+// Codes of a width-block template word.
+constexpr uint32_t kTmplCopy = 0u;           // the template word itself
+constexpr uint32_t kTmplOnes = 0xFFFFFFFFu;  // the all-ones row at the slot's width
+// otherwise ((term + 1) << 4) | r: position r of batch term `term`
+inline uint32_t tmpl_position_code(uint32_t term, uint32_t r) { return ((term + 1u) << 4) | r; }
 
 }  // namespace st
 
@@ -137,4 +147,10 @@ struct st_search_plan {
   uint64_t off_bundle_slot = 0;      // uint32[bound_bundles]
   uint64_t off_bundle_order = 0;     // uint32[bound_bundles]: visiting order
   std::vector<int64_t> slot_width;   // width of each slot
+  // set by st_search_plan_prepare_device_binding: the search call binds the
+  // widths on the device into the part of the device copy past the host blob
+  bool device_bind = false;
+  uint64_t device_bytes = 0;         // size of the device copy
+  uint64_t off_num_slots = 0;        // uint32[1] (device-written)
+  uint64_t off_slot_width = 0;       // int64[kMaxWidthSlots] (device-written)
 };

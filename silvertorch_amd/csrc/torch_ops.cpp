@@ -179,14 +179,15 @@ void prepare_search(PreparedSearch& ps, const Tensor& bloom_index_in,
   ps.Q = st_search_plan_num_queries(ps.plan.p);
   ps.nb = ps.bbo.numel() - 1;
   if (ps.Q == 0 || ps.nb == 0) return;
-  // Bundle widths on the host let the plan carry per-width row positions.
-  const Tensor bbo_h = ps.bbo.to(at::kCPU);
-  check_st(st_search_plan_bind_widths(ps.plan.p, bbo_h.data_ptr<int64_t>(), ps.nb),
-           "bloom_index_search_batch");
+  // The search call binds the programs to the bundle widths on the device
+  // (no copy of the bundle offsets to the host, no synchronisation).
+  check_st(st_search_plan_prepare_device_binding(ps.plan.p, ps.nb), "bloom_index_search_batch");
   const int64_t blob_bytes = st_search_plan_blob_bytes(ps.plan.p);
   Tensor host = at::empty({blob_bytes}, at::TensorOptions().dtype(at::kByte).pinned_memory(true));
   std::memcpy(host.data_ptr(), st_search_plan_blob(ps.plan.p), blob_bytes);
-  ps.blob = host.to(ps.index.device(), /*non_blocking=*/true);
+  ps.blob = at::empty({st_search_plan_device_bytes(ps.plan.p)},
+                      at::TensorOptions().dtype(at::kByte).device(ps.index.device()));
+  ps.blob.narrow(0, 0, blob_bytes).copy_(host, /*non_blocking=*/true);
 }
 
 Tensor search_gpu(const Tensor& bloom_index_in, const Tensor& bundle_b_offsets_in,

@@ -44,24 +44,32 @@ def build(ids, offsets, values, b_multiplier: float, k: int):
 
 
 def search(index, bbo, plans_data, plans_offsets, k: int, hash_k: int, bool_mask: bool = False,
-           bind: bool | None = None):
-    """C-ABI search; index / bbo may be numpy arrays or cuda tensors.  With
-    bind=None both the width-bound and the unbound plan run and must agree."""
+           bind: str | None = None):
+    """C-ABI search; index / bbo may be numpy arrays or cuda tensors.  bind:
+    "host" (st_search_plan_bind_widths), "device"
+    (st_search_plan_prepare_device_binding) or "none"; with bind=None all
+    three run and must agree."""
     if bind is None:
-        a = search(index, bbo, plans_data, plans_offsets, k, hash_k, bool_mask, True)
-        b = search(index, bbo, plans_data, plans_offsets, k, hash_k, bool_mask, False)
-        np.testing.assert_array_equal(a, b, err_msg="width-bound and unbound plans disagree")
+        a = search(index, bbo, plans_data, plans_offsets, k, hash_k, bool_mask, "host")
+        for mode in ("device", "none"):
+            b = search(index, bbo, plans_data, plans_offsets, k, hash_k, bool_mask, mode)
+            np.testing.assert_array_equal(a, b, err_msg=f"host-bound and {mode} plans disagree")
         return a
     L = capi.lib()
     idx_d = index if isinstance(index, torch.Tensor) else torch.as_tensor(np.ascontiguousarray(index, np.int64)).cuda()
     bbo_d = bbo if isinstance(bbo, torch.Tensor) else torch.as_tensor(np.ascontiguousarray(bbo, np.int64)).cuda()
     plan = capi.SearchPlan(bytes(np.asarray(plans_data, dtype=np.int8).tobytes()), plans_offsets, k, hash_k)
-    if bind:
-        plan.bind_widths(bbo_d.cpu().numpy())
-    blob = plan.blob()
-    blob_d = torch.frombuffer(bytearray(blob), dtype=torch.uint8).cuda() if blob else None
-    q = plan.num_queries
     nb = bbo_d.numel() - 1
+    if bind == "host":
+        plan.bind_widths(bbo_d.cpu().numpy())
+    elif bind == "device":
+        plan.prepare_device_binding(nb)
+    blob = plan.blob()
+    blob_d = None
+    if blob:
+        blob_d = torch.zeros(plan.device_bytes, dtype=torch.uint8, device="cuda")
+        blob_d[:len(blob)] = torch.frombuffer(bytearray(blob), dtype=torch.uint8).cuda()
+    q = plan.num_queries
     if bool_mask:
         out = torch.empty((q, nb * 2048), dtype=torch.bool, device="cuda")
     else:
