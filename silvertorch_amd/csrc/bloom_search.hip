@@ -60,6 +60,7 @@ namespace {
 
 constexpr int kCensusThreads = 1024;
 constexpr int kCensusCap = 4096;  // distinct widths tracked; more stay unslotted
+constexpr int kCensusCache = 16384;  // bundle widths kept in LDS between passes
 constexpr long long kCensusEmpty = -1;
 
 __device__ __forceinline__ uint32_t census_hash(long long w) {
@@ -103,6 +104,13 @@ __global__ __launch_bounds__(kCensusThreads) void width_census_kernel(
   __shared__ uint32_t dense[kCensusCap];
   __shared__ uint32_t n_dense;
   __shared__ uint32_t cursor[kMaxWidthSlots + 1];
+  __shared__ uint32_t wcache[kCensusCache];  // widths of the first bundles
+  // Width of bundle i: from the LDS cache after the first pass (widths of
+  // 2^32 rows and more are read again).
+  auto width_of = [&](int64_t i) -> long long {
+    const uint32_t c = i < kCensusCache ? wcache[i] : 0xFFFFFFFFu;
+    return c != 0xFFFFFFFFu ? static_cast<long long>(c) : bundle_width(bbo, i);
+  };
   for (int e = threadIdx.x; e < kCensusCap; e += kCensusThreads) {
     keys[e] = kCensusEmpty;
     count[e] = 0u;
@@ -112,7 +120,9 @@ __global__ __launch_bounds__(kCensusThreads) void width_census_kernel(
   if (threadIdx.x <= kMaxWidthSlots) cursor[threadIdx.x] = 0u;
   __syncthreads();
   for (int64_t i = threadIdx.x; i < nb; i += kCensusThreads) {
-    const int e = census_find(keys, bundle_width(bbo, i), true);
+    const long long w = bundle_width(bbo, i);
+    if (i < kCensusCache) wcache[i] = w < 0xFFFFFFFFll ? static_cast<uint32_t>(w) : 0xFFFFFFFFu;
+    const int e = census_find(keys, w, true);
     if (e >= 0) atomicAdd(count + e, 1u);
   }
   __syncthreads();
@@ -137,7 +147,7 @@ __global__ __launch_bounds__(kCensusThreads) void width_census_kernel(
   if (threadIdx.x == 0) *num_slots = n < static_cast<uint32_t>(kMaxWidthSlots) ? n : kMaxWidthSlots;
   __syncthreads();
   for (int64_t i = threadIdx.x; i < nb; i += kCensusThreads) {
-    const int e = census_find(keys, bundle_width(bbo, i), false);
+    const int e = census_find(keys, width_of(i), false);
     const uint32_t sl = e >= 0 ? slot_of[e] : kNoWidthSlot;
     bundle_slot[i] = sl;
     atomicAdd(cursor + (sl == kNoWidthSlot ? kMaxWidthSlots : sl), 1u);
@@ -153,7 +163,7 @@ __global__ __launch_bounds__(kCensusThreads) void width_census_kernel(
   }
   __syncthreads();
   for (int64_t i = threadIdx.x; i < nb; i += kCensusThreads) {
-    const int e = census_find(keys, bundle_width(bbo, i), false);
+    const int e = census_find(keys, width_of(i), false);
     const uint32_t sl = e >= 0 ? slot_of[e] : kNoWidthSlot;
     const uint32_t pos = atomicAdd(cursor + (sl == kNoWidthSlot ? kMaxWidthSlots : sl), 1u);
     bundle_order[pos] = static_cast<uint32_t>(i);
