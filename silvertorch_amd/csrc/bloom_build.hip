@@ -33,7 +33,8 @@ constexpr int kScanThreads = 1024;
 constexpr int kBuildThreads = 1024;
 constexpr int kBuildTileRows = 512;
 constexpr int kBuildTileWords = kBuildTileRows * 32;
-constexpr int kBuildOffsetCap = 4096;  // int64 slot offsets staged per chunk
+constexpr int kBuildFeatureCache = 256;  // murmur_mix_x of the first feature ids, in LDS
+constexpr int kBuildValueMap = 7168;     // values of a slot group mapped to their slot in LDS
 
 // stats layout (device int64[6]):
 //   [0] total rows  [1] max bundle width  [2] non-decreasing violation flag
@@ -210,9 +211,30 @@ __device__ void scatter_term_generic(const ScatterArgs& a, bool staged,
 }
 
 template <int K>
+__device__ __forceinline__ void scatter_value(const ScatterArgs& a, bool staged,
+                                              unsigned long long* tile,
+                                              unsigned long long* gbase, const FastMod64& fm,
+                                              uint64_t mx, int64_t j, uint32_t col,
+                                              unsigned long long bit) {
+  const uint64_t my = murmur_mix_y(static_cast<uint64_t>(a.values[j]));
+  if constexpr (K > 0) {
+    scatter_term<K>(a, staged, tile, gbase, fm, mx, my, col, bit);
+  } else {
+    scatter_term_generic(a, staged, tile, gbase, fm, mx, my, col, bit);
+  }
+}
+
+// One workgroup per bundle.  The bundle's (doc, feature) slots go in groups
+// of kBuildThreads: each slot thread records its doc and feature for each of
+// its values in an LDS map, then the threads take the group's values one
+// each (all lanes hash, value loads coalesce).  A group with more values than
+// the map holds walks them per slot instead.  The seed-independent half of
+// the feature id's hash comes from LDS.
+template <int K>
 __global__ __launch_bounds__(kBuildThreads) void scatter_kernel(ScatterArgs a) {
   __shared__ unsigned long long tile[kBuildTileWords];
-  __shared__ int64_t soff[kBuildOffsetCap];
+  __shared__ uint64_t mxc[kBuildFeatureCache];
+  __shared__ uint32_t vmap[kBuildValueMap];  // doc | feature << 11 of each value
 
   const int tid = threadIdx.x;
   const int64_t bundle = blockIdx.x;
@@ -221,7 +243,11 @@ __global__ __launch_bounds__(kBuildThreads) void scatter_kernel(ScatterArgs a) {
   const bool staged = b <= kBuildTileRows;
   unsigned long long* gbase = a.index + start * 32;
   const int64_t words = b * 32;
+  const int64_t F = a.num_features;
+  const int64_t cached = min<int64_t>(F, kBuildFeatureCache);
 
+  for (int i = tid; i < cached; i += kBuildThreads)
+    mxc[i] = murmur_mix_x(static_cast<uint64_t>(static_cast<int64_t>(a.feature_ids[i])));
   if (staged) {
     for (int64_t w = tid; w < words; w += kBuildThreads) tile[w] = 0;
   } else {
@@ -234,38 +260,42 @@ __global__ __launch_bounds__(kBuildThreads) void scatter_kernel(ScatterArgs a) {
     const FastMod64 fm = make_fastmod(static_cast<uint64_t>(b));
     const int64_t doc0 = bundle * kDocsPerBundle;
     const int64_t doc1 = min(doc0 + kDocsPerBundle, a.num_docs);
-    const int64_t F = a.num_features;
-    // Slot chunks: slots [c0, c1) with their c1 - c0 + 1 offsets in LDS.
-    for (int64_t c0 = doc0 * F; c0 < doc1 * F; c0 += kBuildOffsetCap - 1) {
-      const int64_t c1 = min(c0 + kBuildOffsetCap - 1, doc1 * F);
-      const int n = static_cast<int>(c1 - c0);
-      __syncthreads();  // previous chunk's readers are done with soff
-      for (int i = tid; i <= n; i += kBuildThreads) soff[i] = a.offsets[c0 + i];
-      __syncthreads();
-      // Values outside [0, num_values) are never read (the host rejects
-      // offsets that would point there before launching).
-      const int64_t v0 = max<int64_t>(soff[0], 0);
-      const int64_t v1 = min<int64_t>(soff[n], a.num_values);
-      for (int64_t j = v0 + tid; j < v1; j += kBuildThreads) {
-        // Largest slot i with soff[i] <= j (offsets are non-decreasing).
-        int lo = 0, hi = n - 1;
-        while (lo < hi) {
-          const int mid = (lo + hi + 1) >> 1;
-          if (soff[mid] <= j) lo = mid; else hi = mid - 1;
+    const int64_t nslots = (doc1 - doc0) * F;
+    const int64_t* offs = a.offsets + doc0 * F;
+    const bool mappable = F < (1 << 21);  // doc (11 bits) and feature share a u32
+    auto mx_of = [&](int64_t f) -> uint64_t {
+      return f < cached
+                 ? mxc[f]
+                 : murmur_mix_x(static_cast<uint64_t>(static_cast<int64_t>(a.feature_ids[f])));
+    };
+    // Values outside [0, num_values) are never read (the host rejects offsets
+    // that would point there before launching).
+    auto clampv = [&](int64_t v) { return min<int64_t>(max<int64_t>(v, 0), a.num_values); };
+    for (int64_t g = 0; g < nslots; g += kBuildThreads) {
+      const int64_t rel = g + tid;
+      const bool has_slot = rel < nslots;
+      const int64_t v0 = has_slot ? clampv(offs[rel]) : 0;
+      const int64_t v1 = has_slot ? clampv(offs[rel + 1]) : 0;
+      const int64_t d = has_slot ? rel / F : 0;
+      const int64_t f = has_slot ? rel - d * F : 0;
+      const int64_t gv0 = clampv(offs[g]);
+      const int64_t gv1 = clampv(offs[min<int64_t>(g + kBuildThreads, nslots)]);
+      if (mappable && gv1 - gv0 <= kBuildValueMap) {  // uniform across the workgroup
+        __syncthreads();  // previous group's readers are done with vmap
+        for (int64_t j = v0; j < v1; ++j)
+          vmap[j - gv0] = static_cast<uint32_t>(d) | (static_cast<uint32_t>(f) << 11);
+        __syncthreads();
+        for (int64_t j = gv0 + tid; j < gv1; j += kBuildThreads) {
+          const uint32_t m = vmap[j - gv0];
+          const uint32_t dd = m & 2047u;
+          scatter_value<K>(a, staged, tile, gbase, fm, mx_of(m >> 11), j, dd >> 6,
+                           1ull << (63 - (dd & 63)));
         }
-        const int64_t slot = c0 + lo;
-        const int64_t doc = slot / F;
-        const int64_t f = slot - doc * F;
-        const int64_t in_bundle = doc - doc0;
-        const uint32_t col = static_cast<uint32_t>(in_bundle >> 6);
-        const unsigned long long bit = 1ull << (63 - (in_bundle & 63));
-        const uint64_t mx = murmur_mix_x(static_cast<uint64_t>(static_cast<int64_t>(a.feature_ids[f])));
-        const uint64_t my = murmur_mix_y(static_cast<uint64_t>(a.values[j]));
-        if constexpr (K > 0) {
-          scatter_term<K>(a, staged, tile, gbase, fm, mx, my, col, bit);
-        } else {
-          scatter_term_generic(a, staged, tile, gbase, fm, mx, my, col, bit);
-        }
+      } else if (v0 < v1) {
+        const uint64_t mx = mx_of(f);
+        for (int64_t j = v0; j < v1; ++j)
+          scatter_value<K>(a, staged, tile, gbase, fm, mx, j, static_cast<uint32_t>(d >> 6),
+                           1ull << (63 - (d & 63)));
       }
     }
   }
