@@ -213,6 +213,9 @@ __global__ void bind_fill_kernel(const uint32_t* __restrict__ tmpl,
   } else if (c == kTmplOnes) {
     v = b <= kSearchTileRows ? static_cast<uint32_t>(kSearchOnesRow) * 256u
                              : static_cast<uint32_t>(kPosOnes);
+  } else if (c == kTmplZeros) {
+    v = b <= kSearchTileRows ? static_cast<uint32_t>(kSearchZerosRow) * 256u
+                             : static_cast<uint32_t>(kPosZeros);
   } else {
     const uint32_t t = (c >> 4) - 1u;
     v = device_term_position(hashes + static_cast<uint64_t>(t) * hash_k, hash_k, k_eff, b,
@@ -270,7 +273,9 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
         bound ? at(plan->off_bundle_slot) : nullptr,
         bound ? at(plan->off_bundle_order) : nullptr,
         bound ? at(bt.off_bound_start) : nullptr, bound ? at(bt.off_bound) : nullptr,
-        bound ? bt.bound_words : 0u, bt.num_terms, static_cast<int32_t>(plan->hash_k),
+        bound ? bt.bound_words : 0u, bound ? at(bt.off_stream_wave) : nullptr,
+        bound ? at(bt.off_stream_skip) : nullptr, bound ? bt.stream_off : 0u,
+        bound ? bt.stream_words : 0u, bt.num_terms, static_cast<int32_t>(plan->hash_k),
         num_bundles * 32, out, counts, num_docs);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)

@@ -46,6 +46,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // counter with the next bundle's tile prefetch, and waiting for it would wait
 // for the whole prefetch.
 #define ST_CONST __attribute__((address_space(4)))
+// Output stores go through the global address space explicitly (a pointer
+// rebuilt from an integer would otherwise be a flat pointer, and flat stores
+// also count against the LDS wait counter).
+#define ST_GLOBAL __attribute__((address_space(1)))
 template <typename T>
 __device__ __forceinline__ const ST_CONST T* as_const(const T* p) {
   return (const ST_CONST T*)(p);  // addrspacecast: only a C-style cast spells it
@@ -68,6 +72,8 @@ struct SearchArgs {
   const ST_CONST uint32_t* bound_start;
   const ST_CONST uint32_t* bound;
   uint32_t bound_words;
+  uint32_t stream_off;                    // literal stream within a width block
+  uint32_t stream_words;                  // 0: no stream
   uint32_t num_terms;
   int32_t hash_k;
   int64_t out_cols;  // columns per output row = num_bundles * 32
@@ -140,12 +146,12 @@ __device__ __forceinline__ int resolve_positions(const ST_CONST uint64_t* h, int
 
 // Expands a 32-bit match half into 32 bool bytes, most significant bit
 // first (the doc order of bloom_index_search.cpp:231-236).
-__device__ __forceinline__ void store_bool32(uint8_t* dst, uint32_t bits) {
+__device__ __forceinline__ void store_bool32(ST_GLOBAL char* dst, uint32_t bits) {
   const uint32_t y = __builtin_bitreverse32(bits);
   uint32_t w[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) w[j] = (((y >> (4 * j)) & 0xFu) * 0x00204081u) & 0x01010101u;
-  u32x4* d = reinterpret_cast<u32x4*>(dst);
+  ST_GLOBAL u32x4* d = (ST_GLOBAL u32x4*)(dst);
   __builtin_nontemporal_store(u32x4{w[0], w[1], w[2], w[3]}, d);
   __builtin_nontemporal_store(u32x4{w[4], w[5], w[6], w[7]}, d + 1);
 }
@@ -528,6 +534,120 @@ __device__ __forceinline__ uint32_t eval_bound_stack(const RowSource& rs, const 
   return acc;
 }
 
+// Where a wave stores its results on one bundle: a per-lane byte offset
+// (constant over the bundle) plus a uniform base per output row, so the
+// address math of a store is scalar.
+struct OutCursor {
+  char* base;            // output byte address of row 0 on this bundle
+  int64_t row_bytes;     // bytes per output row
+  uint32_t lane_off;     // this lane's byte offset within its row's slice
+  uint32_t count_mask;   // kOutCounts: docs of this lane that count
+};
+
+template <int kOut>
+__device__ __forceinline__ OutCursor out_cursor(const SearchArgs& a, int lane, int64_t bundle) {
+  OutCursor c;
+  if constexpr (kOut == kOutBool) {
+    // doc 64c + i at byte 64c + i; the lane's u32 holds docs 0-31 (odd
+    // lanes) or 32-63 (even lanes) of column lane >> 1
+    c.base = static_cast<char*>(a.out) + bundle * kDocsPerBundle;
+    c.row_bytes = a.out_cols * 64;
+    c.lane_off = static_cast<uint32_t>((lane >> 1) * 64 + ((lane & 1) ? 0 : 32));
+  } else {
+    c.base = static_cast<char*>(a.out) + bundle * 256;
+    c.row_bytes = a.out_cols * 8;
+    c.lane_off = static_cast<uint32_t>(lane) * 4u;
+  }
+  c.count_mask = 0u;
+  if constexpr (kOut == kOutCounts) {
+    // The lane's u32 is half (lane & 1) of little-endian word lane >> 1: odd
+    // lanes hold the word's high half (docs 0-31), even lanes docs 32-63.
+    const int64_t first_doc =
+        bundle * kDocsPerBundle + (lane >> 1) * kBitsPerColumn + ((lane & 1) ? 0 : 32);
+    c.count_mask = valid_doc_mask(first_doc, a.num_docs);
+  }
+  return c;
+}
+
+// Stores this lane's 32-bit half of output row `row` on the bundle (and the
+// row's match count on the bundle in kOutCounts mode).
+template <int kOut>
+__device__ __forceinline__ void store_result(const SearchArgs& a, const OutCursor& c, int lane,
+                                             int64_t bundle, uint32_t row, uint32_t acc) {
+  // The row's base is computed in scalar registers and kept there (the empty
+  // asm), so the store takes the scalar-base + per-lane-offset form.
+  const uint64_t addr = reinterpret_cast<uint64_t>(c.base) +
+                        static_cast<uint64_t>(row) * static_cast<uint64_t>(c.row_bytes);
+  uint32_t lo = static_cast<uint32_t>(addr), hi = static_cast<uint32_t>(addr >> 32);
+  asm volatile("" : "+s"(lo), "+s"(hi));
+  ST_GLOBAL char* row_base = (ST_GLOBAL char*)((static_cast<uint64_t>(hi) << 32) | lo);
+  if constexpr (kOut == kOutBool) {
+    store_bool32(row_base + c.lane_off, acc);
+  } else {
+    __builtin_nontemporal_store(acc, (ST_GLOBAL uint32_t*)(row_base + c.lane_off));
+  }
+  if constexpr (kOut == kOutCounts) {
+    const uint32_t n = wave_total_small(static_cast<uint32_t>(__builtin_popcount(acc & c.count_mask)));
+    if (lane == 0) a.counts[static_cast<int64_t>(row) * a.num_bundles + bundle] = n;
+  }
+}
+
+// Evaluates a wave's run of literal records [r_begin, r_end): each block of
+// records arrives with scalar loads (the run is the same for every bundle of
+// a width, so it stays in the scalar cache), then all the block's row words
+// are read from the tile, then the OR-of-ANDs fold runs, storing a query's
+// result after its last literal.  No per-query decoding.
+template <int K, bool STAGED, int kOut>
+__device__ __forceinline__ void eval_stream(const SearchArgs& a, const RowSource& rs,
+                                            const ST_CONST uint32_t* stream, uint32_t r_begin,
+                                            uint32_t r_end, int64_t bundle) {
+  constexpr int RW = ((K + 1 + 3) / 4) * 4;
+  constexpr int NB = 32 / RW;  // records per block
+  const OutCursor oc = out_cursor<kOut>(a, rs.lane, bundle);
+  auto load_block = [&](uint32_t r, uint32_t (&rec)[NB][K + 1]) {
+    const ST_CONST uint32_t* blk = stream + r * RW;
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int v = 0; v <= K; ++v) rec[j][v] = blk[j * RW + v];
+  };
+  uint32_t res = 0, acc = 0;
+  uint32_t rec[NB][K + 1];
+  if (r_begin < r_end) load_block(r_begin, rec);
+  for (uint32_t r = r_begin; r < r_end; r += NB) {
+    uint32_t w[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      uint32_t t = ~0u;
+#pragma unroll
+      for (int k = 0; k < K; ++k) t &= row_word<STAGED>(rs, rec[j][k]);
+      w[j] = t;
+    }
+    // the next block's records load while this block's rows are read
+    uint32_t nxt[NB][K + 1];
+    load_block(r + NB < r_end ? r + NB : r, nxt);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const uint32_t f = rec[j][K];
+      const uint32_t neg = 0u - (f & kStreamNeg);
+      const uint32_t grp = 0u - ((f >> 1) & 1u);
+      res |= acc & grp;
+      acc = (acc | grp) & (w[j] ^ neg);
+      if (f & kStreamLast) {
+        uint32_t v = res | acc;
+        if (f & kStreamComplement) v = ~v;
+        store_result<kOut>(a, oc, rs.lane, bundle, f >> kStreamRowShift, v);
+        res = 0;
+        acc = 0;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int v = 0; v <= K; ++v) rec[j][v] = nxt[j][v];
+  }
+}
+
 // Evaluates this wave's queries [s_begin, s_end) on one bundle and stores
 // their 32-bit halves of the bundle's 32 output words.
 template <int K, int KP, bool STAGED, bool BOUND, int G, int kOut>
@@ -535,28 +655,9 @@ __device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSourc
                                              uint32_t s_begin, uint32_t s_end,
                                              int64_t bundle, uint32_t slot) {
   const int lane = rs.lane;
-  uint32_t count_mask = 0u;
-  if constexpr (kOut == kOutCounts) {
-    // The lane's u32 is half (lane & 1) of little-endian word lane >> 1: odd
-    // lanes hold the word's high half (docs 0-31), even lanes docs 32-63.
-    const int64_t first_doc =
-        bundle * kDocsPerBundle + (lane >> 1) * kBitsPerColumn + ((lane & 1) ? 0 : 32);
-    count_mask = valid_doc_mask(first_doc, a.num_docs);
-  }
+  const OutCursor oc = out_cursor<kOut>(a, lane, bundle);
   auto store = [&](uint32_t row, uint32_t acc) {
-    const int64_t col0 = static_cast<int64_t>(row) * a.out_cols + bundle * 32;
-    if constexpr (kOut == kOutBool) {
-      uint8_t* dst = static_cast<uint8_t*>(a.out) + (col0 + (lane >> 1)) * 64 +
-                     ((lane & 1) ? 0 : 32);
-      store_bool32(dst, acc);
-    } else {
-      uint32_t* dst = static_cast<uint32_t*>(a.out) + col0 * 2 + lane;
-      __builtin_nontemporal_store(acc, dst);
-    }
-    if constexpr (kOut == kOutCounts) {
-      const uint32_t c = wave_total_small(static_cast<uint32_t>(__builtin_popcount(acc & count_mask)));
-      if (lane == 0) a.counts[static_cast<int64_t>(row) * a.num_bundles + bundle] = c;
-    }
+    store_result<kOut>(a, oc, lane, bundle, row, acc);
   };
   if constexpr (BOUND) {
     constexpr int RW = ((K + 1 + 3) / 4) * 4;
@@ -624,7 +725,9 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     const uint64_t* __restrict__ hashes, const uint32_t* __restrict__ bundle_slot,
     const uint32_t* __restrict__ bundle_order,
     const uint32_t* __restrict__ bound_start, const uint32_t* __restrict__ bound,
-    uint32_t bound_words, uint32_t num_terms, int32_t hash_k,
+    uint32_t bound_words, const uint32_t* __restrict__ stream_wave,
+    const uint32_t* __restrict__ stream_skip, uint32_t stream_off, uint32_t stream_words,
+    uint32_t num_terms, int32_t hash_k,
     int64_t out_cols, void* __restrict__ out, int64_t* __restrict__ counts, int64_t num_docs) {
   SearchArgs a;
   a.index = index;
@@ -640,6 +743,8 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
   a.bound_start = as_const(bound_start);
   a.bound = as_const(bound);
   a.bound_words = bound_words;
+  a.stream_off = stream_off;
+  a.stream_words = stream_words;
   a.num_terms = num_terms;
   a.hash_k = hash_k;
   a.out_cols = out_cols;
@@ -649,7 +754,7 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
   constexpr int KP = K <= 4 ? 4 : (K <= 8 ? 8 : 12);
   constexpr int G = KP == 4 ? 4 : (KP == 8 ? 2 : 1);  // terms fetched together
   __shared__ u32x4 tile[(kSearchTileRows + 2) * 16];
-  __shared__ uint32_t pos[kSearchPosSlots];
+  __shared__ __attribute__((aligned(16))) uint32_t pos[kSearchPosSlots];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -667,9 +772,14 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
   u32x4 pre[kPrefetch];
   if (blockIdx.x < a.num_bundles) prefetch_tile(a, bundle_at(blockIdx.x), pre);
 
-  int64_t prev_b = -1;
+  int64_t prev_b = -1;  // width whose term positions are in pos
   const uint32_t s_begin = uniform(a.wave_off[wave]);
   const uint32_t s_end = uniform(a.wave_off[wave + 1]);
+  const bool streamed = a.stream_words != 0;
+  const uint32_t r_begin = streamed ? uniform(stream_wave[wave]) : 0u;
+  const uint32_t r_end = streamed ? uniform(stream_wave[wave + 1]) : 0u;
+  // the flat programs the stream covers are the wave's first ones
+  const uint32_t s_rest = s_begin + (streamed ? uniform(stream_skip[wave]) : 0u);
   const char* tile_lane = reinterpret_cast<const char*>(tile) + lane * 4;
   const uint32_t* index32 = reinterpret_cast<const uint32_t*>(a.index);
 
@@ -729,10 +839,14 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     rs.lane = lane;
     rs.staged = staged;
     if (slot != kNoWidthSlot) {
+      const ST_CONST uint32_t* stream =
+          a.bound + static_cast<uint64_t>(slot) * a.bound_words + a.stream_off;
       if (staged) {
-        eval_queries<K, KP, true, true, G, kOut>(a, rs, s_begin, s_end, bundle, slot);
+        if (streamed) eval_stream<K, true, kOut>(a, rs, stream, r_begin, r_end, bundle);
+        eval_queries<K, KP, true, true, G, kOut>(a, rs, s_rest, s_end, bundle, slot);
       } else {
-        eval_queries<K, KP, false, true, G, kOut>(a, rs, s_begin, s_end, bundle, slot);
+        if (streamed) eval_stream<K, false, kOut>(a, rs, stream, r_begin, r_end, bundle);
+        eval_queries<K, KP, false, true, G, kOut>(a, rs, s_rest, s_end, bundle, slot);
       }
     } else if (staged) {
       eval_queries<K, KP, true, false, G, kOut>(a, rs, s_begin, s_end, bundle, slot);
@@ -748,6 +862,7 @@ using KernelFn = void (*)(const int64_t*, int64_t, const int64_t*, int64_t,
                           const uint32_t*, const uint32_t*,
                           const uint32_t*, const uint64_t*, const uint32_t*,
                           const uint32_t*, const uint32_t*, const uint32_t*, uint32_t,
+                          const uint32_t*, const uint32_t*, uint32_t, uint32_t,
                           uint32_t, int32_t,
                           int64_t, void*, int64_t*, int64_t);
 

@@ -749,6 +749,162 @@ void term_positions(const uint64_t* h, int64_t hash_k, int k_eff, int64_t b,
 }  // namespace
 }  // namespace st
 
+namespace st {
+namespace {
+
+uint64_t align_to(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+
+// Template of one batch's width block: every bound program (the layout the
+// kernel's per-query loop reads), then the batch's literal stream (absent
+// only when an output row does not fit a record's row field).  Each position word is a code (term,
+// position index) resolved at each slot width, on the host
+// (st_search_plan_bind_widths) or on the device.  Sets bt.stream_off and
+// bt.stream_words; wave_rec / wave_skip receive the per-wave stream tables
+// (all zero without a stream).
+void build_block_template(const st_search_plan& plan, SearchBatch& bt,
+                          const std::vector<uint32_t>& insns,
+                          const std::vector<uint32_t>& starts, std::vector<uint32_t>& bstart,
+                          std::vector<uint32_t>& tmpl, std::vector<uint32_t>& code,
+                          std::vector<uint32_t>& wave_rec, std::vector<uint32_t>& wave_skip) {
+  const int k_eff = plan.k_eff, kp = plan.kp, rw = bound_record_words(k_eff);
+  const uint32_t pos_bytes = static_cast<uint32_t>(kp) * 4;
+  std::vector<uint32_t> bound_T(bt.num_slots);
+  for (uint32_t q = 0; q < bt.num_slots; ++q) bound_T[q] = insns[starts[q]] & 0xFFFFu;
+  for (uint32_t q = 0; q + 1 < bt.num_slots; ++q) {
+    if (insns[starts[q]] & kPairedWithNext) {
+      const uint32_t t = std::max(bound_T[q], bound_T[q + 1]);
+      bound_T[q] = bound_T[q + 1] = t;
+    }
+  }
+  bstart.assign(bt.num_slots, 0);
+  uint32_t words = 0;
+  for (uint32_t q = 0; q < bt.num_slots; ++q) {
+    bstart[q] = words;
+    const uint32_t hdr = insns[starts[q]];
+    uint32_t n = kProgHeaderWords;
+    n += (hdr & kFlatForm) ? bound_T[q] * rw : (hdr & 0xFFFFu) * kp + insns[starts[q] + 2];
+    words += (n + 3) & ~3u;
+  }
+  tmpl.assign(words, 0u);
+  code.assign(words, kTmplCopy);
+  for (uint32_t q = 0; q < bt.num_slots; ++q) {
+    const uint32_t* src = insns.data() + starts[q];
+    uint32_t* dst = tmpl.data() + bstart[q];
+    uint32_t* dc = code.data() + bstart[q];
+    const uint32_t hdr = src[0];
+    const uint32_t T = hdr & 0xFFFFu;
+    for (int w = 0; w < kProgHeaderWords; ++w) dst[w] = src[w];
+    if (hdr & kFlatForm) {
+      dst[0] = (hdr & ~0xFFFFu) | bound_T[q];
+      for (uint32_t j = 0; j < T; ++j) {
+        const uint32_t* lit = src + kProgHeaderWords + j * kFlatLiteralWords;
+        const uint32_t term = lit[0] / pos_bytes;
+        const uint32_t at = kProgHeaderWords + j * rw;
+        for (int r = 0; r < k_eff; ++r) dc[at + r] = tmpl_position_code(term, r);
+        dst[at + k_eff] = (lit[1] ? 1u : 0u) | (lit[2] ? 2u : 0u);
+      }
+      for (uint32_t j = T; j < bound_T[q]; ++j) {  // no-op padding records
+        const uint32_t at = kProgHeaderWords + j * rw;
+        for (int r = 0; r < k_eff; ++r) dc[at + r] = kTmplOnes;
+        dst[at + k_eff] = 0u;
+      }
+    } else {
+      const uint32_t nops = src[2];
+      for (uint32_t j = 0; j < T; ++j) {
+        const uint32_t term = src[kProgHeaderWords + j] / pos_bytes;
+        for (int r = 0; r < kp; ++r)
+          dc[kProgHeaderWords + j * kp + r] = tmpl_position_code(term, r);
+      }
+      for (uint32_t o = 0; o < nops; ++o)
+        dst[kProgHeaderWords + T * kp + o] = src[kProgHeaderWords + T + o];
+    }
+  }
+
+  // Literal stream: per wave, its leading flat programs as one run of
+  // records, padded to whole blocks.  Records follow the kernel's K, which
+  // is 1 when no position resolves (k_eff 0: no term literals then).
+  const uint32_t* wave_off = reinterpret_cast<const uint32_t*>(plan.blob.data() + bt.off_wave);
+  const int ks = std::max(k_eff, 1);
+  const int srw = bound_record_words(ks);
+  const uint32_t per_block = static_cast<uint32_t>(stream_block_records(ks));
+  wave_rec.assign(kSearchWaves + 1, 0u);
+  wave_skip.assign(kSearchWaves, 0u);
+  bt.stream_off = static_cast<uint32_t>(tmpl.size());
+  bt.stream_words = 0;
+  uint32_t recs = 0;
+  bool fits = true;
+  auto record = [&](uint32_t pos_code, uint32_t term, uint32_t flags) {
+    const size_t at = tmpl.size();
+    tmpl.resize(at + srw, 0u);
+    code.resize(at + srw, kTmplCopy);
+    for (int r = 0; r < ks; ++r)
+      code[at + r] = pos_code == kTmplCopy ? tmpl_position_code(term, r) : pos_code;
+    tmpl[at + ks] = flags;
+    ++recs;
+  };
+  for (int w = 0; w < kSearchWaves && fits; ++w) {
+    wave_rec[w] = recs;
+    for (uint32_t q = wave_off[w]; q < wave_off[w + 1]; ++q) {
+      const uint32_t* src = insns.data() + starts[q];
+      const uint32_t hdr = src[0];
+      if (!(hdr & kFlatForm)) break;  // flat programs lead each wave's list
+      const uint32_t row = src[1];
+      if (static_cast<int64_t>(row) >= kStreamMaxRows) {
+        fits = false;
+        break;
+      }
+      const uint32_t T = hdr & 0xFFFFu;
+      const uint32_t last = kStreamLast | (row << kStreamRowShift) |
+                            ((hdr & kFlatComplement) ? kStreamComplement : 0u);
+      if (T == 0) record(kTmplZeros, 0, kStreamFirst | last);
+      for (uint32_t j = 0; j < T; ++j) {
+        const uint32_t* lit = src + kProgHeaderWords + j * kFlatLiteralWords;
+        record(kTmplCopy, lit[0] / pos_bytes,
+               (lit[1] ? kStreamNeg : 0u) | (lit[2] ? kStreamFirst : 0u) |
+                   (j + 1 == T ? last : 0u));
+      }
+      ++wave_skip[w];
+    }
+    while (recs % per_block) record(kTmplOnes, 0, 0u);
+  }
+  wave_rec[kSearchWaves] = recs;
+  if (fits && recs > 0) {
+    bt.stream_words = recs * static_cast<uint32_t>(srw);
+  } else {  // no stream: every program runs from the width block
+    tmpl.resize(bt.stream_off);
+    code.resize(bt.stream_off);
+    bt.stream_off = 0;
+    wave_rec.assign(kSearchWaves + 1, 0u);
+    wave_skip.assign(kSearchWaves, 0u);
+  }
+}
+
+// Width block of one slot from the batch's template; spos holds the kp
+// positions of every batch term at the slot's width.
+void expand_block(const std::vector<uint32_t>& tmpl, const std::vector<uint32_t>& code,
+                  const uint32_t* spos, int kp, int64_t width, uint32_t* out) {
+  const bool staged = width <= kSearchTileRows;
+  const uint32_t ones = staged ? static_cast<uint32_t>(kSearchOnesRow) * 256u
+                               : static_cast<uint32_t>(kPosOnes);
+  const uint32_t zeros = staged ? static_cast<uint32_t>(kSearchZerosRow) * 256u
+                                : static_cast<uint32_t>(kPosZeros);
+  for (size_t i = 0; i < tmpl.size(); ++i) {
+    const uint32_t c = code[i];
+    if (c == kTmplCopy) {
+      out[i] = tmpl[i];
+    } else if (c == kTmplOnes) {
+      out[i] = ones;
+    } else if (c == kTmplZeros) {
+      out[i] = zeros;
+    } else {
+      out[i] = spos[static_cast<size_t>((c >> 4) - 1u) * kp + (c & 15u)];
+    }
+  }
+}
+
+}  // namespace
+}  // namespace st
+
 extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
                                           const int64_t* bundle_b_offsets,
                                           int64_t num_bundles) {
@@ -761,8 +917,6 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
              "bundle_b_offsets is null");
     const int k_eff = plan->k_eff;
     const int kp = plan->kp;
-    const int rw = bound_record_words(k_eff);
-    const uint32_t pos_bytes = static_cast<uint32_t>(kp) * 4;
 
     // Most frequent widths get slots (ties to the smaller width).  Census in
     // an open-addressed table keyed by width (few distinct widths).
@@ -835,7 +989,7 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
       const auto& starts = plan->batch_starts[bi];
       const auto& hashes = plan->batch_hashes[bi];
       // positions of every term at every slot width
-      static thread_local std::vector<uint32_t> pos, bound_T, bstart;
+      static thread_local std::vector<uint32_t> pos;
       pos.resize(nslots * bt.num_terms * kp);
       for (size_t s = 0; s < nslots; ++s) {
         const FastMod64 fm = make_fastmod(static_cast<uint64_t>(plan->slot_width[s]));
@@ -844,76 +998,23 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
                          plan->hash_k, k_eff, plan->slot_width[s], fm, kp,
                          &pos[(s * bt.num_terms + u) * kp]);
       }
-      // Literal count of each bound program: paired flat programs are padded
-      // to the larger count of the pair.
-      bound_T.resize(bt.num_slots);
-      for (uint32_t q = 0; q < bt.num_slots; ++q) bound_T[q] = insns[starts[q]] & 0xFFFFu;
-      for (uint32_t q = 0; q + 1 < bt.num_slots; ++q) {
-        if (insns[starts[q]] & kPairedWithNext) {
-          const uint32_t t = std::max(bound_T[q], bound_T[q + 1]);
-          bound_T[q] = bound_T[q + 1] = t;
-        }
-      }
-      // layout of one width block (identical for every slot)
-      bstart.resize(bt.num_slots);
-      uint32_t words = 0;
-      for (uint32_t q = 0; q < bt.num_slots; ++q) {
-        bstart[q] = words;
-        const uint32_t hdr = insns[starts[q]];
-        const uint32_t T = hdr & 0xFFFFu;
-        uint32_t n = kProgHeaderWords;
-        if (hdr & kFlatForm) {
-          n += bound_T[q] * rw;
-        } else {
-          n += T * kp + insns[starts[q] + 2];
-        }
-        words += (n + 3) & ~3u;
-      }
+      static thread_local std::vector<uint32_t> bstart, tmpl, code, wave_rec, wave_skip;
+      build_block_template(*plan, bt, insns, starts, bstart, tmpl, code, wave_rec, wave_skip);
+      const uint32_t words = static_cast<uint32_t>(tmpl.size());
       bt.bound_words = words;
       bt.off_bound_start = blob.size();
       append_bytes(blob, bstart.data(), bstart.size() * 4);
+      bt.off_stream_wave = blob.size();
+      append_bytes(blob, wave_rec.data(), wave_rec.size() * 4);
+      bt.off_stream_skip = blob.size();
+      append_bytes(blob, wave_skip.data(), wave_skip.size() * 4);
       // The width blocks are written in place at the end of the blob.
       bt.off_bound = blob.size();
       blob.resize(blob.size() + nslots * words * 4, 0);
       uint32_t* block = reinterpret_cast<uint32_t*>(blob.data() + bt.off_bound);
-      for (size_t s = 0; s < nslots; ++s) {
-        uint32_t* base = block + s * words;
-        const uint32_t* spos = pos.data() + s * bt.num_terms * kp;
-        for (uint32_t q = 0; q < bt.num_slots; ++q) {
-          const uint32_t* src = insns.data() + starts[q];
-          uint32_t* dst = base + bstart[q];
-          const uint32_t hdr = src[0];
-          const uint32_t T = hdr & 0xFFFFu;
-          for (int w = 0; w < kProgHeaderWords; ++w) dst[w] = src[w];
-          if (hdr & kFlatForm) {
-            dst[0] = (hdr & ~0xFFFFu) | bound_T[q];
-            for (uint32_t j = 0; j < T; ++j) {
-              const uint32_t* lit = src + kProgHeaderWords + j * kFlatLiteralWords;
-              const uint32_t* tp = spos + (lit[0] / pos_bytes) * kp;
-              uint32_t* rec = dst + kProgHeaderWords + j * rw;
-              for (int r = 0; r < k_eff; ++r) rec[r] = tp[r];
-              rec[k_eff] = (lit[1] ? 1u : 0u) | (lit[2] ? 2u : 0u);
-            }
-            // no-op padding: AND with the all-ones row inside the last group
-            const bool staged = plan->slot_width[s] <= kSearchTileRows;
-            const uint32_t ones = staged ? static_cast<uint32_t>(kSearchOnesRow) * 256u
-                                         : static_cast<uint32_t>(kPosOnes);
-            for (uint32_t j = T; j < bound_T[q]; ++j) {
-              uint32_t* rec = dst + kProgHeaderWords + j * rw;
-              for (int r = 0; r < k_eff; ++r) rec[r] = ones;
-              rec[k_eff] = 0;
-            }
-          } else {
-            const uint32_t nops = src[2];
-            for (uint32_t j = 0; j < T; ++j) {
-              const uint32_t* tp = spos + (src[kProgHeaderWords + j] / pos_bytes) * kp;
-              for (int r = 0; r < kp; ++r) dst[kProgHeaderWords + j * kp + r] = tp[r];
-            }
-            for (uint32_t o = 0; o < nops; ++o)
-              dst[kProgHeaderWords + T * kp + o] = src[kProgHeaderWords + T + o];
-          }
-        }
-      }
+      for (size_t s = 0; s < nslots; ++s)
+        expand_block(tmpl, code, pos.data() + s * bt.num_terms * kp, kp, plan->slot_width[s],
+                     block + s * words);
     }
     // Scalar loads may read a few words past the last program.
     blob.resize(blob.size() + 256, 0);
@@ -921,75 +1022,6 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
   });
 }
 
-namespace st {
-namespace {
-
-uint64_t align_to(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
-
-// Template of one batch's width block: the layout of st_search_plan_bind_widths
-// with every position word replaced by a code (term, position index) that the
-// device resolves at each slot width.
-void build_block_template(const st_search_plan& plan, const SearchBatch& bt,
-                          const std::vector<uint32_t>& insns,
-                          const std::vector<uint32_t>& starts, std::vector<uint32_t>& bstart,
-                          std::vector<uint32_t>& tmpl, std::vector<uint32_t>& code) {
-  const int k_eff = plan.k_eff, kp = plan.kp, rw = bound_record_words(k_eff);
-  const uint32_t pos_bytes = static_cast<uint32_t>(kp) * 4;
-  std::vector<uint32_t> bound_T(bt.num_slots);
-  for (uint32_t q = 0; q < bt.num_slots; ++q) bound_T[q] = insns[starts[q]] & 0xFFFFu;
-  for (uint32_t q = 0; q + 1 < bt.num_slots; ++q) {
-    if (insns[starts[q]] & kPairedWithNext) {
-      const uint32_t t = std::max(bound_T[q], bound_T[q + 1]);
-      bound_T[q] = bound_T[q + 1] = t;
-    }
-  }
-  bstart.assign(bt.num_slots, 0);
-  uint32_t words = 0;
-  for (uint32_t q = 0; q < bt.num_slots; ++q) {
-    bstart[q] = words;
-    const uint32_t hdr = insns[starts[q]];
-    uint32_t n = kProgHeaderWords;
-    n += (hdr & kFlatForm) ? bound_T[q] * rw : (hdr & 0xFFFFu) * kp + insns[starts[q] + 2];
-    words += (n + 3) & ~3u;
-  }
-  tmpl.assign(words, 0u);
-  code.assign(words, kTmplCopy);
-  for (uint32_t q = 0; q < bt.num_slots; ++q) {
-    const uint32_t* src = insns.data() + starts[q];
-    uint32_t* dst = tmpl.data() + bstart[q];
-    uint32_t* dc = code.data() + bstart[q];
-    const uint32_t hdr = src[0];
-    const uint32_t T = hdr & 0xFFFFu;
-    for (int w = 0; w < kProgHeaderWords; ++w) dst[w] = src[w];
-    if (hdr & kFlatForm) {
-      dst[0] = (hdr & ~0xFFFFu) | bound_T[q];
-      for (uint32_t j = 0; j < T; ++j) {
-        const uint32_t* lit = src + kProgHeaderWords + j * kFlatLiteralWords;
-        const uint32_t term = lit[0] / pos_bytes;
-        const uint32_t at = kProgHeaderWords + j * rw;
-        for (int r = 0; r < k_eff; ++r) dc[at + r] = tmpl_position_code(term, r);
-        dst[at + k_eff] = (lit[1] ? 1u : 0u) | (lit[2] ? 2u : 0u);
-      }
-      for (uint32_t j = T; j < bound_T[q]; ++j) {  // no-op padding records
-        const uint32_t at = kProgHeaderWords + j * rw;
-        for (int r = 0; r < k_eff; ++r) dc[at + r] = kTmplOnes;
-        dst[at + k_eff] = 0u;
-      }
-    } else {
-      const uint32_t nops = src[2];
-      for (uint32_t j = 0; j < T; ++j) {
-        const uint32_t term = src[kProgHeaderWords + j] / pos_bytes;
-        for (int r = 0; r < kp; ++r)
-          dc[kProgHeaderWords + j * kp + r] = tmpl_position_code(term, r);
-      }
-      for (uint32_t o = 0; o < nops; ++o)
-        dst[kProgHeaderWords + T * kp + o] = src[kProgHeaderWords + T + o];
-    }
-  }
-}
-
-}  // namespace
-}  // namespace st
 
 extern "C" int st_search_plan_prepare_device_binding(st_search_plan* plan,
                                                      int64_t num_bundles) {
@@ -999,14 +1031,18 @@ extern "C" int st_search_plan_prepare_device_binding(st_search_plan* plan,
     ST_CHECK(plan->bound_bundles < 0, "plan is already bound to bundle widths");
     ST_CHECK(num_bundles >= 0, "negative bundle count");
     auto& blob = plan->blob;
-    std::vector<uint32_t> bstart, tmpl, code;
+    std::vector<uint32_t> bstart, tmpl, code, wave_rec, wave_skip;
     for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
       SearchBatch& bt = plan->batches[bi];
       build_block_template(*plan, bt, plan->batch_insns[bi], plan->batch_starts[bi], bstart,
-                           tmpl, code);
+                           tmpl, code, wave_rec, wave_skip);
       bt.bound_words = static_cast<uint32_t>(tmpl.size());
       bt.off_bound_start = blob.size();
       append_bytes(blob, bstart.data(), bstart.size() * 4);
+      bt.off_stream_wave = blob.size();
+      append_bytes(blob, wave_rec.data(), wave_rec.size() * 4);
+      bt.off_stream_skip = blob.size();
+      append_bytes(blob, wave_skip.data(), wave_skip.size() * 4);
       bt.off_tmpl = blob.size();
       append_bytes(blob, tmpl.data(), tmpl.size() * 4);
       bt.off_tmpl_code = blob.size();

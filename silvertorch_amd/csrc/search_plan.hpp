@@ -102,6 +102,26 @@ constexpr uint32_t kNoWidthSlot = 0xFFFFFFFFu;
 
 inline int bound_record_words(int k_eff) { return ((k_eff + 1 + 3) / 4) * 4; }
 
+// Literal stream.  Every width block also carries the batch's flat programs
+// as one run of literal records per wave, which the kernel reads with scalar
+// loads and evaluates in blocks, without per-query decoding.  A record has
+// bound_record_words(K) words: [row position 0 .. K-1, flags, pad...],
+// flags bit 0 = negate,
+// bit 1 = first of its group, bit 2 = last literal of its query (the result
+// is stored after it), bit 3 = complement the result, bits 4..31 = the
+// query's output row.  A query with no literal is one record on the all-zeros
+// row.  Each wave's run is padded to a whole number of blocks with no-op
+// records (all-ones row, flags 0).  The flat programs a wave's run covers are
+// its first ones; the rest are evaluated from the width block.
+constexpr uint32_t kStreamNeg = 1u;
+constexpr uint32_t kStreamFirst = 2u;
+constexpr uint32_t kStreamLast = 4u;
+constexpr uint32_t kStreamComplement = 8u;
+constexpr int kStreamRowShift = 4;
+constexpr int64_t kStreamMaxRows = int64_t{1} << (32 - kStreamRowShift);
+// Records evaluated together: 32 words of records per block.
+inline int stream_block_records(int k_eff) { return 32 / bound_record_words(k_eff); }
+
 // One kernel launch worth of queries.  Offsets are byte offsets into the
 // plan blob.
 struct SearchBatch {
@@ -119,11 +139,18 @@ struct SearchBatch {
   // position words are codes resolved per slot width on the device
   uint64_t off_tmpl = 0;         // uint32[bound_words]: words copied as they are
   uint64_t off_tmpl_code = 0;    // uint32[bound_words]: kTmplCopy / kTmplOnes / term code
+  // literal stream (stream_words == 0: none): words [stream_off,
+  // stream_off + stream_words) of every width block
+  uint32_t stream_off = 0;
+  uint32_t stream_words = 0;
+  uint64_t off_stream_wave = 0;  // uint32[kSearchWaves + 1]: first record of each wave
+  uint64_t off_stream_skip = 0;  // uint32[kSearchWaves]: flat programs each run covers
 };
 
 // Codes of a width-block template word.
 constexpr uint32_t kTmplCopy = 0u;           // the template word itself
 constexpr uint32_t kTmplOnes = 0xFFFFFFFFu;  // the all-ones row at the slot's width
+constexpr uint32_t kTmplZeros = 0xFFFFFFFEu; // the all-zeros row at the slot's width
 // otherwise ((term + 1) << 4) | r: position r of batch term `term`
 inline uint32_t tmpl_position_code(uint32_t term, uint32_t r) { return ((term + 1u) << 4) | r; }
 
