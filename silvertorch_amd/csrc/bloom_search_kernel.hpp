@@ -592,59 +592,60 @@ __device__ __forceinline__ void store_result(const SearchArgs& a, const OutCurso
   }
 }
 
-// Evaluates a wave's run of literal records [r_begin, r_end): each block of
-// records arrives with scalar loads (the run is the same for every bundle of
-// a width, so it stays in the scalar cache), then all the block's row words
-// are read from the tile, then the OR-of-ANDs fold runs, storing a query's
-// result after its last literal.  No per-query decoding.
+// Evaluates a wave's rounds of the literal stream, words [w_begin, w_end):
+// per step, one record of each of the NB slots arrives with scalar loads,
+// then all NB * K row words are read from the tile, then the NB independent
+// OR-of-ANDs folds run; the round's results are stored after its last step.
+// No per-query decoding and no per-literal branches.
 template <int K, bool STAGED, int kOut>
-__device__ __forceinline__ void eval_stream(const SearchArgs& a, const RowSource& rs,
-                                            const ST_CONST uint32_t* stream, uint32_t r_begin,
-                                            uint32_t r_end, int64_t bundle) {
+__device__ __forceinline__ void eval_rounds(const SearchArgs& a, const RowSource& rs,
+                                            const ST_CONST uint32_t* stream, uint32_t w_begin,
+                                            uint32_t w_end, int64_t bundle) {
   constexpr int RW = ((K + 1 + 3) / 4) * 4;
-  constexpr int NB = 32 / RW;  // records per block
+  constexpr int NB = 32 / RW;  // slots per round
   const OutCursor oc = out_cursor<kOut>(a, rs.lane, bundle);
-  auto load_block = [&](uint32_t r, uint32_t (&rec)[NB][K + 1]) {
-    const ST_CONST uint32_t* blk = stream + r * RW;
+  for (uint32_t w = w_begin; w < w_end;) {
+    const ST_CONST uint32_t* hdr = stream + w;
+    const uint32_t T = hdr[0];
+    uint32_t info[NB];
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
+    for (int i = 0; i < NB; ++i) info[i] = hdr[kRoundSlotInfo + i];
+    const ST_CONST uint32_t* step = hdr + kRoundHeaderWords;
+    uint32_t res[NB], acc[NB];
 #pragma unroll
-      for (int v = 0; v <= K; ++v) rec[j][v] = blk[j * RW + v];
-  };
-  uint32_t res = 0, acc = 0;
-  uint32_t rec[NB][K + 1];
-  if (r_begin < r_end) load_block(r_begin, rec);
-  for (uint32_t r = r_begin; r < r_end; r += NB) {
-    uint32_t w[NB];
+    for (int i = 0; i < NB; ++i) res[i] = acc[i] = 0;
+    for (uint32_t j = 0; j < T; ++j, step += NB * RW) {
+      uint32_t rec[NB][K + 1];
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      uint32_t t = ~0u;
+      for (int i = 0; i < NB; ++i)
 #pragma unroll
-      for (int k = 0; k < K; ++k) t &= row_word<STAGED>(rs, rec[j][k]);
-      w[j] = t;
-    }
-    // the next block's records load while this block's rows are read
-    uint32_t nxt[NB][K + 1];
-    load_block(r + NB < r_end ? r + NB : r, nxt);
+        for (int v = 0; v <= K; ++v) rec[i][v] = step[i * RW + v];
+      uint32_t t[NB];
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const uint32_t f = rec[j][K];
-      const uint32_t neg = 0u - (f & kStreamNeg);
-      const uint32_t grp = 0u - ((f >> 1) & 1u);
-      res |= acc & grp;
-      acc = (acc | grp) & (w[j] ^ neg);
-      if (f & kStreamLast) {
-        uint32_t v = res | acc;
-        if (f & kStreamComplement) v = ~v;
-        store_result<kOut>(a, oc, rs.lane, bundle, f >> kStreamRowShift, v);
-        res = 0;
-        acc = 0;
+      for (int i = 0; i < NB; ++i) {
+        uint32_t x = ~0u;
+#pragma unroll
+        for (int k = 0; k < K; ++k) x &= row_word<STAGED>(rs, rec[i][k]);
+        t[i] = x;
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const uint32_t f = rec[i][K];
+        const uint32_t neg = 0u - (f & kStreamNeg);
+        const uint32_t grp = 0u - ((f >> 1) & 1u);
+        res[i] |= acc[i] & grp;
+        acc[i] = (acc[i] | grp) & (t[i] ^ neg);
       }
     }
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-      for (int v = 0; v <= K; ++v) rec[j][v] = nxt[j][v];
+    for (int i = 0; i < NB; ++i) {
+      if (info[i] & kSlotValid) {
+        uint32_t v = res[i] | acc[i];
+        if (info[i] & kSlotComplement) v = ~v;
+        store_result<kOut>(a, oc, rs.lane, bundle, info[i] >> kSlotRowShift, v);
+      }
+    }
+    w += kRoundHeaderWords + T * NB * RW;
   }
 }
 
@@ -842,10 +843,10 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
       const ST_CONST uint32_t* stream =
           a.bound + static_cast<uint64_t>(slot) * a.bound_words + a.stream_off;
       if (staged) {
-        if (streamed) eval_stream<K, true, kOut>(a, rs, stream, r_begin, r_end, bundle);
+        if (streamed) eval_rounds<K, true, kOut>(a, rs, stream, r_begin, r_end, bundle);
         eval_queries<K, KP, true, true, G, kOut>(a, rs, s_rest, s_end, bundle, slot);
       } else {
-        if (streamed) eval_stream<K, false, kOut>(a, rs, stream, r_begin, r_end, bundle);
+        if (streamed) eval_rounds<K, false, kOut>(a, rs, stream, r_begin, r_end, bundle);
         eval_queries<K, KP, false, true, G, kOut>(a, rs, s_rest, s_end, bundle, slot);
       }
     } else if (staged) {

@@ -612,38 +612,72 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
       SearchBatch b;
       b.num_slots = static_cast<uint32_t>(cur.size());
       b.num_terms = terms.size();
-      // Longest-processing-time assignment of queries to the waves of a
-      // workgroup; cost ~ LDS word reads plus instruction count.
-      std::vector<int> order(cur.size());
-      for (size_t i = 0; i < order.size(); ++i) order[i] = static_cast<int>(i);
+      // Assignment of queries to the waves of a workgroup.  Flat programs,
+      // longest first, are cut into rounds of as many programs as the
+      // kernel's literal stream evaluates in lockstep (similar lengths, so
+      // little padding); whole rounds go to the least loaded wave, longest
+      // first, then the stack-form programs one by one.  Cost ~ literal
+      // steps times the row reads and instructions of one step.
+      const int per_round = stream_block_records(std::max(plan->k_eff, 1));
       auto cost = [&](int i) {
         const CompiledQuery& c = cur[i].cq;
         if (c.flat) return 4 + static_cast<int64_t>(c.lits.size()) * (k_eff + 3);
         return 8 + 6 * static_cast<int64_t>(c.ops.size()) +
                static_cast<int64_t>(c.terms.size()) * (k_eff + 3);
       };
-      std::stable_sort(order.begin(), order.end(),
+      std::vector<int> flat_q, stack_q;
+      for (size_t i = 0; i < cur.size(); ++i)
+        (cur[i].cq.flat ? flat_q : stack_q).push_back(static_cast<int>(i));
+      std::stable_sort(flat_q.begin(), flat_q.end(), [&](int a, int c) {
+        return cur[a].cq.lits.size() > cur[c].cq.lits.size();
+      });
+      std::stable_sort(stack_q.begin(), stack_q.end(),
                        [&](int a, int c) { return cost(a) > cost(c); });
+      struct Round {
+        size_t first, count;
+        int64_t cost;
+      };
+      std::vector<Round> rounds;
+      for (size_t r0 = 0; r0 < flat_q.size(); r0 += per_round) {
+        const size_t n = std::min<size_t>(per_round, flat_q.size() - r0);
+        const int64_t steps = std::max<int64_t>(1, cur[flat_q[r0]].cq.lits.size());
+        rounds.push_back({r0, n, 4 + steps * per_round * (k_eff + 3)});
+      }
+      // rounds arrive longest first already; a stable sort keeps the one
+      // partial round behind the full rounds of its length
+      std::stable_sort(rounds.begin(), rounds.end(),
+                       [](const Round& x, const Round& y) { return x.cost > y.cost; });
       std::vector<std::vector<int>> per_wave(kSearchWaves);
+      std::vector<std::vector<const Round*>> wave_rounds(kSearchWaves);
       std::vector<int64_t> load(kSearchWaves, 0);
-      for (int i : order) {
-        int w = static_cast<int>(std::min_element(load.begin(), load.end()) -
-                                 load.begin());
+      auto least_loaded = [&]() {
+        return static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
+      };
+      for (const Round& r : rounds) {
+        const int w = least_loaded();
+        wave_rounds[w].push_back(&r);
+        load[w] += r.cost;
+      }
+      for (int w = 0; w < kSearchWaves; ++w) {
+        // the batch's one partial round (if any) goes last in its wave, so
+        // that cutting the wave's flat programs into rounds in order finds
+        // the same rounds again
+        std::stable_sort(wave_rounds[w].begin(), wave_rounds[w].end(),
+                         [](const Round* x, const Round* y) { return x->count > y->count; });
+        for (const Round* r : wave_rounds[w])
+          for (size_t i = 0; i < r->count; ++i) per_wave[w].push_back(flat_q[r->first + i]);
+      }
+      for (int i : stack_q) {
+        const int w = least_loaded();
         per_wave[w].push_back(i);
         load[w] += cost(i);
       }
       std::vector<uint32_t> wave_off(kSearchWaves + 1, 0), starts, insns;
       const uint32_t pos_bytes = static_cast<uint32_t>(plan->kp) * 4;
       for (int w = 0; w < kSearchWaves; ++w) {
-        // Within a wave: flat programs by decreasing literal count, paired
-        // neighbour by neighbour, then the stack-form ones.
+        // Within a wave: flat programs round by round, paired neighbour by
+        // neighbour, then the stack-form ones.
         auto& list = per_wave[w];
-        std::stable_sort(list.begin(), list.end(), [&](int x, int y) {
-          const CompiledQuery& a = cur[x].cq;
-          const CompiledQuery& c = cur[y].cq;
-          if (a.flat != c.flat) return a.flat;
-          return a.flat && a.lits.size() > c.lits.size();
-        });
         size_t n_flat = 0;
         while (n_flat < list.size() && cur[list[n_flat]].cq.flat) ++n_flat;
         for (size_t li = 0; li < list.size(); ++li) {
@@ -820,9 +854,9 @@ void build_block_template(const st_search_plan& plan, SearchBatch& bt,
     }
   }
 
-  // Literal stream: per wave, its leading flat programs as one run of
-  // records, padded to whole blocks.  Records follow the kernel's K, which
-  // is 1 when no position resolves (k_eff 0: no term literals then).
+  // Literal stream: per wave, its leading flat programs in rounds of
+  // per_block slots, in the order the compiler laid them out.  Records follow the kernel's K, which is 1
+  // when no position resolves (k_eff 0: no term literals then).
   const uint32_t* wave_off = reinterpret_cast<const uint32_t*>(plan.blob.data() + bt.off_wave);
   const int ks = std::max(k_eff, 1);
   const int srw = bound_record_words(ks);
@@ -831,8 +865,11 @@ void build_block_template(const st_search_plan& plan, SearchBatch& bt,
   wave_skip.assign(kSearchWaves, 0u);
   bt.stream_off = static_cast<uint32_t>(tmpl.size());
   bt.stream_words = 0;
-  uint32_t recs = 0;
   bool fits = true;
+  auto word = [&](uint32_t v) {
+    tmpl.push_back(v);
+    code.push_back(kTmplCopy);
+  };
   auto record = [&](uint32_t pos_code, uint32_t term, uint32_t flags) {
     const size_t at = tmpl.size();
     tmpl.resize(at + srw, 0u);
@@ -840,36 +877,60 @@ void build_block_template(const st_search_plan& plan, SearchBatch& bt,
     for (int r = 0; r < ks; ++r)
       code[at + r] = pos_code == kTmplCopy ? tmpl_position_code(term, r) : pos_code;
     tmpl[at + ks] = flags;
-    ++recs;
   };
+  std::vector<uint32_t> flat;
   for (int w = 0; w < kSearchWaves && fits; ++w) {
-    wave_rec[w] = recs;
+    wave_rec[w] = static_cast<uint32_t>(tmpl.size() - bt.stream_off);
+    flat.clear();
     for (uint32_t q = wave_off[w]; q < wave_off[w + 1]; ++q) {
-      const uint32_t* src = insns.data() + starts[q];
-      const uint32_t hdr = src[0];
+      const uint32_t hdr = insns[starts[q]];
       if (!(hdr & kFlatForm)) break;  // flat programs lead each wave's list
-      const uint32_t row = src[1];
-      if (static_cast<int64_t>(row) >= kStreamMaxRows) {
-        fits = false;
-        break;
-      }
-      const uint32_t T = hdr & 0xFFFFu;
-      const uint32_t last = kStreamLast | (row << kStreamRowShift) |
-                            ((hdr & kFlatComplement) ? kStreamComplement : 0u);
-      if (T == 0) record(kTmplZeros, 0, kStreamFirst | last);
-      for (uint32_t j = 0; j < T; ++j) {
-        const uint32_t* lit = src + kProgHeaderWords + j * kFlatLiteralWords;
-        record(kTmplCopy, lit[0] / pos_bytes,
-               (lit[1] ? kStreamNeg : 0u) | (lit[2] ? kStreamFirst : 0u) |
-                   (j + 1 == T ? last : 0u));
-      }
-      ++wave_skip[w];
+      if (static_cast<int64_t>(insns[starts[q] + 1]) >= kStreamMaxRows) fits = false;
+      flat.push_back(q);
     }
-    while (recs % per_block) record(kTmplOnes, 0, 0u);
+    if (!fits) break;
+    // the compiler laid the wave's flat programs out round by round
+    wave_skip[w] = static_cast<uint32_t>(flat.size());
+    for (size_t r0 = 0; r0 < flat.size(); r0 += per_block) {
+      const size_t n = std::min<size_t>(per_block, flat.size() - r0);
+      uint32_t T = 1;  // an empty program still takes one (zeros-row) step
+      for (size_t i = 0; i < n; ++i) T = std::max(T, insns[starts[flat[r0 + i]]] & 0xFFFFu);
+      word(T);
+      for (int i = 1; i < kRoundSlotInfo; ++i) word(0u);
+      for (uint32_t i = 0; i < per_block; ++i) {
+        if (i < n) {
+          const uint32_t* src = insns.data() + starts[flat[r0 + i]];
+          word(kSlotValid | ((src[0] & kFlatComplement) ? kSlotComplement : 0u) |
+               (src[1] << kSlotRowShift));
+        } else {
+          word(0u);
+        }
+      }
+      for (uint32_t i = per_block; kRoundSlotInfo + i < kRoundHeaderWords; ++i) word(0u);
+      for (uint32_t j = 0; j < T; ++j) {
+        for (uint32_t i = 0; i < per_block; ++i) {
+          if (i >= n) {
+            record(kTmplOnes, 0, 0u);
+            continue;
+          }
+          const uint32_t* src = insns.data() + starts[flat[r0 + i]];
+          const uint32_t Tq = src[0] & 0xFFFFu;
+          if (Tq == 0 && j == 0) {
+            record(kTmplZeros, 0, kStreamFirst);
+          } else if (j < Tq) {
+            const uint32_t* lit = src + kProgHeaderWords + j * kFlatLiteralWords;
+            record(kTmplCopy, lit[0] / pos_bytes,
+                   (lit[1] ? kStreamNeg : 0u) | (lit[2] ? kStreamFirst : 0u));
+          } else {
+            record(kTmplOnes, 0, 0u);
+          }
+        }
+      }
+    }
   }
-  wave_rec[kSearchWaves] = recs;
-  if (fits && recs > 0) {
-    bt.stream_words = recs * static_cast<uint32_t>(srw);
+  wave_rec[kSearchWaves] = static_cast<uint32_t>(tmpl.size() - bt.stream_off);
+  if (fits && wave_rec[kSearchWaves] > 0) {
+    bt.stream_words = wave_rec[kSearchWaves];
   } else {  // no stream: every program runs from the width block
     tmpl.resize(bt.stream_off);
     code.resize(bt.stream_off);

@@ -103,23 +103,31 @@ constexpr uint32_t kNoWidthSlot = 0xFFFFFFFFu;
 inline int bound_record_words(int k_eff) { return ((k_eff + 1 + 3) / 4) * 4; }
 
 // Literal stream.  Every width block also carries the batch's flat programs
-// as one run of literal records per wave, which the kernel reads with scalar
-// loads and evaluates in blocks, without per-query decoding.  A record has
-// bound_record_words(K) words: [row position 0 .. K-1, flags, pad...],
-// flags bit 0 = negate,
-// bit 1 = first of its group, bit 2 = last literal of its query (the result
-// is stored after it), bit 3 = complement the result, bits 4..31 = the
-// query's output row.  A query with no literal is one record on the all-zeros
-// row.  Each wave's run is padded to a whole number of blocks with no-op
-// records (all-ones row, flags 0).  The flat programs a wave's run covers are
-// its first ones; the rest are evaluated from the width block.
+// as rounds of literal records, which the kernel reads with scalar loads and
+// evaluates without per-query decoding.  A wave's flat programs are taken
+// longest first, stream_block_records(K) at a time, into rounds; a round
+// evaluates its programs (its slots) in lockstep, one literal of every slot
+// per step:
+//   header, kRoundHeaderWords words: [T, 0 x 7, slot 0 info, slot 1 info,
+//     ...], slot info = bit 0 valid, bit 1 complement the result,
+//     bits 2..31 output row;
+//   then T steps of stream_block_records(K) records (one per slot) of
+//     bound_record_words(K) words: [row position 0 .. K-1, flags, pad...],
+//     flags bit 0 = negate, bit 1 = first of its group.
+// T is the longest program of the round; shorter ones (and empty slots) are
+// padded with no-op records (all-ones row, flags 0).  A program with no
+// literal is one record on the all-zeros row.  The flat programs a wave's
+// rounds cover are its first ones; the rest are evaluated from the width
+// block.
 constexpr uint32_t kStreamNeg = 1u;
 constexpr uint32_t kStreamFirst = 2u;
-constexpr uint32_t kStreamLast = 4u;
-constexpr uint32_t kStreamComplement = 8u;
-constexpr int kStreamRowShift = 4;
-constexpr int64_t kStreamMaxRows = int64_t{1} << (32 - kStreamRowShift);
-// Records evaluated together: 32 words of records per block.
+constexpr uint32_t kSlotValid = 1u;
+constexpr uint32_t kSlotComplement = 2u;
+constexpr int kSlotRowShift = 2;
+constexpr int64_t kStreamMaxRows = int64_t{1} << (32 - kSlotRowShift);
+constexpr int kRoundHeaderWords = 16;
+constexpr int kRoundSlotInfo = 8;  // header word of slot 0's info
+// Slots of a round: 32 words of records per step.
 inline int stream_block_records(int k_eff) { return 32 / bound_record_words(k_eff); }
 
 // One kernel launch worth of queries.  Offsets are byte offsets into the
@@ -143,7 +151,7 @@ struct SearchBatch {
   // stream_off + stream_words) of every width block
   uint32_t stream_off = 0;
   uint32_t stream_words = 0;
-  uint64_t off_stream_wave = 0;  // uint32[kSearchWaves + 1]: first record of each wave
+  uint64_t off_stream_wave = 0;  // uint32[kSearchWaves + 1]: first stream word of each wave
   uint64_t off_stream_skip = 0;  // uint32[kSearchWaves]: flat programs each run covers
 };
 
