@@ -275,7 +275,8 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
         bound ? at(bt.off_bound_start) : nullptr, bound ? at(bt.off_bound) : nullptr,
         bound ? bt.bound_words : 0u, bound ? at(bt.off_stream_wave) : nullptr,
         bound ? at(bt.off_stream_skip) : nullptr, bound ? bt.stream_off : 0u,
-        bound ? bt.stream_words : 0u, bt.num_terms, static_cast<int32_t>(plan->hash_k),
+        bound ? bt.stream_words : 0u, bound ? bt.stream_masks : 0u, bt.num_terms,
+        static_cast<int32_t>(plan->hash_k),
         num_bundles * 32, out, counts, num_docs);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)

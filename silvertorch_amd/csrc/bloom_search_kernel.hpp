@@ -74,6 +74,7 @@ struct SearchArgs {
   uint32_t bound_words;
   uint32_t stream_off;                    // literal stream within a width block
   uint32_t stream_words;                  // 0: no stream
+  uint32_t stream_masks;                  // records carry group masks
   uint32_t num_terms;
   int32_t hash_k;
   int64_t out_cols;  // columns per output row = num_bundles * 32
@@ -597,7 +598,7 @@ __device__ __forceinline__ void store_result(const SearchArgs& a, const OutCurso
 // then all NB * K row words are read from the tile, then the NB independent
 // OR-of-ANDs folds run; the round's results are stored after its last step.
 // No per-query decoding and no per-literal branches.
-template <int K, bool STAGED, int kOut>
+template <int K, bool STAGED, bool MASKS, int kOut>
 __device__ __forceinline__ void eval_rounds(const SearchArgs& a, const RowSource& rs,
                                             const ST_CONST uint32_t* stream, uint32_t w_begin,
                                             uint32_t w_end, int64_t bundle) {
@@ -631,10 +632,15 @@ __device__ __forceinline__ void eval_rounds(const SearchArgs& a, const RowSource
 #pragma unroll
       for (int i = 0; i < NB; ++i) {
         const uint32_t f = rec[i][K];
-        const uint32_t neg = 0u - (f & kStreamNeg);
-        const uint32_t grp = 0u - ((f >> 1) & 1u);
-        res[i] |= acc[i] & grp;
-        acc[i] = (acc[i] | grp) & (t[i] ^ neg);
+        if constexpr (MASKS) {  // f is the group mask; nothing is negated
+          res[i] |= acc[i] & f;
+          acc[i] = (acc[i] | f) & t[i];
+        } else {
+          const uint32_t neg = 0u - (f & kStreamNeg);
+          const uint32_t grp = 0u - ((f >> 1) & 1u);
+          res[i] |= acc[i] & grp;
+          acc[i] = (acc[i] | grp) & (t[i] ^ neg);
+        }
       }
     }
 #pragma unroll
@@ -728,6 +734,7 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     const uint32_t* __restrict__ bound_start, const uint32_t* __restrict__ bound,
     uint32_t bound_words, const uint32_t* __restrict__ stream_wave,
     const uint32_t* __restrict__ stream_skip, uint32_t stream_off, uint32_t stream_words,
+    uint32_t stream_masks,
     uint32_t num_terms, int32_t hash_k,
     int64_t out_cols, void* __restrict__ out, int64_t* __restrict__ counts, int64_t num_docs) {
   SearchArgs a;
@@ -746,6 +753,7 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
   a.bound_words = bound_words;
   a.stream_off = stream_off;
   a.stream_words = stream_words;
+  a.stream_masks = stream_masks;
   a.num_terms = num_terms;
   a.hash_k = hash_k;
   a.out_cols = out_cols;
@@ -843,10 +851,20 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
       const ST_CONST uint32_t* stream =
           a.bound + static_cast<uint64_t>(slot) * a.bound_words + a.stream_off;
       if (staged) {
-        if (streamed) eval_rounds<K, true, kOut>(a, rs, stream, r_begin, r_end, bundle);
+        if (streamed) {
+          if (a.stream_masks)
+            eval_rounds<K, true, true, kOut>(a, rs, stream, r_begin, r_end, bundle);
+          else
+            eval_rounds<K, true, false, kOut>(a, rs, stream, r_begin, r_end, bundle);
+        }
         eval_queries<K, KP, true, true, G, kOut>(a, rs, s_rest, s_end, bundle, slot);
       } else {
-        if (streamed) eval_rounds<K, false, kOut>(a, rs, stream, r_begin, r_end, bundle);
+        if (streamed) {
+          if (a.stream_masks)
+            eval_rounds<K, false, true, kOut>(a, rs, stream, r_begin, r_end, bundle);
+          else
+            eval_rounds<K, false, false, kOut>(a, rs, stream, r_begin, r_end, bundle);
+        }
         eval_queries<K, KP, false, true, G, kOut>(a, rs, s_rest, s_end, bundle, slot);
       }
     } else if (staged) {
@@ -863,7 +881,7 @@ using KernelFn = void (*)(const int64_t*, int64_t, const int64_t*, int64_t,
                           const uint32_t*, const uint32_t*,
                           const uint32_t*, const uint64_t*, const uint32_t*,
                           const uint32_t*, const uint32_t*, const uint32_t*, uint32_t,
-                          const uint32_t*, const uint32_t*, uint32_t, uint32_t,
+                          const uint32_t*, const uint32_t*, uint32_t, uint32_t, uint32_t,
                           uint32_t, int32_t,
                           int64_t, void*, int64_t*, int64_t);
 

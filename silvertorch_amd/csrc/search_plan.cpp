@@ -878,6 +878,21 @@ void build_block_template(const st_search_plan& plan, SearchBatch& bt,
       code[at + r] = pos_code == kTmplCopy ? tmpl_position_code(term, r) : pos_code;
     tmpl[at + ks] = flags;
   };
+  // Group masks instead of flag bits when no literal of the batch's flat
+  // programs is negated.
+  bool masks = true;
+  for (uint32_t q = 0; q < bt.num_slots && masks; ++q) {
+    const uint32_t* src = insns.data() + starts[q];
+    if (!(src[0] & kFlatForm)) continue;
+    const uint32_t T = src[0] & 0xFFFFu;
+    for (uint32_t j = 0; j < T; ++j)
+      if (src[kProgHeaderWords + j * kFlatLiteralWords + 1]) masks = false;
+  }
+  auto lit_flags = [&](bool neg, bool first) -> uint32_t {
+    if (masks) return first ? ~0u : 0u;
+    return (neg ? kStreamNeg : 0u) | (first ? kStreamFirst : 0u);
+  };
+  bt.stream_masks = masks ? 1u : 0u;
   std::vector<uint32_t> flat;
   for (int w = 0; w < kSearchWaves && fits; ++w) {
     wave_rec[w] = static_cast<uint32_t>(tmpl.size() - bt.stream_off);
@@ -916,11 +931,10 @@ void build_block_template(const st_search_plan& plan, SearchBatch& bt,
           const uint32_t* src = insns.data() + starts[flat[r0 + i]];
           const uint32_t Tq = src[0] & 0xFFFFu;
           if (Tq == 0 && j == 0) {
-            record(kTmplZeros, 0, kStreamFirst);
+            record(kTmplZeros, 0, lit_flags(false, true));
           } else if (j < Tq) {
             const uint32_t* lit = src + kProgHeaderWords + j * kFlatLiteralWords;
-            record(kTmplCopy, lit[0] / pos_bytes,
-                   (lit[1] ? kStreamNeg : 0u) | (lit[2] ? kStreamFirst : 0u));
+            record(kTmplCopy, lit[0] / pos_bytes, lit_flags(lit[1] != 0, lit[2] != 0));
           } else {
             record(kTmplOnes, 0, 0u);
           }
@@ -932,6 +946,7 @@ void build_block_template(const st_search_plan& plan, SearchBatch& bt,
   if (fits && wave_rec[kSearchWaves] > 0) {
     bt.stream_words = wave_rec[kSearchWaves];
   } else {  // no stream: every program runs from the width block
+    bt.stream_masks = 0;
     tmpl.resize(bt.stream_off);
     code.resize(bt.stream_off);
     bt.stream_off = 0;

@@ -113,7 +113,9 @@ inline int bound_record_words(int k_eff) { return ((k_eff + 1 + 3) / 4) * 4; }
 //     bits 2..31 output row;
 //   then T steps of stream_block_records(K) records (one per slot) of
 //     bound_record_words(K) words: [row position 0 .. K-1, flags, pad...],
-//     flags bit 0 = negate, bit 1 = first of its group.
+//     flags bit 0 = negate, bit 1 = first of its group; in a batch with no
+//     negated literal (stream_masks set) the flags word is the group mask
+//     itself (~0 on the first literal of a group, else 0).
 // T is the longest program of the round; shorter ones (and empty slots) are
 // padded with no-op records (all-ones row, flags 0).  A program with no
 // literal is one record on the all-zeros row.  The flat programs a wave's
@@ -151,6 +153,7 @@ struct SearchBatch {
   // stream_off + stream_words) of every width block
   uint32_t stream_off = 0;
   uint32_t stream_words = 0;
+  uint32_t stream_masks = 0;     // 1: records carry group masks (no negation)
   uint64_t off_stream_wave = 0;  // uint32[kSearchWaves + 1]: first stream word of each wave
   uint64_t off_stream_skip = 0;  // uint32[kSearchWaves]: flat programs each run covers
 };
