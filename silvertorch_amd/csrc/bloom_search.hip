@@ -11,19 +11,19 @@
 namespace st {
 namespace {
 
-KernelFn select_kernel(int k, int mode) {
+KernelFn select_kernel(int k, int mode, bool quad) {
   switch (k) {
     case 0:
-    case 1: return search_kernel_for<1>(mode);
-    case 2: return search_kernel_for<2>(mode);
-    case 3: return search_kernel_for<3>(mode);
-    case 4: return search_kernel_for<4>(mode);
-    case 5: return search_kernel_for<5>(mode);
-    case 6: return search_kernel_for<6>(mode);
-    case 7: return search_kernel_for<7>(mode);
-    case 8: return search_kernel_for<8>(mode);
-    case 9: return search_kernel_for<9>(mode);
-    case 10: return search_kernel_for<10>(mode);
+    case 1: return search_kernel_for<1>(mode, quad);
+    case 2: return search_kernel_for<2>(mode, quad);
+    case 3: return search_kernel_for<3>(mode, quad);
+    case 4: return search_kernel_for<4>(mode, quad);
+    case 5: return search_kernel_for<5>(mode, quad);
+    case 6: return search_kernel_for<6>(mode, quad);
+    case 7: return search_kernel_for<7>(mode, quad);
+    case 8: return search_kernel_for<8>(mode, quad);
+    case 9: return search_kernel_for<9>(mode, quad);
+    case 10: return search_kernel_for<10>(mode, quad);
     default: fail("unsupported k_eff ", k);
   }
 }
@@ -235,7 +235,6 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
   ST_CHECK(plan->bound_bundles < 0 || plan->bound_bundles == num_bundles,
            "plan was bound to ", plan->bound_bundles, " bundles, the index has ",
            num_bundles);
-  KernelFn fn = select_kernel(plan->k_eff, mode);
   const int grid = static_cast<int>(
       std::min<int64_t>(num_bundles, static_cast<int64_t>(device_cu_count())));
   const char* blob = static_cast<const char*>(plan_blob_device);
@@ -266,6 +265,13 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
     }
   }
   for (const SearchBatch& bt : plan->batches) {
+    // Quad-lane stream evaluation when the batch's literal stream fits the
+    // LDS area after the tile and a stream step holds whole quads (k <= 7).
+    const int kk = std::max(plan->k_eff, 1);
+    const bool quad = bound && bt.stream_words != 0 &&
+                      bt.stream_words <= kQuadStreamMaxWords &&
+                      stream_block_records(kk) >= 4;
+    KernelFn fn = select_kernel(plan->k_eff, mode, quad);
     hipLaunchKernelGGL(
         fn, dim3(grid), dim3(kSearchThreads), 0, stream, bloom_index, bloom_index_numel,
         bundle_b_offsets, num_bundles, at(bt.off_wave), at(bt.off_insn_start),

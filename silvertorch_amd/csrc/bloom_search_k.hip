@@ -9,11 +9,20 @@
 namespace st {
 
 template <>
-KernelFn search_kernel_for<ST_SEARCH_K>(int mode) {
+KernelFn search_kernel_for<ST_SEARCH_K>(int mode, bool quad) {
+  if constexpr (QuadShape<ST_SEARCH_K>::NB >= 4) {
+    if (quad) {
+      switch (mode) {
+        case kOutBool: return bloom_search_kernel<ST_SEARCH_K, kOutBool, true>;
+        case kOutCounts: return bloom_search_kernel<ST_SEARCH_K, kOutCounts, true>;
+        default: return bloom_search_kernel<ST_SEARCH_K, kOutPacked, true>;
+      }
+    }
+  }
   switch (mode) {
-    case kOutBool: return bloom_search_kernel<ST_SEARCH_K, kOutBool>;
-    case kOutCounts: return bloom_search_kernel<ST_SEARCH_K, kOutCounts>;
-    default: return bloom_search_kernel<ST_SEARCH_K, kOutPacked>;
+    case kOutBool: return bloom_search_kernel<ST_SEARCH_K, kOutBool, false>;
+    case kOutCounts: return bloom_search_kernel<ST_SEARCH_K, kOutCounts, false>;
+    default: return bloom_search_kernel<ST_SEARCH_K, kOutPacked, false>;
   }
 }
 

@@ -11,7 +11,8 @@
 // bloom bit `row` of the 64 docs of column c, doc 64c+j at bit 63-j.
 //
 // Work decomposition: one 1024-thread workgroup per CU walks bundles
-// blockIdx.x, blockIdx.x + gridDim.x, ...  For each bundle it
+// blockIdx.x, blockIdx.x + gridDim.x, ... of the visiting order, loading each
+// bundle's extent and width slot one bundle ahead.  For each bundle it
 //   1. moves the bundle's rows (prefetched into registers while the previous
 //      bundle was evaluated) into LDS, so the index is read from HBM once per
 //      query batch;
@@ -101,10 +102,18 @@ __device__ __forceinline__ void bundle_extent(const SearchArgs& a, int64_t bnd,
   if (b < 0) b = 0;
 }
 
-__device__ __forceinline__ void prefetch_tile(const SearchArgs& a, int64_t bnd,
+// Where a bundle sits and which width block evaluates it.
+struct BundleMeta {
+  int64_t bundle;
+  int64_t start;  // first row
+  int64_t b;      // rows
+  uint32_t slot;  // width slot (kNoWidthSlot: none)
+};
+
+// Issues this thread's share of the loads of the rows [start, start + b)
+// into `pre` (nothing when the bundle is wider than the LDS tile).
+__device__ __forceinline__ void prefetch_tile(const SearchArgs& a, int64_t start, int64_t b,
                                               u32x4 (&pre)[kPrefetch]) {
-  int64_t start, b;
-  bundle_extent(a, bnd, start, b);
   const int tid = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < kPrefetch; ++i) pre[i] = u32x4{0, 0, 0, 0};
@@ -593,6 +602,119 @@ __device__ __forceinline__ void store_result(const SearchArgs& a, const OutCurso
   }
 }
 
+// ------------------------------------------------- literal stream, quad lanes
+//
+// When a batch's literal stream fits the LDS area after the tile and a step
+// holds at least four records (k <= 7), the stream of the bundle's width slot
+// is staged in LDS with the tile and evaluated four programs at a time: lane
+// l serves slot 4 * quad + (l >> 4) of the round and owns bytes
+// 16 * (l & 15) .. +15 of every row, so one 16-byte LDS read per lane fetches
+// a row for four programs at once, each 16-lane group reading its own
+// record.  Per literal and four programs that is one record read, k row reads
+// and their address adds, and the OR-of-ANDs fold on four words.
+
+// Record words, u32x4 per record, records per step and quads per step.
+template <int K>
+struct QuadShape {
+  static constexpr int RW = ((K + 1 + 3) / 4) * 4;
+  static constexpr int RV = RW / 4;
+  static constexpr int NB = 32 / RW;
+  static constexpr int NQ = NB / 4;
+};
+
+// LDS words a staged literal stream may take (the area after the tile).
+constexpr uint32_t kQuadStreamMaxWords = kSearchPosSlots;
+// u32x4 registers per thread that carry a stream of that size.
+constexpr int kStreamPrefetch = (kQuadStreamMaxWords / 4 + kSearchThreads - 1) / kSearchThreads;
+
+__device__ __forceinline__ uint32_t u32x4_get(const u32x4& v, int i) {
+  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+// Stores this lane's 16 bytes of output row `row` on the bundle (and, in
+// kOutCounts mode, the row's match count on the bundle, summed over the
+// lane's 16-lane group).  The u32s are, in order, the low and high halves of
+// words 2s and 2s + 1 (s = lane & 15); a word's high half holds its first 32
+// docs.
+template <int kOut>
+__device__ __forceinline__ void store_quad(const SearchArgs& a, int lane, int64_t bundle,
+                                           uint32_t row, u32x4 v) {
+  const uint32_t s = static_cast<uint32_t>(lane & 15);
+  if constexpr (kOut == kOutBool) {
+    ST_GLOBAL char* dst = (ST_GLOBAL char*)(static_cast<char*>(a.out) +
+                                            static_cast<int64_t>(row) * (a.out_cols * 64) +
+                                            bundle * kDocsPerBundle + s * 128);
+    store_bool32(dst, v.y);
+    store_bool32(dst + 32, v.x);
+    store_bool32(dst + 64, v.w);
+    store_bool32(dst + 96, v.z);
+  } else {
+    ST_GLOBAL u32x4* dst = (ST_GLOBAL u32x4*)(static_cast<char*>(a.out) +
+                                              static_cast<int64_t>(row) * (a.out_cols * 8) +
+                                              bundle * 256 + s * 16);
+    __builtin_nontemporal_store(v, dst);
+  }
+  if constexpr (kOut == kOutCounts) {
+    const int64_t first = bundle * kDocsPerBundle + static_cast<int64_t>(s) * 128;
+    uint32_t n = __builtin_popcount(v.y & valid_doc_mask(first, a.num_docs)) +
+                 __builtin_popcount(v.x & valid_doc_mask(first + 32, a.num_docs)) +
+                 __builtin_popcount(v.w & valid_doc_mask(first + 64, a.num_docs)) +
+                 __builtin_popcount(v.z & valid_doc_mask(first + 96, a.num_docs));
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) n += __shfl_xor(n, m, 16);
+    if (s == 0) a.counts[static_cast<int64_t>(row) * a.num_bundles + bundle] = n;
+  }
+}
+
+// Evaluates a wave's rounds of the LDS-staged literal stream `sw`, words
+// [w_begin, w_end), on the bundle in the LDS tile.  Layout as the scalar
+// path reads it (search_plan.hpp): per round a 16-word header (T, slot infos
+// from word kRoundSlotInfo), then T steps of NB records of RW words.
+template <int K, bool MASKS, int kOut>
+__device__ __forceinline__ void eval_quads(const SearchArgs& a, const u32x4* tile,
+                                           const uint32_t* sw, uint32_t w_begin,
+                                           uint32_t w_end, int64_t bundle, int lane) {
+  using S = QuadShape<K>;
+  const int g = lane >> 4;
+  const char* tb = reinterpret_cast<const char*>(tile) + (lane & 15) * 16;
+  for (uint32_t w = w_begin; w < w_end;) {
+    const uint32_t* hdr = sw + w;
+    const uint32_t T = uniform(hdr[0]);
+#pragma unroll
+    for (int qd = 0; qd < S::NQ; ++qd) {
+      const uint32_t info = hdr[kRoundSlotInfo + qd * 4 + g];
+      u32x4 res{0, 0, 0, 0}, acc{0, 0, 0, 0};
+      const u32x4* rec =
+          reinterpret_cast<const u32x4*>(hdr + kRoundHeaderWords) + (qd * 4 + g) * S::RV;
+      for (uint32_t j = 0; j < T; ++j, rec += S::NB * S::RV) {
+        u32x4 r[S::RV];
+#pragma unroll
+        for (int v = 0; v < S::RV; ++v) r[v] = rec[v];
+        u32x4 t = *reinterpret_cast<const u32x4*>(tb + u32x4_get(r[0], 0));
+#pragma unroll
+        for (int k = 1; k < K; ++k)
+          t &= *reinterpret_cast<const u32x4*>(tb + u32x4_get(r[k >> 2], k & 3));
+        const uint32_t f = u32x4_get(r[K >> 2], K & 3);
+        if constexpr (MASKS) {  // f is the group mask; nothing is negated
+          res |= acc & f;
+          acc = (acc | f) & t;
+        } else {
+          const uint32_t neg = 0u - (f & kStreamNeg);
+          const uint32_t grp = 0u - ((f >> 1) & 1u);
+          res |= acc & grp;
+          acc = (acc | grp) & (t ^ neg);
+        }
+      }
+      if (info & kSlotValid) {
+        u32x4 v = res | acc;
+        if (info & kSlotComplement) v = ~v;
+        store_quad<kOut>(a, lane, bundle, info >> kSlotRowShift, v);
+      }
+    }
+    w += kRoundHeaderWords + T * S::NB * S::RW;
+  }
+}
+
 // Evaluates a wave's rounds of the literal stream, words [w_begin, w_end):
 // per step, one record of each of the NB slots arrives with scalar loads,
 // then all NB * K row words are read from the tile, then the NB independent
@@ -657,7 +779,9 @@ __device__ __forceinline__ void eval_rounds(const SearchArgs& a, const RowSource
 
 // Evaluates this wave's queries [s_begin, s_end) on one bundle and stores
 // their 32-bit halves of the bundle's 32 output words.
-template <int K, int KP, bool STAGED, bool BOUND, int G, int kOut>
+// LITE (the quad instance, whose prefetch registers leave less room):
+// programs one by one, literals in groups of G, no fully unrolled forms.
+template <int K, int KP, bool STAGED, bool BOUND, int G, int kOut, bool LITE = false>
 __device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSource& rs,
                                              uint32_t s_begin, uint32_t s_end,
                                              int64_t bundle, uint32_t slot) {
@@ -673,7 +797,7 @@ __device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSourc
       const ST_CONST uint32_t* prog = progs + a.bound_start[s];
       const uint32_t hdr = prog[0];
       const uint32_t T = hdr & 0xFFFFu;
-      if (hdr & kPairedWithNext) {
+      if (!LITE && (hdr & kPairedWithNext)) {
         const ST_CONST uint32_t* prog_b = progs + a.bound_start[s + 1];
         const uint32_t hdr_b = prog_b[0];
         uint32_t acc_a, acc_b;
@@ -691,7 +815,10 @@ __device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSourc
       }
       uint32_t acc;
       if (hdr & kFlatForm) {
-        acc = eval_bound_flat<K, STAGED, G>(rs, prog + kProgHeaderWords, T);
+        if constexpr (LITE)
+          acc = eval_bound_flat_loop<K, STAGED, G>(rs, prog + kProgHeaderWords, T);
+        else
+          acc = eval_bound_flat<K, STAGED, G>(rs, prog + kProgHeaderWords, T);
         if (hdr & kFlatComplement) acc = ~acc;
       } else {
         acc = eval_bound_stack<K, KP, STAGED, G>(rs, prog, T, prog[2]);
@@ -711,7 +838,11 @@ __device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSourc
     const uint32_t T = hdr & 0xFFFFu;
     uint32_t acc;
     if (hdr & kFlatForm) {
-      acc = eval_flat<K, KP, STAGED, G>(rs, reinterpret_cast<const ST_CONST u32x4*>(prog + kProgHeaderWords), T);
+      const ST_CONST u32x4* lits = reinterpret_cast<const ST_CONST u32x4*>(prog + kProgHeaderWords);
+      if constexpr (LITE)
+        acc = eval_flat_loop<K, KP, STAGED, G>(rs, lits, T);
+      else
+        acc = eval_flat<K, KP, STAGED, G>(rs, lits, T);
       if (hdr & kFlatComplement) acc = ~acc;
     } else {
       acc = eval_stack<K, KP, STAGED, G>(rs, prog, T, prog[2]);
@@ -723,7 +854,7 @@ __device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSourc
 // The arrays arrive as separate __restrict__ parameters (not inside
 // SearchArgs) so the compiler can prove the output stores never alias the
 // program and offset arrays and fetch those with scalar loads.
-template <int K, int kOut>
+template <int K, int kOut, bool kQuad>
 __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     const int64_t* __restrict__ index, int64_t index_numel,
     const int64_t* __restrict__ bundle_offsets, int64_t num_bundles,
@@ -762,6 +893,7 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
   a.num_docs = num_docs;
   constexpr int KP = K <= 4 ? 4 : (K <= 8 ? 8 : 12);
   constexpr int G = KP == 4 ? 4 : (KP == 8 ? 2 : 1);  // terms fetched together
+  constexpr int GL = G > 2 ? 2 : G;                    // the same, LITE
   __shared__ u32x4 tile[(kSearchTileRows + 2) * 16];
   __shared__ __attribute__((aligned(16))) uint32_t pos[kSearchPosSlots];
 
@@ -774,12 +906,45 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     tile[kSearchOnesRow * 16 + (tid & 15) + (tid & 16)] = u32x4{fill, fill, fill, fill};
   }
 
-  // Bundle visited at step i of the grid-stride walk.
-  auto bundle_at = [&](int64_t i) -> int64_t {
-    return a.bundle_order ? static_cast<int64_t>(a.bundle_order[i]) : i;
+  // Bundle visited at step i of the grid-stride walk, with its extent and
+  // width slot.  Each bundle's metadata is loaded one bundle ahead of its
+  // tile prefetch, so that neither the prefetch nor the evaluation waits on
+  // a chain of dependent scalar loads.
+  auto meta_at = [&](int64_t i) -> BundleMeta {
+    BundleMeta m;
+    m.bundle = a.bundle_order ? static_cast<int64_t>(a.bundle_order[i]) : i;
+    bundle_extent(a, m.bundle, m.start, m.b);
+    m.slot = a.bundle_slot ? a.bundle_slot[m.bundle] : kNoWidthSlot;
+    return m;
+  };
+  const int64_t grid = gridDim.x;
+  // Quad-lane evaluation of the literal stream (eval_quads): the batch's
+  // stream fits the LDS area after the tile and a step holds whole quads.
+  const bool quad = kQuad && a.stream_words != 0 && a.stream_words <= kQuadStreamMaxWords &&
+                    QuadShape<K>::NB >= 4;
+  auto quad_bundle = [&](const BundleMeta& m) {
+    return quad && m.slot != kNoWidthSlot && m.b <= kSearchTileRows;
+  };
+  // This thread's share of a quad bundle's stream, loaded with its tile.
+  auto prefetch_stream = [&](const BundleMeta& m, u32x4 (&sp)[kQuad ? kStreamPrefetch : 1]) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(
+        bound + static_cast<uint64_t>(m.slot) * a.bound_words + a.stream_off);
+    const uint32_t chunks = a.stream_words / 4;
+#pragma unroll
+    for (int i = 0; i < (kQuad ? kStreamPrefetch : 1); ++i) {
+      const uint32_t c = static_cast<uint32_t>(tid) + static_cast<uint32_t>(i) * kSearchThreads;
+      sp[i] = c < chunks ? src[c] : u32x4{0, 0, 0, 0};
+    }
   };
   u32x4 pre[kPrefetch];
-  if (blockIdx.x < a.num_bundles) prefetch_tile(a, bundle_at(blockIdx.x), pre);
+  u32x4 spre[kQuad ? kStreamPrefetch : 1];
+  BundleMeta cur{0, 0, 0, kNoWidthSlot}, nxt{0, 0, 0, kNoWidthSlot};
+  if (blockIdx.x < a.num_bundles) {
+    cur = meta_at(blockIdx.x);
+    prefetch_tile(a, cur.start, cur.b, pre);
+    if (quad_bundle(cur)) prefetch_stream(cur, spre);
+  }
+  if (blockIdx.x + grid < a.num_bundles) nxt = meta_at(blockIdx.x + grid);
 
   int64_t prev_b = -1;  // width whose term positions are in pos
   const uint32_t s_begin = uniform(a.wave_off[wave]);
@@ -792,11 +957,14 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
   const char* tile_lane = reinterpret_cast<const char*>(tile) + lane * 4;
   const uint32_t* index32 = reinterpret_cast<const uint32_t*>(a.index);
 
-  for (int64_t step = blockIdx.x; step < a.num_bundles; step += gridDim.x) {
-    const int64_t bundle = bundle_at(step);
-    int64_t start, b;
-    bundle_extent(a, bundle, start, b);
+  uint32_t warm = 0;  // scalar-cache warming loads of the next stream (see below)
+  for (int64_t step = blockIdx.x; step < a.num_bundles; step += grid) {
+    const int64_t bundle = cur.bundle;
+    const int64_t start = cur.start, b = cur.b;
+    const uint32_t slot = cur.slot;
     const bool staged = b <= kSearchTileRows;
+
+    const bool quad_here = quad_bundle(cur);
 
     __syncthreads();  // previous bundle's readers are done with tile and pos
     if (staged) {
@@ -807,7 +975,16 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
         if (c < chunks) tile[c] = pre[i];
       }
     }
-    const uint32_t slot = a.bundle_slot ? a.bundle_slot[bundle] : kNoWidthSlot;
+    if (quad_here) {  // the stream goes where unbound bundles keep positions
+      const uint32_t chunks = a.stream_words / 4;
+      u32x4* dst = reinterpret_cast<u32x4*>(pos);
+#pragma unroll
+      for (int i = 0; i < (kQuad ? kStreamPrefetch : 1); ++i) {
+        const uint32_t c = static_cast<uint32_t>(tid) + static_cast<uint32_t>(i) * kSearchThreads;
+        if (c < chunks) dst[c] = spre[i];
+      }
+      prev_b = -1;
+    }
     if (slot == kNoWidthSlot && b != prev_b) {
       const FastMod64 fm = make_fastmod_dev(static_cast<uint64_t>(b));
       for (uint32_t u = tid; u < a.num_terms; u += kSearchThreads) {
@@ -834,9 +1011,15 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
       prev_b = b;
     }
     __syncthreads();
+    asm volatile("" ::"s"(warm));  // the warming loads are complete by now
 
-    const int64_t next = step + gridDim.x;
-    if (next < a.num_bundles) prefetch_tile(a, bundle_at(next), pre);
+    const bool has_next = step + grid < a.num_bundles;
+    if (has_next) {
+      prefetch_tile(a, nxt.start, nxt.b, pre);
+      if (quad_bundle(nxt)) prefetch_stream(nxt, spre);
+    }
+    BundleMeta after{0, 0, 0, kNoWidthSlot};
+    if (step + 2 * grid < a.num_bundles) after = meta_at(step + 2 * grid);
 
     // Evaluate this wave's queries on the bundle.
     RowSource rs;
@@ -847,7 +1030,26 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     rs.start = start;
     rs.lane = lane;
     rs.staged = staged;
-    if (slot != kNoWidthSlot) {
+    if constexpr (kQuad) {
+      // Quad instance: stream programs of staged slot bundles in quads, all
+      // other bundles' programs from the width block one by one.
+      if (quad_here) {
+        if (a.stream_masks)
+          eval_quads<K, true, kOut>(a, tile, pos, r_begin, r_end, bundle, lane);
+        else
+          eval_quads<K, false, kOut>(a, tile, pos, r_begin, r_end, bundle, lane);
+        eval_queries<K, KP, true, true, GL, kOut, true>(a, rs, s_rest, s_end, bundle, slot);
+      } else if (slot != kNoWidthSlot) {
+        if (staged)
+          eval_queries<K, KP, true, true, GL, kOut, true>(a, rs, s_begin, s_end, bundle, slot);
+        else
+          eval_queries<K, KP, false, true, GL, kOut, true>(a, rs, s_begin, s_end, bundle, slot);
+      } else if (staged) {
+        eval_queries<K, KP, true, false, GL, kOut, true>(a, rs, s_begin, s_end, bundle, slot);
+      } else {
+        eval_queries<K, KP, false, false, GL, kOut, true>(a, rs, s_begin, s_end, bundle, slot);
+      }
+    } else if (slot != kNoWidthSlot) {
       const ST_CONST uint32_t* stream =
           a.bound + static_cast<uint64_t>(slot) * a.bound_words + a.stream_off;
       if (staged) {
@@ -872,6 +1074,18 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     } else {
       eval_queries<K, KP, false, false, G, kOut>(a, rs, s_begin, s_end, bundle, slot);
     }
+    // The next bundle's first round header and records (this wave's part of
+    // its width block) are read into the scalar cache now; the loads complete
+    // while the workgroup waits at the barriers and stores the next tile.
+    warm = 0;
+    if (!kQuad && has_next && streamed && nxt.slot != kNoWidthSlot && r_begin < r_end) {
+      const ST_CONST uint32_t* w =
+          a.bound + static_cast<uint64_t>(nxt.slot) * a.bound_words + a.stream_off + r_begin;
+      // a round is a 16-word header and at least one 32-word step
+      warm = w[0] ^ w[kRoundHeaderWords] ^ w[kRoundHeaderWords + 16];
+    }
+    cur = nxt;
+    nxt = after;
   }
 }
 
@@ -885,19 +1099,20 @@ using KernelFn = void (*)(const int64_t*, int64_t, const int64_t*, int64_t,
                           uint32_t, int32_t,
                           int64_t, void*, int64_t*, int64_t);
 
-// The kernels of one K (all output modes), defined in the translation unit
-// compiled with ST_SEARCH_K = K.
+// The kernels of one K (all output modes; the quad instance evaluates the
+// literal stream in quad lanes and needs a stream that fits the LDS and k <= 7),
+// defined in the translation unit compiled with ST_SEARCH_K = K.
 template <int K>
-KernelFn search_kernel_for(int mode);
-template <> KernelFn search_kernel_for<1>(int mode);
-template <> KernelFn search_kernel_for<2>(int mode);
-template <> KernelFn search_kernel_for<3>(int mode);
-template <> KernelFn search_kernel_for<4>(int mode);
-template <> KernelFn search_kernel_for<5>(int mode);
-template <> KernelFn search_kernel_for<6>(int mode);
-template <> KernelFn search_kernel_for<7>(int mode);
-template <> KernelFn search_kernel_for<8>(int mode);
-template <> KernelFn search_kernel_for<9>(int mode);
-template <> KernelFn search_kernel_for<10>(int mode);
+KernelFn search_kernel_for(int mode, bool quad);
+template <> KernelFn search_kernel_for<1>(int mode, bool quad);
+template <> KernelFn search_kernel_for<2>(int mode, bool quad);
+template <> KernelFn search_kernel_for<3>(int mode, bool quad);
+template <> KernelFn search_kernel_for<4>(int mode, bool quad);
+template <> KernelFn search_kernel_for<5>(int mode, bool quad);
+template <> KernelFn search_kernel_for<6>(int mode, bool quad);
+template <> KernelFn search_kernel_for<7>(int mode, bool quad);
+template <> KernelFn search_kernel_for<8>(int mode, bool quad);
+template <> KernelFn search_kernel_for<9>(int mode, bool quad);
+template <> KernelFn search_kernel_for<10>(int mode, bool quad);
 
 }  // namespace st
