@@ -277,7 +277,10 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
         bundle_b_offsets, num_bundles, at(bt.off_wave), at(bt.off_insn_start),
         at(bt.off_insns), reinterpret_cast<const uint64_t*>(blob + bt.off_hashes),
         bound ? at(plan->off_bundle_slot) : nullptr,
-        bound ? at(plan->off_bundle_order) : nullptr,
+        // The quad instance reads its programs from LDS, so it visits bundles
+        // in index order: neighbouring workgroups then write neighbouring
+        // output columns at the same time.
+        bound && !quad ? at(plan->off_bundle_order) : nullptr,
         bound ? at(bt.off_bound_start) : nullptr, bound ? at(bt.off_bound) : nullptr,
         bound ? bt.bound_words : 0u, bound ? at(bt.off_stream_wave) : nullptr,
         bound ? at(bt.off_stream_skip) : nullptr, bound ? bt.stream_off : 0u,
