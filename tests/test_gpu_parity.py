@@ -311,3 +311,63 @@ def test_ops_column_info():  # test_bloom_index_search.py:216-241
     want_f = (offsets % 64).tolist()
     want_c = [(l + f + 63) // 64 if l > 0 else 0 for l, f in zip(lengths.tolist(), want_f)]
     assert counts.cpu().tolist() == want_c and starts.cpu().tolist() == want_s and firsts.cpu().tolist() == want_f
+
+
+@pytest.mark.parametrize("cfg,docs", [("cfg1", 30000), ("cfg2", 40000), ("cfg3", 12000), ("cfg5", 30000)])
+def test_config_shapes_vs_oracle(cfg, docs):
+    """The benchmark configurations' corpus and query distributions
+    (silvertorch_amd.synthetic) at reduced doc counts: the
+    same feature counts, value distributions, k / hash_k / B_MULTIPLIER and
+    query shapes (cfg3: bundles wider than the LDS tile, k = 4, boolean trees
+    with NOT), build and search bit-exact against the oracle."""
+    from silvertorch_amd import synthetic as S
+
+    cspec, qspec = S.CONFIGS[cfg]
+    corp = S.make_corpus(cspec, seed=0, num_docs=docs)
+    queries = S.make_queries(cspec, qspec, seed=0)
+    H.note(f"[config] {cfg} docs={docs} queries={len(queries)} k={cspec.k} bm={cspec.b_multiplier}")
+    index, bbo = H.build(corp.feature_ids, corp.feature_offsets, corp.feature_values, cspec.b_multiplier, cspec.k)
+    want_index, want_bbo = O.bloom_build(corp.feature_ids, corp.feature_offsets, corp.feature_values,
+                                         cspec.b_multiplier, cspec.k)
+    np.testing.assert_array_equal(bbo, want_bbo)
+    np.testing.assert_array_equal(index, want_index)
+    pd, po = _plans(queries, cspec.hash_k)
+    want = O.search_packed(index, bbo, pd, po, cspec.k, cspec.hash_k)
+    np.testing.assert_array_equal(H.search(index, bbo, pd, po, cspec.k, cspec.hash_k), want)
+    if cfg != "cfg3":
+        got_b = H.search(index, bbo, pd, po, cspec.k, cspec.hash_k, bool_mask=True, bind="host")
+        np.testing.assert_array_equal(got_b, O.unpack_bool(want))
+    ids, ro, packed = H.search_ids(index, bbo, pd, po, cspec.k, cspec.hash_k, docs)
+    np.testing.assert_array_equal(packed, want)
+    want_ids, want_ro = O.compact(want, docs)
+    np.testing.assert_array_equal(ro, want_ro)
+    np.testing.assert_array_equal(ids, want_ids)
+
+
+def test_mixed_bundle_kinds_in_one_launch():
+    """One search launch over bundles of every kind: more distinct widths than
+    width slots (bundles without a slot), bundles wider than the LDS tile,
+    and staged slotted bundles whose flat programs run as a literal stream."""
+    rng = np.random.default_rng(77)
+    nb = 150
+    n = nb * 2048
+    cnt = np.ones(n, dtype=np.int64)
+    for b in range(nb):  # one heavy doc per bundle sets the width
+        cnt[b * 2048 + int(rng.integers(0, 2048))] = 1 + (b % 90) if b % 37 else 400
+    offs = np.concatenate([[0], np.cumsum(cnt)]).astype(np.int64)
+    vals = rng.integers(0, 3000, int(offs[-1])).astype(np.int64)
+    ids = np.array([3], dtype=np.int32)
+    index, bbo = H.build(ids, offs, vals, 1.5, 1)
+    widths = np.diff(bbo)
+    assert len(set(widths.tolist())) > 64 and widths.max() > 512
+    queries = []
+    for _ in range(200):
+        t = int(rng.integers(1, 6))
+        queries.append(" OR ".join(" AND ".join(f"3:{int(rng.integers(0, 3000))}" for _ in range(int(rng.integers(1, 3))))
+                                   for _ in range(t)))
+    pd, po = _plans(queries, 5)
+    H.note(f"[mixed] bundles={nb} widths={len(set(widths.tolist()))} max={widths.max()} queries={len(queries)}")
+    want = O.search_packed(index, bbo, pd, po, 1, 5)
+    np.testing.assert_array_equal(H.search(index, bbo, pd, po, 1, 5), want)
+    np.testing.assert_array_equal(H.search(index, bbo, pd, po, 1, 5, bool_mask=True, bind="device"),
+                                  O.unpack_bool(want))
