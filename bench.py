@@ -51,6 +51,7 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-topk", action="store_true", help="skip the cfg5 filter + top-k leg")
     p.add_argument("--no-build4", action="store_true", help="skip the cfg4 build-throughput leg")
+    p.add_argument("--no-cfg3", action="store_true", help="skip the cfg3 wide-bundle search leg")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 512 MiB device-to-device copy, 5 times: the known-size "
                         "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings")
@@ -212,16 +213,8 @@ def measure_build_cfg4(st, O):
 
     cspec, _ = S.CONFIGS["cfg4"]
     N, F = cspec.num_docs, cspec.num_features
-    dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(4)
-    counts = torch.randint(cspec.count_lo, cspec.count_hi + 1, (N * F,), generator=g, device=dev)
-    offs = torch.zeros(N * F + 1, dtype=torch.long, device=dev)
-    torch.cumsum(counts, 0, out=offs[1:])
-    del counts
-    V = int(offs[-1].item())
-    vals = torch.randint(0, cspec.vocab, (V,), generator=g, device=dev)
-    ids = torch.arange(1, F + 1, dtype=torch.int32, device=dev)
+    ids, offs, vals = S.make_corpus_device(cspec, seed=4)
+    V = vals.numel()
     bi, bo = st.bloom_index_build(ids, offs, vals, cspec.b_multiplier, cspec.k)  # warm
     torch.cuda.synchronize()
     times = []
@@ -253,6 +246,59 @@ def measure_build_cfg4(st, O):
         "algorithmic_bytes": alg, "achieved_gbs": alg / secs / 1e9,
         "frac_of_hbm_peak": alg / secs / 1e9 / HBM_PEAK_GBS,
         "note": "wall time of the op (both build kernels and the size readback), median of 3",
+    }
+
+
+def measure_search_cfg3(st, O):
+    """cfg3: 50M docs, 16 features, per-doc value counts
+    uniform in [1, 3], values Zipf(1.05) over 1M, K=4, B_MULTIPLIER=10 (bundles
+    of ~1,700 rows, wider than the LDS tile), 1,024 boolean trees of depth <= 3
+    with NOT on 20% of leaves; packed output.  The corpus is drawn on the
+    device.  Reports the op time and checks sampled bundles bit-exactly
+    against the oracle."""
+    import numpy as np
+    import torch
+
+    from silvertorch_amd import synthetic as S
+
+    cspec, qspec = S.CONFIGS["cfg3"]
+    N = cspec.num_docs
+    ids, offs, vals = S.make_corpus_device(cspec, seed=3)
+    bi, bo = st.bloom_index_build(ids, offs, vals, cspec.b_multiplier, cspec.k)
+    del ids, offs, vals
+    queries = S.make_queries(cspec, qspec, seed=0)
+    _, (pd, po) = st.parse_expression_query_batch(queries, torch.ones(1, dtype=torch.long), cspec.hash_k, True, 5)
+    out = st.bloom_index_search_batch(bi, bo, pd, po, cspec.k, cspec.hash_k, False)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(3):
+        t = time.perf_counter()
+        out = st.bloom_index_search_batch(bi, bo, pd, po, cspec.k, cspec.hash_k, False)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t)
+    secs = sorted(times)[1]
+    Q = len(queries)
+    alg = bi.numel() * 8 + bo.numel() * 8 + pd.numel() + po.numel() * 8 + out.numel() * 8
+    bbo = bo.cpu().numpy()
+    nb = bbo.size - 1
+    ok = True
+    for bnd in (0, nb // 2, nb - 1):
+        s0, e0 = int(bbo[bnd]), int(bbo[bnd + 1])
+        want = O.search_packed(bi[s0 * 32:e0 * 32].cpu().numpy(), np.array([0, e0 - s0], np.int64),
+                               pd.numpy(), po.numpy(), cspec.k, cspec.hash_k)
+        ok &= bool(np.array_equal(out[:, bnd * 32:(bnd + 1) * 32].cpu().numpy(), want))
+    w = np.diff(bbo)
+    log(f"cfg3 search: {N} docs x {Q} queries, widths {w.min()}-{w.max()}, {secs * 1e3:.2f} ms, "
+        f"sampled bundles bit-exact vs oracle: {ok}")
+    if not ok:
+        sys.exit("parity failure in sampled cfg3 bundles")
+    return {
+        "workload": f"cfg3: bloom_index_search_batch, {N} docs x {Q} queries (trees, NOT), k={cspec.k}, "
+                    f"bundle widths {int(w.min())}-{int(w.max())}",
+        "ms": secs * 1e3, "doc_queries_per_s": Q * N / secs,
+        "algorithmic_bytes": alg, "achieved_gbs": alg / secs / 1e9,
+        "frac_of_hbm_peak": alg / secs / 1e9 / HBM_PEAK_GBS,
+        "note": "wall time of the op (plan compile, width binding, search kernel), median of 3",
     }
 
 
@@ -473,6 +519,7 @@ def main():
 
     topk_report = None if args.no_topk else measure_topk(st, capi, args.steps)
     build4_report = None if args.no_build4 else measure_build_cfg4(st, O)
+    cfg3_report = None if args.no_cfg3 else measure_search_cfg3(st, O)
 
     baseline = None
     if not args.no_cpu_baseline:
@@ -512,6 +559,7 @@ def main():
         "cpu_baseline": baseline,
         "build": {"ms": build_s * 1e3, "docs_per_s": N / build_s, "workload": "cfg2 index build"},
         "build_cfg4": build4_report,
+        "search_cfg3": cfg3_report,
         "ids": ids_report,
         "topk": topk_report,
     }

@@ -170,6 +170,42 @@ def make_queries(cspec: CorpusSpec, qspec: QuerySpec, seed: int = 0) -> list[str
     return out
 
 
+def make_corpus_device(spec: CorpusSpec, seed: int = 0, num_docs: int | None = None,
+                       device: str = "cuda", chunk: int = 1 << 26):
+    """Large-scale corpus drawn on the device with a seeded torch generator
+    (same distributions as make_corpus, not the same draws): per (doc,
+    feature) counts uniform in [lo, hi], values Zipf(s) by inverse CDF or
+    uniform.  Returns device tensors (feature_ids, feature_offsets,
+    feature_values)."""
+    import torch
+
+    n = spec.num_docs if num_docs is None else num_docs
+    F = spec.num_features
+    g = torch.Generator(device=device)
+    g.manual_seed(seed * 1_000_003 + STREAM_COUNTS)
+    counts = torch.randint(spec.count_lo, spec.count_hi + 1, (n * F,), generator=g, device=device)
+    offsets = torch.zeros(n * F + 1, dtype=torch.long, device=device)
+    torch.cumsum(counts, 0, out=offsets[1:])
+    total = int(offsets[-1].item())
+    g.manual_seed(seed * 1_000_003 + STREAM_VALUES)
+    values = torch.empty(total, dtype=torch.long, device=device)
+    cdf = None
+    if spec.zipf_s is not None:
+        cdf = torch.from_numpy(_zipf_cdf(spec.vocab, spec.zipf_s)).to(device)
+    for lo in range(0, total, chunk):
+        hi = min(total, lo + chunk)
+        if cdf is None:
+            values[lo:hi] = torch.randint(0, spec.vocab, (hi - lo,), generator=g, device=device)
+        else:
+            u = torch.rand(hi - lo, generator=g, device=device, dtype=torch.float64)
+            values[lo:hi] = torch.clamp(torch.searchsorted(cdf, u, right=True), max=spec.vocab - 1)
+    if spec.feature_offsets:
+        fo = torch.tensor(spec.feature_offsets, dtype=torch.long, device=device)
+        values += torch.repeat_interleave(fo.repeat(n), counts)
+    ids = torch.arange(1, F + 1, dtype=torch.int32, device=device)
+    return ids, offsets, values
+
+
 def make_embeddings(num_docs: int, dim: int, num_queries: int, seed: int = 0):
     """bf16-representable fp32 embeddings: docs ~ N(0, 1/dim), queries ~ N(0, 1)."""
     import torch
