@@ -19,10 +19,13 @@
 //   2. resolves every distinct batch term to its k row positions for this
 //      bundle's width b -- once per bundle instead of once per (query,
 //      column) -- skipping the step when b equals the previous bundle's;
-//   3. has each wave run its queries' accumulator programs: lane l owns the
-//      32-bit half (l & 1) of column l >> 1, so one wave covers the 32
-//      columns of the bundle for one query and all control flow is
-//      wave-uniform.
+//   3. has each wave run its queries' programs.  Flat (OR-of-AND) programs
+//      of a width-bound batch whose literal stream fits the LDS area after
+//      the tile run four at a time in quad lanes (eval_quads: the stream is
+//      staged in LDS with the tile, each 16-lane group serves one program
+//      and every lane reads 16 bytes of a row); the other programs run one
+//      per wave instruction, lane l owning the 32-bit half (l & 1) of column
+//      l >> 1, with wave-uniform control flow.
 // Bundles wider than the LDS tile are evaluated from global memory with the
 // same programs.
 #pragma once
