@@ -988,6 +988,14 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
       }
       prev_b = -1;
     }
+    // The next bundle's loads go out as soon as this thread's registers are
+    // in LDS, before the barrier, so the HBM queue is not left empty while the
+    // workgroup finishes storing the tile.
+    const bool has_next = step + grid < a.num_bundles;
+    if (has_next) {
+      prefetch_tile(a, nxt.start, nxt.b, pre);
+      if (quad_bundle(nxt)) prefetch_stream(nxt, spre);
+    }
     if (slot == kNoWidthSlot && b != prev_b) {
       const FastMod64 fm = make_fastmod_dev(static_cast<uint64_t>(b));
       for (uint32_t u = tid; u < a.num_terms; u += kSearchThreads) {
@@ -1016,11 +1024,6 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     __syncthreads();
     asm volatile("" ::"s"(warm));  // the warming loads are complete by now
 
-    const bool has_next = step + grid < a.num_bundles;
-    if (has_next) {
-      prefetch_tile(a, nxt.start, nxt.b, pre);
-      if (quad_bundle(nxt)) prefetch_stream(nxt, spre);
-    }
     BundleMeta after{0, 0, 0, kNoWidthSlot};
     if (step + 2 * grid < a.num_bundles) after = meta_at(step + 2 * grid);
 
