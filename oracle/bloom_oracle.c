@@ -13,6 +13,9 @@
  *   or_bloom_build         bloom_indexer.cpp:72-110
  *   or_search_batch        bloom_index_search.cpp:27-171 (signature_match,
  *                          run_query_plan) and :173-243 (the q x column loop)
+ *   or_partial_response    bloom_index_search.cpp:246-395 (the cluster-
+ *                          restricted search: per (query, cluster) the
+ *                          columns covering the cluster's docs)
  *   or_unpack_bool         bloom_index_search.cpp:231-236
  *   or_compact             README.md:191 (mask[:, :num_docs].nonzero())
  *   or_filtered_topk       no reference op; top-k by (score desc, id asc) of
@@ -26,6 +29,8 @@
  *               known answers, invariants (exact bit counts per doc).
  *   search      reference CPU search golden fixtures, README known answers,
  *               bitwise identities (De Morgan, EMPTY = all ones).
+ *   partial     reference CPU partial-response golden fixtures; every
+ *               returned column equals the full search's word there.
  *   compact     numpy nonzero on the unpacked mask.
  *   topk        brute-force numpy sort on tiny inputs.
  * Defined where the reference is undefined (documented in DESIGN.md):
@@ -247,6 +252,22 @@ static int eval_plan(const or_plan* pl, const int64_t* index,
   return 0;
 }
 
+/* The four byte ranges of one encoded plan (bloom_index_util.cpp:81-124:
+ * operators, child-count offsets, parameters, hashes); -1 when a range lies
+ * outside plans_data. */
+static int decode_plan(const int8_t* plans_data, int64_t plans_data_len,
+                       const int64_t* o, or_plan* pl) {
+  for (int j = 0; j < 8; j += 2)
+    if (o[j] < 0 || o[j] > o[j + 1] || o[j + 1] > plans_data_len) return -1;
+  pl->ops = (const uint8_t*)plans_data + o[0];
+  pl->n_ops = o[1] - o[0];
+  pl->offsets = (const uint8_t*)plans_data + o[2];
+  pl->n_offsets = (o[3] - o[2]) / 4;
+  pl->hashes = (const uint8_t*)plans_data + o[6];
+  pl->n_hashes = (o[7] - o[6]) / 8;
+  return 0;
+}
+
 /* Packed search: out[q * (nb * 32) + c] for every plan q and column c
  * (bloom_index_search.cpp:173-243 with return_bool_mask = false).
  * Returns 0, or -1 - q for the first malformed plan q. */
@@ -258,16 +279,9 @@ int or_search_batch(const int64_t* index, int64_t index_numel,
   if (k > OR_MAX_SEARCH_K && hash_k > OR_MAX_SEARCH_K) return -1;
   const int64_t C = num_bundles * OR_COLS;
   for (int64_t q = 0; q < num_plans; ++q) {
-    const int64_t* o = plans_offsets + 8 * q;
-    for (int j = 0; j < 8; j += 2)
-      if (o[j] < 0 || o[j] > o[j + 1] || o[j + 1] > plans_data_len) return -1 - (int)q;
     or_plan pl;
-    pl.ops = (const uint8_t*)plans_data + o[0];
-    pl.n_ops = o[1] - o[0];
-    pl.offsets = (const uint8_t*)plans_data + o[2];
-    pl.n_offsets = (o[3] - o[2]) / 4;
-    pl.hashes = (const uint8_t*)plans_data + o[6];
-    pl.n_hashes = (o[7] - o[6]) / 8;
+    if (decode_plan(plans_data, plans_data_len, plans_offsets + 8 * q, &pl) != 0)
+      return -1 - (int)q;
     uint64_t* stack = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)(pl.n_ops + 1));
     if (!stack) return -1 - (int)q;
     for (int64_t c = 0; c < C; ++c) {
@@ -286,6 +300,69 @@ int or_search_batch(const int64_t* index, int64_t index_numel,
     free(stack);
   }
   return 0;
+}
+
+/* Cluster-restricted search (bloom_index_search_common_return_partial_response,
+ * bloom_index_search.cpp:246-395).  For row q and cluster c of the
+ * [rows, clusters] arrays: first column start / 64 (C++ truncation),
+ * first_offsets[q, c] = (int8)(start % 64), ncol = length > 0 ?
+ * (length + offset + 63) / 64 : 0 columns, cumsum[q, c] the running int32
+ * column total, and mask[...] the plan's word on each of those columns, in
+ * (q, c, column) order.  The plan is plan_index[q] when plan_index is given,
+ * else q.  Where the reference reads out of bounds this returns an error:
+ * -1 a plan index outside [0, num_plans), -2 a column outside the index,
+ * -3 an int32 running total overflow, -4 capacity too small (*total still
+ * set), -5 a malformed plan. */
+int or_partial_response(const int64_t* index, int64_t index_numel,
+                        const int64_t* bundle_b_offsets, int64_t num_bundles,
+                        const int8_t* plans_data, int64_t plans_data_len,
+                        const int64_t* plans_offsets, int64_t num_plans, int64_t k,
+                        int64_t hash_k, const int64_t* cluster_offsets,
+                        const int64_t* cluster_lengths, int64_t rows,
+                        int64_t clusters, const int64_t* plan_index,
+                        int32_t* cumsum, int8_t* first_offsets, int64_t* mask,
+                        int64_t capacity, int64_t* total) {
+  const int64_t C = num_bundles * OR_COLS;
+  int64_t acc = 0;
+  *total = 0;
+  for (int64_t q = 0; q < rows; ++q) {
+    for (int64_t c = 0; c < clusters; ++c) {
+      const int64_t start = cluster_offsets[q * clusters + c];
+      const int64_t length = cluster_lengths[q * clusters + c];
+      const int8_t off = (int8_t)(start % OR_BITS);
+      const int64_t first_col = start / OR_BITS;
+      const int64_t ncol = length > 0 ? (length + off + OR_BITS - 1) / OR_BITS : 0;
+      first_offsets[q * clusters + c] = off;
+      acc += ncol;
+      if (acc > INT32_MAX) return -3;
+      cumsum[q * clusters + c] = (int32_t)acc;
+      if (ncol == 0) continue;
+      if (first_col < 0 || first_col + ncol > C) return -2;
+      const int64_t p = plan_index ? plan_index[q] : q;
+      if (p < 0 || p >= num_plans) return -1;
+      or_plan pl;
+      if (decode_plan(plans_data, plans_data_len, plans_offsets + 8 * p, &pl) != 0) return -5;
+      uint64_t* stack = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)(pl.n_ops + 1));
+      if (!stack) return -5;
+      for (int64_t j = 0; j < ncol; ++j, ++*total) {
+        if (*total >= capacity) continue;
+        const int64_t col = first_col + j;
+        const int64_t bundle = col / OR_COLS;
+        const int64_t bstart = bundle_b_offsets[bundle];
+        int64_t b = bundle_b_offsets[bundle + 1] - bstart;
+        if (b < 0) b = 0;
+        uint64_t r;
+        if (eval_plan(&pl, index, index_numel, bstart, b, col % OR_COLS, k, hash_k, stack,
+                      &r) != 0) {
+          free(stack);
+          return -5;
+        }
+        mask[*total] = (int64_t)r;
+      }
+      free(stack);
+    }
+  }
+  return *total > capacity ? -4 : 0;
 }
 
 /* Bool mask from the packed words: mask[q, 64c + i] = bit (63 - i). */

@@ -41,6 +41,12 @@ def lib() -> ctypes.CDLL:
         L.or_bloom_build.argtypes = [ctypes.POINTER(ctypes.c_int32), _i64p, _i64p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _i64p, _i64p]
         L.or_search_batch.restype = ctypes.c_int
         L.or_search_batch.argtypes = [_i64p, ctypes.c_int64, _i64p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int8), ctypes.c_int64, _i64p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _i64p]
+        L.or_partial_response.restype = ctypes.c_int
+        L.or_partial_response.argtypes = [_i64p, ctypes.c_int64, _i64p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int8),
+                                          ctypes.c_int64, _i64p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                          _i64p, _i64p, ctypes.c_int64, ctypes.c_int64, _i64p,
+                                          ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int8), _i64p,
+                                          ctypes.c_int64, _i64p]
         L.or_unpack_bool.restype = None
         L.or_unpack_bool.argtypes = [_i64p, ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(ctypes.c_uint8)]
         L.or_compact.restype = None
@@ -117,6 +123,54 @@ def search_packed(index, bbo, plans_data, plans_offsets, k: int, hash_k: int) ->
     if rc != 0:
         raise ValueError(f"oracle search rejected plan {-rc - 1}")
     return out
+
+
+PARTIAL_ERRORS = {-1: "plan index out of range", -2: "cluster columns outside the index",
+                  -3: "int32 column total overflows", -5: "malformed plan"}
+
+
+def partial_response(index, bbo, plans_data, plans_offsets, k: int, hash_k: int,
+                     cluster_offsets, cluster_lengths, plan_index=None):
+    """bloom_index_search_batch_return_partial_response_cpu
+    (bloom_index_search.cpp:246-395) -> (column_counts_cumsum int32[R*C],
+    first_item_offsets_in_column int8[R*C], column_mask_response int64[...])."""
+    index = np.ascontiguousarray(index, dtype=np.int64)
+    bbo = np.ascontiguousarray(bbo, dtype=np.int64)
+    pdata = np.ascontiguousarray(plans_data, dtype=np.int8)
+    poffs = np.ascontiguousarray(plans_offsets, dtype=np.int64)
+    co = np.ascontiguousarray(cluster_offsets, dtype=np.int64)
+    cl = np.ascontiguousarray(cluster_lengths, dtype=np.int64)
+    if co.ndim != 2 or co.shape != cl.shape:
+        raise ValueError(f"cluster arrays must be 2-D of one shape: {co.shape} vs {cl.shape}")
+    rows, clusters = co.shape
+    pi = None if plan_index is None else np.ascontiguousarray(plan_index, dtype=np.int64)
+    cumsum = np.zeros(max(rows * clusters, 1), dtype=np.int32)
+    first = np.zeros(max(rows * clusters, 1), dtype=np.int8)
+    total = np.zeros(1, dtype=np.int64)
+    idx = index if index.size else np.zeros(1, dtype=np.int64)
+    pd = pdata if pdata.size else np.zeros(1, dtype=np.int8)
+    po = poffs if poffs.size else np.zeros(1, dtype=np.int64)
+    co_ = co if co.size else np.zeros(1, dtype=np.int64)
+    cl_ = cl if cl.size else np.zeros(1, dtype=np.int64)
+
+    def run(mask, cap):
+        return lib().or_partial_response(
+            _p(idx, ctypes.c_int64), index.size, _p(bbo, ctypes.c_int64), bbo.size - 1,
+            _p(pd, ctypes.c_int8), pdata.size, _p(po, ctypes.c_int64), poffs.size // 8, k, hash_k,
+            _p(co_, ctypes.c_int64), _p(cl_, ctypes.c_int64), rows, clusters,
+            None if pi is None else _p(pi, ctypes.c_int64), _p(cumsum, ctypes.c_int32),
+            _p(first, ctypes.c_int8), _p(mask, ctypes.c_int64), cap, _p(total, ctypes.c_int64))
+
+    probe = np.zeros(1, dtype=np.int64)
+    rc = run(probe, 0)
+    if rc not in (0, -4):
+        raise ValueError(f"oracle partial response: {PARTIAL_ERRORS.get(rc, rc)}")
+    mask = np.zeros(max(int(total[0]), 1), dtype=np.int64)
+    rc = run(mask, mask.size)
+    if rc != 0:
+        raise ValueError(f"oracle partial response: {PARTIAL_ERRORS.get(rc, rc)}")
+    n = rows * clusters
+    return cumsum[:n], first[:n], mask[: int(total[0])]
 
 
 def unpack_bool(packed: np.ndarray) -> np.ndarray:

@@ -71,3 +71,31 @@ def encode_plan(ops, offsets, hashes, params=()):
         buf += raw + b"\0" * ((-len(raw)) % 8)
         offs += [start, start + len(raw)]
     return bytes(buf), offs
+
+
+@lru_cache(None)
+def _partial_npz():
+    return dict(np.load(GOLDEN / "ref_partial.npz", allow_pickle=False))
+
+
+def partial_case_names() -> list[str]:
+    return sorted({k.split("/")[0] for k in _partial_npz()
+                   if not k.startswith("multiple")})
+
+
+def partial_case(name: str) -> dict:
+    z = _partial_npz()
+    return {k.split("/", 1)[1]: v for k, v in z.items() if k.startswith(name + "/")}
+
+
+def partial_multiple() -> dict:
+    """Chunks of the _multiple fixture: list of dicts plus the shared plans and
+    the reference outputs for fuse = False / True."""
+    z = _partial_npz()
+    n = len({k.split("/")[1] for k in z if k.startswith("multiple/") and k.split("/")[1].isdigit()})
+    chunks = [{f: z[f"multiple/{i}/{f}"] for f in ("index", "bundle_b_offsets", "cluster_offsets",
+                                                   "cluster_lengths")} for i in range(n)]
+    outs = {fuse: [tuple(z[f"multiple_fuse{fuse}/{i}/{f}"] for f in ("cumsum", "first", "mask"))
+                   for i in range(n)] for fuse in (0, 1)}
+    return {"chunks": chunks, "plans_data": z["multiple/plans_data"],
+            "plans_offsets": z["multiple/plans_offsets"], "outputs": outs}

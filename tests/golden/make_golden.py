@@ -12,9 +12,11 @@ Sources of truth, neither of which is this repository's code:
                         and which expressions raise;
       ref_cases.npz     small build + search cases stored in full;
       ref_digests.json  sha256 digests of larger cases (cfg1 and a case with
-                        bundles wider than 32767 rows) plus generator params.
+                        bundles wider than 32767 rows) plus generator params;
+      ref_partial.npz   cluster-restricted search outputs (partial response,
+                        single and multiple-chunk ops) on small cases.
 
-Usage:  python tests/golden/make_golden.py
+Usage:  python tests/golden/make_golden.py [partial]   (partial: only ref_partial.npz)
 The reference library registers torch.ops.st.*, so this script never imports
 silvertorch_amd.
 """
@@ -223,5 +225,94 @@ def main() -> None:
     print("golden fixtures written to", HERE)
 
 
+def partial_fixtures() -> None:
+    """ref_partial.npz: bloom_index_search_batch_return_partial_response(_multiple)
+    of the reference's CPU op (bloom_index_search.cpp:246-487) on small cases:
+    the reference test's shape (test_bloom_index_search.py:301-423), clusters
+    at unaligned doc offsets crossing bundle boundaries with empty clusters and
+    a query_plan_index, and a three-chunk _multiple call."""
+    import torch
+
+    ref = ROOT / "oracle" / "_ref" / "libst_ref.so"
+    if not ref.exists():
+        subprocess.run(["make", "-C", str(ROOT / "oracle"), "ref"], check=True)
+    torch.ops.load_library(str(ref))
+    st = torch.ops.st
+    out = {}
+    rng = np.random.default_rng(11)
+
+    def corpus(n, F, vocab):
+        cnt = rng.integers(0, 4, (n, F))
+        offs = np.concatenate([[0], np.cumsum(cnt.reshape(-1))]).astype(np.int64)
+        vals = rng.integers(0, vocab, int(offs[-1])).astype(np.int64)
+        return np.arange(1, F + 1, dtype=np.int32), offs, vals
+
+    def add(name, ids, offs, vals, queries, co, cl, pi, k=3, hash_k=7, bm=3.0):
+        bi, bo = st.bloom_index_build(torch.from_numpy(ids), torch.from_numpy(offs), torch.from_numpy(vals), bm, k)
+        _, (pd, po) = st.parse_expression_query_batch(queries, torch.ones(1, dtype=torch.long), hash_k, True, 5)
+        res = st.bloom_index_search_batch_return_partial_response(
+            bi, bo, pd, po, torch.from_numpy(co), torch.from_numpy(cl), k, hash_k,
+            None if pi is None else torch.from_numpy(pi))
+        for key, v in (("index", bi.numpy()), ("bundle_b_offsets", bo.numpy()), ("plans_data", pd.numpy()),
+                       ("plans_offsets", po.numpy()), ("cluster_offsets", co), ("cluster_lengths", cl),
+                       ("params", np.array([k, hash_k], dtype=np.int64)),
+                       ("cumsum", res[0].numpy()), ("first", res[1].numpy()), ("mask", res[2].numpy())):
+            out[f"{name}/{key}"] = v
+        if pi is not None:
+            out[f"{name}/plan_index"] = pi
+
+    # the reference test's shape: 256 docs x 3 features, "0:0" twice, 2 clusters
+    n, F = 256, 3
+    ids = np.arange(F, dtype=np.int32)
+    vals = np.array([d * 100 + f for d in range(n) for f in range(F)], dtype=np.int64)
+    offs = np.arange(n * F + 1, dtype=np.int64)
+    add("basic", ids, offs, vals, ["0:0"] * 2, np.array([[0, 128]] * 2, dtype=np.int64),
+        np.array([[128, 128]] * 2, dtype=np.int64), None, hash_k=7, bm=5.0)
+
+    ids, offs, vals = corpus(6000, 2, 300)
+    qs = ["1:5", "1:7 AND 2:9", "1:3 OR NOT 2:4", "", "NOT (1:1 OR 2:2) AND 1:8", "2:11 OR 2:12 OR 1:13"]
+    total = 6000
+    co = rng.integers(0, total - 1, (5, 3)).astype(np.int64)
+    cl = np.minimum(rng.integers(0, 900, (5, 3)), total - co).astype(np.int64)
+    cl[1, 2] = 0
+    cl[3, 0] = -5
+    co[2, 1] = 2040  # crosses the first bundle boundary
+    cl[2, 1] = 30
+    add("varied_plan_index", ids, offs, vals, qs, co, cl, np.array([3, 0, 5, 1, 1], dtype=np.int64))
+    add("varied_rows", ids, offs, vals, qs, np.concatenate([co, co[:1]]), np.concatenate([cl, cl[:1]]), None)
+
+    # _multiple over three chunks, one plan batch
+    chunks = []
+    for n in (3000, 700, 4500):
+        ids, offs, vals = corpus(n, 2, 200)
+        bi, bo = st.bloom_index_build(torch.from_numpy(ids), torch.from_numpy(offs), torch.from_numpy(vals), 3.0, 3)
+        co = rng.integers(0, n - 1, (3, 2)).astype(np.int64)
+        cl = np.minimum(rng.integers(1, 500, (3, 2)), n - co).astype(np.int64)
+        chunks.append((bi, bo, co, cl))
+    qs = ["1:5 OR 2:6", "NOT 1:7", "2:8 AND 1:9"]
+    _, (pd, po) = st.parse_expression_query_batch(qs, torch.ones(1, dtype=torch.long), 7, True, 5)
+    for fuse in (False, True):
+        r = st.bloom_index_search_batch_return_partial_response_multiple(
+            [c[0] for c in chunks], [c[1] for c in chunks], pd, po,
+            [torch.from_numpy(c[2]) for c in chunks], [torch.from_numpy(c[3]) for c in chunks], 3, 7, None, fuse)
+        for i in range(len(chunks)):
+            out[f"multiple_fuse{int(fuse)}/{i}/cumsum"] = r[0][i].numpy()
+            out[f"multiple_fuse{int(fuse)}/{i}/first"] = r[1][i].numpy()
+            out[f"multiple_fuse{int(fuse)}/{i}/mask"] = r[2][i].numpy()
+    for i, (bi, bo, co, cl) in enumerate(chunks):
+        out[f"multiple/{i}/index"] = bi.numpy()
+        out[f"multiple/{i}/bundle_b_offsets"] = bo.numpy()
+        out[f"multiple/{i}/cluster_offsets"] = co
+        out[f"multiple/{i}/cluster_lengths"] = cl
+    out["multiple/plans_data"] = pd.numpy()
+    out["multiple/plans_offsets"] = po.numpy()
+    np.savez_compressed(HERE / "ref_partial.npz", **out)
+    print("partial-response fixtures written to", HERE / "ref_partial.npz")
+
+
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["partial"]:
+        partial_fixtures()
+    else:
+        main()
+        partial_fixtures()

@@ -226,3 +226,61 @@ def test_planted_mistakes_are_caught():
     h = P.murmur3_pair(5, int(vals[4200]), 0)
     b1 = int(bbo[2] - bbo[1])
     assert np.int16(np.int64(h % b1).astype(np.int16)) != h % b1 or h % b1 < 32768
+
+
+@pytest.mark.parametrize("name", G.partial_case_names())
+def test_oracle_partial_response_matches_reference(name):
+    """Cluster-restricted search (bloom_index_search.cpp:246-395): the oracle
+    reproduces the reference CPU op's three outputs exactly."""
+    c = G.partial_case(name)
+    k, hk = (int(v) for v in c["params"])
+    got = O.partial_response(c["index"], c["bundle_b_offsets"], c["plans_data"], c["plans_offsets"], k, hk,
+                             c["cluster_offsets"], c["cluster_lengths"], c.get("plan_index"))
+    for g, w in zip(got, (c["cumsum"], c["first"], c["mask"])):
+        assert g.dtype == w.dtype
+        np.testing.assert_array_equal(g, w)
+
+
+def test_oracle_partial_multiple_matches_reference():
+    """_multiple (bloom_index_search.cpp:420-487) is the single op per chunk;
+    the reference's fuse flag does not change its outputs."""
+    m = G.partial_multiple()
+    for fuse in (0, 1):
+        for ch, want in zip(m["chunks"], m["outputs"][fuse]):
+            got = O.partial_response(ch["index"], ch["bundle_b_offsets"], m["plans_data"], m["plans_offsets"],
+                                     3, 7, ch["cluster_offsets"], ch["cluster_lengths"])
+            for g, w in zip(got, want):
+                np.testing.assert_array_equal(g, w)
+
+
+def test_partial_response_columns_are_search_columns():
+    """Every returned column word is the full search's word for that plan
+    and column; cumsum / offsets follow the integer rules (C++ truncating
+    division, int8 offsets) on negative and unaligned starts."""
+    c = G.partial_case("varied_plan_index")
+    k, hk = (int(v) for v in c["params"])
+    full = O.search_packed(c["index"], c["bundle_b_offsets"], c["plans_data"], c["plans_offsets"], k, hk)
+    co, cl, pi = c["cluster_offsets"], c["cluster_lengths"], c["plan_index"]
+    cumsum, first, mask = O.partial_response(c["index"], c["bundle_b_offsets"], c["plans_data"],
+                                             c["plans_offsets"], k, hk, co, cl, pi)
+    pos = 0
+    for q in range(co.shape[0]):
+        for j in range(co.shape[1]):
+            s, ln = int(co[q, j]), int(cl[q, j])
+            off = int(np.fmod(s, 64))
+            assert first[q * co.shape[1] + j] == off
+            n = (ln + off + 63) // 64 if ln > 0 else 0
+            first_col = int(s / 64) if s >= 0 else -((-s) // 64)
+            np.testing.assert_array_equal(mask[pos:pos + n], full[pi[q], first_col:first_col + n])
+            pos += n
+            assert cumsum[q * co.shape[1] + j] == pos
+    assert pos == mask.size
+    # out-of-range plan indices and columns are errors, not reads past the end
+    with pytest.raises(ValueError, match="plan index"):
+        O.partial_response(c["index"], c["bundle_b_offsets"], c["plans_data"], c["plans_offsets"], k, hk,
+                           co, cl, np.full(co.shape[0], 99, dtype=np.int64))
+    bad = co.copy()
+    bad[0, 0] = int(c["bundle_b_offsets"].size - 1) * 2048
+    with pytest.raises(ValueError, match="outside the index"):
+        O.partial_response(c["index"], c["bundle_b_offsets"], c["plans_data"], c["plans_offsets"], k, hk,
+                           bad, np.maximum(cl, 1), pi)
