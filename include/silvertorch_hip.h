@@ -227,6 +227,56 @@ int st_generate_column_info_for_clusters(const int64_t* offsets,
                                          int8_t* first_offsets, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Cluster-restricted search.  Replaces
+ * bloom_index_search_batch_return_partial_response (bloom_index_search.cpp:
+ * 246-418, bloom_index_search_cuda.cu:617-1648); the _multiple variant
+ * (bloom_index_search.cpp:420-487) is the same per index chunk.  For row q and
+ * cluster c of the HOST int64[rows, clusters] arrays cluster_offsets (first
+ * doc) and cluster_lengths:
+ *   first_offsets[q, c] = (int8)(offset % 64)  (C++ truncating division),
+ *   ncol = length > 0 ? (length + first_offset + 63) / 64 : 0 columns from
+ *   column offset / 64, column_counts_cumsum[q, c] = running int32 total;
+ * the response holds, in (q, c, column) order, the 64-bit match word of plan
+ * plan_index[q] (or q when plan_index is NULL) on each of those columns.
+ *
+ * st_search_plan_partial_items (host) validates the arrays and writes the
+ * two host outputs above (rows * clusters entries each) and one work item per
+ * cluster with columns into items (capacity rows * clusters), with the item
+ * count and the response length (total columns).  Where the reference reads
+ * out of bounds it fails: a plan index outside [0, queries), columns outside
+ * [0, num_bundles * 32), an int32 running total that overflows.
+ * st_bloom_index_search_partial then fills the device int64[total] response
+ * from a device copy of the items and of st_search_plan_blob(plan); the plan
+ * need not be width-bound (widths are resolved per column).
+ * ------------------------------------------------------------------------- */
+typedef struct st_partial_item {
+  int64_t first_column;  /* first column of the cluster */
+  int64_t out_offset;    /* first response entry */
+  int32_t num_columns;
+  uint32_t program;      /* word offset of the plan's program in the blob */
+  uint32_t hashes;       /* uint64 offset of its batch's term hashes */
+  uint32_t reserved;
+} st_partial_item;
+
+int st_search_plan_partial_items(const st_search_plan* plan,
+                                 const int64_t* cluster_offsets,
+                                 const int64_t* cluster_lengths, int64_t rows,
+                                 int64_t clusters, const int64_t* plan_index,
+                                 int64_t num_bundles,
+                                 int32_t* column_counts_cumsum,
+                                 int8_t* first_offsets, st_partial_item* items,
+                                 int64_t* num_items, int64_t* total_columns);
+int st_bloom_index_search_partial(const int64_t* bloom_index,
+                                  int64_t bloom_index_numel,
+                                  const int64_t* bundle_b_offsets,
+                                  int64_t num_bundles,
+                                  const st_search_plan* plan,
+                                  const void* plan_blob_device,
+                                  const st_partial_item* items_device,
+                                  int64_t num_items, int64_t* out,
+                                  void* stream);
+
+/* ---------------------------------------------------------------------------
  * Compaction of matching doc ids.  No reference operator: the reference's
  * users call mask[:, :num_docs].nonzero() on the search output (README.md:
  * 191-193, :265-266 of the reference).  `packed` is a packed search output,

@@ -46,6 +46,7 @@ LIB_SOURCES = [
     *[("bloom_search_k.hip", k) for k in range(1, 11)],
     "bloom_build.hip",
     "bloom_compact.hip",
+    "bloom_partial.hip",
     "filtered_topk.hip",
     "search_plan.cpp",
     "expression_parser.cpp",

@@ -46,7 +46,13 @@ SIGNATURES = {
     "st_filtered_topk_workspace_bytes": (_i64, [_i64]),
     "st_filtered_topk": (ctypes.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp]),
     "st_bloom_index_search_batch_counts": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
+    "st_search_plan_partial_items": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp,
+                                                    _i64p, _i64p]),
+    "st_bloom_index_search_partial": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp]),
 }
+
+# struct st_partial_item (include/silvertorch_hip.h)
+PARTIAL_ITEM_BYTES = 32
 
 _lib = None
 

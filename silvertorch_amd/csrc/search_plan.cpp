@@ -1167,3 +1167,71 @@ extern "C" void st_search_plan_destroy(st_search_plan* plan) {
   st::return_blob_buffer(std::move(plan->blob));
   delete plan;
 }
+
+// Work items of the cluster-restricted search
+// (bloom_index_search_common_return_partial_response,
+// bloom_index_search.cpp:246-395): the reference's column bookkeeping per
+// (row, cluster), and the location of each row's program in the blob.
+extern "C" int st_search_plan_partial_items(const st_search_plan* plan,
+                                            const int64_t* cluster_offsets,
+                                            const int64_t* cluster_lengths, int64_t rows,
+                                            int64_t clusters, const int64_t* plan_index,
+                                            int64_t num_bundles,
+                                            int32_t* column_counts_cumsum,
+                                            int8_t* first_offsets, st_partial_item* items,
+                                            int64_t* num_items, int64_t* total_columns) {
+  using namespace st;
+  return guarded([&] {
+    ST_CHECK(plan != nullptr, "plan is null");
+    ST_CHECK(rows >= 0 && clusters >= 0 && num_bundles >= 0, "negative sizes");
+    ST_CHECK(num_items != nullptr && total_columns != nullptr, "null output");
+    const int64_t n = rows * clusters;
+    ST_CHECK(n == 0 || (cluster_offsets && cluster_lengths && column_counts_cumsum &&
+                        first_offsets && items),
+             "null array");
+    // program word and hash offset of every plan, from the batches' layout
+    std::vector<uint32_t> prog(plan->num_queries, 0), hash(plan->num_queries, 0);
+    for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
+      const SearchBatch& bt = plan->batches[bi];
+      const auto& insns = plan->batch_insns[bi];
+      const auto& starts = plan->batch_starts[bi];
+      for (uint32_t s = 0; s < bt.num_slots; ++s) {
+        const uint32_t row = insns[starts[s] + 1];
+        prog[row] = static_cast<uint32_t>(bt.off_insns / 4 + starts[s]);
+        hash[row] = static_cast<uint32_t>(bt.off_hashes / 8);
+      }
+    }
+    const int64_t C = num_bundles * kColumnsPerBundle;
+    int64_t acc = 0, m = 0;
+    for (int64_t q = 0; q < rows; ++q) {
+      const int64_t p = plan_index ? plan_index[q] : q;
+      for (int64_t c = 0; c < clusters; ++c) {
+        const int64_t i = q * clusters + c;
+        const int64_t start = cluster_offsets[i], length = cluster_lengths[i];
+        const int64_t off = start % kBitsPerColumn;  // truncating, as in C++
+        const int64_t first_col = start / kBitsPerColumn;
+        const int64_t ncol = length > 0 ? (length + off + kBitsPerColumn - 1) / kBitsPerColumn : 0;
+        first_offsets[i] = static_cast<int8_t>(off);
+        acc += ncol;
+        ST_CHECK(acc <= INT32_MAX, "the response of clusters up to row ", q, ", cluster ", c,
+                 " holds more than 2^31 - 1 columns (the column counts are int32)");
+        column_counts_cumsum[i] = static_cast<int32_t>(acc);
+        if (ncol == 0) continue;
+        ST_CHECK(first_col >= 0 && first_col + ncol <= C, "cluster (", q, ", ", c, ") at doc ",
+                 start, " of length ", length, " covers columns [", first_col, ", ",
+                 first_col + ncol, ") outside the index's ", C, " columns");
+        ST_CHECK(p >= 0 && p < plan->num_queries, "query_plan_index[", q, "] = ", p,
+                 " is outside the ", plan->num_queries, " query plans");
+        st_partial_item& it = items[m++];
+        it.first_column = first_col;
+        it.out_offset = acc - ncol;
+        it.num_columns = static_cast<int32_t>(ncol);
+        it.program = prog[p];
+        it.hashes = hash[p];
+        it.reserved = 0;
+      }
+    }
+    *num_items = m;
+    *total_columns = acc;
+  });
+}

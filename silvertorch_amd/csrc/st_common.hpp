@@ -101,4 +101,25 @@ ST_HD uint64_t fast_mod(uint64_t n, const FastMod64& f) {
   return r;
 }
 
+#if defined(__HIPCC__)
+// make_fastmod in device code without a 64-bit divide for divisors below
+// 2^32, from 32-bit divides only:
+// (2^64-1)/d = ((2^32-1)/d) * 2^32 + (((2^32-1) % d) * 2^32 + 2^32-1) / d.
+__device__ __forceinline__ FastMod64 make_fastmod_dev(uint64_t d) {
+  if (d == 0 || (d >> 32)) return make_fastmod(d);
+  const uint32_t d32 = static_cast<uint32_t>(d);
+  const uint32_t qh = 0xFFFFFFFFu / d32;
+  const uint32_t rh = 0xFFFFFFFFu % d32;
+  const uint64_t n = (static_cast<uint64_t>(rh) << 32) | 0xFFFFFFFFull;  // < d * 2^32
+  uint64_t ql = static_cast<uint64_t>(static_cast<double>(n) / static_cast<double>(d32));
+  // the double quotient is within one of the true one; fix it exactly
+  while (ql * d32 > n) --ql;
+  while (n - ql * d32 >= d32) ++ql;
+  FastMod64 f;
+  f.d = d;
+  f.magic = (static_cast<uint64_t>(qh) << 32) + ql;
+  return f;
+}
+#endif
+
 }  // namespace st

@@ -1,7 +1,7 @@
 // torch.ops.st.* registration for the MI355X build.
 //
 // Registers the same schemas as the reference (bloom_indexer.cpp:115-125,
-// bloom_index_search.cpp:542-558, expression_query_parser.cpp:456-465) and
+// bloom_index_search.cpp:542-585, expression_query_parser.cpp:456-465) and
 // binds both dispatch keys to the HIP implementation behind the C ABI in
 // include/silvertorch_hip.h:
 //   CUDA key (HIP tensors under ROCm torch): runs on the tensors' device.
@@ -295,6 +295,169 @@ std::tuple<Tensor, Tensor, Tensor> column_info(const Tensor& offsets_in,
   return {counts, starts, firsts};
 }
 
+// ------------------------------------------ cluster-restricted search
+// bloom_index_search_batch_return_partial_response(_multiple)
+// (bloom_index_search.cpp:246-487): the argument checks are the reference's,
+// with its messages; column ranges outside the index and plan indices
+// outside the plans, which the reference reads past, raise.
+
+struct PartialPlan {
+  PlanHolder plan;
+  Tensor blob;  // device copy of the (unbound) plan blob
+};
+
+void check_partial_args(const Tensor& bloom_index, const Tensor& offsets, const Tensor& lengths,
+                        const c10::optional<Tensor>& query_plan_index, int64_t plan_count) {
+  TORCH_CHECK(bloom_index.scalar_type() == at::kLong, "bloom_index dtype must be Long");
+  TORCH_CHECK(offsets.dim() == 2, "selected_cluster_offsets dim must be 2, but got ", offsets.dim());
+  TORCH_CHECK(lengths.dim() == 2, "selected_cluster_lengths dim must be 2, but got ", lengths.dim());
+  TORCH_CHECK(offsets.scalar_type() == at::kLong, "selected_cluster_offsets dtype must be Long");
+  TORCH_CHECK(lengths.scalar_type() == at::kLong, "selected_cluster_lengths dtype must be Long");
+  const int64_t rows = offsets.size(0);
+  TORCH_CHECK(rows == lengths.size(0) && offsets.size(1) == lengths.size(1),
+              "selected_cluster_offsets must have same shape with selected_cluster_lengths, but got ",
+              offsets.sizes(), " vs ", lengths.sizes());
+  if (query_plan_index.has_value()) {
+    TORCH_CHECK(query_plan_index->dim() == 1, "query_plan_index dim must be 1, but got ",
+                query_plan_index->dim());
+    TORCH_CHECK(query_plan_index->size(0) == rows,
+                "query_plan count must be same with selected_cluster size[0], but got ",
+                query_plan_index->size(0), " vs ", rows);
+    TORCH_CHECK(query_plan_index->scalar_type() == at::kLong, "query_plan_index dtype must be Long");
+  } else {
+    TORCH_CHECK(plan_count == rows,
+                "query_plan_count must be equal to query_count if no query_plan_index, but got ",
+                plan_count, " vs ", rows);
+  }
+  TORCH_CHECK(bloom_index.dim() == 1, "bloom_index dim must be 1 for v2");
+}
+
+void prepare_partial_plan(PartialPlan& pp, const Tensor& plans_data, const Tensor& plans_offsets,
+                          int64_t k, int64_t hash_k, at::Device dev) {
+  TORCH_CHECK(plans_data.scalar_type() == at::kChar || plans_data.scalar_type() == at::kByte,
+              "bloom_query_plans_data must be int8");
+  TORCH_CHECK(plans_offsets.scalar_type() == at::kLong, "bloom_query_plans_offsets must be int64");
+  const Tensor pd = plans_data.to(at::kCPU).contiguous();
+  const Tensor po = plans_offsets.to(at::kCPU).contiguous();
+  check_st(st_search_plan_create(reinterpret_cast<const int8_t*>(pd.data_ptr()), pd.numel(),
+                                 po.data_ptr<int64_t>(), po.numel(), k, hash_k, &pp.plan.p),
+           "bloom_index_search_batch_return_partial_response");
+  const int64_t n = st_search_plan_blob_bytes(pp.plan.p);
+  Tensor host = at::empty({std::max<int64_t>(n, 1)}, at::TensorOptions().dtype(at::kByte).pinned_memory(true));
+  if (n) std::memcpy(host.data_ptr(), st_search_plan_blob(pp.plan.p), n);
+  pp.blob = host.to(dev, /*non_blocking=*/true);
+}
+
+// One index chunk: host-side layout (one copy of the cluster arrays to the
+// host: the response length sizes the output), then the kernel.
+std::tuple<Tensor, Tensor, Tensor> partial_chunk(const PartialPlan& pp, const Tensor& index_in,
+                                                 const Tensor& bbo_in, const Tensor& offsets,
+                                                 const Tensor& lengths,
+                                                 const c10::optional<Tensor>& query_plan_index) {
+  TORCH_CHECK(index_in.is_cuda(), "bloom_index must be a GPU tensor");
+  TORCH_CHECK(bbo_in.scalar_type() == at::kLong, "bloom_bundle_b_offsets must be int64");
+  TORCH_CHECK(bbo_in.device() == index_in.device(),
+              "bloom_bundle_b_offsets must be on the device of bloom_index");
+  TORCH_CHECK(bbo_in.numel() >= 1, "bloom_bundle_b_offsets must hold at least one entry");
+  const auto dev = index_in.device();
+  const Tensor index = index_in.contiguous(), bbo = bbo_in.contiguous();
+  const int64_t rows = offsets.size(0), clusters = offsets.size(1), n = rows * clusters;
+  const Tensor co = offsets.to(at::kCPU).contiguous(), cl = lengths.to(at::kCPU).contiguous();
+  Tensor pi;
+  if (query_plan_index.has_value()) pi = query_plan_index->to(at::kCPU).contiguous();
+  Tensor cumsum = at::empty({n}, at::kInt), first = at::empty({n}, at::kChar);
+  Tensor items = at::empty({std::max<int64_t>(n, 1) * static_cast<int64_t>(sizeof(st_partial_item))},
+                           at::TensorOptions().dtype(at::kByte).pinned_memory(true));
+  int64_t num_items = 0, total = 0;
+  check_st(st_search_plan_partial_items(pp.plan.p, co.data_ptr<int64_t>(), cl.data_ptr<int64_t>(), rows,
+                                        clusters, pi.defined() ? pi.data_ptr<int64_t>() : nullptr,
+                                        bbo.numel() - 1, cumsum.data_ptr<int32_t>(),
+                                        first.data_ptr<int8_t>(),
+                                        reinterpret_cast<st_partial_item*>(items.data_ptr()),
+                                        &num_items, &total),
+           "bloom_index_search_batch_return_partial_response");
+  Tensor mask = at::empty({total}, at::TensorOptions().dtype(at::kLong).device(dev));
+  if (num_items > 0) {
+    const Tensor items_d = items.to(dev, /*non_blocking=*/true);
+    check_st(st_bloom_index_search_partial(index.data_ptr<int64_t>(), index.numel(),
+                                           bbo.data_ptr<int64_t>(), bbo.numel() - 1, pp.plan.p,
+                                           pp.blob.data_ptr(),
+                                           reinterpret_cast<const st_partial_item*>(items_d.data_ptr()),
+                                           num_items, mask.data_ptr<int64_t>(), current_stream(index)),
+             "bloom_index_search_batch_return_partial_response");
+    // items_d is freed here; the caching allocator keeps it until the stream
+    // has used it (record_stream semantics of the current stream)
+  }
+  return {cumsum.to(dev), first.to(dev), mask};
+}
+
+std::tuple<Tensor, Tensor, Tensor> partial_gpu(const Tensor& bloom_index, const Tensor& bbo,
+                                               const Tensor& plans_data, const Tensor& plans_offsets,
+                                               const Tensor& offsets, const Tensor& lengths, int64_t k,
+                                               int64_t hash_k,
+                                               const c10::optional<Tensor>& query_plan_index) {
+  check_partial_args(bloom_index, offsets, lengths, query_plan_index, plans_offsets.numel() / 8);
+  TORCH_CHECK(bloom_index.is_cuda(), "bloom_index must be a GPU tensor");
+  c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(bloom_index.device());
+  PartialPlan pp;
+  prepare_partial_plan(pp, plans_data, plans_offsets, k, hash_k, bloom_index.device());
+  return partial_chunk(pp, bloom_index, bbo, offsets, lengths, query_plan_index);
+}
+
+std::tuple<Tensor, Tensor, Tensor> partial_cpu(const Tensor& bloom_index, const Tensor& bbo,
+                                               const Tensor& plans_data, const Tensor& plans_offsets,
+                                               const Tensor& offsets, const Tensor& lengths, int64_t k,
+                                               int64_t hash_k,
+                                               const c10::optional<Tensor>& query_plan_index) {
+  check_partial_args(bloom_index, offsets, lengths, query_plan_index, plans_offsets.numel() / 8);
+  const at::Device gpu = gpu_for_cpu_call();
+  auto [c, f, m] = partial_gpu(bloom_index.to(gpu), bbo.to(gpu), plans_data, plans_offsets, offsets,
+                               lengths, k, hash_k, query_plan_index);
+  return {c.cpu(), f.cpu(), m.cpu()};
+}
+
+// _multiple: the single-chunk op per chunk with one compiled plan; `fuse`
+// changes only the reference CUDA path's launch structure, not the outputs.
+std::tuple<std::vector<Tensor>, std::vector<Tensor>, std::vector<Tensor>> partial_multiple(
+    const std::vector<Tensor>& indices, const std::vector<Tensor>& bbos, const Tensor& plans_data,
+    const Tensor& plans_offsets, const std::vector<Tensor>& offsets,
+    const std::vector<Tensor>& lengths, int64_t k, int64_t hash_k,
+    const c10::optional<Tensor>& query_plan_index, bool /*fuse*/) {
+  const size_t n = indices.size();
+  TORCH_CHECK(n > 0, "bloom_index_search_batch_return_partial_response_multiple: "
+                     "list_bloom_index should not be empty.");
+  TORCH_CHECK(bbos.size() == n,
+              "list_bloom_index and list_bloom_bundle_b_offsets should have the same size, got ", n,
+              " vs ", bbos.size());
+  TORCH_CHECK(offsets.size() == n,
+              "list_bloom_index and list_selected_cluster_offsets should have the same size, got ", n,
+              " vs ", offsets.size());
+  TORCH_CHECK(lengths.size() == n,
+              "list_bloom_index and list_selected_cluster_lengths should have the same size, got ", n,
+              " vs ", lengths.size());
+  for (size_t i = 0; i < n; ++i)
+    check_partial_args(indices[i], offsets[i], lengths[i], query_plan_index, plans_offsets.numel() / 8);
+  const bool on_cpu = !indices[0].is_cuda();
+  const at::Device dev = on_cpu ? gpu_for_cpu_call() : indices[0].device();
+  c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(dev);
+  PartialPlan pp;
+  prepare_partial_plan(pp, plans_data, plans_offsets, k, hash_k, dev);
+  std::vector<Tensor> cs, fs, ms;
+  for (size_t i = 0; i < n; ++i) {
+    auto [c, f, m] = partial_chunk(pp, indices[i].to(dev), bbos[i].to(dev), offsets[i], lengths[i],
+                                   query_plan_index);
+    if (on_cpu) {
+      c = c.cpu();
+      f = f.cpu();
+      m = m.cpu();
+    }
+    cs.push_back(c);
+    fs.push_back(f);
+    ms.push_back(m);
+  }
+  return {cs, fs, ms};
+}
+
 // ------------------------------------------ compaction of matching ids
 // No reference operator: the reference's users call
 // mask[:, :num_docs].nonzero() on the search output (README.md:191-193).
@@ -474,6 +637,18 @@ TORCH_LIBRARY_FRAGMENT(st, m) {
   m.def(
       "generate_column_info_for_clusters(Tensor selected_cluster_offsets, "
       "Tensor selected_cluster_lengths) -> (Tensor, Tensor, Tensor)");
+  m.def(
+      "bloom_index_search_batch_return_partial_response(Tensor bloom_index, "
+      "Tensor bloom_bundle_b_offsets, Tensor bloom_query_plans_data, "
+      "Tensor bloom_query_plans_offsets, Tensor selected_cluster_offsets, "
+      "Tensor selected_cluster_lengths, int k, int hash_k, "
+      "Tensor? query_plan_index=None)-> (Tensor, Tensor, Tensor)");
+  m.def(
+      "bloom_index_search_batch_return_partial_response_multiple(Tensor[] list_bloom_index, "
+      "Tensor[] list_bloom_bundle_b_offsets, Tensor bloom_query_plans_data, "
+      "Tensor bloom_query_plans_offsets, Tensor[] list_selected_cluster_offsets, "
+      "Tensor[] list_selected_cluster_lengths, int k, int hash_k, "
+      "Tensor? query_plan_index=None, bool fuse=False)-> (Tensor[], Tensor[], Tensor[])");
   // Ops of this build without a reference counterpart: matching ids as CSR
   // (ids, row_offsets) instead of a mask.
   m.def("bloom_mask_to_ids(Tensor packed_mask, int num_docs, bool int64_ids=False) "
@@ -499,6 +674,8 @@ TORCH_LIBRARY_IMPL(st, CUDA, m) {
   m.impl("bloom_index_search_batch", TORCH_FN(search_gpu));
   m.impl("parse_expression_query_batch", TORCH_FN(parse_batch));
   m.impl("generate_column_info_for_clusters", TORCH_FN(column_info));
+  m.impl("bloom_index_search_batch_return_partial_response", TORCH_FN(partial_gpu));
+  m.impl("bloom_index_search_batch_return_partial_response_multiple", TORCH_FN(partial_multiple));
   m.impl("bloom_mask_to_ids", TORCH_FN(mask_to_ids_gpu));
   m.impl("bloom_index_search_batch_ids", TORCH_FN(search_ids_gpu));
   m.impl("filtered_topk", TORCH_FN(filtered_topk_gpu));
@@ -510,6 +687,8 @@ TORCH_LIBRARY_IMPL(st, CPU, m) {
   m.impl("bloom_index_search_batch", TORCH_FN(search_cpu_tensors));
   m.impl("parse_expression_query_batch", TORCH_FN(parse_batch));
   m.impl("generate_column_info_for_clusters", TORCH_FN(column_info));
+  m.impl("bloom_index_search_batch_return_partial_response", TORCH_FN(partial_cpu));
+  m.impl("bloom_index_search_batch_return_partial_response_multiple", TORCH_FN(partial_multiple));
   m.impl("bloom_mask_to_ids", TORCH_FN(mask_to_ids_cpu));
   m.impl("bloom_index_search_batch_ids", TORCH_FN(search_ids_cpu));
   m.impl("filtered_topk", TORCH_FN(filtered_topk_cpu));

@@ -187,3 +187,28 @@ def test_cpu_tensor_calls_fail_loudly_without_gpu():
         torch.ops.st.bloom_index_search_batch(torch.from_numpy(c["index"]), torch.from_numpy(c["bundle_b_offsets"]),
                                               torch.frombuffer(bytearray(data), dtype=torch.int8),
                                               torch.tensor(offs, dtype=torch.long), 3, 7, False)
+
+
+def test_partial_response_argument_errors_before_device_work():
+    """The cluster-restricted op checks its arguments as the reference does
+    (bloom_index_search.cpp:256-311) before any device work."""
+    import torch
+
+    import silvertorch_amd.ops._load_ops  # noqa: F401
+
+    st = torch.ops.st
+    idx = torch.zeros(64, dtype=torch.long)
+    bbo = torch.tensor([0, 2], dtype=torch.long)
+    pd = torch.zeros(8, dtype=torch.int8)
+    po = torch.zeros(8, dtype=torch.long)
+    co = torch.zeros((1, 1), dtype=torch.long)
+    with pytest.raises(RuntimeError, match="selected_cluster_offsets dim must be 2"):
+        st.bloom_index_search_batch_return_partial_response(idx, bbo, pd, po, co[0], co, 3, 7)
+    with pytest.raises(RuntimeError, match="selected_cluster_lengths dtype must be Long"):
+        st.bloom_index_search_batch_return_partial_response(idx, bbo, pd, po, co, co.int(), 3, 7)
+    with pytest.raises(RuntimeError, match="must have same shape"):
+        st.bloom_index_search_batch_return_partial_response(idx, bbo, pd, po, co, torch.zeros((1, 2), dtype=torch.long), 3, 7)
+    with pytest.raises(RuntimeError, match="query_plan_index dim must be 1"):
+        st.bloom_index_search_batch_return_partial_response(idx, bbo, pd, po, co, co, 3, 7, co)
+    with pytest.raises(RuntimeError, match="list_bloom_index should not be empty"):
+        st.bloom_index_search_batch_return_partial_response_multiple([], [], pd, po, [], [], 3, 7)
