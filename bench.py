@@ -199,6 +199,54 @@ def measure_ids(st, capi, O, bi, bo, pd, po, k, hk, N, Q, packed, steps, warmup)
     }
 
 
+def measure_partial(st, bi, bo, pd, po, k, hk, N, packed, steps):
+    """Cluster-restricted search (bloom_index_search_batch_return_partial_response)
+    on the cfg2 index and queries, IVF-style: the docs form 2,500 clusters of
+    4,000 docs and every query selects 16 of them (seeded).  Op time per call,
+    and a full check: every returned column word equals the packed search
+    output's word for that query and column."""
+    import numpy as np
+    import torch
+
+    Q = packed.shape[0]
+    csize, nclust, per_q = 4000, N // 4000, 16
+    rng = np.random.default_rng(42)
+    sel = np.stack([rng.choice(nclust, per_q, replace=False) for _ in range(Q)])
+    co = torch.from_numpy((sel * csize).astype(np.int64)).cuda()
+    cl = torch.full((Q, per_q), csize, dtype=torch.long, device="cuda")
+
+    def step():
+        return st.bloom_index_search_batch_return_partial_response(bi, bo, pd, po, co, cl, k, hk)
+
+    cs, first, mask = step()
+    torch.cuda.synchronize()
+    n = max(steps // 10, 5)
+    t = time.perf_counter()
+    for _ in range(n):
+        cs, first, mask = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t) * 1e3 / n
+    # full check against the packed search output
+    counts = torch.diff(cs.long(), prepend=torch.zeros(1, dtype=torch.long, device="cuda"))
+    first_col = (co // 64).reshape(-1)
+    rows = torch.arange(Q, device="cuda").repeat_interleave(per_q)
+    item = torch.repeat_interleave(torch.arange(Q * per_q, device="cuda"), counts)
+    within = torch.arange(mask.numel(), device="cuda") - (cs.long() - counts)[item]
+    want = packed[rows[item], first_col[item] + within]
+    ok = bool(torch.equal(mask, want)) and bool(torch.equal(first.long(), (co % 64).reshape(-1)))
+    log(f"partial response: {Q} queries x {per_q} clusters of {csize} docs, {mask.numel()} columns, "
+        f"{ms:.3f} ms/call, all columns equal the full search: {ok}")
+    if not ok:
+        sys.exit("parity failure in the partial response")
+    return {
+        "op": "bloom_index_search_batch_return_partial_response",
+        "workload": f"cfg2 index and queries; {nclust} clusters of {csize} docs, {per_q} per query",
+        "ms_per_call": ms, "columns": int(mask.numel()),
+        "doc_queries_per_s": int(mask.numel()) * 64 / (ms * 1e-3),
+        "note": "op wall time (host layout, one copy of the cluster arrays to the host, kernel)",
+    }
+
+
 def measure_build_cfg4(st, O):
     """cfg4: bloom_index_build on 100M docs, 4 features,
     per-doc value counts uniform in [1, 8], values uniform over 10M, K=3,
@@ -517,6 +565,7 @@ def main():
     ids_report = measure_ids(st, capi, O, bi, bo, pd, po, k, hk, N, Q, out if not args.bool_mask else None,
                              args.steps, args.warmup)
 
+    partial_report = None if args.bool_mask else measure_partial(st, bi, bo, pd, po, k, hk, N, out, args.steps)
     topk_report = None if args.no_topk else measure_topk(st, capi, args.steps)
     build4_report = None if args.no_build4 else measure_build_cfg4(st, O)
     cfg3_report = None if args.no_cfg3 else measure_search_cfg3(st, O)
@@ -561,6 +610,7 @@ def main():
         "build_cfg4": build4_report,
         "search_cfg3": cfg3_report,
         "ids": ids_report,
+        "partial": partial_report,
         "topk": topk_report,
     }
     print(json.dumps(result), flush=True)
