@@ -1,0 +1,101 @@
+"""The nn.Module surface (silvertorch_amd.modules) against the operators it
+wraps, after the reference's module tests
+(silvertorch/modules/tests/test_bloom_index_search_module.py,
+test_filter_query_parser_module.py).  Parser-module and builder-error tests
+run on the CPU; search-module tests need the GPU."""
+
+import numpy as np
+import pytest
+import torch
+
+import silvertorch_amd.ops._load_ops  # noqa: F401
+from oracle import oracle as O
+from oracle import parser_oracle as P
+from silvertorch_amd.modules import (BloomIndexSearchModule, BloomIndexSearchModuleBuilder,
+                                     FilterQueryParserModule, FilterQueryParserModuleBuilder)
+
+
+def _features(n=300, F=3):  # the reference tests' fixture shape (d * 100 + f values)
+    ids = torch.arange(F, dtype=torch.int32)
+    vals = torch.tensor([d * 100 + f for d in range(n) for f in range(F)], dtype=torch.long)
+    offs = torch.arange(n * F + 1, dtype=torch.long)
+    return ids, offs, vals
+
+
+def test_parser_module_matches_parser_bytes():
+    m = FilterQueryParserModule(hash_k=7)
+    exprs = ["0:0", "0:0 AND 1:1", "NOT 2:200 OR 1:101", ""]
+    max_stack, (data, offsets) = m(exprs, torch.ones(1, dtype=torch.long))
+    want_stack, want_data, want_offs = P.parse_batch(exprs, 7, True, 5)
+    assert max_stack == want_stack
+    assert data.dtype == torch.int8 and offsets.dtype == torch.long
+    assert data.numpy().tobytes() == want_data and offsets.tolist() == list(want_offs)
+
+
+def test_parser_module_builder():
+    m = FilterQueryParserModuleBuilder(hash_k=3, max_sub_queries=2).build()
+    assert isinstance(m, FilterQueryParserModule) and not m.training
+    assert (m.hash_k, m.max_sub_queries) == (3, 2)
+    exprs = ["1:1 | 2:2 | 3:3 | 4:4"]
+    _, (data, offsets) = m(exprs, torch.ones(1, dtype=torch.long))
+    _, want_data, want_offs = P.parse_batch(exprs, 3, True, 2)
+    assert data.numpy().tobytes() == want_data and offsets.tolist() == list(want_offs)
+
+
+def test_builder_needs_data():
+    with pytest.raises(ValueError, match="Either feature data"):
+        BloomIndexSearchModuleBuilder(k=3, hash_k=7).build()
+    with pytest.raises(ValueError, match="bloom_bundle_b_offsets must be set"):
+        BloomIndexSearchModuleBuilder(k=3, hash_k=7).set_bloom_index(torch.zeros(32, dtype=torch.long)).build()
+
+
+def test_search_module_buffers_and_state_dict():
+    m = BloomIndexSearchModule(k=3, hash_k=7)
+    assert set(dict(m.named_buffers())) == {"bloom_index", "bloom_bundle_b_offsets"}
+    m.set_bloom_index(torch.arange(64, dtype=torch.long))
+    m.set_bloom_bundle_b_offsets(torch.tensor([0, 2], dtype=torch.long))
+    fresh = BloomIndexSearchModule(k=3, hash_k=7)
+    fresh.load_state_dict(m.state_dict())
+    assert torch.equal(fresh.bloom_index, m.bloom_index)
+    assert torch.equal(fresh.bloom_bundle_b_offsets, m.bloom_bundle_b_offsets)
+
+
+@pytest.fixture()
+def gpu():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a HIP device")
+    return torch.device("cuda")
+
+
+@pytest.mark.gpu
+def test_search_module_forward_matches_op_and_oracle(gpu):
+    ids, offs, vals = _features()
+    index, bbo = torch.ops.st.bloom_index_build(ids.to(gpu), offs.to(gpu), vals.to(gpu), 5.0, 3)
+    m = BloomIndexSearchModuleBuilder(k=3, hash_k=7).set_bloom_index(index).set_bloom_bundle_b_offsets(bbo).build()
+    _, (pd, po) = FilterQueryParserModule(hash_k=7)(["0:0", "1:101 AND 2:102", "NOT 0:0"],
+                                                     torch.ones(1, dtype=torch.long))
+    boolm = m(pd, po)
+    packed = m(pd, po, return_bool_mask=False)
+    assert boolm.dtype == torch.bool and boolm.shape == (3, 2048) and packed.dtype == torch.long
+    want = O.search_packed(index.cpu().numpy(), bbo.cpu().numpy(), pd.numpy(), po.numpy(), 3, 7)
+    np.testing.assert_array_equal(packed.cpu().numpy(), want)
+    np.testing.assert_array_equal(boolm.cpu().numpy(), O.unpack_bool(want))
+    assert boolm[0, 0] and boolm[1, 1] and not boolm[2, 0]
+
+
+@pytest.mark.gpu
+def test_builder_from_features_moves_and_reloads(gpu):
+    ids, offs, vals = _features()
+    m = (BloomIndexSearchModuleBuilder(k=3, hash_k=4).set_feature_data(ids, offs, vals)
+         .set_b_multiplier(3.0).set_device(gpu).build())
+    assert m.bloom_index.device.type == "cuda" and m.bloom_bundle_b_offsets.device.type == "cuda"
+    # the reference builder builds with hash_k bits per term
+    want_index, want_bbo = O.bloom_build(ids.numpy(), offs.numpy(), vals.numpy(), 3.0, 4)
+    np.testing.assert_array_equal(m.bloom_index.cpu().numpy(), want_index)
+    np.testing.assert_array_equal(m.bloom_bundle_b_offsets.cpu().numpy(), want_bbo)
+    # persisted and reloaded into a fresh module, the search is unchanged
+    fresh = BloomIndexSearchModule(k=3, hash_k=4)
+    fresh.load_state_dict({k: v.cpu() for k, v in m.state_dict().items()})
+    fresh = fresh.to(gpu)
+    _, (pd, po) = FilterQueryParserModule(hash_k=4)(["1:1", "0:200 OR 2:5"], torch.ones(1, dtype=torch.long))
+    assert torch.equal(fresh(pd, po, False), m(pd, po, False))
