@@ -616,8 +616,8 @@ __device__ __forceinline__ uint32_t u32x4_get(const u32x4& v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 
-// Stores this lane's 16 bytes of output row `row` on the bundle (and, in
-// kOutCounts mode, the row's match count on the bundle, summed over the
+// Stores this lane's 16 bytes of packed output row `row` on the bundle (and,
+// in kOutCounts mode, the row's match count on the bundle, summed over the
 // lane's 16-lane group).  The u32s are, in order, the low and high halves of
 // words 2s and 2s + 1 (s = lane & 15); a word's high half holds its first 32
 // docs.
@@ -625,20 +625,11 @@ template <int kOut>
 __device__ __forceinline__ void store_quad(const SearchArgs& a, int lane, int64_t bundle,
                                            uint32_t row, u32x4 v) {
   const uint32_t s = static_cast<uint32_t>(lane & 15);
-  if constexpr (kOut == kOutBool) {
-    ST_GLOBAL char* dst = (ST_GLOBAL char*)(static_cast<char*>(a.out) +
-                                            static_cast<int64_t>(row) * (a.out_cols * 64) +
-                                            bundle * kDocsPerBundle + s * 128);
-    store_bool32(dst, v.y);
-    store_bool32(dst + 32, v.x);
-    store_bool32(dst + 64, v.w);
-    store_bool32(dst + 96, v.z);
-  } else {
-    ST_GLOBAL u32x4* dst = (ST_GLOBAL u32x4*)(static_cast<char*>(a.out) +
-                                              static_cast<int64_t>(row) * (a.out_cols * 8) +
-                                              bundle * 256 + s * 16);
-    __builtin_nontemporal_store(v, dst);
-  }
+  static_assert(kOut != kOutBool, "bool output of a quad goes through store_quad_bool");
+  ST_GLOBAL u32x4* dst = (ST_GLOBAL u32x4*)(static_cast<char*>(a.out) +
+                                            static_cast<int64_t>(row) * (a.out_cols * 8) +
+                                            bundle * 256 + s * 16);
+  __builtin_nontemporal_store(v, dst);
   if constexpr (kOut == kOutCounts) {
     const int64_t first = bundle * kDocsPerBundle + static_cast<int64_t>(s) * 128;
     uint32_t n = __builtin_popcount(v.y & valid_doc_mask(first, a.num_docs)) +
@@ -648,6 +639,44 @@ __device__ __forceinline__ void store_quad(const SearchArgs& a, int lane, int64_
 #pragma unroll
     for (int m = 8; m >= 1; m >>= 1) n += __shfl_xor(n, m, 16);
     if (s == 0) a.counts[static_cast<int64_t>(row) * a.num_bundles + bundle] = n;
+  }
+}
+
+// Bool output of a quad: the four 2 KB rows of the wave's four programs,
+// each written as two 1 KB stores of 16 consecutive bytes per lane.  Lane l
+// of a store covers docs 1024 j + 16 l .. +15, i.e. one half of a packed
+// 32-doc word that sits in another lane of the program's group: the four
+// components of that lane are fetched with ds_bpermute and the lane's one is
+// kept.  Called by all lanes (the permutes need the whole wave).
+__device__ __forceinline__ void store_quad_bool(const SearchArgs& a, int lane, int64_t bundle,
+                                                uint32_t info, u32x4 v) {
+  const uint32_t t = ((static_cast<uint32_t>(lane) >> 1) ^ 1u) & 3u;  // component wanted
+  const uint32_t shift = (lane & 1) * 16;                             // docs 0-15 or 16-31
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t gi = __builtin_amdgcn_readlane(info, 16 * g);
+    if (!(gi & kSlotValid)) continue;
+    ST_GLOBAL char* base = (ST_GLOBAL char*)(static_cast<char*>(a.out) +
+                                             static_cast<int64_t>(gi >> kSlotRowShift) *
+                                                 (a.out_cols * 64) +
+                                             bundle * kDocsPerBundle);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int src = 16 * g + (((32 * j + (lane >> 1)) ^ 1) >> 2);
+      const int addr = src * 4;
+      const uint32_t c0 = __builtin_amdgcn_ds_bpermute(addr, v.x);
+      const uint32_t c1 = __builtin_amdgcn_ds_bpermute(addr, v.y);
+      const uint32_t c2 = __builtin_amdgcn_ds_bpermute(addr, v.z);
+      const uint32_t c3 = __builtin_amdgcn_ds_bpermute(addr, v.w);
+      const uint32_t p = t == 0 ? c0 : (t == 1 ? c1 : (t == 2 ? c2 : c3));
+      const uint32_t y = __builtin_bitreverse32(p) >> shift;
+      u32x4 o;
+      o.x = ((y & 0xFu) * 0x00204081u) & 0x01010101u;
+      o.y = (((y >> 4) & 0xFu) * 0x00204081u) & 0x01010101u;
+      o.z = (((y >> 8) & 0xFu) * 0x00204081u) & 0x01010101u;
+      o.w = (((y >> 12) & 0xFu) * 0x00204081u) & 0x01010101u;
+      __builtin_nontemporal_store(o, (ST_GLOBAL u32x4*)(base + 1024 * j + 16 * lane));
+    }
   }
 }
 
@@ -690,9 +719,11 @@ __device__ __forceinline__ void eval_quads(const SearchArgs& a, const u32x4* til
           acc = (acc | grp) & (t ^ neg);
         }
       }
-      if (info & kSlotValid) {
-        u32x4 v = res | acc;
-        if (info & kSlotComplement) v = ~v;
+      u32x4 v = res | acc;
+      if (info & kSlotComplement) v = ~v;
+      if constexpr (kOut == kOutBool) {
+        store_quad_bool(a, lane, bundle, info, v);
+      } else if (info & kSlotValid) {
         store_quad<kOut>(a, lane, bundle, info >> kSlotRowShift, v);
       }
     }
