@@ -10,10 +10,12 @@
 // id -1 and score -inf (the reference's padding, fused_kmean_ann.cpp:139-167).
 //
 // Scoring is a dense bf16 contraction on the matrix cores
-// (v_mfma_f32_32x32x16_bf16): each wave holds the embeddings of 64 docs in
-// registers (two 32-doc A operands) and sweeps the query chunk staged in LDS
-// 32 queries at a time, so one LDS read of a query fragment feeds two MFMAs.
-// A 32 x 32 tile whose filter bits are all zero is skipped.
+// (v_mfma_f32_32x32x16_bf16): each wave keeps the fragments of its 32 or 64
+// queries in registers (B operands) for the whole launch, the workgroup
+// streams 64 KB steps of doc rows and their filter words through LDS (the
+// next step is loaded into registers while the current one is scored), and
+// one LDS read of a doc fragment feeds the MFMAs of every query tile of the
+// wave.  A doc tile whose filter bits are all zero for the wave is skipped.
 //
 // Selection is exact and runs in rounds over growing doc ranges: a scored
 // pair enters query q's candidate list when it passes the filter and its
@@ -27,6 +29,7 @@
 #include <algorithm>
 #include <cmath>
 #include <mutex>
+#include <utility>
 #include <vector>
 
 #include "st_common.hpp"
@@ -42,8 +45,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kScoreThreads = 512;   // 8 waves; one workgroup per CU
 constexpr int kScoreWaves = kScoreThreads / 64;
-constexpr int kDocsPerWave = 64;     // two 32-doc MFMA A operands
-constexpr int kDocsPerStep = kScoreWaves * kDocsPerWave;
 constexpr int kQueryTile = 32;
 constexpr int kLdsBytes = 160 * 1024;
 constexpr int kSelectThreads = 256;
@@ -87,176 +88,275 @@ __global__ void topk_reset_kernel(TopkState st, int64_t num_queries) {
   if (i == 0) st.overflow[0] = 0u;
 }
 
-// LDS bytes per query of a chunk: its row (D bf16) plus, per wave, the two
-// u32 filter words of the wave's 64 docs.
+// Scoring geometry for embedding dimension D.  Each of the 8 waves keeps
+// QT query tiles (32 queries each) as MFMA B operands in registers, so one
+// launch pass covers 8 * 32 * QT queries; the workgroup streams its docs in
+// steps of kDocs rows (32 KB of embeddings) through two LDS buffers, each with
+// the queries' filter words for those docs.
 template <int D>
-constexpr int lds_bytes_per_query() {
-  return D * 2 + kScoreWaves * 8;
+struct ScoreShape {
+  static constexpr int S = D / 16;                     // MFMA k-steps
+  static constexpr int QT = D <= 128 ? 2 : 1;          // query tiles per wave
+  static constexpr int kQueries = kScoreWaves * kQueryTile * QT;  // per pass
+  static constexpr int kStepBytes = 32768;
+  static constexpr int kDocs = kStepBytes / (2 * D);   // docs per step
+  static constexpr int kDocTiles = kDocs / 32;
+  static constexpr int kPieces = D / 8;                // 16-byte pieces per doc row
+  // Rows padded by 16 bytes: the 16 rows an A-operand read serves at once
+  // start 4 banks apart, and every piece sits at a fixed offset of its row.
+  static constexpr int kRowBytes = 2 * D + 16;
+  static constexpr int kCols = kDocs / 64;             // mask columns per step
+  static constexpr int kMaskWords = kDocTiles + 1;     // u32 per query, padded
+  static constexpr int kDocBuf = kDocs * kRowBytes;
+  static constexpr int kMaskBuf = kQueries * kMaskWords * 4;
+  static constexpr int kBuf = kDocBuf + kMaskBuf;
+  static constexpr int kLds = 2 * kBuf;
+  static constexpr int kDocLoads = kStepBytes / 16 / kScoreThreads;  // u32x4 per thread
+  static constexpr int kMaskLoads = (kQueries * kCols + kScoreThreads - 1) / kScoreThreads;
+  static_assert(kLds <= kLdsBytes, "two steps must fit in LDS");
+  static_assert(kDocs % 64 == 0 && kStepBytes % (16 * kScoreThreads) == 0, "step shape");
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Filter bits of the 32 docs from g0 that lie below hi (doc g0 at bit 31).
+__device__ __forceinline__ uint32_t valid_doc_mask(int64_t g0, int64_t hi) {
+  const int64_t left = hi - g0;
+  return left >= 32 ? ~0u : (left <= 0 ? 0u : ~0u << (32 - static_cast<int>(left)));
 }
 
-template <int D>
-constexpr int64_t query_chunk() {
-  return (kLdsBytes / lds_bytes_per_query<D>()) / kQueryTile * kQueryTile;
+// acc[j] of a 32 x 32 MFMA result holds doc row 8 (j / 4) + 4 h + j % 4 of
+// the tile for lane half h = lane / 32 (query column lane % 32).  Returns the
+// filter bits of those rows, row of acc[j] at bit j (doc row r of m at bit
+// 31 - r).
+__device__ __forceinline__ uint32_t lane_rows(uint32_t m, int h) {
+  uint32_t x = (__builtin_bitreverse32(m) >> (4 * h)) & 0x0F0F0F0Fu;
+  x = (x | (x >> 4)) & 0x00FF00FFu;
+  return (x | (x >> 8)) & 0xFFFFu;
 }
 
-// Scores docs [lo, hi) against queries [q_begin, q_begin + q_count).
-// LDS: the query rows (16-byte pieces XOR-swizzled by row, so the 32 rows a
-// wave reads at once hit distinct banks), then per wave the filter words of
-// its 64 docs for every query of the chunk.
+// Whether this lane's part of a 32 x 32 score tile (16 docs of its query)
+// may hold a candidate: a filter bit, and a score at the threshold.
+__device__ __forceinline__ bool tile_gate(const f32x16& acc, uint32_t m, float th) {
+  float mx = acc[0];
+#pragma unroll
+  for (int j = 1; j < 16; ++j) mx = fmaxf(mx, acc[j]);
+  return m != 0u && mx >= th;
+}
+
+// Candidates of one 32 x 32 score tile (docs x this lane's query): pairs that
+// pass the filter with a score >= th go to the query's candidate list.
+// Called by the whole wave.
+__device__ __forceinline__ void tile_candidates(const TopkState& st, const f32x16& acc, uint32_t m,
+                                                float th, int64_t q, int64_t doc0, int lane) {
+  uint32_t ge = 0u;
+#pragma unroll
+  for (int j = 15; j >= 0; --j) ge = (ge << 1) | (acc[j] >= th ? 1u : 0u);
+  const int h = lane >> 5;
+  uint32_t hits = ge & lane_rows(m, h);
+  if (__ballot(hits != 0u) == 0) return;
+  const uint32_t cnt = __builtin_popcount(hits);
+  const uint32_t cnt_pair = __shfl_xor(cnt, 32, 64);  // lanes l, l ^ 32: same query
+  uint32_t base = 0u;
+  if (lane < 32 && cnt + cnt_pair > 0u) base = atomicAdd(st.counts + q, cnt + cnt_pair);
+  const uint32_t base_pair = __shfl_xor(base, 32, 64);
+  uint32_t slot = lane < 32 ? base : base_pair + cnt_pair;
+  while (__ballot(hits != 0u) != 0) {
+    if (hits != 0u) {
+      const int j = __builtin_ctz(hits);
+      hits &= hits - 1u;
+      float v = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v = j == i ? acc[i] : v;
+      const int64_t doc = doc0 + 8 * (j >> 2) + 4 * h + (j & 3);
+      if (slot < st.capacity) st.cand[q * st.capacity + slot] = make_key(v, doc);
+      else atomicOr(st.overflow, 1u);
+      ++slot;
+    }
+  }
+}
+
+// Scores docs [lo, hi) against queries [q_begin, q_begin + q_count)
+// (q_count <= ScoreShape<D>::kQueries).  Wave w holds queries
+// w * 32 * QT + 32 t + (lane & 31) of tile t as B operands (lanes 32-63
+// carry the second half of each 16-wide k step); each workgroup takes one
+// contiguous run of steps.  A step's rows and filter words are loaded into
+// registers while the step before is scored and stored into the other LDS
+// buffer after it, so each step needs one barrier.
 template <int D>
 __global__ __launch_bounds__(kScoreThreads) void topk_score_kernel(
     const uint16_t* __restrict__ emb, const uint16_t* __restrict__ qv,
-    const uint32_t* __restrict__ mask32, int64_t num_columns, int64_t q_begin,
-    int64_t q_count, int64_t lo, int64_t hi, TopkState st) {
-  constexpr int S = D / 16;        // MFMA k-steps
-  constexpr int kPieces = D / 8;   // 16-byte pieces per row
-  // 16 lanes read at once on gfx950 (64 banks): spread 16 rows.
-  constexpr int kSwz = kPieces < 16 ? kPieces - 1 : 15;
+    const uint64_t* __restrict__ mask64, int64_t num_columns, int64_t q_begin,
+    int64_t q_count, int64_t lo, int64_t hi, int64_t steps_per_group, TopkState st) {
+  using SS = ScoreShape<D>;
+  constexpr int S = SS::S, QT = SS::QT;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int q_tiles = static_cast<int>((q_count + kQueryTile - 1) / kQueryTile);
-  const int rows = q_tiles * kQueryTile;
-  uint32_t* masks = reinterpret_cast<uint32_t*>(lds + static_cast<int64_t>(rows) * D * 2) +
-                    wave * rows * 2;  // [tile][64]: lanes 0-31 docs 0-31, 32-63 docs 32-63
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int h = lane >> 5;
 
-  for (int i = threadIdx.x; i < rows * kPieces; i += kScoreThreads) {
-    const int r = i / kPieces, c = i - r * kPieces;
-    bf16x8 v = {};
-    if (r < q_count) v = *reinterpret_cast<const bf16x8*>(qv + (q_begin + r) * D + c * 8);
-    *reinterpret_cast<bf16x8*>(lds + r * (D * 2) + ((c ^ (r & kSwz)) << 4)) = v;
+  const int64_t first = lo + static_cast<int64_t>(blockIdx.x) * steps_per_group * SS::kDocs;
+  const int64_t last = min(hi, first + steps_per_group * SS::kDocs);
+  if (first >= last) return;  // whole workgroup
+
+  // This wave's query fragments (zero past q_count) and entry thresholds
+  // (fixed for the launch).
+  bf16x8 b[QT][S];
+  int ql[QT];
+  float th[QT];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    ql[t] = (wave * QT + t) * kQueryTile + (lane & 31);
+    const bool valid = ql[t] < q_count;
+    const uint16_t* row = qv + (q_begin + (valid ? ql[t] : 0)) * D + h * 8;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      b[t][s] = *reinterpret_cast<const bf16x8*>(row + s * 16);
+      if (!valid) b[t][s] = bf16x8{};
+    }
+    th[t] = st.thr[q_begin + (valid ? ql[t] : 0)];
   }
-  __syncthreads();
 
-  for (int64_t base = lo + static_cast<int64_t>(blockIdx.x) * kDocsPerStep; base < hi;
-       base += static_cast<int64_t>(gridDim.x) * kDocsPerStep) {
-    const int64_t d0 = base + wave * kDocsPerWave;  // first doc of this wave
-    if (d0 >= hi) continue;                         // wave-uniform
-    // Filter words of the wave's 64 docs for every query: docs 0-31 of a
-    // word are its high half, the second u32 in memory (d0 is a multiple of
-    // 64 within the round).
-    {
-      constexpr int kBatch = 16;  // loads in flight before the LDS stores
-      const int64_t col = d0 >> 6;
-      const int half = lane >> 5;
-      const bool has = half == 0 || d0 + 32 < hi;
-      // docs at or past hi never pass (bit 31 is the half-word's first doc)
-      const int64_t left = hi - (d0 + 32 * half);
-      const uint32_t valid = left >= 32 ? ~0u : (left <= 0 ? 0u : ~0u << (32 - static_cast<int>(left)));
-      for (int t0 = 0; t0 < q_tiles; t0 += kBatch) {
-        uint32_t mv[kBatch];
-        // Unconditional loads from a valid address (selected afterwards), so
-        // that all of them are in flight before the first is waited for.
+  u32x4 dpre[SS::kDocLoads];
+  uint64_t mpre[SS::kMaskLoads];
+  // Step d0's rows and filter words into registers: rows at or past hi read
+  // as zero, and so do columns past the last and queries past the chunk.
+  // d0 is a multiple of 64; a mask row is only 8-byte aligned.
+  auto prefetch = [&](int64_t d0) {
+    const int64_t rows = hi - d0 < SS::kDocs ? hi - d0 : SS::kDocs;
+    const u32x4* src = reinterpret_cast<const u32x4*>(emb + d0 * D);
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          const int64_t ql = static_cast<int64_t>(t0 + u) * kQueryTile + (lane & 31);
-          const bool ok = t0 + u < q_tiles && ql < q_count && has;
-          const int64_t idx = ok ? (q_begin + ql) * 2 * num_columns + 2 * col + 1 - half : 0;
-          mv[u] = mask32[idx];
-          mv[u] = ok ? mv[u] & valid : 0u;
-        }
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u)
-          if (t0 + u < q_tiles) masks[(t0 + u) * 64 + lane] = mv[u];
-      }
+    for (int i = 0; i < SS::kDocLoads; ++i) {
+      const int c = tid + i * kScoreThreads;
+      dpre[i] = (c / SS::kPieces < rows) ? __builtin_nontemporal_load(src + c) : u32x4{0, 0, 0, 0};
     }
-    bf16x8 a0[S], a1[S];
-    {
-      const int kofs = (lane >> 5) * 8;
-      // Rows past hi read row hi - 1 (valid) and are zeroed afterwards.
-      const int64_t da = d0 + (lane & 31), db = da + 32;
-      const int64_t ra = da < hi ? da : hi - 1, rb = db < hi ? db : hi - 1;
+    const int64_t col0 = d0 >> 6;
 #pragma unroll
-      for (int s = 0; s < S; ++s) {
-        a0[s] = *reinterpret_cast<const bf16x8*>(emb + ra * D + s * 16 + kofs);
-        a1[s] = *reinterpret_cast<const bf16x8*>(emb + rb * D + s * 16 + kofs);
-      }
-      if (da >= hi) {
-#pragma unroll
-        for (int s = 0; s < S; ++s) a0[s] = bf16x8{};
-      }
-      if (db >= hi) {
-#pragma unroll
-        for (int s = 0; s < S; ++s) a1[s] = bf16x8{};
-      }
+    for (int i = 0; i < SS::kMaskLoads; ++i) {
+      const int w = tid + i * kScoreThreads;
+      const int qq = w / SS::kCols, cc = w - qq * SS::kCols;
+      const bool ok = qq < q_count && col0 + cc < num_columns;
+      mpre[i] = ok ? mask64[(q_begin + qq) * num_columns + col0 + cc] : 0ull;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    float th_next = st.thr[q_begin + ((lane & 31) < q_count ? (lane & 31) : 0)];
-    for (int t = 0; t < q_tiles; ++t) {
-      const int ql = t * kQueryTile + (lane & 31);  // query of this lane's column
-      const bool qvalid = ql < q_count;
-      const int64_t q = q_begin + ql;
-      const float th = qvalid ? th_next : INFINITY;
-      {  // threshold of the next tile, one tile ahead (clamped address)
-        const int qn = ql + kQueryTile;
-        th_next = st.thr[q_begin + (qn < q_count ? qn : 0)];
-      }
-      // lane's column: docs 0-31 in slot (lane & 31), docs 32-63 in slot 32 + (lane & 31)
-      const uint32_t m0 = masks[t * 64 + (lane & 31)];
-      const uint32_t m1 = masks[t * 64 + 32 + (lane & 31)];
-      if (__ballot((m0 | m1) != 0u) == 0) continue;  // no filter bit in the tile
-      // All query fragments first (one LDS latency per tile), then the two
-      // MFMA chains; a half-tile without filter bits still runs (rare at
-      // useful selectivities, and cheaper than a branch per MFMA).
-      f32x16 acc0 = {}, acc1 = {};
-      const uint8_t* qrow = lds + ql * (D * 2);
-      const int sw = ql & kSwz;
-      bf16x8 b[S];
+  };
+  // The registers into LDS buffer buf, with the filter bits of docs at or
+  // past hi cleared.  A column word holds docs 0-31 in its high half.
+  auto stage = [&](int buf, int64_t d0) {
+    uint8_t* docs = lds + buf * SS::kBuf;
+    uint32_t* masks = reinterpret_cast<uint32_t*>(docs + SS::kDocBuf);
 #pragma unroll
-      for (int s = 0; s < S; ++s)
-        b[s] = *reinterpret_cast<const bf16x8*>(qrow + (((2 * s + (lane >> 5)) ^ sw) << 4));
+    for (int i = 0; i < SS::kDocLoads; ++i) {
+      const int c = tid + i * kScoreThreads;
+      const int r = c / SS::kPieces, k = c - r * SS::kPieces;
+      *reinterpret_cast<u32x4*>(docs + r * SS::kRowBytes + k * 16) = dpre[i];
+    }
 #pragma unroll
-      for (int s = 0; s < S; ++s) {
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[s], b[s], acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[s], b[s], acc1, 0, 0, 0);
-      }
-      // acc[j] holds doc row 8*(j/4) + 4*(lane/32) + j%4 of the tile, query
-      // column lane % 32.
-      {
-        // Gate on the lane maxima (no score of the tile at the threshold),
-        // then per-lane hit bits, one atomic per query per tile for a run of
-        // slots, and the writes.
-        float mx = fmaxf(acc0[0], acc1[0]);
+    for (int i = 0; i < SS::kMaskLoads; ++i) {
+      const int w = tid + i * kScoreThreads;
+      if (w >= SS::kQueries * SS::kCols) continue;
+      const int qq = w / SS::kCols, cc = w - qq * SS::kCols;
+      const int64_t g0 = d0 + 64 * cc;
+      uint32_t* dst = masks + qq * SS::kMaskWords + 2 * cc;
+      dst[0] = static_cast<uint32_t>(mpre[i] >> 32) & valid_doc_mask(g0, hi);
+      dst[1] = static_cast<uint32_t>(mpre[i]) & valid_doc_mask(g0 + 32, hi);
+    }
+  };
+
+  prefetch(first);
+  stage(0, first);
+  if (first + SS::kDocs < last) prefetch(first + SS::kDocs);
+  __syncthreads();
+  // Scored tiles whose epilogue is still to run (two accumulator sets).
+  f32x16 acc[2][QT];
+  uint32_t mb[2][QT];
+  int64_t docb[2] = {0, 0};
+  bool pend[2] = {false, false};
 #pragma unroll
-        for (int j = 1; j < 16; ++j) mx = fmaxf(mx, fmaxf(acc0[j], acc1[j]));
-        if (__ballot(mx >= th) == 0) continue;
-        uint32_t hits = 0u;
+  for (int x = 0; x < 2; ++x)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int r = 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-          const bool h0 = ((m0 >> (31 - r)) & 1u) && acc0[j] >= th;
-          const bool h1 = ((m1 >> (31 - r)) & 1u) && acc1[j] >= th;
-          hits |= (h0 ? 1u << j : 0u) | (h1 ? 1u << (16 + j) : 0u);
-        }
-        if (__ballot(hits != 0u) == 0) continue;
-        const uint32_t cnt = __builtin_popcount(hits);
-        const uint32_t cnt_pair = __shfl_xor(cnt, 32, 64);  // lanes l, l ^ 32: same query
-        uint32_t base = 0u;
-        if (lane < 32 && cnt + cnt_pair > 0u) base = atomicAdd(st.counts + q, cnt + cnt_pair);
-        const uint32_t base_pair = __shfl_xor(base, 32, 64);
-        uint32_t slot = lane < 32 ? base : base_pair + cnt_pair;
-        while (__ballot(hits != 0u) != 0) {
-          if (hits != 0u) {
-            const int j = __builtin_ctz(hits);
-            hits &= hits - 1u;
-            const int jj = j & 15;
-            const bool second = j >= 16;
-            float v = 0.0f;
+    for (int t = 0; t < QT; ++t) {
+      acc[x][t] = f32x16{};
+      mb[x][t] = 0u;
+    }
+  int buf = 0;
+  for (int64_t d0 = first; d0 < last; d0 += SS::kDocs, buf ^= 1) {
+    const uint8_t* docs = lds + buf * SS::kBuf;
+    const uint32_t* masks = reinterpret_cast<const uint32_t*>(docs + SS::kDocBuf);
+    const int tiles = static_cast<int>(min<int64_t>(SS::kDocTiles, (last - d0 + 31) / 32));
+    uint32_t m[QT][SS::kDocTiles];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v = jj == i ? (second ? acc1[i] : acc0[i]) : v;
-            const int64_t doc = d0 + (second ? 32 : 0) + 8 * (jj >> 2) + 4 * (lane >> 5) + (jj & 3);
-            if (slot < st.capacity) st.cand[q * st.capacity + slot] = make_key(v, doc);
-            else atomicOr(st.overflow, 1u);
-            ++slot;
+    for (int t = 0; t < QT; ++t)
+#pragma unroll
+      for (int dt = 0; dt < SS::kDocTiles; ++dt)
+        m[t][dt] = masks[ql[t] * SS::kMaskWords + dt];  // zero past q_count
+    // A operands: doc row 32 dt + (lane & 31), k half h, read from LDS just
+    // ahead of their MFMAs.  The epilogue of a tile is deferred to the next
+    // tile, whose MFMAs its gate is interleaved with, so each wave keeps the
+    // matrix cores fed by itself.  Tiles alternate between the two
+    // accumulator sets; pend[x] says set x holds a tile still to finish.
+    const uint8_t* arow = docs + (lane & 31) * SS::kRowBytes + h * 16;
+#pragma unroll
+    for (int dt = 0; dt < SS::kDocTiles; ++dt) {
+      if (dt < tiles) {
+        const int cb = dt & 1, pb = cb ^ 1;
+        bool any = false;
+#pragma unroll
+        for (int t = 0; t < QT; ++t) any |= m[t][dt] != 0u;
+        const bool run = __ballot(any) != 0;  // some filter bit in this doc tile
+        bool gate[QT];
+        if (run) {
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            const bf16x8 av = *reinterpret_cast<const bf16x8*>(arow + dt * 32 * SS::kRowBytes + s * 32);
+#pragma unroll
+            for (int t = 0; t < QT; ++t)
+              acc[cb][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b[t][s], s == 0 ? f32x16{} : acc[cb][t], 0, 0, 0);
           }
+#pragma unroll
+          for (int t = 0; t < QT; ++t) gate[t] = tile_gate(acc[pb][t], mb[pb][t], th[t]) & pend[pb];
+          // three fragment reads ahead, then MFMAs with the gate's VALU work
+          // and the remaining reads between them
+          __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+#pragma unroll
+          for (int i = 0; i < S; ++i) {
+#pragma unroll
+            for (int t = 0; t < QT; ++t) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+              __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+        } else {
+#pragma unroll
+          for (int t = 0; t < QT; ++t) gate[t] = tile_gate(acc[pb][t], mb[pb][t], th[t]) & pend[pb];
         }
+#pragma unroll
+        for (int t = 0; t < QT; ++t)
+          if (__ballot(gate[t]) != 0)
+            tile_candidates(st, acc[pb][t], mb[pb][t], th[t], q_begin + ql[t], docb[pb], lane);
+        pend[pb] = false;
+        pend[cb] = run;
+#pragma unroll
+        for (int t = 0; t < QT; ++t) mb[cb][t] = m[t][dt];
+        docb[cb] = d0 + dt * 32;
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int64_t next = d0 + SS::kDocs;
+    if (next < last) {
+      stage(buf ^ 1, next);
+      if (next + SS::kDocs < last) prefetch(next + SS::kDocs);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    if (pend[x]) {
+#pragma unroll
+      for (int t = 0; t < QT; ++t)
+        if (__ballot(tile_gate(acc[x][t], mb[x][t], th[t])) != 0)
+          tile_candidates(st, acc[x][t], mb[x][t], th[t], q_begin + ql[t], docb[x], lane);
+    }
   }
 }
 
@@ -330,24 +430,23 @@ void check_launch(const char* what) {
 }
 
 template <int D>
-void launch_score(const uint16_t* emb, const uint16_t* qv, const uint32_t* mask32,
+void launch_score(const uint16_t* emb, const uint16_t* qv, const uint64_t* mask64,
                   int64_t num_columns, int64_t num_queries, int64_t lo, int64_t hi,
                   const TopkState& st, hipStream_t s) {
-  const int64_t q_chunk = query_chunk<D>();
-  const int64_t steps = (hi - lo + kDocsPerStep - 1) / kDocsPerStep;
-  const int grid = static_cast<int>(std::max<int64_t>(
-      1, std::min<int64_t>(steps, static_cast<int64_t>(cu_count()))));
-  for (int64_t qb = 0; qb < num_queries; qb += q_chunk) {
-    const int64_t qn = std::min(q_chunk, num_queries - qb);
-    const size_t lds = static_cast<size_t>((qn + kQueryTile - 1) / kQueryTile * kQueryTile) *
-                       lds_bytes_per_query<D>();
-    hipLaunchKernelGGL(topk_score_kernel<D>, dim3(grid), dim3(kScoreThreads), lds, s, emb, qv,
-                       mask32, num_columns, qb, qn, lo, hi, st);
+  using SS = ScoreShape<D>;
+  // One contiguous run of steps per workgroup, one workgroup per CU.
+  const int64_t steps = (hi - lo + SS::kDocs - 1) / SS::kDocs;
+  const int64_t per_group = (steps + cu_count() - 1) / cu_count();
+  const int grid = static_cast<int>(std::max<int64_t>(1, (steps + per_group - 1) / per_group));
+  for (int64_t qb = 0; qb < num_queries; qb += SS::kQueries) {
+    const int64_t qn = std::min<int64_t>(SS::kQueries, num_queries - qb);
+    hipLaunchKernelGGL(topk_score_kernel<D>, dim3(grid), dim3(kScoreThreads), SS::kLds, s, emb,
+                       qv, mask64, num_columns, qb, qn, lo, hi, per_group, st);
     check_launch("topk_score_kernel");
   }
 }
 
-using ScoreFn = void (*)(const uint16_t*, const uint16_t*, const uint32_t*, int64_t, int64_t,
+using ScoreFn = void (*)(const uint16_t*, const uint16_t*, const uint64_t*, int64_t, int64_t,
                          int64_t, int64_t, const TopkState&, hipStream_t);
 
 ScoreFn score_fn(int64_t dim) {
@@ -359,15 +458,18 @@ ScoreFn score_fn(int64_t dim) {
   }
 }
 
-// The scoring kernel stages up to 160 KB of queries in LDS.
+// The scoring kernel stages a step of doc rows and filter words in LDS
+// (more than the 64 KB default limit).
 void set_lds_limits() {
   static std::once_flag once;
   static hipError_t status = hipSuccess;
   std::call_once(once, [] {
-    for (const void* k : {reinterpret_cast<const void*>(topk_score_kernel<64>),
-                          reinterpret_cast<const void*>(topk_score_kernel<128>),
-                          reinterpret_cast<const void*>(topk_score_kernel<256>)}) {
-      const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    const std::pair<const void*, int> kernels[] = {
+        {reinterpret_cast<const void*>(topk_score_kernel<64>), ScoreShape<64>::kLds},
+        {reinterpret_cast<const void*>(topk_score_kernel<128>), ScoreShape<128>::kLds},
+        {reinterpret_cast<const void*>(topk_score_kernel<256>), ScoreShape<256>::kLds}};
+    for (const auto& k : kernels) {
+      const hipError_t e = hipFuncSetAttribute(k.first, hipFuncAttributeMaxDynamicSharedMemorySize, k.second);
       if (e != hipSuccess && status == hipSuccess) status = e;
     }
   });
@@ -430,7 +532,7 @@ extern "C" int st_filtered_topk(const int64_t* packed, int64_t num_queries,
     state.capacity = kCandidateCapacity;
     const uint16_t* emb = static_cast<const uint16_t*>(doc_embeddings);
     const uint16_t* qv = static_cast<const uint16_t*>(query_embeddings);
-    const uint32_t* m32 = reinterpret_cast<const uint32_t*>(packed);
+    const uint64_t* m64 = reinterpret_cast<const uint64_t*>(packed);
     const unsigned qgrid = static_cast<unsigned>(num_queries);
 
     for (int attempt = 0; attempt < 2; ++attempt) {
@@ -440,7 +542,7 @@ extern "C" int st_filtered_topk(const int64_t* packed, int64_t num_queries,
       check_launch("topk_reset_kernel");
       const std::vector<int64_t> bounds = round_bounds(num_docs, topk, safe);
       for (size_t r = 0; r + 1 < bounds.size(); ++r) {
-        score(emb, qv, m32, num_columns, num_queries, bounds[r], bounds[r + 1], state, s);
+        score(emb, qv, m64, num_columns, num_queries, bounds[r], bounds[r + 1], state, s);
         const bool last = r + 2 == bounds.size();
         hipLaunchKernelGGL(topk_select_kernel, dim3(qgrid), dim3(kSelectThreads), 0, s, state,
                            topk, last ? 1 : 0, out_ids, out_scores);
