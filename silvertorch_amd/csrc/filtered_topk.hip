@@ -52,6 +52,11 @@ constexpr int kSelectSlots = 4096;   // bitonic buffer: best 2048 + a chunk of 2
 constexpr int kSelectChunk = kSelectSlots / 2;
 constexpr int kMaxTopk = kSelectChunk;
 constexpr uint32_t kCandidateCapacity = 32768;  // per query
+// A query's candidate list: the best kept so far in slots [0, kMaxTopk), then
+// one segment per scoring workgroup (at most kMaxSegments of them), each
+// filled by its workgroup alone.
+constexpr int kMaxSegments = 256;
+constexpr uint32_t kSegmentSlots = kCandidateCapacity - kMaxTopk;
 constexpr int64_t kRoundAlign = 2048;
 
 // Monotone map of floats to unsigned ints (larger float -> larger int).
@@ -72,11 +77,13 @@ __device__ __forceinline__ uint64_t make_key(float score, int64_t doc) {
 }
 
 struct TopkState {
-  uint32_t* counts;    // [Q] candidates held
+  uint32_t* counts;    // [Q] best candidates kept (<= topk)
   float* thr;          // [Q] entry threshold
   uint64_t* cand;      // [Q * capacity] keys
+  uint32_t* segn;      // [Q * kMaxSegments] entries in each segment
   uint32_t* overflow;  // [1]
   uint32_t capacity;
+  uint32_t seg;        // slots per segment in the current round
 };
 
 __global__ void topk_reset_kernel(TopkState st, int64_t num_queries) {
@@ -110,7 +117,7 @@ struct ScoreShape {
   static constexpr int kDocBuf = kDocs * kRowBytes;
   static constexpr int kMaskBuf = kQueries * kMaskWords * 4;
   static constexpr int kBuf = kDocBuf + kMaskBuf;
-  static constexpr int kLds = 2 * kBuf;
+  static constexpr int kLds = 2 * kBuf + kQueries * 4;  // + segment slot counters
   static constexpr int kDocLoads = kStepBytes / 16 / kScoreThreads;  // u32x4 per thread
   static constexpr int kMaskLoads = (kQueries * kCols + kScoreThreads - 1) / kScoreThreads;
   static_assert(kLds <= kLdsBytes, "two steps must fit in LDS");
@@ -148,7 +155,8 @@ __device__ __forceinline__ bool tile_gate(const f32x16& acc, uint32_t m, float t
 // pass the filter with a score >= th go to the query's candidate list.
 // Called by the whole wave.
 __device__ __forceinline__ void tile_candidates(const TopkState& st, const f32x16& acc, uint32_t m,
-                                                float th, int64_t q, int64_t doc0, int lane) {
+                                                float th, int64_t q, uint32_t* slot_count,
+                                                int64_t doc0, int lane) {
   uint32_t ge = 0u;
 #pragma unroll
   for (int j = 15; j >= 0; --j) ge = (ge << 1) | (acc[j] >= th ? 1u : 0u);
@@ -157,10 +165,12 @@ __device__ __forceinline__ void tile_candidates(const TopkState& st, const f32x1
   if (__ballot(hits != 0u) == 0) return;
   const uint32_t cnt = __builtin_popcount(hits);
   const uint32_t cnt_pair = __shfl_xor(cnt, 32, 64);  // lanes l, l ^ 32: same query
+  // slots of this workgroup's segment, counted in LDS
   uint32_t base = 0u;
-  if (lane < 32 && cnt + cnt_pair > 0u) base = atomicAdd(st.counts + q, cnt + cnt_pair);
+  if (lane < 32 && cnt + cnt_pair > 0u) base = atomicAdd(slot_count, cnt + cnt_pair);
   const uint32_t base_pair = __shfl_xor(base, 32, 64);
   uint32_t slot = lane < 32 ? base : base_pair + cnt_pair;
+  uint64_t* seg = st.cand + q * st.capacity + kMaxTopk + static_cast<uint64_t>(blockIdx.x) * st.seg;
   while (__ballot(hits != 0u) != 0) {
     if (hits != 0u) {
       const int j = __builtin_ctz(hits);
@@ -169,7 +179,7 @@ __device__ __forceinline__ void tile_candidates(const TopkState& st, const f32x1
 #pragma unroll
       for (int i = 0; i < 16; ++i) v = j == i ? acc[i] : v;
       const int64_t doc = doc0 + 8 * (j >> 2) + 4 * h + (j & 3);
-      if (slot < st.capacity) st.cand[q * st.capacity + slot] = make_key(v, doc);
+      if (slot < st.seg) seg[slot] = make_key(v, doc);
       else atomicOr(st.overflow, 1u);
       ++slot;
     }
@@ -198,7 +208,14 @@ __global__ __launch_bounds__(kScoreThreads) void topk_score_kernel(
 
   const int64_t first = lo + static_cast<int64_t>(blockIdx.x) * steps_per_group * SS::kDocs;
   const int64_t last = min(hi, first + steps_per_group * SS::kDocs);
-  if (first >= last) return;  // whole workgroup
+  uint32_t* segn = st.segn + q_begin * kMaxSegments + blockIdx.x;  // query stride kMaxSegments
+  if (first >= last) {  // whole workgroup; its segments stay empty
+    for (int i = tid; i < q_count; i += kScoreThreads) segn[i * kMaxSegments] = 0u;
+    return;
+  }
+  // Entries this workgroup put in each query's segment.
+  uint32_t* slot_count = reinterpret_cast<uint32_t*>(lds + 2 * SS::kBuf);
+  for (int i = tid; i < SS::kQueries; i += kScoreThreads) slot_count[i] = 0u;
 
   // This wave's query fragments (zero past q_count) and entry thresholds
   // (fixed for the launch).
@@ -283,60 +300,69 @@ __global__ __launch_bounds__(kScoreThreads) void topk_score_kernel(
   for (int64_t d0 = first; d0 < last; d0 += SS::kDocs, buf ^= 1) {
     const uint8_t* docs = lds + buf * SS::kBuf;
     const uint32_t* masks = reinterpret_cast<const uint32_t*>(docs + SS::kDocBuf);
-    const int tiles = static_cast<int>(min<int64_t>(SS::kDocTiles, (last - d0 + 31) / 32));
     uint32_t m[QT][SS::kDocTiles];
 #pragma unroll
     for (int t = 0; t < QT; ++t)
 #pragma unroll
       for (int dt = 0; dt < SS::kDocTiles; ++dt)
         m[t][dt] = masks[ql[t] * SS::kMaskWords + dt];  // zero past q_count
-    // A operands: doc row 32 dt + (lane & 31), k half h, read from LDS just
-    // ahead of their MFMAs.  The epilogue of a tile is deferred to the next
-    // tile, whose MFMAs its gate is interleaved with, so each wave keeps the
+    // A operands: doc row 32 dt + (lane & 31), k half h.  The step's
+    // fragments are read from LDS in one stream, kAhead ahead of their MFMAs
+    // and across tile boundaries (rows past hi are zero in LDS and carry no
+    // filter bit).  The epilogue of a tile is deferred to the next tile,
+    // whose MFMAs its gate is interleaved with, so each wave keeps the
     // matrix cores fed by itself.  Tiles alternate between the two
-    // accumulator sets; pend[x] says set x holds a tile still to finish.
-    const uint8_t* arow = docs + (lane & 31) * SS::kRowBytes + h * 16;
+    // accumulator sets; pend[x] says set x holds a tile still to finish.  A
+    // step with no filter bit for any of the wave's queries is skipped.
+    bool any = false;
 #pragma unroll
-    for (int dt = 0; dt < SS::kDocTiles; ++dt) {
-      if (dt < tiles) {
+    for (int t = 0; t < QT; ++t)
+#pragma unroll
+      for (int dt = 0; dt < SS::kDocTiles; ++dt) any |= m[t][dt] != 0u;
+    if (__ballot(any) != 0) {
+      constexpr int kFrags = SS::kDocTiles * S;
+      constexpr int kAhead = 3;
+      const uint8_t* arow = docs + (lane & 31) * SS::kRowBytes + h * 16;
+      bf16x8 fr[kAhead + 1];
+      auto read = [&](int g) {
+        fr[g % (kAhead + 1)] = *reinterpret_cast<const bf16x8*>(
+            arow + (g / S) * 32 * SS::kRowBytes + (g % S) * 32);
+      };
+#pragma unroll
+      for (int g = 0; g < kAhead; ++g) read(g);
+#pragma unroll
+      for (int dt = 0; dt < SS::kDocTiles; ++dt) {
         const int cb = dt & 1, pb = cb ^ 1;
-        bool any = false;
 #pragma unroll
-        for (int t = 0; t < QT; ++t) any |= m[t][dt] != 0u;
-        const bool run = __ballot(any) != 0;  // some filter bit in this doc tile
+        for (int s = 0; s < S; ++s) {
+          const int g = dt * S + s;
+          if (g + kAhead < kFrags) read(g + kAhead);
+#pragma unroll
+          for (int t = 0; t < QT; ++t)
+            acc[cb][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[g % (kAhead + 1)], b[t][s],
+                                                                 s == 0 ? f32x16{} : acc[cb][t], 0, 0, 0);
+        }
         bool gate[QT];
-        if (run) {
 #pragma unroll
-          for (int s = 0; s < S; ++s) {
-            const bf16x8 av = *reinterpret_cast<const bf16x8*>(arow + dt * 32 * SS::kRowBytes + s * 32);
+        for (int t = 0; t < QT; ++t) gate[t] = tile_gate(acc[pb][t], mb[pb][t], th[t]) & pend[pb];
+        // MFMAs with a fragment read and the pending tile's gate VALU work
+        // between them
 #pragma unroll
-            for (int t = 0; t < QT; ++t)
-              acc[cb][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b[t][s], s == 0 ? f32x16{} : acc[cb][t], 0, 0, 0);
+        for (int i = 0; i < S; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+          for (int t = 0; t < QT; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
           }
-#pragma unroll
-          for (int t = 0; t < QT; ++t) gate[t] = tile_gate(acc[pb][t], mb[pb][t], th[t]) & pend[pb];
-          // three fragment reads ahead, then MFMAs with the gate's VALU work
-          // and the remaining reads between them
-          __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
-#pragma unroll
-          for (int i = 0; i < S; ++i) {
-#pragma unroll
-            for (int t = 0; t < QT; ++t) {
-              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-              __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          }
-        } else {
-#pragma unroll
-          for (int t = 0; t < QT; ++t) gate[t] = tile_gate(acc[pb][t], mb[pb][t], th[t]) & pend[pb];
         }
 #pragma unroll
         for (int t = 0; t < QT; ++t)
           if (__ballot(gate[t]) != 0)
-            tile_candidates(st, acc[pb][t], mb[pb][t], th[t], q_begin + ql[t], docb[pb], lane);
+            tile_candidates(st, acc[pb][t], mb[pb][t], th[t], q_begin + ql[t], slot_count + ql[t],
+                            docb[pb], lane);
+        pend[cb] = true;
         pend[pb] = false;
-        pend[cb] = run;
 #pragma unroll
         for (int t = 0; t < QT; ++t) mb[cb][t] = m[t][dt];
         docb[cb] = d0 + dt * 32;
@@ -355,9 +381,12 @@ __global__ __launch_bounds__(kScoreThreads) void topk_score_kernel(
 #pragma unroll
       for (int t = 0; t < QT; ++t)
         if (__ballot(tile_gate(acc[x][t], mb[x][t], th[t])) != 0)
-          tile_candidates(st, acc[x][t], mb[x][t], th[t], q_begin + ql[t], docb[x], lane);
+          tile_candidates(st, acc[x][t], mb[x][t], th[t], q_begin + ql[t], slot_count + ql[t],
+                          docb[x], lane);
     }
   }
+  __syncthreads();
+  for (int i = tid; i < q_count; i += kScoreThreads) segn[i * kMaxSegments] = min(slot_count[i], st.seg);
 }
 
 // Descending bitonic sort of the first `size` keys in LDS (a power of two).
@@ -381,19 +410,48 @@ __device__ void bitonic_sort_desc(uint64_t* keys, int size) {
 }
 
 // One workgroup per query: keeps the best `topk` candidates (sorted), sets
-// the entry threshold, and on the last round writes the outputs.
+// the entry threshold, and on the last round writes the outputs.  The
+// candidates are the kept best (slots [0, counts[q])) followed by the entries
+// of the round's nseg segments, gathered in that order.
 __global__ __launch_bounds__(kSelectThreads) void topk_select_kernel(
-    TopkState st, int64_t topk, int final_round, int64_t* __restrict__ out_ids,
+    TopkState st, int64_t topk, int nseg, int final_round, int64_t* __restrict__ out_ids,
     float* __restrict__ out_scores) {
+  static_assert(kSelectThreads == kMaxSegments, "one thread per segment");
   __shared__ uint64_t keys[kSelectSlots];
+  __shared__ uint32_t start[kMaxSegments + 1];  // virtual index of each segment's first entry
   const int64_t q = blockIdx.x;
   uint64_t* cand = st.cand + q * st.capacity;
-  const uint32_t n = min(st.counts[q], st.capacity);
+  const uint32_t kept = st.counts[q];
+  // Exclusive scan of the segment counts, one thread per segment.
+  const int g = threadIdx.x;
+  const uint32_t mine = g < nseg ? min(st.segn[q * kMaxSegments + g], st.seg) : 0u;
+  start[g + 1] = mine;
+  if (g == 0) start[0] = 0u;
+  __syncthreads();
+  for (int off = 1; off < kMaxSegments; off <<= 1) {
+    const uint32_t v = g + 1 - off >= 1 ? start[g + 1 - off] : 0u;
+    __syncthreads();
+    start[g + 1] += v;
+    __syncthreads();
+  }
+  const uint32_t n = kept + start[kMaxSegments];
+  // Candidate v of the virtual list: the kept best, then the segments.
+  auto at = [&](uint32_t v) -> uint64_t {
+    if (v < kept) return cand[v];
+    const uint32_t w = v - kept;
+    int lo = 0, hi = nseg;  // last segment with start <= w
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (start[mid] <= w) lo = mid;
+      else hi = mid;
+    }
+    return cand[kMaxTopk + static_cast<uint64_t>(lo) * st.seg + (w - start[lo])];
+  };
   if (n <= static_cast<uint32_t>(kSelectSlots)) {
     // One sort of the smallest power of two holding every candidate.
     int size = 64;
     while (size < static_cast<int>(n)) size <<= 1;
-    for (int i = threadIdx.x; i < size; i += kSelectThreads) keys[i] = i < static_cast<int>(n) ? cand[i] : 0ull;
+    for (int i = threadIdx.x; i < size; i += kSelectThreads) keys[i] = i < static_cast<int>(n) ? at(i) : 0ull;
     __syncthreads();
     bitonic_sort_desc(keys, size);
   } else {
@@ -402,25 +460,25 @@ __global__ __launch_bounds__(kSelectThreads) void topk_select_kernel(
     for (int i = threadIdx.x; i < kSelectChunk; i += kSelectThreads) keys[i] = 0ull;
     for (uint32_t c0 = 0; c0 < n; c0 += kSelectChunk) {
       for (int i = threadIdx.x; i < kSelectChunk; i += kSelectThreads)
-        keys[kSelectChunk + i] = c0 + i < n ? cand[c0 + i] : 0ull;
+        keys[kSelectChunk + i] = c0 + i < n ? at(c0 + i) : 0ull;
       __syncthreads();
       bitonic_sort_desc(keys, kSelectSlots);
     }
   }
-  const uint32_t kept = min(n, static_cast<uint32_t>(topk));
+  const uint32_t best = min(n, static_cast<uint32_t>(topk));
   if (final_round) {
     for (int64_t i = threadIdx.x; i < topk; i += kSelectThreads) {
-      const bool have = i < kept;
+      const bool have = i < best;
       out_ids[q * topk + i] = have ? static_cast<int64_t>(0xFFFFFFFFu - static_cast<uint32_t>(keys[i]))
                                    : -1;
       out_scores[q * topk + i] = have ? from_ordered(static_cast<uint32_t>(keys[i] >> 32)) : -INFINITY;
     }
     return;
   }
-  for (uint32_t i = threadIdx.x; i < kept; i += kSelectThreads) cand[i] = keys[i];
+  for (uint32_t i = threadIdx.x; i < best; i += kSelectThreads) cand[i] = keys[i];
   if (threadIdx.x == 0) {
-    st.counts[q] = kept;
-    st.thr[q] = kept == topk ? from_ordered(static_cast<uint32_t>(keys[topk - 1] >> 32)) : -INFINITY;
+    st.counts[q] = best;
+    st.thr[q] = best == topk ? from_ordered(static_cast<uint32_t>(keys[topk - 1] >> 32)) : -INFINITY;
   }
 }
 
@@ -429,25 +487,33 @@ void check_launch(const char* what) {
   if (e != hipSuccess) throw Error(ST_ERR_HIP, cat(what, " launch failed: ", hipGetErrorString(e)));
 }
 
+// Scores docs [lo, hi) for every query; returns the number of workgroups
+// (segments) used.  A workgroup scores at most docs_per_group docs, the bound
+// on the entries of one segment that a round without a threshold can make.
 template <int D>
-void launch_score(const uint16_t* emb, const uint16_t* qv, const uint64_t* mask64,
-                  int64_t num_columns, int64_t num_queries, int64_t lo, int64_t hi,
-                  const TopkState& st, hipStream_t s) {
+int launch_score(const uint16_t* emb, const uint16_t* qv, const uint64_t* mask64,
+                 int64_t num_columns, int64_t num_queries, int64_t lo, int64_t hi,
+                 TopkState st, bool need_fit, hipStream_t s) {
   using SS = ScoreShape<D>;
   // One contiguous run of steps per workgroup, one workgroup per CU.
   const int64_t steps = (hi - lo + SS::kDocs - 1) / SS::kDocs;
-  const int64_t per_group = (steps + cu_count() - 1) / cu_count();
+  const int64_t groups = std::min<int64_t>(cu_count(), kMaxSegments);
+  const int64_t per_group = (steps + groups - 1) / groups;
   const int grid = static_cast<int>(std::max<int64_t>(1, (steps + per_group - 1) / per_group));
+  st.seg = kSegmentSlots / static_cast<uint32_t>(grid);
+  if (need_fit && static_cast<int64_t>(st.seg) < per_group * SS::kDocs)
+    fail("internal: a segment of ", st.seg, " slots cannot hold ", per_group * SS::kDocs, " docs");
   for (int64_t qb = 0; qb < num_queries; qb += SS::kQueries) {
     const int64_t qn = std::min<int64_t>(SS::kQueries, num_queries - qb);
     hipLaunchKernelGGL(topk_score_kernel<D>, dim3(grid), dim3(kScoreThreads), SS::kLds, s, emb,
                        qv, mask64, num_columns, qb, qn, lo, hi, per_group, st);
     check_launch("topk_score_kernel");
   }
+  return grid;
 }
 
-using ScoreFn = void (*)(const uint16_t*, const uint16_t*, const uint64_t*, int64_t, int64_t,
-                         int64_t, int64_t, const TopkState&, hipStream_t);
+using ScoreFn = int (*)(const uint16_t*, const uint16_t*, const uint64_t*, int64_t, int64_t,
+                        int64_t, int64_t, TopkState, bool, hipStream_t);
 
 ScoreFn score_fn(int64_t dim) {
   switch (dim) {
@@ -479,12 +545,13 @@ void set_lds_limits() {
 
 // Doc ranges of the rounds: a first round of 8192 docs, then each round
 // eight times everything before it (rounds aligned to bundles), or, in the
-// safe schedule, rounds no larger than a candidate list can always hold.
-std::vector<int64_t> round_bounds(int64_t num_docs, int64_t topk, bool safe) {
+// safe schedule, rounds no larger than the candidate segments can always hold.
+std::vector<int64_t> round_bounds(int64_t num_docs, bool safe) {
   std::vector<int64_t> b{0};
   int64_t pos = 0;
-  const int64_t safe_step =
-      std::max<int64_t>(kRoundAlign, (static_cast<int64_t>(kCandidateCapacity) - topk) / kRoundAlign * kRoundAlign);
+  // A safe round gives each workgroup at most one segment's worth of docs.
+  static_assert(kSegmentSlots % kRoundAlign == 0, "safe rounds stay aligned");
+  const int64_t safe_step = kSegmentSlots;
   while (pos < num_docs) {
     int64_t step = safe ? safe_step : (pos == 0 ? 8192 : 8 * pos);
     step = (step + kRoundAlign - 1) / kRoundAlign * kRoundAlign;
@@ -499,7 +566,9 @@ std::vector<int64_t> round_bounds(int64_t num_docs, int64_t topk, bool safe) {
 
 extern "C" int64_t st_filtered_topk_workspace_bytes(int64_t num_queries) {
   if (num_queries <= 0) return 0;
-  return num_queries * (4 + 4 + 8 * static_cast<int64_t>(st::kCandidateCapacity)) + 256;
+  return num_queries * (4 + 4 + 8 * static_cast<int64_t>(st::kCandidateCapacity) +
+                       4 * static_cast<int64_t>(st::kMaxSegments)) +
+         256;
 }
 
 extern "C" int st_filtered_topk(const int64_t* packed, int64_t num_queries,
@@ -530,6 +599,8 @@ extern "C" int st_filtered_topk(const int64_t* packed, int64_t num_queries,
     state.overflow = reinterpret_cast<uint32_t*>(ws + 8 * num_queries);
     state.cand = reinterpret_cast<uint64_t*>(ws + ((8 * num_queries + 4 + 255) / 256) * 256);
     state.capacity = kCandidateCapacity;
+    state.segn = reinterpret_cast<uint32_t*>(state.cand + num_queries * static_cast<int64_t>(kCandidateCapacity));
+    state.seg = 0;
     const uint16_t* emb = static_cast<const uint16_t*>(doc_embeddings);
     const uint16_t* qv = static_cast<const uint16_t*>(query_embeddings);
     const uint64_t* m64 = reinterpret_cast<const uint64_t*>(packed);
@@ -540,17 +611,20 @@ extern "C" int st_filtered_topk(const int64_t* packed, int64_t num_queries,
       hipLaunchKernelGGL(topk_reset_kernel, dim3(static_cast<unsigned>((num_queries + 255) / 256)),
                          dim3(256), 0, s, state, num_queries);
       check_launch("topk_reset_kernel");
-      const std::vector<int64_t> bounds = round_bounds(num_docs, topk, safe);
+      const std::vector<int64_t> bounds = round_bounds(num_docs, safe);
       for (size_t r = 0; r + 1 < bounds.size(); ++r) {
-        score(emb, qv, m64, num_columns, num_queries, bounds[r], bounds[r + 1], state, s);
+        const int nseg = score(emb, qv, m64, num_columns, num_queries, bounds[r], bounds[r + 1],
+                               state, safe, s);
+        TopkState sel = state;
+        sel.seg = kSegmentSlots / static_cast<uint32_t>(nseg);
         const bool last = r + 2 == bounds.size();
-        hipLaunchKernelGGL(topk_select_kernel, dim3(qgrid), dim3(kSelectThreads), 0, s, state,
-                           topk, last ? 1 : 0, out_ids, out_scores);
+        hipLaunchKernelGGL(topk_select_kernel, dim3(qgrid), dim3(kSelectThreads), 0, s, sel,
+                           topk, nseg, last ? 1 : 0, out_ids, out_scores);
         check_launch("topk_select_kernel");
       }
       if (bounds.size() == 1) {  // no docs: every output is padding
         hipLaunchKernelGGL(topk_select_kernel, dim3(qgrid), dim3(kSelectThreads), 0, s, state,
-                           topk, 1, out_ids, out_scores);
+                           topk, 0, 1, out_ids, out_scores);
         check_launch("topk_select_kernel");
         return;
       }

@@ -93,8 +93,8 @@ def test_topk_random(dim, n, q, topk, density):
 
 def test_topk_rounds_and_query_chunks():
     """60k docs cross several selection rounds (first round 8192 docs, then
-    x4) and selections of more than one 2048-key chunk; 600 queries cross
-    the LDS query chunk of the dim-128 kernel (576)."""
+    x8) and selections of more than one 2048-key chunk; 600 queries cross
+    the 512 queries one launch of the dim-128 kernel scores."""
     rng = np.random.default_rng(7)
     emb_bf, qv_bf, emb32, qv32, packed = _random_case(rng, 60000, 128, 600, 0.3)
     H.note("[topk] 60000 docs x 600 queries")
@@ -103,11 +103,12 @@ def test_topk_rounds_and_query_chunks():
     _check(ids[560:], sc[560:], emb32, qv32[560:], packed[560:], 60000, 100)
 
 
-def test_topk_ties_overflow_and_safe_rounds():
+@pytest.mark.parametrize("dim", [64, 128, 256])
+def test_topk_ties_overflow_and_safe_rounds(dim):
     """All scores equal: the second round sends every doc past the threshold
-    (ties are kept), overflowing the candidate lists, so the selection is
+    (ties are kept), overflowing the candidate segments, so the selection is
     redone with small rounds; the answer is the lowest ids."""
-    n, dim, q = 50000, 64, 3
+    n, q = 50000, 3
     emb_bf = torch.ones((n, dim), dtype=torch.bfloat16)
     qv_bf = torch.ones((q, dim), dtype=torch.bfloat16)
     cols = (n + 2047) // 2048 * 32
