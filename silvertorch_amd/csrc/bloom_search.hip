@@ -11,6 +11,19 @@
 namespace st {
 namespace {
 
+WideFn select_wide_kernel(int k) {
+  switch (k) {
+    case 1: return wide_kernel_for<1>();
+    case 2: return wide_kernel_for<2>();
+    case 3: return wide_kernel_for<3>();
+    case 4: return wide_kernel_for<4>();
+    case 5: return wide_kernel_for<5>();
+    case 6: return wide_kernel_for<6>();
+    case 7: return wide_kernel_for<7>();
+    default: return nullptr;
+  }
+}
+
 KernelFn select_kernel(int k, int mode, bool quad) {
   switch (k) {
     case 0:
@@ -190,6 +203,7 @@ __device__ uint32_t device_term_position(const uint64_t* h, int hash_k, int k_ef
   const int16_t row = cnt == 0 ? 0 : (r < cnt ? found[r] : found[0]);
   if (b <= kSearchTileRows)
     return static_cast<uint32_t>(cnt == 0 ? kSearchZerosRow : row) * 256u;
+  if (wide_width(b)) return static_cast<uint32_t>(cnt == 0 ? kWideZerosRow : row);
   return cnt == 0 ? static_cast<uint32_t>(kPosZeros)
                   : static_cast<uint32_t>(static_cast<int32_t>(row));
 }
@@ -212,10 +226,10 @@ __global__ void bind_fill_kernel(const uint32_t* __restrict__ tmpl,
     v = tmpl[i];
   } else if (c == kTmplOnes) {
     v = b <= kSearchTileRows ? static_cast<uint32_t>(kSearchOnesRow) * 256u
-                             : static_cast<uint32_t>(kPosOnes);
+                             : static_cast<uint32_t>(wide_width(b) ? kWideOnesRow : kPosOnes);
   } else if (c == kTmplZeros) {
     v = b <= kSearchTileRows ? static_cast<uint32_t>(kSearchZerosRow) * 256u
-                             : static_cast<uint32_t>(kPosZeros);
+                             : static_cast<uint32_t>(wide_width(b) ? kWideZerosRow : kPosZeros);
   } else {
     const uint32_t t = (c >> 4) - 1u;
     v = device_term_position(hashes + static_cast<uint64_t>(t) * hash_k, hash_k, k_eff, b,
@@ -264,6 +278,20 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
         throw Error(ST_ERR_HIP, cat("bind fill launch failed: ", hipGetErrorString(e)));
     }
   }
+  // Wide bundles (kSearchTileRows < b <= kWideRows, width-bound) have their
+  // literal streams evaluated by the column-slice kernel, in packed mode;
+  // the per-batch kernels then skip those streams there.  With host-bound
+  // widths the launch is decided here; with device binding the kernel
+  // returns at once when no slot width is wide.
+  WideFn wide_fn = nullptr;
+  if (bound && mode == kOutPacked && plan->off_wide != 0) {
+    wide_fn = select_wide_kernel(plan->k_eff);
+    if (wide_fn != nullptr && !plan->device_bind) {
+      bool any = false;
+      for (int64_t w : plan->slot_width) any |= wide_width(w);
+      if (!any) wide_fn = nullptr;
+    }
+  }
   for (const SearchBatch& bt : plan->batches) {
     // Quad-lane stream evaluation when the batch's literal stream fits the
     // LDS area after the tile and a stream step holds whole quads (k <= 7).
@@ -286,10 +314,24 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
         bound ? at(bt.off_stream_skip) : nullptr, bound ? bt.stream_off : 0u,
         bound ? bt.stream_words : 0u, bound ? bt.stream_masks : 0u, bt.num_terms,
         static_cast<int32_t>(plan->hash_k),
-        num_bundles * 32, out, counts, num_docs);
+        num_bundles * 32, out, counts, num_docs, wide_fn != nullptr ? 1u : 0u);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
       throw Error(ST_ERR_HIP, cat("search kernel launch failed: ", hipGetErrorString(e)));
+  }
+  if (wide_fn != nullptr) {
+    hipLaunchKernelGGL(wide_fn, dim3(grid), dim3(kSearchThreads), 0, stream, bloom_index,
+                       bloom_index_numel, bundle_b_offsets, num_bundles,
+                       at(plan->off_bundle_slot),
+                       plan->device_bind ? at(plan->off_num_slots) : nullptr,
+                       plan->device_bind
+                           ? reinterpret_cast<const int64_t*>(blob + plan->off_slot_width)
+                           : nullptr,
+                       reinterpret_cast<const uint32_t*>(blob), at(plan->off_wide),
+                       num_bundles * 32, static_cast<int64_t*>(out));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+      throw Error(ST_ERR_HIP, cat("wide search kernel launch failed: ", hipGetErrorString(e)));
   }
 }
 

@@ -27,3 +27,16 @@ KernelFn search_kernel_for<ST_SEARCH_K>(int mode, bool quad) {
 }
 
 }  // namespace st
+
+namespace st {
+
+template <>
+WideFn wide_kernel_for<ST_SEARCH_K>() {
+  if constexpr (ST_SEARCH_K <= 7) {
+    return bloom_wide_kernel<ST_SEARCH_K>;
+  } else {
+    return nullptr;
+  }
+}
+
+}  // namespace st

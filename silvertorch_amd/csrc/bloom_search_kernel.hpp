@@ -205,6 +205,7 @@ struct RowSource {
   const uint32_t* index32;
   int64_t index_numel;
   int64_t start;          // first row of the bundle
+  int64_t b;              // rows of the bundle
   int lane;
   bool staged;            // rows in the LDS tile (else global memory)
 };
@@ -372,6 +373,8 @@ __device__ __forceinline__ uint32_t row_word(const RowSource& rs, uint32_t p) {
     const int32_t r = static_cast<int32_t>(p);
     if (r == kPosZeros) return 0;
     if (r == kPosOnes) return ~0u;
+    // a row at or past the width is a no-op code of a wide width
+    if (r >= rs.b) return r == kWideOnesRow ? ~0u : 0u;
     const int64_t row = rs.start + r;
     if (row < 0 || (row * 32 + (rs.lane >> 1)) >= rs.index_numel) return 0;
     return rs.index32[row * 64 + rs.lane];
@@ -883,7 +886,8 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     const uint32_t* __restrict__ stream_skip, uint32_t stream_off, uint32_t stream_words,
     uint32_t stream_masks,
     uint32_t num_terms, int32_t hash_k,
-    int64_t out_cols, void* __restrict__ out, int64_t* __restrict__ counts, int64_t num_docs) {
+    int64_t out_cols, void* __restrict__ out, int64_t* __restrict__ counts, int64_t num_docs,
+    uint32_t wide_skip) {
   SearchArgs a;
   a.index = index;
   a.index_numel = index_numel;
@@ -981,6 +985,8 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     const bool staged = b <= kSearchTileRows;
 
     const bool quad_here = quad_bundle(cur);
+    // the wide-bundle kernel evaluates the literal stream of this bundle
+    const bool wide_here = wide_skip != 0 && slot != kNoWidthSlot && wide_width(b);
 
     __syncthreads();  // previous bundle's readers are done with tile and pos
     if (staged) {
@@ -1047,6 +1053,7 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     rs.index32 = index32;
     rs.index_numel = a.index_numel;
     rs.start = start;
+    rs.b = b;
     rs.lane = lane;
     rs.staged = staged;
     if constexpr (kQuad) {
@@ -1062,7 +1069,8 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
         if (staged)
           eval_queries<K, KP, true, true, GL, kOut, true>(a, rs, s_begin, s_end, bundle, slot);
         else
-          eval_queries<K, KP, false, true, GL, kOut, true>(a, rs, s_begin, s_end, bundle, slot);
+          eval_queries<K, KP, false, true, GL, kOut, true>(a, rs, wide_here ? s_rest : s_begin,
+                                                           s_end, bundle, slot);
       } else if (staged) {
         eval_queries<K, KP, true, false, GL, kOut, true>(a, rs, s_begin, s_end, bundle, slot);
       } else {
@@ -1080,7 +1088,7 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
         }
         eval_queries<K, KP, true, true, G, kOut>(a, rs, s_rest, s_end, bundle, slot);
       } else {
-        if (streamed) {
+        if (streamed && !wide_here) {
           if (a.stream_masks)
             eval_rounds<K, false, true, kOut>(a, rs, stream, r_begin, r_end, bundle);
           else
@@ -1108,7 +1116,210 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
   }
 }
 
+// ------------------------------------------------ wide bundles, column slices
+//
+// Width-bound bundles of kSearchTileRows < b <= kWideRows rows do not fit the
+// LDS tile.  bloom_wide_kernel searches them in kWideSlices column slices:
+// the slice's 64 bytes of every row (512 docs) are staged in LDS, followed by
+// the all-ones and all-zeros rows (kWideOnesRow, kWideZerosRow), and the
+// literal streams of every batch are evaluated on the slice sixteen programs
+// per wave instruction: lane l serves program l >> 2 of the wave's current
+// group (round (l >> 2) / NB, slot (l >> 2) % NB) and owns bytes
+// 16 * (l & 3) .. +15 of every slice row, so one 16-byte LDS read per lane
+// fetches a row for its program.  Each lane reads its program's records from
+// the width block in global memory (shared by every bundle of the width,
+// so L2-resident), two steps ahead.  The index is read once per search,
+// whatever the number of batches.  Packed output only.
+
+constexpr int kWidePieces = kWideSliceBytes / 16;  // u32x4 per slice row
+constexpr int kWidePrefetch = kWideRows * kWidePieces / kSearchThreads;
+static_assert(kWidePrefetch * kSearchThreads == kWideRows * kWidePieces, "slice split");
+
+// One group of 16 programs on the staged slice: each lane folds its
+// program's literals over its 16 bytes and stores them to output row
+// (info >> kSlotRowShift).  `out_lane` is the lane's byte address in output
+// row 0.
+template <int K, bool MASKS>
+__device__ __forceinline__ void wide_eval_group(const uint32_t* stream,
+                                                const ST_CONST uint32_t* grp,
+                                                const char* tile_lane, int lane,
+                                                int64_t row_bytes, char* out_lane) {
+  using S = QuadShape<K>;
+  constexpr uint32_t kStep = S::NB * S::RV;  // u32x4 per stream step
+  const int pg = lane >> 2;
+  const int rr = pg / S::NB;
+  const int sl = pg % S::NB;
+  const uint32_t r0 = grp[2], r1 = grp[3], r2 = grp[4], r3 = grp[5];
+  const uint32_t roff = rr == 0 ? r0 : (rr == 1 ? r1 : (rr == 2 ? r2 : r3));
+  if (roff == ~0u) return;
+  const uint32_t* round = stream + roff;
+  const uint32_t T = round[0];
+  const uint32_t info = round[kRoundSlotInfo + sl];
+  const u32x4* rec = reinterpret_cast<const u32x4*>(round + kRoundHeaderWords + sl * S::RW);
+  u32x4 ra[S::RV], rb[S::RV];
+  const uint32_t last = T > 0 ? T - 1 : 0;
+#pragma unroll
+  for (int v = 0; v < S::RV; ++v) {
+    ra[v] = rec[v];
+    rb[v] = rec[min(1u, last) * kStep + v];
+  }
+  u32x4 res{0, 0, 0, 0}, acc{0, 0, 0, 0};
+  for (uint32_t j = 0; j < T; ++j) {
+    // the record two steps ahead (the last one again near the end)
+    u32x4 rc[S::RV];
+    const u32x4* nx = rec + min(j + 2, last) * kStep;
+#pragma unroll
+    for (int v = 0; v < S::RV; ++v) rc[v] = nx[v];
+    u32x4 t = *reinterpret_cast<const u32x4*>(tile_lane + (u32x4_get(ra[0], 0) << 6));
+#pragma unroll
+    for (int k = 1; k < K; ++k)
+      t &= *reinterpret_cast<const u32x4*>(tile_lane + (u32x4_get(ra[k >> 2], k & 3) << 6));
+    const uint32_t f = u32x4_get(ra[K >> 2], K & 3);
+    if constexpr (MASKS) {  // f is the group mask; nothing is negated
+      res |= acc & f;
+      acc = (acc | f) & t;
+    } else {
+      const uint32_t neg = 0u - (f & kStreamNeg);
+      const uint32_t grpm = 0u - ((f >> 1) & 1u);
+      res |= acc & grpm;
+      acc = (acc | grpm) & (t ^ neg);
+    }
+#pragma unroll
+    for (int v = 0; v < S::RV; ++v) {
+      ra[v] = rb[v];
+      rb[v] = rc[v];
+    }
+  }
+  u32x4 v = res | acc;
+  if (info & kSlotComplement) v = ~v;
+  if (info & kSlotValid)
+    __builtin_nontemporal_store(
+        v, (ST_GLOBAL u32x4*)(out_lane + static_cast<int64_t>(info >> kSlotRowShift) * row_bytes));
+}
+
+// Grid: one 1024-thread workgroup per CU; workgroup w takes the wide
+// bundles w, w + grid, ... of index order, each as kWideSlices slices in
+// order, the next slice's loads in flight while the current one is
+// evaluated.  `num_slots` / `slot_width` (device binding; nullptr when the
+// host decided to launch) let the kernel return at once when no slot width
+// is wide.
+template <int K>
+__global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
+    const int64_t* __restrict__ index, int64_t index_numel,
+    const int64_t* __restrict__ bundle_offsets, int64_t num_bundles,
+    const uint32_t* __restrict__ bundle_slot, const uint32_t* __restrict__ num_slots,
+    const int64_t* __restrict__ slot_width, const uint32_t* __restrict__ blob,
+    const uint32_t* __restrict__ table, int64_t out_cols, int64_t* __restrict__ out) {
+  __shared__ u32x4 tile[(kWideRows + 2) * kWidePieces];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const uint32_t wave = uniform(tid >> 6);
+  const ST_CONST int64_t* boff = as_const(bundle_offsets);
+  const ST_CONST uint32_t* bslot = as_const(bundle_slot);
+  const ST_CONST uint32_t* tab = as_const(table);
+
+  if (num_slots != nullptr) {
+    const ST_CONST uint32_t* ns = as_const(num_slots);
+    const ST_CONST int64_t* sw = as_const(slot_width);
+    const uint32_t n = min(ns[0], static_cast<uint32_t>(kMaxWidthSlots));
+    bool any = false;
+    for (uint32_t s = 0; s < n; ++s) any |= wide_width(sw[s]);
+    if (!any) return;
+  }
+  if (tid < 2 * kWidePieces) {
+    const uint32_t fill = tid < kWidePieces ? ~0u : 0u;
+    tile[kWideOnesRow * kWidePieces + tid] = u32x4{fill, fill, fill, fill};
+  }
+  const uint32_t nbt = tab[0];
+  const uint32_t g_begin = uniform(tab[4 + wave]), g_end = uniform(tab[5 + wave]);
+  const ST_CONST uint32_t* batches = tab + kWideTableHead;
+  const ST_CONST uint32_t* groups = batches + 4 * nbt;
+  const int64_t grid = gridDim.x;
+
+  // first wide bundle at or after i on this workgroup's stride
+  auto next_wide = [&](int64_t i) -> int64_t {
+    for (; i < num_bundles; i += grid) {
+      const int64_t b = boff[i + 1] - boff[i];
+      if (bslot[i] != kNoWidthSlot && wide_width(b)) return i;
+    }
+    return num_bundles;
+  };
+  const u32x4* src = reinterpret_cast<const u32x4*>(index);
+  auto prefetch = [&](int64_t bnd, int slice, u32x4 (&pre)[kWidePrefetch]) {
+    const int64_t start = boff[bnd];
+    const int64_t b = boff[bnd + 1] - start;
+#pragma unroll
+    for (int i = 0; i < kWidePrefetch; ++i) {
+      const int c = tid + i * kSearchThreads;
+      const int64_t row = c / kWidePieces;
+      const int64_t word = (start + row) * 32 + slice * (kWideSliceBytes / 8) +
+                           (c % kWidePieces) * 2;
+      pre[i] = u32x4{0, 0, 0, 0};
+      if (row < b && word >= 0 && word + 1 < index_numel) pre[i] = src[word / 2];
+    }
+  };
+
+  int64_t cb = next_wide(blockIdx.x);
+  if (cb >= num_bundles) return;
+  int cs = 0;
+  u32x4 pre[kWidePrefetch];
+  prefetch(cb, cs, pre);
+  const char* tile_lane = reinterpret_cast<const char*>(tile) + (lane & 3) * 16;
+  const int64_t row_bytes = out_cols * 8;
+  for (;;) {
+    const int64_t b = boff[cb + 1] - boff[cb];
+    const uint32_t slot = bslot[cb];
+    int64_t nb = cb;
+    int ns = cs + 1;
+    if (ns == kWideSlices) {
+      nb = next_wide(cb + grid);
+      ns = 0;
+    }
+    const bool has_next = nb < num_bundles;
+    __syncthreads();  // the previous slice's readers are done
+#pragma unroll
+    for (int i = 0; i < kWidePrefetch; ++i) {
+      const int c = tid + i * kSearchThreads;
+      if (c < b * kWidePieces) tile[c] = pre[i];
+    }
+    if (has_next) prefetch(nb, ns, pre);
+    __syncthreads();
+    char* out_lane = reinterpret_cast<char*>(out) + cb * 256 + cs * kWideSliceBytes + (lane & 3) * 16;
+    for (uint32_t g = g_begin; g < g_end; ++g) {
+      const ST_CONST uint32_t* grp = groups + static_cast<uint64_t>(g) * kWideGroupWords;
+      const ST_CONST uint32_t* bt = batches + 4 * grp[0];
+      const uint32_t* stream =
+          blob + bt[0] + static_cast<uint64_t>(slot) * bt[1] + bt[2];
+      if (bt[3])
+        wide_eval_group<K, true>(stream, grp, tile_lane, lane, row_bytes, out_lane);
+      else
+        wide_eval_group<K, false>(stream, grp, tile_lane, lane, row_bytes, out_lane);
+    }
+    if (!has_next) break;
+    cb = nb;
+    cs = ns;
+  }
+}
+
 }  // namespace
+
+using WideFn = void (*)(const int64_t*, int64_t, const int64_t*, int64_t, const uint32_t*,
+                        const uint32_t*, const int64_t*, const uint32_t*, const uint32_t*,
+                        int64_t, int64_t*);
+// The wide-bundle kernel of one K (nullptr for K > 7), defined in the
+// translation unit compiled with ST_SEARCH_K = K.
+template <int K>
+WideFn wide_kernel_for();
+template <> WideFn wide_kernel_for<1>();
+template <> WideFn wide_kernel_for<2>();
+template <> WideFn wide_kernel_for<3>();
+template <> WideFn wide_kernel_for<4>();
+template <> WideFn wide_kernel_for<5>();
+template <> WideFn wide_kernel_for<6>();
+template <> WideFn wide_kernel_for<7>();
+template <> WideFn wide_kernel_for<8>();
+template <> WideFn wide_kernel_for<9>();
+template <> WideFn wide_kernel_for<10>();
 
 using KernelFn = void (*)(const int64_t*, int64_t, const int64_t*, int64_t,
                           const uint32_t*, const uint32_t*,
@@ -1116,7 +1327,7 @@ using KernelFn = void (*)(const int64_t*, int64_t, const int64_t*, int64_t,
                           const uint32_t*, const uint32_t*, const uint32_t*, uint32_t,
                           const uint32_t*, const uint32_t*, uint32_t, uint32_t, uint32_t,
                           uint32_t, int32_t,
-                          int64_t, void*, int64_t*, int64_t);
+                          int64_t, void*, int64_t*, int64_t, uint32_t);
 
 // The kernels of one K (all output modes; the quad instance evaluates the
 // literal stream in quad lanes and needs a stream that fits the LDS and k <= 7),

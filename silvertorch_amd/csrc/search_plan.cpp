@@ -773,6 +773,8 @@ void term_positions(const uint64_t* h, int64_t hash_k, int k_eff, int64_t b,
     const int16_t r = j < cnt ? found[j] : found[0];
     if (staged) {
       out[j] = static_cast<uint32_t>(cnt == 0 ? kSearchZerosRow : r) * 256u;
+    } else if (wide_width(b)) {
+      out[j] = static_cast<uint32_t>(cnt == 0 ? kWideZerosRow : r);
     } else {
       out[j] = cnt == 0 ? static_cast<uint32_t>(kPosZeros)
                         : static_cast<uint32_t>(static_cast<int32_t>(r));
@@ -960,10 +962,11 @@ void build_block_template(const st_search_plan& plan, SearchBatch& bt,
 void expand_block(const std::vector<uint32_t>& tmpl, const std::vector<uint32_t>& code,
                   const uint32_t* spos, int kp, int64_t width, uint32_t* out) {
   const bool staged = width <= kSearchTileRows;
+  const bool wide = wide_width(width);
   const uint32_t ones = staged ? static_cast<uint32_t>(kSearchOnesRow) * 256u
-                               : static_cast<uint32_t>(kPosOnes);
+                               : static_cast<uint32_t>(wide ? kWideOnesRow : kPosOnes);
   const uint32_t zeros = staged ? static_cast<uint32_t>(kSearchZerosRow) * 256u
-                                : static_cast<uint32_t>(kPosZeros);
+                                : static_cast<uint32_t>(wide ? kWideZerosRow : kPosZeros);
   for (size_t i = 0; i < tmpl.size(); ++i) {
     const uint32_t c = code[i];
     if (c == kTmplCopy) {
@@ -975,6 +978,107 @@ void expand_block(const std::vector<uint32_t>& tmpl, const std::vector<uint32_t>
     } else {
       out[i] = spos[static_cast<size_t>((c >> 4) - 1u) * kp + (c & 15u)];
     }
+  }
+}
+
+// Rounds of a batch's literal stream, read from its width-block template:
+// (first word within the stream, steps).
+using RoundList = std::vector<std::pair<uint32_t, uint32_t>>;
+void stream_rounds(const std::vector<uint32_t>& tmpl, const SearchBatch& bt, int k_eff,
+                   RoundList& out) {
+  out.clear();
+  if (bt.stream_words == 0) return;
+  const int ks = std::max(k_eff, 1);
+  const uint32_t step_words =
+      static_cast<uint32_t>(stream_block_records(ks) * bound_record_words(ks));
+  for (uint32_t w = 0; w < bt.stream_words;) {
+    const uint32_t T = tmpl[bt.stream_off + w];
+    out.emplace_back(w, T);
+    w += kRoundHeaderWords + T * step_words;
+  }
+}
+
+// Appends the wide-bundle kernel's work table (layout in search_plan.hpp):
+// each batch's rounds, longest first, in groups of 16 programs; groups go
+// longest first to the least loaded wave.  The batches' block offsets are
+// written by patch_wide_table once the blocks have their place.  No table
+// (off_wide = 0) when a batch has no literal stream or k is outside 1..7
+// (a step must hold four or eight records).
+void append_wide_table(st_search_plan& plan, const std::vector<RoundList>& rounds) {
+  plan.off_wide = 0;
+  const int k = plan.k_eff;
+  if (k < 1 || k > 7 || plan.batches.empty()) return;
+  for (const SearchBatch& bt : plan.batches)
+    if (bt.stream_words == 0) return;
+  const int rg = kWidePrograms / stream_block_records(k);
+  struct Group {
+    uint32_t batch, steps;
+    uint32_t r[4];
+  };
+  std::vector<Group> groups;
+  RoundList rs;
+  for (size_t bi = 0; bi < rounds.size(); ++bi) {
+    rs = rounds[bi];
+    std::stable_sort(rs.begin(), rs.end(),
+                     [](const auto& x, const auto& y) { return x.second > y.second; });
+    for (size_t i = 0; i < rs.size(); i += rg) {
+      Group g{static_cast<uint32_t>(bi), rs[i].second, {~0u, ~0u, ~0u, ~0u}};
+      for (int j = 0; j < rg && i + j < rs.size(); ++j) g.r[j] = rs[i + j].first;
+      groups.push_back(g);
+    }
+  }
+  std::vector<int> order(groups.size());
+  for (size_t i = 0; i < order.size(); ++i) order[i] = static_cast<int>(i);
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int x, int y) { return groups[x].steps > groups[y].steps; });
+  std::vector<std::vector<int>> per_wave(kSearchWaves);
+  std::vector<int64_t> load(kSearchWaves, 0);
+  for (int i : order) {
+    const int w = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
+    per_wave[w].push_back(i);
+    load[w] += 2 + groups[i].steps;
+  }
+  const size_t nbt = plan.batches.size();
+  std::vector<uint32_t> t(kWideTableHead + 4 * nbt + kWideGroupWords * groups.size(), 0u);
+  t[0] = static_cast<uint32_t>(nbt);
+  t[1] = static_cast<uint32_t>(groups.size());
+  t[2] = static_cast<uint32_t>(rg);
+  for (size_t bi = 0; bi < nbt; ++bi) {
+    const SearchBatch& bt = plan.batches[bi];
+    t[kWideTableHead + 4 * bi + 1] = bt.bound_words;
+    t[kWideTableHead + 4 * bi + 2] = bt.stream_off;
+    t[kWideTableHead + 4 * bi + 3] = bt.stream_masks;
+  }
+  size_t at = kWideTableHead + 4 * nbt;
+  uint32_t g = 0;
+  for (int w = 0; w < kSearchWaves; ++w) {
+    t[4 + w] = g;
+    for (int i : per_wave[w]) {
+      const Group& gr = groups[i];
+      t[at] = gr.batch;
+      t[at + 1] = gr.steps;
+      for (int j = 0; j < 4; ++j) t[at + 2 + j] = gr.r[j];
+      at += kWideGroupWords;
+      ++g;
+    }
+  }
+  t[4 + kSearchWaves] = g;
+  plan.off_wide = plan.blob.size();
+  append_bytes(plan.blob, t.data(), t.size() * 4);
+}
+
+// Writes each batch's width-block offset (in words of the device blob) into
+// the wide-bundle table; drops the table if an offset does not fit 32 bits.
+void patch_wide_table(st_search_plan& plan) {
+  if (plan.off_wide == 0) return;
+  uint32_t* t = reinterpret_cast<uint32_t*>(plan.blob.data() + plan.off_wide);
+  for (size_t bi = 0; bi < plan.batches.size(); ++bi) {
+    const uint64_t words = plan.batches[bi].off_bound / 4;
+    if (words > UINT32_MAX) {
+      plan.off_wide = 0;
+      return;
+    }
+    t[kWideTableHead + 4 * bi] = static_cast<uint32_t>(words);
   }
 }
 
@@ -1059,6 +1163,7 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
     append_bytes(blob, order.data(), order.size() * 4);
 
     const size_t nslots = plan->slot_width.size();
+    std::vector<RoundList> rounds(plan->batches.size());
     for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
       SearchBatch& bt = plan->batches[bi];
       const auto& insns = plan->batch_insns[bi];
@@ -1076,6 +1181,7 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
       }
       static thread_local std::vector<uint32_t> bstart, tmpl, code, wave_rec, wave_skip;
       build_block_template(*plan, bt, insns, starts, bstart, tmpl, code, wave_rec, wave_skip);
+      stream_rounds(tmpl, bt, k_eff, rounds[bi]);
       const uint32_t words = static_cast<uint32_t>(tmpl.size());
       bt.bound_words = words;
       bt.off_bound_start = blob.size();
@@ -1092,6 +1198,8 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
         expand_block(tmpl, code, pos.data() + s * bt.num_terms * kp, kp, plan->slot_width[s],
                      block + s * words);
     }
+    append_wide_table(*plan, rounds);
+    patch_wide_table(*plan);
     // Scalar loads may read a few words past the last program.
     blob.resize(blob.size() + 256, 0);
     plan->bound_bundles = num_bundles;
@@ -1108,10 +1216,12 @@ extern "C" int st_search_plan_prepare_device_binding(st_search_plan* plan,
     ST_CHECK(num_bundles >= 0, "negative bundle count");
     auto& blob = plan->blob;
     std::vector<uint32_t> bstart, tmpl, code, wave_rec, wave_skip;
+    std::vector<RoundList> rounds(plan->batches.size());
     for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
       SearchBatch& bt = plan->batches[bi];
       build_block_template(*plan, bt, plan->batch_insns[bi], plan->batch_starts[bi], bstart,
                            tmpl, code, wave_rec, wave_skip);
+      stream_rounds(tmpl, bt, plan->k_eff, rounds[bi]);
       bt.bound_words = static_cast<uint32_t>(tmpl.size());
       bt.off_bound_start = blob.size();
       append_bytes(blob, bstart.data(), bstart.size() * 4);
@@ -1124,6 +1234,7 @@ extern "C" int st_search_plan_prepare_device_binding(st_search_plan* plan,
       bt.off_tmpl_code = blob.size();
       append_bytes(blob, code.data(), code.size() * 4);
     }
+    append_wide_table(*plan, rounds);
     blob.resize(blob.size() + 256, 0);  // slack for scalar loads
     // The device-written part follows the uploaded bytes.
     uint64_t d = align_to(blob.size(), 256);
@@ -1139,6 +1250,7 @@ extern "C" int st_search_plan_prepare_device_binding(st_search_plan* plan,
       bt.off_bound = d;
       d = align_to(d + 4ull * kMaxWidthSlots * bt.bound_words, 256);
     }
+    patch_wide_table(*plan);
     plan->device_bytes = d + 256;  // slack after the last width block
     plan->bound_bundles = num_bundles;
     plan->device_bind = true;

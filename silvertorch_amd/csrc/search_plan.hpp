@@ -96,7 +96,8 @@ inline int positions_per_term(int k_eff) {
 // Bound stack form: header, T position lists of positions_per_term(K)
 // words, then the operations.
 // Positions are LDS byte offsets (row * 256) for bundles staged in LDS and
-// signed rows relative to the bundle start otherwise.
+// signed rows relative to the bundle start otherwise (no-op rows: kPosOnes /
+// kPosZeros, or kWideOnesRow / kWideZerosRow at wide widths, see below).
 constexpr int kMaxWidthSlots = 64;
 constexpr uint32_t kNoWidthSlot = 0xFFFFFFFFu;
 
@@ -158,6 +159,35 @@ struct SearchBatch {
   uint64_t off_stream_skip = 0;  // uint32[kSearchWaves]: flat programs each run covers
 };
 
+// Wide bundles (kSearchTileRows < b <= kWideRows rows, width-bound) are
+// searched by a second kernel in column slices: 64 bytes (8 words, 512
+// docs) of every row staged in LDS at a time, four slices per bundle, the
+// literal streams of all batches evaluated on each slice.  Their bound
+// positions are plain row numbers; the all-ones and all-zeros no-op rows are
+// coded as rows kWideRows and kWideRows + 1 (the slice tile's two virtual
+// rows).
+constexpr int kWideRows = 2048;
+constexpr int kWideOnesRow = kWideRows;
+constexpr int kWideZerosRow = kWideRows + 1;
+constexpr int kWideSliceBytes = 64;
+constexpr int kWideSlices = 256 / kWideSliceBytes;
+constexpr bool wide_width(int64_t b) { return b > kSearchTileRows && b <= kWideRows; }
+
+// Work table of the wide-bundle kernel (uint32 words at
+// st_search_plan::off_wide, absent when off_wide == 0):
+//   [0] batches, [1] groups, [2] rounds per group, [3] 0,
+//   [4 .. 4 + kSearchWaves] first group of each wave (groups are stored
+//     wave by wave), padded to kWideTableHead words;
+//   per batch, 4 words: [word offset of its width blocks in the device blob,
+//     words per width block, stream offset within a block, stream_masks];
+//   per group, 8 words: [batch, longest round's steps, round 0 .. 3 word
+//     offsets within the stream (~0u: none), 0, 0].
+// A group is stream_block_records(k) * rounds-per-group = 16 programs, one
+// per 4-lane group of a wave.
+constexpr int kWideTableHead = 24;
+constexpr int kWideGroupWords = 8;
+constexpr int kWidePrograms = 16;
+
 // Codes of a width-block template word.
 constexpr uint32_t kTmplCopy = 0u;           // the template word itself
 constexpr uint32_t kTmplOnes = 0xFFFFFFFFu;  // the all-ones row at the slot's width
@@ -191,4 +221,6 @@ struct st_search_plan {
   uint64_t device_bytes = 0;         // size of the device copy
   uint64_t off_num_slots = 0;        // uint32[1] (device-written)
   uint64_t off_slot_width = 0;       // int64[kMaxWidthSlots] (device-written)
+  // work table of the wide-bundle kernel (0: none), set by either binding
+  uint64_t off_wide = 0;
 };

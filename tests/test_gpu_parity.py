@@ -371,3 +371,48 @@ def test_mixed_bundle_kinds_in_one_launch():
     np.testing.assert_array_equal(H.search(index, bbo, pd, po, 1, 5), want)
     np.testing.assert_array_equal(H.search(index, bbo, pd, po, 1, 5, bool_mask=True, bind="device"),
                                   O.unpack_bool(want))
+
+
+@pytest.mark.parametrize("k,neg,many", [(1, False, False), (3, True, False), (4, False, False),
+                                        (4, True, True), (7, True, False)])
+def test_wide_bundle_slices_vs_oracle(k, neg, many):
+    """Bundles wider than the LDS tile and at most 2048 rows (searched in
+    column slices by the wide-bundle kernel in packed mode) next to staged
+    bundles and bundles past 2048 rows (global-memory path), for several k,
+    with and without negated literals, in one or several query batches
+    (`many`: more distinct terms than one batch holds).  Packed, bool and
+    counted outputs against the oracle, for host-bound, device-bound and
+    unbound plans."""
+    rng = np.random.default_rng(500 + k)
+    heavy = {1: [150, 300, 700, 1024, 1100], 3: [50, 100, 300, 341, 400],
+             4: [40, 100, 200, 256, 300], 7: [20, 50, 100, 146, 200]}[k]
+    nb, F, vocab = 23, 2, 3000
+    n = nb * 2048 - 700  # ragged last bundle
+    cnt = rng.integers(1, 4, (n, F)).astype(np.int64)
+    for b in range(nb):  # one heavy doc per bundle sets the width
+        cnt[b * 2048 + int(rng.integers(0, min(2048, n - b * 2048))), 0] = heavy[b % len(heavy)]
+    offs = np.concatenate([[0], np.cumsum(cnt.reshape(-1))]).astype(np.int64)
+    vals = rng.integers(0, vocab, int(offs[-1])).astype(np.int64)
+    ids = np.array([1, 2], dtype=np.int32)
+    index, bbo = H.build(ids, offs, vals, 2.0, k)
+    widths = np.diff(bbo)
+    assert (widths <= 512).any() and ((widths > 512) & (widths <= 2048)).any() and (widths > 2048).any()
+
+    def term():
+        t = f"{int(rng.integers(1, F + 1))}:{int(rng.integers(0, vocab))}"
+        return ("NOT " + t) if neg and rng.random() < 0.2 else t
+
+    if many:
+        queries = [" OR ".join(term() for _ in range(40)) for _ in range(120)]
+    else:
+        queries = [" OR ".join(" AND ".join(term() for _ in range(int(rng.integers(1, 3))))
+                               for _ in range(int(rng.integers(1, 5)))) for _ in range(300)]
+    pd, po = _plans(queries, 7, 64 if many else 5)
+    H.note(f"[wide] k={k} neg={neg} many={many} widths={sorted(set(widths.tolist()))}")
+    want = O.search_packed(index, bbo, pd, po, k, 7)
+    np.testing.assert_array_equal(H.search(index, bbo, pd, po, k, 7), want)
+    np.testing.assert_array_equal(H.search(index, bbo, pd, po, k, 7, bool_mask=True, bind="device"),
+                                  O.unpack_bool(want))
+    _, ro, packed = H.search_ids(index, bbo, pd, po, k, 7, n)
+    np.testing.assert_array_equal(packed, want)
+    np.testing.assert_array_equal(ro, O.compact(want, n)[1])
