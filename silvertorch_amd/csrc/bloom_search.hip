@@ -167,6 +167,11 @@ __global__ __launch_bounds__(kCensusThreads) void width_census_kernel(
   }
   __syncthreads();
   if (threadIdx.x == 0) {  // bucket sizes -> bucket starts
+    // num_slots[1]: every bundle has a slot, and every slot width is wide
+    bool all_wide = cursor[kMaxWidthSlots] == 0;
+    const uint32_t ns = n < static_cast<uint32_t>(kMaxWidthSlots) ? n : kMaxWidthSlots;
+    for (uint32_t s = 0; s < ns; ++s) all_wide &= wide_width(slot_width[s]);
+    num_slots[1] = all_wide ? 1u : 0u;
     uint32_t run = 0;
     for (int b = 0; b <= kMaxWidthSlots; ++b) {
       const uint32_t c = cursor[b];
@@ -203,7 +208,8 @@ __device__ uint32_t device_term_position(const uint64_t* h, int hash_k, int k_ef
   const int16_t row = cnt == 0 ? 0 : (r < cnt ? found[r] : found[0]);
   if (b <= kSearchTileRows)
     return static_cast<uint32_t>(cnt == 0 ? kSearchZerosRow : row) * 256u;
-  if (wide_width(b)) return static_cast<uint32_t>(cnt == 0 ? kWideZerosRow : row);
+  if (wide_width(b))
+    return static_cast<uint32_t>(cnt == 0 ? kWideZerosRow : row) * kWideSliceBytes;
   return cnt == 0 ? static_cast<uint32_t>(kPosZeros)
                   : static_cast<uint32_t>(static_cast<int32_t>(row));
 }
@@ -226,10 +232,12 @@ __global__ void bind_fill_kernel(const uint32_t* __restrict__ tmpl,
     v = tmpl[i];
   } else if (c == kTmplOnes) {
     v = b <= kSearchTileRows ? static_cast<uint32_t>(kSearchOnesRow) * 256u
-                             : static_cast<uint32_t>(wide_width(b) ? kWideOnesRow : kPosOnes);
+        : wide_width(b)      ? static_cast<uint32_t>(kWideOnesRow) * kWideSliceBytes
+                             : static_cast<uint32_t>(kPosOnes);
   } else if (c == kTmplZeros) {
     v = b <= kSearchTileRows ? static_cast<uint32_t>(kSearchZerosRow) * 256u
-                             : static_cast<uint32_t>(wide_width(b) ? kWideZerosRow : kPosZeros);
+        : wide_width(b)      ? static_cast<uint32_t>(kWideZerosRow) * kWideSliceBytes
+                             : static_cast<uint32_t>(kPosZeros);
   } else {
     const uint32_t t = (c >> 4) - 1u;
     v = device_term_position(hashes + static_cast<uint64_t>(t) * hash_k, hash_k, k_eff, b,
@@ -293,6 +301,19 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
     }
   }
   for (const SearchBatch& bt : plan->batches) {
+    // 2 tells the kernel that every program of the batch is in the stream,
+    // so that wide bundles need nothing from it
+    uint32_t wide_flag = 0;
+    if (wide_fn != nullptr) {
+      const auto* wo = reinterpret_cast<const uint32_t*>(plan->blob.data() + bt.off_wave);
+      const auto* sk = reinterpret_cast<const uint32_t*>(plan->blob.data() + bt.off_stream_skip);
+      bool all = true;
+      for (int w = 0; w < kSearchWaves; ++w) all &= wo[w + 1] - wo[w] == sk[w];
+      wide_flag = all ? 2u : 1u;
+    }
+    // Nothing for the per-batch kernel when the wide-bundle kernel covers
+    // every bundle (known here with host-bound widths).
+    if (wide_flag == 2 && !plan->device_bind && plan->all_wide) continue;
     // Quad-lane stream evaluation when the batch's literal stream fits the
     // LDS area after the tile and a stream step holds whole quads (k <= 7).
     const int kk = std::max(plan->k_eff, 1);
@@ -314,7 +335,8 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
         bound ? at(bt.off_stream_skip) : nullptr, bound ? bt.stream_off : 0u,
         bound ? bt.stream_words : 0u, bound ? bt.stream_masks : 0u, bt.num_terms,
         static_cast<int32_t>(plan->hash_k),
-        num_bundles * 32, out, counts, num_docs, wide_fn != nullptr ? 1u : 0u);
+        num_bundles * 32, out, counts, num_docs, wide_flag,
+        plan->device_bind ? at(plan->off_num_slots) : nullptr);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
       throw Error(ST_ERR_HIP, cat("search kernel launch failed: ", hipGetErrorString(e)));

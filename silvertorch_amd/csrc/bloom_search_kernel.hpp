@@ -370,11 +370,13 @@ __device__ __forceinline__ uint32_t row_word(const RowSource& rs, uint32_t p) {
   if constexpr (STAGED) {
     return *reinterpret_cast<const uint32_t*>(rs.tile_lane + p);
   } else {
-    const int32_t r = static_cast<int32_t>(p);
+    int32_t r = static_cast<int32_t>(p);
     if (r == kPosZeros) return 0;
     if (r == kPosOnes) return ~0u;
-    // a row at or past the width is a no-op code of a wide width
-    if (r >= rs.b) return r == kWideOnesRow ? ~0u : 0u;
+    if (wide_width(rs.b)) {  // a slice-tile byte offset; rows past b are no-op rows
+      r /= kWideSliceBytes;
+      if (r >= rs.b) return r == kWideOnesRow ? ~0u : 0u;
+    }
     const int64_t row = rs.start + r;
     if (row < 0 || (row * 32 + (rs.lane >> 1)) >= rs.index_numel) return 0;
     return rs.index32[row * 64 + rs.lane];
@@ -887,7 +889,11 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     uint32_t stream_masks,
     uint32_t num_terms, int32_t hash_k,
     int64_t out_cols, void* __restrict__ out, int64_t* __restrict__ counts, int64_t num_docs,
-    uint32_t wide_skip) {
+    uint32_t wide_skip, const uint32_t* __restrict__ census) {
+  // wide_skip == 2: the wide-bundle kernel evaluates every program of this
+  // batch on wide bundles; census[1] (device binding) says every bundle is
+  // one, so nothing is left for this launch
+  if (wide_skip == 2 && census != nullptr && as_const(census)[1] != 0u) return;
   SearchArgs a;
   a.index = index;
   a.index_numel = index_numel;
@@ -987,8 +993,10 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     const bool quad_here = quad_bundle(cur);
     // the wide-bundle kernel evaluates the literal stream of this bundle
     const bool wide_here = wide_skip != 0 && slot != kNoWidthSlot && wide_width(b);
+    // ... and every program of this batch is in the stream: nothing to do here
+    const bool skip = wide_here && wide_skip == 2;
 
-    __syncthreads();  // previous bundle's readers are done with tile and pos
+    if (!skip) __syncthreads();  // previous bundle's readers are done with tile and pos
     if (staged) {
       const int64_t chunks = b * 16;
 #pragma unroll
@@ -1015,7 +1023,7 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
       prefetch_tile(a, nxt.start, nxt.b, pre);
       if (quad_bundle(nxt)) prefetch_stream(nxt, spre);
     }
-    if (slot == kNoWidthSlot && b != prev_b) {
+    if (!skip && slot == kNoWidthSlot && b != prev_b) {
       const FastMod64 fm = make_fastmod_dev(static_cast<uint64_t>(b));
       for (uint32_t u = tid; u < a.num_terms; u += kSearchThreads) {
         int16_t found[K];
@@ -1040,7 +1048,7 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
       }
       prev_b = b;
     }
-    __syncthreads();
+    if (!skip) __syncthreads();
     asm volatile("" ::"s"(warm));  // the warming loads are complete by now
 
     BundleMeta after{0, 0, 0, kNoWidthSlot};
@@ -1056,7 +1064,9 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     rs.b = b;
     rs.lane = lane;
     rs.staged = staged;
-    if constexpr (kQuad) {
+    if (skip) {
+      // evaluated by the wide-bundle kernel
+    } else if constexpr (kQuad) {
       // Quad instance: stream programs of staged slot bundles in quads, all
       // other bundles' programs from the width block one by one.
       if (quad_here) {
@@ -1122,87 +1132,169 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
 // LDS tile.  bloom_wide_kernel searches them in kWideSlices column slices:
 // the slice's 64 bytes of every row (512 docs) are staged in LDS, followed by
 // the all-ones and all-zeros rows (kWideOnesRow, kWideZerosRow), and the
-// literal streams of every batch are evaluated on the slice sixteen programs
-// per wave instruction: lane l serves program l >> 2 of the wave's current
-// group (round (l >> 2) / NB, slot (l >> 2) % NB) and owns bytes
-// 16 * (l & 3) .. +15 of every slice row, so one 16-byte LDS read per lane
-// fetches a row for its program.  Each lane reads its program's records from
-// the width block in global memory (shared by every bundle of the width,
-// so L2-resident), two steps ahead.  The index is read once per search,
-// whatever the number of batches.  Packed output only.
+// literal streams of every batch are evaluated on it 16 programs per wave
+// instruction: the four lanes of quad p serve program p of the wave's current
+// group (round p / NB, slot p % NB), each owning 16 bytes of every slice row
+// (one 16-byte LDS read per row position).  The quad loads its program's
+// stream record together (a quarter each; values reach the other lanes by
+// DPP, fused into the LDS address add) from the width block in global
+// memory, shared by every bundle of the width and so L2-resident, three
+// steps ahead.  The index is read once per search, whatever the number of
+// batches.  Packed output only.
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kWidePieces = kWideSliceBytes / 16;  // u32x4 per slice row
 constexpr int kWidePrefetch = kWideRows * kWidePieces / kSearchThreads;
 static_assert(kWidePrefetch * kSearchThreads == kWideRows * kWidePieces, "slice split");
 
+// LDS pointers (address space 3): reads through them are ds_read, and a
+// byte offset added to one is a 32-bit add.
+#define ST_LDS __attribute__((address_space(3)))
+
+// Word i of a quad's stream record as every lane of the quad sees it: lane q
+// holds words WPL * q .. WPL * q + WPL - 1, and the value moves by DPP
+// (quad_perm broadcast, with bound_ctrl so that a following add absorbs
+// the move).
+template <int WPL>
+__device__ __forceinline__ uint32_t quad_word(const uint32_t (&r)[WPL], int i) {
+  const uint32_t v = r[i % WPL];
+  switch (i / WPL) {
+    case 0: return __builtin_amdgcn_mov_dpp(v, 0x00, 0xF, 0xF, true);
+    case 1: return __builtin_amdgcn_mov_dpp(v, 0x55, 0xF, 0xF, true);
+    case 2: return __builtin_amdgcn_mov_dpp(v, 0xAA, 0xF, 0xF, true);
+    default: return __builtin_amdgcn_mov_dpp(v, 0xFF, 0xF, 0xF, true);
+  }
+}
+
+// 3-input bitwise functions (v_bitop3_b32 truth tables over a = 0xF0,
+// b = 0xCC, c = 0xAA).
+__device__ __forceinline__ uint32_t and_xor(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0x6A);  // (a & b) ^ c
+}
+__device__ __forceinline__ uint32_t or_and(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0xA8);  // (a | b) & c
+}
+__device__ __forceinline__ uint32_t or_andb(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0xF8);  // a | (b & c)
+}
+
+// One literal step of a lane's program: K row positions (slice-tile byte
+// offsets) and the flags from the quad's record, K LDS reads of the lane's
+// 16 bytes, the OR-of-ANDs fold.
+template <int K, bool MASKS, int WPL>
+__device__ __forceinline__ void wide_step(const uint32_t (&r)[WPL], const ST_LDS char* tile_lane,
+                                          u32x4& res, u32x4& acc) {
+  u32x4 row[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    row[k] = *reinterpret_cast<const ST_LDS u32x4*>(tile_lane + quad_word<WPL>(r, k));
+  const uint32_t f = quad_word<WPL>(r, K);
+  u32x4 t = row[0];
+#pragma unroll
+  for (int k = 1; k + 1 < K; ++k) t &= row[k];
+  // negated literal (mask neg) folded into the last AND; group mask g
+  const uint32_t neg = MASKS ? 0u : 0u - (f & kStreamNeg);
+  const uint32_t g = MASKS ? f : 0u - ((f >> 1) & 1u);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    uint32_t tc = u32x4_get(t, c);
+    if constexpr (K > 1)
+      tc = MASKS ? (tc & u32x4_get(row[K - 1], c)) : and_xor(tc, u32x4_get(row[K - 1], c), neg);
+    else if constexpr (!MASKS)
+      tc ^= neg;
+    const uint32_t ac = u32x4_get(acc, c), rc = u32x4_get(res, c);
+    const uint32_t nres = or_andb(rc, ac, g);
+    const uint32_t nacc = or_and(ac, g, tc);
+    if (c == 0) { res.x = nres; acc.x = nacc; }
+    if (c == 1) { res.y = nres; acc.y = nacc; }
+    if (c == 2) { res.z = nres; acc.z = nacc; }
+    if (c == 3) { res.w = nres; acc.w = nacc; }
+  }
+}
+
 // One group of 16 programs on the staged slice: each lane folds its
 // program's literals over its 16 bytes and stores them to output row
-// (info >> kSlotRowShift).  `out_lane` is the lane's byte address in output
-// row 0.
+// (info >> kSlotRowShift).  `stream` is the batch's stream in this bundle's
+// width block; `out_lane` the lane's byte address in output row 0.  The loop
+// runs the group's longest round (its first) with uniform control; a lane
+// whose round is shorter repeats its last record, which leaves the
+// OR-of-ANDs fold unchanged.  Each lane loads its share of the record three
+// steps ahead into one of three buffers.
 template <int K, bool MASKS>
-__device__ __forceinline__ void wide_eval_group(const uint32_t* stream,
-                                                const ST_CONST uint32_t* grp,
-                                                const char* tile_lane, int lane,
+__device__ __forceinline__ void wide_eval_group(const char* stream, const ST_CONST uint32_t* grp,
+                                                const ST_LDS char* tile_lane, int lane,
                                                 int64_t row_bytes, char* out_lane) {
   using S = QuadShape<K>;
-  constexpr uint32_t kStep = S::NB * S::RV;  // u32x4 per stream step
+  constexpr int WPL = S::RW / 4;  // record words per lane
+  constexpr int kRounds = kWidePrograms / S::NB;
+  constexpr uint32_t kStepBytes = S::NB * S::RW * 4;  // 128
   const int pg = lane >> 2;
   const int rr = pg / S::NB;
   const int sl = pg % S::NB;
-  const uint32_t r0 = grp[2], r1 = grp[3], r2 = grp[4], r3 = grp[5];
-  const uint32_t roff = rr == 0 ? r0 : (rr == 1 ? r1 : (rr == 2 ? r2 : r3));
-  if (roff == ~0u) return;
-  const uint32_t* round = stream + roff;
-  const uint32_t T = round[0];
-  const uint32_t info = round[kRoundSlotInfo + sl];
-  const u32x4* rec = reinterpret_cast<const u32x4*>(round + kRoundHeaderWords + sl * S::RW);
-  u32x4 ra[S::RV], rb[S::RV];
-  const uint32_t last = T > 0 ? T - 1 : 0;
+  uint32_t roff = grp[2], T = grp[2 + kWideMaxRounds];
 #pragma unroll
-  for (int v = 0; v < S::RV; ++v) {
-    ra[v] = rec[v];
-    rb[v] = rec[min(1u, last) * kStep + v];
+  for (int i = 1; i < kRounds; ++i) {
+    if (rr == i) {
+      roff = grp[2 + i];
+      T = grp[2 + kWideMaxRounds + i];
+    }
   }
-  u32x4 res{0, 0, 0, 0}, acc{0, 0, 0, 0};
-  for (uint32_t j = 0; j < T; ++j) {
-    // the record two steps ahead (the last one again near the end)
-    u32x4 rc[S::RV];
-    const u32x4* nx = rec + min(j + 2, last) * kStep;
-#pragma unroll
-    for (int v = 0; v < S::RV; ++v) rc[v] = nx[v];
-    u32x4 t = *reinterpret_cast<const u32x4*>(tile_lane + (u32x4_get(ra[0], 0) << 6));
-#pragma unroll
-    for (int k = 1; k < K; ++k)
-      t &= *reinterpret_cast<const u32x4*>(tile_lane + (u32x4_get(ra[k >> 2], k & 3) << 6));
-    const uint32_t f = u32x4_get(ra[K >> 2], K & 3);
-    if constexpr (MASKS) {  // f is the group mask; nothing is negated
-      res |= acc & f;
-      acc = (acc | f) & t;
+  const bool valid = roff != ~0u;
+  if (!valid) {  // compute on a real round, store nothing
+    roff = grp[2];
+    T = grp[2 + kWideMaxRounds];
+  }
+  const uint32_t rb = roff * 4;
+  const uint32_t info = *reinterpret_cast<const uint32_t*>(stream + rb + (kRoundSlotInfo + sl) * 4);
+  const uint32_t steps = grp[1];
+  const uint32_t o_first = rb + kRoundHeaderWords * 4 + sl * S::RW * 4 + (lane & 3) * WPL * 4;
+  const uint32_t o_last = o_first + (T > 0 ? T - 1 : 0) * kStepBytes;
+  uint32_t o = o_first;
+  typedef uint32_t Share[WPL];
+  auto next = [&](Share& r) {
+    if constexpr (WPL == 1) {
+      r[0] = *reinterpret_cast<const uint32_t*>(stream + o);
     } else {
-      const uint32_t neg = 0u - (f & kStreamNeg);
-      const uint32_t grpm = 0u - ((f >> 1) & 1u);
-      res |= acc & grpm;
-      acc = (acc | grpm) & (t ^ neg);
+      const u32x2 v = *reinterpret_cast<const u32x2*>(stream + o);
+      r[0] = v.x;
+      r[1] = v.y;
     }
-#pragma unroll
-    for (int v = 0; v < S::RV; ++v) {
-      ra[v] = rb[v];
-      rb[v] = rc[v];
-    }
+    o = min(o + kStepBytes, o_last);
+  };
+  Share b0, b1, b2;
+  next(b0);
+  next(b1);
+  next(b2);
+  u32x4 res{0, 0, 0, 0}, acc{0, 0, 0, 0};
+  // whole triples with a branch-free body (loads stay three steps ahead),
+  // then the one or two steps left
+  uint32_t j = 0;
+  for (; j + 3 <= steps; j += 3) {
+    wide_step<K, MASKS, WPL>(b0, tile_lane, res, acc);
+    next(b0);
+    wide_step<K, MASKS, WPL>(b1, tile_lane, res, acc);
+    next(b1);
+    wide_step<K, MASKS, WPL>(b2, tile_lane, res, acc);
+    next(b2);
   }
+  if (j < steps) wide_step<K, MASKS, WPL>(b0, tile_lane, res, acc);
+  if (j + 1 < steps) wide_step<K, MASKS, WPL>(b1, tile_lane, res, acc);
   u32x4 v = res | acc;
   if (info & kSlotComplement) v = ~v;
-  if (info & kSlotValid)
+  if (valid && (info & kSlotValid))
     __builtin_nontemporal_store(
         v, (ST_GLOBAL u32x4*)(out_lane + static_cast<int64_t>(info >> kSlotRowShift) * row_bytes));
 }
 
-// Grid: one 1024-thread workgroup per CU; workgroup w takes the wide
-// bundles w, w + grid, ... of index order, each as kWideSlices slices in
-// order, the next slice's loads in flight while the current one is
-// evaluated.  `num_slots` / `slot_width` (device binding; nullptr when the
-// host decided to launch) let the kernel return at once when no slot width
-// is wide.
+// Grid: 1024-thread workgroups, one per CU.  When the grid is a multiple
+// of 16, workgroups w and w + 8 (dispatched to the same XCD) form a pair
+// that walks the wide bundles p, p + grid / 2, ... of index order, one
+// member taking slices 0 and 2, the other 1 and 3, so the two halves of each
+// 128-byte index line are read by the same XCD at about the same time;
+// otherwise workgroup w takes bundles w, w + grid, ... with all slices.  The
+// next slice's loads are in flight while the current one is evaluated.
+// `num_slots` / `slot_width` (device binding; nullptr when the host decided
+// to launch) let the kernel return at once when no slot width is wide.
 template <int K>
 __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
     const int64_t* __restrict__ index, int64_t index_numel,
@@ -1235,10 +1327,15 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
   const ST_CONST uint32_t* batches = tab + kWideTableHead;
   const ST_CONST uint32_t* groups = batches + 4 * nbt;
   const int64_t grid = gridDim.x;
+  const bool paired = grid % 16 == 0;
+  const int64_t first = paired ? (blockIdx.x >> 4) * 8 + (blockIdx.x & 7) : blockIdx.x;
+  const int64_t stride = paired ? grid / 2 : grid;
+  const int s_first = paired ? static_cast<int>((blockIdx.x >> 3) & 1) : 0;
+  const int s_step = paired ? 2 : 1;
 
   // first wide bundle at or after i on this workgroup's stride
   auto next_wide = [&](int64_t i) -> int64_t {
-    for (; i < num_bundles; i += grid) {
+    for (; i < num_bundles; i += stride) {
       const int64_t b = boff[i + 1] - boff[i];
       if (bslot[i] != kNoWidthSlot && wide_width(b)) return i;
     }
@@ -1259,21 +1356,21 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
     }
   };
 
-  int64_t cb = next_wide(blockIdx.x);
+  int64_t cb = next_wide(first);
   if (cb >= num_bundles) return;
-  int cs = 0;
+  int cs = s_first;
   u32x4 pre[kWidePrefetch];
   prefetch(cb, cs, pre);
-  const char* tile_lane = reinterpret_cast<const char*>(tile) + (lane & 3) * 16;
+  const ST_LDS char* tile_lane = (const ST_LDS char*)(tile) + (lane & 3) * 16;
   const int64_t row_bytes = out_cols * 8;
   for (;;) {
     const int64_t b = boff[cb + 1] - boff[cb];
     const uint32_t slot = bslot[cb];
     int64_t nb = cb;
-    int ns = cs + 1;
-    if (ns == kWideSlices) {
-      nb = next_wide(cb + grid);
-      ns = 0;
+    int ns = cs + s_step;
+    if (ns >= kWideSlices) {
+      nb = next_wide(cb + stride);
+      ns = s_first;
     }
     const bool has_next = nb < num_bundles;
     __syncthreads();  // the previous slice's readers are done
@@ -1284,12 +1381,13 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
     }
     if (has_next) prefetch(nb, ns, pre);
     __syncthreads();
-    char* out_lane = reinterpret_cast<char*>(out) + cb * 256 + cs * kWideSliceBytes + (lane & 3) * 16;
+    char* out_lane =
+        reinterpret_cast<char*>(out) + cb * 256 + cs * kWideSliceBytes + (lane & 3) * 16;
     for (uint32_t g = g_begin; g < g_end; ++g) {
       const ST_CONST uint32_t* grp = groups + static_cast<uint64_t>(g) * kWideGroupWords;
       const ST_CONST uint32_t* bt = batches + 4 * grp[0];
-      const uint32_t* stream =
-          blob + bt[0] + static_cast<uint64_t>(slot) * bt[1] + bt[2];
+      const char* stream = reinterpret_cast<const char*>(
+          blob + bt[0] + static_cast<uint64_t>(slot) * bt[1] + bt[2]);
       if (bt[3])
         wide_eval_group<K, true>(stream, grp, tile_lane, lane, row_bytes, out_lane);
       else
@@ -1327,7 +1425,7 @@ using KernelFn = void (*)(const int64_t*, int64_t, const int64_t*, int64_t,
                           const uint32_t*, const uint32_t*, const uint32_t*, uint32_t,
                           const uint32_t*, const uint32_t*, uint32_t, uint32_t, uint32_t,
                           uint32_t, int32_t,
-                          int64_t, void*, int64_t*, int64_t, uint32_t);
+                          int64_t, void*, int64_t*, int64_t, uint32_t, const uint32_t*);
 
 // The kernels of one K (all output modes; the quad instance evaluates the
 // literal stream in quad lanes and needs a stream that fits the LDS and k <= 7),

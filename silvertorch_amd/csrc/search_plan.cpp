@@ -774,7 +774,7 @@ void term_positions(const uint64_t* h, int64_t hash_k, int k_eff, int64_t b,
     if (staged) {
       out[j] = static_cast<uint32_t>(cnt == 0 ? kSearchZerosRow : r) * 256u;
     } else if (wide_width(b)) {
-      out[j] = static_cast<uint32_t>(cnt == 0 ? kWideZerosRow : r);
+      out[j] = static_cast<uint32_t>(cnt == 0 ? kWideZerosRow : r) * kWideSliceBytes;
     } else {
       out[j] = cnt == 0 ? static_cast<uint32_t>(kPosZeros)
                         : static_cast<uint32_t>(static_cast<int32_t>(r));
@@ -964,9 +964,11 @@ void expand_block(const std::vector<uint32_t>& tmpl, const std::vector<uint32_t>
   const bool staged = width <= kSearchTileRows;
   const bool wide = wide_width(width);
   const uint32_t ones = staged ? static_cast<uint32_t>(kSearchOnesRow) * 256u
-                               : static_cast<uint32_t>(wide ? kWideOnesRow : kPosOnes);
+                       : wide ? static_cast<uint32_t>(kWideOnesRow) * kWideSliceBytes
+                              : static_cast<uint32_t>(kPosOnes);
   const uint32_t zeros = staged ? static_cast<uint32_t>(kSearchZerosRow) * 256u
-                                : static_cast<uint32_t>(wide ? kWideZerosRow : kPosZeros);
+                        : wide ? static_cast<uint32_t>(kWideZerosRow) * kWideSliceBytes
+                               : static_cast<uint32_t>(kPosZeros);
   for (size_t i = 0; i < tmpl.size(); ++i) {
     const uint32_t c = code[i];
     if (c == kTmplCopy) {
@@ -1013,7 +1015,7 @@ void append_wide_table(st_search_plan& plan, const std::vector<RoundList>& round
   const int rg = kWidePrograms / stream_block_records(k);
   struct Group {
     uint32_t batch, steps;
-    uint32_t r[4];
+    uint32_t r[kWideMaxRounds], t[kWideMaxRounds];
   };
   std::vector<Group> groups;
   RoundList rs;
@@ -1022,8 +1024,12 @@ void append_wide_table(st_search_plan& plan, const std::vector<RoundList>& round
     std::stable_sort(rs.begin(), rs.end(),
                      [](const auto& x, const auto& y) { return x.second > y.second; });
     for (size_t i = 0; i < rs.size(); i += rg) {
-      Group g{static_cast<uint32_t>(bi), rs[i].second, {~0u, ~0u, ~0u, ~0u}};
-      for (int j = 0; j < rg && i + j < rs.size(); ++j) g.r[j] = rs[i + j].first;
+      Group g{static_cast<uint32_t>(bi), rs[i].second, {}};
+      for (int j = 0; j < kWideMaxRounds; ++j) g.r[j] = ~0u, g.t[j] = 0;
+      for (int j = 0; j < rg && i + j < rs.size(); ++j) {
+        g.r[j] = rs[i + j].first;
+        g.t[j] = rs[i + j].second;
+      }
       groups.push_back(g);
     }
   }
@@ -1057,7 +1063,10 @@ void append_wide_table(st_search_plan& plan, const std::vector<RoundList>& round
       const Group& gr = groups[i];
       t[at] = gr.batch;
       t[at + 1] = gr.steps;
-      for (int j = 0; j < 4; ++j) t[at + 2 + j] = gr.r[j];
+      for (int j = 0; j < kWideMaxRounds; ++j) {
+        t[at + 2 + j] = gr.r[j];
+        t[at + 2 + kWideMaxRounds + j] = gr.t[j];
+      }
       at += kWideGroupWords;
       ++g;
     }
@@ -1136,7 +1145,11 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
       plan->slot_width.push_back(wf.first);
     }
     std::vector<uint32_t> bundle_slot(num_bundles);
-    for (int64_t i = 0; i < num_bundles; ++i) bundle_slot[i] = census_slot[cell_of(width[i])];
+    plan->all_wide = true;
+    for (int64_t i = 0; i < num_bundles; ++i) {
+      bundle_slot[i] = census_slot[cell_of(width[i])];
+      plan->all_wide &= bundle_slot[i] != kNoWidthSlot && wide_width(width[i]);
+    }
     // Visiting order: bundles grouped by slot (then by width), so that a
     // workgroup striding through it meets long runs of one width and reuses
     // that width's programs from the scalar cache.

@@ -97,7 +97,7 @@ inline int positions_per_term(int k_eff) {
 // words, then the operations.
 // Positions are LDS byte offsets (row * 256) for bundles staged in LDS and
 // signed rows relative to the bundle start otherwise (no-op rows: kPosOnes /
-// kPosZeros, or kWideOnesRow / kWideZerosRow at wide widths, see below).
+// kPosZeros), except at wide widths (see below): slice-tile byte offsets.
 constexpr int kMaxWidthSlots = 64;
 constexpr uint32_t kNoWidthSlot = 0xFFFFFFFFu;
 
@@ -163,9 +163,9 @@ struct SearchBatch {
 // searched by a second kernel in column slices: 64 bytes (8 words, 512
 // docs) of every row staged in LDS at a time, four slices per bundle, the
 // literal streams of all batches evaluated on each slice.  Their bound
-// positions are plain row numbers; the all-ones and all-zeros no-op rows are
-// coded as rows kWideRows and kWideRows + 1 (the slice tile's two virtual
-// rows).
+// positions are byte offsets in that slice tile (row * kWideSliceBytes);
+// the all-ones and all-zeros no-op rows are the tile's rows kWideOnesRow and
+// kWideZerosRow.
 constexpr int kWideRows = 2048;
 constexpr int kWideOnesRow = kWideRows;
 constexpr int kWideZerosRow = kWideRows + 1;
@@ -180,13 +180,15 @@ constexpr bool wide_width(int64_t b) { return b > kSearchTileRows && b <= kWideR
 //     wave by wave), padded to kWideTableHead words;
 //   per batch, 4 words: [word offset of its width blocks in the device blob,
 //     words per width block, stream offset within a block, stream_masks];
-//   per group, 8 words: [batch, longest round's steps, round 0 .. 3 word
-//     offsets within the stream (~0u: none), 0, 0].
+//   per group, kWideGroupWords words: [batch, longest round's steps,
+//     round 0 .. 3 word offsets within the stream (~0u: none),
+//     round 0 .. 3 steps, 0, 0].
 // A group is stream_block_records(k) * rounds-per-group = 16 programs, one
-// per 4-lane group of a wave.
+// per lane quad of a wave.
 constexpr int kWideTableHead = 24;
-constexpr int kWideGroupWords = 8;
+constexpr int kWideGroupWords = 12;
 constexpr int kWidePrograms = 16;
+constexpr int kWideMaxRounds = 4;
 
 // Codes of a width-block template word.
 constexpr uint32_t kTmplCopy = 0u;           // the template word itself
@@ -223,4 +225,6 @@ struct st_search_plan {
   uint64_t off_slot_width = 0;       // int64[kMaxWidthSlots] (device-written)
   // work table of the wide-bundle kernel (0: none), set by either binding
   uint64_t off_wide = 0;
+  // host binding: every bundle has a slot and every slot width is wide
+  bool all_wide = false;
 };
