@@ -1291,8 +1291,9 @@ __device__ __forceinline__ void wide_eval_group(const char* stream, const ST_CON
 // that walks the wide bundles p, p + grid / 2, ... of index order, one
 // member taking slices 0 and 2, the other 1 and 3, so the two halves of each
 // 128-byte index line are read by the same XCD at about the same time;
-// otherwise workgroup w takes bundles w, w + grid, ... with all slices.  The
-// next slice's loads are in flight while the current one is evaluated.
+// otherwise workgroup w takes bundles w, w + grid, ... with all slices.  Each
+// wave issues its share of the next slice's loads when it has evaluated the
+// current one.
 // `num_slots` / `slot_width` (device binding; nullptr when the host decided
 // to launch) let the kernel return at once when no slot width is wide.
 template <int K>
@@ -1379,7 +1380,6 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
       const int c = tid + i * kSearchThreads;
       if (c < b * kWidePieces) tile[c] = pre[i];
     }
-    if (has_next) prefetch(nb, ns, pre);
     __syncthreads();
     char* out_lane =
         reinterpret_cast<char*>(out) + cb * 256 + cs * kWideSliceBytes + (lane & 3) * 16;
@@ -1393,6 +1393,10 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
       else
         wide_eval_group<K, false>(stream, grp, tile_lane, lane, row_bytes, out_lane);
     }
+    // The next slice's loads go out after this wave's evaluation: issued
+    // earlier, every wait for a stream record (in-order vmcnt) would also
+    // wait for them.
+    if (has_next) prefetch(nb, ns, pre);
     if (!has_next) break;
     cb = nb;
     cs = ns;
