@@ -11,11 +11,12 @@
 //                   bundle_b_offsets, plus the totals the host needs.
 //   scatter_kernel  one workgroup per bundle: zeroes a b x 32-word tile in
 //                   LDS, hashes every (doc, feature, value) term of the bundle
-//                   (one thread per value, the owning slot found by binary
-//                   search over an LDS copy of the offsets), ORs its k bits
-//                   into the tile with LDS atomics and writes the tile out with
-//                   coalesced stores.  Bundles wider than the tile OR straight
-//                   into global memory.
+//                   (one thread per value, its doc and feature from an LDS
+//                   map of the slot group), ORs its k bits into the tile with
+//                   LDS atomics and writes the tile out with coalesced stores.
+//                   Bundles of up to kBuildSliceRows rows go in four passes of
+//                   512 docs, each over a b x 8-word tile (the docs' columns);
+//                   wider ones OR straight into global memory.
 // The reference's per-doc byte signatures and 64-way transpose
 // (bloom_indexer_cuda.cu:137-251, ~N*b/8 bytes of scratch) are not needed.
 #include <hip/hip_runtime.h>
@@ -33,6 +34,8 @@ constexpr int kScanThreads = 1024;
 constexpr int kBuildThreads = 1024;
 constexpr int kBuildTileRows = 512;
 constexpr int kBuildTileWords = kBuildTileRows * 32;
+constexpr int kBuildSliceRows = kBuildTileWords / 8;  // rows of a 8-column slice tile
+constexpr int kBuildSlices = 4;                       // 512-doc passes of a sliced bundle
 constexpr int kBuildFeatureCache = 256;  // murmur_mix_x of the first feature ids, in LDS
 constexpr int kBuildValueMap = 7168;     // values of a slot group mapped to their slot in LDS
 
@@ -156,15 +159,15 @@ struct ScatterArgs {
   unsigned long long* index;
 };
 
-// Swizzled LDS word of tile (row p, column c): spreads the 64 lanes of a
-// wave, which mostly share a column, over the LDS banks.
-__device__ __forceinline__ int tile_word(uint32_t p, uint32_t c) {
-  return static_cast<int>(p * 32 + (c ^ (p & 31)));
+// Swizzled LDS word of a tile of 2^lc columns (row p, column c): spreads the
+// 64 lanes of a wave, which mostly share a column, over the LDS banks.
+__device__ __forceinline__ int tile_word(uint32_t p, uint32_t c, int lc) {
+  return static_cast<int>((p << lc) + (c ^ (p & ((1u << lc) - 1u))));
 }
 
 // Sets the term's bits either in the LDS tile or in global memory.
 template <int K>
-__device__ __forceinline__ void scatter_term(const ScatterArgs& a, bool staged,
+__device__ __forceinline__ void scatter_term(const ScatterArgs& a, int lc,
                                              unsigned long long* tile,
                                              unsigned long long* gbase,
                                              const FastMod64& fm, uint64_t mx,
@@ -176,8 +179,8 @@ __device__ __forceinline__ void scatter_term(const ScatterArgs& a, bool staged,
   build_positions<K>(mx, my, fm, found);
 #pragma unroll
   for (int j = 0; j < K; ++j) {
-    if (staged) {
-      atomicOr(tile + tile_word(found[j], col), bit);
+    if (lc >= 0) {
+      atomicOr(tile + tile_word(found[j], col, lc), bit);
     } else {
       atomicOr(gbase + static_cast<uint64_t>(found[j]) * 32 + col, bit);
     }
@@ -185,7 +188,7 @@ __device__ __forceinline__ void scatter_term(const ScatterArgs& a, bool staged,
 }
 
 // Runtime-k variant for k above the templated range (k <= 64).
-__device__ void scatter_term_generic(const ScatterArgs& a, bool staged,
+__device__ void scatter_term_generic(const ScatterArgs& a, int lc,
                                      unsigned long long* tile,
                                      unsigned long long* gbase,
                                      const FastMod64& fm, uint64_t mx,
@@ -202,8 +205,8 @@ __device__ void scatter_term_generic(const ScatterArgs& a, bool staged,
     if (!dup) found[cnt++] = p;
   }
   for (int j = 0; j < k; ++j) {
-    if (staged) {
-      atomicOr(tile + tile_word(found[j], col), bit);
+    if (lc >= 0) {
+      atomicOr(tile + tile_word(found[j], col, lc), bit);
     } else {
       atomicOr(gbase + static_cast<uint64_t>(found[j]) * 32 + col, bit);
     }
@@ -211,16 +214,16 @@ __device__ void scatter_term_generic(const ScatterArgs& a, bool staged,
 }
 
 template <int K>
-__device__ __forceinline__ void scatter_value(const ScatterArgs& a, bool staged,
+__device__ __forceinline__ void scatter_value(const ScatterArgs& a, int lc,
                                               unsigned long long* tile,
                                               unsigned long long* gbase, const FastMod64& fm,
                                               uint64_t mx, int64_t j, uint32_t col,
                                               unsigned long long bit) {
   const uint64_t my = murmur_mix_y(static_cast<uint64_t>(a.values[j]));
   if constexpr (K > 0) {
-    scatter_term<K>(a, staged, tile, gbase, fm, mx, my, col, bit);
+    scatter_term<K>(a, lc, tile, gbase, fm, mx, my, col, bit);
   } else {
-    scatter_term_generic(a, staged, tile, gbase, fm, mx, my, col, bit);
+    scatter_term_generic(a, lc, tile, gbase, fm, mx, my, col, bit);
   }
 }
 
@@ -240,46 +243,53 @@ __global__ __launch_bounds__(kBuildThreads) void scatter_kernel(ScatterArgs a) {
   const int64_t bundle = blockIdx.x;
   const int64_t start = a.bundle_b_offsets[bundle];
   const int64_t b = a.bundle_b_offsets[bundle + 1] - start;
-  const bool staged = b <= kBuildTileRows;
+  // tile columns 2^lc: the whole bundle (32), a 512-doc slice (8), or no
+  // tile (-1: bits go straight to global memory)
+  const int lc = b <= kBuildTileRows ? 5 : (b <= kBuildSliceRows ? 3 : -1);
+  const int passes = lc == 3 ? kBuildSlices : 1;
   unsigned long long* gbase = a.index + start * 32;
-  const int64_t words = b * 32;
   const int64_t F = a.num_features;
   const int64_t cached = min<int64_t>(F, kBuildFeatureCache);
 
   for (int i = tid; i < cached; i += kBuildThreads)
     mxc[i] = murmur_mix_x(static_cast<uint64_t>(static_cast<int64_t>(a.feature_ids[i])));
-  if (staged) {
-    for (int64_t w = tid; w < words; w += kBuildThreads) tile[w] = 0;
-  } else {
-    for (int64_t w = tid; w < words; w += kBuildThreads) gbase[w] = 0;
+  if (lc < 0) {
+    for (int64_t w = tid; w < b * 32; w += kBuildThreads) gbase[w] = 0;
     __threadfence();
   }
-  __syncthreads();
+  const FastMod64 fm = make_fastmod(static_cast<uint64_t>(b > 0 ? b : 1));
+  const int64_t doc0 = bundle * kDocsPerBundle;
+  const int64_t doc1 = min(doc0 + kDocsPerBundle, a.num_docs);
+  const int64_t* offs = a.offsets + doc0 * F;
+  const bool mappable = F < (1 << 21);  // doc (11 bits) and feature share a u32
+  auto mx_of = [&](int64_t f) -> uint64_t {
+    return f < cached
+               ? mxc[f]
+               : murmur_mix_x(static_cast<uint64_t>(static_cast<int64_t>(a.feature_ids[f])));
+  };
+  // Values outside [0, num_values) are never read (the host rejects offsets
+  // that would point there before launching).
+  auto clampv = [&](int64_t v) { return min<int64_t>(max<int64_t>(v, 0), a.num_values); };
 
-  if (b > 0) {
-    const FastMod64 fm = make_fastmod(static_cast<uint64_t>(b));
-    const int64_t doc0 = bundle * kDocsPerBundle;
-    const int64_t doc1 = min(doc0 + kDocsPerBundle, a.num_docs);
-    const int64_t nslots = (doc1 - doc0) * F;
-    const int64_t* offs = a.offsets + doc0 * F;
-    const bool mappable = F < (1 << 21);  // doc (11 bits) and feature share a u32
-    auto mx_of = [&](int64_t f) -> uint64_t {
-      return f < cached
-                 ? mxc[f]
-                 : murmur_mix_x(static_cast<uint64_t>(static_cast<int64_t>(a.feature_ids[f])));
-    };
-    // Values outside [0, num_values) are never read (the host rejects offsets
-    // that would point there before launching).
-    auto clampv = [&](int64_t v) { return min<int64_t>(max<int64_t>(v, 0), a.num_values); };
-    for (int64_t g = 0; g < nslots; g += kBuildThreads) {
+  for (int pass = 0; pass < passes; ++pass) {
+    // this pass's docs [dlo, dhi) (bundle-relative) and first tile column
+    const int64_t dlo = lc == 3 ? pass * (kDocsPerBundle / kBuildSlices) : 0;
+    const int64_t dhi = lc == 3 ? min<int64_t>(dlo + kDocsPerBundle / kBuildSlices, doc1 - doc0)
+                                : doc1 - doc0;
+    const uint32_t c0 = static_cast<uint32_t>(dlo >> 6);
+    const int64_t tw = lc < 0 ? 0 : (b << lc);
+    for (int64_t w = tid; w < tw; w += kBuildThreads) tile[w] = 0;
+    __syncthreads();
+    const int64_t slot_lo = dlo * F, slot_hi = max<int64_t>(dhi, dlo) * F;
+    for (int64_t g = slot_lo; b > 0 && g < slot_hi; g += kBuildThreads) {
       const int64_t rel = g + tid;
-      const bool has_slot = rel < nslots;
+      const bool has_slot = rel < slot_hi;
       const int64_t v0 = has_slot ? clampv(offs[rel]) : 0;
       const int64_t v1 = has_slot ? clampv(offs[rel + 1]) : 0;
       const int64_t d = has_slot ? rel / F : 0;
       const int64_t f = has_slot ? rel - d * F : 0;
       const int64_t gv0 = clampv(offs[g]);
-      const int64_t gv1 = clampv(offs[min<int64_t>(g + kBuildThreads, nslots)]);
+      const int64_t gv1 = clampv(offs[min<int64_t>(g + kBuildThreads, slot_hi)]);
       if (mappable && gv1 - gv0 <= kBuildValueMap) {  // uniform across the workgroup
         __syncthreads();  // previous group's readers are done with vmap
         for (int64_t j = v0; j < v1; ++j)
@@ -288,23 +298,26 @@ __global__ __launch_bounds__(kBuildThreads) void scatter_kernel(ScatterArgs a) {
         for (int64_t j = gv0 + tid; j < gv1; j += kBuildThreads) {
           const uint32_t m = vmap[j - gv0];
           const uint32_t dd = m & 2047u;
-          scatter_value<K>(a, staged, tile, gbase, fm, mx_of(m >> 11), j, dd >> 6,
+          scatter_value<K>(a, lc, tile, gbase, fm, mx_of(m >> 11), j, (dd >> 6) - c0,
                            1ull << (63 - (dd & 63)));
         }
       } else if (v0 < v1) {
         const uint64_t mx = mx_of(f);
         for (int64_t j = v0; j < v1; ++j)
-          scatter_value<K>(a, staged, tile, gbase, fm, mx, j, static_cast<uint32_t>(d >> 6),
+          scatter_value<K>(a, lc, tile, gbase, fm, mx, j, static_cast<uint32_t>(d >> 6) - c0,
                            1ull << (63 - (d & 63)));
       }
     }
-  }
-  __syncthreads();
-  if (staged) {
-    for (int64_t w = tid; w < words; w += kBuildThreads) {
-      const uint32_t p = static_cast<uint32_t>(w >> 5);
-      const uint32_t c = static_cast<uint32_t>(w & 31);
-      __builtin_nontemporal_store(tile[tile_word(p, c)], gbase + w);
+    __syncthreads();
+    if (lc >= 0) {
+      const uint32_t cmask = (1u << lc) - 1u;
+      for (int64_t w = tid; w < tw; w += kBuildThreads) {
+        const uint32_t p = static_cast<uint32_t>(w >> lc);
+        const uint32_t c = static_cast<uint32_t>(w) & cmask;
+        __builtin_nontemporal_store(tile[tile_word(p, c, lc)],
+                                    gbase + static_cast<int64_t>(p) * 32 + c0 + c);
+      }
+      if (pass + 1 < passes) __syncthreads();  // the stores have read the tile
     }
   }
 }
