@@ -262,11 +262,14 @@ struct Dnf {
   }
 };
 
-// Conjunction of two DNFs by distribution; false when it exceeds the budget.
+// Conjunction of two DNFs by distribution, built in `out` (which must be
+// neither operand); false when it exceeds the budget.
 bool dnf_and(const Dnf& a, const Dnf& b, Dnf& out) {
   if (a.is_true) { out = b; return true; }
   if (b.is_true) { out = a; return true; }
-  Dnf r;
+  Dnf& r = out;
+  r.is_true = false;
+  r.nlits = r.ngroups = 0;
   Lit g[2 * kFlatMaxLiterals];
   for (int ia = 0; ia < a.ngroups; ++ia) {
     for (int ib = 0; ib < b.ngroups; ++ib) {
@@ -289,7 +292,6 @@ bool dnf_and(const Dnf& a, const Dnf& b, Dnf& out) {
       if (!r.push(g, n)) return false;
     }
   }
-  out = r;
   return true;
 }
 
@@ -310,26 +312,31 @@ bool to_dnf(const Tree& t, int id, bool negated, int depth, Dnf& out) {
       return to_dnf(t, t.kid(id, 0), !negated, depth + 1, out);
     case NodeKind::kAnd:
     case NodeKind::kOr: {
+      // accumulated in `out`; conjunctions alternate between `out` and a
+      // second buffer (no copies of the running DNF)
       const bool conj = (n.kind == NodeKind::kAnd) != negated;
-      Dnf acc(conj);
+      out.is_true = conj;
+      out.nlits = out.ngroups = 0;
+      Dnf d, other;
+      Dnf* acc = &out;
+      Dnf* spare = &other;
       for (int j = 0; j < n.kn; ++j) {
-        Dnf d;
         if (!to_dnf(t, t.kid(id, j), negated, depth + 1, d)) return false;
         if (conj) {
-          Dnf next;
-          if (!dnf_and(acc, d, next)) return false;
-          acc = next;
+          if (!dnf_and(*acc, d, *spare)) return false;
+          std::swap(acc, spare);
         } else {
-          if (acc.is_true) continue;
+          if (acc->is_true) continue;
           if (d.is_true) {
-            acc = Dnf(true);
+            acc->is_true = true;
+            acc->nlits = acc->ngroups = 0;
             continue;
           }
           for (int g = 0; g < d.ngroups; ++g)
-            if (!acc.push(d.lits + d.gbegin(g), d.gend[g] - d.gbegin(g))) return false;
+            if (!acc->push(d.lits + d.gbegin(g), d.gend[g] - d.gbegin(g))) return false;
         }
       }
-      out = acc;
+      if (acc != &out) out = *acc;
       return true;
     }
   }
