@@ -105,12 +105,29 @@ __device__ __forceinline__ void bundle_extent(const SearchArgs& a, int64_t bnd,
   if (b < 0) b = 0;
 }
 
-// Where a bundle sits and which width block evaluates it.
+// Where a bundle sits and which width block evaluates it; which share of
+// its programs a visit evaluates (part of parts: rounds and programs whose
+// index is part mod parts).  bundle < 0: no bundle.
 struct BundleMeta {
   int64_t bundle;
   int64_t start;  // first row
   int64_t b;      // rows
   uint32_t slot;  // width slot (kNoWidthSlot: none)
+  uint32_t part, parts;
+};
+
+// The bundles of the grid's last, partial round are split among up to this
+// many workgroups each, by program.
+constexpr int kTailParts = 4;
+
+// Cycles a program or round counter through the parts of a split visit.
+struct PartFilter {
+  uint32_t part, parts, at;
+  __device__ __forceinline__ bool take() {
+    const bool mine = at == part;
+    at = at + 1 == parts ? 0u : at + 1;
+    return mine;
+  }
 };
 
 // Issues this thread's share of the loads of the rows [start, start + b)
@@ -692,13 +709,18 @@ __device__ __forceinline__ void store_quad_bool(const SearchArgs& a, int lane, i
 template <int K, bool MASKS, int kOut>
 __device__ __forceinline__ void eval_quads(const SearchArgs& a, const u32x4* tile,
                                            const uint32_t* sw, uint32_t w_begin,
-                                           uint32_t w_end, int64_t bundle, int lane) {
+                                           uint32_t w_end, int64_t bundle, int lane,
+                                           PartFilter pf) {
   using S = QuadShape<K>;
   const int g = lane >> 4;
   const char* tb = reinterpret_cast<const char*>(tile) + (lane & 15) * 16;
   for (uint32_t w = w_begin; w < w_end;) {
     const uint32_t* hdr = sw + w;
     const uint32_t T = uniform(hdr[0]);
+    if (!pf.take()) {  // another workgroup's share of a split bundle
+      w += kRoundHeaderWords + T * S::NB * S::RW;
+      continue;
+    }
 #pragma unroll
     for (int qd = 0; qd < S::NQ; ++qd) {
       const uint32_t info = hdr[kRoundSlotInfo + qd * 4 + g];
@@ -744,13 +766,17 @@ __device__ __forceinline__ void eval_quads(const SearchArgs& a, const u32x4* til
 template <int K, bool STAGED, bool MASKS, int kOut>
 __device__ __forceinline__ void eval_rounds(const SearchArgs& a, const RowSource& rs,
                                             const ST_CONST uint32_t* stream, uint32_t w_begin,
-                                            uint32_t w_end, int64_t bundle) {
+                                            uint32_t w_end, int64_t bundle, PartFilter pf) {
   constexpr int RW = ((K + 1 + 3) / 4) * 4;
   constexpr int NB = 32 / RW;  // slots per round
   const OutCursor oc = out_cursor<kOut>(a, rs.lane, bundle);
   for (uint32_t w = w_begin; w < w_end;) {
     const ST_CONST uint32_t* hdr = stream + w;
     const uint32_t T = hdr[0];
+    if (!pf.take()) {  // another workgroup's share of a split bundle
+      w += kRoundHeaderWords + T * NB * RW;
+      continue;
+    }
     uint32_t info[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) info[i] = hdr[kRoundSlotInfo + i];
@@ -805,7 +831,7 @@ __device__ __forceinline__ void eval_rounds(const SearchArgs& a, const RowSource
 template <int K, int KP, bool STAGED, bool BOUND, int G, int kOut, bool LITE = false>
 __device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSource& rs,
                                              uint32_t s_begin, uint32_t s_end,
-                                             int64_t bundle, uint32_t slot) {
+                                             int64_t bundle, uint32_t slot, PartFilter pf) {
   const int lane = rs.lane;
   const OutCursor oc = out_cursor<kOut>(a, lane, bundle);
   auto store = [&](uint32_t row, uint32_t acc) {
@@ -818,6 +844,10 @@ __device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSourc
       const ST_CONST uint32_t* prog = progs + a.bound_start[s];
       const uint32_t hdr = prog[0];
       const uint32_t T = hdr & 0xFFFFu;
+      if (!pf.take()) {  // another workgroup's share of a split bundle
+        s += (!LITE && (hdr & kPairedWithNext)) ? 2 : 1;
+        continue;
+      }
       if (!LITE && (hdr & kPairedWithNext)) {
         const ST_CONST uint32_t* prog_b = progs + a.bound_start[s + 1];
         const uint32_t hdr_b = prog_b[0];
@@ -853,6 +883,7 @@ __device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSourc
   const ST_CONST uint32_t* progs = a.insns;
   const ST_CONST uint32_t* starts = a.insn_start;
   for (uint32_t s = s_begin; s < s_end; ++s) {
+    if (!pf.take()) continue;  // another workgroup's share of a split bundle
     const ST_CONST uint32_t* prog = progs + starts[s];
     const uint32_t hdr = prog[0];
     const uint32_t row = prog[1];
@@ -941,9 +972,28 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     m.bundle = a.bundle_order ? static_cast<int64_t>(a.bundle_order[i]) : i;
     bundle_extent(a, m.bundle, m.start, m.b);
     m.slot = a.bundle_slot ? a.bundle_slot[m.bundle] : kNoWidthSlot;
+    m.part = 0;
+    m.parts = 1;
     return m;
   };
   const int64_t grid = gridDim.x;
+  // Visit v of this workgroup: order index blockIdx.x + v * grid while every
+  // workgroup has one; the `tail` bundles of the last, partial round are
+  // split `parts` ways by program among the first tail * parts workgroups,
+  // so that round takes a fraction of a bundle's time instead of a whole one.
+  const int64_t full = a.num_bundles / grid;
+  const int64_t tail = a.num_bundles - full * grid;
+  const int64_t parts = tail > 0 ? min<int64_t>(grid / tail, kTailParts) : 1;
+  auto visit = [&](int64_t v) -> BundleMeta {
+    if (v < full) return meta_at(blockIdx.x + v * grid);
+    if (v == full && static_cast<int64_t>(blockIdx.x) < tail * parts) {
+      BundleMeta m = meta_at(full * grid + blockIdx.x % tail);
+      m.part = static_cast<uint32_t>(blockIdx.x / tail);
+      m.parts = static_cast<uint32_t>(parts);
+      return m;
+    }
+    return BundleMeta{-1, 0, 0, kNoWidthSlot, 0, 1};
+  };
   // Quad-lane evaluation of the literal stream (eval_quads): the batch's
   // stream fits the LDS area after the tile and a step holds whole quads.
   const bool quad = kQuad && a.stream_words != 0 && a.stream_words <= kQuadStreamMaxWords &&
@@ -964,13 +1014,11 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
   };
   u32x4 pre[kPrefetch];
   u32x4 spre[kQuad ? kStreamPrefetch : 1];
-  BundleMeta cur{0, 0, 0, kNoWidthSlot}, nxt{0, 0, 0, kNoWidthSlot};
-  if (blockIdx.x < a.num_bundles) {
-    cur = meta_at(blockIdx.x);
+  BundleMeta cur = visit(0), nxt = visit(1);
+  if (cur.bundle >= 0) {
     prefetch_tile(a, cur.start, cur.b, pre);
     if (quad_bundle(cur)) prefetch_stream(cur, spre);
   }
-  if (blockIdx.x + grid < a.num_bundles) nxt = meta_at(blockIdx.x + grid);
 
   int64_t prev_b = -1;  // width whose term positions are in pos
   const uint32_t s_begin = uniform(a.wave_off[wave]);
@@ -984,8 +1032,9 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
   const uint32_t* index32 = reinterpret_cast<const uint32_t*>(a.index);
 
   uint32_t warm = 0;  // scalar-cache warming loads of the next stream (see below)
-  for (int64_t step = blockIdx.x; step < a.num_bundles; step += grid) {
+  for (int64_t v = 0; cur.bundle >= 0; ++v) {
     const int64_t bundle = cur.bundle;
+    const PartFilter pf{cur.part, cur.parts, 0u};
     const int64_t start = cur.start, b = cur.b;
     const uint32_t slot = cur.slot;
     const bool staged = b <= kSearchTileRows;
@@ -1018,7 +1067,7 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     // The next bundle's loads go out as soon as this thread's registers are
     // in LDS, before the barrier, so the HBM queue is not left empty while the
     // workgroup finishes storing the tile.
-    const bool has_next = step + grid < a.num_bundles;
+    const bool has_next = nxt.bundle >= 0;
     if (has_next) {
       prefetch_tile(a, nxt.start, nxt.b, pre);
       if (quad_bundle(nxt)) prefetch_stream(nxt, spre);
@@ -1051,8 +1100,7 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     if (!skip) __syncthreads();
     asm volatile("" ::"s"(warm));  // the warming loads are complete by now
 
-    BundleMeta after{0, 0, 0, kNoWidthSlot};
-    if (step + 2 * grid < a.num_bundles) after = meta_at(step + 2 * grid);
+    const BundleMeta after = visit(v + 2);
 
     // Evaluate this wave's queries on the bundle.
     RowSource rs;
@@ -1071,20 +1119,20 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
       // other bundles' programs from the width block one by one.
       if (quad_here) {
         if (a.stream_masks)
-          eval_quads<K, true, kOut>(a, tile, pos, r_begin, r_end, bundle, lane);
+          eval_quads<K, true, kOut>(a, tile, pos, r_begin, r_end, bundle, lane, pf);
         else
-          eval_quads<K, false, kOut>(a, tile, pos, r_begin, r_end, bundle, lane);
-        eval_queries<K, KP, true, true, GL, kOut, true>(a, rs, s_rest, s_end, bundle, slot);
+          eval_quads<K, false, kOut>(a, tile, pos, r_begin, r_end, bundle, lane, pf);
+        eval_queries<K, KP, true, true, GL, kOut, true>(a, rs, s_rest, s_end, bundle, slot, pf);
       } else if (slot != kNoWidthSlot) {
         if (staged)
-          eval_queries<K, KP, true, true, GL, kOut, true>(a, rs, s_begin, s_end, bundle, slot);
+          eval_queries<K, KP, true, true, GL, kOut, true>(a, rs, s_begin, s_end, bundle, slot, pf);
         else
           eval_queries<K, KP, false, true, GL, kOut, true>(a, rs, wide_here ? s_rest : s_begin,
-                                                           s_end, bundle, slot);
+                                                           s_end, bundle, slot, pf);
       } else if (staged) {
-        eval_queries<K, KP, true, false, GL, kOut, true>(a, rs, s_begin, s_end, bundle, slot);
+        eval_queries<K, KP, true, false, GL, kOut, true>(a, rs, s_begin, s_end, bundle, slot, pf);
       } else {
-        eval_queries<K, KP, false, false, GL, kOut, true>(a, rs, s_begin, s_end, bundle, slot);
+        eval_queries<K, KP, false, false, GL, kOut, true>(a, rs, s_begin, s_end, bundle, slot, pf);
       }
     } else if (slot != kNoWidthSlot) {
       const ST_CONST uint32_t* stream =
@@ -1092,24 +1140,24 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
       if (staged) {
         if (streamed) {
           if (a.stream_masks)
-            eval_rounds<K, true, true, kOut>(a, rs, stream, r_begin, r_end, bundle);
+            eval_rounds<K, true, true, kOut>(a, rs, stream, r_begin, r_end, bundle, pf);
           else
-            eval_rounds<K, true, false, kOut>(a, rs, stream, r_begin, r_end, bundle);
+            eval_rounds<K, true, false, kOut>(a, rs, stream, r_begin, r_end, bundle, pf);
         }
-        eval_queries<K, KP, true, true, G, kOut>(a, rs, s_rest, s_end, bundle, slot);
+        eval_queries<K, KP, true, true, G, kOut>(a, rs, s_rest, s_end, bundle, slot, pf);
       } else {
         if (streamed && !wide_here) {
           if (a.stream_masks)
-            eval_rounds<K, false, true, kOut>(a, rs, stream, r_begin, r_end, bundle);
+            eval_rounds<K, false, true, kOut>(a, rs, stream, r_begin, r_end, bundle, pf);
           else
-            eval_rounds<K, false, false, kOut>(a, rs, stream, r_begin, r_end, bundle);
+            eval_rounds<K, false, false, kOut>(a, rs, stream, r_begin, r_end, bundle, pf);
         }
-        eval_queries<K, KP, false, true, G, kOut>(a, rs, s_rest, s_end, bundle, slot);
+        eval_queries<K, KP, false, true, G, kOut>(a, rs, s_rest, s_end, bundle, slot, pf);
       }
     } else if (staged) {
-      eval_queries<K, KP, true, false, G, kOut>(a, rs, s_begin, s_end, bundle, slot);
+      eval_queries<K, KP, true, false, G, kOut>(a, rs, s_begin, s_end, bundle, slot, pf);
     } else {
-      eval_queries<K, KP, false, false, G, kOut>(a, rs, s_begin, s_end, bundle, slot);
+      eval_queries<K, KP, false, false, G, kOut>(a, rs, s_begin, s_end, bundle, slot, pf);
     }
     // The next bundle's first round header and records (this wave's part of
     // its width block) are read into the scalar cache now; the loads complete
