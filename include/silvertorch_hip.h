@@ -337,6 +337,39 @@ int st_filtered_topk(const int64_t* packed, int64_t num_queries,
                      int64_t dim, int64_t topk, void* workspace,
                      int64_t* out_ids, float* out_scores, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Clustered nearest-neighbour scoring, the consumer step after the search.
+ * Replaces fused_kmean_ann (fused_kmean_ann.cpp:85-227; CUDA op
+ * fused_kmean_ann_cuda.cu:1797-1926).  For each query row b, over the probes
+ * p in order, the docs cluster_offsets[cluster_ids[b][p]] + i,
+ * 0 <= i < cluster_length[b][p] (int64 arrays; cluster_ids / cluster_length
+ * [batch, probes]) that pass the row's filter take consecutive output slots
+ * until max_per_row are filled; the rest is padding (score dtype minimum,
+ * invalid_index_value).  Filter (optional): int64 filter_mask
+ * [*, filter_cols], row filter_index[b] (or b when filter_index is null);
+ * doc d passes when bit 63 - d % 64 of word d / 64 is set, or when that word
+ * is past filter_cols.  embeddings [total_docs, dim] and queries [batch, dim]
+ * share emb_dtype: 0 float32, 1 float16, 2 bfloat16, 3 int8.  Scores
+ * (st_kmean_ann_score_dtype: the embedding dtype; for int8, int32 (code 4),
+ * or float16 when divisor_for_int8 != -1 or per_embedding_scale (float16
+ * [total_docs]) is given) are float64 dot products converted to the score
+ * dtype (int8: exact int32 sums, divided as float when scaled); indices are
+ * int32 doc ids.  1 <= dim <= 1280.  A cluster id outside
+ * [0, num_offsets) or a negative length selects nothing.
+ * ------------------------------------------------------------------------- */
+int st_kmean_ann_score_dtype(int emb_dtype, int64_t divisor_for_int8,
+                             int has_per_embedding_scale);
+int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_offsets,
+                       const int64_t* cluster_ids, const int64_t* cluster_length,
+                       int64_t batch, int64_t probes, const void* embeddings,
+                       int64_t total_docs, int64_t dim, int emb_dtype,
+                       const void* queries, int64_t max_per_row,
+                       const int64_t* filter_mask, int64_t filter_cols,
+                       const int64_t* filter_index,
+                       const uint16_t* per_embedding_scale,
+                       int64_t divisor_for_int8, int64_t invalid_index_value,
+                       void* scores, int32_t* indices, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

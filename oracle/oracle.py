@@ -212,3 +212,89 @@ def filtered_topk(emb: np.ndarray, qv: np.ndarray, packed: np.ndarray, topk: int
     if rc != 0:
         raise MemoryError("oracle top-k allocation failed")
     return ids, scores
+
+
+def bf16_round(f32: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns (uint16), round to nearest even, as
+    c10::BFloat16's conversion does (finite inputs)."""
+    u = np.ascontiguousarray(f32, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def fused_kmean_ann(cluster_offsets, cluster_ids, cluster_length, embeddings, queries,
+                    max_size: int, filter_mask=None, invalid_index: int = -1, divisor: int = -1,
+                    filter_index=None, scale=None, bf16: bool = False):
+    """Restates the reference CPU op fused_kmean_ann (fused_kmean_ann.cpp:85-227):
+    per query row, over the probes in order, the docs of each selected cluster
+    (cluster_offsets[cid] + i, i < cluster_length) that pass the row's filter
+    take consecutive slots until the row width (max_size rounded up to 32,
+    :104-107) is full; the rest is padding.  Float scores: the float64 dot
+    product summed in dimension order (:45-55), then converted to the score
+    dtype; int8: the exact integer sum, divided as float32 by divisor_for_int8
+    or the per-embedding float16 scale and stored as float16 when either is
+    given (:30-41, :196-206).  One deliberate difference: the filter bit of doc
+    d is bit 63 - d % 64 of word d / 64 (the search output's layout and the
+    reference CUDA op's reading), where the CPU op reads bit d % 64.  bfloat16
+    embeddings arrive as uint16 bit patterns with bf16=True; their padding is
+    0xFF7F (the CUDA op's, simple_index_mm.cuh:123; the CPU op raises).
+    Returns (scores, indices int32), both [B, width]."""
+    cluster_offsets = np.asarray(cluster_offsets, np.int64)
+    cluster_ids = np.asarray(cluster_ids, np.int64)
+    cluster_length = np.asarray(cluster_length, np.int64)
+    B, P = cluster_ids.shape
+    width = (max_size + 31) // 32 * 32
+    is_i8 = embeddings.dtype == np.int8
+    if bf16:
+        e64 = bf16_to_f32(embeddings).astype(np.float64)
+        q64 = bf16_to_f32(queries).astype(np.float64)
+    elif not is_i8:
+        e64 = embeddings.astype(np.float64)
+        q64 = queries.astype(np.float64)
+    if is_i8:
+        half = divisor != -1 or scale is not None
+        scores = np.full((B, width), np.float16(-65504.0) if half else np.iinfo(np.int32).min,
+                         dtype=np.float16 if half else np.int32)
+    elif bf16:
+        scores = np.full((B, width), 0xFF7F, dtype=np.uint16)
+    elif embeddings.dtype == np.float16:
+        scores = np.full((B, width), -65504.0, dtype=np.float16)
+    else:
+        scores = np.full((B, width), -np.finfo(np.float32).max, dtype=np.float32)
+    indices = np.full((B, width), invalid_index, dtype=np.int32)
+    for b in range(B):
+        write = 0
+        frow = int(filter_index[b]) if filter_index is not None else b
+        for p in range(P):
+            cid, clen = int(cluster_ids[b, p]), int(cluster_length[b, p])
+            start = int(cluster_offsets[cid])
+            for i in range(clen):
+                if write >= width:
+                    break
+                doc = start + i
+                if filter_mask is not None:
+                    word = doc >> 6
+                    if word < filter_mask.shape[1]:
+                        w = int(np.asarray(filter_mask[frow, word]).view(np.uint64))
+                        if not (w >> (63 - (doc & 63))) & 1:
+                            continue
+                if is_i8:
+                    raw = int(np.dot(embeddings[doc].astype(np.int64), queries[b].astype(np.int64)))
+                    if scale is not None:
+                        scores[b, write] = np.float16(np.float32(raw) / np.float32(scale[doc]))
+                    elif divisor != -1:
+                        scores[b, write] = np.float16(np.float32(raw) / np.float32(divisor))
+                    else:
+                        scores[b, write] = raw
+                else:
+                    s = float(np.cumsum(e64[doc] * q64[b])[-1])  # sequential float64 sum
+                    if bf16:
+                        scores[b, write] = bf16_round(np.array([s], np.float32))[0]
+                    else:
+                        scores[b, write] = scores.dtype.type(np.float32(s))
+                indices[b, write] = doc
+                write += 1
+    return scores, indices

@@ -48,6 +48,7 @@ LIB_SOURCES = [
     "bloom_compact.hip",
     "bloom_partial.hip",
     "filtered_topk.hip",
+    "kmean_ann.hip",
     "search_plan.cpp",
     "expression_parser.cpp",
 ]

@@ -1,0 +1,328 @@
+// Clustered nearest-neighbour scoring: the consumer step after the bloom
+// search.  Replaces fused_kmean_ann (fused_kmean_ann.cpp:85-227,
+// fused_kmean_ann_cuda.cu) behind the same operator.
+//
+// Per query row b the candidate docs are the selected clusters' doc ranges
+// [cluster_offsets[cluster_ids[b][p]], + cluster_length[b][p]) in probe
+// order; docs failing the row's filter mask are skipped, the rest take
+// consecutive output slots (as the reference CPU op lays them out) until the
+// row is full; the remaining slots hold the padding values.  Filter bit of
+// doc d: bit 63 - d % 64 of word d / 64 (the bloom search's packed mask, read
+// as the reference CUDA op reads it); docs past the mask's words pass.
+//
+// Scores are accumulated per doc in float64, dimension by dimension, with no
+// fused multiply-add (as fused_kmean_ann.cpp:45-55 does), then converted to
+// the score dtype, so every float score equals the reference CPU op's bit
+// for bit; int8 dot products are exact int32 sums.
+//
+// One 256-thread workgroup per query row: the query is staged in LDS as
+// float64; docs go 256 at a time, one per thread (16-byte loads of the
+// embedding row); a workgroup-wide exclusive scan of the pass flags gives
+// the output slots.  Memory-bound on the embedding rows read.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "st_errors.hpp"
+
+namespace st {
+namespace {
+
+constexpr int kKmThreads = 256;
+constexpr int kKmWaves = kKmThreads / 64;
+constexpr int kKmMaxDim = 1280;
+
+// Embedding / score dtype codes of the C ABI (include/silvertorch_hip.h).
+enum KmDtype : int { kKmF32 = 0, kKmF16 = 1, kKmBF16 = 2, kKmI8 = 3, kKmI32 = 4 };
+
+
+__device__ __forceinline__ float half_to_float(uint16_t h) {
+  return __half2float(__ushort_as_half(h));
+}
+__device__ __forceinline__ uint16_t float_to_half(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+__device__ __forceinline__ float bf16_to_float(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+// Round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t float_to_bf16(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  return static_cast<uint16_t>((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+// Element d of an embedding row as float (exactly representable) or int.
+template <int DT>
+__device__ __forceinline__ float elem_f(const void* row, int d) {
+  if constexpr (DT == kKmF32) return static_cast<const float*>(row)[d];
+  if constexpr (DT == kKmF16) return half_to_float(static_cast<const uint16_t*>(row)[d]);
+  if constexpr (DT == kKmBF16) return bf16_to_float(static_cast<const uint16_t*>(row)[d]);
+  return 0.f;
+}
+
+// Float64 dot product of the doc row with the staged query, sequential over
+// d, each product and sum rounded on its own (no contraction).
+template <int DT>
+__device__ double dot_f64(const void* row, const double* q, int dim) {
+#pragma clang fp contract(off)
+  double acc = 0.0;
+  if ((reinterpret_cast<uintptr_t>(row) & 15u) != 0) {  // no 16-byte loads
+    for (int d = 0; d < dim; ++d) acc = acc + static_cast<double>(elem_f<DT>(row, d)) * q[d];
+    return acc;
+  }
+  if constexpr (DT == kKmF32) {
+    const float4* r4 = static_cast<const float4*>(row);
+    int d = 0;
+    for (; d + 4 <= dim; d += 4) {
+      const float4 v = r4[d / 4];
+      acc = acc + static_cast<double>(v.x) * q[d];
+      acc = acc + static_cast<double>(v.y) * q[d + 1];
+      acc = acc + static_cast<double>(v.z) * q[d + 2];
+      acc = acc + static_cast<double>(v.w) * q[d + 3];
+    }
+    for (; d < dim; ++d) acc = acc + static_cast<double>(elem_f<DT>(row, d)) * q[d];
+  } else {
+    const uint4* r8 = static_cast<const uint4*>(row);
+    int d = 0;
+    for (; d + 8 <= dim; d += 8) {
+      const uint4 v = r8[d / 8];
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint16_t lo = static_cast<uint16_t>(w[j] & 0xFFFFu);
+        const uint16_t hi = static_cast<uint16_t>(w[j] >> 16);
+        const float flo = DT == kKmF16 ? half_to_float(lo) : bf16_to_float(lo);
+        const float fhi = DT == kKmF16 ? half_to_float(hi) : bf16_to_float(hi);
+        acc = acc + static_cast<double>(flo) * q[d + 2 * j];
+        acc = acc + static_cast<double>(fhi) * q[d + 2 * j + 1];
+      }
+    }
+    for (; d < dim; ++d) acc = acc + static_cast<double>(elem_f<DT>(row, d)) * q[d];
+  }
+  return acc;
+}
+
+__device__ int32_t dot_i8(const int8_t* row, const int8_t* q, int dim) {
+  int32_t acc = 0;
+  int d = 0;
+  if ((reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
+    for (; d + 16 <= dim; d += 16) {
+      const uint4 v = *reinterpret_cast<const uint4*>(row + d);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        acc += static_cast<int32_t>(static_cast<int8_t>(w[j / 4] >> (8 * (j % 4)))) *
+               static_cast<int32_t>(q[d + j]);
+    }
+  }
+  for (; d < dim; ++d) acc += static_cast<int32_t>(row[d]) * static_cast<int32_t>(q[d]);
+  return acc;
+}
+
+struct KmArgs {
+  const int64_t* cluster_offsets;
+  int64_t num_offsets;
+  const int64_t* cluster_ids;
+  const int64_t* cluster_length;
+  int64_t probes;
+  const void* embeddings;
+  int64_t total_docs;
+  int dim;
+  const void* queries;
+  int64_t max_per_row;
+  const int64_t* filter_mask;
+  int64_t filter_cols;
+  const int64_t* filter_index;
+  const uint16_t* scale;  // int8 only: per-doc float16 divisor
+  int64_t divisor;        // int8 only: -1 = none
+  int64_t invalid_index;
+  void* scores;
+  int32_t* indices;
+};
+
+// Workgroup-wide exclusive scan of 0/1 flags; *total receives the sum.
+__device__ __forceinline__ uint32_t block_scan_flags(bool f, uint32_t* wave_sums, uint32_t* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t m = __ballot(f);
+  const uint32_t below =
+      __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+  if (lane == 0) wave_sums[wave] = static_cast<uint32_t>(__popcll(m));
+  __syncthreads();
+  uint32_t before = 0, sum = 0;
+#pragma unroll
+  for (int w = 0; w < kKmWaves; ++w) {
+    const uint32_t s = wave_sums[w];
+    before += w < wave ? s : 0u;
+    sum += s;
+  }
+  __syncthreads();  // wave_sums is reused by the next call
+  *total = sum;
+  return before + below;
+}
+
+template <int DT, int ST>
+__device__ __forceinline__ void put_score(void* scores, int64_t at, double f64, int32_t i32,
+                                          float f32_for_half) {
+  if constexpr (ST == kKmF32) static_cast<float*>(scores)[at] = static_cast<float>(f64);
+  if constexpr (ST == kKmF16) {
+    const float f = DT == kKmI8 ? f32_for_half : static_cast<float>(f64);
+    static_cast<uint16_t*>(scores)[at] = float_to_half(f);
+  }
+  if constexpr (ST == kKmBF16)
+    static_cast<uint16_t*>(scores)[at] = float_to_bf16(static_cast<float>(f64));
+  if constexpr (ST == kKmI32) static_cast<int32_t*>(scores)[at] = i32;
+}
+
+// DT: embedding dtype; ST: score dtype.
+template <int DT, int ST>
+__global__ __launch_bounds__(kKmThreads) void kmean_ann_kernel(KmArgs a) {
+  __shared__ double qd[kKmMaxDim];
+  __shared__ int8_t qi[kKmMaxDim];
+  __shared__ uint32_t wave_sums[kKmWaves];
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int dim = a.dim;
+  if constexpr (DT == kKmI8) {
+    const int8_t* q = static_cast<const int8_t*>(a.queries) + b * dim;
+    for (int d = tid; d < dim; d += kKmThreads) qi[d] = q[d];
+  } else {
+    const size_t es = DT == kKmF32 ? 4 : 2;
+    const char* q = static_cast<const char*>(a.queries) + static_cast<size_t>(b) * dim * es;
+    for (int d = tid; d < dim; d += kKmThreads) qd[d] = static_cast<double>(elem_f<DT>(q, d));
+  }
+  __syncthreads();
+
+  const int64_t* mask = nullptr;
+  if (a.filter_mask != nullptr) {
+    const int64_t frow = a.filter_index != nullptr ? a.filter_index[b] : b;
+    mask = a.filter_mask + frow * a.filter_cols;
+  }
+  const size_t row_bytes = static_cast<size_t>(dim) * (DT == kKmF32 ? 4 : (DT == kKmI8 ? 1 : 2));
+  const int64_t out0 = b * a.max_per_row;
+  int64_t written = 0;
+  for (int64_t p = 0; p < a.probes && written < a.max_per_row; ++p) {
+    const int64_t cid = a.cluster_ids[b * a.probes + p];
+    int64_t len = a.cluster_length[b * a.probes + p];
+    // a cluster id outside the offsets or a negative length is an empty
+    // cluster (the reference reads out of bounds there)
+    if (cid < 0 || cid >= a.num_offsets || len < 0) len = 0;
+    const int64_t start = len > 0 ? a.cluster_offsets[cid] : 0;
+    for (int64_t base = 0; base < len && written < a.max_per_row; base += kKmThreads) {
+      const int64_t i = base + tid;
+      const int64_t doc = start + i;
+      bool pass = i < len && doc >= 0 && doc < a.total_docs;
+      if (pass && mask != nullptr) {
+        const int64_t word = doc >> 6;
+        if (word < a.filter_cols)
+          pass = (static_cast<uint64_t>(mask[word]) >> (63 - (doc & 63))) & 1u;
+      }
+      uint32_t total;
+      const uint32_t slot_in = block_scan_flags(pass, wave_sums, &total);
+      const int64_t slot = written + slot_in;
+      if (pass && slot < a.max_per_row) {
+        const char* row = static_cast<const char*>(a.embeddings) + static_cast<size_t>(doc) * row_bytes;
+        double f64 = 0.0;
+        int32_t i32 = 0;
+        float f32h = 0.f;
+        if constexpr (DT == kKmI8) {
+          i32 = dot_i8(reinterpret_cast<const int8_t*>(row), qi, dim);
+          if (a.scale != nullptr)
+            f32h = static_cast<float>(i32) / half_to_float(a.scale[doc]);
+          else if (a.divisor != -1)
+            f32h = static_cast<float>(i32) / static_cast<float>(a.divisor);
+        } else {
+          f64 = dot_f64<DT>(row, qd, dim);
+        }
+        put_score<DT, ST>(a.scores, out0 + slot, f64, i32, f32h);
+        a.indices[out0 + slot] = static_cast<int32_t>(doc);
+      }
+      written += total;
+    }
+  }
+  // padding: the score dtype's most negative finite value (-FLT_MAX, -65504
+  // for float16, 0xFF7F for bfloat16 as the reference CUDA op pads,
+  // simple_index_mm.cuh:99-123) or INT32_MIN, and invalid_index
+  if (written > a.max_per_row) written = a.max_per_row;
+  for (int64_t s = written + tid; s < a.max_per_row; s += kKmThreads) {
+    if constexpr (ST == kKmF32) static_cast<float*>(a.scores)[out0 + s] = -3.402823466e38f;
+    if constexpr (ST == kKmF16) static_cast<uint16_t*>(a.scores)[out0 + s] = 0xFBFFu;
+    if constexpr (ST == kKmBF16) static_cast<uint16_t*>(a.scores)[out0 + s] = 0xFF7Fu;
+    if constexpr (ST == kKmI32) static_cast<int32_t*>(a.scores)[out0 + s] = INT32_MIN;
+    a.indices[out0 + s] = static_cast<int32_t>(a.invalid_index);
+  }
+}
+
+}  // namespace
+}  // namespace st
+
+extern "C" int st_kmean_ann_score_dtype(int emb_dtype, int64_t divisor_for_int8,
+                                        int has_per_embedding_scale) {
+  using namespace st;
+  if (emb_dtype != kKmI8) return emb_dtype;
+  return (divisor_for_int8 != -1 || has_per_embedding_scale) ? kKmF16 : kKmI32;
+}
+
+extern "C" int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_offsets,
+                                  const int64_t* cluster_ids, const int64_t* cluster_length,
+                                  int64_t batch, int64_t probes, const void* embeddings,
+                                  int64_t total_docs, int64_t dim, int emb_dtype,
+                                  const void* queries, int64_t max_per_row,
+                                  const int64_t* filter_mask, int64_t filter_cols,
+                                  const int64_t* filter_index,
+                                  const uint16_t* per_embedding_scale, int64_t divisor_for_int8,
+                                  int64_t invalid_index_value, void* scores, int32_t* indices,
+                                  void* stream) {
+  using namespace st;
+  return guarded([&] {
+    ST_CHECK(batch >= 0 && probes >= 0 && total_docs >= 0 && max_per_row >= 0 && num_offsets >= 0,
+             "negative sizes");
+    ST_CHECK(dim >= 1 && dim <= kKmMaxDim, "embedding dim must be in [1, ", kKmMaxDim, "], got ",
+             dim);
+    ST_CHECK(emb_dtype >= kKmF32 && emb_dtype <= kKmI8, "unsupported embedding dtype code ",
+             emb_dtype);
+    if (batch == 0 || max_per_row == 0) return;
+    ST_CHECK(scores != nullptr && indices != nullptr && queries != nullptr, "null device pointer");
+    ST_CHECK(probes == 0 || (cluster_ids != nullptr && cluster_length != nullptr &&
+                             cluster_offsets != nullptr),
+             "null cluster arrays");
+    ST_CHECK(filter_mask == nullptr || filter_cols >= 0, "negative filter mask width");
+    KmArgs a;
+    a.cluster_offsets = cluster_offsets;
+    a.num_offsets = num_offsets;
+    a.cluster_ids = cluster_ids;
+    a.cluster_length = cluster_length;
+    a.probes = probes;
+    a.embeddings = embeddings;
+    a.total_docs = embeddings != nullptr ? total_docs : 0;
+    a.dim = static_cast<int>(dim);
+    a.queries = queries;
+    a.max_per_row = max_per_row;
+    a.filter_mask = filter_mask;
+    a.filter_cols = filter_cols;
+    a.filter_index = filter_index;
+    a.scale = emb_dtype == kKmI8 ? per_embedding_scale : nullptr;
+    a.divisor = divisor_for_int8;
+    a.invalid_index = invalid_index_value;
+    a.scores = scores;
+    a.indices = indices;
+    const int st = st_kmean_ann_score_dtype(emb_dtype, divisor_for_int8, a.scale != nullptr);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid(static_cast<unsigned>(batch)), block(kKmThreads);
+    switch (emb_dtype) {
+      case kKmF32: hipLaunchKernelGGL((kmean_ann_kernel<kKmF32, kKmF32>), grid, block, 0, s, a); break;
+      case kKmF16: hipLaunchKernelGGL((kmean_ann_kernel<kKmF16, kKmF16>), grid, block, 0, s, a); break;
+      case kKmBF16: hipLaunchKernelGGL((kmean_ann_kernel<kKmBF16, kKmBF16>), grid, block, 0, s, a); break;
+      default:
+        if (st == kKmI32)
+          hipLaunchKernelGGL((kmean_ann_kernel<kKmI8, kKmI32>), grid, block, 0, s, a);
+        else
+          hipLaunchKernelGGL((kmean_ann_kernel<kKmI8, kKmF16>), grid, block, 0, s, a);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+      throw Error(ST_ERR_HIP, cat("fused_kmean_ann launch failed: ", hipGetErrorString(e)));
+  });
+}

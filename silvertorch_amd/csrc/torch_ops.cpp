@@ -618,6 +618,188 @@ std::tuple<Tensor, Tensor> search_topk_cpu(const Tensor& bloom_index, const Tens
   return filtered_topk_cpu(packed, emb, qv, num_docs, topk);
 }
 
+// ------------------------------------------ clustered ANN scoring (fused_kmean_ann)
+// fused_kmean_ann.cpp:85-227 (argument checks :96-102, output dtypes and
+// padding :30-41, :134-165, the row width rounded up to 32 :104-107).
+
+int km_dtype_code(at::ScalarType t) {
+  switch (t) {
+    case at::kFloat: return 0;
+    case at::kHalf: return 1;
+    case at::kBFloat16: return 2;
+    case at::kChar: return 3;
+    default:
+      TORCH_CHECK(false, "fused_kmean_ann: embeddings must be float32, float16, bfloat16 or int8, got ",
+                  t);
+  }
+  return -1;
+}
+
+at::ScalarType km_score_type(int code) {
+  switch (code) {
+    case 0: return at::kFloat;
+    case 1: return at::kHalf;
+    case 2: return at::kBFloat16;
+    default: return at::kInt;
+  }
+}
+
+std::tuple<Tensor, Tensor> kmean_gpu(const Tensor& cluster_offsets_in, const Tensor& cluster_ids_in,
+                                     const Tensor& cluster_length_in, const Tensor& embeddings_in,
+                                     const Tensor& queries_in, int64_t max_tensor_size_per_row,
+                                     const std::optional<Tensor>& filtering_bit_mask,
+                                     int64_t invalid_index_value, int64_t divisor_for_int8,
+                                     const std::optional<Tensor>& filtering_bit_index,
+                                     const std::optional<Tensor>& per_embedding_scale) {
+  TORCH_CHECK(cluster_offsets_in.dim() == 1);
+  TORCH_CHECK(cluster_ids_in.dim() == 2);
+  TORCH_CHECK(cluster_length_in.dim() == 2);
+  TORCH_CHECK(embeddings_in.dim() == 2);
+  TORCH_CHECK(queries_in.dim() == 2);
+  TORCH_CHECK(cluster_ids_in.size(0) == cluster_length_in.size(0));
+  TORCH_CHECK(cluster_ids_in.size(0) == queries_in.size(0));
+  TORCH_CHECK(cluster_ids_in.sizes() == cluster_length_in.sizes(),
+              "cluster_ids and cluster_length must have the same shape");
+  TORCH_CHECK(queries_in.size(1) == embeddings_in.size(1), "queries have dimension ",
+              queries_in.size(1), ", embeddings ", embeddings_in.size(1));
+  TORCH_CHECK(queries_in.scalar_type() == embeddings_in.scalar_type(),
+              "queries and embeddings must have the same dtype");
+  TORCH_CHECK(max_tensor_size_per_row >= 0, "max_tensor_size_per_row must be non-negative");
+  const at::Device dev = embeddings_in.device();
+  TORCH_CHECK(dev.is_cuda(), "fused_kmean_ann inputs must be GPU tensors");
+  for (const Tensor* t : {&cluster_offsets_in, &cluster_ids_in, &cluster_length_in, &queries_in})
+    TORCH_CHECK(t->device() == dev, "fused_kmean_ann inputs must be on one device");
+  c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(dev);
+  const int code = km_dtype_code(embeddings_in.scalar_type());
+  const Tensor offsets = cluster_offsets_in.to(at::kLong).contiguous();
+  const Tensor ids = cluster_ids_in.to(at::kLong).contiguous();
+  const Tensor lens = cluster_length_in.to(at::kLong).contiguous();
+  const Tensor emb = embeddings_in.contiguous(), q = queries_in.contiguous();
+  Tensor mask, findex, scale;
+  if (filtering_bit_mask) {
+    TORCH_CHECK(filtering_bit_mask->dim() == 2 && filtering_bit_mask->scalar_type() == at::kLong,
+                "filtering_bit_mask must be a 2-D int64 tensor");
+    TORCH_CHECK(filtering_bit_mask->device() == dev, "filtering_bit_mask must be on the embeddings' device");
+    mask = filtering_bit_mask->contiguous();
+  }
+  if (filtering_bit_index) {
+    TORCH_CHECK(filtering_bit_index->numel() == ids.size(0),
+                "filtering_bit_index must hold one row per query");
+    findex = filtering_bit_index->to(dev, at::kLong).contiguous();
+  }
+  const bool has_scale = per_embedding_scale.has_value() && code == 3;
+  if (has_scale) {
+    TORCH_CHECK(per_embedding_scale->numel() >= emb.size(0),
+                "per_embedding_scale must hold one value per embedding row");
+    scale = per_embedding_scale->to(dev, at::kHalf).contiguous();
+  }
+  // the reference rounds the row width up to a multiple of 32 (its warp)
+  const int64_t width = (max_tensor_size_per_row + 31) / 32 * 32;
+  const int64_t B = ids.size(0);
+  auto opts = at::TensorOptions().device(dev);
+  const int score_code = st_kmean_ann_score_dtype(code, divisor_for_int8, has_scale ? 1 : 0);
+  Tensor scores = at::empty({B, width}, opts.dtype(km_score_type(score_code)));
+  Tensor indices = at::empty({B, width}, opts.dtype(at::kInt));
+  if (B == 0 || width == 0) return {scores, indices};
+  if (mask.defined() && findex.defined()) {
+    // rows of the mask named by filtering_bit_index must exist
+    const Tensor bad = (findex < 0).logical_or(findex >= mask.size(0)).any();
+    TORCH_CHECK(!bad.item<bool>(), "filtering_bit_index names a row outside filtering_bit_mask (",
+                mask.size(0), " rows)");
+  } else if (mask.defined()) {
+    TORCH_CHECK(mask.size(0) >= B, "filtering_bit_mask has ", mask.size(0), " rows for ", B,
+                " queries");
+  }
+  check_st(st_fused_kmean_ann(offsets.numel() ? offsets.data_ptr<int64_t>() : nullptr,
+                              offsets.numel(), ids.numel() ? ids.data_ptr<int64_t>() : nullptr,
+                              lens.numel() ? lens.data_ptr<int64_t>() : nullptr, B, ids.size(1),
+                              emb.numel() ? emb.data_ptr() : nullptr, emb.size(0), emb.size(1), code,
+                              q.data_ptr(), width,
+                              mask.defined() && mask.numel() ? mask.data_ptr<int64_t>() : nullptr,
+                              mask.defined() ? mask.size(1) : 0,
+                              findex.defined() ? findex.data_ptr<int64_t>() : nullptr,
+                              has_scale ? reinterpret_cast<const uint16_t*>(scale.data_ptr()) : nullptr,
+                              divisor_for_int8, invalid_index_value, scores.data_ptr(),
+                              indices.data_ptr<int32_t>(), current_stream(emb)),
+           "fused_kmean_ann");
+  return {scores, indices};
+}
+
+std::optional<Tensor> opt_to(const std::optional<Tensor>& t, const at::Device& d) {
+  if (!t) return std::nullopt;
+  return t->to(d);
+}
+
+std::tuple<Tensor, Tensor> kmean_cpu(const Tensor& cluster_offsets, const Tensor& cluster_ids,
+                                     const Tensor& cluster_length, const Tensor& embeddings,
+                                     const Tensor& queries, int64_t max_tensor_size_per_row,
+                                     const std::optional<Tensor>& filtering_bit_mask,
+                                     int64_t invalid_index_value, int64_t divisor_for_int8,
+                                     const std::optional<Tensor>& filtering_bit_index,
+                                     const std::optional<Tensor>& per_embedding_scale) {
+  const at::Device gpu = gpu_for_cpu_call();
+  auto [scores, indices] = kmean_gpu(
+      cluster_offsets.to(gpu), cluster_ids.to(gpu), cluster_length.to(gpu), embeddings.to(gpu),
+      queries.to(gpu), max_tensor_size_per_row, opt_to(filtering_bit_mask, gpu),
+      invalid_index_value, divisor_for_int8, opt_to(filtering_bit_index, gpu),
+      opt_to(per_embedding_scale, gpu));
+  return {scores.cpu(), indices.cpu()};
+}
+
+// fused_kmean_ann_with_partial_masks: the reference's CPU op scores every doc
+// of the selected clusters and ignores the partial masks and
+// filtering_bit_index (fused_kmean_ann.cpp:229-260); so does this build.
+std::tuple<Tensor, Tensor> kmean_partial(
+    const Tensor& cluster_offsets, const Tensor& cluster_ids, const Tensor& cluster_length,
+    const Tensor& embeddings, const Tensor& queries, int64_t max_tensor_size_per_row,
+    const Tensor& /*partial_mask_column_counts_cumsum*/,
+    const Tensor& /*partial_mask_first_item_offset_in_column*/,
+    const Tensor& /*partial_mask_column_results*/, int64_t invalid_index_value,
+    int64_t divisor_for_int8, const std::optional<Tensor>& /*filtering_bit_index*/,
+    const std::optional<Tensor>& per_embedding_scale, const std::optional<Tensor>&,
+    const std::optional<Tensor>&, const std::optional<Tensor>&, const std::optional<Tensor>&,
+    int64_t, int64_t) {
+  if (embeddings.is_cuda())
+    return kmean_gpu(cluster_offsets, cluster_ids, cluster_length, embeddings, queries,
+                     max_tensor_size_per_row, std::nullopt, invalid_index_value,
+                     divisor_for_int8, std::nullopt, per_embedding_scale);
+  return kmean_cpu(cluster_offsets, cluster_ids, cluster_length, embeddings, queries,
+                   max_tensor_size_per_row, std::nullopt, invalid_index_value, divisor_for_int8,
+                   std::nullopt, per_embedding_scale);
+}
+
+// ..._multiple: one call per chunk (fused_kmean_ann.cpp:262-311, which passes
+// no per-embedding scale and ignores `fuse`).
+std::tuple<std::vector<Tensor>, std::vector<Tensor>> kmean_partial_multiple(
+    const Tensor& queries, const std::vector<Tensor>& list_cluster_offsets,
+    const std::vector<Tensor>& list_selected_cluster_ids,
+    const std::vector<Tensor>& list_selected_cluster_lengths,
+    const std::vector<Tensor>& list_embeddings, const std::vector<int64_t>& list_max_tensor_size_per_row,
+    const std::vector<Tensor>& list_counts, const std::vector<Tensor>& list_first,
+    const std::vector<Tensor>& list_results, int64_t invalid_index_value, int64_t divisor_for_int8,
+    const std::optional<Tensor>& filtering_bit_index,
+    const std::optional<std::vector<Tensor>>& /*list_per_embedding_scale*/, bool /*fuse*/) {
+  const size_t n = list_cluster_offsets.size();
+  TORCH_CHECK(list_selected_cluster_ids.size() == n && list_selected_cluster_lengths.size() == n &&
+                  list_embeddings.size() == n && list_max_tensor_size_per_row.size() == n &&
+                  list_counts.size() == n && list_first.size() == n && list_results.size() == n,
+              "fused_kmean_ann_with_partial_masks_multiple: the lists must have one entry per chunk");
+  std::vector<Tensor> scores, indices;
+  scores.reserve(n);
+  indices.reserve(n);
+  for (size_t i = 0; i < n; ++i) {
+    auto [s, ix] = kmean_partial(list_cluster_offsets[i], list_selected_cluster_ids[i],
+                                 list_selected_cluster_lengths[i], list_embeddings[i], queries,
+                                 list_max_tensor_size_per_row[i], list_counts[i], list_first[i],
+                                 list_results[i], invalid_index_value, divisor_for_int8,
+                                 filtering_bit_index, std::nullopt, std::nullopt, std::nullopt,
+                                 std::nullopt, std::nullopt, 0, 0);
+    scores.push_back(std::move(s));
+    indices.push_back(std::move(ix));
+  }
+  return {scores, indices};
+}
+
 }  // namespace
 
 TORCH_LIBRARY_FRAGMENT(st, m) {
@@ -667,6 +849,60 @@ TORCH_LIBRARY_FRAGMENT(st, m) {
       "Tensor bloom_query_plans_data, Tensor bloom_query_plans_offsets, int k, int hash_k, "
       "Tensor doc_embeddings, Tensor query_embeddings, int num_docs, int topk) "
       "-> (Tensor, Tensor)");
+  // fused_kmean_ann.cpp:400-455, verbatim
+  m.def(
+      "fused_kmean_ann("
+      "Tensor cluster_offsets, "
+      "Tensor cluster_ids, "
+      "Tensor cluster_length, "
+      "Tensor embeddings, "
+      "Tensor queries, "
+      "int max_tensor_size_per_row, "
+      "Tensor? filtering_bit_mask=None, "
+      "int invalid_index_value=-1,"
+      "int divisor_for_int8=-1,"
+      "Tensor? filtering_bit_index=None, "
+      "Tensor? per_embedding_scale=None "
+      ") -> (Tensor, Tensor)");
+  m.def(
+      "fused_kmean_ann_with_partial_masks("
+      "Tensor cluster_offsets, "
+      "Tensor cluster_ids, "
+      "Tensor cluster_length, "
+      "Tensor embeddings, "
+      "Tensor queries, "
+      "int max_tensor_size_per_row, "
+      "Tensor partial_mask_column_counts_cumsum, "
+      "Tensor partial_mask_first_item_offset_in_column, "
+      "Tensor partial_mask_column_results, "
+      "int invalid_index_value=-1,"
+      "int divisor_for_int8=-1,"
+      "Tensor? filtering_bit_index=None, "
+      "Tensor? per_embedding_scale=None, "
+      "Tensor? cluster_warp_size=None, "
+      "Tensor? cluster_warp_rounded_length_cumsum=None, "
+      "Tensor? cluster_remaining_length_cumsum=None, "
+      "Tensor? cluster_warp_size_cumsum=None, "
+      "int total_cluster_rounded_warps=0, "
+      "int total_cluster_remaining_warps=0 "
+      ") -> (Tensor, Tensor)");
+  m.def(
+      "fused_kmean_ann_with_partial_masks_multiple("
+      "Tensor queries, "
+      "Tensor[] list_cluster_offsets, "
+      "Tensor[] list_selected_cluster_ids, "
+      "Tensor[] list_selected_cluster_lengths, "
+      "Tensor[] list_embeddings, "
+      "int[] list_max_tensor_size_per_row, "
+      "Tensor[] list_partial_mask_column_counts_cumsum, "
+      "Tensor[] list_partial_mask_first_item_offset_in_column, "
+      "Tensor[] list_partial_mask_column_results, "
+      "int invalid_index_value=-1, "
+      "int divisor_for_int8=-1, "
+      "Tensor? filtering_bit_index=None, "
+      "Tensor[]? list_per_embedding_scale=None, "
+      "bool fuse=False "
+      ") -> (Tensor[], Tensor[])");
 }
 
 TORCH_LIBRARY_IMPL(st, CUDA, m) {
@@ -680,6 +916,9 @@ TORCH_LIBRARY_IMPL(st, CUDA, m) {
   m.impl("bloom_index_search_batch_ids", TORCH_FN(search_ids_gpu));
   m.impl("filtered_topk", TORCH_FN(filtered_topk_gpu));
   m.impl("bloom_index_search_topk", TORCH_FN(search_topk_gpu));
+  m.impl("fused_kmean_ann", TORCH_FN(kmean_gpu));
+  m.impl("fused_kmean_ann_with_partial_masks", TORCH_FN(kmean_partial));
+  m.impl("fused_kmean_ann_with_partial_masks_multiple", TORCH_FN(kmean_partial_multiple));
 }
 
 TORCH_LIBRARY_IMPL(st, CPU, m) {
@@ -693,6 +932,9 @@ TORCH_LIBRARY_IMPL(st, CPU, m) {
   m.impl("bloom_index_search_batch_ids", TORCH_FN(search_ids_cpu));
   m.impl("filtered_topk", TORCH_FN(filtered_topk_cpu));
   m.impl("bloom_index_search_topk", TORCH_FN(search_topk_cpu));
+  m.impl("fused_kmean_ann", TORCH_FN(kmean_cpu));
+  m.impl("fused_kmean_ann_with_partial_masks", TORCH_FN(kmean_partial));
+  m.impl("fused_kmean_ann_with_partial_masks_multiple", TORCH_FN(kmean_partial_multiple));
 }
 
 // Python module entry point: importing silvertorch_amd._C loads this library,

@@ -99,3 +99,32 @@ def partial_multiple() -> dict:
                    for i in range(n)] for fuse in (0, 1)}
     return {"chunks": chunks, "plans_data": z["multiple/plans_data"],
             "plans_offsets": z["multiple/plans_offsets"], "outputs": outs}
+
+
+@lru_cache(None)
+def _kmean_npz():
+    return dict(np.load(GOLDEN / "ref_kmean.npz", allow_pickle=False))
+
+
+KMEAN_CASES = ["readme", "f32_trunc", "f16", "bf16", "i8_raw", "i8_div", "i8_scale", "f32_odd_dim",
+               "f32_filter", "bf16_filter_index"]
+
+
+def kmean_case(name: str) -> dict:
+    """One fused_kmean_ann fixture of the reference CPU op (see
+    tests/golden/make_golden.py): inputs, parameters and expected outputs.
+    bfloat16 cases: 'bf16' is set, embeddings/queries are uint16 bit patterns
+    and 'scores' holds the reference's float32 scores of the exactly widened
+    values (the reference CPU op raises for bfloat16)."""
+    z = _kmean_npz()
+    pre = name + "/"
+    c = {k[len(pre):]: v for k, v in z.items() if k.startswith(pre)}
+    c["bf16"] = "embeddings@bf16" in c
+    max_size, divisor, invalid = (int(v) for v in c["params"])
+    c.update(max_size=max_size, divisor=divisor, invalid=invalid)
+    return c
+
+
+def kmean_group(prefix: str) -> dict:
+    z = _kmean_npz()
+    return {k[len(prefix) + 1:]: v for k, v in z.items() if k.startswith(prefix + "/")}

@@ -16,7 +16,12 @@ Sources of truth, neither of which is this repository's code:
       ref_partial.npz   cluster-restricted search outputs (partial response,
                         single and multiple-chunk ops) on small cases.
 
-Usage:  python tests/golden/make_golden.py [partial]   (partial: only ref_partial.npz)
+      ref_kmean.npz     fused_kmean_ann(_with_partial_masks(_multiple)) of the
+                        reference's CPU op (fused_kmean_ann.cpp) on small
+                        cases: every embedding dtype, int8 divisor and
+                        per-embedding scale, truncated rows, filtered rows.
+
+Usage:  python tests/golden/make_golden.py [partial|kmean]   (only that file)
 The reference library registers torch.ops.st.*, so this script never imports
 silvertorch_amd.
 """
@@ -310,9 +315,146 @@ def partial_fixtures() -> None:
     print("partial-response fixtures written to", HERE / "ref_partial.npz")
 
 
+def kmean_fixtures() -> None:
+    """ref_kmean.npz: fused_kmean_ann of the reference's CPU op
+    (fused_kmean_ann.cpp:85-227) and its partial-mask wrappers (:229-311).
+    Filtered cases: the reference CPU op reads doc d's filter bit as bit d % 64
+    (LSB first) while the search output and the reference CUDA op put doc d
+    at bit 63 - d % 64; those cases give the CPU op the bit-reversed words of
+    an MSB-first mask, so the stored output is the MSB-first semantics."""
+    import torch
+
+    ref = ROOT / "oracle" / "_ref" / "libst_ref.so"
+    if not ref.exists():
+        subprocess.run(["make", "-C", str(ROOT / "oracle"), "ref"], check=True)
+    torch.ops.load_library(str(ref))
+    st = torch.ops.st
+    out = {}
+    rng = np.random.default_rng(21)
+
+    def rev64(words: np.ndarray) -> np.ndarray:
+        w = words.view(np.uint64).copy()
+        r = np.zeros_like(w)
+        for i in range(64):
+            r |= ((w >> np.uint64(i)) & np.uint64(1)) << np.uint64(63 - i)
+        return r.view(np.int64)
+
+    def emb(n, dim, dtype):
+        if dtype == "int8":
+            return torch.from_numpy(rng.integers(-128, 128, (n, dim)).astype(np.int8))
+        t = torch.from_numpy(rng.standard_normal((n, dim)).astype(np.float32))
+        return t.to({"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}[dtype])
+
+    def save_tensor(key, t):
+        if t.dtype == torch.bfloat16:
+            out[key] = t.view(torch.int16).numpy().view(np.uint16)
+            out[key + "@bf16"] = np.array(1)
+        else:
+            out[key] = t.numpy()
+
+    def add(name, sizes, dim, dtype, batch, probes, max_size, divisor=-1, scale=False,
+            filtered=False, findex=False, invalid=-1):
+        sizes = np.asarray(sizes, np.int64)
+        offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+        n = int(offs[-1])
+        e, q = emb(n, dim, dtype), emb(batch, dim, dtype)
+        cids = rng.integers(0, len(sizes), (batch, probes)).astype(np.int64)
+        clen = sizes[cids]
+        kw = dict(invalid_index_value=invalid, divisor_for_int8=divisor)
+        mask = fi = None
+        if scale:
+            sc = torch.from_numpy((rng.random(n) * 4 + 0.5).astype(np.float32)).to(torch.float16)
+            kw["per_embedding_scale"] = sc
+            save_tensor(f"{name}/scale", sc)
+        if filtered:
+            rows = batch if not findex else 3
+            mask = rng.integers(-2**63, 2**63 - 1, (rows, (n + 63) // 64 - 1 if n > 128 else (n + 63) // 64),
+                                dtype=np.int64)
+            kw["filtering_bit_mask"] = torch.from_numpy(rev64(mask))
+            out[f"{name}/mask_msb"] = mask
+            if findex:
+                fi = rng.integers(0, rows, batch).astype(np.int64)
+                kw["filtering_bit_index"] = torch.from_numpy(fi)
+                out[f"{name}/filter_index"] = fi
+        if dtype == "bfloat16":
+            # the reference CPU op raises for bfloat16 (its -FLT_MAX padding
+            # overflows BFloat16); its float32 scores on the same (exactly
+            # widened) values are stored, the test rounds them to bfloat16
+            try:
+                st.fused_kmean_ann(torch.from_numpy(offs), torch.from_numpy(cids), torch.from_numpy(clen),
+                                   e, q, max_size, **kw)
+                raise SystemExit("the reference CPU op accepted bfloat16 embeddings")
+            except RuntimeError as err:
+                out[f"{name}/ref_error"] = np.array(str(err).splitlines()[0])
+            sc_, ix_ = st.fused_kmean_ann(torch.from_numpy(offs), torch.from_numpy(cids),
+                                          torch.from_numpy(clen), e.float(), q.float(), max_size, **kw)
+        else:
+            sc_, ix_ = st.fused_kmean_ann(torch.from_numpy(offs), torch.from_numpy(cids),
+                                          torch.from_numpy(clen), e, q, max_size, **kw)
+        out[f"{name}/cluster_offsets"] = offs
+        out[f"{name}/cluster_ids"] = cids
+        out[f"{name}/cluster_length"] = clen
+        save_tensor(f"{name}/embeddings", e)
+        save_tensor(f"{name}/queries", q)
+        out[f"{name}/params"] = np.array([max_size, divisor, invalid], np.int64)
+        save_tensor(f"{name}/scores", sc_)
+        out[f"{name}/indices"] = ix_.numpy()
+
+    add("readme", [3, 5, 7], 64, "float32", 2, 2, 12)  # the op's documented example shape
+    add("f32_trunc", rng.integers(1, 70, 9), 16, "float32", 4, 3, 40)
+    add("f16", rng.integers(1, 70, 9), 64, "float16", 3, 3, 200)
+    add("bf16", rng.integers(1, 70, 9), 128, "bfloat16", 3, 2, 150)
+    add("i8_raw", rng.integers(1, 70, 9), 32, "int8", 3, 3, 200)
+    add("i8_div", rng.integers(1, 70, 9), 32, "int8", 3, 3, 200, divisor=7)
+    add("i8_scale", rng.integers(1, 70, 9), 48, "int8", 3, 3, 200, scale=True)
+    add("f32_odd_dim", rng.integers(1, 40, 6), 17, "float32", 2, 4, 64, invalid=-99)
+    add("f32_filter", rng.integers(20, 90, 8), 32, "float32", 4, 3, 250, filtered=True)
+    add("bf16_filter_index", rng.integers(20, 90, 8), 32, "bfloat16", 5, 3, 250, filtered=True,
+        findex=True)
+
+    # partial-mask wrappers: the CPU op ignores the masks (and filtering_bit_index)
+    sizes = rng.integers(1, 40, 6).astype(np.int64)
+    offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    e, q = emb(int(offs[-1]), 32, "float32"), emb(3, 32, "float32")
+    cids = rng.integers(0, 6, (3, 2)).astype(np.int64)
+    dummy = torch.zeros(1, dtype=torch.long)
+    s1, i1 = st.fused_kmean_ann_with_partial_masks(torch.from_numpy(offs), torch.from_numpy(cids),
+                                                   torch.from_numpy(sizes[cids]), e, q, 70, dummy,
+                                                   dummy.to(torch.int8), dummy)
+    out["partial/cluster_offsets"] = offs
+    out["partial/cluster_ids"] = cids
+    out["partial/cluster_length"] = sizes[cids]
+    out["partial/embeddings"] = e.numpy()
+    out["partial/queries"] = q.numpy()
+    out["partial/scores"] = s1.numpy()
+    out["partial/indices"] = i1.numpy()
+    lo, ll, le, lm = [], [], [], []
+    for c in range(2):
+        sz = rng.integers(1, 30, 5).astype(np.int64)
+        of = np.concatenate([[0], np.cumsum(sz)]).astype(np.int64)
+        ci = rng.integers(0, 5, (3, 2)).astype(np.int64)
+        lo.append(torch.from_numpy(of)); ll.append(torch.from_numpy(ci)); le.append(torch.from_numpy(sz[ci]))
+        lm.append(emb(int(of[-1]), 32, "float32"))
+        out[f"multiple/{c}/cluster_offsets"] = of
+        out[f"multiple/{c}/cluster_ids"] = ci
+        out[f"multiple/{c}/cluster_length"] = sz[ci]
+        out[f"multiple/{c}/embeddings"] = lm[-1].numpy()
+    ms = st.fused_kmean_ann_with_partial_masks_multiple(q, lo, ll, le, lm, [33, 50], [dummy] * 2,
+                                                        [dummy.to(torch.int8)] * 2, [dummy] * 2)
+    out["multiple/queries"] = q.numpy()
+    for c in range(2):
+        out[f"multiple/{c}/scores"] = ms[0][c].numpy()
+        out[f"multiple/{c}/indices"] = ms[1][c].numpy()
+    np.savez_compressed(HERE / "ref_kmean.npz", **out)
+    print("fused_kmean_ann fixtures written to", HERE / "ref_kmean.npz")
+
+
 if __name__ == "__main__":
     if sys.argv[1:] == ["partial"]:
         partial_fixtures()
+    elif sys.argv[1:] == ["kmean"]:
+        kmean_fixtures()
     else:
         main()
         partial_fixtures()
+        kmean_fixtures()

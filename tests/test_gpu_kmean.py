@@ -1,0 +1,210 @@
+"""GPU parity of fused_kmean_ann (the clustered scoring step after the search)
+and its partial-mask wrappers: the reference CPU op's fixtures bit for bit,
+random shapes against the oracle, the search's packed mask as the filter, and
+a direct C-ABI call.  Reference: fused_kmean_ann.cpp:85-311,
+test_fused_kmean_ann.py."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import silvertorch_amd.ops._load_ops  # noqa: F401
+from oracle import oracle as O
+from oracle import parser_oracle as P
+from silvertorch_amd import capi
+from tests import _fixtures as G
+from tests import gpu_helpers as H
+
+pytestmark = pytest.mark.gpu
+st = torch.ops.st
+
+def _t(a: np.ndarray, bf16: bool = False, dev="cuda"):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if bf16:
+        t = t.view(torch.int16).view(torch.bfloat16)
+    return t.to(dev)
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    t = t.cpu()
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+def _run(c, dev="cuda", **over):
+    kw = dict(invalid_index_value=c["invalid"], divisor_for_int8=c["divisor"])
+    if "mask_msb" in c:
+        kw["filtering_bit_mask"] = _t(c["mask_msb"], dev=dev)
+    if "filter_index" in c:
+        kw["filtering_bit_index"] = _t(c["filter_index"], dev=dev)
+    if "scale" in c:
+        kw["per_embedding_scale"] = _t(c["scale"], dev=dev)
+    kw.update(over)
+    return st.fused_kmean_ann(_t(c["cluster_offsets"], dev=dev), _t(c["cluster_ids"], dev=dev),
+                              _t(c["cluster_length"], dev=dev), _t(c["embeddings"], c["bf16"], dev),
+                              _t(c["queries"], c["bf16"], dev), c["max_size"], **kw)
+
+@pytest.mark.parametrize("name", G.KMEAN_CASES)
+def test_matches_reference_fixtures(name):
+    c = G.kmean_case(name)
+    H.note(f"[kmean] fixture {name}")
+    sc, ix = _run(c)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ix.cpu().numpy(), c["indices"])
+    got = _bits(sc)
+    if c["bf16"]:
+        valid = c["indices"] != c["invalid"]
+        want = O.bf16_round(c["scores"])
+        np.testing.assert_array_equal(got[valid], want[valid])
+        assert (got[~valid] == 0xFF7F).all()
+    else:
+        assert sc.cpu().numpy().dtype == c["scores"].dtype
+        np.testing.assert_array_equal(got.view(np.uint8), c["scores"].view(np.uint8))
+
+def test_cpu_key_matches_cuda_key():
+    c = G.kmean_case("i8_scale")
+    a_s, a_i = _run(c)
+    b_s, b_i = _run(c, dev="cpu")
+    assert b_s.device.type == "cpu"
+    assert torch.equal(a_s.cpu(), b_s) and torch.equal(a_i.cpu(), b_i)
+
+def test_partial_mask_wrappers_match_reference():
+    p = G.kmean_group("partial")
+    dummy = torch.zeros(1, dtype=torch.long, device="cuda")
+    sc, ix = st.fused_kmean_ann_with_partial_masks(
+        _t(p["cluster_offsets"]), _t(p["cluster_ids"]), _t(p["cluster_length"]), _t(p["embeddings"]),
+        _t(p["queries"]), 70, dummy, dummy.to(torch.int8), dummy)
+    np.testing.assert_array_equal(ix.cpu().numpy(), p["indices"])
+    np.testing.assert_array_equal(sc.cpu().numpy(), p["scores"])
+    m = G.kmean_group("multiple")
+    ms = st.fused_kmean_ann_with_partial_masks_multiple(
+        _t(m["queries"]), [_t(m[f"{c}/cluster_offsets"]) for c in range(2)],
+        [_t(m[f"{c}/cluster_ids"]) for c in range(2)], [_t(m[f"{c}/cluster_length"]) for c in range(2)],
+        [_t(m[f"{c}/embeddings"]) for c in range(2)], [33, 50], [dummy] * 2, [dummy.to(torch.int8)] * 2,
+        [dummy] * 2, fuse=True)
+    for c in range(2):
+        np.testing.assert_array_equal(ms[1][c].cpu().numpy(), m[f"{c}/indices"])
+        np.testing.assert_array_equal(ms[0][c].cpu().numpy(), m[f"{c}/scores"])
+
+def _random_case(rng, dim, dtype, batch, probes, max_size, filtered=False):
+    nclus = int(rng.integers(3, 12))
+    sizes = rng.integers(0, 700, nclus)
+    offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    n = int(offs[-1])
+    if dtype == "int8":
+        emb = rng.integers(-128, 128, (n, dim)).astype(np.int8)
+        q = rng.integers(-128, 128, (batch, dim)).astype(np.int8)
+    else:
+        emb = rng.standard_normal((n, dim)).astype(np.float32)
+        q = rng.standard_normal((batch, dim)).astype(np.float32)
+        if dtype == "float16":
+            emb, q = emb.astype(np.float16), q.astype(np.float16)
+        if dtype == "bfloat16":
+            emb, q = O.bf16_round(emb), O.bf16_round(q)
+    cids = rng.integers(0, nclus, (batch, probes)).astype(np.int64)
+    mask = rng.integers(-2**63, 2**63 - 1, (batch, max(1, n // 64)), dtype=np.int64) if filtered else None
+    return dict(cluster_offsets=offs, cluster_ids=cids, cluster_length=sizes[cids].astype(np.int64),
+                embeddings=emb, queries=q, max_size=max_size, mask=mask, bf16=dtype == "bfloat16")
+
+@pytest.mark.parametrize("dim,dtype,filtered,divisor", [
+    (128, "float32", False, -1), (1280, "float32", True, -1), (17, "float32", True, -1),
+    (64, "float16", True, -1), (256, "bfloat16", False, -1), (96, "bfloat16", True, -1),
+    (32, "int8", False, -1), (128, "int8", True, 13)])
+def test_random_vs_oracle(dim, dtype, filtered, divisor):
+    rng = np.random.default_rng(dim + len(dtype))
+    c = _random_case(rng, dim, dtype, int(rng.integers(1, 24)), int(rng.integers(1, 6)),
+                     int(rng.integers(1, 2500)), filtered)
+    H.note(f"[kmean] random dim={dim} {dtype} filtered={filtered} docs={c['cluster_offsets'][-1]}")
+    kw = dict(divisor_for_int8=divisor)
+    if filtered:
+        kw["filtering_bit_mask"] = _t(c["mask"])
+    sc, ix = st.fused_kmean_ann(_t(c["cluster_offsets"]), _t(c["cluster_ids"]), _t(c["cluster_length"]),
+                                _t(c["embeddings"], c["bf16"]), _t(c["queries"], c["bf16"]),
+                                c["max_size"], **kw)
+    want_s, want_i = O.fused_kmean_ann(c["cluster_offsets"], c["cluster_ids"], c["cluster_length"],
+                                       c["embeddings"], c["queries"], c["max_size"], filter_mask=c["mask"],
+                                       divisor=divisor, bf16=c["bf16"])
+    np.testing.assert_array_equal(ix.cpu().numpy(), want_i)
+    np.testing.assert_array_equal(_bits(sc).view(np.uint8), want_s.view(np.uint8))
+
+def test_search_mask_as_filter():
+    """The packed output of bloom_index_search_batch filters the scoring, doc d
+    at bit 63 - d % 64, as the reference CUDA op reads it."""
+    rng = np.random.default_rng(9)
+    n, F = 9000, 2
+    cnt = rng.integers(1, 3, (n, F))
+    offs = np.concatenate([[0], np.cumsum(cnt.reshape(-1))]).astype(np.int64)
+    vals = rng.integers(0, 40, int(offs[-1])).astype(np.int64)
+    ids = np.array([1, 2], np.int32)
+    bi, bo = st.bloom_index_build(_t(ids), _t(offs), _t(vals), 3.0, 3)
+    queries = ["1:3 OR 2:5", "1:7", "NOT 2:1", "1:2 AND 2:2"]
+    _, data, po = P.parse_batch(queries, 7, True, 5)
+    pd = torch.from_numpy(np.frombuffer(data, dtype=np.int8).copy())
+    packed = st.bloom_index_search_batch(bi, bo, pd.cuda(), torch.tensor(po).cuda(), 3, 7, False)
+    coffs = np.concatenate([[0], np.sort(rng.choice(n, 13, replace=False)), [n]]).astype(np.int64)
+    sizes = np.diff(coffs)  # 14 clusters covering the docs
+    emb = rng.standard_normal((n, 48)).astype(np.float32)
+    qv = rng.standard_normal((4, 48)).astype(np.float32)
+    cids = rng.integers(0, len(sizes), (4, 5)).astype(np.int64)
+    sc, ix = st.fused_kmean_ann(_t(coffs), _t(cids), _t(sizes[cids].astype(np.int64)), _t(emb), _t(qv),
+                                4000, filtering_bit_mask=packed)
+    want_s, want_i = O.fused_kmean_ann(coffs, cids, sizes[cids], emb, qv, 4000,
+                                       filter_mask=packed.cpu().numpy())
+    np.testing.assert_array_equal(ix.cpu().numpy(), want_i)
+    np.testing.assert_array_equal(sc.cpu().numpy(), want_s)
+    # every returned doc passes its query's search
+    m = O.unpack_bool(packed.cpu().numpy())
+    for b in range(4):
+        got = ix[b].cpu().numpy()
+        got = got[got >= 0]
+        assert m[b, got].all()
+
+def test_edge_cases():
+    rng = np.random.default_rng(4)
+    emb = _t(rng.standard_normal((50, 16)).astype(np.float32))
+    q = _t(rng.standard_normal((2, 16)).astype(np.float32))
+    offs = _t(np.array([0, 20, 50], np.int64))
+    # no probes: all padding
+    sc, ix = st.fused_kmean_ann(offs, _t(np.zeros((2, 0), np.int64)), _t(np.zeros((2, 0), np.int64)),
+                                emb, q, 5, invalid_index_value=-7)
+    assert sc.shape == (2, 32) and (ix.cpu() == -7).all()
+    assert (sc.cpu() == -torch.finfo(torch.float32).max).all()
+    # a cluster id outside the offsets selects nothing; width 0 gives empty rows
+    sc, ix = st.fused_kmean_ann(offs, _t(np.array([[5, 1], [-1, 0]], np.int64)),
+                                _t(np.array([[3, 4], [2, 3]], np.int64)), emb, q, 40)
+    np.testing.assert_array_equal(ix.cpu().numpy()[0, :5], [20, 21, 22, 23, -1])
+    np.testing.assert_array_equal(ix.cpu().numpy()[1, :4], [0, 1, 2, -1])
+    sc, ix = st.fused_kmean_ann(offs, _t(np.array([[1]], np.int64))[:, :1].expand(2, 1).contiguous(),
+                                _t(np.array([[3], [3]], np.int64)), emb, q, 0)
+    assert sc.shape == (2, 0) and ix.shape == (2, 0)
+    with pytest.raises(RuntimeError):
+        st.fused_kmean_ann(offs, _t(np.zeros((2, 1), np.int64)), _t(np.zeros((3, 1), np.int64)), emb, q, 5)
+    with pytest.raises(RuntimeError):
+        st.fused_kmean_ann(offs, _t(np.zeros((2, 1), np.int64)), _t(np.zeros((2, 1), np.int64)),
+                           emb.double(), q.double(), 5)
+
+def test_c_abi_direct():
+    """st_fused_kmean_ann through ctypes on device buffers equals the op."""
+    c = G.kmean_case("i8_div")
+    L = capi.lib()
+    offs, cids, clen = _t(c["cluster_offsets"]), _t(c["cluster_ids"]), _t(c["cluster_length"])
+    emb, q = _t(c["embeddings"]), _t(c["queries"])
+    B, P_ = cids.shape
+    width = (c["max_size"] + 31) // 32 * 32
+    assert L.st_kmean_ann_score_dtype(3, c["divisor"], 0) == 1
+    sc = torch.empty((B, width), dtype=torch.float16, device="cuda")
+    ix = torch.empty((B, width), dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    capi.check(L.st_fused_kmean_ann(offs.data_ptr(), offs.numel(), cids.data_ptr(), clen.data_ptr(), B, P_,
+                                    emb.data_ptr(), emb.shape[0], emb.shape[1], 3, q.data_ptr(), width,
+                                    None, 0, None, None, c["divisor"], c["invalid"], sc.data_ptr(),
+                                    ix.data_ptr(), stream))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ix.cpu().numpy(), c["indices"])
+    np.testing.assert_array_equal(_bits(sc), c["scores"].view(np.uint16))
+    # a dim outside [1, 1280] is rejected before any launch
+    rc = L.st_fused_kmean_ann(offs.data_ptr(), offs.numel(), cids.data_ptr(), clen.data_ptr(), B, P_,
+                              emb.data_ptr(), emb.shape[0], 2048, 3, q.data_ptr(), width, None, 0, None,
+                              None, c["divisor"], c["invalid"], sc.data_ptr(), ix.data_ptr(), stream)
+    assert rc != 0 and b"dim" in L.st_last_error()

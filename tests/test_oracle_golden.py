@@ -284,3 +284,80 @@ def test_partial_response_columns_are_search_columns():
     with pytest.raises(ValueError, match="outside the index"):
         O.partial_response(c["index"], c["bundle_b_offsets"], c["plans_data"], c["plans_offsets"], k, hk,
                            bad, np.maximum(cl, 1), pi)
+
+
+@pytest.mark.parametrize("name", G.KMEAN_CASES)
+def test_kmean_oracle_matches_reference(name):
+    """fused_kmean_ann oracle vs the reference CPU op's fixtures: every score
+    and index bit for bit (filtered cases: the reference was given the
+    bit-reversed words of the MSB-first mask; bfloat16 cases: the reference's
+    float32 scores of the same values, rounded to bfloat16 by the independent
+    torch conversion)."""
+    import torch
+
+    c = G.kmean_case(name)
+    sc, ix = O.fused_kmean_ann(c["cluster_offsets"], c["cluster_ids"], c["cluster_length"],
+                               c["embeddings"], c["queries"], c["max_size"],
+                               filter_mask=c.get("mask_msb"), invalid_index=c["invalid"],
+                               divisor=c["divisor"], filter_index=c.get("filter_index"),
+                               scale=c.get("scale"), bf16=c["bf16"])
+    np.testing.assert_array_equal(ix, c["indices"])
+    if c["bf16"]:
+        valid = c["indices"] != c["invalid"]
+        want = torch.from_numpy(c["scores"]).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        np.testing.assert_array_equal(sc[valid], want[valid])
+        assert (sc[~valid] == 0xFF7F).all()
+        assert "BFloat16" in str(c["ref_error"])
+    else:
+        assert sc.dtype == c["scores"].dtype
+        np.testing.assert_array_equal(sc.view(np.uint8), c["scores"].view(np.uint8))
+
+
+def test_kmean_oracle_partial_wrappers_match_reference():
+    """The partial-mask wrappers of the reference CPU op score every doc of the
+    selected clusters (the masks are ignored): the unfiltered oracle equals
+    them."""
+    p = G.kmean_group("partial")
+    sc, ix = O.fused_kmean_ann(p["cluster_offsets"], p["cluster_ids"], p["cluster_length"],
+                               p["embeddings"], p["queries"], 70)
+    np.testing.assert_array_equal(ix, p["indices"])
+    np.testing.assert_array_equal(sc, p["scores"])
+    m = G.kmean_group("multiple")
+    for c, size in enumerate((33, 50)):
+        sc, ix = O.fused_kmean_ann(m[f"{c}/cluster_offsets"], m[f"{c}/cluster_ids"],
+                                   m[f"{c}/cluster_length"], m[f"{c}/embeddings"], m["queries"], size)
+        np.testing.assert_array_equal(ix, m[f"{c}/indices"])
+        np.testing.assert_array_equal(sc, m[f"{c}/scores"])
+
+
+def test_kmean_oracle_filter_identity():
+    """Filtering = the unfiltered rows restricted, in order, to the docs whose
+    MSB-first mask bit is set (and docs past the mask's words pass); a planted
+    LSB-first reading is caught."""
+    rng = np.random.default_rng(5)
+    sizes = rng.integers(1, 90, 7)
+    offs = np.concatenate([[0], np.cumsum(sizes)])
+    emb = rng.standard_normal((int(offs[-1]), 16)).astype(np.float32)
+    q = rng.standard_normal((3, 16)).astype(np.float32)
+    cids = rng.integers(0, 7, (3, 3))
+    mask = rng.integers(-2**63, 2**63 - 1, (3, int(offs[-1]) // 64), dtype=np.int64)
+    big = 1000
+    full_s, full_i = O.fused_kmean_ann(offs, cids, sizes[cids], emb, q, big)
+    f_s, f_i = O.fused_kmean_ann(offs, cids, sizes[cids], emb, q, big, filter_mask=mask)
+    for b in range(3):
+        keep = []
+        for j, d in enumerate(full_i[b].tolist()):
+            if d < 0:
+                break
+            w = d >> 6
+            if w >= mask.shape[1] or (int(mask[b, w].view(np.uint64)) >> (63 - (d & 63))) & 1:
+                keep.append(j)
+        np.testing.assert_array_equal(f_i[b][:len(keep)], full_i[b][keep])
+        np.testing.assert_array_equal(f_s[b][:len(keep)], full_s[b][keep])
+        assert (f_i[b][len(keep):] == -1).all()
+    lsb = mask.view(np.uint64)
+    rev = np.zeros_like(lsb)
+    for i in range(64):
+        rev |= ((lsb >> np.uint64(i)) & np.uint64(1)) << np.uint64(63 - i)
+    planted, _ = O.fused_kmean_ann(offs, cids, sizes[cids], emb, q, big, filter_mask=rev.view(np.int64))
+    assert not np.array_equal(planted, f_s)
