@@ -247,6 +247,77 @@ def measure_partial(st, bi, bo, pd, po, k, hk, N, packed, steps):
     }
 
 
+def measure_kmean(st, O, N, packed, steps):
+    """fused_kmean_ann, the scoring step after the search, on the cfg2 corpus:
+    IVF-style clusters of 4,000 docs, 16 per query (seeded), bf16[128] doc
+    embeddings drawn on the device, the packed cfg2 search output as
+    filtering_bit_mask.  Op time per call; algorithmic bytes = the passing
+    docs' embedding rows + the mask words of the selected clusters + the
+    outputs; two sampled rows checked against the oracle (bit-exact)."""
+    import numpy as np
+    import torch
+
+    Q = packed.shape[0]
+    csize, nclust, per_q, dim = 4000, N // 4000, 16, 128
+    rng = np.random.default_rng(42)
+    sel = np.stack([rng.choice(nclust, per_q, replace=False) for _ in range(Q)])
+    coffs = torch.arange(0, nclust * csize + 1, csize, dtype=torch.long, device="cuda")
+    cids = torch.from_numpy(sel.astype(np.int64)).cuda()
+    clen = torch.full((Q, per_q), csize, dtype=torch.long, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    emb = (torch.randn(N, dim, generator=g, device="cuda") / dim ** 0.5).to(torch.bfloat16)
+    qv = torch.randn(Q, dim, generator=g, device="cuda").to(torch.bfloat16)
+    width = per_q * csize
+
+    def step():
+        return st.fused_kmean_ann(coffs, cids, clen, emb, qv, width, filtering_bit_mask=packed)
+
+    sc, ix = step()
+    torch.cuda.synchronize()
+    n = max(steps // 10, 5)
+    t = time.perf_counter()
+    for _ in range(n):
+        sc, ix = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t) * 1e3 / n
+    passing = int((ix >= 0).sum().item())
+    alg = passing * dim * 2 + Q * per_q * (csize // 64 + 1) * 8 + sc.numel() * 2 + ix.numel() * 4
+    ok = True
+    bits = emb.view(torch.int16)
+    for b in (0, Q - 1):
+        rows = torch.cat([torch.arange(int(c) * csize, int(c) * csize + csize) for c in sel[b]])
+        e_np = bits[rows].cpu().numpy().view(np.uint16)
+        # oracle on this row alone: one cluster spanning the selected docs in order
+        ws, wi = O.fused_kmean_ann(np.array([0, rows.numel()]), np.zeros((1, 1), np.int64),
+                                   np.array([[rows.numel()]]), e_np,
+                                   qv[b:b + 1].view(torch.int16).cpu().numpy().view(np.uint16), width,
+                                   filter_mask=None, bf16=True)
+        # filter by the search mask (MSB-first) on the real doc ids
+        words = packed[b].cpu().numpy().view(np.uint64)
+        docs = rows.numpy()
+        keep = ((words[docs >> 6] >> (63 - (docs & 63)).astype(np.uint64)) & np.uint64(1)).astype(bool)
+        want_i = docs[keep]
+        got_i = ix[b].cpu().numpy()
+        got_i = got_i[got_i >= 0]
+        ok &= bool(np.array_equal(got_i, want_i))
+        want_s = ws[0][:rows.numel()][keep]
+        ok &= bool(np.array_equal(sc[b].view(torch.int16).cpu().numpy().view(np.uint16)[:len(got_i)], want_s))
+    log(f"fused_kmean_ann: {Q} queries x {per_q} clusters of {csize} docs, bf16[{dim}], search mask filter: "
+        f"{passing} docs scored, {ms:.3f} ms/call, sampled rows bit-exact vs oracle: {ok}")
+    if not ok:
+        sys.exit("parity failure in fused_kmean_ann")
+    return {
+        "op": "fused_kmean_ann (filtering_bit_mask = packed cfg2 search output)",
+        "workload": f"cfg2 corpus; {nclust} clusters of {csize} docs, {per_q} per query, bf16[{dim}]",
+        "ms_per_call": ms, "docs_scored": passing,
+        "scored_doc_queries_per_s": passing / (ms * 1e-3),
+        "algorithmic_bytes": alg, "achieved_gbs": alg / (ms * 1e-3) / 1e9,
+        "frac_of_hbm_peak": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "note": "op wall time; bytes: passing docs' embedding rows, the selected clusters' mask words, outputs",
+    }
+
+
 def measure_build_cfg4(st, O):
     """cfg4: bloom_index_build on 100M docs, 4 features,
     per-doc value counts uniform in [1, 8], values uniform over 10M, K=3,
@@ -624,6 +695,7 @@ def main():
                              args.steps, args.warmup)
 
     partial_report = None if args.bool_mask else measure_partial(st, bi, bo, pd, po, k, hk, N, out, args.steps)
+    kmean_report = None if args.bool_mask else measure_kmean(st, O, N, out, args.steps)
     topk_report = None if args.no_topk else measure_topk(st, capi, args.steps)
     build4_report = None if args.no_build4 else measure_build_cfg4(st, O)
     cfg3_report = None if args.no_cfg3 else measure_search_cfg3(st, O)
@@ -670,6 +742,7 @@ def main():
         "bool_mask": bool_report,
         "ids": ids_report,
         "partial": partial_report,
+        "kmean_ann": kmean_report,
         "topk": topk_report,
     }
     print(json.dumps(result), flush=True)

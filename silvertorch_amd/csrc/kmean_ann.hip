@@ -15,10 +15,12 @@
 // the score dtype, so every float score equals the reference CPU op's bit
 // for bit; int8 dot products are exact int32 sums.
 //
-// One 256-thread workgroup per query row: the query is staged in LDS as
-// float64; docs go 256 at a time, one per thread (16-byte loads of the
-// embedding row); a workgroup-wide exclusive scan of the pass flags gives
-// the output slots.  Memory-bound on the embedding rows read.
+// One 1024-thread workgroup per query row: the query is staged in LDS as
+// float64; a cluster's docs go 16,384 at a time, 16 per thread as pass bits
+// (filter words shifted to the docs), the passing ones listed in LDS in doc
+// order (workgroup scan of the counts), then scored by all threads (16-byte
+// loads of the embedding rows) into the next output slots.  Memory-bound on
+// the embedding rows read.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -29,7 +31,8 @@
 namespace st {
 namespace {
 
-constexpr int kKmThreads = 256;
+constexpr int kKmThreads = 1024;
+constexpr int kKmDocsPerThread = 16;  // docs whose pass bits one thread forms per chunk
 constexpr int kKmWaves = kKmThreads / 64;
 constexpr int kKmMaxDim = 1280;
 
@@ -142,14 +145,16 @@ struct KmArgs {
   int32_t* indices;
 };
 
-// Workgroup-wide exclusive scan of 0/1 flags; *total receives the sum.
-__device__ __forceinline__ uint32_t block_scan_flags(bool f, uint32_t* wave_sums, uint32_t* total) {
+// Workgroup-wide exclusive scan of per-thread counts; *total receives the sum.
+__device__ __forceinline__ uint32_t block_scan(uint32_t v, uint32_t* wave_sums, uint32_t* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint64_t m = __ballot(f);
-  const uint32_t below =
-      __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
-  if (lane == 0) wave_sums[wave] = static_cast<uint32_t>(__popcll(m));
+  uint32_t incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) wave_sums[wave] = incl;
   __syncthreads();
   uint32_t before = 0, sum = 0;
 #pragma unroll
@@ -160,7 +165,7 @@ __device__ __forceinline__ uint32_t block_scan_flags(bool f, uint32_t* wave_sums
   }
   __syncthreads();  // wave_sums is reused by the next call
   *total = sum;
-  return before + below;
+  return before + incl - v;
 }
 
 template <int DT, int ST>
@@ -176,12 +181,41 @@ __device__ __forceinline__ void put_score(void* scores, int64_t at, double f64, 
   if constexpr (ST == kKmI32) static_cast<int32_t*>(scores)[at] = i32;
 }
 
-// DT: embedding dtype; ST: score dtype.
+// Pass bits of the 64 docs s .. s + 63 (bit 63 = doc s): doc d passes when it
+// is one of the first n, lies in [0, total_docs), and its filter bit (bit
+// 63 - d % 64 of mask word d / 64) is set or that word is past the mask.
+__device__ __forceinline__ uint64_t pass_bits(const int64_t* mask, int64_t cols, int64_t s, int n,
+                                              int64_t total_docs) {
+  if (n <= 0) return 0;
+  uint64_t bits = n >= 64 ? ~0ull : ~(~0ull >> n);
+  // docs outside [0, total_docs)
+  if (s < 0) bits &= s + 64 <= 0 ? 0ull : (~0ull >> static_cast<int>(-s));
+  if (s + 64 > total_docs) {
+    const int64_t keep = total_docs - s;
+    bits &= keep <= 0 ? 0ull : (keep >= 64 ? ~0ull : ~(~0ull >> keep));
+  }
+  if (mask == nullptr || bits == 0) return bits;
+  const int64_t w = s >> 6;  // arithmetic shift: s may be negative
+  const int o = static_cast<int>(s & 63);
+  auto word = [&](int64_t i) -> uint64_t {
+    return i < 0 ? 0ull : (i < cols ? static_cast<uint64_t>(mask[i]) : ~0ull);
+  };
+  uint64_t f = word(w) << o;
+  if (o != 0) f |= word(w + 1) >> (64 - o);
+  return bits & f;
+}
+
+// DT: embedding dtype; ST: score dtype.  Per chunk of 16,384 docs of a
+// cluster: every thread takes 16 docs, forms their pass bits, and the passing
+// docs of the chunk are listed in LDS in doc order (workgroup scan of the
+// counts); then all threads score the listed docs, two at a time (independent
+// float64 sums), and write them to the next output slots.
 template <int DT, int ST>
 __global__ __launch_bounds__(kKmThreads) void kmean_ann_kernel(KmArgs a) {
   __shared__ double qd[kKmMaxDim];
   __shared__ int8_t qi[kKmMaxDim];
   __shared__ uint32_t wave_sums[kKmWaves];
+  __shared__ int32_t list[kKmThreads * kKmDocsPerThread];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
   const int dim = a.dim;
@@ -202,7 +236,25 @@ __global__ __launch_bounds__(kKmThreads) void kmean_ann_kernel(KmArgs a) {
   }
   const size_t row_bytes = static_cast<size_t>(dim) * (DT == kKmF32 ? 4 : (DT == kKmI8 ? 1 : 2));
   const int64_t out0 = b * a.max_per_row;
+  auto score = [&](int32_t doc, int64_t slot) {
+    const char* row = static_cast<const char*>(a.embeddings) + static_cast<size_t>(doc) * row_bytes;
+    double f64 = 0.0;
+    int32_t i32 = 0;
+    float f32h = 0.f;
+    if constexpr (DT == kKmI8) {
+      i32 = dot_i8(reinterpret_cast<const int8_t*>(row), qi, dim);
+      if (a.scale != nullptr)
+        f32h = static_cast<float>(i32) / half_to_float(a.scale[doc]);
+      else if (a.divisor != -1)
+        f32h = static_cast<float>(i32) / static_cast<float>(a.divisor);
+    } else {
+      f64 = dot_f64<DT>(row, qd, dim);
+    }
+    put_score<DT, ST>(a.scores, out0 + slot, f64, i32, f32h);
+    a.indices[out0 + slot] = doc;
+  };
   int64_t written = 0;
+  constexpr int64_t kChunk = kKmThreads * kKmDocsPerThread;
   for (int64_t p = 0; p < a.probes && written < a.max_per_row; ++p) {
     const int64_t cid = a.cluster_ids[b * a.probes + p];
     int64_t len = a.cluster_length[b * a.probes + p];
@@ -210,42 +262,30 @@ __global__ __launch_bounds__(kKmThreads) void kmean_ann_kernel(KmArgs a) {
     // cluster (the reference reads out of bounds there)
     if (cid < 0 || cid >= a.num_offsets || len < 0) len = 0;
     const int64_t start = len > 0 ? a.cluster_offsets[cid] : 0;
-    for (int64_t base = 0; base < len && written < a.max_per_row; base += kKmThreads) {
-      const int64_t i = base + tid;
-      const int64_t doc = start + i;
-      bool pass = i < len && doc >= 0 && doc < a.total_docs;
-      if (pass && mask != nullptr) {
-        const int64_t word = doc >> 6;
-        if (word < a.filter_cols)
-          pass = (static_cast<uint64_t>(mask[word]) >> (63 - (doc & 63))) & 1u;
-      }
+    for (int64_t base = 0; base < len && written < a.max_per_row; base += kChunk) {
+      const int64_t i0 = base + static_cast<int64_t>(tid) * kKmDocsPerThread;
+      const int n = static_cast<int>(min<int64_t>(max<int64_t>(len - i0, 0), kKmDocsPerThread));
+      uint64_t bits = pass_bits(mask, a.filter_cols, start + i0, n, a.total_docs);
       uint32_t total;
-      const uint32_t slot_in = block_scan_flags(pass, wave_sums, &total);
-      const int64_t slot = written + slot_in;
-      if (pass && slot < a.max_per_row) {
-        const char* row = static_cast<const char*>(a.embeddings) + static_cast<size_t>(doc) * row_bytes;
-        double f64 = 0.0;
-        int32_t i32 = 0;
-        float f32h = 0.f;
-        if constexpr (DT == kKmI8) {
-          i32 = dot_i8(reinterpret_cast<const int8_t*>(row), qi, dim);
-          if (a.scale != nullptr)
-            f32h = static_cast<float>(i32) / half_to_float(a.scale[doc]);
-          else if (a.divisor != -1)
-            f32h = static_cast<float>(i32) / static_cast<float>(a.divisor);
-        } else {
-          f64 = dot_f64<DT>(row, qd, dim);
-        }
-        put_score<DT, ST>(a.scores, out0 + slot, f64, i32, f32h);
-        a.indices[out0 + slot] = static_cast<int32_t>(doc);
+      uint32_t at = block_scan(static_cast<uint32_t>(__popcll(bits)), wave_sums, &total);
+      while (bits != 0) {  // this thread's passing docs, in order
+        const int j = __clzll(bits);
+        list[at++] = static_cast<int32_t>(start + i0 + j);
+        bits &= ~(0x8000000000000000ull >> j);
       }
-      written += total;
+      __syncthreads();
+      const int64_t m = min<int64_t>(total, a.max_per_row - written);
+      for (int64_t i = tid; i < m; i += 2 * kKmThreads) {
+        score(list[i], written + i);
+        if (i + kKmThreads < m) score(list[i + kKmThreads], written + i + kKmThreads);
+      }
+      written += m;
+      __syncthreads();  // the list is refilled by the next chunk
     }
   }
   // padding: the score dtype's most negative finite value (-FLT_MAX, -65504
   // for float16, 0xFF7F for bfloat16 as the reference CUDA op pads,
   // simple_index_mm.cuh:99-123) or INT32_MIN, and invalid_index
-  if (written > a.max_per_row) written = a.max_per_row;
   for (int64_t s = written + tid; s < a.max_per_row; s += kKmThreads) {
     if constexpr (ST == kKmF32) static_cast<float*>(a.scores)[out0 + s] = -3.402823466e38f;
     if constexpr (ST == kKmF16) static_cast<uint16_t*>(a.scores)[out0 + s] = 0xFBFFu;
