@@ -355,8 +355,11 @@ int st_filtered_topk(const int64_t* packed, int64_t num_queries,
  * [total_docs]) is given) are float64 dot products converted to the score
  * dtype (int8: exact int32 sums, divided as float when scaled); indices are
  * int32 doc ids.  1 <= dim <= 1280.  A cluster id outside
- * [0, num_offsets) or a negative length selects nothing.
+ * [0, num_offsets) or a negative length selects nothing.  workspace: device
+ * memory of st_fused_kmean_ann_workspace_bytes(batch, probes) bytes (the
+ * per-(row, probe) counts of passing docs).
  * ------------------------------------------------------------------------- */
+int64_t st_fused_kmean_ann_workspace_bytes(int64_t batch, int64_t probes);
 int st_kmean_ann_score_dtype(int emb_dtype, int64_t divisor_for_int8,
                              int has_per_embedding_scale);
 int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_offsets,
@@ -368,7 +371,8 @@ int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_offsets,
                        const int64_t* filter_index,
                        const uint16_t* per_embedding_scale,
                        int64_t divisor_for_int8, int64_t invalid_index_value,
-                       void* scores, int32_t* indices, void* stream);
+                       void* workspace, void* scores, int32_t* indices,
+                       void* stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

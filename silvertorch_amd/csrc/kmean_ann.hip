@@ -15,15 +15,19 @@
 // the score dtype, so every float score equals the reference CPU op's bit
 // for bit; int8 dot products are exact int32 sums.
 //
-// One 1024-thread workgroup per query row: the query is staged in LDS as
-// float64; a cluster's docs go 16,384 at a time, 16 per thread as pass bits
-// (filter words shifted to the docs), the passing ones listed in LDS in doc
-// order (workgroup scan of the counts), then scored by all threads (16-byte
-// loads of the embedding rows) into the next output slots.  Memory-bound on
-// the embedding rows read.
+// Two launches: kmean_count_kernel counts the passing docs of every (row,
+// probe); kmean_ann_kernel, one 1024-thread workgroup per (row, probe),
+// starts at the row's count of the earlier probes, stages the query in LDS
+// as float64, takes its cluster's docs 16,384 at a time (16 per thread as
+// pass bits: the filter words shifted to the docs), lists the passing ones
+// in LDS in doc order (workgroup scan) and scores them with all threads
+// (16-byte loads of the embedding rows) into the next output slots.  A heavy
+// row is spread over its probes' workgroups.  Memory-bound on the embedding
+// rows read.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "st_errors.hpp"
@@ -205,20 +209,84 @@ __device__ __forceinline__ uint64_t pass_bits(const int64_t* mask, int64_t cols,
   return bits & f;
 }
 
-// DT: embedding dtype; ST: score dtype.  Per chunk of 16,384 docs of a
-// cluster: every thread takes 16 docs, forms their pass bits, and the passing
-// docs of the chunk are listed in LDS in doc order (workgroup scan of the
-// counts); then all threads score the listed docs, two at a time (independent
-// float64 sums), and write them to the next output slots.
+// Pass bits of this thread's docs of chunk `base` of cluster (b, p).
+struct KmProbe {
+  int64_t start, len;
+};
+
+__device__ __forceinline__ KmProbe km_probe(const KmArgs& a, int64_t b, int64_t p) {
+  const int64_t cid = a.cluster_ids[b * a.probes + p];
+  int64_t len = a.cluster_length[b * a.probes + p];
+  // a cluster id outside the offsets or a negative length is an empty
+  // cluster (the reference reads out of bounds there)
+  if (cid < 0 || cid >= a.num_offsets || len < 0) len = 0;
+  return KmProbe{len > 0 ? a.cluster_offsets[cid] : 0, len};
+}
+
+__device__ __forceinline__ const int64_t* km_mask_row(const KmArgs& a, int64_t b) {
+  if (a.filter_mask == nullptr) return nullptr;
+  const int64_t frow = a.filter_index != nullptr ? a.filter_index[b] : b;
+  return a.filter_mask + frow * a.filter_cols;
+}
+
+__device__ __forceinline__ uint64_t chunk_bits(const KmArgs& a, const int64_t* mask, KmProbe pr,
+                                               int64_t base, int64_t& i0) {
+  i0 = base + static_cast<int64_t>(threadIdx.x) * kKmDocsPerThread;
+  const int n = static_cast<int>(min<int64_t>(max<int64_t>(pr.len - i0, 0), kKmDocsPerThread));
+  return pass_bits(mask, a.filter_cols, pr.start + i0, n, a.total_docs);
+}
+
+constexpr int64_t kKmChunk = kKmThreads * kKmDocsPerThread;
+
+// Passing docs of each (row, probe): counts[b * probes + p], one wave per
+// (row, probe), 64 docs per lane per step.
+constexpr int kKmCountThreads = 256;
+__global__ __launch_bounds__(kKmCountThreads) void kmean_count_kernel(KmArgs a, int64_t* counts,
+                                                                      int64_t items) {
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * (kKmCountThreads / 64) + (threadIdx.x >> 6);
+  if (item >= items) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t b = item / a.probes, p = item % a.probes;
+  const KmProbe pr = km_probe(a, b, p);
+  const int64_t* mask = km_mask_row(a, b);
+  int64_t sum = 0;
+  for (int64_t i0 = static_cast<int64_t>(lane) * 64; i0 < pr.len; i0 += 64 * 64) {
+    const int n = static_cast<int>(min<int64_t>(pr.len - i0, 64));
+    sum += __popcll(pass_bits(mask, a.filter_cols, pr.start + i0, n, a.total_docs));
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  if (lane == 0) counts[item] = sum;
+}
+
+// DT: embedding dtype; ST: score dtype.  One workgroup per (row, probe):
+// its first output slot is the row's passing docs of the earlier probes
+// (from counts); per chunk of 16,384 docs of the cluster every thread forms
+// the pass bits of 16 docs, the passing docs are listed in LDS in doc order
+// (workgroup scan of the counts), then the whole workgroup scores them, two
+// per thread at a time (independent float64 sums), into the next slots while
+// the row has room.  The row's last probe (or, without probes, the only
+// workgroup) writes the padding.
 template <int DT, int ST>
-__global__ __launch_bounds__(kKmThreads) void kmean_ann_kernel(KmArgs a) {
+__global__ __launch_bounds__(kKmThreads) void kmean_ann_kernel(KmArgs a, const int64_t* counts) {
   __shared__ double qd[kKmMaxDim];
   __shared__ int8_t qi[kKmMaxDim];
   __shared__ uint32_t wave_sums[kKmWaves];
+  __shared__ int64_t base_sum[kKmWaves];
   __shared__ int32_t list[kKmThreads * kKmDocsPerThread];
-  const int64_t b = blockIdx.x;
+  const int64_t nprobes = a.probes > 0 ? a.probes : 1;
+  const int64_t b = blockIdx.x / nprobes, p = blockIdx.x % nprobes;
   const int tid = threadIdx.x;
   const int dim = a.dim;
+  const int64_t out0 = b * a.max_per_row;
+
+  // first slot: passing docs of the row's probes before p
+  int64_t part = 0;
+  if (a.probes > 0)
+    for (int64_t q = tid; q < p; q += kKmThreads) part += counts[b * a.probes + q];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
+  if ((tid & 63) == 0) base_sum[tid >> 6] = part;
   if constexpr (DT == kKmI8) {
     const int8_t* q = static_cast<const int8_t*>(a.queries) + b * dim;
     for (int d = tid; d < dim; d += kKmThreads) qi[d] = q[d];
@@ -228,14 +296,11 @@ __global__ __launch_bounds__(kKmThreads) void kmean_ann_kernel(KmArgs a) {
     for (int d = tid; d < dim; d += kKmThreads) qd[d] = static_cast<double>(elem_f<DT>(q, d));
   }
   __syncthreads();
+  int64_t written = 0;
+#pragma unroll
+  for (int w = 0; w < kKmWaves; ++w) written += base_sum[w];
 
-  const int64_t* mask = nullptr;
-  if (a.filter_mask != nullptr) {
-    const int64_t frow = a.filter_index != nullptr ? a.filter_index[b] : b;
-    mask = a.filter_mask + frow * a.filter_cols;
-  }
   const size_t row_bytes = static_cast<size_t>(dim) * (DT == kKmF32 ? 4 : (DT == kKmI8 ? 1 : 2));
-  const int64_t out0 = b * a.max_per_row;
   auto score = [&](int32_t doc, int64_t slot) {
     const char* row = static_cast<const char*>(a.embeddings) + static_cast<size_t>(doc) * row_bytes;
     double f64 = 0.0;
@@ -253,24 +318,17 @@ __global__ __launch_bounds__(kKmThreads) void kmean_ann_kernel(KmArgs a) {
     put_score<DT, ST>(a.scores, out0 + slot, f64, i32, f32h);
     a.indices[out0 + slot] = doc;
   };
-  int64_t written = 0;
-  constexpr int64_t kChunk = kKmThreads * kKmDocsPerThread;
-  for (int64_t p = 0; p < a.probes && written < a.max_per_row; ++p) {
-    const int64_t cid = a.cluster_ids[b * a.probes + p];
-    int64_t len = a.cluster_length[b * a.probes + p];
-    // a cluster id outside the offsets or a negative length is an empty
-    // cluster (the reference reads out of bounds there)
-    if (cid < 0 || cid >= a.num_offsets || len < 0) len = 0;
-    const int64_t start = len > 0 ? a.cluster_offsets[cid] : 0;
-    for (int64_t base = 0; base < len && written < a.max_per_row; base += kChunk) {
-      const int64_t i0 = base + static_cast<int64_t>(tid) * kKmDocsPerThread;
-      const int n = static_cast<int>(min<int64_t>(max<int64_t>(len - i0, 0), kKmDocsPerThread));
-      uint64_t bits = pass_bits(mask, a.filter_cols, start + i0, n, a.total_docs);
+  if (a.probes > 0) {
+    const KmProbe pr = km_probe(a, b, p);
+    const int64_t* mask = km_mask_row(a, b);
+    for (int64_t base = 0; base < pr.len && written < a.max_per_row; base += kKmChunk) {
+      int64_t i0;
+      uint64_t bits = chunk_bits(a, mask, pr, base, i0);
       uint32_t total;
       uint32_t at = block_scan(static_cast<uint32_t>(__popcll(bits)), wave_sums, &total);
       while (bits != 0) {  // this thread's passing docs, in order
         const int j = __clzll(bits);
-        list[at++] = static_cast<int32_t>(start + i0 + j);
+        list[at++] = static_cast<int32_t>(pr.start + i0 + j);
         bits &= ~(0x8000000000000000ull >> j);
       }
       __syncthreads();
@@ -279,14 +337,15 @@ __global__ __launch_bounds__(kKmThreads) void kmean_ann_kernel(KmArgs a) {
         score(list[i], written + i);
         if (i + kKmThreads < m) score(list[i + kKmThreads], written + i + kKmThreads);
       }
-      written += m;
+      written += total;
       __syncthreads();  // the list is refilled by the next chunk
     }
   }
+  if (p != nprobes - 1) return;
   // padding: the score dtype's most negative finite value (-FLT_MAX, -65504
   // for float16, 0xFF7F for bfloat16 as the reference CUDA op pads,
   // simple_index_mm.cuh:99-123) or INT32_MIN, and invalid_index
-  for (int64_t s = written + tid; s < a.max_per_row; s += kKmThreads) {
+  for (int64_t s = min(written, a.max_per_row) + tid; s < a.max_per_row; s += kKmThreads) {
     if constexpr (ST == kKmF32) static_cast<float*>(a.scores)[out0 + s] = -3.402823466e38f;
     if constexpr (ST == kKmF16) static_cast<uint16_t*>(a.scores)[out0 + s] = 0xFBFFu;
     if constexpr (ST == kKmBF16) static_cast<uint16_t*>(a.scores)[out0 + s] = 0xFF7Fu;
@@ -305,6 +364,10 @@ extern "C" int st_kmean_ann_score_dtype(int emb_dtype, int64_t divisor_for_int8,
   return (divisor_for_int8 != -1 || has_per_embedding_scale) ? kKmF16 : kKmI32;
 }
 
+extern "C" int64_t st_fused_kmean_ann_workspace_bytes(int64_t batch, int64_t probes) {
+  return batch > 0 && probes > 0 ? batch * probes * static_cast<int64_t>(sizeof(int64_t)) : 0;
+}
+
 extern "C" int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_offsets,
                                   const int64_t* cluster_ids, const int64_t* cluster_length,
                                   int64_t batch, int64_t probes, const void* embeddings,
@@ -313,8 +376,8 @@ extern "C" int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_of
                                   const int64_t* filter_mask, int64_t filter_cols,
                                   const int64_t* filter_index,
                                   const uint16_t* per_embedding_scale, int64_t divisor_for_int8,
-                                  int64_t invalid_index_value, void* scores, int32_t* indices,
-                                  void* stream) {
+                                  int64_t invalid_index_value, void* workspace, void* scores,
+                                  int32_t* indices, void* stream) {
   using namespace st;
   return guarded([&] {
     ST_CHECK(batch >= 0 && probes >= 0 && total_docs >= 0 && max_per_row >= 0 && num_offsets >= 0,
@@ -350,16 +413,25 @@ extern "C" int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_of
     a.indices = indices;
     const int st = st_kmean_ann_score_dtype(emb_dtype, divisor_for_int8, a.scale != nullptr);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid(static_cast<unsigned>(batch)), block(kKmThreads);
+    const int64_t groups = batch * std::max<int64_t>(probes, 1);
+    ST_CHECK(groups <= INT32_MAX, "batch x probes = ", groups, " workgroups; at most 2^31 - 1");
+    int64_t* counts = static_cast<int64_t*>(workspace);
+    if (probes > 0) {
+      ST_CHECK(counts != nullptr, "workspace is null");
+      const int64_t items = batch * probes, per = kKmCountThreads / 64;
+      hipLaunchKernelGGL(kmean_count_kernel, dim3(static_cast<unsigned>((items + per - 1) / per)),
+                         dim3(kKmCountThreads), 0, s, a, counts, items);
+    }
+    const dim3 grid(static_cast<unsigned>(groups)), block(kKmThreads);
     switch (emb_dtype) {
-      case kKmF32: hipLaunchKernelGGL((kmean_ann_kernel<kKmF32, kKmF32>), grid, block, 0, s, a); break;
-      case kKmF16: hipLaunchKernelGGL((kmean_ann_kernel<kKmF16, kKmF16>), grid, block, 0, s, a); break;
-      case kKmBF16: hipLaunchKernelGGL((kmean_ann_kernel<kKmBF16, kKmBF16>), grid, block, 0, s, a); break;
+      case kKmF32: hipLaunchKernelGGL((kmean_ann_kernel<kKmF32, kKmF32>), grid, block, 0, s, a, counts); break;
+      case kKmF16: hipLaunchKernelGGL((kmean_ann_kernel<kKmF16, kKmF16>), grid, block, 0, s, a, counts); break;
+      case kKmBF16: hipLaunchKernelGGL((kmean_ann_kernel<kKmBF16, kKmBF16>), grid, block, 0, s, a, counts); break;
       default:
         if (st == kKmI32)
-          hipLaunchKernelGGL((kmean_ann_kernel<kKmI8, kKmI32>), grid, block, 0, s, a);
+          hipLaunchKernelGGL((kmean_ann_kernel<kKmI8, kKmI32>), grid, block, 0, s, a, counts);
         else
-          hipLaunchKernelGGL((kmean_ann_kernel<kKmI8, kKmF16>), grid, block, 0, s, a);
+          hipLaunchKernelGGL((kmean_ann_kernel<kKmI8, kKmF16>), grid, block, 0, s, a, counts);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)

@@ -710,6 +710,8 @@ std::tuple<Tensor, Tensor> kmean_gpu(const Tensor& cluster_offsets_in, const Ten
     TORCH_CHECK(mask.size(0) >= B, "filtering_bit_mask has ", mask.size(0), " rows for ", B,
                 " queries");
   }
+  Tensor ws = at::empty({std::max<int64_t>(st_fused_kmean_ann_workspace_bytes(B, ids.size(1)), 1)},
+                        opts.dtype(at::kByte));
   check_st(st_fused_kmean_ann(offsets.numel() ? offsets.data_ptr<int64_t>() : nullptr,
                               offsets.numel(), ids.numel() ? ids.data_ptr<int64_t>() : nullptr,
                               lens.numel() ? lens.data_ptr<int64_t>() : nullptr, B, ids.size(1),
@@ -719,8 +721,8 @@ std::tuple<Tensor, Tensor> kmean_gpu(const Tensor& cluster_offsets_in, const Ten
                               mask.defined() ? mask.size(1) : 0,
                               findex.defined() ? findex.data_ptr<int64_t>() : nullptr,
                               has_scale ? reinterpret_cast<const uint16_t*>(scale.data_ptr()) : nullptr,
-                              divisor_for_int8, invalid_index_value, scores.data_ptr(),
-                              indices.data_ptr<int32_t>(), current_stream(emb)),
+                              divisor_for_int8, invalid_index_value, ws.data_ptr(),
+                              scores.data_ptr(), indices.data_ptr<int32_t>(), current_stream(emb)),
            "fused_kmean_ann");
   return {scores, indices};
 }

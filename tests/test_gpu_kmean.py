@@ -196,15 +196,17 @@ def test_c_abi_direct():
     sc = torch.empty((B, width), dtype=torch.float16, device="cuda")
     ix = torch.empty((B, width), dtype=torch.int32, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
+    ws = torch.empty(L.st_fused_kmean_ann_workspace_bytes(B, P_), dtype=torch.uint8, device="cuda")
     capi.check(L.st_fused_kmean_ann(offs.data_ptr(), offs.numel(), cids.data_ptr(), clen.data_ptr(), B, P_,
                                     emb.data_ptr(), emb.shape[0], emb.shape[1], 3, q.data_ptr(), width,
-                                    None, 0, None, None, c["divisor"], c["invalid"], sc.data_ptr(),
-                                    ix.data_ptr(), stream))
+                                    None, 0, None, None, c["divisor"], c["invalid"], ws.data_ptr(),
+                                    sc.data_ptr(), ix.data_ptr(), stream))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(ix.cpu().numpy(), c["indices"])
     np.testing.assert_array_equal(_bits(sc), c["scores"].view(np.uint16))
     # a dim outside [1, 1280] is rejected before any launch
     rc = L.st_fused_kmean_ann(offs.data_ptr(), offs.numel(), cids.data_ptr(), clen.data_ptr(), B, P_,
                               emb.data_ptr(), emb.shape[0], 2048, 3, q.data_ptr(), width, None, 0, None,
-                              None, c["divisor"], c["invalid"], sc.data_ptr(), ix.data_ptr(), stream)
+                              None, c["divisor"], c["invalid"], ws.data_ptr(), sc.data_ptr(), ix.data_ptr(),
+                              stream)
     assert rc != 0 and b"dim" in L.st_last_error()
