@@ -16,14 +16,14 @@
 // for bit; int8 dot products are exact int32 sums.
 //
 // Two launches: kmean_count_kernel counts the passing docs of every (row,
-// probe); kmean_ann_kernel, one 1024-thread workgroup per (row, probe),
+// probe); kmean_ann_kernel, one 512-thread workgroup per (row, probe),
 // starts at the row's count of the earlier probes, stages the query in LDS
-// as float64, takes its cluster's docs 16,384 at a time (16 per thread as
+// as float64, takes its cluster's docs 4,096 at a time (8 per thread as
 // pass bits: the filter words shifted to the docs), lists the passing ones
-// in LDS in doc order (workgroup scan) and scores them with all threads
-// (16-byte loads of the embedding rows) into the next output slots.  A heavy
-// row is spread over its probes' workgroups.  Memory-bound on the embedding
-// rows read.
+// in LDS in doc order (workgroup scan) and scores them, one doc per lane,
+// the rows staged through LDS with whole-line loads, into the next output
+// slots.  A heavy row is spread over its probes' workgroups.  Memory-bound
+// on the embedding rows read.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -35,8 +35,15 @@
 namespace st {
 namespace {
 
-constexpr int kKmThreads = 1024;
-constexpr int kKmDocsPerThread = 16;  // docs whose pass bits one thread forms per chunk
+constexpr int kKmThreads = 512;
+constexpr int kKmDocsPerThread = 8;  // docs whose pass bits one thread forms per chunk
+// Scoring stages the listed docs' rows through LDS, 64 rows per wave and 64
+// bytes of each row per step (16 rows x 64 contiguous bytes per load
+// instruction); rows padded to 80 bytes so the lanes' 16-byte reads of their
+// own rows fall in distinct banks.
+constexpr int kKmSliceBytes = 64;
+constexpr int kKmStageStride = 80;
+constexpr int kKmAhead = 2;  // staging steps whose loads are in flight
 constexpr int kKmWaves = kKmThreads / 64;
 constexpr int kKmMaxDim = 1280;
 
@@ -109,6 +116,35 @@ __device__ double dot_f64(const void* row, const double* q, int dim) {
     for (; d < dim; ++d) acc = acc + static_cast<double>(elem_f<DT>(row, d)) * q[d];
   }
   return acc;
+}
+
+// Adds the 16-byte piece v of a row, whose first element is d0, to the
+// running dot product: the same operations in the same order as dot_f64 /
+// dot_i8 (so a staged row gives the same bits).
+template <int DT>
+__device__ __forceinline__ void acc_piece(const uint4& v, const double* q, const int8_t* qi, int d0,
+                                          double& acc, int32_t& iacc) {
+#pragma clang fp contract(off)
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  if constexpr (DT == kKmF32) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = acc + static_cast<double>(__uint_as_float(w[j])) * q[d0 + j];
+  } else if constexpr (DT == kKmI8) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      iacc += static_cast<int32_t>(static_cast<int8_t>(w[j / 4] >> (8 * (j % 4)))) *
+              static_cast<int32_t>(qi[d0 + j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint16_t lo = static_cast<uint16_t>(w[j] & 0xFFFFu);
+      const uint16_t hi = static_cast<uint16_t>(w[j] >> 16);
+      const float flo = DT == kKmF16 ? half_to_float(lo) : bf16_to_float(lo);
+      const float fhi = DT == kKmF16 ? half_to_float(hi) : bf16_to_float(hi);
+      acc = acc + static_cast<double>(flo) * q[d0 + 2 * j];
+      acc = acc + static_cast<double>(fhi) * q[d0 + 2 * j + 1];
+    }
+  }
 }
 
 __device__ int32_t dot_i8(const int8_t* row, const int8_t* q, int dim) {
@@ -261,19 +297,19 @@ __global__ __launch_bounds__(kKmCountThreads) void kmean_count_kernel(KmArgs a, 
 
 // DT: embedding dtype; ST: score dtype.  One workgroup per (row, probe):
 // its first output slot is the row's passing docs of the earlier probes
-// (from counts); per chunk of 16,384 docs of the cluster every thread forms
-// the pass bits of 16 docs, the passing docs are listed in LDS in doc order
-// (workgroup scan of the counts), then the whole workgroup scores them, two
-// per thread at a time (independent float64 sums), into the next slots while
-// the row has room.  The row's last probe (or, without probes, the only
+// (from counts); per chunk of 4,096 docs of the cluster every thread forms
+// the pass bits of 8 docs, the passing docs are listed in LDS in doc order
+// (workgroup scan of the counts), then the whole workgroup scores them, one
+// doc per lane, into the next slots while the row has room.  The row's last probe (or, without probes, the only
 // workgroup) writes the padding.
 template <int DT, int ST>
-__global__ __launch_bounds__(kKmThreads) void kmean_ann_kernel(KmArgs a, const int64_t* counts) {
+__global__ __launch_bounds__(kKmThreads) __attribute__((amdgpu_waves_per_eu(4))) void kmean_ann_kernel(KmArgs a, const int64_t* counts) {
   __shared__ double qd[kKmMaxDim];
   __shared__ int8_t qi[kKmMaxDim];
   __shared__ uint32_t wave_sums[kKmWaves];
   __shared__ int64_t base_sum[kKmWaves];
   __shared__ int32_t list[kKmThreads * kKmDocsPerThread];
+  __shared__ __align__(16) char stage[kKmWaves * 64 * kKmStageStride];
   const int64_t nprobes = a.probes > 0 ? a.probes : 1;
   const int64_t b = blockIdx.x / nprobes, p = blockIdx.x % nprobes;
   const int tid = threadIdx.x;
@@ -301,22 +337,91 @@ __global__ __launch_bounds__(kKmThreads) void kmean_ann_kernel(KmArgs a, const i
   for (int w = 0; w < kKmWaves; ++w) written += base_sum[w];
 
   const size_t row_bytes = static_cast<size_t>(dim) * (DT == kKmF32 ? 4 : (DT == kKmI8 ? 1 : 2));
-  auto score = [&](int32_t doc, int64_t slot) {
-    const char* row = static_cast<const char*>(a.embeddings) + static_cast<size_t>(doc) * row_bytes;
-    double f64 = 0.0;
-    int32_t i32 = 0;
+  const char* emb = static_cast<const char*>(a.embeddings);
+  auto finish = [&](int32_t doc, int64_t slot, double f64, int32_t i32) {
     float f32h = 0.f;
     if constexpr (DT == kKmI8) {
-      i32 = dot_i8(reinterpret_cast<const int8_t*>(row), qi, dim);
       if (a.scale != nullptr)
         f32h = static_cast<float>(i32) / half_to_float(a.scale[doc]);
       else if (a.divisor != -1)
         f32h = static_cast<float>(i32) / static_cast<float>(a.divisor);
-    } else {
-      f64 = dot_f64<DT>(row, qd, dim);
     }
     put_score<DT, ST>(a.scores, out0 + slot, f64, i32, f32h);
     a.indices[out0 + slot] = doc;
+  };
+  // Unstaged: each thread reads its own row (rows not 16-byte aligned).
+  auto score = [&](int32_t doc, int64_t slot) {
+    const char* row = emb + static_cast<size_t>(doc) * row_bytes;
+    if constexpr (DT == kKmI8)
+      finish(doc, slot, 0.0, dot_i8(reinterpret_cast<const int8_t*>(row), qi, dim));
+    else
+      finish(doc, slot, dot_f64<DT>(row, qd, dim), 0);
+  };
+  const bool staged = (reinterpret_cast<uintptr_t>(emb) & 15u) == 0 && row_bytes % 16 == 0;
+  // Staged: wave w scores list entries [64 g, 64 g + 64) for g = w, w + 8, ...
+  // lane l the entry 64 g + l.  Step t of the wave = (group t / nslices, 64-byte
+  // slice t % nslices); slices t + 1 .. t + 4 are in flight into registers
+  // while slice t is summed from LDS.  LDS ops of one wave execute in order, so the lanes'
+  // reads see the whole wave's writes and precede the next step's writes.
+  auto score_staged = [&](int64_t m, int64_t slot0) {
+    const int wave = tid >> 6, lane = tid & 63;
+    char* stg = stage + wave * (64 * kKmStageStride);
+    const int pieces = static_cast<int>(row_bytes / 16);
+    const int per_slice = kKmSliceBytes / 16;
+    const int nslices = (pieces + per_slice - 1) / per_slice;
+    const int elems = DT == kKmF32 ? 4 : (DT == kKmI8 ? 16 : 8);  // per piece
+    const int64_t ngroups = (m + 63) / 64;
+    const int64_t mine = ngroups > wave ? (ngroups - wave + kKmWaves - 1) / kKmWaves : 0;
+    const int64_t steps = mine * nslices;
+    const int lr = lane >> 2, lp = lane & 3;  // load: row lr + 16 i, piece lp of the slice
+    auto load = [&](int64_t t, uint4 (&buf)[4]) {
+      const int64_t g = wave + (t / nslices) * kKmWaves;
+      const int pc = static_cast<int>(t % nslices) * per_slice + lp;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t li = g * 64 + lr + 16 * i;
+        buf[i] = li < m && pc < pieces
+                     ? *reinterpret_cast<const uint4*>(emb + static_cast<size_t>(list[li]) * row_bytes +
+                                                       static_cast<size_t>(pc) * 16)
+                     : make_uint4(0u, 0u, 0u, 0u);
+      }
+    };
+    double acc = 0.0;
+    int32_t iacc = 0;
+    uint4 buf[kKmAhead][4];  // steps t .. t + kKmAhead - 1 in flight
+#pragma unroll
+    for (int j = 0; j < kKmAhead; ++j)
+      if (j < steps) load(j, buf[j]);
+    for (int64_t t0 = 0; t0 < steps; t0 += kKmAhead) {
+#pragma unroll
+      for (int j = 0; j < kKmAhead; ++j) {
+        const int64_t t = t0 + j;
+        if (t >= steps) break;
+        const int sl = static_cast<int>(t % nslices);
+        const int64_t li = (wave + (t / nslices) * kKmWaves) * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<uint4*>(stg + (lr + 16 * i) * kKmStageStride + lp * 16) = buf[j][i];
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (t + kKmAhead < steps) load(t + kKmAhead, buf[j]);
+        if (li < m) {
+#pragma unroll
+          for (int q = 0; q < per_slice; ++q) {
+            const int pc = sl * per_slice + q;
+            if (pc < pieces) {
+              const uint4 v = *reinterpret_cast<const uint4*>(stg + lane * kKmStageStride + q * 16);
+              acc_piece<DT>(v, qd, qi, pc * elems, acc, iacc);
+            }
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (sl == nslices - 1) {
+          if (li < m) finish(list[li], slot0 + li, acc, iacc);
+          acc = 0.0;
+          iacc = 0;
+        }
+      }
+    }
   };
   if (a.probes > 0) {
     const KmProbe pr = km_probe(a, b, p);
@@ -333,9 +438,13 @@ __global__ __launch_bounds__(kKmThreads) void kmean_ann_kernel(KmArgs a, const i
       }
       __syncthreads();
       const int64_t m = min<int64_t>(total, a.max_per_row - written);
-      for (int64_t i = tid; i < m; i += 2 * kKmThreads) {
-        score(list[i], written + i);
-        if (i + kKmThreads < m) score(list[i + kKmThreads], written + i + kKmThreads);
+      if (staged) {
+        score_staged(m, written);
+      } else {
+        for (int64_t i = tid; i < m; i += 2 * kKmThreads) {
+          score(list[i], written + i);
+          if (i + kKmThreads < m) score(list[i + kKmThreads], written + i + kKmThreads);
+        }
       }
       written += total;
       __syncthreads();  // the list is refilled by the next chunk
