@@ -346,9 +346,11 @@ int st_filtered_topk(const int64_t* packed, int64_t num_queries,
  * [batch, probes]) that pass the row's filter take consecutive output slots
  * until max_per_row are filled; the rest is padding (score dtype minimum,
  * invalid_index_value).  Filter (optional): int64 filter_mask
- * [*, filter_cols], row filter_index[b] (or b when filter_index is null);
- * doc d passes when bit 63 - d % 64 of word d / 64 is set, or when that word
- * is past filter_cols.  embeddings [total_docs, dim] and queries [batch, dim]
+ * [filter_rows, filter_cols], row filter_index[b] (or b when filter_index is
+ * null; then filter_rows >= batch); doc d passes when bit 63 - d % 64 of
+ * word d / 64 is set, or when that word is past filter_cols.  A
+ * filter_index[b] outside [0, filter_rows) passes no doc (the reference
+ * reads out of bounds there).  embeddings [total_docs, dim] and queries [batch, dim]
  * share emb_dtype: 0 float32, 1 float16, 2 bfloat16, 3 int8.  Scores
  * (st_kmean_ann_score_dtype: the embedding dtype; for int8, int32 (code 4),
  * or float16 when divisor_for_int8 != -1 or per_embedding_scale (float16
@@ -367,8 +369,8 @@ int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_offsets,
                        int64_t batch, int64_t probes, const void* embeddings,
                        int64_t total_docs, int64_t dim, int emb_dtype,
                        const void* queries, int64_t max_per_row,
-                       const int64_t* filter_mask, int64_t filter_cols,
-                       const int64_t* filter_index,
+                       const int64_t* filter_mask, int64_t filter_rows,
+                       int64_t filter_cols, const int64_t* filter_index,
                        const uint16_t* per_embedding_scale,
                        int64_t divisor_for_int8, int64_t invalid_index_value,
                        void* workspace, void* scores, int32_t* indices,

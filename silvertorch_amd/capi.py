@@ -48,7 +48,8 @@ SIGNATURES = {
     "st_kmean_ann_score_dtype": (ctypes.c_int, [ctypes.c_int, _i64, ctypes.c_int]),
     "st_fused_kmean_ann_workspace_bytes": (_i64, [_i64, _i64]),
     "st_fused_kmean_ann": (ctypes.c_int, [_vp, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _i64, ctypes.c_int,
-                                          _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp]),
+                                          _vp, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp,
+                                          _vp]),
     "st_bloom_index_search_batch_counts": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
     "st_search_plan_partial_items": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp,
                                                     _i64p, _i64p]),

@@ -54,8 +54,23 @@ enum KmDtype : int { kKmF32 = 0, kKmF16 = 1, kKmBF16 = 2, kKmI8 = 3, kKmI32 = 4 
 __device__ __forceinline__ float half_to_float(uint16_t h) {
   return __half2float(__ushort_as_half(h));
 }
+// Float32 -> float16, round to nearest even, computed from the float32 bits
+// so that a float64 -> float32 -> float16 chain keeps both roundings (a
+// single float64 -> float16 rounding differs when the float32 value sits on
+// a float16 half-way point).  NaN -> quiet NaN, |f| >= 65520 -> infinity.
 __device__ __forceinline__ uint16_t float_to_half(float f) {
-  return __half_as_ushort(__float2half_rn(f));
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t sign = (u >> 16) & 0x8000u;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return static_cast<uint16_t>(sign | 0x7E00u);
+  if (a >= 0x477FF000u) return static_cast<uint16_t>(sign | 0x7C00u);
+  if (a < 0x38800000u) {
+    // below the smallest normal half: the float32 sum with 0.5 rounds to a
+    // multiple of 2^-24 (the ulp of 0.5), which is the subnormal half's unit
+    const float r = __uint_as_float(a) + 0.5f;
+    return static_cast<uint16_t>(sign | (__float_as_uint(r) - 0x3F000000u));
+  }
+  return static_cast<uint16_t>(sign | ((a + 0xFFFu + ((a >> 13) & 1u) - 0x38000000u) >> 13));
 }
 __device__ __forceinline__ float bf16_to_float(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
@@ -176,6 +191,7 @@ struct KmArgs {
   const void* queries;
   int64_t max_per_row;
   const int64_t* filter_mask;
+  int64_t filter_rows;
   int64_t filter_cols;
   const int64_t* filter_index;
   const uint16_t* scale;  // int8 only: per-doc float16 divisor
@@ -259,10 +275,14 @@ __device__ __forceinline__ KmProbe km_probe(const KmArgs& a, int64_t b, int64_t 
   return KmProbe{len > 0 ? a.cluster_offsets[cid] : 0, len};
 }
 
-__device__ __forceinline__ const int64_t* km_mask_row(const KmArgs& a, int64_t b) {
+// The row's filter words, nullptr without a filter; `none` is set when the
+// row's filter_index names no row of the mask (then no doc passes).
+__device__ __forceinline__ const int64_t* km_mask_row(const KmArgs& a, int64_t b, bool& none) {
+  none = false;
   if (a.filter_mask == nullptr) return nullptr;
   const int64_t frow = a.filter_index != nullptr ? a.filter_index[b] : b;
-  return a.filter_mask + frow * a.filter_cols;
+  none = frow < 0 || frow >= a.filter_rows;
+  return none ? nullptr : a.filter_mask + frow * a.filter_cols;
 }
 
 __device__ __forceinline__ uint64_t chunk_bits(const KmArgs& a, const int64_t* mask, KmProbe pr,
@@ -283,8 +303,10 @@ __global__ __launch_bounds__(kKmCountThreads) void kmean_count_kernel(KmArgs a, 
   if (item >= items) return;
   const int lane = threadIdx.x & 63;
   const int64_t b = item / a.probes, p = item % a.probes;
-  const KmProbe pr = km_probe(a, b, p);
-  const int64_t* mask = km_mask_row(a, b);
+  KmProbe pr = km_probe(a, b, p);
+  bool none;
+  const int64_t* mask = km_mask_row(a, b, none);
+  if (none) pr.len = 0;
   int64_t sum = 0;
   for (int64_t i0 = static_cast<int64_t>(lane) * 64; i0 < pr.len; i0 += 64 * 64) {
     const int n = static_cast<int>(min<int64_t>(pr.len - i0, 64));
@@ -424,8 +446,10 @@ __global__ __launch_bounds__(kKmThreads) __attribute__((amdgpu_waves_per_eu(4)))
     }
   };
   if (a.probes > 0) {
-    const KmProbe pr = km_probe(a, b, p);
-    const int64_t* mask = km_mask_row(a, b);
+    KmProbe pr = km_probe(a, b, p);
+    bool none;
+    const int64_t* mask = km_mask_row(a, b, none);
+    if (none) pr.len = 0;
     for (int64_t base = 0; base < pr.len && written < a.max_per_row; base += kKmChunk) {
       int64_t i0;
       uint64_t bits = chunk_bits(a, mask, pr, base, i0);
@@ -482,8 +506,8 @@ extern "C" int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_of
                                   int64_t batch, int64_t probes, const void* embeddings,
                                   int64_t total_docs, int64_t dim, int emb_dtype,
                                   const void* queries, int64_t max_per_row,
-                                  const int64_t* filter_mask, int64_t filter_cols,
-                                  const int64_t* filter_index,
+                                  const int64_t* filter_mask, int64_t filter_rows,
+                                  int64_t filter_cols, const int64_t* filter_index,
                                   const uint16_t* per_embedding_scale, int64_t divisor_for_int8,
                                   int64_t invalid_index_value, void* workspace, void* scores,
                                   int32_t* indices, void* stream) {
@@ -500,7 +524,10 @@ extern "C" int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_of
     ST_CHECK(probes == 0 || (cluster_ids != nullptr && cluster_length != nullptr &&
                              cluster_offsets != nullptr),
              "null cluster arrays");
-    ST_CHECK(filter_mask == nullptr || filter_cols >= 0, "negative filter mask width");
+    ST_CHECK(filter_mask == nullptr || (filter_cols >= 0 && filter_rows >= 0),
+             "negative filter mask shape");
+    ST_CHECK(filter_mask == nullptr || filter_index != nullptr || filter_rows >= batch,
+             "filter mask has ", filter_rows, " rows for ", batch, " queries");
     KmArgs a;
     a.cluster_offsets = cluster_offsets;
     a.num_offsets = num_offsets;
@@ -513,6 +540,7 @@ extern "C" int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_of
     a.queries = queries;
     a.max_per_row = max_per_row;
     a.filter_mask = filter_mask;
+    a.filter_rows = filter_rows;
     a.filter_cols = filter_cols;
     a.filter_index = filter_index;
     a.scale = emb_dtype == kKmI8 ? per_embedding_scale : nullptr;

@@ -701,12 +701,9 @@ std::tuple<Tensor, Tensor> kmean_gpu(const Tensor& cluster_offsets_in, const Ten
   Tensor scores = at::empty({B, width}, opts.dtype(km_score_type(score_code)));
   Tensor indices = at::empty({B, width}, opts.dtype(at::kInt));
   if (B == 0 || width == 0) return {scores, indices};
-  if (mask.defined() && findex.defined()) {
-    // rows of the mask named by filtering_bit_index must exist
-    const Tensor bad = (findex < 0).logical_or(findex >= mask.size(0)).any();
-    TORCH_CHECK(!bad.item<bool>(), "filtering_bit_index names a row outside filtering_bit_mask (",
-                mask.size(0), " rows)");
-  } else if (mask.defined()) {
+  // a filtering_bit_index entry outside the mask's rows passes no doc (checked
+  // on the device: no host wait)
+  if (mask.defined() && !findex.defined()) {
     TORCH_CHECK(mask.size(0) >= B, "filtering_bit_mask has ", mask.size(0), " rows for ", B,
                 " queries");
   }
@@ -718,7 +715,7 @@ std::tuple<Tensor, Tensor> kmean_gpu(const Tensor& cluster_offsets_in, const Ten
                               emb.numel() ? emb.data_ptr() : nullptr, emb.size(0), emb.size(1), code,
                               q.data_ptr(), width,
                               mask.defined() && mask.numel() ? mask.data_ptr<int64_t>() : nullptr,
-                              mask.defined() ? mask.size(1) : 0,
+                              mask.defined() ? mask.size(0) : 0, mask.defined() ? mask.size(1) : 0,
                               findex.defined() ? findex.data_ptr<int64_t>() : nullptr,
                               has_scale ? reinterpret_cast<const uint16_t*>(scale.data_ptr()) : nullptr,
                               divisor_for_int8, invalid_index_value, ws.data_ptr(),

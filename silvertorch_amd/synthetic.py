@@ -170,6 +170,35 @@ def make_queries(cspec: CorpusSpec, qspec: QuerySpec, seed: int = 0) -> list[str
     return out
 
 
+DIGEST_CHUNK = 1 << 26
+
+
+def digest(a: np.ndarray) -> str:
+    """sha256 over the sha256 digests of the array's bytes in 64 MiB pieces
+    (hashed on a thread pool), so multi-GB outputs are digested in seconds;
+    the same rule is applied to the reference's outputs and to this build's."""
+    import hashlib
+
+    buf = memoryview(np.ascontiguousarray(a).reshape(-1).view(np.uint8))
+    pieces = [buf[i:i + DIGEST_CHUNK] for i in range(0, len(buf), DIGEST_CHUNK)] or [buf]
+    workers = max(1, min(16, os.cpu_count() or 1, len(pieces)))
+    with ThreadPoolExecutor(workers) as ex:
+        parts = list(ex.map(lambda p: hashlib.sha256(p).digest(), pieces))
+    return hashlib.sha256(b"".join(parts)).hexdigest()
+
+
+def match_counts(packed: np.ndarray, num_docs: int) -> list[int]:
+    """Per query, the set bits of a packed [Q, C] search output among docs
+    d < num_docs (doc d at bit 63 - d % 64 of word d / 64)."""
+    words = np.ascontiguousarray(packed).view(np.uint64)
+    full, rest = divmod(num_docs, 64)
+    out = [int(v) for v in np.bitwise_count(words[:, :full]).sum(axis=1, dtype=np.int64)]
+    if rest:
+        tail = words[:, full] >> np.uint64(64 - rest)
+        out = [c + int(t) for c, t in zip(out, np.bitwise_count(tail))]
+    return out
+
+
 def make_corpus_device(spec: CorpusSpec, seed: int = 0, num_docs: int | None = None,
                        device: str = "cuda", chunk: int = 1 << 26):
     """Large-scale corpus drawn on the device with a seeded torch generator

@@ -106,7 +106,7 @@ def _kmean_npz():
     return dict(np.load(GOLDEN / "ref_kmean.npz", allow_pickle=False))
 
 
-KMEAN_CASES = ["readme", "f32_trunc", "f16", "bf16", "i8_raw", "i8_div", "i8_scale", "f32_odd_dim",
+KMEAN_CASES = ["readme", "f32_trunc", "f16", "f16_halfway", "bf16", "i8_raw", "i8_div", "i8_scale", "f32_odd_dim",
                "f32_filter", "bf16_filter_index"]
 
 

@@ -445,6 +445,35 @@ def kmean_fixtures() -> None:
     for c in range(2):
         out[f"multiple/{c}/scores"] = ms[0][c].numpy()
         out[f"multiple/{c}/indices"] = ms[1][c].numpy()
+
+    # float16 rounding: the reference rounds float64 -> float32 -> float16
+    # (fused_kmean_ann.cpp:214).  Query (1, 1, 2^-10); each doc's exact sum:
+    # 1 + 2^-11 (a half-way point, ties to 1.0), 1 + 2^-11 + 2^-34 (float32
+    # rounds it onto the half-way point -> 1.0; one float64 -> float16
+    # rounding gives 1 + 2^-10), 1 + 2^-11 + 2^-22 (above it), 1 + 3*2^-11
+    # (ties to even upwards), the negation of the second, 2^-24 and 3*2^-24
+    # (subnormal; halved by the second query's 0.5 they become ties), 65519
+    # and 65520 (largest finite / infinity).
+    t = 2.0 ** -11
+    rows = [[1, t, 0], [1, t, 2.0 ** -24], [1, t, 2.0 ** -12], [1 + 2 * t, t, 0], [-1, -t, -(2.0 ** -24)],
+            [2.0 ** -24, 0, 0], [3 * 2.0 ** -24, 0, 0], [65504, 15, 0], [65504, 16, 0]]
+    e = torch.tensor(rows, dtype=torch.float64).to(torch.float16)
+    assert torch.equal(e.double(), torch.tensor(rows, dtype=torch.float64)), "rows must be exact in float16"
+    q = torch.tensor([[1.0, 1.0, 2.0 ** -10], [0.5, 1.0, 2.0 ** -10]], dtype=torch.float16)
+    offs = np.array([0, len(rows)], np.int64)
+    cids = np.zeros((2, 1), np.int64)
+    clen = np.full((2, 1), len(rows), np.int64)
+    sc_, ix_ = st.fused_kmean_ann(torch.from_numpy(offs), torch.from_numpy(cids), torch.from_numpy(clen),
+                                  e, q, 32)
+    name = "f16_halfway"
+    out[f"{name}/cluster_offsets"] = offs
+    out[f"{name}/cluster_ids"] = cids
+    out[f"{name}/cluster_length"] = clen
+    out[f"{name}/embeddings"] = e.numpy()
+    out[f"{name}/queries"] = q.numpy()
+    out[f"{name}/params"] = np.array([32, -1, -1], np.int64)
+    out[f"{name}/scores"] = sc_.numpy()
+    out[f"{name}/indices"] = ix_.numpy()
     np.savez_compressed(HERE / "ref_kmean.npz", **out)
     print("fused_kmean_ann fixtures written to", HERE / "ref_kmean.npz")
 

@@ -108,20 +108,16 @@ def _random_case(rng, dim, dtype, batch, probes, max_size, filtered=False, clust
                 embeddings=emb, queries=q, max_size=max_size, mask=mask, bf16=dtype == "bfloat16")
 
 # dims 40 (bf16) and 20 (f32): 80-byte rows, a partial last 64-byte staging
-# slice; maxlen 12000: clusters longer than one 4,096-doc pass-bit chunk
-_UNRUN = pytest.mark.skip(reason="added without a GPU run yet; enable once run on the GPU")
-_ULP = pytest.mark.skip(reason="one float16 score 1 ulp off the oracle (1 of 52,416) on this seed; "
-                               "cause not yet found, the kernel's and the oracle's operation order agree")
+# slice; maxlen 12000: clusters longer than one 4,096-doc pass-bit chunk;
+# seed 2571: a float64 sum that float32 rounds onto a float16 half-way point
 @pytest.mark.parametrize("dim,dtype,filtered,divisor,maxlen,seed", [
     (128, "float32", False, -1, 2500, None), (1280, "float32", True, -1, 2500, None),
     (17, "float32", True, -1, 2500, None), (64, "float16", True, -1, 2500, None),
     (256, "bfloat16", False, -1, 2500, None), (96, "bfloat16", True, -1, 2500, None),
     (32, "int8", False, -1, 2500, None), (128, "int8", True, 13, 2500, None),
-    pytest.param(64, "float16", True, -1, 2500, 2571, marks=_ULP),
-    pytest.param(40, "bfloat16", True, -1, 2500, None, marks=_UNRUN),
-    pytest.param(20, "float32", False, -1, 2500, None, marks=_UNRUN),
-    pytest.param(64, "bfloat16", True, -1, 12000, None, marks=_UNRUN),
-    pytest.param(48, "float32", False, -1, 12000, None, marks=_UNRUN)])
+    (64, "float16", True, -1, 2500, 2571), (40, "bfloat16", True, -1, 2500, None),
+    (20, "float32", False, -1, 2500, None), (64, "bfloat16", True, -1, 12000, None),
+    (48, "float32", False, -1, 12000, None)])
 def test_random_vs_oracle(dim, dtype, filtered, divisor, maxlen, seed):
     rng = np.random.default_rng(dim + len(dtype) if seed is None else seed)
     long_clusters = maxlen > 2500
@@ -191,6 +187,21 @@ def test_edge_cases():
     sc, ix = st.fused_kmean_ann(offs, _t(np.array([[1]], np.int64))[:, :1].expand(2, 1).contiguous(),
                                 _t(np.array([[3], [3]], np.int64)), emb, q, 0)
     assert sc.shape == (2, 0) and ix.shape == (2, 0)
+    # a filtering_bit_index row outside the mask passes no doc; a valid one
+    # filters as that row of the mask does
+    mask = _t(np.array([[-1, -1]], np.int64))
+    sc, ix = st.fused_kmean_ann(offs, _t(np.array([[1], [1]], np.int64)), _t(np.array([[30], [30]], np.int64)),
+                                emb, q, 40, filtering_bit_mask=mask,
+                                filtering_bit_index=_t(np.array([3, 0], np.int64)))
+    assert (ix.cpu()[0] == -1).all()
+    np.testing.assert_array_equal(ix.cpu().numpy()[1, :31], list(range(20, 50)) + [-1])
+    sc, ix = st.fused_kmean_ann(offs, _t(np.array([[1], [1]], np.int64)), _t(np.array([[30], [30]], np.int64)),
+                                emb, q, 40, filtering_bit_mask=mask,
+                                filtering_bit_index=_t(np.array([-1, 0], np.int64)))
+    assert (ix.cpu()[0] == -1).all() and ix.cpu()[1, 0] == 20
+    with pytest.raises(RuntimeError):  # two queries, one mask row, no index
+        st.fused_kmean_ann(offs, _t(np.array([[1], [1]], np.int64)), _t(np.array([[3], [3]], np.int64)),
+                           emb, q, 40, filtering_bit_mask=mask)
     with pytest.raises(RuntimeError):
         st.fused_kmean_ann(offs, _t(np.zeros((2, 1), np.int64)), _t(np.zeros((3, 1), np.int64)), emb, q, 5)
     with pytest.raises(RuntimeError):
@@ -212,14 +223,14 @@ def test_c_abi_direct():
     ws = torch.empty(L.st_fused_kmean_ann_workspace_bytes(B, P_), dtype=torch.uint8, device="cuda")
     capi.check(L.st_fused_kmean_ann(offs.data_ptr(), offs.numel(), cids.data_ptr(), clen.data_ptr(), B, P_,
                                     emb.data_ptr(), emb.shape[0], emb.shape[1], 3, q.data_ptr(), width,
-                                    None, 0, None, None, c["divisor"], c["invalid"], ws.data_ptr(),
+                                    None, 0, 0, None, None, c["divisor"], c["invalid"], ws.data_ptr(),
                                     sc.data_ptr(), ix.data_ptr(), stream))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(ix.cpu().numpy(), c["indices"])
     np.testing.assert_array_equal(_bits(sc), c["scores"].view(np.uint16))
     # a dim outside [1, 1280] is rejected before any launch
     rc = L.st_fused_kmean_ann(offs.data_ptr(), offs.numel(), cids.data_ptr(), clen.data_ptr(), B, P_,
-                              emb.data_ptr(), emb.shape[0], 2048, 3, q.data_ptr(), width, None, 0, None,
+                              emb.data_ptr(), emb.shape[0], 2048, 3, q.data_ptr(), width, None, 0, 0, None,
                               None, c["divisor"], c["invalid"], ws.data_ptr(), sc.data_ptr(), ix.data_ptr(),
                               stream)
     assert rc != 0 and b"dim" in L.st_last_error()

@@ -313,6 +313,24 @@ def test_kmean_oracle_matches_reference(name):
         np.testing.assert_array_equal(sc.view(np.uint8), c["scores"].view(np.uint8))
 
 
+def test_kmean_halfway_fixture_catches_single_rounding():
+    """The f16_halfway fixture separates the reference's float64 -> float32 ->
+    float16 chain (fused_kmean_ann.cpp:214) from one direct float64 -> float16
+    rounding: a planted single rounding of the exact sums differs from the
+    fixture, the double rounding equals it."""
+    c = G.kmean_case("f16_halfway")
+    e = c["embeddings"].astype(np.float64)
+    q = c["queries"].astype(np.float64)
+    exact = q @ e.T  # the sums are exact in float64 here
+    n = e.shape[0]
+    with np.errstate(over="ignore"):
+        double = exact.astype(np.float32).astype(np.float16)
+        single = exact.astype(np.float16)
+    np.testing.assert_array_equal(double.view(np.uint16), c["scores"][:, :n].view(np.uint16))
+    assert not np.array_equal(single.view(np.uint16), c["scores"][:, :n].view(np.uint16))
+    assert c["scores"][0, 1].view(np.uint16) == 0x3C00 and single[0, 1].view(np.uint16) == 0x3C01
+
+
 def test_kmean_oracle_partial_wrappers_match_reference():
     """The partial-mask wrappers of the reference CPU op score every doc of the
     selected clusters (the masks are ignored): the unfiltered oracle equals
