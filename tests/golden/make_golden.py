@@ -22,6 +22,8 @@ Sources of truth, neither of which is this repository's code:
                         per-embedding scale, truncated rows, filtered rows.
 
 Usage:  python tests/golden/make_golden.py [partial|kmean]   (only that file)
+        python tests/golden/make_golden.py full [cfg2 cfg5 cfg4 ...]
+                (ref_full_digests.json: full-size configurations, minutes)
 The reference library registers torch.ops.st.*, so this script never imports
 silvertorch_amd.
 """
@@ -478,11 +480,64 @@ def kmean_fixtures() -> None:
     print("fused_kmean_ann fixtures written to", HERE / "ref_kmean.npz")
 
 
+def full_digests(names: list[str]) -> None:
+    """ref_full_digests.json: the benchmark configurations at full size,
+    built and searched by the reference's CPU ops on the numpy-generated
+    corpora (silvertorch_amd.synthetic.make_corpus / make_queries, seed 0):
+    digests (synthetic.digest) of the inputs, bundle_b_offsets, bloom_index,
+    the plan bytes and the packed search output, and the per-query match
+    counts.  cfg4 is a build-only configuration."""
+    import torch
+
+    from silvertorch_amd import synthetic as S
+
+    ref = ROOT / "oracle" / "_ref" / "libst_ref.so"
+    if not ref.exists():
+        subprocess.run(["make", "-C", str(ROOT / "oracle"), "ref"], check=True)
+    torch.ops.load_library(str(ref))
+    st = torch.ops.st
+    path = HERE / "ref_full_digests.json"
+    out = json.loads(path.read_text()) if path.exists() else {}
+    for name in names:
+        import time
+
+        t0 = time.time()
+        cspec, qspec = S.CONFIGS[name]
+        corp = S.make_corpus(cspec, seed=0)
+        rec = {"seed": 0, "num_docs": cspec.num_docs, "num_values": int(corp.feature_values.size),
+               "inputs": {"offsets": S.digest(corp.feature_offsets), "values": S.digest(corp.feature_values)}}
+        print(f"{name}: corpus {time.time() - t0:.0f}s", flush=True)
+        bi, bo = st.bloom_index_build(torch.from_numpy(corp.feature_ids), torch.from_numpy(corp.feature_offsets),
+                                      torch.from_numpy(corp.feature_values), cspec.b_multiplier, cspec.k)
+        del corp
+        print(f"{name}: reference build {time.time() - t0:.0f}s", flush=True)
+        rec.update(index=S.digest(bi.numpy()), index_len=int(bi.numel()),
+                   bundle_b_offsets=S.digest(bo.numpy()), bundles=int(bo.numel() - 1),
+                   bundle_b_offsets_head=bo[:4].tolist(), bundle_b_offsets_last=int(bo[-1]))
+        if qspec is not None:
+            queries = S.make_queries(cspec, qspec, seed=0)
+            _, (pd, po) = st.parse_expression_query_batch(queries, torch.ones(1, dtype=torch.long),
+                                                          cspec.hash_k, True, 5)
+            packed = st.bloom_index_search_batch(bi, bo, pd, po, cspec.k, cspec.hash_k, False).numpy()
+            print(f"{name}: reference search {time.time() - t0:.0f}s", flush=True)
+            rec.update(queries_sha256=hashlib.sha256("\n".join(queries).encode()).hexdigest(),
+                       plans_data=S.digest(pd.numpy()), plans_offsets=S.digest(po.numpy()),
+                       packed=S.digest(packed), packed_shape=list(packed.shape),
+                       match_counts=S.match_counts(packed, cspec.num_docs))
+            del packed
+        out[name] = rec
+        del bi, bo
+        path.write_text(json.dumps(out, indent=1))
+        print(f"{name} written to {path} ({time.time() - t0:.0f}s)", flush=True)
+
+
 if __name__ == "__main__":
     if sys.argv[1:] == ["partial"]:
         partial_fixtures()
     elif sys.argv[1:] == ["kmean"]:
         kmean_fixtures()
+    elif sys.argv[1:2] == ["full"]:
+        full_digests(sys.argv[2:] or ["cfg2", "cfg5", "cfg4"])
     else:
         main()
         partial_fixtures()

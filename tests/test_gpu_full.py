@@ -1,0 +1,174 @@
+"""Full-size parity of the benchmark configurations against the reference's
+own CPU ops: the corpora are regenerated with the seeded numpy generator
+(silvertorch_amd.synthetic, seed 0), built and searched on the GPU through
+torch.ops.st, and every output compared with the digests the reference CPU
+build and search (bloom_indexer.cpp:26-113, bloom_index_search.cpp:173-243)
+wrote for the same inputs (tests/golden/ref_full_digests.json, written by
+tests/golden/make_golden.py full):
+
+* cfg2 (the headline: 10M docs x 256 queries) and cfg5 (20M docs x 512
+  queries): input digests (the generator itself), bundle_b_offsets,
+  bloom_index, plan bytes, the packed search output, per-query match counts;
+  the bool output equals the packed words bit for bit; the CSR row offsets of
+  the ids op are the running sums of the reference's match counts;
+* cfg4 (100M docs, build only): input digests, bundle_b_offsets and the
+  5.9 GB bloom_index;
+* cfg5's fused search + filtered top-k on a doc prefix of its corpus, its
+  512 queries and seeded embeddings, against the oracle's fp64 top-k under
+  the stated tolerance (ids equal except swaps between scores within 1e-3
+  relative; scores within 1e-3 of the fp64 score of the returned id).
+"""
+
+from __future__ import annotations
+
+import json
+import time
+from functools import lru_cache
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from silvertorch_amd import synthetic as S
+from tests import gpu_helpers as H
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+@lru_cache(None)
+def _digests() -> dict:
+    return json.loads((GOLDEN / "ref_full_digests.json").read_text())
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _ops():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a HIP device")
+    import silvertorch_amd.ops._load_ops  # noqa: F401
+
+
+def _corpus_on_device(cfg: str, t0: float):
+    cspec, _ = S.CONFIGS[cfg]
+    d = _digests()[cfg]
+    H.note(f"[full] {cfg}: generating {cspec.num_docs} docs")
+    corp = S.make_corpus(cspec, seed=0)
+    assert corp.feature_values.size == d["num_values"], "the generator drew another corpus"
+    assert S.digest(corp.feature_offsets) == d["inputs"]["offsets"], "feature_offsets differ from the reference's"
+    assert S.digest(corp.feature_values) == d["inputs"]["values"], "feature_values differ from the reference's"
+    H.note(f"[full] {cfg}: corpus of {corp.feature_values.size} values equals the reference's inputs "
+           f"({time.time() - t0:.0f}s)")
+    dev = torch.device("cuda:0")
+    ids = torch.from_numpy(corp.feature_ids).to(dev)
+    offs = torch.from_numpy(corp.feature_offsets).to(dev)
+    vals = torch.from_numpy(corp.feature_values).to(dev)
+    del corp
+    return cspec, ids, offs, vals
+
+
+def _check_build(cfg: str, bi: torch.Tensor, bo: torch.Tensor, t0: float) -> None:
+    d = _digests()[cfg]
+    bo_h = bo.cpu().numpy()
+    assert bo.numel() - 1 == d["bundles"] and int(bo_h[-1]) == d["bundle_b_offsets_last"]
+    assert bo_h[:4].tolist() == d["bundle_b_offsets_head"]
+    assert S.digest(bo_h) == d["bundle_b_offsets"], "bundle_b_offsets differ from the reference build"
+    assert bi.numel() == d["index_len"]
+    assert S.digest(bi.cpu().numpy()) == d["index"], "bloom_index differs from the reference build"
+    H.note(f"[full] {cfg}: bundle_b_offsets and the {bi.numel() * 8 / 1e9:.2f} GB bloom_index equal the "
+           f"reference's ({time.time() - t0:.0f}s)")
+
+
+def _bool_equals_packed(boolm: torch.Tensor, packed: torch.Tensor) -> bool:
+    """bool[Q, 64 C] == the packed words (doc 64 c + i at bit 63 - i of word
+    c), on the device, 16 queries at a time."""
+    Q, C = packed.shape
+    w = torch.tensor([128, 64, 32, 16, 8, 4, 2, 1], dtype=torch.uint8, device=packed.device)
+    for q0 in range(0, Q, 16):
+        q1 = min(Q, q0 + 16)
+        b = boolm[q0:q1].view(torch.uint8).view(q1 - q0, C, 8, 8)
+        be = (b * w).sum(-1, dtype=torch.uint8)  # big-endian bytes of each word
+        want = packed[q0:q1].contiguous().view(torch.uint8).view(q1 - q0, C, 8).flip(-1)
+        if not torch.equal(be, want):
+            return False
+    return True
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("cfg", ["cfg2", "cfg5"])
+def test_full_size_build_and_search_vs_reference(cfg):
+    t0 = time.time()
+    cspec, ids, offs, vals = _corpus_on_device(cfg, t0)
+    _, qspec = S.CONFIGS[cfg]
+    st = torch.ops.st
+    d = _digests()[cfg]
+    bi, bo = st.bloom_index_build(ids, offs, vals, cspec.b_multiplier, cspec.k)
+    torch.cuda.synchronize()
+    del ids, offs, vals
+    _check_build(cfg, bi, bo, t0)
+
+    queries = S.make_queries(cspec, qspec, seed=0)
+    import hashlib
+
+    assert hashlib.sha256("\n".join(queries).encode()).hexdigest() == d["queries_sha256"]
+    _, (pd, po) = st.parse_expression_query_batch(queries, torch.ones(1, dtype=torch.long), cspec.hash_k, True, 5)
+    assert S.digest(pd.numpy()) == d["plans_data"] and S.digest(po.numpy()) == d["plans_offsets"], \
+        "plan bytes differ from the reference parser's"
+    packed = st.bloom_index_search_batch(bi, bo, pd, po, cspec.k, cspec.hash_k, False)
+    torch.cuda.synchronize()
+    assert list(packed.shape) == d["packed_shape"]
+    got = packed.cpu().numpy()
+    counts = S.match_counts(got, cspec.num_docs)
+    bad = [q for q, (a, b) in enumerate(zip(counts, d["match_counts"])) if a != b]
+    assert not bad, f"match counts differ from the reference's for queries {bad[:10]}"
+    assert S.digest(got) == d["packed"], "packed search output differs from the reference's"
+    del got
+    H.note(f"[full] {cfg}: packed output {list(packed.shape)} of {len(queries)} queries equals the reference's "
+           f"({time.time() - t0:.0f}s)")
+
+    boolm = st.bloom_index_search_batch(bi, bo, pd, po, cspec.k, cspec.hash_k, True)
+    assert boolm.dtype == torch.bool and boolm.shape == (packed.shape[0], packed.shape[1] * 64)
+    assert _bool_equals_packed(boolm, packed), "bool output differs from the packed words"
+    del boolm
+    ids_out, ro = st.bloom_index_search_batch_ids(bi, bo, pd, po, cspec.k, cspec.hash_k, cspec.num_docs)
+    want_ro = np.concatenate([[0], np.cumsum(d["match_counts"])])
+    np.testing.assert_array_equal(ro.cpu().numpy(), want_ro)
+    assert ids_out.numel() == want_ro[-1]
+    H.note(f"[full] {cfg}: bool output and CSR row offsets agree ({time.time() - t0:.0f}s)")
+
+
+@pytest.mark.timeout(900)
+def test_full_size_cfg4_build_vs_reference():
+    t0 = time.time()
+    cspec, ids, offs, vals = _corpus_on_device("cfg4", t0)
+    bi, bo = torch.ops.st.bloom_index_build(ids, offs, vals, cspec.b_multiplier, cspec.k)
+    torch.cuda.synchronize()
+    del ids, offs, vals
+    _check_build("cfg4", bi, bo, t0)
+
+
+@pytest.mark.timeout(600)
+def test_cfg5_search_topk_prefix_vs_oracle():
+    """bloom_index_search_topk on cfg5's corpus (its first 131,072 docs), its
+    512 three-term AND/OR filters and bf16[128] embeddings (docs N(0, 1/128),
+    queries N(0, 1), seeded numpy), top-100, against the oracle."""
+    from tests.test_gpu_topk import _check
+
+    cspec, qspec = S.CONFIGS["cfg5"]
+    n, dim, topk = 131072, 128, 100
+    corp = S.make_corpus(cspec, seed=0, num_docs=n)
+    queries = S.make_queries(cspec, qspec, seed=0)
+    emb, qv = S.make_embeddings(n, dim, len(queries), seed=0)
+    H.note(f"[full] cfg5 top-k: {n} docs x {len(queries)} queries, bf16[{dim}], top-{topk}")
+    st = torch.ops.st
+    dev = torch.device("cuda:0")
+    bi, bo = st.bloom_index_build(torch.from_numpy(corp.feature_ids).to(dev),
+                                  torch.from_numpy(corp.feature_offsets).to(dev),
+                                  torch.from_numpy(corp.feature_values).to(dev), cspec.b_multiplier, cspec.k)
+    _, (pd, po) = st.parse_expression_query_batch(queries, torch.ones(1, dtype=torch.long), cspec.hash_k, True, 5)
+    ids, sc = st.bloom_index_search_topk(bi, bo, pd, po, cspec.k, cspec.hash_k, emb.to(dev), qv.to(dev), n, topk)
+    packed = st.bloom_index_search_batch(bi, bo, pd, po, cspec.k, cspec.hash_k, False).cpu().numpy()
+    passing = sum(S.match_counts(packed, n))
+    H.note(f"[full] cfg5 top-k: {passing} passing doc-query pairs; checking against the oracle")
+    _check(ids.cpu().numpy(), sc.cpu().numpy(), emb.float().numpy(), qv.float().numpy(), packed, n, topk)

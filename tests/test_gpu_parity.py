@@ -313,18 +313,29 @@ def test_ops_column_info():  # test_bloom_index_search.py:216-241
     assert counts.cpu().tolist() == want_c and starts.cpu().tolist() == want_s and firsts.cpu().tolist() == want_f
 
 
-@pytest.mark.parametrize("cfg,docs", [("cfg1", 30000), ("cfg2", 40000), ("cfg3", 12000), ("cfg5", 30000)])
+@pytest.mark.parametrize("cfg,docs", [("cfg1", 30000), ("cfg2", 40000), ("cfg3", 12000), ("cfg4", 30000),
+                                      ("cfg5", 30000)])
 def test_config_shapes_vs_oracle(cfg, docs):
     """The benchmark configurations' corpus and query distributions
     (silvertorch_amd.synthetic) at reduced doc counts: the
     same feature counts, value distributions, k / hash_k / B_MULTIPLIER and
     query shapes (cfg3: bundles wider than the LDS tile, k = 4, boolean trees
-    with NOT), build and search bit-exact against the oracle."""
+    with NOT; cfg4, a build-only configuration: uniform values over 10M and
+    1-8 values per feature, searched with flat queries of 1-4 terms drawn
+    from its value distribution), build and search bit-exact against the
+    oracle."""
     from silvertorch_amd import synthetic as S
 
     cspec, qspec = S.CONFIGS[cfg]
+    if qspec is None:
+        qspec = S.QuerySpec(64, "flat", 1, 4)
     corp = S.make_corpus(cspec, seed=0, num_docs=docs)
     queries = S.make_queries(cspec, qspec, seed=0)
+    if cfg == "cfg4":  # terms of docs in the corpus, so that queries match
+        rng = np.random.default_rng(4)
+        d = rng.integers(0, docs, 32)
+        queries += [f"{f + 1}:{int(corp.feature_values[corp.feature_offsets[x * 4 + f]])}"
+                    for x, f in zip(d, rng.integers(0, 4, 32))]
     H.note(f"[config] {cfg} docs={docs} queries={len(queries)} k={cspec.k} bm={cspec.b_multiplier}")
     index, bbo = H.build(corp.feature_ids, corp.feature_offsets, corp.feature_values, cspec.b_multiplier, cspec.k)
     want_index, want_bbo = O.bloom_build(corp.feature_ids, corp.feature_offsets, corp.feature_values,
