@@ -376,6 +376,33 @@ int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_offsets,
                        void* workspace, void* scores, int32_t* indices,
                        void* stream);
 
+/* ---------------------------------------------------------------------------
+ * st_fused_kmean_ann without allocation.  No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as st_fused_kmean_ann minus `workspace`: the
+ * per-(row, probe) counts go to a fixed device array of the library, one
+ * copy per GPU (8 MiB, held until the process ends), so batch x probes must
+ * not exceed ST_KMEAN_NOALLOC_MAX_PAIRS (larger calls are rejected before
+ * any launch).  The device current on the calling thread must be the one
+ * the buffers and the stream belong to.  Allocates nothing (no hipMalloc,
+ * hipFree or allocating library call).  Calls that overlap on one GPU share
+ * the array and race: serialise them (one stream, or events).
+ * ------------------------------------------------------------------------- */
+#define ST_KMEAN_NOALLOC_MAX_PAIRS (1 << 20)
+int st_fused_kmean_ann_noalloc(const int64_t* cluster_offsets, int64_t num_offsets,
+                               const int64_t* cluster_ids,
+                               const int64_t* cluster_length, int64_t batch,
+                               int64_t probes, const void* embeddings,
+                               int64_t total_docs, int64_t dim, int emb_dtype,
+                               const void* queries, int64_t max_per_row,
+                               const int64_t* filter_mask, int64_t filter_rows,
+                               int64_t filter_cols, const int64_t* filter_index,
+                               const uint16_t* per_embedding_scale,
+                               int64_t divisor_for_int8,
+                               int64_t invalid_index_value, void* scores,
+                               int32_t* indices, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

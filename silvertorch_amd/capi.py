@@ -50,6 +50,9 @@ SIGNATURES = {
     "st_fused_kmean_ann": (ctypes.c_int, [_vp, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _i64, ctypes.c_int,
                                           _vp, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp,
                                           _vp]),
+    "st_fused_kmean_ann_noalloc": (ctypes.c_int, [_vp, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _i64, ctypes.c_int,
+                                                  _vp, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp,
+                                                  _vp]),
     "st_bloom_index_search_batch_counts": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
     "st_search_plan_partial_items": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp,
                                                     _i64p, _i64p]),

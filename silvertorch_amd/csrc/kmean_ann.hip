@@ -29,6 +29,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <mutex>
 
 #include "st_errors.hpp"
 
@@ -501,6 +502,84 @@ extern "C" int64_t st_fused_kmean_ann_workspace_bytes(int64_t batch, int64_t pro
   return batch > 0 && probes > 0 ? batch * probes * static_cast<int64_t>(sizeof(int64_t)) : 0;
 }
 
+namespace st {
+namespace {
+
+// Validates the arguments, fills KmArgs and launches both kernels with
+// `counts` (batch x probes int64) as the per-(row, probe) count buffer;
+// `counts_capacity` (items) bounds it, -1 = unchecked (caller-sized).
+void kmean_run(const int64_t* cluster_offsets, int64_t num_offsets, const int64_t* cluster_ids,
+               const int64_t* cluster_length, int64_t batch, int64_t probes, const void* embeddings,
+               int64_t total_docs, int64_t dim, int emb_dtype, const void* queries, int64_t max_per_row,
+               const int64_t* filter_mask, int64_t filter_rows, int64_t filter_cols,
+               const int64_t* filter_index, const uint16_t* per_embedding_scale, int64_t divisor_for_int8,
+               int64_t invalid_index_value, int64_t* counts, int64_t counts_capacity, void* scores,
+               int32_t* indices, void* stream) {
+  ST_CHECK(batch >= 0 && probes >= 0 && total_docs >= 0 && max_per_row >= 0 && num_offsets >= 0,
+           "negative sizes");
+  ST_CHECK(dim >= 1 && dim <= kKmMaxDim, "embedding dim must be in [1, ", kKmMaxDim, "], got ", dim);
+  ST_CHECK(emb_dtype >= kKmF32 && emb_dtype <= kKmI8, "unsupported embedding dtype code ", emb_dtype);
+  if (batch == 0 || max_per_row == 0) return;
+  ST_CHECK(counts_capacity < 0 || probes == 0 || batch <= counts_capacity / probes,
+           "batch x probes = ", batch, " x ", probes, " exceeds the ", counts_capacity,
+           " (row, probe) pairs of the no-allocation entry point's scratch");
+  ST_CHECK(scores != nullptr && indices != nullptr && queries != nullptr, "null device pointer");
+  ST_CHECK(probes == 0 || (cluster_ids != nullptr && cluster_length != nullptr &&
+                           cluster_offsets != nullptr),
+           "null cluster arrays");
+  ST_CHECK(filter_mask == nullptr || (filter_cols >= 0 && filter_rows >= 0),
+           "negative filter mask shape");
+  ST_CHECK(filter_mask == nullptr || filter_index != nullptr || filter_rows >= batch,
+           "filter mask has ", filter_rows, " rows for ", batch, " queries");
+  KmArgs a;
+  a.cluster_offsets = cluster_offsets;
+  a.num_offsets = num_offsets;
+  a.cluster_ids = cluster_ids;
+  a.cluster_length = cluster_length;
+  a.probes = probes;
+  a.embeddings = embeddings;
+  a.total_docs = embeddings != nullptr ? total_docs : 0;
+  a.dim = static_cast<int>(dim);
+  a.queries = queries;
+  a.max_per_row = max_per_row;
+  a.filter_mask = filter_mask;
+  a.filter_rows = filter_rows;
+  a.filter_cols = filter_cols;
+  a.filter_index = filter_index;
+  a.scale = emb_dtype == kKmI8 ? per_embedding_scale : nullptr;
+  a.divisor = divisor_for_int8;
+  a.invalid_index = invalid_index_value;
+  a.scores = scores;
+  a.indices = indices;
+  const int st = st_kmean_ann_score_dtype(emb_dtype, divisor_for_int8, a.scale != nullptr);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t groups = batch * std::max<int64_t>(probes, 1);
+  ST_CHECK(groups <= INT32_MAX, "batch x probes = ", groups, " workgroups; at most 2^31 - 1");
+  if (probes > 0) {
+    ST_CHECK(counts != nullptr, "workspace is null");
+    const int64_t items = batch * probes, per = kKmCountThreads / 64;
+    hipLaunchKernelGGL(kmean_count_kernel, dim3(static_cast<unsigned>((items + per - 1) / per)),
+                       dim3(kKmCountThreads), 0, s, a, counts, items);
+  }
+  const dim3 grid(static_cast<unsigned>(groups)), block(kKmThreads);
+  switch (emb_dtype) {
+    case kKmF32: hipLaunchKernelGGL((kmean_ann_kernel<kKmF32, kKmF32>), grid, block, 0, s, a, counts); break;
+    case kKmF16: hipLaunchKernelGGL((kmean_ann_kernel<kKmF16, kKmF16>), grid, block, 0, s, a, counts); break;
+    case kKmBF16: hipLaunchKernelGGL((kmean_ann_kernel<kKmBF16, kKmBF16>), grid, block, 0, s, a, counts); break;
+    default:
+      if (st == kKmI32)
+        hipLaunchKernelGGL((kmean_ann_kernel<kKmI8, kKmI32>), grid, block, 0, s, a, counts);
+      else
+        hipLaunchKernelGGL((kmean_ann_kernel<kKmI8, kKmF16>), grid, block, 0, s, a, counts);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    throw Error(ST_ERR_HIP, cat("fused_kmean_ann launch failed: ", hipGetErrorString(e)));
+}
+
+}  // namespace
+}  // namespace st
+
 extern "C" int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_offsets,
                                   const int64_t* cluster_ids, const int64_t* cluster_length,
                                   int64_t batch, int64_t probes, const void* embeddings,
@@ -513,65 +592,71 @@ extern "C" int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_of
                                   int32_t* indices, void* stream) {
   using namespace st;
   return guarded([&] {
-    ST_CHECK(batch >= 0 && probes >= 0 && total_docs >= 0 && max_per_row >= 0 && num_offsets >= 0,
-             "negative sizes");
-    ST_CHECK(dim >= 1 && dim <= kKmMaxDim, "embedding dim must be in [1, ", kKmMaxDim, "], got ",
-             dim);
-    ST_CHECK(emb_dtype >= kKmF32 && emb_dtype <= kKmI8, "unsupported embedding dtype code ",
-             emb_dtype);
-    if (batch == 0 || max_per_row == 0) return;
-    ST_CHECK(scores != nullptr && indices != nullptr && queries != nullptr, "null device pointer");
-    ST_CHECK(probes == 0 || (cluster_ids != nullptr && cluster_length != nullptr &&
-                             cluster_offsets != nullptr),
-             "null cluster arrays");
-    ST_CHECK(filter_mask == nullptr || (filter_cols >= 0 && filter_rows >= 0),
-             "negative filter mask shape");
-    ST_CHECK(filter_mask == nullptr || filter_index != nullptr || filter_rows >= batch,
-             "filter mask has ", filter_rows, " rows for ", batch, " queries");
-    KmArgs a;
-    a.cluster_offsets = cluster_offsets;
-    a.num_offsets = num_offsets;
-    a.cluster_ids = cluster_ids;
-    a.cluster_length = cluster_length;
-    a.probes = probes;
-    a.embeddings = embeddings;
-    a.total_docs = embeddings != nullptr ? total_docs : 0;
-    a.dim = static_cast<int>(dim);
-    a.queries = queries;
-    a.max_per_row = max_per_row;
-    a.filter_mask = filter_mask;
-    a.filter_rows = filter_rows;
-    a.filter_cols = filter_cols;
-    a.filter_index = filter_index;
-    a.scale = emb_dtype == kKmI8 ? per_embedding_scale : nullptr;
-    a.divisor = divisor_for_int8;
-    a.invalid_index = invalid_index_value;
-    a.scores = scores;
-    a.indices = indices;
-    const int st = st_kmean_ann_score_dtype(emb_dtype, divisor_for_int8, a.scale != nullptr);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const int64_t groups = batch * std::max<int64_t>(probes, 1);
-    ST_CHECK(groups <= INT32_MAX, "batch x probes = ", groups, " workgroups; at most 2^31 - 1");
-    int64_t* counts = static_cast<int64_t*>(workspace);
-    if (probes > 0) {
-      ST_CHECK(counts != nullptr, "workspace is null");
-      const int64_t items = batch * probes, per = kKmCountThreads / 64;
-      hipLaunchKernelGGL(kmean_count_kernel, dim3(static_cast<unsigned>((items + per - 1) / per)),
-                         dim3(kKmCountThreads), 0, s, a, counts, items);
-    }
-    const dim3 grid(static_cast<unsigned>(groups)), block(kKmThreads);
-    switch (emb_dtype) {
-      case kKmF32: hipLaunchKernelGGL((kmean_ann_kernel<kKmF32, kKmF32>), grid, block, 0, s, a, counts); break;
-      case kKmF16: hipLaunchKernelGGL((kmean_ann_kernel<kKmF16, kKmF16>), grid, block, 0, s, a, counts); break;
-      case kKmBF16: hipLaunchKernelGGL((kmean_ann_kernel<kKmBF16, kKmBF16>), grid, block, 0, s, a, counts); break;
-      default:
-        if (st == kKmI32)
-          hipLaunchKernelGGL((kmean_ann_kernel<kKmI8, kKmI32>), grid, block, 0, s, a, counts);
-        else
-          hipLaunchKernelGGL((kmean_ann_kernel<kKmI8, kKmF16>), grid, block, 0, s, a, counts);
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess)
-      throw Error(ST_ERR_HIP, cat("fused_kmean_ann launch failed: ", hipGetErrorString(e)));
+    kmean_run(cluster_offsets, num_offsets, cluster_ids, cluster_length, batch, probes, embeddings,
+              total_docs, dim, emb_dtype, queries, max_per_row, filter_mask, filter_rows, filter_cols,
+              filter_index, per_embedding_scale, divisor_for_int8, invalid_index_value,
+              static_cast<int64_t*>(workspace), -1, scores, indices, stream);
+  });
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation variant: the per-(row, probe) counts live in a file-scope
+// device array (one copy per GPU, held until the process ends) instead of a
+// caller-provided workspace.  Its address is taken once per device with
+// hipGetSymbolAddress, on that device's first call; host code uses only that
+// address, never the array's name.  Every (row, probe) count is written by
+// kmean_count_kernel before kmean_ann_kernel reads it, so nothing needs
+// clearing between calls; calls that overlap on one GPU share the array and
+// race.
+
+namespace st {
+namespace {
+
+constexpr int64_t kKmScratchItems = ST_KMEAN_NOALLOC_MAX_PAIRS;
+static_assert(kKmScratchItems == (int64_t{1} << 20), "the header's limit and the array size differ");
+static __device__ __align__(256) int64_t scratch[kKmScratchItems];
+
+constexpr int kKmMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kKmMaxDevices] = {};
+
+// The calling thread's current device's copy of `scratch`.
+int64_t* device_scratch() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) throw Error(ST_ERR_HIP, cat("hipGetDevice failed: ", hipGetErrorString(e)));
+  ST_CHECK(dev >= 0 && dev < kKmMaxDevices, "device ordinal ", dev, " out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      throw Error(ST_ERR_HIP, cat("hipGetSymbolAddress(scratch) failed on device ", dev, ": ",
+                                  hipGetErrorString(e)));
+    g_scratch_ptr[dev] = ptr;
+  }
+  return static_cast<int64_t*>(g_scratch_ptr[dev]);
+}
+
+}  // namespace
+}  // namespace st
+
+extern "C" int st_fused_kmean_ann_noalloc(
+    const int64_t* cluster_offsets, int64_t num_offsets, const int64_t* cluster_ids,
+    const int64_t* cluster_length, int64_t batch, int64_t probes, const void* embeddings,
+    int64_t total_docs, int64_t dim, int emb_dtype, const void* queries, int64_t max_per_row,
+    const int64_t* filter_mask, int64_t filter_rows, int64_t filter_cols,
+    const int64_t* filter_index, const uint16_t* per_embedding_scale, int64_t divisor_for_int8,
+    int64_t invalid_index_value, void* scores, int32_t* indices, void* stream) {
+  using namespace st;
+  return guarded([&] {
+    ST_CHECK(batch < 0 || probes <= 0 || batch <= kKmScratchItems / probes, "batch x probes = ", batch,
+             " x ", probes, " exceeds the ", kKmScratchItems,
+             " (row, probe) pairs of the no-allocation entry point's scratch");
+    int64_t* counts = batch > 0 && probes > 0 && max_per_row > 0 ? device_scratch() : nullptr;
+    kmean_run(cluster_offsets, num_offsets, cluster_ids, cluster_length, batch, probes, embeddings,
+              total_docs, dim, emb_dtype, queries, max_per_row, filter_mask, filter_rows, filter_cols,
+              filter_index, per_embedding_scale, divisor_for_int8, invalid_index_value, counts,
+              kKmScratchItems, scores, indices, stream);
   });
 }
