@@ -21,6 +21,8 @@
  *   st::parse_expression_query_batch  expression_query_parser.cpp:456-472
  *   st::generate_column_info_for_clusters
  *                                     bloom_index_search.cpp:489-540, :543-547
+ *   st::take_top_k_and_gather_from_main_and_fresh
+ *                                     fresh_index_post_processing.cpp:231-287
  */
 #ifndef SILVERTORCH_HIP_H_
 #define SILVERTORCH_HIP_H_
@@ -375,6 +377,49 @@ int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_offsets,
                        int64_t divisor_for_int8, int64_t invalid_index_value,
                        void* workspace, void* scores, int32_t* indices,
                        void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Merge of a main and a fresh candidate list.  Replaces
+ * take_top_k_and_gather_from_main_and_fresh (schema
+ * fresh_index_post_processing.cpp:275-287, CPU impl :231-270, gather
+ * :44-163).  Two calls:
+ *
+ * st_fresh_topk: row r's merged scores are fresh_scores[r, 0..num_fresh)
+ * followed by main_scores[r, 0..num_main) (both row-major, contiguous, of
+ * score_type); the k best (0 <= k <= num_fresh + num_main), best first, go
+ * to top_scores [rows, k] (score_type, the input values), top_index int64
+ * [rows, k] (merged column) and is_from_fresh uint8 [rows, k] (top_index <
+ * num_fresh).  Larger scores rank first; NaN above every number; -0.0 and
+ * +0.0 are equal; equal scores in merged-column order.  workspace: device
+ * memory of st_fresh_topk_workspace_bytes(rows, k) bytes (0 for k <= 8192).
+ *
+ * st_fresh_gather: one data tensor.  For output row o = r * k + j with
+ * t = top_index[o]: source row s = fresh_indices[r * fresh_index_cols + t]
+ * when t < num_fresh, else main_indices[r * main_index_cols + t - num_fresh]
+ * (indices int32 or int64: index_bytes 4 or 8); s outside [0, data rows)
+ * reads row 0 (an empty data tensor gives zeros); out[o, 0..dim) =
+ * data[s, 0..dim) with elements of elem_bytes (1, 2, 4 or 8) bytes.
+ * ------------------------------------------------------------------------- */
+#define ST_SCORE_F32 0
+#define ST_SCORE_F16 1
+#define ST_SCORE_BF16 2
+#define ST_SCORE_F64 3
+#define ST_SCORE_I64 4
+#define ST_SCORE_I32 5
+#define ST_SCORE_I16 6
+#define ST_SCORE_I8 7
+#define ST_SCORE_U8 8
+int64_t st_fresh_topk_workspace_bytes(int64_t rows, int64_t k);
+int st_fresh_topk(const void* main_scores, const void* fresh_scores, int score_type,
+                  int64_t rows, int64_t num_main, int64_t num_fresh, int64_t k,
+                  void* workspace, void* top_scores, int64_t* top_index,
+                  uint8_t* is_from_fresh, void* stream);
+int st_fresh_gather(const int64_t* top_index, int64_t rows, int64_t k,
+                    const void* fresh_indices, const void* main_indices,
+                    int index_bytes, int64_t fresh_index_cols, int64_t main_index_cols,
+                    int64_t num_fresh, int64_t num_main, const void* fresh_data,
+                    int64_t fresh_rows, const void* main_data, int64_t main_rows,
+                    int64_t dim, int elem_bytes, void* out, void* stream);
 
 /* ---------------------------------------------------------------------------
  * st_fused_kmean_ann without allocation.  No counterpart in the reference:

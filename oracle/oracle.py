@@ -298,3 +298,58 @@ def fused_kmean_ann(cluster_offsets, cluster_ids, cluster_length, embeddings, qu
                 indices[b, write] = doc
                 write += 1
     return scores, indices
+
+
+def _score_rank_columns(scores: np.ndarray):
+    """(is_nan, value) per score: NaN ranks above every number (the
+    comparator of at::topk's CPU kernel) and -0.0 equals +0.0."""
+    s = np.asarray(scores)
+    if s.dtype.kind == "f":
+        f = s.astype(np.float64)
+        nan = np.isnan(f)
+        return nan.astype(np.int64), np.where(nan, 0.0, f) + 0.0  # -0.0 + 0.0 == +0.0
+    return np.zeros(s.shape, np.int64), s.astype(np.int64)
+
+
+def fresh_topk_gather(main_scores, fresh_scores, main_indices, fresh_indices, k: int,
+                      main_data: list, fresh_data: list):
+    """Restates take_top_k_and_gather_from_main_and_fresh_cpu
+    (fresh_index_post_processing.cpp:231-270) and its gather (:44-163):
+    merged = cat(fresh, main) per row; the min(k, Nf + Nm) best, largest
+    first; is_from_fresh = merged index < Nf; data row through fresh_indices
+    [r, t] (t < Nf) or main_indices[r, t - Nf], a row outside the data read
+    as row 0.  at::topk leaves the order of equal scores open; this
+    restatement puts the lower merged index first (the order the HIP kernel
+    promises).  Scores must share one dtype (bf16 as float32 values).
+    Returns (top_scores, top_indices int64, is_from_fresh bool, [gathered])."""
+    main_scores = np.asarray(main_scores)
+    fresh_scores = np.asarray(fresh_scores)
+    R, Nm = main_scores.shape
+    Nf = fresh_scores.shape[1]
+    merged = np.concatenate([fresh_scores, main_scores], axis=1)
+    kc = min(k, Nf + Nm)
+    is_nan, vals = _score_rank_columns(merged)
+    cols = np.arange(Nf + Nm)
+    top_idx = np.zeros((R, kc), np.int64)
+    for r in range(R):
+        # NaN first, then larger value, then lower merged index
+        top_idx[r] = np.lexsort((cols, -vals[r], -is_nan[r]))[:kc]
+    top_scores = np.take_along_axis(merged, top_idx, axis=1)
+    is_fresh = top_idx < Nf
+    gathered = []
+    for md, fd in zip(main_data, fresh_data):
+        md, fd = np.asarray(md), np.asarray(fd)
+        rows = []
+        for r in range(R):
+            for j in range(kc):
+                t = int(top_idx[r, j])
+                if t < Nf:
+                    src, data = int(fresh_indices[r, t]), fd
+                else:
+                    src, data = int(main_indices[r, t - Nf]), md
+                if src < 0 or src >= data.shape[0]:
+                    src = 0
+                rows.append(data[src])
+        shape = (R * kc,) + md.shape[1:]
+        gathered.append(np.array(rows, dtype=md.dtype).reshape(shape) if rows else np.zeros(shape, md.dtype))
+    return top_scores, top_idx, is_fresh, gathered

@@ -49,6 +49,7 @@ LIB_SOURCES = [
     "bloom_partial.hip",
     "filtered_topk.hip",
     "kmean_ann.hip",
+    "fresh_topk.hip",
     "search_plan.cpp",
     "expression_parser.cpp",
 ]
@@ -64,10 +65,24 @@ def _run(cmd: list[str]) -> None:
         sys.stderr.write(out + "\n")
 
 
+def _stale(obj: Path, src: Path) -> bool:
+    """True when obj is missing or older than its source or any header."""
+    if not obj.exists():
+        return True
+    t = obj.stat().st_mtime
+    deps = [src, *CSRC.glob("*.hpp"), ROOT / "include" / "silvertorch_hip.h"]
+    return any(d.stat().st_mtime > t for d in deps)
+
+
+INCREMENTAL = False  # set by `python -m silvertorch_amd._build --incremental`
+
+
 def _compile_lib_object(spec) -> Path:
     src, k = spec if isinstance(spec, tuple) else (spec, None)
     obj = OBJ / (src + ("" if k is None else f".k{k}") + ".o")
     path = CSRC / src
+    if INCREMENTAL and not _stale(obj, path):
+        return obj
     if src.endswith(".cpp"):  # host-only C++
         cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-c"]
     else:
@@ -126,5 +141,6 @@ def build(jobs: int = os.cpu_count() or 8) -> None:
 
 
 if __name__ == "__main__":
+    INCREMENTAL = "--incremental" in sys.argv[1:]
     build()
     print(f"built {LIB.relative_to(ROOT)} and {EXT.relative_to(ROOT)}")

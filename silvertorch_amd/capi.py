@@ -57,7 +57,15 @@ SIGNATURES = {
     "st_search_plan_partial_items": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp,
                                                     _i64p, _i64p]),
     "st_bloom_index_search_partial": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp]),
+    "st_fresh_topk_workspace_bytes": (_i64, [_i64, _i64]),
+    "st_fresh_topk": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "st_fresh_gather": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, ctypes.c_int, _i64, _i64, _i64, _i64, _vp, _i64,
+                                       _vp, _i64, _i64, ctypes.c_int, _vp, _vp]),
 }
+
+# score type codes of st_fresh_topk (ST_SCORE_*)
+FRESH_SCORE_TYPES = {"float32": 0, "float16": 1, "bfloat16": 2, "float64": 3, "int64": 4, "int32": 5,
+                     "int16": 6, "int8": 7, "uint8": 8}
 
 # struct st_partial_item (include/silvertorch_hip.h)
 PARTIAL_ITEM_BYTES = 32

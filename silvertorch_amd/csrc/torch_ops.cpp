@@ -799,9 +799,175 @@ std::tuple<std::vector<Tensor>, std::vector<Tensor>> kmean_partial_multiple(
   return {scores, indices};
 }
 
+// ------------------------------------------ main + fresh candidate merge
+
+int fresh_score_type(at::ScalarType t) {
+  switch (t) {
+    case at::kFloat: return ST_SCORE_F32;
+    case at::kHalf: return ST_SCORE_F16;
+    case at::kBFloat16: return ST_SCORE_BF16;
+    case at::kDouble: return ST_SCORE_F64;
+    case at::kLong: return ST_SCORE_I64;
+    case at::kInt: return ST_SCORE_I32;
+    case at::kShort: return ST_SCORE_I16;
+    case at::kChar: return ST_SCORE_I8;
+    case at::kByte: return ST_SCORE_U8;
+    default: TORCH_CHECK(false, "\"topk\" not implemented for '", t, "'");
+  }
+  return -1;
+}
+
+// The data types the reference's gather dispatches on
+// (AT_DISPATCH_ALL_TYPES_AND2(Half, BFloat16), fresh_index_post_processing.cpp:88-93).
+bool fresh_data_type_ok(at::ScalarType t) {
+  switch (t) {
+    case at::kByte: case at::kChar: case at::kShort: case at::kInt: case at::kLong:
+    case at::kFloat: case at::kDouble: case at::kHalf: case at::kBFloat16:
+      return true;
+    default:
+      return false;
+  }
+}
+
+// take_top_k_and_gather_from_main_and_fresh (fresh_index_post_processing.cpp:231-270):
+// argument checks in the reference's order, then the top-k and one gather
+// per key on the device.  kernel_version selects nothing (the reference's
+// CPU op ignores it too).
+std::tuple<Tensor, Tensor, Tensor, c10::Dict<std::string, Tensor>> fresh_merge_gpu(
+    const Tensor& main_scores_in, const Tensor& fresh_scores_in, const Tensor& main_indices_in,
+    const Tensor& fresh_indices_in, int64_t k, const std::vector<std::string>& keys,
+    const std::vector<Tensor>& list_main_data, const std::vector<Tensor>& list_fresh_data,
+    int64_t /*kernel_version*/) {
+  TORCH_CHECK(main_scores_in.dim() == 2 && fresh_scores_in.dim() == 2,
+              "main_scores and fresh_scores must be 2-D [rows, candidates]");
+  TORCH_CHECK(main_scores_in.size(0) == fresh_scores_in.size(0),
+              "main_scores and fresh_scores must have the same number of rows");
+  const at::Device dev = main_scores_in.device();
+  TORCH_CHECK(dev.is_cuda(), "take_top_k_and_gather_from_main_and_fresh inputs must be GPU tensors");
+  for (const Tensor* t : {&fresh_scores_in, &main_indices_in, &fresh_indices_in})
+    TORCH_CHECK(t->device() == dev, "take_top_k_and_gather_from_main_and_fresh inputs must be on one device");
+  c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(dev);
+  const int64_t R = main_scores_in.size(0);
+  const int64_t Nf = fresh_scores_in.size(1), Nm = main_scores_in.size(1);
+  // at::cat promotes the two score tensors to one type
+  const at::ScalarType st_type = at::result_type(fresh_scores_in, main_scores_in);
+  const int code = fresh_score_type(st_type);
+  const Tensor fs = fresh_scores_in.to(st_type).contiguous();
+  const Tensor ms = main_scores_in.to(st_type).contiguous();
+  TORCH_CHECK(k >= 0, "selected index k out of range");
+  const int64_t kc = std::min<int64_t>(k, Nf + Nm);
+  auto opts = at::TensorOptions().device(dev);
+  Tensor top_scores = at::empty({R, kc}, opts.dtype(st_type));
+  Tensor top_index = at::empty({R, kc}, opts.dtype(at::kLong));
+  Tensor from_fresh = at::empty({R, kc}, opts.dtype(at::kBool));
+  void* stream = current_stream(fs);
+  const int64_t ws_bytes = st_fresh_topk_workspace_bytes(R, kc);
+  Tensor ws = at::empty({std::max<int64_t>(ws_bytes, 1)}, opts.dtype(at::kByte));
+  check_st(st_fresh_topk(Nm ? ms.data_ptr() : nullptr, Nf ? fs.data_ptr() : nullptr, code, R, Nm,
+                         Nf, kc, ws.data_ptr(), top_scores.data_ptr(),
+                         top_index.data_ptr<int64_t>(),
+                         reinterpret_cast<uint8_t*>(from_fresh.data_ptr<bool>()), stream),
+           "take_top_k_and_gather_from_main_and_fresh");
+
+  // gather_data_from_main_and_fresh_index_cpu (fresh_index_post_processing.cpp:165-228)
+  TORCH_CHECK(keys.size() == list_main_data.size(),
+              "keys and list_main_data should have the same size. ", "keys.size()=", keys.size(),
+              ", list_main_data.size()=", list_main_data.size());
+  TORCH_CHECK(keys.size() == list_fresh_data.size(),
+              "keys and list_fresh_data should have the same size. ", "keys.size()=", keys.size(),
+              ", list_fresh_data.size()=", list_fresh_data.size());
+  for (size_t i = 0; i < keys.size(); ++i) {
+    const Tensor& md = list_main_data[i];
+    const Tensor& fd = list_fresh_data[i];
+    TORCH_CHECK(md.dim() == fd.dim(), "main_data and fresh_data should have the same dim. ", "key=",
+                keys[i], ", main_data.dim()=", md.dim(), ", fresh_data.dim()=", fd.dim());
+    if (md.dim() > 1) {
+      TORCH_CHECK(md.size(-1) == fd.size(-1),
+                  "main_data and fresh_data should have the same number of element in the last dim. "
+                  "key=", keys[i], ", main_data.size(-1)=", md.size(-1),
+                  ", fresh_data.size(-1)=", fd.size(-1));
+    }
+    TORCH_CHECK(md.scalar_type() == fd.scalar_type(),
+                "main_data and fresh_data should have the same scalar_type. ", "key=", keys[i],
+                ", main_data.scalar_type()=", md.scalar_type(),
+                ", fresh_data.scalar_type()=", fd.scalar_type());
+  }
+  c10::Dict<std::string, Tensor> gathered;
+  if (!keys.empty()) {
+    TORCH_CHECK(main_indices_in.dim() == 2 && fresh_indices_in.dim() == 2,
+                "main_indices and fresh_indices must be 2-D");
+    TORCH_CHECK(main_indices_in.scalar_type() == at::kInt || main_indices_in.scalar_type() == at::kLong,
+                "\"gather_data_from_main_and_fresh_index_cpu_impl_index\" not implemented for '",
+                main_indices_in.scalar_type(), "'");
+    TORCH_CHECK(fresh_indices_in.scalar_type() == main_indices_in.scalar_type(),
+                "expected scalar type ", main_indices_in.scalar_type(),
+                " but found ", fresh_indices_in.scalar_type());
+    TORCH_CHECK(main_indices_in.size(0) >= R && fresh_indices_in.size(0) >= R,
+                "main_indices and fresh_indices must hold a row per score row");
+  }
+  const Tensor mi = main_indices_in.contiguous(), fi = fresh_indices_in.contiguous();
+  for (size_t i = 0; i < keys.size(); ++i) {
+    const Tensor& md_in = list_main_data[i];
+    const Tensor& fd_in = list_fresh_data[i];
+    TORCH_CHECK(md_in.dim() > 0 && md_in.dim() <= 2,
+                "The main data dim must be in [1, 2], main_data.dim()=", md_in.dim());
+    TORCH_CHECK(fd_in.dim() > 0 && fd_in.dim() <= 2,
+                "The fresh data dim must be in [1, 2], fresh_data.dim()=", fd_in.dim());
+    TORCH_CHECK(fresh_data_type_ok(md_in.scalar_type()),
+                "\"gather_data_from_main_and_fresh_index_cpu_impl\" not implemented for '",
+                md_in.scalar_type(), "'");
+    TORCH_CHECK(md_in.device() == dev && fd_in.device() == dev,
+                "data tensors must be on the scores' device");
+    const Tensor md = md_in.contiguous(), fd = fd_in.contiguous();
+    const int64_t D = md.dim() == 2 ? md.size(1) : 1;
+    Tensor out = md.dim() == 2 ? at::empty({R * kc, D}, md.options())
+                               : at::empty({R * kc}, md.options());
+    check_st(st_fresh_gather(top_index.data_ptr<int64_t>(), R, kc,
+                             fi.numel() ? fi.data_ptr() : nullptr,
+                             mi.numel() ? mi.data_ptr() : nullptr,
+                             static_cast<int>(mi.element_size()), fi.size(1), mi.size(1), Nf, Nm,
+                             fd.numel() ? fd.data_ptr() : nullptr, fd.size(0),
+                             md.numel() ? md.data_ptr() : nullptr, md.size(0), D,
+                             static_cast<int>(md.element_size()), out.data_ptr(), stream),
+             "take_top_k_and_gather_from_main_and_fresh");
+    gathered.insert(keys[i], out);
+  }
+  return {top_scores, top_index, from_fresh, gathered};
+}
+
+std::tuple<Tensor, Tensor, Tensor, c10::Dict<std::string, Tensor>> fresh_merge_cpu(
+    const Tensor& main_scores, const Tensor& fresh_scores, const Tensor& main_indices,
+    const Tensor& fresh_indices, int64_t k, const std::vector<std::string>& keys,
+    const std::vector<Tensor>& list_main_data, const std::vector<Tensor>& list_fresh_data,
+    int64_t kernel_version) {
+  const at::Device gpu = gpu_for_cpu_call();
+  std::vector<Tensor> md, fd;
+  for (const Tensor& t : list_main_data) md.push_back(t.to(gpu));
+  for (const Tensor& t : list_fresh_data) fd.push_back(t.to(gpu));
+  auto [s, ix, ff, g] = fresh_merge_gpu(main_scores.to(gpu), fresh_scores.to(gpu),
+                                        main_indices.to(gpu), fresh_indices.to(gpu), k, keys, md,
+                                        fd, kernel_version);
+  c10::Dict<std::string, Tensor> out;
+  for (const auto& e : g) out.insert(e.key(), e.value().cpu());
+  return {s.cpu(), ix.cpu(), ff.cpu(), out};
+}
+
 }  // namespace
 
 TORCH_LIBRARY_FRAGMENT(st, m) {
+  // fresh_index_post_processing.cpp:275-287, verbatim
+  m.def(
+      "take_top_k_and_gather_from_main_and_fresh("
+      "Tensor main_scores, "
+      "Tensor fresh_scores, "
+      "Tensor main_indices, "
+      "Tensor fresh_indices, "
+      "int k, "
+      "str[] keys, "
+      "Tensor[] list_main_data, "
+      "Tensor[] list_fresh_data, "
+      "int kernel_version=2 "
+      ") -> (Tensor, Tensor, Tensor, Dict(str, Tensor))");
   m.def(
       "bloom_index_build(Tensor feature_ids, Tensor feature_offsets, "
       "Tensor feature_values, float b_multiplier, int k, "
@@ -918,6 +1084,7 @@ TORCH_LIBRARY_IMPL(st, CUDA, m) {
   m.impl("fused_kmean_ann", TORCH_FN(kmean_gpu));
   m.impl("fused_kmean_ann_with_partial_masks", TORCH_FN(kmean_partial));
   m.impl("fused_kmean_ann_with_partial_masks_multiple", TORCH_FN(kmean_partial_multiple));
+  m.impl("take_top_k_and_gather_from_main_and_fresh", TORCH_FN(fresh_merge_gpu));
 }
 
 TORCH_LIBRARY_IMPL(st, CPU, m) {
@@ -934,6 +1101,7 @@ TORCH_LIBRARY_IMPL(st, CPU, m) {
   m.impl("fused_kmean_ann", TORCH_FN(kmean_cpu));
   m.impl("fused_kmean_ann_with_partial_masks", TORCH_FN(kmean_partial));
   m.impl("fused_kmean_ann_with_partial_masks_multiple", TORCH_FN(kmean_partial_multiple));
+  m.impl("take_top_k_and_gather_from_main_and_fresh", TORCH_FN(fresh_merge_cpu));
 }
 
 // Python module entry point: importing silvertorch_amd._C loads this library,

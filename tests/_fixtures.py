@@ -128,3 +128,41 @@ def kmean_case(name: str) -> dict:
 def kmean_group(prefix: str) -> dict:
     z = _kmean_npz()
     return {k[len(prefix) + 1:]: v for k, v in z.items() if k.startswith(prefix + "/")}
+
+
+@lru_cache(None)
+def _fresh_npz():
+    return dict(np.load(GOLDEN / "ref_fresh.npz", allow_pickle=False))
+
+
+def fresh_case_names() -> list[str]:
+    return sorted({k.split("/")[0] for k in _fresh_npz()})
+
+
+def fresh_case(name: str) -> dict:
+    """One take_top_k_and_gather_from_main_and_fresh fixture of the reference
+    CPU op (tests/golden/make_golden.py fresh_fixtures): arrays by field, with
+    'main_data' / 'fresh_data' / 'gathered' dicts by key.  bfloat16 arrays are
+    uint16 bit patterns listed in 'bf16' (the set of field paths)."""
+    z = _fresh_npz()
+    pre = name + "/"
+    c: dict = {"main_data": {}, "fresh_data": {}, "gathered": {}, "bf16": set()}
+    for k, v in z.items():
+        if not k.startswith(pre):
+            continue
+        path = k[len(pre):]
+        if path.endswith("@bf16"):
+            c["bf16"].add(path[:-5])
+            continue
+        parts = path.split("/")
+        if len(parts) == 2:
+            c[parts[0]][parts[1]] = v
+        else:
+            c[path] = v
+    c["k"] = int(c["k"])
+    c["keys"] = [str(s) for s in c["keys"]]
+    return c
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)

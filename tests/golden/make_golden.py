@@ -20,8 +20,12 @@ Sources of truth, neither of which is this repository's code:
                         reference's CPU op (fused_kmean_ann.cpp) on small
                         cases: every embedding dtype, int8 divisor and
                         per-embedding scale, truncated rows, filtered rows.
+      ref_fresh.npz     take_top_k_and_gather_from_main_and_fresh of the
+                        reference's CPU op (fresh_index_post_processing.cpp)
+                        on cases with distinct scores per row (at::topk
+                        leaves the order of equal scores open).
 
-Usage:  python tests/golden/make_golden.py [partial|kmean]   (only that file)
+Usage:  python tests/golden/make_golden.py [partial|kmean|fresh]   (only that file)
         python tests/golden/make_golden.py full [cfg2 cfg5 cfg4 ...]
                 (ref_full_digests.json: full-size configurations, minutes)
 The reference library registers torch.ops.st.*, so this script never imports
@@ -480,6 +484,123 @@ def kmean_fixtures() -> None:
     print("fused_kmean_ann fixtures written to", HERE / "ref_kmean.npz")
 
 
+def fresh_fixtures() -> None:
+    """ref_fresh.npz: take_top_k_and_gather_from_main_and_fresh of the
+    reference's CPU op (fresh_index_post_processing.cpp:231-270).  Scores are
+    distinct within each merged row (a permutation of exactly representable
+    values), so the reference's top-k order is fully determined.  Indices
+    include values outside the data rows (read as row 0).  Per case: inputs,
+    k, the data tensors, and the four outputs; bfloat16 tensors are stored as
+    uint16 bits with a '@bf16' marker."""
+    import torch
+
+    ref = ROOT / "oracle" / "_ref" / "libst_ref.so"
+    if not ref.exists():
+        subprocess.run(["make", "-C", str(ROOT / "oracle"), "ref"], check=True)
+    torch.ops.load_library(str(ref))
+    st = torch.ops.st
+    out = {}
+    rng = np.random.default_rng(77)
+
+    def save(key, t):
+        if t.dtype == torch.bfloat16:
+            out[key] = t.view(torch.int16).numpy().view(np.uint16)
+            out[key + "@bf16"] = np.array(1)
+        else:
+            out[key] = t.numpy()
+
+    def distinct_scores(R, n, dtype):
+        # permutations of values exact in every score dtype used here
+        if dtype in (torch.float16, torch.bfloat16):
+            base = np.arange(n, dtype=np.float64) - n // 2      # |v| <= 256 for bf16 cases
+        elif not dtype.is_floating_point:
+            base = np.arange(n, dtype=np.float64) - (0 if dtype == torch.uint8 else n // 2)
+        else:
+            base = (np.arange(n, dtype=np.float64) - n / 3) * 0.37
+        rows = np.stack([rng.permutation(base) for _ in range(R)]) if n else np.zeros((R, 0))
+        return torch.from_numpy(rows).to(dtype)
+
+    def add(name, R, nf, nm, k, score_dtype, index_dtype, datas, main_rows, fresh_rows):
+        merged = distinct_scores(R, nf + nm, score_dtype)
+        fresh_s, main_s = merged[:, :nf].contiguous(), merged[:, nf:].contiguous()
+        # source rows mostly valid, some negative or past the data (read as row 0)
+        mi = torch.from_numpy(rng.integers(-2, main_rows + 2, (R, nm))).to(index_dtype)
+        fi = torch.from_numpy(rng.integers(-2, fresh_rows + 2, (R, nf))).to(index_dtype)
+        keys, mds, fds = [], [], []
+        for key, (dtype, dim) in datas.items():
+            shape_m = (main_rows,) if dim == 0 else (main_rows, dim)
+            shape_f = (fresh_rows,) if dim == 0 else (fresh_rows, dim)
+            if dtype.is_floating_point:
+                md = torch.from_numpy(rng.standard_normal(shape_m)).to(dtype)
+                fd = torch.from_numpy(rng.standard_normal(shape_f)).to(dtype)
+            else:
+                hi = 100 if dtype in (torch.int8, torch.uint8) else 1 << 20
+                md = torch.from_numpy(rng.integers(0, hi, shape_m)).to(dtype)
+                fd = torch.from_numpy(rng.integers(0, hi, shape_f)).to(dtype)
+            keys.append(key)
+            mds.append(md)
+            fds.append(fd)
+        ts, ti, ff, g = st.take_top_k_and_gather_from_main_and_fresh(main_s, fresh_s, mi, fi, k, keys, mds, fds, 2)
+        save(f"{name}/main_scores", main_s)
+        save(f"{name}/fresh_scores", fresh_s)
+        out[f"{name}/main_indices"] = mi.numpy()
+        out[f"{name}/fresh_indices"] = fi.numpy()
+        out[f"{name}/k"] = np.array(k)
+        out[f"{name}/keys"] = np.array(keys)
+        for key, md, fd in zip(keys, mds, fds):
+            save(f"{name}/main_data/{key}", md)
+            save(f"{name}/fresh_data/{key}", fd)
+            save(f"{name}/gathered/{key}", g[key])
+        save(f"{name}/top_scores", ts)
+        out[f"{name}/top_indices"] = ti.numpy()
+        out[f"{name}/is_from_fresh"] = ff.numpy()
+
+    # the reference test's own inputs (test_fresh_index_post_processing.py:38-100)
+    main_scores = torch.tensor([[0.90, 0.10, 0.70, 0.80, 0.40], [0.15, 0.28, 0.85, 0.05, 0.38]], dtype=torch.float16)
+    fresh_scores = torch.tensor([[0.95, 0.20, 0.30, 0.60], [0.62, 0.99, 0.48, 0.31]], dtype=torch.float16)
+    vecs = [[float(i), float(i) + 0.5, float(i) - 0.5, float(i) * 2.0] for i in range(7)]
+    for index_dtype in (torch.int32, torch.int64):
+        for k in (3, 7, 20):
+            name = f"readme_{str(index_dtype)[6:]}_k{k}"
+            mi = torch.tensor([[2, 5, 4, 3, 0], [6, 2, 3, 1, 0]], dtype=index_dtype)
+            fi = torch.tensor([[1, 0, 2, 3], [4, 1, 3, 0]], dtype=index_dtype)
+            mds = [torch.tensor([10, 20, 30, 40, 50, 60, 70]), torch.tensor(vecs, dtype=torch.bfloat16)]
+            fds = [torch.tensor([100, 200, 300, 400, 500]), torch.tensor(vecs[:5], dtype=torch.bfloat16)]
+            keys = ["item_ids", "embeddings"]
+            ts, ti, ff, g = st.take_top_k_and_gather_from_main_and_fresh(main_scores, fresh_scores, mi, fi, k,
+                                                                         keys, mds, fds, 2)
+            save(f"{name}/main_scores", main_scores)
+            save(f"{name}/fresh_scores", fresh_scores)
+            out[f"{name}/main_indices"] = mi.numpy()
+            out[f"{name}/fresh_indices"] = fi.numpy()
+            out[f"{name}/k"] = np.array(k)
+            out[f"{name}/keys"] = np.array(keys)
+            for key, md, fd in zip(keys, mds, fds):
+                save(f"{name}/main_data/{key}", md)
+                save(f"{name}/fresh_data/{key}", fd)
+                save(f"{name}/gathered/{key}", g[key])
+            save(f"{name}/top_scores", ts)
+            out[f"{name}/top_indices"] = ti.numpy()
+            out[f"{name}/is_from_fresh"] = ff.numpy()
+
+    add("f32_mixed", 7, 33, 300, 50, torch.float32, torch.int64,
+        {"ids": (torch.int64, 0), "emb": (torch.float32, 5), "tag": (torch.uint8, 0)}, 40, 9)
+    add("f64_main_only", 3, 0, 100, 10, torch.float64, torch.int32,
+        {"ids": (torch.int32, 0), "w": (torch.float16, 3)}, 17, 4)
+    add("f16_fresh_only", 4, 120, 0, 16, torch.float16, torch.int64,
+        {"v": (torch.int16, 2)}, 5, 60)
+    add("bf16_k_clamped", 5, 200, 300, 1000, torch.bfloat16, torch.int32,
+        {"e": (torch.bfloat16, 8), "d": (torch.float64, 0)}, 500, 200)
+    add("i32_scores", 4, 20, 10, 7, torch.int32, torch.int64, {"x": (torch.int8, 0)}, 3, 30)
+    add("i64_scores_k0", 2, 5, 6, 0, torch.int64, torch.int64, {"x": (torch.int64, 0)}, 6, 5)
+    add("f32_long_rows", 3, 1500, 12000, 300, torch.float32, torch.int64, {"ids": (torch.int32, 0)}, 2000, 300)
+    add("f32_k_global", 2, 3000, 7000, 9000, torch.float32, torch.int32,
+        {"ids": (torch.int32, 0)}, 1000, 500)
+    add("u8_scores", 3, 40, 60, 25, torch.uint8, torch.int64, {"x": (torch.float32, 0)}, 60, 40)
+    np.savez_compressed(HERE / "ref_fresh.npz", **out)
+    print("take_top_k_and_gather_from_main_and_fresh fixtures written to", HERE / "ref_fresh.npz")
+
+
 def full_digests(names: list[str]) -> None:
     """ref_full_digests.json: the benchmark configurations at full size,
     built and searched by the reference's CPU ops on the numpy-generated
@@ -536,9 +657,12 @@ if __name__ == "__main__":
         partial_fixtures()
     elif sys.argv[1:] == ["kmean"]:
         kmean_fixtures()
+    elif sys.argv[1:] == ["fresh"]:
+        fresh_fixtures()
     elif sys.argv[1:2] == ["full"]:
         full_digests(sys.argv[2:] or ["cfg2", "cfg5", "cfg4"])
     else:
         main()
         partial_fixtures()
         kmean_fixtures()
+        fresh_fixtures()

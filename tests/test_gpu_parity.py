@@ -44,6 +44,25 @@ def test_build_matches_reference(name):
 
 
 @pytest.mark.parametrize("name", G.case_names())
+@pytest.mark.parametrize("fast_build", [False, True])
+def test_op_build_fast_build_flag_matches_reference(name, fast_build):
+    """torch.ops.st.bloom_index_build with fast_build=True returns the same
+    bits as the default build: the reference's flag selects another CUDA
+    algorithm with identical output (bloom_indexer_cuda.cu:838-853) and is
+    ignored by its CPU op (bloom_indexer.cpp:32), so both are checked against
+    the reference CPU op's fixtures, on GPU and on CPU tensors."""
+    c = G.case(name)
+    H.note(f"[build op] case={name} fast_build={fast_build}")
+    args = [torch.from_numpy(c["ids"]), torch.from_numpy(c["offsets"]), torch.from_numpy(c["values"])]
+    for dev in ("cuda", "cpu"):
+        bi, bo = torch.ops.st.bloom_index_build(*[a.to(dev) for a in args], c["b_multiplier"], c["build_k"],
+                                                fast_build=fast_build)
+        assert bi.device.type == dev
+        np.testing.assert_array_equal(bo.cpu().numpy(), c["bundle_b_offsets"])
+        np.testing.assert_array_equal(bi.cpu().numpy(), c["index"])
+
+
+@pytest.mark.parametrize("name", G.case_names())
 @pytest.mark.parametrize("bool_mask", [False, True])
 def test_search_matches_reference(name, bool_mask):
     c = G.case(name)

@@ -379,3 +379,62 @@ def test_kmean_oracle_filter_identity():
         rev |= ((lsb >> np.uint64(i)) & np.uint64(1)) << np.uint64(63 - i)
     planted, _ = O.fused_kmean_ann(offs, cids, sizes[cids], emb, q, big, filter_mask=rev.view(np.int64))
     assert not np.array_equal(planted, f_s)
+
+
+@pytest.mark.parametrize("name", G.fresh_case_names())
+def test_fresh_oracle_matches_reference(name):
+    """take_top_k_and_gather_from_main_and_fresh oracle vs the reference CPU
+    op's fixtures (distinct scores per row): top scores, merged indices,
+    is_from_fresh and every gathered tensor, bit for bit."""
+    c = G.fresh_case(name)
+
+    def arr(path, a):
+        return G.bf16_bits_to_f32(a) if path in c["bf16"] else a
+
+    ms, fs = arr("main_scores", c["main_scores"]), arr("fresh_scores", c["fresh_scores"])
+    keys = c["keys"]
+    ts, ti, ff, g = O.fresh_topk_gather(ms, fs, c["main_indices"], c["fresh_indices"], c["k"],
+                                        [arr(f"main_data/{k}", c["main_data"][k]) for k in keys],
+                                        [arr(f"fresh_data/{k}", c["fresh_data"][k]) for k in keys])
+    np.testing.assert_array_equal(ti, c["top_indices"])
+    np.testing.assert_array_equal(ff, c["is_from_fresh"])
+    np.testing.assert_array_equal(np.asarray(ts).view(np.uint8) if "top_scores" not in c["bf16"] else ts,
+                                  c["top_scores"].view(np.uint8) if "top_scores" not in c["bf16"]
+                                  else G.bf16_bits_to_f32(c["top_scores"]))
+    for i, k in enumerate(keys):
+        want = c["gathered"][k]
+        got = g[i]
+        if f"gathered/{k}" in c["bf16"]:
+            want = G.bf16_bits_to_f32(want)
+        assert got.shape == want.shape and got.dtype == want.dtype, (k, got.shape, want.shape)
+        np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+def test_fresh_oracle_ties_nan_and_zero_signs():
+    """Cases the fixtures leave open (at::topk does not order equal scores):
+    the oracle ranks NaN first, treats -0.0 and +0.0 as equal and breaks ties
+    by the lower merged index; a brute-force rank count agrees, and a planted
+    mistake (ties by the higher index) is caught."""
+    rng = np.random.default_rng(5)
+    ms = rng.integers(0, 4, (6, 50)).astype(np.float32)
+    fs = rng.integers(0, 4, (6, 20)).astype(np.float32)
+    ms[0, 3] = np.nan
+    fs[1, 0] = -0.0
+    ms[1, :] = 0.0
+    ts, ti, ff, _ = O.fresh_topk_gather(ms, fs, None, None, 40, [], [])
+    merged = np.concatenate([fs, ms], axis=1)
+    for r in range(6):
+        def beats(a, b):
+            xa, xb = merged[r, a], merged[r, b]
+            if np.isnan(xa) != np.isnan(xb):
+                return bool(np.isnan(xa))
+            if xa != xb and not np.isnan(xa):
+                return bool(xa > xb)
+            return a < b
+        rank = [sum(beats(b, a) for b in range(70) if b != a) for a in range(70)]
+        want = sorted(range(70), key=lambda a: rank[a])[:40]
+        assert ti[r].tolist() == want
+    assert np.isnan(ts[0, 0]) and ti[0, 0] == 20 + 3
+    assert ff.tolist() == (ti < 20).tolist()
+    planted = np.array([sorted(range(70), key=lambda a: (-merged[r, a], -a))[:40] for r in range(2, 6)])
+    assert not np.array_equal(planted, ti[2:])
