@@ -162,6 +162,15 @@ int st_search_plan_bind_widths(st_search_plan* plan,
 int st_search_plan_prepare_device_binding(st_search_plan* plan,
                                           int64_t num_bundles);
 int64_t st_search_plan_device_bytes(const st_search_plan* plan);
+/* Optional: the search calls with this plan copy the blob into
+ * plan_blob_device themselves, in their first kernel, from `pinned_host` --
+ * pinned, device-accessible host memory (hipHostMalloc, e.g. a pinned torch
+ * tensor), 16-byte aligned, holding st_search_plan_blob_bytes bytes of the
+ * blob, unchanged until the stream has run the call.  The caller then does
+ * not copy the blob.  No reference counterpart (the reference copies its
+ * plans with two host-to-device copies per call,
+ * bloom_index_search_cuda.cu:1043-1098). */
+int st_search_plan_upload_source(st_search_plan* plan, const void* pinned_host);
 int64_t st_search_plan_num_queries(const st_search_plan* plan);
 int64_t st_search_plan_blob_bytes(const st_search_plan* plan);
 const void* st_search_plan_blob(const st_search_plan* plan);

@@ -71,9 +71,16 @@ namespace {
 // ------------------------------------------------- width binding on the device
 // The host-side equivalent is st_search_plan_bind_widths (search_plan.cpp).
 
-constexpr int kCensusThreads = 1024;
-constexpr int kCensusCap = 4096;  // distinct widths tracked; more stay unslotted
-constexpr int kCensusCache = 16384;  // bundle widths kept in LDS between passes
+constexpr int kBindThreads = 1024;
+constexpr int kBindGrid = 256;     // workgroups of the binding kernel
+// Distinct widths the census tracks.  An index with more gets no slots at
+// all (every bundle resolves its positions itself): whether the table
+// overflows does not depend on the order of insertions, so every workgroup
+// of the binding kernel reaches the same decision.
+constexpr int kCensusCap = 2048;
+constexpr int kBindChunk = 16;     // bundle widths loaded per thread at a time
+constexpr int kBindHashBatch = 8;  // term hashes loaded per thread at a time
+constexpr int kBindFillBatch = 4;  // template words loaded per thread at a time
 constexpr long long kCensusEmpty = -1;
 
 __device__ __forceinline__ uint32_t census_hash(long long w) {
@@ -104,146 +111,254 @@ __device__ __forceinline__ long long bundle_width(const int64_t* bbo, int64_t i)
   return w > 0 ? w : 0;
 }
 
-// One workgroup: the kMaxWidthSlots most frequent widths get slots (ties to
-// the smaller width), every bundle its slot, and the visiting order groups
-// bundles by slot (a counting sort; order within a slot is arbitrary).
-__global__ __launch_bounds__(kCensusThreads) void width_census_kernel(
-    const int64_t* __restrict__ bbo, int64_t nb, uint32_t* __restrict__ num_slots,
-    int64_t* __restrict__ slot_width, uint32_t* __restrict__ bundle_slot,
-    uint32_t* __restrict__ bundle_order) {
+// Runs f(i, width of bundle i) over all bundles, this thread's share,
+// kBindChunk widths loaded before any is used (the loads overlap).
+template <typename F>
+__device__ __forceinline__ void for_each_width(const int64_t* bbo, int64_t nb, F&& f) {
+  for (int64_t base = 0; base < nb; base += static_cast<int64_t>(kBindThreads) * kBindChunk) {
+    long long w[kBindChunk];
+#pragma unroll
+    for (int j = 0; j < kBindChunk; ++j) {
+      const int64_t i = base + threadIdx.x + static_cast<int64_t>(j) * kBindThreads;
+      w[j] = i < nb ? bundle_width(bbo, i) : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < kBindChunk; ++j) {
+      const int64_t i = base + threadIdx.x + static_cast<int64_t>(j) * kBindThreads;
+      if (i < nb) f(i, w[j]);
+    }
+  }
+}
+
+// Width binding of a device-bound plan (the host-side equivalent is
+// st_search_plan_bind_widths, search_plan.cpp), in two launches.
+//
+// bind_prologue_kernel: workgroups [0, upload_groups) copy the plan's bytes
+// from pinned host memory into the device blob (when the caller left that
+// to the search call); workgroup `upload_groups` takes the census of the
+// bundle widths -- the kMaxWidthSlots most frequent widths get slots, ties
+// to the smaller width -- and writes the slot table, every bundle's slot
+// and, when `bundle_order` is given, a visiting order grouped by slot (a
+// counting sort; order within a slot is arbitrary).  The census reads only
+// the bundle offsets, so it runs while the copy waits on PCIe.
+constexpr int kUploadPerThread = 4;   // 16-byte pieces per thread of an upload group
+
+__global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
+    const uint8_t* __restrict__ host_src, uint8_t* __restrict__ blob, int64_t upload_bytes,
+    uint32_t upload_groups, const int64_t* __restrict__ bbo, int64_t nb,
+    uint32_t* __restrict__ num_slots, int64_t* __restrict__ slot_width,
+    uint32_t* __restrict__ bundle_slot, uint32_t* __restrict__ bundle_order) {
+  const int tid = threadIdx.x;
+  if (blockIdx.x < upload_groups) {
+    typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+    const int64_t vec = upload_bytes / 16;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kBindThreads * kUploadPerThread;
+    v4 v[kUploadPerThread];
+#pragma unroll
+    for (int j = 0; j < kUploadPerThread; ++j) {
+      const int64_t i = base + tid + static_cast<int64_t>(j) * kBindThreads;
+      if (i < vec) v[j] = reinterpret_cast<const v4*>(host_src)[i];
+    }
+#pragma unroll
+    for (int j = 0; j < kUploadPerThread; ++j) {
+      const int64_t i = base + tid + static_cast<int64_t>(j) * kBindThreads;
+      if (i < vec) reinterpret_cast<v4*>(blob)[i] = v[j];
+    }
+    if (blockIdx.x == 0 && tid < 16 && vec * 16 + tid < upload_bytes) blob[vec * 16 + tid] = host_src[vec * 16 + tid];
+    return;
+  }
+  if (num_slots == nullptr) return;  // host-bound plan: nothing to bind
   __shared__ long long keys[kCensusCap];
   __shared__ uint32_t count[kCensusCap];
   __shared__ uint32_t slot_of[kCensusCap];
-  __shared__ uint32_t dense[kCensusCap];
+  __shared__ uint32_t dense[kCensusCap];     // table entry of each distinct width
+  __shared__ long long dense_w[kCensusCap];  // its width and count, stored flat so
+  __shared__ uint32_t dense_c[kCensusCap];   // that the rank loop reads no pointer chain
   __shared__ uint32_t n_dense;
+  __shared__ uint32_t overflow;
+  __shared__ long long s_width[kMaxWidthSlots];
   __shared__ uint32_t cursor[kMaxWidthSlots + 1];
-  __shared__ uint32_t wcache[kCensusCache];  // widths of the first bundles
-  // Width of bundle i: from the LDS cache after the first pass (widths of
-  // 2^32 rows and more are read again).
-  auto width_of = [&](int64_t i) -> long long {
-    const uint32_t c = i < kCensusCache ? wcache[i] : 0xFFFFFFFFu;
-    return c != 0xFFFFFFFFu ? static_cast<long long>(c) : bundle_width(bbo, i);
-  };
-  for (int e = threadIdx.x; e < kCensusCap; e += kCensusThreads) {
+  for (int e = tid; e < kCensusCap; e += kBindThreads) {
     keys[e] = kCensusEmpty;
     count[e] = 0u;
     slot_of[e] = kNoWidthSlot;
   }
-  if (threadIdx.x == 0) n_dense = 0u;
-  if (threadIdx.x <= kMaxWidthSlots) cursor[threadIdx.x] = 0u;
+  if (tid == 0) {
+    n_dense = 0u;
+    overflow = 0u;
+  }
+  if (tid <= kMaxWidthSlots) cursor[tid] = 0u;
   __syncthreads();
-  for (int64_t i = threadIdx.x; i < nb; i += kCensusThreads) {
-    const long long w = bundle_width(bbo, i);
-    if (i < kCensusCache) wcache[i] = w < 0xFFFFFFFFll ? static_cast<uint32_t>(w) : 0xFFFFFFFFu;
+  for_each_width(bbo, nb, [&](int64_t, long long w) {
+    if (overflow) return;  // the outcome is decided
     const int e = census_find(keys, w, true);
     if (e >= 0) atomicAdd(count + e, 1u);
-  }
+    else overflow = 1u;
+  });
   __syncthreads();
-  for (int e = threadIdx.x; e < kCensusCap; e += kCensusThreads)
-    if (keys[e] != kCensusEmpty) dense[atomicAdd(&n_dense, 1u)] = static_cast<uint32_t>(e);
+  if (overflow) {  // no slots: clear the table (census_find then finds nothing)
+    for (int e = tid; e < kCensusCap; e += kBindThreads) keys[e] = kCensusEmpty;
+    __syncthreads();
+  }
+  for (int e = tid; e < kCensusCap; e += kBindThreads) {
+    const long long w = keys[e];
+    if (w != kCensusEmpty) {
+      const uint32_t a = atomicAdd(&n_dense, 1u);
+      dense[a] = static_cast<uint32_t>(e);
+      dense_w[a] = w;
+      dense_c[a] = count[e];
+    }
+  }
   __syncthreads();
   const uint32_t n = n_dense;
-  for (uint32_t a = threadIdx.x; a < n; a += kCensusThreads) {
-    const uint32_t e = dense[a];
-    const uint32_t c = count[e];
-    const long long w = keys[e];
+  for (uint32_t a = tid; a < n; a += kBindThreads) {
+    const uint32_t c = dense_c[a];
+    const long long w = dense_w[a];
     uint32_t rank = 0;
+#pragma unroll 8
     for (uint32_t b = 0; b < n; ++b) {
-      const uint32_t f = dense[b];
-      rank += (count[f] > c || (count[f] == c && keys[f] < w)) ? 1u : 0u;
+      const uint32_t cb = dense_c[b];
+      rank += (cb > c || (cb == c && dense_w[b] < w)) ? 1u : 0u;
     }
     if (rank < static_cast<uint32_t>(kMaxWidthSlots)) {
-      slot_of[e] = rank;
-      slot_width[rank] = w;
+      slot_of[dense[a]] = rank;
+      s_width[rank] = w;
     }
   }
-  if (threadIdx.x == 0) *num_slots = n < static_cast<uint32_t>(kMaxWidthSlots) ? n : kMaxWidthSlots;
   __syncthreads();
-  for (int64_t i = threadIdx.x; i < nb; i += kCensusThreads) {
-    const int e = census_find(keys, width_of(i), false);
+  const uint32_t ns = n < static_cast<uint32_t>(kMaxWidthSlots) ? n : kMaxWidthSlots;
+  if (tid < static_cast<int>(ns)) slot_width[tid] = s_width[tid];
+  for_each_width(bbo, nb, [&](int64_t i, long long w) {
+    const int e = census_find(keys, w, false);
     const uint32_t sl = e >= 0 ? slot_of[e] : kNoWidthSlot;
     bundle_slot[i] = sl;
     atomicAdd(cursor + (sl == kNoWidthSlot ? kMaxWidthSlots : sl), 1u);
-  }
+  });
   __syncthreads();
-  if (threadIdx.x == 0) {  // bucket sizes -> bucket starts
+  static_assert(kMaxWidthSlots == 64, "one wave scans the slot buckets");
+  if (tid < 64) {
     // num_slots[1]: every bundle has a slot, and every slot width is wide
-    bool all_wide = cursor[kMaxWidthSlots] == 0;
-    const uint32_t ns = n < static_cast<uint32_t>(kMaxWidthSlots) ? n : kMaxWidthSlots;
-    for (uint32_t s = 0; s < ns; ++s) all_wide &= wide_width(slot_width[s]);
-    num_slots[1] = all_wide ? 1u : 0u;
-    uint32_t run = 0;
-    for (int b = 0; b <= kMaxWidthSlots; ++b) {
-      const uint32_t c = cursor[b];
-      cursor[b] = run;
-      run += c;
+    const bool narrow = tid < static_cast<int>(ns) && !wide_width(s_width[tid]);
+    const bool all_wide = __ballot(narrow) == 0ull && cursor[kMaxWidthSlots] == 0;
+    // bucket sizes -> bucket starts (exclusive scan over the wave; the
+    // unslotted bucket goes last)
+    const uint32_t c = cursor[tid];
+    uint32_t incl = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t y = __shfl_up(incl, d, 64);
+      if (tid >= d) incl += y;
+    }
+    cursor[tid] = incl - c;
+    if (tid == 63) cursor[kMaxWidthSlots] = incl;
+    if (tid == 0) {
+      num_slots[0] = ns;
+      num_slots[1] = all_wide ? 1u : 0u;
     }
   }
   __syncthreads();
-  for (int64_t i = threadIdx.x; i < nb; i += kCensusThreads) {
-    const int e = census_find(keys, width_of(i), false);
-    const uint32_t sl = e >= 0 ? slot_of[e] : kNoWidthSlot;
-    const uint32_t pos = atomicAdd(cursor + (sl == kNoWidthSlot ? kMaxWidthSlots : sl), 1u);
-    bundle_order[pos] = static_cast<uint32_t>(i);
+  if (bundle_order != nullptr) {
+    for_each_width(bbo, nb, [&](int64_t i, long long w) {
+      const int e = census_find(keys, w, false);
+      const uint32_t sl = e >= 0 ? slot_of[e] : kNoWidthSlot;
+      const uint32_t at = atomicAdd(cursor + (sl == kNoWidthSlot ? kMaxWidthSlots : sl), 1u);
+      bundle_order[at] = static_cast<uint32_t>(i);
+    });
   }
 }
 
-// Position r of a term at width b, as term_positions (search_plan.cpp) and
-// signature_match (bloom_index_search.cpp:40-61) resolve it: over hashes
-// p < hash_k, b_p = (int16)(h[p] % b), repeats skipped, at most k_eff kept,
-// unused slots repeat the first; LDS byte offsets for staged widths, rows
-// relative to the bundle start otherwise.
-__device__ uint32_t device_term_position(const uint64_t* h, int hash_k, int k_eff, int64_t b,
-                                         int r) {
-  int16_t found[kMaxSearchK];
-  int cnt = 0;
-  if (b > 0) {
-    for (int p = 0; p < hash_k && cnt < k_eff; ++p) {
-      const int16_t bp = static_cast<int16_t>(h[p] % static_cast<uint64_t>(b));
-      bool dup = false;
-      for (int j = 0; j < cnt; ++j) dup |= found[j] == bp;
-      if (!dup) found[cnt++] = bp;
+// bind_fill_kernel: workgroup g serves slot g % ns and part g / ns of the
+// slot's width blocks: it resolves the row positions of every batch term at
+// the slot's width once (as signature_match does, bloom_index_search.cpp:
+// 40-61: b_p = (int16)(h[p] % b) over p < hash_k, repeats skipped, at most
+// k_eff kept, unused positions repeat the first) and expands its part of
+// every batch's width-block template.
+__global__ __launch_bounds__(kBindThreads) void bind_fill_kernel(
+    char* __restrict__ blob, uint64_t off_table, uint32_t n_batches, int hash_k, int k_eff, int kp,
+    const uint32_t* __restrict__ num_slots, const int64_t* __restrict__ slot_width) {
+  __shared__ uint32_t pos[kSearchPosSlots];
+  const int tid = threadIdx.x;
+  const uint32_t ns = num_slots[0];
+  if (ns == 0) return;
+  const uint32_t parts = gridDim.x / ns;
+  if (parts == 0 || blockIdx.x >= parts * ns) return;
+  const uint32_t sl = blockIdx.x % ns, part = blockIdx.x / ns;
+  const long long b = slot_width[sl];
+  const FastMod64 fm = make_fastmod_dev(static_cast<uint64_t>(b > 0 ? b : 1));
+  const bool staged = b <= kSearchTileRows, wide = wide_width(b);
+  const uint32_t ones = staged ? static_cast<uint32_t>(kSearchOnesRow) * 256u
+                        : wide ? static_cast<uint32_t>(kWideOnesRow) * kWideSliceBytes
+                               : static_cast<uint32_t>(kPosOnes);
+  const uint32_t zeros = staged ? static_cast<uint32_t>(kSearchZerosRow) * 256u
+                         : wide ? static_cast<uint32_t>(kWideZerosRow) * kWideSliceBytes
+                                : static_cast<uint32_t>(kPosZeros);
+  const uint64_t* table = reinterpret_cast<const uint64_t*>(blob + off_table);
+  for (uint32_t t = 0; t < n_batches; ++t) {
+    const uint64_t* e = table + static_cast<uint64_t>(t) * kBindTableWords;
+    const uint32_t* tmpl = reinterpret_cast<const uint32_t*>(blob + e[0]);
+    const uint32_t* code = reinterpret_cast<const uint32_t*>(blob + e[1]);
+    const uint64_t* hashes = reinterpret_cast<const uint64_t*>(blob + e[2]);
+    uint32_t* bound = reinterpret_cast<uint32_t*>(blob + e[3]);
+    const uint32_t words = static_cast<uint32_t>(e[4]);
+    const uint32_t n_terms = static_cast<uint32_t>(e[5]);
+    if (words == 0) continue;
+    __syncthreads();  // the previous batch's positions are no longer read
+    for (uint32_t u = tid; u < n_terms; u += kBindThreads) {
+      int16_t found[kMaxSearchK];
+      int cnt = 0;
+      if (b > 0) {
+        const uint64_t* h = hashes + static_cast<uint64_t>(u) * hash_k;
+        for (int p0 = 0; p0 < hash_k && cnt < k_eff; p0 += kBindHashBatch) {
+          // the batch's hashes are loaded before any is used (one wait)
+          uint64_t hv[kBindHashBatch];
+#pragma unroll
+          for (int j = 0; j < kBindHashBatch; ++j) hv[j] = p0 + j < hash_k ? h[p0 + j] : 0;
+#pragma unroll
+          for (int j = 0; j < kBindHashBatch; ++j) {
+            if (p0 + j >= hash_k || cnt >= k_eff) break;
+            const int16_t bp = static_cast<int16_t>(fast_mod(hv[j], fm));
+            bool dup = false;
+            for (int q = 0; q < cnt; ++q) dup |= found[q] == bp;
+            if (!dup) found[cnt++] = bp;
+          }
+        }
+      }
+      for (int r = 0; r < kp; ++r) {
+        const int16_t row = cnt == 0 ? 0 : (r < cnt ? found[r] : found[0]);
+        uint32_t v;
+        if (cnt == 0) v = zeros;
+        else if (staged) v = static_cast<uint32_t>(row) * 256u;
+        else if (wide) v = static_cast<uint32_t>(row) * kWideSliceBytes;
+        else v = static_cast<uint32_t>(static_cast<int32_t>(row));
+        pos[u * kp + r] = v;
+      }
+    }
+    __syncthreads();
+    const uint32_t w0 = static_cast<uint32_t>(static_cast<uint64_t>(words) * part / parts);
+    const uint32_t w1 = static_cast<uint32_t>(static_cast<uint64_t>(words) * (part + 1) / parts);
+    uint32_t* dst = bound + static_cast<uint64_t>(sl) * words;
+    for (uint32_t i0 = w0; i0 < w1; i0 += kBindThreads * kBindFillBatch) {
+      // every load of the batch is issued before any value is used
+      uint32_t c[kBindFillBatch], t[kBindFillBatch];
+#pragma unroll
+      for (int j = 0; j < kBindFillBatch; ++j) {
+        const uint32_t i = i0 + tid + j * kBindThreads;
+        c[j] = i < w1 ? code[i] : kTmplCopy;
+        t[j] = i < w1 ? tmpl[i] : 0u;
+      }
+#pragma unroll
+      for (int j = 0; j < kBindFillBatch; ++j) {
+        const uint32_t i = i0 + tid + j * kBindThreads;
+        if (i >= w1) break;
+        uint32_t v;
+        if (c[j] == kTmplCopy) v = t[j];
+        else if (c[j] == kTmplOnes) v = ones;
+        else if (c[j] == kTmplZeros) v = zeros;
+        else v = pos[((c[j] >> 4) - 1u) * kp + (c[j] & 15u)];
+        dst[i] = v;
+      }
     }
   }
-  const int16_t row = cnt == 0 ? 0 : (r < cnt ? found[r] : found[0]);
-  if (b <= kSearchTileRows)
-    return static_cast<uint32_t>(cnt == 0 ? kSearchZerosRow : row) * 256u;
-  if (wide_width(b))
-    return static_cast<uint32_t>(cnt == 0 ? kWideZerosRow : row) * kWideSliceBytes;
-  return cnt == 0 ? static_cast<uint32_t>(kPosZeros)
-                  : static_cast<uint32_t>(static_cast<int32_t>(row));
-}
-
-// Expands a batch's width-block template for every slot.
-__global__ void bind_fill_kernel(const uint32_t* __restrict__ tmpl,
-                                 const uint32_t* __restrict__ code, uint32_t words,
-                                 const uint64_t* __restrict__ hashes, int hash_k, int k_eff,
-                                 const uint32_t* __restrict__ num_slots,
-                                 const int64_t* __restrict__ slot_width,
-                                 uint32_t* __restrict__ bound) {
-  const uint32_t sl = blockIdx.y;
-  if (sl >= *num_slots) return;
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= words) return;
-  const int64_t b = slot_width[sl];
-  const uint32_t c = code[i];
-  uint32_t v;
-  if (c == kTmplCopy) {
-    v = tmpl[i];
-  } else if (c == kTmplOnes) {
-    v = b <= kSearchTileRows ? static_cast<uint32_t>(kSearchOnesRow) * 256u
-        : wide_width(b)      ? static_cast<uint32_t>(kWideOnesRow) * kWideSliceBytes
-                             : static_cast<uint32_t>(kPosOnes);
-  } else if (c == kTmplZeros) {
-    v = b <= kSearchTileRows ? static_cast<uint32_t>(kSearchZerosRow) * 256u
-        : wide_width(b)      ? static_cast<uint32_t>(kWideZerosRow) * kWideSliceBytes
-                             : static_cast<uint32_t>(kPosZeros);
-  } else {
-    const uint32_t t = (c >> 4) - 1u;
-    v = device_term_position(hashes + static_cast<uint64_t>(t) * hash_k, hash_k, k_eff, b,
-                             static_cast<int>(c & 15u));
-  }
-  bound[static_cast<uint64_t>(sl) * words + i] = v;
 }
 
 // Validates the arguments and launches the search kernel once per batch.
@@ -262,28 +377,41 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
   const char* blob = static_cast<const char*>(plan_blob_device);
   const bool bound = plan->bound_bundles >= 0;
   auto at = [&](uint64_t off) { return reinterpret_cast<const uint32_t*>(blob + off); };
-  if (plan->device_bind) {
-    // Width binding on the device, ahead of the search on the same stream.
+  // The plan's bytes, when the caller left the copy to this call
+  // (st_search_plan_upload_source), and the width census of a device-bound
+  // plan: one launch, ahead of the search on the same stream.
+  const uint64_t upload_bytes = plan->upload_source != nullptr ? plan->blob.size() : 0;
+  const uint32_t upload_groups = static_cast<uint32_t>(
+      (upload_bytes + 16ull * kBindThreads * kUploadPerThread - 1) / (16ull * kBindThreads * kUploadPerThread));
+  if (upload_bytes != 0 || plan->device_bind) {
     char* dev = const_cast<char*>(blob);
-    auto* nsl = reinterpret_cast<uint32_t*>(dev + plan->off_num_slots);
-    auto* sw = reinterpret_cast<int64_t*>(dev + plan->off_slot_width);
-    hipLaunchKernelGGL(width_census_kernel, dim3(1), dim3(kCensusThreads), 0, stream,
-                       bundle_b_offsets, num_bundles, nsl, sw,
-                       reinterpret_cast<uint32_t*>(dev + plan->off_bundle_slot),
-                       reinterpret_cast<uint32_t*>(dev + plan->off_bundle_order));
+    // The visiting order is needed only by batches outside the quad-lane
+    // path (the quad instance visits bundles in index order).
+    bool need_order = false;
+    for (const SearchBatch& bt : plan->batches)
+      need_order |= !(bt.stream_words != 0 && bt.stream_words <= kQuadStreamMaxWords &&
+                      stream_block_records(std::max(plan->k_eff, 1)) >= 4);
+    const bool db = plan->device_bind;
+    hipLaunchKernelGGL(bind_prologue_kernel, dim3(upload_groups + (db ? 1 : 0)), dim3(kBindThreads), 0,
+                       stream, static_cast<const uint8_t*>(plan->upload_device_src),
+                       reinterpret_cast<uint8_t*>(dev), static_cast<int64_t>(upload_bytes), upload_groups,
+                       bundle_b_offsets, num_bundles,
+                       db ? reinterpret_cast<uint32_t*>(dev + plan->off_num_slots) : nullptr,
+                       db ? reinterpret_cast<int64_t*>(dev + plan->off_slot_width) : nullptr,
+                       db ? reinterpret_cast<uint32_t*>(dev + plan->off_bundle_slot) : nullptr,
+                       db && need_order ? reinterpret_cast<uint32_t*>(dev + plan->off_bundle_order) : nullptr);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
-      throw Error(ST_ERR_HIP, cat("width census launch failed: ", hipGetErrorString(e)));
-    for (const SearchBatch& bt : plan->batches) {
-      if (bt.bound_words == 0) continue;
-      hipLaunchKernelGGL(bind_fill_kernel, dim3((bt.bound_words + 255) / 256, kMaxWidthSlots),
-                         dim3(256), 0, stream, at(bt.off_tmpl), at(bt.off_tmpl_code),
-                         bt.bound_words, reinterpret_cast<const uint64_t*>(blob + bt.off_hashes),
-                         static_cast<int>(plan->hash_k), plan->k_eff, nsl, sw,
-                         reinterpret_cast<uint32_t*>(dev + bt.off_bound));
+      throw Error(ST_ERR_HIP, cat("plan upload / width census launch failed: ", hipGetErrorString(e)));
+    if (db) {
+      hipLaunchKernelGGL(bind_fill_kernel, dim3(kBindGrid), dim3(kBindThreads), 0, stream, dev,
+                         plan->off_bind_table, static_cast<uint32_t>(plan->batches.size()),
+                         static_cast<int>(plan->hash_k), plan->k_eff, plan->kp,
+                         reinterpret_cast<const uint32_t*>(dev + plan->off_num_slots),
+                         reinterpret_cast<const int64_t*>(dev + plan->off_slot_width));
       e = hipGetLastError();
       if (e != hipSuccess)
-        throw Error(ST_ERR_HIP, cat("bind fill launch failed: ", hipGetErrorString(e)));
+        throw Error(ST_ERR_HIP, cat("width binding launch failed: ", hipGetErrorString(e)));
     }
   }
   // Wide bundles (kSearchTileRows < b <= kWideRows, width-bound) have their
@@ -364,6 +492,26 @@ void compact_scan_counts(int64_t* counts, int64_t num_queries, int64_t nch,
 void compact_zero_offsets(int64_t* row_offsets, int64_t n, hipStream_t s);
 
 }  // namespace st
+
+extern "C" int st_search_plan_upload_source(st_search_plan* plan, const void* pinned_host) {
+  using namespace st;
+  return guarded([&] {
+    ST_CHECK(plan != nullptr, "plan is null");
+    if (pinned_host == nullptr) {
+      plan->upload_source = plan->upload_device_src = nullptr;
+      return;
+    }
+    ST_CHECK(reinterpret_cast<uintptr_t>(pinned_host) % 16 == 0,
+             "the pinned plan buffer must be 16-byte aligned");
+    void* dev = nullptr;
+    const hipError_t e = hipHostGetDevicePointer(&dev, const_cast<void*>(pinned_host), 0);
+    ST_CHECK(e == hipSuccess, "the plan buffer is not pinned, device-accessible host memory (",
+             hipGetErrorString(e), ")");
+    ST_CHECK(reinterpret_cast<uintptr_t>(dev) % 16 == 0, "the pinned plan buffer must be 16-byte aligned");
+    plan->upload_source = pinned_host;
+    plan->upload_device_src = dev;
+  });
+}
 
 extern "C" int st_bloom_index_search_batch(
     const int64_t* bloom_index, int64_t bloom_index_numel,

@@ -418,7 +418,66 @@ struct CompileScratch {
   Tree tree;
   std::vector<int> stack;
   std::vector<int> depth;
+  // flat_direct: literals in stack order, and the stack of (kind, first literal)
+  std::vector<CompiledQuery::FlatLit> lits;
+  std::vector<std::pair<uint8_t, uint32_t>> items;
 };
+
+// Direct flat form of a query whose plan is already an OR of AND-groups of
+// terms (nested ANDs / ORs of the same shape included, as the parser's
+// max_sub_queries folding makes them): one pass over the postfix operators,
+// no tree.  Literals are kept in stack order, so the operands an operator
+// pops are one contiguous run: AND joins the run into one group, OR keeps
+// the runs' groups.  Returns false (nothing interned is lost: interning is
+// idempotent) for anything else -- NOT, EMPTY, an AND over an OR, a child
+// count outside [1, stack size], more than kFlatMaxLiterals literals, a
+// malformed plan -- and the general compiler then handles the query (and
+// raises its errors).  The result equals the general DNF of such a plan up
+// to the order of literals within a group and repeated literals, which do
+// not change the OR-of-ANDs value.
+bool flat_direct(const int8_t* ops, int64_t n_ops, const int8_t* offsets, int64_t n_offsets,
+                 const int8_t* hashes, int64_t n_hashes, int64_t hash_k, int k_eff,
+                 TermTable& terms, CompileScratch& cs, CompiledQuery& cq) {
+  if (k_eff == 0 || hash_k <= 0 || n_offsets < n_ops + 1) return false;
+  constexpr uint8_t kLit = 0, kAndGroup = 1, kOrGroups = 2;
+  auto& lits = cs.lits;
+  auto& items = cs.items;
+  lits.clear();
+  items.clear();
+  int64_t term_counter = 0;
+  for (int64_t i = 0; i < n_ops; ++i) {
+    const uint8_t op = static_cast<uint8_t>(ops[i]);
+    if (op == kOpTerm) {
+      if ((term_counter + 1) * hash_k > n_hashes || lits.size() >= kFlatMaxLiterals) return false;
+      const uint32_t t = terms.intern(hashes + 8 * term_counter * hash_k);
+      ++term_counter;
+      items.emplace_back(kLit, static_cast<uint32_t>(lits.size()));
+      lits.push_back(CompiledQuery::FlatLit{t, false, true});
+      continue;
+    }
+    if (op != kOpAnd && op != kOpOr) return false;
+    const int32_t children = load_le<int32_t>(offsets + 4 * (i + 1)) - load_le<int32_t>(offsets + 4 * i);
+    if (children < 1 || static_cast<size_t>(children) > items.size()) return false;
+    const size_t first = items.size() - static_cast<size_t>(children);
+    const uint32_t begin = items[first].second;
+    if (op == kOpAnd) {
+      for (size_t j = first; j < items.size(); ++j)
+        if (items[j].first == kOrGroups) return false;
+      for (size_t l = begin + 1; l < lits.size(); ++l) lits[l].first = false;
+      items.resize(first);
+      items.emplace_back(kAndGroup, begin);
+    } else {
+      items.resize(first);
+      items.emplace_back(kOrGroups, begin);
+    }
+  }
+  if (items.empty()) return false;
+  const uint32_t begin = items.back().second;
+  cq.flat = true;
+  cq.complement = false;
+  cq.lits.assign(lits.begin() + begin, lits.end());
+  return true;
+}
 
 // Decodes query q, builds its tree and returns its program.  Terms are
 // interned in `terms` (ids are batch-local).
@@ -439,6 +498,11 @@ CompiledQuery compile_query(const int8_t* data, int64_t data_len,
   const int8_t* offsets = data + o[2];
   const int8_t* hashes = data + o[6];
   ST_CHECK(n_ops > 0, "query plan ", q, " has no operators");
+  {
+    CompiledQuery cq;
+    if (flat_direct(ops, n_ops, offsets, n_offsets, hashes, n_hashes, hash_k, k_eff, terms, cs, cq))
+      return cq;
+  }
 
   Tree& tree = cs.tree;
   std::vector<int>& stack = cs.stack;
@@ -609,6 +673,7 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
       CompiledQuery cq;
     };
     std::vector<Pending> cur;
+    cur.reserve(static_cast<size_t>(std::min<int64_t>(num_queries, 1 << 16)));
     static thread_local TermTable terms;
     static thread_local CompileScratch scratch;
     terms.hash_k = std::max<int64_t>(hash_k, 0);
@@ -680,6 +745,11 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
         load[w] += cost(i);
       }
       std::vector<uint32_t> wave_off(kSearchWaves + 1, 0), starts, insns;
+      size_t insn_words = 0;
+      for (const Pending& pq : cur)
+        insn_words += 8 + (pq.cq.flat ? 4 * pq.cq.lits.size() : pq.cq.terms.size() + pq.cq.ops.size());
+      insns.reserve(insn_words);
+      starts.reserve(cur.size());
       const uint32_t pos_bytes = static_cast<uint32_t>(plan->kp) * 4;
       for (int w = 0; w < kSearchWaves; ++w) {
         // Within a wave: flat programs round by round, paired neighbour by
@@ -723,9 +793,9 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
       b.off_hashes = blob.size();
       append_bytes(blob, terms.hashes.data(), terms.hashes.size() * 8);
       plan->batches.push_back(b);
-      plan->batch_insns.push_back(insns);
-      plan->batch_starts.push_back(starts);
-      plan->batch_hashes.push_back(terms.hashes);
+      plan->batch_insns.push_back(std::move(insns));
+      plan->batch_starts.push_back(std::move(starts));
+      plan->batch_hashes.push_back(std::move(terms.hashes));
       cur.clear();
       terms.clear();
     };
@@ -875,17 +945,28 @@ void build_block_template(const st_search_plan& plan, SearchBatch& bt,
   bt.stream_off = static_cast<uint32_t>(tmpl.size());
   bt.stream_words = 0;
   bool fits = true;
-  auto word = [&](uint32_t v) {
-    tmpl.push_back(v);
-    code.push_back(kTmplCopy);
-  };
+  // The stream's exact size first, so that it is written in place.
+  size_t stream_total = 0;
+  for (int w = 0; w < kSearchWaves; ++w) {
+    uint32_t n_flat = 0;
+    while (wave_off[w] + n_flat < wave_off[w + 1] && (insns[starts[wave_off[w] + n_flat]] & kFlatForm))
+      ++n_flat;
+    for (uint32_t r0 = 0; r0 < n_flat; r0 += per_block) {
+      const uint32_t n = std::min(per_block, n_flat - r0);
+      uint32_t T = 1;
+      for (uint32_t i = 0; i < n; ++i) T = std::max(T, insns[starts[wave_off[w] + r0 + i]] & 0xFFFFu);
+      stream_total += kRoundHeaderWords + static_cast<size_t>(T) * per_block * srw;
+    }
+  }
+  size_t at = tmpl.size();
+  tmpl.resize(at + stream_total, 0u);
+  code.resize(at + stream_total, kTmplCopy);
+  auto word = [&](uint32_t v) { tmpl[at++] = v; };
   auto record = [&](uint32_t pos_code, uint32_t term, uint32_t flags) {
-    const size_t at = tmpl.size();
-    tmpl.resize(at + srw, 0u);
-    code.resize(at + srw, kTmplCopy);
     for (int r = 0; r < ks; ++r)
       code[at + r] = pos_code == kTmplCopy ? tmpl_position_code(term, r) : pos_code;
     tmpl[at + ks] = flags;
+    at += srw;
   };
   // Group masks instead of flag bits when no literal of the batch's flat
   // programs is negated.
@@ -904,7 +985,7 @@ void build_block_template(const st_search_plan& plan, SearchBatch& bt,
   bt.stream_masks = masks ? 1u : 0u;
   std::vector<uint32_t> flat;
   for (int w = 0; w < kSearchWaves && fits; ++w) {
-    wave_rec[w] = static_cast<uint32_t>(tmpl.size() - bt.stream_off);
+    wave_rec[w] = static_cast<uint32_t>(at - bt.stream_off);
     flat.clear();
     for (uint32_t q = wave_off[w]; q < wave_off[w + 1]; ++q) {
       const uint32_t hdr = insns[starts[q]];
@@ -951,8 +1032,9 @@ void build_block_template(const st_search_plan& plan, SearchBatch& bt,
       }
     }
   }
-  wave_rec[kSearchWaves] = static_cast<uint32_t>(tmpl.size() - bt.stream_off);
+  wave_rec[kSearchWaves] = static_cast<uint32_t>(at - bt.stream_off);
   if (fits && wave_rec[kSearchWaves] > 0) {
+    if (at != tmpl.size()) fail("literal stream size mismatch: ", at, " != ", tmpl.size());
     bt.stream_words = wave_rec[kSearchWaves];
   } else {  // no stream: every program runs from the width block
     bt.stream_masks = 0;
@@ -1235,7 +1317,8 @@ extern "C" int st_search_plan_prepare_device_binding(st_search_plan* plan,
     ST_CHECK(plan->bound_bundles < 0, "plan is already bound to bundle widths");
     ST_CHECK(num_bundles >= 0, "negative bundle count");
     auto& blob = plan->blob;
-    std::vector<uint32_t> bstart, tmpl, code, wave_rec, wave_skip;
+    // working vectors keep their capacity between calls on a thread
+    static thread_local std::vector<uint32_t> bstart, tmpl, code, wave_rec, wave_skip;
     std::vector<RoundList> rounds(plan->batches.size());
     for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
       SearchBatch& bt = plan->batches[bi];
@@ -1255,6 +1338,9 @@ extern "C" int st_search_plan_prepare_device_binding(st_search_plan* plan,
       append_bytes(blob, code.data(), code.size() * 4);
     }
     append_wide_table(*plan, rounds);
+    blob.resize(align_to(blob.size(), 8), 0);
+    plan->off_bind_table = blob.size();
+    blob.resize(blob.size() + 8 * kBindTableWords * plan->batches.size(), 0);
     blob.resize(blob.size() + 256, 0);  // slack for scalar loads
     // The device-written part follows the uploaded bytes.
     uint64_t d = align_to(blob.size(), 256);
@@ -1266,9 +1352,13 @@ extern "C" int st_search_plan_prepare_device_binding(st_search_plan* plan,
     d = align_to(d + 4 * static_cast<uint64_t>(num_bundles), 256);
     plan->off_bundle_order = d;
     d = align_to(d + 4 * static_cast<uint64_t>(num_bundles), 256);
-    for (SearchBatch& bt : plan->batches) {
+    for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
+      SearchBatch& bt = plan->batches[bi];
       bt.off_bound = d;
       d = align_to(d + 4ull * kMaxWidthSlots * bt.bound_words, 256);
+      const uint64_t row[kBindTableWords] = {bt.off_tmpl, bt.off_tmpl_code, bt.off_hashes,
+                                             bt.off_bound, bt.bound_words, bt.num_terms};
+      std::memcpy(blob.data() + plan->off_bind_table + 8 * kBindTableWords * bi, row, sizeof(row));
     }
     patch_wide_table(*plan);
     plan->device_bytes = d + 256;  // slack after the last width block

@@ -190,6 +190,12 @@ constexpr int kWideGroupWords = 12;
 constexpr int kWidePrograms = 16;
 constexpr int kWideMaxRounds = 4;
 
+// Batch table of the device binding kernel (uint64 words at
+// st_search_plan::off_bind_table), per batch: byte offsets of its template,
+// template codes, term hashes and width blocks in the device blob, words per
+// width block, distinct terms.
+constexpr int kBindTableWords = 6;
+
 // Codes of a width-block template word.
 constexpr uint32_t kTmplCopy = 0u;           // the template word itself
 constexpr uint32_t kTmplOnes = 0xFFFFFFFFu;  // the all-ones row at the slot's width
@@ -221,8 +227,13 @@ struct st_search_plan {
   // widths on the device into the part of the device copy past the host blob
   bool device_bind = false;
   uint64_t device_bytes = 0;         // size of the device copy
-  uint64_t off_num_slots = 0;        // uint32[1] (device-written)
+  uint64_t off_num_slots = 0;        // uint32[2] (device-written): slots, all wide
   uint64_t off_slot_width = 0;       // int64[kMaxWidthSlots] (device-written)
+  uint64_t off_bind_table = 0;       // uint64[batches * kBindTableWords]
+  // set by st_search_plan_upload_source: the search calls copy the blob
+  // from this pinned host buffer (device address upload_device_src)
+  const void* upload_source = nullptr;
+  const void* upload_device_src = nullptr;
   // work table of the wide-bundle kernel (0: none), set by either binding
   uint64_t off_wide = 0;
   // host binding: every bundle has a slot and every slot width is wide

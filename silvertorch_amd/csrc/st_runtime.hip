@@ -2,6 +2,8 @@
 // cluster column-geometry kernel.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cstdint>
 #include <string>
 
 #include "st_common.hpp"

@@ -11,6 +11,7 @@
 // The parser is host code on both keys, as in the reference
 // (expression_query_parser_cuda.cu:27-44).
 #include <ATen/ATen.h>
+#include <ATen/core/CachingHostAllocator.h>
 #include <c10/hip/HIPFunctions.h>
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
@@ -144,9 +145,18 @@ struct PlanHolder {
 // Checks, plan compilation, width binding and plan upload shared by the
 // search ops.
 struct PreparedSearch {
-  Tensor index, bbo, blob;
+  Tensor index, bbo, blob;  // blob: device copy of the plan
+  at::DataPtr host_blob;    // pinned copy the search call uploads from
   PlanHolder plan;
   int64_t Q = 0, nb = 0;
+  // Runs after the op's launches: the pinned block goes back to torch's host
+  // allocator, which reuses it only once the stream has passed them.
+  ~PreparedSearch() {
+    if (!host_blob) return;
+    const auto stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(index.device().index());
+    at::getHostAllocator(at::kCUDA)->record_event(host_blob.get(), host_blob.get_context(),
+                                                  stream.unwrap());
+  }
 };
 
 void prepare_search(PreparedSearch& ps, const Tensor& bloom_index_in,
@@ -182,12 +192,19 @@ void prepare_search(PreparedSearch& ps, const Tensor& bloom_index_in,
   // The search call binds the programs to the bundle widths on the device
   // (no copy of the bundle offsets to the host, no synchronisation).
   check_st(st_search_plan_prepare_device_binding(ps.plan.p, ps.nb), "bloom_index_search_batch");
+  // The plan bytes go to pinned memory of torch's host allocator, and the
+  // search call's first kernel copies them to the device on the caller's
+  // stream (no copy-engine hand-off between the previous call's kernels and
+  // this call's); the allocator reuses the pinned block only after that
+  // stream has passed the call.
   const int64_t blob_bytes = st_search_plan_blob_bytes(ps.plan.p);
-  Tensor host = at::empty({blob_bytes}, at::TensorOptions().dtype(at::kByte).pinned_memory(true));
-  std::memcpy(host.data_ptr(), st_search_plan_blob(ps.plan.p), blob_bytes);
+  at::HostAllocator* host_alloc = at::getHostAllocator(at::kCUDA);
+  at::DataPtr host = host_alloc->allocate(static_cast<size_t>(blob_bytes));
+  std::memcpy(host.get(), st_search_plan_blob(ps.plan.p), blob_bytes);
+  check_st(st_search_plan_upload_source(ps.plan.p, host.get()), "bloom_index_search_batch");
   ps.blob = at::empty({st_search_plan_device_bytes(ps.plan.p)},
                       at::TensorOptions().dtype(at::kByte).device(ps.index.device()));
-  ps.blob.narrow(0, 0, blob_bytes).copy_(host, /*non_blocking=*/true);
+  ps.host_blob = std::move(host);
 }
 
 Tensor search_gpu(const Tensor& bloom_index_in, const Tensor& bundle_b_offsets_in,

@@ -44,7 +44,7 @@ def build(ids, offsets, values, b_multiplier: float, k: int):
 
 
 def search(index, bbo, plans_data, plans_offsets, k: int, hash_k: int, bool_mask: bool = False,
-           bind: str | None = None):
+           bind: str | None = None, upload: bool = False):
     """C-ABI search; index / bbo may be numpy arrays or cuda tensors.  bind:
     "host" (st_search_plan_bind_widths), "device"
     (st_search_plan_prepare_device_binding) or "none"; with bind=None all
@@ -66,7 +66,12 @@ def search(index, bbo, plans_data, plans_offsets, k: int, hash_k: int, bool_mask
         plan.prepare_device_binding(nb)
     blob = plan.blob()
     blob_d = None
-    if blob:
+    pinned = None
+    if blob and upload:  # the search call copies the blob from pinned memory itself
+        pinned = torch.frombuffer(bytearray(blob), dtype=torch.uint8).pin_memory()
+        capi.check(L.st_search_plan_upload_source(plan.handle, pinned.data_ptr()))
+        blob_d = torch.full((plan.device_bytes,), 0xEE, dtype=torch.uint8, device="cuda")
+    elif blob:
         blob_d = torch.zeros(plan.device_bytes, dtype=torch.uint8, device="cuda")
         blob_d[:len(blob)] = torch.frombuffer(bytearray(blob), dtype=torch.uint8).cuda()
     q = plan.num_queries

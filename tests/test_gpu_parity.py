@@ -403,6 +403,49 @@ def test_mixed_bundle_kinds_in_one_launch():
                                   O.unpack_bool(want))
 
 
+@pytest.mark.parametrize("bind", ["host", "device", "none"])
+def test_search_copies_its_plan_from_pinned_memory(bind):
+    """st_search_plan_upload_source: the search call's first kernel copies
+    the plan blob from pinned host memory into a device buffer that starts
+    as garbage (0xEE); the output equals the oracle's, packed and bool."""
+    c = G.case("random3")
+    H.note(f"[upload source] bind={bind}")
+    want = O.search_packed(c["index"], c["bundle_b_offsets"], c["plans_data"], c["plans_offsets"], c["k"], c["hash_k"])
+    for bool_mask in (False, True):
+        got = H.search(c["index"], c["bundle_b_offsets"], c["plans_data"], c["plans_offsets"], c["k"], c["hash_k"],
+                       bool_mask, bind=bind, upload=True)
+        np.testing.assert_array_equal(got, O.unpack_bool(want) if bool_mask else want)
+
+
+@pytest.mark.timeout(600)
+def test_more_distinct_widths_than_the_census_holds():
+    """2100 bundles of 2100 distinct widths (1 .. 2102 rows: staged, column-
+    slice and global-memory bundles), more than the device census tracks: no
+    width gets a slot, every bundle resolves its own positions.  Packed and
+    bool outputs against the oracle for host-bound, device-bound and unbound
+    plans (host binding still slots the 64 most frequent widths)."""
+    rng = np.random.default_rng(2100)
+    nb = 2100
+    n = nb * 2048
+    cnt = np.zeros(n, dtype=np.int64)
+    heavy = np.arange(nb) * 2048 + rng.integers(0, 2048, nb)
+    cnt[heavy] = 1 + np.arange(nb)  # width of bundle b: (int)((1 + b) * 1.001)
+    offs = np.concatenate([[0], np.cumsum(cnt)]).astype(np.int64)
+    vals = rng.integers(0, 5000, int(offs[-1])).astype(np.int64)
+    ids = np.array([2], dtype=np.int32)
+    index, bbo = H.build(ids, offs, vals, 1.001, 1)
+    widths = np.diff(bbo)
+    assert len(set(widths.tolist())) == nb and widths.max() > 2048
+    queries = [" OR ".join(f"2:{int(v)}" for v in rng.integers(0, 5000, int(rng.integers(1, 4))))
+               for _ in range(24)] + ["2:1 AND NOT 2:2", ""]
+    pd, po = _plans(queries, 3)
+    H.note(f"[census overflow] bundles={nb} distinct widths={len(set(widths.tolist()))}")
+    want = O.search_packed(index, bbo, pd, po, 1, 3)
+    np.testing.assert_array_equal(H.search(index, bbo, pd, po, 1, 3), want)
+    np.testing.assert_array_equal(H.search(index, bbo, pd, po, 1, 3, bool_mask=True, bind="device")[:, :nb * 64],
+                                  O.unpack_bool(want)[:, :nb * 64])
+
+
 @pytest.mark.parametrize("k,neg,many", [(1, False, False), (3, True, False), (4, False, False),
                                         (4, True, True), (7, True, False)])
 def test_wide_bundle_slices_vs_oracle(k, neg, many):
