@@ -47,6 +47,7 @@ LIB_SOURCES = [
     "bloom_build.hip",
     "bloom_compact.hip",
     "bloom_partial.hip",
+    "bloom_generic.hip",
     "filtered_topk.hip",
     "kmean_ann.hip",
     "fresh_topk.hip",

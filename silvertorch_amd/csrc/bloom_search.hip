@@ -6,6 +6,7 @@
 #include <mutex>
 #include <vector>
 
+#include "bloom_generic.hpp"
 #include "bloom_search_kernel.hpp"
 
 namespace st {
@@ -361,6 +362,10 @@ __global__ __launch_bounds__(kBindThreads) void bind_fill_kernel(
   }
 }
 
+static_assert(kOutPacked == kGenericPacked && kOutBool == kGenericBool &&
+                  kOutCounts == kGenericCounts,
+              "one output-mode numbering for the batch and generic kernels");
+
 // Validates the arguments and launches the search kernel once per batch.
 void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
                    const int64_t* bundle_b_offsets, int64_t num_bundles,
@@ -389,7 +394,8 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
     // path (the quad instance visits bundles in index order).
     bool need_order = false;
     for (const SearchBatch& bt : plan->batches)
-      need_order |= !(bt.stream_words != 0 && bt.stream_words <= kQuadStreamMaxWords &&
+      need_order |= !bt.generic &&
+                    !(bt.stream_words != 0 && bt.stream_words <= kQuadStreamMaxWords &&
                       stream_block_records(std::max(plan->k_eff, 1)) >= 4);
     const bool db = plan->device_bind;
     hipLaunchKernelGGL(bind_prologue_kernel, dim3(upload_groups + (db ? 1 : 0)), dim3(kBindThreads), 0,
@@ -428,7 +434,15 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
       if (!any) wide_fn = nullptr;
     }
   }
-  for (const SearchBatch& bt : plan->batches) {
+  for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
+    const SearchBatch& bt = plan->batches[bi];
+    if (bt.generic) {
+      launch_generic_batch(bloom_index, bloom_index_numel, bundle_b_offsets, num_bundles,
+                           plan_blob_device, bt, plan->batch_starts[bi], plan->batch_insns[bi],
+                           plan->k_eff, static_cast<int>(plan->hash_k), plan->kp, mode, out,
+                           counts, num_docs, stream);
+      continue;
+    }
     // 2 tells the kernel that every program of the batch is in the stream,
     // so that wide bundles need nothing from it
     uint32_t wide_flag = 0;

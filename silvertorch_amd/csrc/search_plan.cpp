@@ -54,8 +54,6 @@ struct Tree {
   int kid(int id, int j) const { return kids[nodes[id].kb + j]; }
 };
 
-// Deepest nesting a query may have; recursion over the tree is bounded by it.
-constexpr int kMaxPlanDepth = 4096;
 // Deepest subtree the flat-form search descends into.
 constexpr int kMaxFlatDepth = 64;
 
@@ -139,16 +137,18 @@ int add_const(Tree& t, bool ones) {
   return t.add(k);
 }
 
-// Simplifies in place (flatten same-kind children, drop double negation) and
-// computes `need`.  Returns the id that replaces `id`.
-int normalize(Tree& t, int id) {
+// Simplifies one node whose children are already simplified (their ids in
+// `repl`): flattens same-kind children, drops double negation, folds
+// constants under NOT, orders the children and computes `need`.  Returns
+// the id that replaces `id`.
+int normalize_node(Tree& t, int id, const std::vector<int>& repl) {
   const NodeKind kind = t.nodes[id].kind;
   if (kind == NodeKind::kTerm || kind == NodeKind::kConst) {
     t.nodes[id].need = 0;
     return id;
   }
   if (kind == NodeKind::kNot) {
-    const int c = normalize(t, t.kid(id, 0));
+    const int c = repl[t.kid(id, 0)];
     if (t.nodes[c].kind == NodeKind::kNot) return t.kid(c, 0);
     if (t.nodes[c].kind == NodeKind::kConst) return add_const(t, !t.nodes[c].ones);
     t.kids[t.nodes[id].kb] = c;
@@ -156,10 +156,7 @@ int normalize(Tree& t, int id) {
     return id;
   }
   const int kb = t.nodes[id].kb, kn = t.nodes[id].kn;
-  for (int j = 0; j < kn; ++j) {
-    const int c = normalize(t, t.kids[kb + j]);
-    t.kids[kb + j] = c;
-  }
+  for (int j = 0; j < kn; ++j) t.kids[kb + j] = repl[t.kids[kb + j]];
   // Flattened child list, appended to the pool.
   const int fb = static_cast<int>(t.kids.size());
   for (int j = 0; j < kn; ++j) {
@@ -177,21 +174,25 @@ int normalize(Tree& t, int id) {
   const int fn = static_cast<int>(t.kids.size()) - fb;
   if (fn == 0) return add_const(t, kind == NodeKind::kAnd);
   // Evaluation order: the most demanding subtree first, the other subtrees
-  // by decreasing demand, leaves last (stable insertion sort: lists are short).
+  // by decreasing demand, leaves last (stable: equal demands keep their order).
   auto before = [&](int a, int b) {
     const bool la = is_leaf(t, a), lb = is_leaf(t, b);
     if (la != lb) return !la;
     return t.nodes[a].need > t.nodes[b].need;
   };
   int* f = t.kids.data() + fb;
-  for (int i = 1; i < fn; ++i) {
-    const int v = f[i];
-    int j = i;
-    while (j > 0 && before(v, f[j - 1])) {
-      f[j] = f[j - 1];
-      --j;
+  if (fn > 32) {
+    std::stable_sort(f, f + fn, before);
+  } else {  // insertion sort (stable; child lists are short)
+    for (int i = 1; i < fn; ++i) {
+      const int v = f[i];
+      int j = i;
+      while (j > 0 && before(v, f[j - 1])) {
+        f[j] = f[j - 1];
+        --j;
+      }
+      f[j] = v;
     }
-    f[j] = v;
   }
   int need = t.nodes[f[0]].need;
   for (int i = 1; i < fn; ++i) {
@@ -203,10 +204,34 @@ int normalize(Tree& t, int id) {
   return id;
 }
 
+// Simplifies the tree under `root` bottom-up with an explicit stack (no
+// recursion: plans may nest without limit).  Returns the new root.
+int normalize(Tree& t, int root, std::vector<int>& repl, std::vector<std::pair<int, int>>& st) {
+  repl.assign(t.nodes.size(), -1);
+  st.clear();
+  st.emplace_back(root, 0);
+  while (!st.empty()) {
+    const int id = st.back().first;
+    const int j = st.back().second;
+    const NodeKind kind = t.nodes[id].kind;
+    const int kn = (kind == NodeKind::kAnd || kind == NodeKind::kOr || kind == NodeKind::kNot)
+                       ? t.nodes[id].kn : 0;
+    if (j < kn) {
+      st.back().second = j + 1;
+      st.emplace_back(t.kid(id, j), 0);
+      continue;
+    }
+    repl[id] = normalize_node(t, id, repl);  // ids on the stack are nodes of the built tree
+    st.pop_back();
+  }
+  return repl[root];
+}
+
 struct CompiledQuery {
   std::vector<uint32_t> terms;  // stack form: term ids in consumption order
   std::vector<uint32_t> ops;    // stack form: operations
   int need = 0;
+  bool generic = false;         // stack form beyond the batch kernels' limits
   bool flat = false;            // flat form: OR of AND-groups
   bool complement = false;
   struct FlatLit {
@@ -387,28 +412,50 @@ void emit_leaf(const Tree& t, int id, uint32_t mode, CompiledQuery& out) {
   }
 }
 
-void emit(const Tree& t, int id, CompiledQuery& out) {
-  if (is_leaf(t, id)) {
-    emit_leaf(t, id, kModeSet, out);
-    return;
-  }
-  const Node& n = t.nodes[id];
-  if (n.kind == NodeKind::kNot) {
-    emit(t, t.kid(id, 0), out);
-    out.ops.push_back(encode_insn(kInsNot, 0, false));
-    return;
-  }
-  const uint32_t mode = n.kind == NodeKind::kAnd ? kModeAnd : kModeOr;
-  emit(t, t.kid(id, 0), out);
-  for (int i = 1; i < n.kn; ++i) {
-    const int c = t.kid(id, i);
-    if (is_leaf(t, c)) {
-      emit_leaf(t, c, mode, out);
-    } else {
-      out.ops.push_back(encode_insn(kInsPush, 0, false));
-      emit(t, c, out);
-      out.ops.push_back(encode_insn(kInsPop, mode, false));
+// Stack-form program of the tree under `root`: a leaf is loaded into the
+// accumulator; a NOT complements it; an AND / OR evaluates its first child
+// into the accumulator and combines each further child -- a leaf directly,
+// a subtree by PUSH, the subtree, POP.  Explicit stack of (node, state):
+// state -1 = not started, else (next child << 1) | (a POP is due).
+void emit(const Tree& t, int root, CompiledQuery& out, std::vector<std::pair<int, int>>& st) {
+  st.clear();
+  st.emplace_back(root, -1);
+  while (!st.empty()) {
+    const int id = st.back().first;
+    const int state = st.back().second;
+    if (state == -1) {
+      if (is_leaf(t, id)) {
+        emit_leaf(t, id, kModeSet, out);
+        st.pop_back();
+        continue;
+      }
+      st.back().second = 1 << 1;
+      st.emplace_back(t.kid(id, 0), -1);
+      continue;
     }
+    const Node& n = t.nodes[id];
+    if (n.kind == NodeKind::kNot) {
+      out.ops.push_back(encode_insn(kInsNot, 0, false));
+      st.pop_back();
+      continue;
+    }
+    const uint32_t mode = n.kind == NodeKind::kAnd ? kModeAnd : kModeOr;
+    if (state & 1) out.ops.push_back(encode_insn(kInsPop, mode, false));
+    int next = state >> 1;
+    bool descended = false;
+    for (; next < n.kn; ++next) {
+      const int c = t.kid(id, next);
+      if (is_leaf(t, c)) {
+        emit_leaf(t, c, mode, out);
+        continue;
+      }
+      out.ops.push_back(encode_insn(kInsPush, 0, false));
+      st.back().second = ((next + 1) << 1) | 1;
+      st.emplace_back(c, -1);
+      descended = true;
+      break;
+    }
+    if (!descended) st.pop_back();
   }
 }
 
@@ -417,7 +464,8 @@ void emit(const Tree& t, int id, CompiledQuery& out) {
 struct CompileScratch {
   Tree tree;
   std::vector<int> stack;
-  std::vector<int> depth;
+  std::vector<int> repl;                     // normalize: replacement of each node
+  std::vector<std::pair<int, int>> walk;     // normalize / emit: explicit traversal stack
   // flat_direct: literals in stack order, and the stack of (kind, first literal)
   std::vector<CompiledQuery::FlatLit> lits;
   std::vector<std::pair<uint8_t, uint32_t>> items;
@@ -506,10 +554,8 @@ CompiledQuery compile_query(const int8_t* data, int64_t data_len,
 
   Tree& tree = cs.tree;
   std::vector<int>& stack = cs.stack;
-  std::vector<int>& depth = cs.depth;  // nesting depth of each stack entry
   tree.clear();
   stack.clear();
-  depth.clear();
   int64_t term_counter = 0;
   auto child_count = [&](int64_t i) -> int32_t {
     ST_CHECK(i + 1 < n_offsets, "query plan ", q, ": operator ", i,
@@ -518,12 +564,7 @@ CompiledQuery compile_query(const int8_t* data, int64_t data_len,
     return load_le<int32_t>(offsets + 4 * (i + 1)) -
            load_le<int32_t>(offsets + 4 * i);
   };
-  auto push = [&](const Node& n, int d) {
-    ST_CHECK(d <= kMaxPlanDepth, "query plan ", q, " nests operators more than ",
-             kMaxPlanDepth, " levels deep");
-    stack.push_back(tree.add(n));
-    depth.push_back(d);
-  };
+  auto push = [&](const Node& n) { stack.push_back(tree.add(n)); };
   for (int64_t i = 0; i < n_ops; ++i) {
     const uint8_t op = static_cast<uint8_t>(ops[i]);
     switch (op) {
@@ -542,14 +583,14 @@ CompiledQuery compile_query(const int8_t* data, int64_t data_len,
           n.term = terms.intern(hashes + 8 * term_counter * hash_k);
         }
         ++term_counter;
-        push(n, 1);
+        push(n);
         break;
       }
       case kOpEmpty: {
         Node n;
         n.kind = NodeKind::kConst;
         n.ones = true;
-        push(n, 1);
+        push(n);
         break;
       }
       case kOpAnd:
@@ -563,14 +604,11 @@ CompiledQuery compile_query(const int8_t* data, int64_t data_len,
         n.kind = op == kOpAnd ? NodeKind::kAnd : NodeKind::kOr;
         n.kb = static_cast<int>(tree.kids.size());
         n.kn = children;
-        int d = 0;
         for (int32_t j = 0; j < children; ++j) {  // top of the stack first
           tree.kids.push_back(stack.back());
-          d = std::max(d, depth.back());
           stack.pop_back();
-          depth.pop_back();
         }
-        push(n, d + 1);
+        push(n);
         break;
       }
       case kOpNot: {
@@ -584,10 +622,8 @@ CompiledQuery compile_query(const int8_t* data, int64_t data_len,
         n.kb = static_cast<int>(tree.kids.size());
         n.kn = 1;
         tree.kids.push_back(stack.back());
-        const int d = depth.back();
         stack.pop_back();
-        depth.pop_back();
-        push(n, d + 1);
+        push(n);
         break;
       }
       default:
@@ -595,16 +631,20 @@ CompiledQuery compile_query(const int8_t* data, int64_t data_len,
     }
   }
   ST_CHECK(!stack.empty(), "query plan ", q, " leaves an empty stack");
-  const int root = normalize(tree, stack.back());
+  const int root = normalize(tree, stack.back(), cs.repl, cs.walk);
   CompiledQuery cq;
   if (try_flat(tree, root, static_cast<int>(term_counter), cq)) return cq;
-  emit(tree, root, cq);
+  emit(tree, root, cq, cs.walk);
   cq.need = tree.nodes[root].need;
-  ST_CHECK(cq.need <= kSearchMaxStack, "query plan ", q, " needs ", cq.need,
-           " stack slots; this build evaluates at most ", kSearchMaxStack);
-  ST_CHECK(cq.terms.size() <= kMaxTermsPerQuery && cq.ops.size() <= kMaxOpsPerQuery,
+  // Children are ordered by demand, so a program needs at most about
+  // log2(leaves) + 1 slots: within the size limits below, at most 30.
+  ST_CHECK(cq.need <= kGenericMaxStack, "query plan ", q, " needs ", cq.need,
+           " stack slots; this build evaluates at most ", kGenericMaxStack);
+  ST_CHECK(cq.terms.size() < kGenericMaxTerms && cq.ops.size() < kGenericMaxTerms,
            "query plan ", q, " is too long (", cq.terms.size(), " terms, ",
            cq.ops.size(), " operations)");
+  cq.generic = cq.need > kSearchMaxStack || cq.terms.size() > kMaxTermsPerQuery ||
+               cq.ops.size() > kMaxOpsPerQuery;
   return cq;
 }
 
@@ -633,6 +673,34 @@ void append_bytes(std::vector<uint8_t>& blob, const void* p, size_t n) {
   const uint8_t* b = static_cast<const uint8_t*>(p);
   blob.insert(blob.end(), b, b + n);
   while (blob.size() % 16) blob.push_back(0);
+}
+
+}  // namespace
+}  // namespace st
+
+namespace st {
+namespace {
+
+// Appends query `row`'s program (search_plan.hpp layouts), 16-byte aligned;
+// returns its first word.  Term references are term * pos_bytes.
+uint32_t append_program(std::vector<uint32_t>& insns, const CompiledQuery& cq, uint32_t row,
+                        uint32_t pos_bytes, bool paired) {
+  while (insns.size() % 4) insns.push_back(0);
+  const uint32_t start = static_cast<uint32_t>(insns.size());
+  if (cq.flat) {
+    insns.insert(insns.end(),
+                 {static_cast<uint32_t>(cq.lits.size()) | kFlatForm |
+                      (cq.complement ? kFlatComplement : 0u) | (paired ? kPairedWithNext : 0u),
+                  row, 0u, 0u});
+    for (const auto& l : cq.lits)
+      insns.insert(insns.end(), {l.term * pos_bytes, l.neg ? ~0u : 0u, l.first ? ~0u : 0u, 0u});
+  } else {
+    insns.insert(insns.end(), {static_cast<uint32_t>(cq.terms.size()), row,
+                               static_cast<uint32_t>(cq.ops.size()), 0u});
+    for (uint32_t t : cq.terms) insns.push_back(t * pos_bytes);
+    insns.insert(insns.end(), cq.ops.begin(), cq.ops.end());
+  }
+  return start;
 }
 
 }  // namespace
@@ -760,26 +828,8 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
         for (size_t li = 0; li < list.size(); ++li) {
           const int i = list[li];
           const CompiledQuery& cq = cur[i].cq;
-          while (insns.size() % 4) insns.push_back(0);  // 16-byte aligned programs
-          starts.push_back(static_cast<uint32_t>(insns.size()));
-          const uint32_t row = static_cast<uint32_t>(cur[i].row);
-          const bool paired = cq.flat && li % 2 == 0 && li + 1 < n_flat;
-          if (cq.flat) {
-            insns.insert(insns.end(),
-                         {static_cast<uint32_t>(cq.lits.size()) | kFlatForm |
-                              (cq.complement ? kFlatComplement : 0u) |
-                              (paired ? kPairedWithNext : 0u),
-                          row, 0u, 0u});
-            for (const auto& l : cq.lits) {
-              insns.insert(insns.end(), {l.term * pos_bytes, l.neg ? ~0u : 0u,
-                                         l.first ? ~0u : 0u, 0u});
-            }
-          } else {
-            insns.insert(insns.end(), {static_cast<uint32_t>(cq.terms.size()), row,
-                                       static_cast<uint32_t>(cq.ops.size()), 0u});
-            for (uint32_t t : cq.terms) insns.push_back(t * pos_bytes);
-            insns.insert(insns.end(), cq.ops.begin(), cq.ops.end());
-          }
+          starts.push_back(append_program(insns, cq, static_cast<uint32_t>(cur[i].row), pos_bytes,
+                                          cq.flat && li % 2 == 0 && li + 1 < n_flat));
         }
         wave_off[w + 1] = static_cast<uint32_t>(starts.size());
       }
@@ -800,25 +850,58 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
       terms.clear();
     };
 
+    // Queries beyond the batch kernels' limits (stack depth, program size,
+    // or more distinct terms than a batch's position area holds on their
+    // own) each become a generic batch, after the regular ones.
+    std::vector<int64_t> generic_q;
     for (int64_t q = 0; q < num_queries; ++q) {
       CompiledQuery cq = compile_query(plans_data, plans_data_len,
                                        plans_offsets, q, hash_k,
                                        plan->k_eff, terms, scratch);
-      if (static_cast<int64_t>(terms.size()) > term_capacity) {
+      if (!cq.generic && static_cast<int64_t>(terms.size()) > term_capacity) {
         terms.rollback();
         flush();
         cq = compile_query(plans_data, plans_data_len, plans_offsets, q,
                            hash_k, plan->k_eff, terms, scratch);
-        ST_CHECK(static_cast<int64_t>(terms.size()) <= term_capacity,
-                 "query plan ", q, " has ", terms.size(),
-                 " distinct terms; at most ", term_capacity,
-                 " fit one search pass at k = ", plan->k_eff);
+      }
+      if (cq.generic || static_cast<int64_t>(terms.size()) > term_capacity) {
+        terms.rollback();
+        generic_q.push_back(q);
+        continue;
       }
       terms.commit();
       plan->max_stack = std::max(plan->max_stack, cq.need);
       cur.push_back(Pending{q, std::move(cq)});
     }
     flush();
+    for (const int64_t q : generic_q) {
+      terms.clear();
+      const CompiledQuery cq = compile_query(plans_data, plans_data_len, plans_offsets, q, hash_k,
+                                             plan->k_eff, terms, scratch);
+      plan->max_stack = std::max(plan->max_stack, cq.need);
+      SearchBatch b;
+      b.generic = true;
+      b.num_slots = 1;
+      b.num_terms = terms.size();
+      std::vector<uint32_t> wave_off(kSearchWaves + 1, 1u), starts, insns;
+      wave_off[0] = 0;
+      starts.push_back(append_program(insns, cq, static_cast<uint32_t>(q),
+                                      static_cast<uint32_t>(plan->kp) * 4, false));
+      auto& blob = plan->blob;
+      b.off_wave = blob.size();
+      append_bytes(blob, wave_off.data(), wave_off.size() * 4);
+      b.off_insn_start = blob.size();
+      append_bytes(blob, starts.data(), starts.size() * 4);
+      b.off_insns = blob.size();
+      append_bytes(blob, insns.data(), insns.size() * 4);
+      b.off_hashes = blob.size();
+      append_bytes(blob, terms.hashes.data(), terms.hashes.size() * 8);
+      plan->batches.push_back(b);
+      plan->batch_insns.push_back(std::move(insns));
+      plan->batch_starts.push_back(std::move(starts));
+      plan->batch_hashes.push_back(std::move(terms.hashes));
+    }
+    terms.clear();
     plan->blob.resize(plan->blob.size() + 256, 0);  // slack for scalar loads
     *out = plan.release();
   });
@@ -1100,7 +1183,7 @@ void append_wide_table(st_search_plan& plan, const std::vector<RoundList>& round
   const int k = plan.k_eff;
   if (k < 1 || k > 7 || plan.batches.empty()) return;
   for (const SearchBatch& bt : plan.batches)
-    if (bt.stream_words == 0) return;
+    if (!bt.generic && bt.stream_words == 0) return;
   const int rg = kWidePrograms / stream_block_records(k);
   struct Group {
     uint32_t batch, steps;
@@ -1268,6 +1351,7 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
     std::vector<RoundList> rounds(plan->batches.size());
     for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
       SearchBatch& bt = plan->batches[bi];
+      if (bt.generic) continue;  // no width blocks: the generic kernel resolves positions
       const auto& insns = plan->batch_insns[bi];
       const auto& starts = plan->batch_starts[bi];
       const auto& hashes = plan->batch_hashes[bi];
@@ -1322,6 +1406,7 @@ extern "C" int st_search_plan_prepare_device_binding(st_search_plan* plan,
     std::vector<RoundList> rounds(plan->batches.size());
     for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
       SearchBatch& bt = plan->batches[bi];
+      if (bt.generic) continue;  // no width blocks: the generic kernel resolves positions
       build_block_template(*plan, bt, plan->batch_insns[bi], plan->batch_starts[bi], bstart,
                            tmpl, code, wave_rec, wave_skip);
       stream_rounds(tmpl, bt, plan->k_eff, rounds[bi]);

@@ -73,8 +73,21 @@ inline uint32_t encode_insn(uint32_t op, uint32_t mode, bool neg) {
   return op | (mode << 3) | (static_cast<uint32_t>(neg) << 5);
 }
 
+// Largest program the batch kernels run; larger ones, and programs needing
+// more than kSearchMaxStack slots, run in generic batches (one query each,
+// evaluated by the generic kernel with its positions resolved per lane).
 constexpr uint32_t kMaxTermsPerQuery = 0xFFFF;
 constexpr uint32_t kMaxOpsPerQuery = 0x7FFF;
+constexpr int kGenericMaxStack = 32;
+// Term and operation counts of a generic program stay below this (the
+// stack-form header's term count keeps clear of the flag bits).
+constexpr uint32_t kGenericMaxTerms = 1u << 29;
+
+// Term count of a program header (stack form: the whole word below the
+// flags; flat form: the low 16 bits).
+constexpr uint32_t program_terms(uint32_t hdr) {
+  return (hdr & (1u << 31)) ? (hdr & 0xFFFFu) : (hdr & (kGenericMaxTerms - 1u));
+}
 
 // Positions stored per term in LDS, padded so a term's list is read with
 // 16-byte loads.
@@ -136,6 +149,7 @@ inline int stream_block_records(int k_eff) { return 32 / bound_record_words(k_ef
 // One kernel launch worth of queries.  Offsets are byte offsets into the
 // plan blob.
 struct SearchBatch {
+  bool generic = false;     // one query for the generic kernel (no width blocks)
   uint32_t num_slots = 0;   // queries in this batch
   uint32_t num_terms = 0;   // distinct terms in this batch
   uint64_t off_wave = 0;    // uint32[kSearchWaves + 1]: slot range per wave

@@ -130,15 +130,21 @@ def test_plan_compiler_limits():
 
 
 def test_plan_compiler_nesting_and_identity_operators():
-    # 5000 nested NOTs around one term: deeper than the compiler's recursion
-    # bound, rejected with an error instead of exhausting the host stack.
-    n = 5000
+    # Nesting has no limit (the compiler walks trees with explicit stacks, as
+    # the reference's std::stack evaluation has none): 100000 nested NOTs
+    # around one term, and a 20000-deep left chain (((t0 AND t1) OR t2) AND
+    # t3) ... of distinct terms (more than a batch's position area holds: a
+    # generic batch).
+    n = 100_000
     data, offs = _plan([4] + [3] * n, list(range(n + 2)), list(range(7)))
-    with pytest.raises(capi.StError, match="levels deep"):
-        capi.SearchPlan(data, offs, 3, 7)
-    # 4000 levels are accepted (double negations cancel).
-    data, offs = _plan([4] + [3] * 4000, list(range(4002)), list(range(7)))
-    capi.SearchPlan(data, offs, 3, 7)
+    assert capi.SearchPlan(data, offs, 3, 7).num_queries == 1
+    n = 20_000
+    ops, cnt = [4], [0, 1]
+    for i in range(1, n):
+        ops += [4, 1 if i % 2 else 2]
+        cnt += [cnt[-1] + 1, cnt[-1] + 3]
+    data, offs = _plan(ops, cnt, list(range(7 * n)))
+    assert capi.SearchPlan(data, offs, 3, 7).num_queries == 1
     # A negative child count pops nothing, as the reference's pop loop does
     # not run: AND/OR push their identity.
     data, offs = _plan([4, 1], [0, 1, -2], list(range(7)))
