@@ -65,16 +65,21 @@ __global__ __launch_bounds__(kWidthThreads) void widths_kernel(
   const int64_t bundle = blockIdx.x;
   const int64_t doc0 = bundle * kDocsPerBundle;
   const int64_t doc1 = min(doc0 + kDocsPerBundle, num_docs);
-  // Every offset of the bundle's slots is read once: the slot boundaries
-  // give the monotonicity check, the per-doc differences the counts.
-  const int64_t s0 = doc0 * num_features;
-  const int64_t s1 = doc1 * num_features;
+  // One pass: a thread walks its doc's num_features + 1 offsets (the
+  // neighbouring threads' docs share cache lines, so HBM sees each offset
+  // once), checking that they never decrease and taking the doc's term
+  // count from the first and the last.
   int bad = 0;
-  for (int64_t s = s0 + threadIdx.x; s < s1; s += kWidthThreads)
-    bad |= offsets[s + 1] < offsets[s];
   int64_t best = 0;
   for (int64_t d = doc0 + threadIdx.x; d < doc1; d += kWidthThreads) {
-    const int64_t cnt = offsets[(d + 1) * num_features] - offsets[d * num_features];
+    const int64_t* o = offsets + d * num_features;
+    int64_t prev = o[0];
+    for (int64_t f = 1; f <= num_features; ++f) {
+      const int64_t v = o[f];
+      bad |= v < prev;
+      prev = v;
+    }
+    const int64_t cnt = prev - o[0];
     best = cnt > best ? cnt : best;
   }
   best = wave_max(best);
@@ -133,8 +138,14 @@ __device__ __forceinline__ void build_positions(uint64_t mx, uint64_t my,
                                                 uint32_t (&found)[K]) {
   int cnt = 0;
   uint64_t seed = 0;
+  // The seed-independent rotations once per key; seeds stay far below
+  // 2^27 (k distinct positions out of b >= k need few more than k seeds).
+  const uint64_t rx = rotl64(mx, 27), ry = rotl64(my, 31);
+  const bool small = fm.d < (1ull << 30);
   while (cnt < K) {
-    const uint32_t p = static_cast<uint32_t>(fast_mod(murmur_finish(mx, my, seed++), fm));
+    const uint64_t h = seed < (1ull << 27) ? murmur_finish_rot(rx, ry, seed) : murmur_finish(mx, my, seed);
+    ++seed;
+    const uint32_t p = small ? fast_mod_small(h, fm) : static_cast<uint32_t>(fast_mod(h, fm));
     bool dup = false;
 #pragma unroll
     for (int j = 0; j < K; ++j) dup |= (j < cnt) && (found[j] == p);

@@ -70,6 +70,27 @@ ST_HD uint64_t murmur_pair(uint64_t x, uint64_t y, uint64_t seed) {
   return murmur_finish(murmur_mix_x(x), murmur_mix_y(y), seed);
 }
 
+// murmur_finish for one key under many small seeds: the seed enters the
+// rotations only through seed ^ mx and seed ^ my, and for seed < 2^27
+// rotl(seed ^ m, r) = rotl(m, r) ^ (seed << r) (r = 27, 31), so the
+// rotations of mx and my are taken once per key (rx = rotl(mx, 27),
+// ry = rotl(my, 31)).  Equal to murmur_finish(mx, my, seed) for those seeds.
+ST_HD uint64_t murmur_finish_rot(uint64_t rx, uint64_t ry, uint64_t seed) {
+  uint64_t h1 = (rx ^ (seed << 27)) + seed;
+  h1 = h1 * 5 + 0x52dce729ULL;
+  uint64_t h2 = (ry ^ (seed << 31)) + h1;
+  h2 = h2 * 5 + 0x38495ab5ULL;
+  h1 ^= 16;
+  h2 ^= 16;
+  h1 += h2;
+  h2 += h1;
+  h1 = fmix64(h1);
+  h2 = fmix64(h2);
+  h1 += h2;
+  h2 += h1;
+  return h1 ^ h2;
+}
+
 ST_HD uint64_t mulhi64(uint64_t a, uint64_t b) {
 #if defined(__HIP_DEVICE_COMPILE__)
   return __umul64hi(a, b);
@@ -98,6 +119,17 @@ ST_HD uint64_t fast_mod(uint64_t n, const FastMod64& f) {
   uint64_t r = n - q * f.d;
   if (r >= f.d) r -= f.d;
   if (r >= f.d) r -= f.d;
+  return r;
+}
+
+// fast_mod for divisors below 2^30: n - q * d lies in [0, 3d) < 2^32, so it
+// equals its low 32 bits, and those are n_lo - q_lo * d (mod 2^32).
+ST_HD uint32_t fast_mod_small(uint64_t n, const FastMod64& f) {
+  const uint64_t q = mulhi64(n, f.magic);
+  const uint32_t d = static_cast<uint32_t>(f.d);
+  uint32_t r = static_cast<uint32_t>(n) - static_cast<uint32_t>(q) * d;
+  if (r >= d) r -= d;
+  if (r >= d) r -= d;
   return r;
 }
 
