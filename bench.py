@@ -33,6 +33,15 @@ sys.path.insert(0, str(ROOT))
 METRIC = "bloom search doc-queries/sec at 10M docs; achieved HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = ROOT / "profiles" / "search_cfg2_traffic.json"
+# VALU / MFMA counters of the cfg4 build and the cfg5 top-k kernels
+# (profiles/build_scatter_cfg4.md, profiles/topk_score_cfg5.md)
+COUNTERS_FILE = ROOT / "profiles" / "counters_build_topk.json"
+
+
+def counters(name: str):
+    if not COUNTERS_FILE.exists():
+        return None
+    return json.loads(COUNTERS_FILE.read_text()).get(name)
 
 
 def log(msg: str) -> None:
@@ -70,9 +79,24 @@ def calibrate_copy():
     print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n, "launches": 5}), flush=True)
 
 
-def cpu_baseline(index, bbo, queries, k, hash_k, num_docs, n_queries):
+def host_cpu() -> tuple[str, int]:
+    """(CPU model, logical CPUs) of this host."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, os.cpu_count() or 0
+
+
+def cpu_baseline(index, bbo, queries, k, hash_k, num_docs, n_queries, gpu_packed=None):
     """Times the reference's CPU search (oracle/_ref, compiled from the
-    reference sources) in a child process; falls back to the C oracle."""
+    reference sources) in a child process; falls back to the C oracle.  The
+    child also returns a digest of its output, which is compared with the
+    GPU's packed output of the same queries (gpu_packed, numpy)."""
     import numpy as np
 
     ref_so = ROOT / "oracle" / "_ref" / "libst_ref.so"
@@ -95,9 +119,11 @@ _, (pd, po) = st.parse_expression_query_batch(qs, torch.ones(1, dtype=torch.long
 st.bloom_index_search_batch(idx, bbo, pd[:0], po[:0], {k}, {hash_k}, False)
 t, passes = time.perf_counter(), 0
 while passes < 8 and (passes == 0 or time.perf_counter() - t < 10.0):
-    st.bloom_index_search_batch(idx, bbo, pd, po, {k}, {hash_k}, False)
+    out = st.bloom_index_search_batch(idx, bbo, pd, po, {k}, {hash_k}, False)
     passes += 1
-print(json.dumps({{"seconds": (time.perf_counter() - t) / passes, "passes": passes}}))
+secs = (time.perf_counter() - t) / passes
+import hashlib
+print(json.dumps({{"seconds": secs, "passes": passes, "sha256": hashlib.sha256(out.numpy().tobytes()).hexdigest()}}))
 """
         else:
             kind = "port"
@@ -110,9 +136,11 @@ qs = json.load(open({td!r} + '/queries.json'))
 _, data, offs = P.parse_batch(qs, {hash_k})
 t, passes = time.perf_counter(), 0
 while passes < 8 and (passes == 0 or time.perf_counter() - t < 10.0):
-    O.search_packed(idx, bbo, np.frombuffer(data, np.int8), np.array(offs), {k}, {hash_k})
+    out = O.search_packed(idx, bbo, np.frombuffer(data, np.int8), np.array(offs), {k}, {hash_k})
     passes += 1
-print(json.dumps({{"seconds": (time.perf_counter() - t) / passes, "passes": passes}}))
+secs = (time.perf_counter() - t) / passes
+import hashlib
+print(json.dumps({{"seconds": secs, "passes": passes, "sha256": hashlib.sha256(out.tobytes()).hexdigest()}}))
 """
         env = dict(os.environ, OMP_NUM_THREADS="1")
         out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=900)
@@ -121,13 +149,24 @@ print(json.dumps({{"seconds": (time.perf_counter() - t) / passes, "passes": pass
             return None
         res = json.loads(out.stdout.strip().splitlines()[-1])
         secs, passes = res["seconds"], res["passes"]
+    matches = None
+    if gpu_packed is not None:
+        import hashlib
+
+        matches = hashlib.sha256(np.ascontiguousarray(gpu_packed[:len(sample)]).tobytes()).hexdigest() == res["sha256"]
+        log(f"CPU baseline output ({kind}) equals the GPU's packed output of the same {len(sample)} queries: {matches}")
+    model, nproc = host_cpu()
     return {
         "value": len(sample) * num_docs / secs,
         "unit": "doc-queries/s",
         "cores": 1,
         "kind": kind,
+        "cpu_model": model,
+        "nproc": nproc,
+        "threads_used": 1,
+        "output_equals_gpu": matches,
         "sample": f"{len(sample)} of the {len(queries)} queries over all {num_docs} docs, packed output, "
-                  f"mean of {passes} passes of {secs:.2f} s, single-threaded "
+                  f"mean of {passes} passes of {secs:.2f} s, 1 thread used of {nproc} on {model} "
                   f"({'reference CPU op compiled from its sources' if kind == 'reference' else 'C oracle'})",
     }
 
@@ -364,7 +403,9 @@ def measure_build_cfg4(st, O):
         "ms": secs * 1e3, "docs_per_s": N / secs,
         "algorithmic_bytes": alg, "achieved_gbs": alg / secs / 1e9,
         "frac_of_hbm_peak": alg / secs / 1e9 / HBM_PEAK_GBS,
-        "note": "wall time of the op (both build kernels and the size readback), median of 3",
+        "compute": counters("build_cfg4"),
+        "note": "wall time of the op (both build kernels and the size readback), median of 3; "
+                "the scatter kernel is VALU-bound (compute: counters of the same workload)",
     }
 
 
@@ -547,7 +588,8 @@ def measure_topk(st, capi, steps):
         "passing_pairs": passing, "selectivity": passing / (Q * N),
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / MFMA_BF16_PEAK_TFLOPS,
-                     "note": "dense-equivalent 2*D*Q*N flops; tiles with no passing doc are skipped"},
+                     "note": "dense-equivalent 2*D*Q*N flops (a tile with no passing doc for any query would be skipped; at cfg5 none is: mfma_counters)"},
+        "mfma_counters": counters("topk_cfg5"),
         "hbm_gbs": (emb.numel() * 2 + packed.numel() * 8) / (topk_ms * 1e-3) / 1e9,
     }
 
@@ -702,7 +744,10 @@ def main():
 
     baseline = None
     if not args.no_cpu_baseline:
-        baseline = cpu_baseline(bi.cpu().numpy(), bo.cpu().numpy(), queries, k, hk, N, args.cpu_queries)
+        baseline = cpu_baseline(bi.cpu().numpy(), bo.cpu().numpy(), queries, k, hk, N, args.cpu_queries,
+                                out.cpu().numpy() if not args.bool_mask else None)
+        if baseline is not None and baseline["output_equals_gpu"] is False:
+            sys.exit("the GPU search output differs from the CPU baseline's")
 
     result = {
         "metric": METRIC,

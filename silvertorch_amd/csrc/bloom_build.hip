@@ -57,30 +57,48 @@ __device__ __forceinline__ int64_t wave_max(int64_t v) {
   return v;
 }
 
+// Feature counts up to this stage a chunk's offsets in LDS (below).
+constexpr int kWidthStageFeatures = 16;
+
 __global__ __launch_bounds__(kWidthThreads) void widths_kernel(
     const int64_t* __restrict__ offsets, int64_t num_docs, int64_t num_features,
     int64_t k, double b_multiplier, int64_t* __restrict__ bundle_b_offsets,
     int64_t* __restrict__ stats) {
   __shared__ int64_t red[kWidthThreads / 64];
+  __shared__ int64_t stage[kWidthThreads * kWidthStageFeatures + 1];
   const int64_t bundle = blockIdx.x;
   const int64_t doc0 = bundle * kDocsPerBundle;
   const int64_t doc1 = min(doc0 + kDocsPerBundle, num_docs);
-  // One pass: a thread walks its doc's num_features + 1 offsets (the
-  // neighbouring threads' docs share cache lines, so HBM sees each offset
-  // once), checking that they never decrease and taking the doc's term
-  // count from the first and the last.
+  const int64_t F = num_features;
   int bad = 0;
   int64_t best = 0;
-  for (int64_t d = doc0 + threadIdx.x; d < doc1; d += kWidthThreads) {
-    const int64_t* o = offsets + d * num_features;
-    int64_t prev = o[0];
-    for (int64_t f = 1; f <= num_features; ++f) {
-      const int64_t v = o[f];
-      bad |= v < prev;
-      prev = v;
+  if (F <= kWidthStageFeatures) {
+    // Chunks of kWidthThreads docs: the chunk's offsets (F per doc and the
+    // next doc's first) are loaded once with coalesced loads into LDS; then
+    // thread t checks that its doc's offsets never decrease and takes its
+    // count from the first and the last.
+    for (int64_t c0 = doc0; c0 < doc1; c0 += kWidthThreads) {
+      const int64_t nd = min<int64_t>(kWidthThreads, doc1 - c0);
+      const int64_t s0 = c0 * F, ns = nd * F + 1;
+      __syncthreads();  // the previous chunk's readers are done with stage
+      for (int64_t i = threadIdx.x; i < ns; i += kWidthThreads) stage[i] = offsets[s0 + i];
+      __syncthreads();
+      if (threadIdx.x < nd) {
+        const int64_t* o = stage + threadIdx.x * F;
+        for (int64_t f = 0; f < F; ++f) bad |= o[f + 1] < o[f];
+        const int64_t cnt = o[F] - o[0];
+        best = cnt > best ? cnt : best;
+      }
     }
-    const int64_t cnt = prev - o[0];
-    best = cnt > best ? cnt : best;
+  } else {
+    // Wide docs: every offset is read once for the monotonicity check, the
+    // doc boundaries again for the counts (L2 hits).
+    for (int64_t s = doc0 * F + threadIdx.x; s < doc1 * F; s += kWidthThreads)
+      bad |= offsets[s + 1] < offsets[s];
+    for (int64_t d = doc0 + threadIdx.x; d < doc1; d += kWidthThreads) {
+      const int64_t cnt = offsets[(d + 1) * F] - offsets[d * F];
+      best = cnt > best ? cnt : best;
+    }
   }
   best = wave_max(best);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;

@@ -150,6 +150,25 @@ def test_random_vs_oracle(seed):
     np.testing.assert_array_equal(got, O.search_packed(index, bbo, pd, po, ks, hk))
 
 
+@pytest.mark.parametrize("F,n", [(1, 5000), (16, 3000), (17, 2500), (40, 2100), (3, 257)])
+def test_build_feature_counts_vs_oracle(F, n):
+    """Bundle widths for feature counts on both sides of the widths kernel's
+    LDS staging limit (16), ragged last bundles and docs without terms;
+    decreasing offsets are rejected."""
+    rng = np.random.default_rng(40 + F)
+    ids, offs, vals = _random_corpus(rng, n, F, 0, 4, 3000)
+    H.note(f"[build widths] F={F} docs={n}")
+    index, bbo = H.build(ids, offs, vals, 2.0, 3)
+    want_index, want_bbo = O.bloom_build(ids, offs, vals, 2.0, 3)
+    np.testing.assert_array_equal(bbo, want_bbo)
+    np.testing.assert_array_equal(index, want_index)
+    bad = offs.copy()
+    bad[len(bad) // 2] = bad[len(bad) // 2 + 1] + 1  # one decrease
+    with pytest.raises(RuntimeError, match="non-decreasing"):
+        torch.ops.st.bloom_index_build(torch.from_numpy(ids).cuda(), torch.from_numpy(bad).cuda(),
+                                       torch.from_numpy(vals).cuda(), 2.0, 3)
+
+
 def test_many_terms_split_into_passes():
     """More distinct terms than one LDS position area holds -> several passes."""
     rng = np.random.default_rng(77)
