@@ -74,15 +74,33 @@ __global__ __launch_bounds__(kWidthThreads) void widths_kernel(
   int64_t best = 0;
   if (F <= kWidthStageFeatures) {
     // Chunks of kWidthThreads docs: the chunk's offsets (F per doc and the
-    // next doc's first) are loaded once with coalesced loads into LDS; then
-    // thread t checks that its doc's offsets never decrease and takes its
-    // count from the first and the last.
+    // next doc's first) are loaded once with coalesced loads into registers,
+    // the next chunk's loads are issued before this chunk is evaluated, and
+    // the values pass through LDS so that thread t can check that its doc's
+    // offsets never decrease and take its count from the first and the last.
+    constexpr int kPer = kWidthStageFeatures + 1;  // ns <= kPer * kWidthThreads
+    int64_t r[kPer];
+    const auto load = [&](int64_t c0) {
+      const int64_t ns = min<int64_t>(kWidthThreads, doc1 - c0) * F + 1;
+      const int64_t* src = offsets + c0 * F;
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int64_t i = threadIdx.x + u * kWidthThreads;
+        r[u] = i < ns ? src[i] : 0;
+      }
+    };
+    if (doc0 < doc1) load(doc0);
     for (int64_t c0 = doc0; c0 < doc1; c0 += kWidthThreads) {
       const int64_t nd = min<int64_t>(kWidthThreads, doc1 - c0);
-      const int64_t s0 = c0 * F, ns = nd * F + 1;
+      const int64_t ns = nd * F + 1;
       __syncthreads();  // the previous chunk's readers are done with stage
-      for (int64_t i = threadIdx.x; i < ns; i += kWidthThreads) stage[i] = offsets[s0 + i];
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int64_t i = threadIdx.x + u * kWidthThreads;
+        if (i < ns) stage[i] = r[u];
+      }
       __syncthreads();
+      if (c0 + kWidthThreads < doc1) load(c0 + kWidthThreads);
       if (threadIdx.x < nd) {
         const int64_t* o = stage + threadIdx.x * F;
         for (int64_t f = 0; f < F; ++f) bad |= o[f + 1] < o[f];

@@ -8,6 +8,7 @@
 
 #include "bloom_generic.hpp"
 #include "bloom_search_kernel.hpp"
+#include "wide_balance.hpp"
 
 namespace st {
 namespace {
@@ -140,15 +141,18 @@ __device__ __forceinline__ void for_each_width(const int64_t* bbo, int64_t nb, F
 // bundle widths -- the kMaxWidthSlots most frequent widths get slots, ties
 // to the smaller width -- and writes the slot table, every bundle's slot
 // and, when `bundle_order` is given, a visiting order grouped by slot (a
-// counting sort; order within a slot is arbitrary).  The census reads only
-// the bundle offsets, so it runs while the copy waits on PCIe.
+// counting sort; order within a slot is arbitrary) -- with `order_if_wide`
+// only when some slot width is wide (the wide-bundle kernel's order).  The
+// census reads only the bundle offsets, so it runs while the copy waits on
+// PCIe.
 constexpr int kUploadPerThread = 4;   // 16-byte pieces per thread of an upload group
 
 __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
     const uint8_t* __restrict__ host_src, uint8_t* __restrict__ blob, int64_t upload_bytes,
     uint32_t upload_groups, const int64_t* __restrict__ bbo, int64_t nb,
     uint32_t* __restrict__ num_slots, int64_t* __restrict__ slot_width,
-    uint32_t* __restrict__ bundle_slot, uint32_t* __restrict__ bundle_order) {
+    uint32_t* __restrict__ bundle_slot, uint32_t* __restrict__ bundle_order,
+    uint32_t order_if_wide) {
   const int tid = threadIdx.x;
   if (blockIdx.x < upload_groups) {
     typedef uint32_t v4 __attribute__((ext_vector_type(4)));
@@ -179,6 +183,7 @@ __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
   __shared__ uint32_t overflow;
   __shared__ long long s_width[kMaxWidthSlots];
   __shared__ uint32_t cursor[kMaxWidthSlots + 1];
+  __shared__ uint32_t any_wide;
   for (int e = tid; e < kCensusCap; e += kBindThreads) {
     keys[e] = kCensusEmpty;
     count[e] = 0u;
@@ -241,6 +246,8 @@ __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
     // num_slots[1]: every bundle has a slot, and every slot width is wide
     const bool narrow = tid < static_cast<int>(ns) && !wide_width(s_width[tid]);
     const bool all_wide = __ballot(narrow) == 0ull && cursor[kMaxWidthSlots] == 0;
+    const bool wide = tid < static_cast<int>(ns) && wide_width(s_width[tid]);
+    const bool some_wide = __ballot(wide) != 0ull;
     // bucket sizes -> bucket starts (exclusive scan over the wave; the
     // unslotted bucket goes last)
     const uint32_t c = cursor[tid];
@@ -255,10 +262,11 @@ __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
     if (tid == 0) {
       num_slots[0] = ns;
       num_slots[1] = all_wide ? 1u : 0u;
+      any_wide = some_wide ? 1u : 0u;
     }
   }
   __syncthreads();
-  if (bundle_order != nullptr) {
+  if (bundle_order != nullptr && (order_if_wide == 0u || any_wide != 0u)) {
     for_each_width(bbo, nb, [&](int64_t i, long long w) {
       const int e = census_find(keys, w, false);
       const uint32_t sl = e >= 0 ? slot_of[e] : kNoWidthSlot;
@@ -273,7 +281,10 @@ __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
 // the slot's width once (as signature_match does, bloom_index_search.cpp:
 // 40-61: b_p = (int16)(h[p] % b) over p < hash_k, repeats skipped, at most
 // k_eff kept, unused positions repeat the first) and expands its part of
-// every batch's width-block template.
+// every batch's width-block template.  On a wide slot the literal stream's
+// positions are written unit by unit instead (its part of the units), in
+// the read order balance_wide_choice gives them; the words of the two passes
+// are disjoint, so no workgroup reads what another writes.
 __global__ __launch_bounds__(kBindThreads) void bind_fill_kernel(
     char* __restrict__ blob, uint64_t off_table, uint32_t n_batches, int hash_k, int k_eff, int kp,
     const uint32_t* __restrict__ num_slots, const int64_t* __restrict__ slot_width) {
@@ -294,6 +305,15 @@ __global__ __launch_bounds__(kBindThreads) void bind_fill_kernel(
                          : wide ? static_cast<uint32_t>(kWideZerosRow) * kWideSliceBytes
                                 : static_cast<uint32_t>(kPosZeros);
   const uint64_t* table = reinterpret_cast<const uint64_t*>(blob + off_table);
+  // a template word at this slot's width; pos holds the batch's positions
+  const auto resolve = [&](uint32_t c, uint32_t t) -> uint32_t {
+    if (c == kTmplCopy) return t;
+    if (c == kTmplOnes) return ones;
+    if (c == kTmplZeros) return zeros;
+    return pos[((c >> 4) - 1u) * kp + (c & 15u)];
+  };
+  // positions per stream record (the unit pass runs when balance_applies)
+  const int ks = k_eff > 1 ? k_eff : 1;
   for (uint32_t t = 0; t < n_batches; ++t) {
     const uint64_t* e = table + static_cast<uint64_t>(t) * kBindTableWords;
     const uint32_t* tmpl = reinterpret_cast<const uint32_t*>(blob + e[0]);
@@ -302,6 +322,11 @@ __global__ __launch_bounds__(kBindThreads) void bind_fill_kernel(
     uint32_t* bound = reinterpret_cast<uint32_t*>(blob + e[3]);
     const uint32_t words = static_cast<uint32_t>(e[4]);
     const uint32_t n_terms = static_cast<uint32_t>(e[5]);
+    const uint32_t* units = reinterpret_cast<const uint32_t*>(blob + e[6]);
+    const uint32_t n_units = wide ? static_cast<uint32_t>(e[7]) : 0u;
+    // stream words left to the unit pass (none unless it runs)
+    const uint32_t s_lo = static_cast<uint32_t>(e[8]);
+    const uint32_t s_hi = n_units != 0 ? s_lo + static_cast<uint32_t>(e[8] >> 32) : s_lo;
     if (words == 0) continue;
     __syncthreads();  // the previous batch's positions are no longer read
     for (uint32_t u = tid; u < n_terms; u += kBindThreads) {
@@ -335,9 +360,9 @@ __global__ __launch_bounds__(kBindThreads) void bind_fill_kernel(
       }
     }
     __syncthreads();
+    uint32_t* dst = bound + static_cast<uint64_t>(sl) * words;
     const uint32_t w0 = static_cast<uint32_t>(static_cast<uint64_t>(words) * part / parts);
     const uint32_t w1 = static_cast<uint32_t>(static_cast<uint64_t>(words) * (part + 1) / parts);
-    uint32_t* dst = bound + static_cast<uint64_t>(sl) * words;
     for (uint32_t i0 = w0; i0 < w1; i0 += kBindThreads * kBindFillBatch) {
       // every load of the batch is issued before any value is used
       uint32_t c[kBindFillBatch], t[kBindFillBatch];
@@ -351,13 +376,28 @@ __global__ __launch_bounds__(kBindThreads) void bind_fill_kernel(
       for (int j = 0; j < kBindFillBatch; ++j) {
         const uint32_t i = i0 + tid + j * kBindThreads;
         if (i >= w1) break;
-        uint32_t v;
-        if (c[j] == kTmplCopy) v = t[j];
-        else if (c[j] == kTmplOnes) v = ones;
-        else if (c[j] == kTmplZeros) v = zeros;
-        else v = pos[((c[j] >> 4) - 1u) * kp + (c[j] & 15u)];
-        dst[i] = v;
+        if (c[j] != kTmplCopy && i >= s_lo && i < s_hi) continue;  // the unit pass's
+        dst[i] = resolve(c[j], t[j]);
       }
+    }
+    if (n_units == 0) continue;
+    const int srw = bound_record_words(ks);
+    const uint32_t u0 = static_cast<uint32_t>(static_cast<uint64_t>(n_units) * part / parts);
+    const uint32_t u1 = static_cast<uint32_t>(static_cast<uint64_t>(n_units) * (part + 1) / parts);
+    for (uint32_t u = u0 + tid; u < u1; u += kBindThreads) {
+      const uint32_t* c = code + units[u];
+      uint32_t res[kBalanceRecords], choice[kBalanceRecords];
+#pragma unroll
+      for (int i = 0; i < kBalanceRecords; ++i) {
+        res[i] = 0;
+        for (int j = 0; j < ks; ++j) res[i] |= wide_bank_group(resolve(c[i * srw + j], 0u)) << (2 * j);
+      }
+      balance_wide_choice(res, ks, choice);
+      uint32_t* d = dst + units[u];
+#pragma unroll
+      for (int i = 0; i < kBalanceRecords; ++i)
+        for (int k = 0; k < ks; ++k)
+          d[i * srw + k] = resolve(c[i * srw + balance_source(res[i], choice[i], k, ks)], 0u);
     }
   }
 }
@@ -390,8 +430,9 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
       (upload_bytes + 16ull * kBindThreads * kUploadPerThread - 1) / (16ull * kBindThreads * kUploadPerThread));
   if (upload_bytes != 0 || plan->device_bind) {
     char* dev = const_cast<char*>(blob);
-    // The visiting order is needed only by batches outside the quad-lane
-    // path (the quad instance visits bundles in index order).
+    // The visiting order is needed by batches outside the quad-lane path
+    // (the quad instance visits bundles in index order) and by the
+    // wide-bundle kernel when some slot width is wide.
     bool need_order = false;
     for (const SearchBatch& bt : plan->batches)
       need_order |= !bt.generic &&
@@ -405,7 +446,10 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
                        db ? reinterpret_cast<uint32_t*>(dev + plan->off_num_slots) : nullptr,
                        db ? reinterpret_cast<int64_t*>(dev + plan->off_slot_width) : nullptr,
                        db ? reinterpret_cast<uint32_t*>(dev + plan->off_bundle_slot) : nullptr,
-                       db && need_order ? reinterpret_cast<uint32_t*>(dev + plan->off_bundle_order) : nullptr);
+                       db && (need_order || plan->off_wide != 0)
+                           ? reinterpret_cast<uint32_t*>(dev + plan->off_bundle_order)
+                           : nullptr,
+                       need_order ? 0u : 1u);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
       throw Error(ST_ERR_HIP, cat("plan upload / width census launch failed: ", hipGetErrorString(e)));
@@ -486,7 +530,7 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
   if (wide_fn != nullptr) {
     hipLaunchKernelGGL(wide_fn, dim3(grid), dim3(kSearchThreads), 0, stream, bloom_index,
                        bloom_index_numel, bundle_b_offsets, num_bundles,
-                       at(plan->off_bundle_slot),
+                       at(plan->off_bundle_slot), at(plan->off_bundle_order),
                        plan->device_bind ? at(plan->off_num_slots) : nullptr,
                        plan->device_bind
                            ? reinterpret_cast<const int64_t*>(blob + plan->off_slot_width)

@@ -1336,8 +1336,10 @@ __device__ __forceinline__ void wide_eval_group(const char* stream, const ST_CON
 
 // Grid: 1024-thread workgroups, one per CU.  When the grid is a multiple
 // of 16, workgroups w and w + 8 (dispatched to the same XCD) form a pair
-// that walks the wide bundles p, p + grid / 2, ... of index order, one
-// member taking slices 0 and 2, the other 1 and 3, so the two halves of each
+// that walks the wide bundles p, p + grid / 2, ... of the visiting order
+// `bundle_order` (bundles grouped by width slot, so that the workgroups
+// working at one time share the slot's literal stream in L2), one member
+// taking slices 0 and 2, the other 1 and 3, so the two halves of each
 // 128-byte index line are read by the same XCD at about the same time;
 // otherwise workgroup w takes bundles w, w + grid, ... with all slices.  Each
 // wave issues its share of the next slice's loads when it has evaluated the
@@ -1348,15 +1350,17 @@ template <int K>
 __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
     const int64_t* __restrict__ index, int64_t index_numel,
     const int64_t* __restrict__ bundle_offsets, int64_t num_bundles,
-    const uint32_t* __restrict__ bundle_slot, const uint32_t* __restrict__ num_slots,
-    const int64_t* __restrict__ slot_width, const uint32_t* __restrict__ blob,
-    const uint32_t* __restrict__ table, int64_t out_cols, int64_t* __restrict__ out) {
+    const uint32_t* __restrict__ bundle_slot, const uint32_t* __restrict__ bundle_order,
+    const uint32_t* __restrict__ num_slots, const int64_t* __restrict__ slot_width,
+    const uint32_t* __restrict__ blob, const uint32_t* __restrict__ table, int64_t out_cols,
+    int64_t* __restrict__ out) {
   __shared__ u32x4 tile[(kWideRows + 2) * kWidePieces];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const uint32_t wave = uniform(tid >> 6);
   const ST_CONST int64_t* boff = as_const(bundle_offsets);
   const ST_CONST uint32_t* bslot = as_const(bundle_slot);
+  const ST_CONST uint32_t* border = as_const(bundle_order);
   const ST_CONST uint32_t* tab = as_const(table);
 
   if (num_slots != nullptr) {
@@ -1382,11 +1386,13 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
   const int s_first = paired ? static_cast<int>((blockIdx.x >> 3) & 1) : 0;
   const int s_step = paired ? 2 : 1;
 
-  // first wide bundle at or after i on this workgroup's stride
-  auto next_wide = [&](int64_t i) -> int64_t {
+  // first wide bundle at or after visiting position i on this workgroup's
+  // stride: (position, bundle), position num_bundles when there is none
+  auto next_wide = [&](int64_t i, int64_t& bnd) -> int64_t {
     for (; i < num_bundles; i += stride) {
-      const int64_t b = boff[i + 1] - boff[i];
-      if (bslot[i] != kNoWidthSlot && wide_width(b)) return i;
+      bnd = border[i];
+      const int64_t b = boff[bnd + 1] - boff[bnd];
+      if (bslot[bnd] != kNoWidthSlot && wide_width(b)) return i;
     }
     return num_bundles;
   };
@@ -1405,23 +1411,25 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
     }
   };
 
-  int64_t cb = next_wide(first);
-  if (cb >= num_bundles) return;
+  int64_t cbnd = 0;  // bundle at visiting position cp
+  int64_t cp = next_wide(first, cbnd);
+  if (cp >= num_bundles) return;
   int cs = s_first;
   u32x4 pre[kWidePrefetch];
-  prefetch(cb, cs, pre);
+  prefetch(cbnd, cs, pre);
   const ST_LDS char* tile_lane = (const ST_LDS char*)(tile) + (lane & 3) * 16;
   const int64_t row_bytes = out_cols * 8;
   for (;;) {
+    const int64_t cb = cbnd;
     const int64_t b = boff[cb + 1] - boff[cb];
     const uint32_t slot = bslot[cb];
-    int64_t nb = cb;
+    int64_t np = cp, nbnd = cb;
     int ns = cs + s_step;
     if (ns >= kWideSlices) {
-      nb = next_wide(cb + stride);
+      np = next_wide(cp + stride, nbnd);
       ns = s_first;
     }
-    const bool has_next = nb < num_bundles;
+    const bool has_next = np < num_bundles;
     __syncthreads();  // the previous slice's readers are done
 #pragma unroll
     for (int i = 0; i < kWidePrefetch; ++i) {
@@ -1444,9 +1452,10 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
     // The next slice's loads go out after this wave's evaluation: issued
     // earlier, every wait for a stream record (in-order vmcnt) would also
     // wait for them.
-    if (has_next) prefetch(nb, ns, pre);
+    if (has_next) prefetch(nbnd, ns, pre);
     if (!has_next) break;
-    cb = nb;
+    cp = np;
+    cbnd = nbnd;
     cs = ns;
   }
 }
@@ -1454,8 +1463,8 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
 }  // namespace
 
 using WideFn = void (*)(const int64_t*, int64_t, const int64_t*, int64_t, const uint32_t*,
-                        const uint32_t*, const int64_t*, const uint32_t*, const uint32_t*,
-                        int64_t, int64_t*);
+                        const uint32_t*, const uint32_t*, const int64_t*, const uint32_t*,
+                        const uint32_t*, int64_t, int64_t*);
 // The wide-bundle kernel of one K (nullptr for K > 7), defined in the
 // translation unit compiled with ST_SEARCH_K = K.
 template <int K>

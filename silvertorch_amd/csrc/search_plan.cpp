@@ -23,6 +23,7 @@
 #include "search_plan.hpp"
 #include "st_common.hpp"
 #include "st_errors.hpp"
+#include "wide_balance.hpp"
 
 namespace st {
 namespace {
@@ -956,12 +957,14 @@ uint64_t align_to(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 // position index) resolved at each slot width, on the host
 // (st_search_plan_bind_widths) or on the device.  Sets bt.stream_off and
 // bt.stream_words; wave_rec / wave_skip receive the per-wave stream tables
-// (all zero without a stream).
+// (all zero without a stream), units the stream's balance units (the block
+// word of every fourth record of a round step, when balance_applies).
 void build_block_template(const st_search_plan& plan, SearchBatch& bt,
                           const std::vector<uint32_t>& insns,
                           const std::vector<uint32_t>& starts, std::vector<uint32_t>& bstart,
                           std::vector<uint32_t>& tmpl, std::vector<uint32_t>& code,
-                          std::vector<uint32_t>& wave_rec, std::vector<uint32_t>& wave_skip) {
+                          std::vector<uint32_t>& wave_rec, std::vector<uint32_t>& wave_skip,
+                          std::vector<uint32_t>& units) {
   const int k_eff = plan.k_eff, kp = plan.kp, rw = bound_record_words(k_eff);
   const uint32_t pos_bytes = static_cast<uint32_t>(kp) * 4;
   std::vector<uint32_t> bound_T(bt.num_slots);
@@ -1025,6 +1028,8 @@ void build_block_template(const st_search_plan& plan, SearchBatch& bt,
   const uint32_t per_block = static_cast<uint32_t>(stream_block_records(ks));
   wave_rec.assign(kSearchWaves + 1, 0u);
   wave_skip.assign(kSearchWaves, 0u);
+  units.clear();
+  const bool balance = balance_applies(ks);
   bt.stream_off = static_cast<uint32_t>(tmpl.size());
   bt.stream_words = 0;
   bool fits = true;
@@ -1097,6 +1102,7 @@ void build_block_template(const st_search_plan& plan, SearchBatch& bt,
       for (uint32_t i = per_block; kRoundSlotInfo + i < kRoundHeaderWords; ++i) word(0u);
       for (uint32_t j = 0; j < T; ++j) {
         for (uint32_t i = 0; i < per_block; ++i) {
+          if (balance && i % kBalanceRecords == 0) units.push_back(static_cast<uint32_t>(at));
           if (i >= n) {
             record(kTmplOnes, 0, 0u);
             continue;
@@ -1126,6 +1132,24 @@ void build_block_template(const st_search_plan& plan, SearchBatch& bt,
     bt.stream_off = 0;
     wave_rec.assign(kSearchWaves + 1, 0u);
     wave_skip.assign(kSearchWaves, 0u);
+    units.clear();
+  }
+}
+
+// Balances the read order of every unit of a wide slot's width block
+// (out: the block, expanded).
+void balance_block(const std::vector<uint32_t>& units, int ks, uint32_t* out) {
+  const int srw = bound_record_words(ks);
+  for (const uint32_t u : units) {
+    uint32_t res[kBalanceRecords] = {}, choice[kBalanceRecords], v[kBalanceMaxK];
+    for (int i = 0; i < kBalanceRecords; ++i)
+      for (int j = 0; j < ks; ++j) res[i] |= wide_bank_group(out[u + i * srw + j]) << (2 * j);
+    balance_wide_choice(res, ks, choice);
+    for (int i = 0; i < kBalanceRecords; ++i) {
+      uint32_t* rec = out + u + i * srw;
+      for (int k = 0; k < ks; ++k) v[k] = rec[balance_source(res[i], choice[i], k, ks)];
+      for (int k = 0; k < ks; ++k) rec[k] = v[k];
+    }
   }
 }
 
@@ -1365,8 +1389,8 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
                          plan->hash_k, k_eff, plan->slot_width[s], fm, kp,
                          &pos[(s * bt.num_terms + u) * kp]);
       }
-      static thread_local std::vector<uint32_t> bstart, tmpl, code, wave_rec, wave_skip;
-      build_block_template(*plan, bt, insns, starts, bstart, tmpl, code, wave_rec, wave_skip);
+      static thread_local std::vector<uint32_t> bstart, tmpl, code, wave_rec, wave_skip, units;
+      build_block_template(*plan, bt, insns, starts, bstart, tmpl, code, wave_rec, wave_skip, units);
       stream_rounds(tmpl, bt, k_eff, rounds[bi]);
       const uint32_t words = static_cast<uint32_t>(tmpl.size());
       bt.bound_words = words;
@@ -1380,9 +1404,12 @@ extern "C" int st_search_plan_bind_widths(st_search_plan* plan,
       bt.off_bound = blob.size();
       blob.resize(blob.size() + nslots * words * 4, 0);
       uint32_t* block = reinterpret_cast<uint32_t*>(blob.data() + bt.off_bound);
-      for (size_t s = 0; s < nslots; ++s)
+      for (size_t s = 0; s < nslots; ++s) {
         expand_block(tmpl, code, pos.data() + s * bt.num_terms * kp, kp, plan->slot_width[s],
                      block + s * words);
+        if (wide_width(plan->slot_width[s]))
+          balance_block(units, std::max(k_eff, 1), block + s * words);
+      }
     }
     append_wide_table(*plan, rounds);
     patch_wide_table(*plan);
@@ -1402,13 +1429,13 @@ extern "C" int st_search_plan_prepare_device_binding(st_search_plan* plan,
     ST_CHECK(num_bundles >= 0, "negative bundle count");
     auto& blob = plan->blob;
     // working vectors keep their capacity between calls on a thread
-    static thread_local std::vector<uint32_t> bstart, tmpl, code, wave_rec, wave_skip;
+    static thread_local std::vector<uint32_t> bstart, tmpl, code, wave_rec, wave_skip, units;
     std::vector<RoundList> rounds(plan->batches.size());
     for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
       SearchBatch& bt = plan->batches[bi];
       if (bt.generic) continue;  // no width blocks: the generic kernel resolves positions
       build_block_template(*plan, bt, plan->batch_insns[bi], plan->batch_starts[bi], bstart,
-                           tmpl, code, wave_rec, wave_skip);
+                           tmpl, code, wave_rec, wave_skip, units);
       stream_rounds(tmpl, bt, plan->k_eff, rounds[bi]);
       bt.bound_words = static_cast<uint32_t>(tmpl.size());
       bt.off_bound_start = blob.size();
@@ -1421,6 +1448,9 @@ extern "C" int st_search_plan_prepare_device_binding(st_search_plan* plan,
       append_bytes(blob, tmpl.data(), tmpl.size() * 4);
       bt.off_tmpl_code = blob.size();
       append_bytes(blob, code.data(), code.size() * 4);
+      bt.off_units = blob.size();
+      bt.n_units = static_cast<uint32_t>(units.size());
+      append_bytes(blob, units.data(), units.size() * 4);
     }
     append_wide_table(*plan, rounds);
     blob.resize(align_to(blob.size(), 8), 0);
@@ -1441,8 +1471,9 @@ extern "C" int st_search_plan_prepare_device_binding(st_search_plan* plan,
       SearchBatch& bt = plan->batches[bi];
       bt.off_bound = d;
       d = align_to(d + 4ull * kMaxWidthSlots * bt.bound_words, 256);
-      const uint64_t row[kBindTableWords] = {bt.off_tmpl, bt.off_tmpl_code, bt.off_hashes,
-                                             bt.off_bound, bt.bound_words, bt.num_terms};
+      const uint64_t row[kBindTableWords] = {
+          bt.off_tmpl, bt.off_tmpl_code, bt.off_hashes, bt.off_bound, bt.bound_words, bt.num_terms,
+          bt.off_units, bt.n_units, bt.stream_off | (static_cast<uint64_t>(bt.stream_words) << 32)};
       std::memcpy(blob.data() + plan->off_bind_table + 8 * kBindTableWords * bi, row, sizeof(row));
     }
     patch_wide_table(*plan);

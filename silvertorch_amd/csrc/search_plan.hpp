@@ -114,7 +114,7 @@ inline int positions_per_term(int k_eff) {
 constexpr int kMaxWidthSlots = 64;
 constexpr uint32_t kNoWidthSlot = 0xFFFFFFFFu;
 
-inline int bound_record_words(int k_eff) { return ((k_eff + 1 + 3) / 4) * 4; }
+constexpr int bound_record_words(int k_eff) { return ((k_eff + 1 + 3) / 4) * 4; }
 
 // Literal stream.  Every width block also carries the batch's flat programs
 // as rounds of literal records, which the kernel reads with scalar loads and
@@ -171,6 +171,11 @@ struct SearchBatch {
   uint32_t stream_masks = 0;     // 1: records carry group masks (no negation)
   uint64_t off_stream_wave = 0;  // uint32[kSearchWaves + 1]: first stream word of each wave
   uint64_t off_stream_skip = 0;  // uint32[kSearchWaves]: flat programs each run covers
+  // device binding: the stream's balance units, the block word of the first
+  // of four records one 16-lane group of the wide-bundle kernel reads
+  // together (none unless the records hold 2 .. 7 positions)
+  uint64_t off_units = 0;        // uint32[n_units]
+  uint32_t n_units = 0;
 };
 
 // Wide bundles (kSearchTileRows < b <= kWideRows rows, width-bound) are
@@ -207,8 +212,9 @@ constexpr int kWideMaxRounds = 4;
 // Batch table of the device binding kernel (uint64 words at
 // st_search_plan::off_bind_table), per batch: byte offsets of its template,
 // template codes, term hashes and width blocks in the device blob, words per
-// width block, distinct terms.
-constexpr int kBindTableWords = 6;
+// width block, distinct terms, byte offset of its balance units, their
+// number, and its literal stream's words within a block (first | count << 32).
+constexpr int kBindTableWords = 9;
 
 // Codes of a width-block template word.
 constexpr uint32_t kTmplCopy = 0u;           // the template word itself
