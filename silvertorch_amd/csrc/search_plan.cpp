@@ -12,12 +12,20 @@
 // AND pops `children` values and ANDs them into all-ones; OR ORs them into
 // zero; NOT needs exactly one child; EMPTY pushes all-ones; the answer is the
 // top of the stack.
+#include <unistd.h>
+
 #include <algorithm>
+#include <atomic>
 #include <climits>
+#include <condition_variable>
+#include <cstdlib>
 #include <cstring>
+#include <exception>
+#include <functional>
 #include <memory>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <unordered_map>
 
 #include "search_plan.hpp"
@@ -91,12 +99,14 @@ struct TermTable {
     slots.assign(n, 0);
     for (uint32_t id = 0; id < count; ++id) place(id);
   }
-  uint32_t intern(const int8_t* h) {
+  uint32_t intern(const int8_t* h) { return intern(h, digest(h)); }
+  // with the digest of h already known
+  uint32_t intern(const int8_t* h, uint64_t dg) {
     if ((static_cast<size_t>(count) + 1) * 2 > slots.size())
       rehash(std::max<size_t>(256, slots.size() * 2));
     const size_t mask = slots.size() - 1;
     const size_t bytes = static_cast<size_t>(hash_k) * 8;
-    for (size_t i = digest(h) & mask;; i = (i + 1) & mask) {
+    for (size_t i = dg & mask;; i = (i + 1) & mask) {
       const uint32_t s = slots[i];
       if (s == 0) {
         slots[i] = count + 1;
@@ -108,6 +118,12 @@ struct TermTable {
     }
   }
   uint32_t size() const { return count; }
+  // room for n terms without growing
+  void reserve(size_t n) {
+    size_t want = 256;
+    while (want < 2 * n + 2) want *= 2;
+    if (want > slots.size()) rehash(want);
+  }
   void commit() { committed = count; }
   void rollback() {  // forget the terms interned since the last commit()
     count = committed;
@@ -707,6 +723,134 @@ uint32_t append_program(std::vector<uint32_t>& insns, const CompiledQuery& cq, u
 }  // namespace
 }  // namespace st
 
+namespace st {
+namespace {
+
+// Plans of at least this many bytes are compiled on the pool (below it the
+// workers' wake-up costs more than it saves: 256 flat queries take ~0.15 ms
+// on one thread).
+constexpr int64_t kParallelCompileBytes = 192 * 1024;
+
+// Host threads of the plan compiler: a few workers started on first use
+// (ST_PLAN_THREADS, default min(8, hardware threads) including the caller)
+// that share one job at a time with the calling thread.  A caller that
+// finds the pool busy, or runs in a child of the process that started it,
+// does the work alone.
+class CompilePool {
+ public:
+  static CompilePool& get() {
+    static CompilePool* pool = new CompilePool();  // never destroyed: workers may still wait
+    return *pool;
+  }
+  // fn(i) for every i in [0, n), chunks of `chunk` taken in turn by the
+  // workers and the caller; fn must not throw.
+  void run(int64_t n, int64_t chunk, const std::function<void(int64_t)>& fn) {
+    std::unique_lock<std::mutex> busy(job_mu_, std::try_to_lock);
+    if (!busy.owns_lock() || getpid() != pid_ || workers_ == 0) {
+      for (int64_t i = 0; i < n; ++i) fn(i);
+      return;
+    }
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      fn_ = &fn;
+      n_ = n;
+      chunk_ = chunk;
+      next_.store(0);
+      active_ = workers_;
+      ++generation_;
+    }
+    cv_.notify_all();
+    work();
+    std::unique_lock<std::mutex> lk(mu_);
+    done_cv_.wait(lk, [&] { return active_ == 0; });
+    fn_ = nullptr;
+  }
+
+ private:
+  CompilePool() : pid_(getpid()) {
+    int threads = static_cast<int>(std::min(8u, std::max(1u, std::thread::hardware_concurrency())));
+    if (const char* e = std::getenv("ST_PLAN_THREADS")) threads = std::max(1, std::atoi(e));
+    workers_ = threads - 1;
+    for (int i = 0; i < workers_; ++i) std::thread([this] { loop(); }).detach();
+  }
+  void work() {
+    for (;;) {
+      const int64_t b = next_.fetch_add(chunk_);
+      if (b >= n_) return;
+      const int64_t e = std::min(n_, b + chunk_);
+      for (int64_t i = b; i < e; ++i) (*fn_)(i);
+    }
+  }
+  void loop() {
+    uint64_t seen = 0;
+    for (;;) {
+      {
+        std::unique_lock<std::mutex> lk(mu_);
+        cv_.wait(lk, [&] { return generation_ != seen; });
+        seen = generation_;
+      }
+      work();
+      std::lock_guard<std::mutex> lk(mu_);
+      if (--active_ == 0) done_cv_.notify_one();
+    }
+  }
+  const pid_t pid_;
+  int workers_ = 0;
+  std::mutex job_mu_;  // one job at a time
+  std::mutex mu_;
+  std::condition_variable cv_, done_cv_;
+  uint64_t generation_ = 0;
+  int active_ = 0;
+  const std::function<void(int64_t)>* fn_ = nullptr;
+  int64_t n_ = 0, chunk_ = 1;
+  std::atomic<int64_t> next_{0};
+};
+
+// One query compiled on its own: its term ids are local (first appearance
+// in the query), local_hashes holds their hashes, and the batch ids replace
+// them when the query joins a batch.  A query that fails keeps its error.
+struct LocalQuery {
+  CompiledQuery cq;
+  std::vector<uint64_t> local_hashes;
+  std::vector<uint64_t> digests;  // TermTable digest of each local term
+  uint32_t local_terms = 0;
+  std::exception_ptr error;
+};
+
+void compile_local(const int8_t* data, int64_t data_len, const int64_t* offs, int64_t q,
+                   int64_t hash_k, int k_eff, LocalQuery& out) {
+  static thread_local TermTable terms;
+  static thread_local CompileScratch scratch;
+  terms.hash_k = std::max<int64_t>(hash_k, 0);
+  terms.clear();
+  try {
+    out.cq = compile_query(data, data_len, offs, q, hash_k, k_eff, terms, scratch);
+    out.local_terms = terms.size();
+    out.local_hashes.assign(terms.hashes.begin(), terms.hashes.end());
+    out.digests.resize(out.local_terms);
+    for (uint32_t i = 0; i < out.local_terms; ++i)
+      out.digests[i] = terms.digest(reinterpret_cast<const int8_t*>(terms.hashes.data() + i * terms.hash_k));
+  } catch (...) {
+    out.error = std::current_exception();
+  }
+}
+
+// Batch ids of a compiled query's local terms, interned into `terms`.
+void intern_local(const LocalQuery& lq, int64_t hash_k, TermTable& terms, std::vector<uint32_t>& ids) {
+  ids.resize(lq.local_terms);
+  for (uint32_t i = 0; i < lq.local_terms; ++i)
+    ids[i] = terms.intern(reinterpret_cast<const int8_t*>(lq.local_hashes.data() + i * hash_k),
+                          lq.digests[i]);
+}
+
+void rename_terms(CompiledQuery& cq, const std::vector<uint32_t>& ids) {
+  for (auto& l : cq.lits) l.term = ids[l.term];
+  for (auto& t : cq.terms) t = ids[t];
+}
+
+}  // namespace
+}  // namespace st
+
 extern "C" int st_search_plan_create(const int8_t* plans_data,
                                      int64_t plans_data_len,
                                      const int64_t* plans_offsets,
@@ -744,7 +888,6 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
     std::vector<Pending> cur;
     cur.reserve(static_cast<size_t>(std::min<int64_t>(num_queries, 1 << 16)));
     static thread_local TermTable terms;
-    static thread_local CompileScratch scratch;
     terms.hash_k = std::max<int64_t>(hash_k, 0);
     terms.clear();
 
@@ -851,34 +994,56 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
       terms.clear();
     };
 
-    // Queries beyond the batch kernels' limits (stack depth, program size,
-    // or more distinct terms than a batch's position area holds on their
-    // own) each become a generic batch, after the regular ones.
+    // Every query is compiled on its own (in parallel for large batches);
+    // then, in query order, its terms join the running batch.  Queries
+    // beyond the batch kernels' limits (stack depth, program size, or more
+    // distinct terms than a batch's position area holds on their own) each
+    // become a generic batch, after the regular ones.
+    std::vector<LocalQuery> local(static_cast<size_t>(num_queries));
+    const auto compile_one = [&](int64_t q) {
+      compile_local(plans_data, plans_data_len, plans_offsets, q, hash_k, plan->k_eff,
+                    local[static_cast<size_t>(q)]);
+    };
+    if (plans_data_len >= kParallelCompileBytes && num_queries > 1) {
+      CompilePool::get().run(num_queries, 32, compile_one);
+    } else {
+      for (int64_t q = 0; q < num_queries; ++q) compile_one(q);
+    }
+    for (const LocalQuery& lq : local)  // the first failing query's error
+      if (lq.error) std::rethrow_exception(lq.error);
+    const int64_t hk = std::max<int64_t>(hash_k, 0);
     std::vector<int64_t> generic_q;
+    std::vector<uint32_t> ids;
+    {
+      size_t leaves = 0;
+      for (const LocalQuery& lq : local) leaves += lq.local_terms;
+      terms.reserve(std::min<size_t>(leaves, static_cast<size_t>(term_capacity) + 1));
+    }
     for (int64_t q = 0; q < num_queries; ++q) {
-      CompiledQuery cq = compile_query(plans_data, plans_data_len,
-                                       plans_offsets, q, hash_k,
-                                       plan->k_eff, terms, scratch);
-      if (!cq.generic && static_cast<int64_t>(terms.size()) > term_capacity) {
+      LocalQuery& lq = local[static_cast<size_t>(q)];
+      intern_local(lq, hk, terms, ids);
+      if (!lq.cq.generic && static_cast<int64_t>(terms.size()) > term_capacity) {
         terms.rollback();
         flush();
-        cq = compile_query(plans_data, plans_data_len, plans_offsets, q,
-                           hash_k, plan->k_eff, terms, scratch);
+        intern_local(lq, hk, terms, ids);
       }
-      if (cq.generic || static_cast<int64_t>(terms.size()) > term_capacity) {
+      if (lq.cq.generic || static_cast<int64_t>(terms.size()) > term_capacity) {
         terms.rollback();
         generic_q.push_back(q);
         continue;
       }
       terms.commit();
-      plan->max_stack = std::max(plan->max_stack, cq.need);
-      cur.push_back(Pending{q, std::move(cq)});
+      rename_terms(lq.cq, ids);
+      plan->max_stack = std::max(plan->max_stack, lq.cq.need);
+      cur.push_back(Pending{q, std::move(lq.cq)});
     }
     flush();
     for (const int64_t q : generic_q) {
+      // alone in its batch: the local term ids are the batch's
       terms.clear();
-      const CompiledQuery cq = compile_query(plans_data, plans_data_len, plans_offsets, q, hash_k,
-                                             plan->k_eff, terms, scratch);
+      const LocalQuery& lq = local[static_cast<size_t>(q)];
+      intern_local(lq, hk, terms, ids);
+      const CompiledQuery& cq = lq.cq;
       plan->max_stack = std::max(plan->max_stack, cq.need);
       SearchBatch b;
       b.generic = true;

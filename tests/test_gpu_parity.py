@@ -358,8 +358,9 @@ def test_config_shapes_vs_oracle(cfg, docs):
     (silvertorch_amd.synthetic) at reduced doc counts: the
     same feature counts, value distributions, k / hash_k / B_MULTIPLIER and
     query shapes (cfg3: bundles wider than the LDS tile, k = 4, boolean trees
-    with NOT; cfg4, a build-only configuration: uniform values over 10M and
-    1-8 values per feature, searched with flat queries of 1-4 terms drawn
+    with NOT, whose 1,024 plans are large enough for the multi-threaded
+    host compile; cfg4, a build-only configuration: uniform values over 10M
+    and 1-8 values per feature, searched with flat queries of 1-4 terms drawn
     from its value distribution), build and search bit-exact against the
     oracle."""
     from silvertorch_amd import synthetic as S

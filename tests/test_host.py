@@ -151,6 +151,59 @@ def test_plan_compiler_nesting_and_identity_operators():
     assert capi.SearchPlan(data, offs, 3, 7).num_queries == 1
 
 
+_BIG_PLAN_SCRIPT = r"""
+import hashlib, sys
+import numpy as np
+from silvertorch_amd import capi, synthetic as S
+cspec, qspec = S.CONFIGS["cfg3"]
+queries = S.make_queries(cspec, qspec, seed=1)
+_, data, offs = capi.parse_expression_query_batch(queries, cspec.hash_k, True, 5)
+assert len(data) >= 192 * 1024, len(data)  # large enough for the parallel compile
+plan = capi.SearchPlan(data, offs, cspec.k, cspec.hash_k)
+w = 1600 + 40 * (np.arange(300) % 9)
+plan.bind_widths(np.concatenate([[0], np.cumsum(w)]))
+print(hashlib.sha256(plan.blob()).hexdigest())
+"""
+
+
+def test_plan_compiler_threads_give_identical_plans():
+    """Large plans are compiled query by query on several host threads; the
+    bound plan must not depend on their number or timing."""
+    import os
+    import subprocess
+    import sys
+
+    digests = set()
+    for threads in ("1", "3", "8", "8"):
+        env = dict(os.environ, ST_PLAN_THREADS=threads, PYTHONPATH=str(ROOT))
+        out = subprocess.run([sys.executable, "-c", _BIG_PLAN_SCRIPT], env=env, cwd=ROOT,
+                             capture_output=True, text=True, timeout=300)
+        assert out.returncode == 0, out.stderr
+        digests.add(out.stdout.strip())
+    assert len(digests) == 1
+
+
+def test_plan_compiler_reports_first_failing_query_of_a_large_plan():
+    """With the parallel compile, the error raised is the one of the first
+    malformed query, as in a query-by-query compile."""
+    from silvertorch_amd import synthetic as S
+
+    cspec, qspec = S.CONFIGS["cfg3"]
+    queries = S.make_queries(cspec, qspec, seed=2)
+    _, data, offs = capi.parse_expression_query_batch(queries, cspec.hash_k, True, 5)
+    assert len(data) >= 192 * 1024
+    data = bytearray(data)
+    for q in (900, 700):  # an unknown operator code as the first op of each
+        data[offs[8 * q]] = 9
+    with pytest.raises(capi.StError, match="unknown operator: 9"):
+        capi.SearchPlan(bytes(data), offs, cspec.k, cspec.hash_k)
+    data[offs[8 * 700]] = 9
+    bad = list(offs)
+    bad[8 * 650 + 7] = len(data) + 8  # query 650's hash range runs past the data
+    with pytest.raises(capi.StError, match="query plan 650"):
+        capi.SearchPlan(bytes(data), bad, cspec.k, cspec.hash_k)
+
+
 def test_torch_ops_schemas_and_cpu_parser():
     import torch
 
