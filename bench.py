@@ -286,6 +286,73 @@ def measure_partial(st, bi, bo, pd, po, k, hk, N, packed, steps):
     }
 
 
+def measure_fresh(st, O, steps):
+    """take_top_k_and_gather_from_main_and_fresh (fresh_index_post_processing.cpp:
+    231-290): 512 query rows, 10,000 main and 2,000 fresh candidates per row
+    (float32 scores), the best 1,000 of each merged row with their doc ids
+    (int64 [N, 1]) and bf16[128] embeddings gathered from a 1M-row main and a
+    100K-row fresh table.  Op time per call; algorithmic bytes: the scores
+    read, the chosen index-table entries and data rows read, the outputs
+    written.  Checks: 8 sampled rows' top lists against the oracle, every
+    gathered row against a torch gather through the returned indices."""
+    import numpy as np
+    import torch
+
+    R, Nm, Nf, K, D = 512, 10_000, 2_000, 1_000, 128
+    Dm, Df = 1_000_000, 100_000
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    ms_ = torch.rand(R, Nm, device="cuda", generator=g)
+    fs_ = torch.rand(R, Nf, device="cuda", generator=g)
+    mi = torch.randint(0, Dm, (R, Nm), device="cuda", generator=g)
+    fi = torch.randint(0, Df, (R, Nf), device="cuda", generator=g)
+    main_data = [torch.arange(Dm, device="cuda").view(Dm, 1),
+                 torch.randn(Dm, D, device="cuda", generator=g).to(torch.bfloat16)]
+    fresh_data = [torch.arange(Df, device="cuda").view(Df, 1) + 10**9,
+                  torch.randn(Df, D, device="cuda", generator=g).to(torch.bfloat16)]
+    keys = ["doc_id", "embedding"]
+
+    def step():
+        return st.take_top_k_and_gather_from_main_and_fresh(ms_, fs_, mi, fi, K, keys, main_data, fresh_data)
+
+    out = step()
+    torch.cuda.synchronize()
+    n = max(steps // 5, 10)
+    t = time.perf_counter()
+    for _ in range(n):
+        out = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t) * 1e3 / n
+    top_s, top_i, from_f, gathered = out
+    # sampled rows vs the oracle (scores and indices), all rows' gathers vs torch
+    rows = [0, 1, 100, 255, 256, 400, 510, 511]
+    want_s, want_i, want_f, _ = O.fresh_topk_gather(ms_[rows].cpu().numpy(), fs_[rows].cpu().numpy(),
+                                                     mi[rows].cpu().numpy(), fi[rows].cpu().numpy(), K, [], [])
+    ok = (np.array_equal(top_i[rows].cpu().numpy(), want_i) and np.array_equal(top_s[rows].cpu().numpy(), want_s)
+          and np.array_equal(from_f[rows].cpu().numpy(), want_f))
+    fresh = top_i < Nf
+    src_f = torch.gather(fi, 1, top_i.clamp(max=Nf - 1))
+    src_m = torch.gather(mi, 1, (top_i - Nf).clamp(min=0))
+    for key, md, fd in zip(keys, main_data, fresh_data):
+        want = torch.where(fresh.reshape(-1, 1), fd[src_f.reshape(-1)], md[src_m.reshape(-1)])
+        ok &= bool(torch.equal(gathered[key].reshape(want.shape), want))
+    row_bytes = 8 + 2 * D
+    alg = R * (Nm + Nf) * 4 + R * K * (8 + row_bytes) + R * K * (4 + 8 + 1 + row_bytes)
+    log(f"fresh merge: {R} rows x ({Nm} main + {Nf} fresh), top {K}, ids + bf16[{D}] gathered, {ms:.3f} ms/call, "
+        f"sampled rows equal the oracle and gathers equal torch's: {ok}")
+    if not ok:
+        sys.exit("parity failure in the fresh merge")
+    return {
+        "op": "take_top_k_and_gather_from_main_and_fresh",
+        "workload": f"{R} rows x ({Nm} main + {Nf} fresh) float32 scores, k={K}, int64 ids + bf16[{D}] rows "
+                    f"gathered from {Dm} main / {Df} fresh rows",
+        "ms_per_call": ms, "algorithmic_bytes": alg, "achieved_gbs": alg / ms / 1e6,
+        "frac_of_hbm_peak": alg / ms / 1e6 / HBM_PEAK_GBS,
+        "note": "op wall time (top-k, two gathers); bytes: scores read, chosen index entries and data rows "
+                "read, top scores / indices / flags and gathered rows written",
+    }
+
+
 def measure_kmean(st, O, N, packed, steps):
     """fused_kmean_ann, the scoring step after the search, on the cfg2 corpus:
     IVF-style clusters of 4,000 docs, 16 per query (seeded), bf16[128] doc
@@ -738,6 +805,7 @@ def main():
 
     partial_report = None if args.bool_mask else measure_partial(st, bi, bo, pd, po, k, hk, N, out, args.steps)
     kmean_report = None if args.bool_mask else measure_kmean(st, O, N, out, args.steps)
+    fresh_report = None if args.bool_mask else measure_fresh(st, O, args.steps)
     topk_report = None if args.no_topk else measure_topk(st, capi, args.steps)
     build4_report = None if args.no_build4 else measure_build_cfg4(st, O)
     cfg3_report = None if args.no_cfg3 else measure_search_cfg3(st, O)
@@ -788,6 +856,7 @@ def main():
         "ids": ids_report,
         "partial": partial_report,
         "kmean_ann": kmean_report,
+        "fresh_merge": fresh_report,
         "topk": topk_report,
     }
     print(json.dumps(result), flush=True)

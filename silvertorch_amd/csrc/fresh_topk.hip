@@ -15,7 +15,10 @@
 // lower merged index first.  NaN ranks above every number (at::topk's CPU
 // comparator); -0.0 and +0.0 are equal.
 //
-// Selection: one workgroup per row keeps the row's best P = pow2 >= k'
+// Selection, rows of at most 16,384 entries with k' <= 4,096: one workgroup
+// per row holds the row in registers, finds the k'-th best key by a radix
+// select and sorts the k' best in LDS (fresh_select_kernel).  Other rows:
+// one workgroup per row keeps the row's best P = pow2 >= k'
 // entries (key, index) sorted, best first.  The row is read 1024 entries at
 // a time; entries better than the running k'-th best are compacted into a
 // candidate buffer (wave ballot + per-wave counts), and a full buffer is
@@ -110,8 +113,9 @@ __device__ void bitonic_sort(uint64_t* keys, uint32_t* idx, int n) {
   const int tid = threadIdx.x;
   for (int size = 2; size <= n; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const int ls = __builtin_ctz(stride);
       for (int p = tid; p < n / 2; p += kFreshThreads) {
-        const int i = (p / stride) * 2 * stride + (p % stride);
+        const int i = ((p >> ls) << (ls + 1)) | (p & (stride - 1));
         const int l = i + stride;
         const bool best_first = (i & size) == 0;
         const uint64_t ki = keys[i], kl = keys[l];
@@ -149,8 +153,9 @@ __device__ void merge_into(KeyPtr rk, IdxPtr ri, int64_t P, const uint64_t* ck,
   }
   __syncthreads();
   for (int64_t stride = P >> 1; stride > 0; stride >>= 1) {
+    const int ls = __builtin_ctzll(static_cast<uint64_t>(stride));
     for (int64_t p = tid; p < P / 2; p += kFreshThreads) {
-      const int64_t i = (p / stride) * 2 * stride + (p % stride);
+      const int64_t i = ((p >> ls) << (ls + 1)) | (p & (stride - 1));
       const int64_t l = i + stride;
       const uint64_t ki = rk[i], kl = rk[l];
       const uint32_t ii = ri[i], il = ri[l];
@@ -280,8 +285,250 @@ __global__ __launch_bounds__(kFreshThreads) void fresh_topk_kernel(FreshTopkArgs
   }
 }
 
+// Rows of at most kSelectThreads * kSelectMaxPer entries with k <= kSelectMaxK
+// take a selection instead of the streaming merge: each thread holds kPer
+// consecutive entries of the row in registers; a radix select over the
+// bits in which the row's keys differ (8 bits a pass, histogram in LDS)
+// finds the k-th best key T and how many keys exceed it; the entries above
+// T and the lowest-indexed entries equal to T (as many as k needs) are
+// compacted in index order into LDS and sorted (bitonic) best first.
+constexpr int kSelectThreads = 1024;
+constexpr int kSelectWaves = kSelectThreads / 64;
+constexpr int kSelectMaxPer = 16;  // keys per thread (64-bit, in registers)
+constexpr int kSelectMaxK = 4096;
+
+// Exclusive prefix sum over the workgroup of one value per thread (in
+// thread order); *total receives the sum.  Uses scratch[kSelectWaves + 1].
+__device__ __forceinline__ uint32_t select_scan(uint32_t v, uint32_t* scratch, uint32_t* total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t y = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += y;
+  }
+  if (lane == 63) scratch[wave] = incl;
+  __syncthreads();
+  uint32_t before = 0, sum = 0;
+#pragma unroll
+  for (int w = 0; w < kSelectWaves; ++w) {
+    const uint32_t c = scratch[w];
+    before += w < wave ? c : 0u;
+    sum += c;
+  }
+  __syncthreads();  // scratch is reused by the next scan
+  *total = sum;
+  return before + incl - v;
+}
+
+template <int kType, int kPer>
+__global__ __launch_bounds__(kSelectThreads) void fresh_select_kernel(FreshTopkArgs a) {
+  __shared__ uint32_t hist[kSelectWaves][256];  // one histogram per wave
+  __shared__ uint32_t scan_scratch[kSelectWaves + 1];
+  __shared__ uint64_t red_and[kSelectWaves], red_or[kSelectWaves];
+  __shared__ uint64_t s_key[kSelectMaxK];
+  __shared__ uint32_t s_idx[kSelectMaxK];
+  __shared__ uint64_t s_prefix;
+  __shared__ uint32_t s_remaining, s_above;
+
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t N = a.num_fresh + a.num_main;
+  const int64_t k = a.k;
+  const void* fs = static_cast<const char*>(a.fresh_scores) + row * a.num_fresh * score_bytes(kType);
+  const void* ms = static_cast<const char*>(a.main_scores) + row * a.num_main * score_bytes(kType);
+
+  // entries m = tid * kPer + j of the merged row
+  uint64_t key[kPer];
+  const int64_t m0 = static_cast<int64_t>(tid) * kPer;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int64_t m = m0 + j;
+    key[j] = m >= N ? 0ull : (m < a.num_fresh ? score_key<kType>(fs, m) : score_key<kType>(ms, m - a.num_fresh));
+  }
+  // bits in which the row's keys differ
+  uint64_t kand = ~0ull, kor = 0ull;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    if (m0 + j < N) {
+      kand &= key[j];
+      kor |= key[j];
+    }
+  }
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) {
+    kand &= __shfl_xor(kand, d, 64);
+    kor |= __shfl_xor(kor, d, 64);
+  }
+  if (lane == 0) {
+    red_and[wave] = kand;
+    red_or[wave] = kor;
+  }
+  for (int i = tid; i < kSelectWaves * 256; i += kSelectThreads) (&hist[0][0])[i] = 0u;
+  __syncthreads();
+  kand = ~0ull;
+  kor = 0ull;
+#pragma unroll
+  for (int w = 0; w < kSelectWaves; ++w) {
+    kand &= red_and[w];
+    kor |= red_or[w];
+  }
+  const uint64_t diff = kand ^ kor;
+  // Radix select: prefix holds the bits of T above `shift` (bits above the
+  // highest differing bit are common to every key); `remaining` is how many
+  // entries of the current prefix k still needs.
+  uint64_t prefix = kand & ~((diff == 0ull) ? 0ull : ((~0ull) >> __builtin_clzll(diff)));
+  uint32_t remaining = static_cast<uint32_t>(k), above = 0u;
+  int shift = diff == 0ull ? -1 : ((63 - __builtin_clzll(diff)) / 8) * 8;
+  for (; shift >= 0; shift -= 8) {
+    const uint64_t hi_mask = shift + 8 >= 64 ? 0ull : (~0ull << (shift + 8));
+    // each wave counts the digits of its keys under the current prefix in
+    // its own histogram (score rows are often narrow in their top digits:
+    // one histogram for the workgroup would serialize on a few bins)
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+      if (m0 + j < N && (key[j] & hi_mask) == (prefix & hi_mask))
+        atomicAdd(&hist[wave][(key[j] >> shift) & 0xFFu], 1u);
+    __syncthreads();
+    if (wave == 0) {
+      // bins from the top digit down: 4 per lane, lane 0 holding 255..252
+      uint32_t c[4], sum = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c[i] = 0;
+#pragma unroll
+        for (int w = 0; w < kSelectWaves; ++w) c[i] += hist[w][255 - (lane * 4 + i)];
+        sum += c[i];
+      }
+      uint32_t incl = sum;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t y = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += y;
+      }
+      // the digit where the count from the top reaches `remaining`
+      uint32_t run = incl - sum;
+      int digit = -1;
+      uint32_t run_before = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (digit < 0 && run + c[i] >= remaining && run < remaining) {
+          digit = 255 - (lane * 4 + i);
+          run_before = run;
+        }
+        run += c[i];
+      }
+      if (digit >= 0) {
+        s_prefix = (prefix & hi_mask) | (static_cast<uint64_t>(digit) << shift);
+        s_remaining = remaining - run_before;
+        s_above = above + run_before;
+      }
+    }
+    __syncthreads();
+    prefix = s_prefix;
+    remaining = s_remaining;
+    above = s_above;
+    for (int i = tid; i < kSelectWaves * 256; i += kSelectThreads) (&hist[0][0])[i] = 0u;
+    __syncthreads();
+  }
+  const uint64_t T = prefix;  // the k-th best key; `above` keys exceed it
+  const uint32_t ties_taken = static_cast<uint32_t>(k) - above;
+  // in index order: every key above T, and the first ties_taken keys == T
+  uint32_t n_tie = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) n_tie += (m0 + j < N && key[j] == T) ? 1u : 0u;
+  uint32_t tie_total;
+  uint32_t tie_before = select_scan(n_tie, scan_scratch, &tie_total);
+  uint32_t mine = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    if (m0 + j >= N) continue;
+    if (key[j] > T) {
+      ++mine;
+    } else if (key[j] == T) {
+      if (tie_before < ties_taken) ++mine;
+      ++tie_before;
+    }
+  }
+  uint32_t total;
+  uint32_t at = select_scan(mine, scan_scratch, &total);
+  tie_before -= n_tie;
+  int n = 2;
+  while (n < static_cast<int>(k)) n <<= 1;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    if (m0 + j >= N) continue;
+    bool take = key[j] > T;
+    if (key[j] == T) {
+      take = tie_before < ties_taken;
+      ++tie_before;
+    }
+    if (take) {
+      s_key[at] = key[j];
+      s_idx[at] = static_cast<uint32_t>(m0 + j);
+      ++at;
+    }
+  }
+  for (int i = static_cast<int>(k) + tid; i < n; i += kSelectThreads) {
+    s_key[i] = 0ull;
+    s_idx[i] = kNoIndex;
+  }
+  __syncthreads();
+  // bitonic sort of s_key / s_idx [0, n), best first
+  for (int size = 2; size <= n; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const int ls = __builtin_ctz(stride);
+      for (int p = tid; p < n / 2; p += kSelectThreads) {
+        const int i = ((p >> ls) << (ls + 1)) | (p & (stride - 1));
+        const int l = i + stride;
+        const bool best_first = (i & size) == 0;
+        const uint64_t ki = s_key[i], kl = s_key[l];
+        const uint32_t ii = s_idx[i], il = s_idx[l];
+        if (before(kl, il, ki, ii) == best_first) {
+          s_key[i] = kl;
+          s_key[l] = ki;
+          s_idx[i] = il;
+          s_idx[l] = ii;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int64_t j = tid; j < k; j += kSelectThreads) {
+    uint32_t m = s_idx[j];
+    if (static_cast<int64_t>(m) >= N) m = 0;  // never: exactly k entries were taken
+    const int64_t o = row * k + j;
+    a.top_index[o] = static_cast<int64_t>(m);
+    a.from_fresh[o] = static_cast<int64_t>(m) < a.num_fresh ? 1 : 0;
+    constexpr int B = score_bytes(kType);
+    const char* src = m < a.num_fresh ? static_cast<const char*>(fs) + static_cast<int64_t>(m) * B
+                                      : static_cast<const char*>(ms) + (static_cast<int64_t>(m) - a.num_fresh) * B;
+    char* dst = static_cast<char*>(a.top_scores) + o * B;
+    if constexpr (B == 8) {
+      *reinterpret_cast<uint64_t*>(dst) = *reinterpret_cast<const uint64_t*>(src);
+    } else if constexpr (B == 4) {
+      *reinterpret_cast<uint32_t*>(dst) = *reinterpret_cast<const uint32_t*>(src);
+    } else if constexpr (B == 2) {
+      *reinterpret_cast<uint16_t*>(dst) = *reinterpret_cast<const uint16_t*>(src);
+    } else {
+      *dst = *src;
+    }
+  }
+}
+
 template <int kType>
 void launch_topk_typed(const FreshTopkArgs& a, hipStream_t s) {
+  const int64_t N = a.num_fresh + a.num_main;
+  if (a.k <= kSelectMaxK && N <= static_cast<int64_t>(kSelectThreads) * kSelectMaxPer) {
+    const dim3 g(static_cast<unsigned>(a.rows)), b(kSelectThreads);
+    if (N <= kSelectThreads * 4)
+      hipLaunchKernelGGL((fresh_select_kernel<kType, 4>), g, b, 0, s, a);
+    else if (N <= kSelectThreads * 8)
+      hipLaunchKernelGGL((fresh_select_kernel<kType, 8>), g, b, 0, s, a);
+    else
+      hipLaunchKernelGGL((fresh_select_kernel<kType, 16>), g, b, 0, s, a);
+    return;
+  }
   if (a.p <= kFreshLdsMaxK)
     hipLaunchKernelGGL((fresh_topk_kernel<kType, true>), dim3(a.rows), dim3(kFreshThreads), 0, s, a);
   else
@@ -294,8 +541,8 @@ int64_t kept_length(int64_t k) {
   return p;
 }
 
-// Gather of one data tensor: element e of the output is element e % D of the
-// source row chosen for output row e / D.
+// Gather of one data tensor: unit e of the output is unit e % D of the
+// source row chosen for output row e / D (D units per row).
 template <typename Idx, typename Elem>
 __global__ void fresh_gather_kernel(const int64_t* __restrict__ top_index, int64_t k,
                                     int64_t total, const Idx* __restrict__ fresh_idx,
@@ -318,27 +565,40 @@ __global__ void fresh_gather_kernel(const int64_t* __restrict__ top_index, int64
   out[e] = rows > 0 ? data[src * dim + d] : Elem{};
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// The rows are moved in the widest unit (16, 8, 4, 2 or 1 bytes) that
+// divides a row and the alignment of the three data pointers.
 template <typename Idx>
 void launch_gather_idx(const int64_t* top_index, int64_t rows, int64_t k, const void* fi,
                        int64_t fs, const void* mi, int64_t ms, int64_t num_fresh,
                        const void* fd, int64_t frows, const void* md, int64_t mrows,
                        int64_t dim, int elem_bytes, void* out, hipStream_t s) {
-  const int64_t total = rows * k * dim;
+  ST_CHECK(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8,
+           "unsupported element size ", elem_bytes);
+  const int64_t row_bytes = dim * elem_bytes;
+  const uintptr_t align = reinterpret_cast<uintptr_t>(fd) | reinterpret_cast<uintptr_t>(md) |
+                          reinterpret_cast<uintptr_t>(out);
+  int unit = 16;
+  while (unit > 1 && (row_bytes % unit != 0 || align % unit != 0)) unit >>= 1;
+  const int64_t units = row_bytes / unit;
+  const int64_t total = rows * k * units;
   const int threads = 256;
+  ST_CHECK((total + threads - 1) / threads <= 0x7FFFFFFF, "gather of ", total, " units is too large");
   const dim3 grid(static_cast<unsigned>((total + threads - 1) / threads));
   auto go = [&](auto tag) {
     using E = decltype(tag);
     hipLaunchKernelGGL((fresh_gather_kernel<Idx, E>), grid, dim3(threads), 0, s, top_index, k,
                        total, static_cast<const Idx*>(fi), fs, static_cast<const Idx*>(mi), ms,
                        num_fresh, static_cast<const E*>(fd), frows, static_cast<const E*>(md),
-                       mrows, dim, static_cast<E*>(out));
+                       mrows, units, static_cast<E*>(out));
   };
-  switch (elem_bytes) {
+  switch (unit) {
     case 1: go(uint8_t{}); break;
     case 2: go(uint16_t{}); break;
     case 4: go(uint32_t{}); break;
     case 8: go(uint64_t{}); break;
-    default: fail("unsupported element size ", elem_bytes);
+    default: go(u32x4{}); break;
   }
 }
 

@@ -994,54 +994,76 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
       terms.clear();
     };
 
-    // Every query is compiled on its own (in parallel for large batches);
-    // then, in query order, its terms join the running batch.  Queries
-    // beyond the batch kernels' limits (stack depth, program size, or more
-    // distinct terms than a batch's position area holds on their own) each
-    // become a generic batch, after the regular ones.
-    std::vector<LocalQuery> local(static_cast<size_t>(num_queries));
-    const auto compile_one = [&](int64_t q) {
-      compile_local(plans_data, plans_data_len, plans_offsets, q, hash_k, plan->k_eff,
-                    local[static_cast<size_t>(q)]);
-    };
-    if (plans_data_len >= kParallelCompileBytes && num_queries > 1) {
-      CompilePool::get().run(num_queries, 32, compile_one);
-    } else {
-      for (int64_t q = 0; q < num_queries; ++q) compile_one(q);
-    }
-    for (const LocalQuery& lq : local)  // the first failing query's error
-      if (lq.error) std::rethrow_exception(lq.error);
+    // Queries are compiled in order, their terms interned into the running
+    // batch.  Large plans are first compiled query by query on the pool with
+    // local term ids; in query order, each query's terms then join the
+    // batch and its program is renamed.  Queries beyond the batch kernels'
+    // limits (stack depth, program size, or more distinct terms than a
+    // batch's position area holds on their own) each become a generic batch,
+    // after the regular ones.
+    const bool parallel = plans_data_len >= kParallelCompileBytes && num_queries > 1;
     const int64_t hk = std::max<int64_t>(hash_k, 0);
+    std::vector<LocalQuery> local;
     std::vector<int64_t> generic_q;
     std::vector<uint32_t> ids;
-    {
+    if (parallel) {
+      local.resize(static_cast<size_t>(num_queries));
+      CompilePool::get().run(num_queries, 32, [&](int64_t q) {
+        compile_local(plans_data, plans_data_len, plans_offsets, q, hash_k, plan->k_eff,
+                      local[static_cast<size_t>(q)]);
+      });
+      for (const LocalQuery& lq : local)  // the first failing query's error
+        if (lq.error) std::rethrow_exception(lq.error);
       size_t leaves = 0;
       for (const LocalQuery& lq : local) leaves += lq.local_terms;
       terms.reserve(std::min<size_t>(leaves, static_cast<size_t>(term_capacity) + 1));
-    }
-    for (int64_t q = 0; q < num_queries; ++q) {
-      LocalQuery& lq = local[static_cast<size_t>(q)];
-      intern_local(lq, hk, terms, ids);
-      if (!lq.cq.generic && static_cast<int64_t>(terms.size()) > term_capacity) {
-        terms.rollback();
-        flush();
+      for (int64_t q = 0; q < num_queries; ++q) {
+        LocalQuery& lq = local[static_cast<size_t>(q)];
         intern_local(lq, hk, terms, ids);
+        if (!lq.cq.generic && static_cast<int64_t>(terms.size()) > term_capacity) {
+          terms.rollback();
+          flush();
+          intern_local(lq, hk, terms, ids);
+        }
+        if (lq.cq.generic || static_cast<int64_t>(terms.size()) > term_capacity) {
+          terms.rollback();
+          generic_q.push_back(q);
+          continue;
+        }
+        terms.commit();
+        rename_terms(lq.cq, ids);
+        plan->max_stack = std::max(plan->max_stack, lq.cq.need);
+        cur.push_back(Pending{q, std::move(lq.cq)});
       }
-      if (lq.cq.generic || static_cast<int64_t>(terms.size()) > term_capacity) {
-        terms.rollback();
-        generic_q.push_back(q);
-        continue;
+    } else {
+      static thread_local CompileScratch scratch;
+      for (int64_t q = 0; q < num_queries; ++q) {
+        CompiledQuery cq = compile_query(plans_data, plans_data_len, plans_offsets, q, hash_k,
+                                         plan->k_eff, terms, scratch);
+        if (!cq.generic && static_cast<int64_t>(terms.size()) > term_capacity) {
+          terms.rollback();
+          flush();
+          cq = compile_query(plans_data, plans_data_len, plans_offsets, q, hash_k, plan->k_eff,
+                             terms, scratch);
+        }
+        if (cq.generic || static_cast<int64_t>(terms.size()) > term_capacity) {
+          terms.rollback();
+          generic_q.push_back(q);
+          continue;
+        }
+        terms.commit();
+        plan->max_stack = std::max(plan->max_stack, cq.need);
+        cur.push_back(Pending{q, std::move(cq)});
       }
-      terms.commit();
-      rename_terms(lq.cq, ids);
-      plan->max_stack = std::max(plan->max_stack, lq.cq.need);
-      cur.push_back(Pending{q, std::move(lq.cq)});
     }
     flush();
     for (const int64_t q : generic_q) {
       // alone in its batch: the local term ids are the batch's
       terms.clear();
-      const LocalQuery& lq = local[static_cast<size_t>(q)];
+      LocalQuery single;
+      if (!parallel)
+        compile_local(plans_data, plans_data_len, plans_offsets, q, hash_k, plan->k_eff, single);
+      const LocalQuery& lq = parallel ? local[static_cast<size_t>(q)] : single;
       intern_local(lq, hk, terms, ids);
       const CompiledQuery& cq = lq.cq;
       plan->max_stack = std::max(plan->max_stack, cq.need);

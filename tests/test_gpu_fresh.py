@@ -109,6 +109,8 @@ def _capi_topk(ms, fs, k, stype):
     (3, 0, 500, 500, 4),         # main only, k = the whole row
     (4, 2000, 0, 64, 50),        # fresh only
     (2, 3000, 9000, 9000, 40),   # kept list in global memory, ties
+    (3, 6000, 10384, 4096, 30),  # the largest row and k of the register selection
+    (2, 8000, 8385, 3000, 20),   # one entry more: the streaming merge, kept list in LDS
     (9, 1, 1, 1, 2),
 ])
 def test_capi_topk_ties_vs_oracle(stype, rows, nf, nm, k, levels):
