@@ -262,6 +262,7 @@ __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
     if (tid == 0) {
       num_slots[0] = ns;
       num_slots[1] = all_wide ? 1u : 0u;
+      num_slots[2] = some_wide ? 1u : 0u;
       any_wide = some_wide ? 1u : 0u;
     }
   }

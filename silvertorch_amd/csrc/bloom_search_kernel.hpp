@@ -1344,8 +1344,8 @@ __device__ __forceinline__ void wide_eval_group(const char* stream, const ST_CON
 // otherwise workgroup w takes bundles w, w + grid, ... with all slices.  Each
 // wave issues its share of the next slice's loads when it has evaluated the
 // current one.
-// `num_slots` / `slot_width` (device binding; nullptr when the host decided
-// to launch) let the kernel return at once when no slot width is wide.
+// `num_slots` (device binding; nullptr when the host decided to launch) lets
+// the kernel return at once when no slot width is wide (its word 2).
 template <int K>
 __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
     const int64_t* __restrict__ index, int64_t index_numel,
@@ -1363,14 +1363,8 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
   const ST_CONST uint32_t* border = as_const(bundle_order);
   const ST_CONST uint32_t* tab = as_const(table);
 
-  if (num_slots != nullptr) {
-    const ST_CONST uint32_t* ns = as_const(num_slots);
-    const ST_CONST int64_t* sw = as_const(slot_width);
-    const uint32_t n = min(ns[0], static_cast<uint32_t>(kMaxWidthSlots));
-    bool any = false;
-    for (uint32_t s = 0; s < n; ++s) any |= wide_width(sw[s]);
-    if (!any) return;
-  }
+  // the census's word: some slot width is wide
+  if (num_slots != nullptr && as_const(num_slots)[2] == 0u) return;
   if (tid < 2 * kWidePieces) {
     const uint32_t fill = tid < kWidePieces ? ~0u : 0u;
     tile[kWideOnesRow * kWidePieces + tid] = u32x4{fill, fill, fill, fill};

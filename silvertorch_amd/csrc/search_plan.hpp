@@ -247,7 +247,7 @@ struct st_search_plan {
   // widths on the device into the part of the device copy past the host blob
   bool device_bind = false;
   uint64_t device_bytes = 0;         // size of the device copy
-  uint64_t off_num_slots = 0;        // uint32[2] (device-written): slots, all wide
+  uint64_t off_num_slots = 0;        // uint32[3] (device-written): slots, all wide, some wide
   uint64_t off_slot_width = 0;       // int64[kMaxWidthSlots] (device-written)
   uint64_t off_bind_table = 0;       // uint64[batches * kBindTableWords]
   // set by st_search_plan_upload_source: the search calls copy the blob
