@@ -31,6 +31,7 @@
 #include <cstdint>
 
 #include "../../include/silvertorch_hip.h"
+#include "st_common.hpp"
 #include "st_errors.hpp"
 
 namespace st {

@@ -31,6 +31,7 @@
 #include <cstdint>
 #include <mutex>
 
+#include "st_common.hpp"
 #include "st_errors.hpp"
 
 namespace st {

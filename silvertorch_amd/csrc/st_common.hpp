@@ -11,6 +11,12 @@
 #define ST_HD inline
 #endif
 
+// The kernels are written for gfx950 (MI355X): 160 KB of LDS per workgroup
+// (the search tile, the wide-bundle slice, kmean_ann's staging), wave64.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "silvertorch_amd device code is built for gfx950 only"
+#endif
+
 namespace st {
 
 constexpr int64_t kBitsPerColumn = 64;
