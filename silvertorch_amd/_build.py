@@ -52,6 +52,7 @@ LIB_SOURCES = [
     "kmean_ann.hip",
     "fresh_topk.hip",
     "search_plan.cpp",
+    "host_pool.cpp",
     "expression_parser.cpp",
 ]
 

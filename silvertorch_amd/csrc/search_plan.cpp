@@ -12,12 +12,8 @@
 // AND pops `children` values and ANDs them into all-ones; OR ORs them into
 // zero; NOT needs exactly one child; EMPTY pushes all-ones; the answer is the
 // top of the stack.
-#include <unistd.h>
-
 #include <algorithm>
-#include <atomic>
 #include <climits>
-#include <condition_variable>
 #include <cstdlib>
 #include <cstring>
 #include <exception>
@@ -25,11 +21,11 @@
 #include <memory>
 #include <mutex>
 #include <string>
-#include <thread>
 #include <unordered_map>
 
 #include "search_plan.hpp"
 #include "st_common.hpp"
+#include "host_pool.hpp"
 #include "st_errors.hpp"
 #include "wide_balance.hpp"
 
@@ -731,81 +727,6 @@ namespace {
 // on one thread).
 constexpr int64_t kParallelCompileBytes = 192 * 1024;
 
-// Host threads of the plan compiler: a few workers started on first use
-// (ST_PLAN_THREADS, default min(8, hardware threads) including the caller)
-// that share one job at a time with the calling thread.  A caller that
-// finds the pool busy, or runs in a child of the process that started it,
-// does the work alone.
-class CompilePool {
- public:
-  static CompilePool& get() {
-    static CompilePool* pool = new CompilePool();  // never destroyed: workers may still wait
-    return *pool;
-  }
-  // fn(i) for every i in [0, n), chunks of `chunk` taken in turn by the
-  // workers and the caller; fn must not throw.
-  void run(int64_t n, int64_t chunk, const std::function<void(int64_t)>& fn) {
-    std::unique_lock<std::mutex> busy(job_mu_, std::try_to_lock);
-    if (!busy.owns_lock() || getpid() != pid_ || workers_ == 0) {
-      for (int64_t i = 0; i < n; ++i) fn(i);
-      return;
-    }
-    {
-      std::lock_guard<std::mutex> lk(mu_);
-      fn_ = &fn;
-      n_ = n;
-      chunk_ = chunk;
-      next_.store(0);
-      active_ = workers_;
-      ++generation_;
-    }
-    cv_.notify_all();
-    work();
-    std::unique_lock<std::mutex> lk(mu_);
-    done_cv_.wait(lk, [&] { return active_ == 0; });
-    fn_ = nullptr;
-  }
-
- private:
-  CompilePool() : pid_(getpid()) {
-    int threads = static_cast<int>(std::min(8u, std::max(1u, std::thread::hardware_concurrency())));
-    if (const char* e = std::getenv("ST_PLAN_THREADS")) threads = std::max(1, std::atoi(e));
-    workers_ = threads - 1;
-    for (int i = 0; i < workers_; ++i) std::thread([this] { loop(); }).detach();
-  }
-  void work() {
-    for (;;) {
-      const int64_t b = next_.fetch_add(chunk_);
-      if (b >= n_) return;
-      const int64_t e = std::min(n_, b + chunk_);
-      for (int64_t i = b; i < e; ++i) (*fn_)(i);
-    }
-  }
-  void loop() {
-    uint64_t seen = 0;
-    for (;;) {
-      {
-        std::unique_lock<std::mutex> lk(mu_);
-        cv_.wait(lk, [&] { return generation_ != seen; });
-        seen = generation_;
-      }
-      work();
-      std::lock_guard<std::mutex> lk(mu_);
-      if (--active_ == 0) done_cv_.notify_one();
-    }
-  }
-  const pid_t pid_;
-  int workers_ = 0;
-  std::mutex job_mu_;  // one job at a time
-  std::mutex mu_;
-  std::condition_variable cv_, done_cv_;
-  uint64_t generation_ = 0;
-  int active_ = 0;
-  const std::function<void(int64_t)>* fn_ = nullptr;
-  int64_t n_ = 0, chunk_ = 1;
-  std::atomic<int64_t> next_{0};
-};
-
 // One query compiled on its own: its term ids are local (first appearance
 // in the query), local_hashes holds their hashes, and the batch ids replace
 // them when the query joins a batch.  A query that fails keeps its error.
@@ -1008,7 +929,7 @@ extern "C" int st_search_plan_create(const int8_t* plans_data,
     std::vector<uint32_t> ids;
     if (parallel) {
       local.resize(static_cast<size_t>(num_queries));
-      CompilePool::get().run(num_queries, 32, [&](int64_t q) {
+      host_pool_run(num_queries, 32, [&](int64_t q) {
         compile_local(plans_data, plans_data_len, plans_offsets, q, hash_k, plan->k_eff,
                       local[static_cast<size_t>(q)]);
       });

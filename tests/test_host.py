@@ -69,6 +69,35 @@ def test_parser_errors_match_reference():
         assert str(ei.value) == msg
 
 
+def test_parser_int64_limits():
+    """Feature ids and values span int64; one past either end is an error that
+    names the token (the reference's std::stoll throws out_of_range there,
+    expression_query_parser.cpp:342-343)."""
+    lo, hi = -(1 << 63), (1 << 63) - 1
+    exprs = [f"{hi}:{lo}", f"{lo}:{hi}", "-0:0"]
+    assert capi.parse_expression_query_batch(exprs, 3, True, 5) == P.parse_batch(exprs, 3, True, 5)
+    for expr, what, tok, pos in [(f"{hi + 1}:1", "feature id", str(hi + 1), 0),
+                                 (f"1:{lo - 1}", "feature value", str(lo - 1), 2),
+                                 (f"2:2 AND 99999999999999999999:1", "feature id", "99999999999999999999", 8)]:
+        with pytest.raises(capi.StError) as ei:
+            capi.parse_expression_query_batch([expr], 7)
+        assert str(ei.value) == f"{what} '{tok}' at position {pos} does not fit a signed 64-bit integer"
+
+
+def test_parser_parallel_batch_matches_oracle():
+    """A batch large enough for the host pool gives the oracle's bytes and the
+    first failing expression's error."""
+    rng = np.random.default_rng(7)
+    exprs = [_random_expr(rng) for _ in range(300)]
+    assert capi.parse_expression_query_batch(exprs, 5, True, 4) == P.parse_batch(exprs, 5, True, 4)
+    bad = list(exprs)
+    bad[200] = "1:1 XOR 2:2"
+    bad[250] = "$"
+    with pytest.raises(capi.StError) as ei:
+        capi.parse_expression_query_batch(bad, 5)
+    assert str(ei.value) == "Unknown keyword 'XOR' at position 4"
+
+
 def _random_expr(rng, depth=0):
     if depth > 2 or rng.random() < 0.35:
         t = f"{int(rng.integers(-3, 20))}:{int(rng.integers(-50, 50))}"
