@@ -9,17 +9,24 @@
 //
 // A chunk is the 32 words (2048 docs) of one bundle; an item is one
 // (query, chunk) pair, and items are numbered query-major.  Three steps:
-//   count    one wave per item: lane l holds the 32-bit half (l & 1) of word
-//            l >> 1 (one coalesced 256-byte row per wave), masks docs at or
-//            past num_docs, popcounts; the wave sum is the item's count.
+//   count    when num_columns is a multiple of 32, item i is bytes
+//            [256 i, 256 i + 256) of the mask: each lane loads 16 bytes, a
+//            row of 16 lanes holds one item and DPP row shifts sum its
+//            popcounts (one load instruction covers four items); otherwise
+//            one wave per item, lane l holding the 32-bit half (l & 1) of
+//            word l >> 1.  Docs at or past num_docs are masked out.
 //   scan     one flat exclusive scan over the counts in item order: since the
 //            ids are laid out query by query and, within a query, chunk by
 //            chunk, the scanned value of an item is its first output slot.
 //            row_offsets[q] is the value of item (q, 0); row_offsets[Q] is
 //            the total.
-//   write    one wave per item again: an exclusive wave prefix of the lane
-//            popcounts places each lane's ids (lane order is doc order), and
-//            every lane writes its set bits from the most significant down.
+//   write    one wave per item, lane l again holding half (l & 1) of word
+//            l >> 1 (lane order is doc order): a DPP prefix of the lane
+//            popcounts places each lane's ids, which the lane stages in LDS as
+//            16-bit offsets within the chunk (lowest bit of the bit-reversed
+//            half first); the wave then writes the item's run with 16-byte
+//            stores.  A wave takes kWriteItems consecutive items at a time
+//            and loads the next such group before it stages the current one.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -35,9 +42,14 @@ namespace {
 
 constexpr int kCompactThreads = 256;            // 4 waves per workgroup
 constexpr int kCompactWaves = kCompactThreads / 64;
-constexpr int kCountItems = 8;   // row loads in flight per wave, count pass
-constexpr int kWriteItems = 8;   // and write pass (register bound)
+constexpr int kCountItems = 8;   // row loads in flight per wave, count pass by rows
+constexpr int kCountLines = 4;   // 1 KB loads (4 items each) in flight, count pass by lines
+constexpr int kWriteItems = 4;   // items per group of the write pass
 constexpr int kChunkWords = kColumnsPerBundle;  // 32 words = 2048 docs
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4_u __attribute__((ext_vector_type(4), aligned(4)));
+typedef int64_t i64x2_u __attribute__((ext_vector_type(2), aligned(8)));
 
 constexpr int kScanThreads = 1024;
 constexpr int kScanPerThread = 8;
@@ -89,6 +101,49 @@ __global__ __launch_bounds__(kCompactThreads) void compact_count_kernel(
     for (int u = 0; u < kCountItems; ++u) {
       const uint32_t c = wave_total_small(static_cast<uint32_t>(__builtin_popcount(bits[u])));
       if (lane == 0 && first + u < n_items) counts[first + u] = c;
+    }
+  }
+}
+
+// Count pass over contiguous items (num_columns a multiple of 32).  Lane l
+// of a wave loads bytes [16 l, 16 l + 16) of a 1 KB line of four items: row
+// r = l >> 4 of the wave holds item 4 g + r, lane l & 15 its docs
+// 128 (l & 15) .. + 127 (u32 y: docs 0-31, x: 32-63, w: 64-95, z: 96-127).
+__global__ __launch_bounds__(kCompactThreads) void compact_count_lines_kernel(
+    const u32x4* __restrict__ packed16, int64_t nch, int64_t num_docs, int64_t n_items,
+    int64_t* __restrict__ counts) {
+  const int lane = threadIdx.x & 63;
+  const int row = lane >> 4, rl = lane & 15;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kCompactWaves + (threadIdx.x >> 6);
+  const int64_t lines = (n_items + 3) / 4;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCompactWaves * kCountLines;
+  for (int64_t g0 = wave * kCountLines; g0 < lines; g0 += stride) {
+    u32x4 v[kCountLines];
+#pragma unroll
+    for (int u = 0; u < kCountLines; ++u) {
+      const int64_t item = 4 * (g0 + u) + row;
+      v[u] = item < n_items ? __builtin_nontemporal_load(packed16 + 64 * (g0 + u) + lane)
+                            : u32x4{0u, 0u, 0u, 0u};
+    }
+    int64_t item = 4 * g0 + row;
+    int64_t ch = item % nch;
+#pragma unroll
+    for (int u = 0; u < kCountLines; ++u) {
+      u32x4 w = v[u];
+      const int64_t first_doc = ch * kDocsPerBundle + 128 * rl;
+      if (first_doc + 128 > num_docs) {
+        w.y &= valid_doc_mask(first_doc, num_docs);
+        w.x &= valid_doc_mask(first_doc + 32, num_docs);
+        w.w &= valid_doc_mask(first_doc + 64, num_docs);
+        w.z &= valid_doc_mask(first_doc + 96, num_docs);
+      }
+      const uint32_t c = row16_inclusive_sum(
+          static_cast<uint32_t>(__builtin_popcount(w.x) + __builtin_popcount(w.y) +
+                                __builtin_popcount(w.z) + __builtin_popcount(w.w)));
+      if (rl == 15 && item < n_items) counts[item] = c;
+      item += 4;
+      ch += 4;
+      while (ch >= nch) ch -= nch;
     }
   }
 }
@@ -197,55 +252,117 @@ __global__ void zero_offsets_kernel(int64_t* __restrict__ row_offsets, int64_t n
   if (i < n) row_offsets[i] = 0;
 }
 
-// Each wave stages an item's ids in LDS as 16-bit offsets within the chunk
-// (lane order is doc order, so the wave prefix of lane popcounts places
-// them), then copies the run out with coalesced stores.
+// The lane's 32 doc bits of item (q, ch) as loaded (not yet masked at
+// num_docs); 0 for columns past the row's end, which only the last chunk
+// of a row has when num_columns is not a multiple of 32.
+__device__ __forceinline__ uint32_t load_lane_half(const uint32_t* __restrict__ packed32,
+                                                   int64_t num_columns, int64_t q, int64_t ch,
+                                                   int lane) {
+  const int64_t w0 = ch * kChunkWords;
+  if ((lane >> 1) >= num_columns - w0) return 0u;
+  return __builtin_nontemporal_load(packed32 + 2 * (q * num_columns + w0) + (lane ^ 1));
+}
+
+// Writes the item's staged run my[0 .. total) as ids doc0 + my[i] to
+// dst[0 .. total), 16 bytes per lane and store; the run's last partial unit
+// is written id by id (the ids after it belong to the next item).
+__device__ __forceinline__ void write_run(const uint16_t* my, uint32_t total, int lane,
+                                          int64_t doc0, int32_t* dst) {
+  const int32_t d0 = static_cast<int32_t>(doc0);  // ids fit int32 (checked by the host)
+  for (uint32_t i = 4u * lane; i < total; i += 256u) {
+    const uint2 pr = *reinterpret_cast<const uint2*>(my + i);
+    const int32_t a = d0 + static_cast<int32_t>(pr.x & 0xFFFFu);
+    const int32_t b = d0 + static_cast<int32_t>(pr.x >> 16);
+    const int32_t c = d0 + static_cast<int32_t>(pr.y & 0xFFFFu);
+    const int32_t d = d0 + static_cast<int32_t>(pr.y >> 16);
+    if (i + 4u <= total) {
+      *reinterpret_cast<i32x4_u*>(dst + i) = i32x4_u{a, b, c, d};
+    } else {
+      dst[i] = a;
+      if (i + 1u < total) dst[i + 1] = b;
+      if (i + 2u < total) dst[i + 2] = c;
+    }
+  }
+}
+
+__device__ __forceinline__ void write_run(const uint16_t* my, uint32_t total, int lane,
+                                          int64_t doc0, int64_t* dst) {
+  for (uint32_t i = 2u * lane; i < total; i += 128u) {
+    const uint32_t pr = *reinterpret_cast<const uint32_t*>(my + i);
+    const int64_t a = doc0 + static_cast<int64_t>(pr & 0xFFFFu);
+    const int64_t b = doc0 + static_cast<int64_t>(pr >> 16);
+    if (i + 2u <= total) {
+      *reinterpret_cast<i64x2_u*>(dst + i) = i64x2_u{a, b};
+    } else {
+      dst[i] = a;
+    }
+  }
+}
+
 template <typename Id>
 __global__ __launch_bounds__(kCompactThreads) void compact_write_kernel(
     const uint32_t* __restrict__ packed32, int64_t num_columns, int64_t nch,
     int64_t num_docs, int64_t n_items, const int64_t* __restrict__ item_base,
     Id* __restrict__ ids) {
-  __shared__ uint16_t stage[kCompactWaves][kDocsPerBundle];
+  __shared__ __align__(16) uint16_t stage[kCompactWaves][kDocsPerBundle];
   const int lane = threadIdx.x & 63;
-  uint16_t* my = stage[threadIdx.x >> 6];
-  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kCompactWaves + (threadIdx.x >> 6);
+  const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  uint16_t* my = stage[wv];
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kCompactWaves + wv;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kCompactWaves * kWriteItems;
-  for (int64_t first = wave * kWriteItems; first < n_items; first += stride) {
-    uint32_t bits[kWriteItems];
-    int64_t pos[kWriteItems];
-    ItemCursor it(first, nch);
-    const int64_t ch0 = it.ch;
+  const int64_t step_q = stride / nch, step_ch = stride - step_q * nch;
+  const uint32_t lane_doc = static_cast<uint32_t>(lane) * 32u;
+  int64_t first = wave * kWriteItems;
+  if (first >= n_items) return;
+  ItemCursor at(first, nch);  // first item of the current group
+  uint32_t next_bits[kWriteItems];
+  int64_t next_pos[kWriteItems];
+  const auto load_group = [&](int64_t f, ItemCursor it) {
 #pragma unroll
     for (int u = 0; u < kWriteItems; ++u) {
-      const bool valid = first + u < n_items;
-      bits[u] = valid ? lane_bits(packed32, num_columns, num_docs, it.q, it.ch, lane) : 0u;
-      pos[u] = valid ? item_base[first + u] : 0;
+      const bool valid = f + u < n_items;
+      next_bits[u] = valid ? load_lane_half(packed32, num_columns, it.q, it.ch, lane) : 0u;
+      next_pos[u] = valid ? item_base[f + u] : 0;
       it.next(nch);
     }
-    int64_t ch = ch0;
+  };
+  load_group(first, at);
+  for (; first < n_items; first += stride) {
+    uint32_t bits[kWriteItems];
+    int64_t pos[kWriteItems];
+#pragma unroll
+    for (int u = 0; u < kWriteItems; ++u) {
+      bits[u] = next_bits[u];
+      pos[u] = next_pos[u];
+    }
+    ItemCursor it = at;
+    at.q += step_q;
+    at.ch += step_ch;
+    if (at.ch >= nch) {
+      at.ch -= nch;
+      ++at.q;
+    }
+    if (first + stride < n_items) load_group(first + stride, at);
 #pragma unroll
     for (int u = 0; u < kWriteItems; ++u) {
       if (first + u >= n_items) break;  // wave-uniform
+      const int64_t doc0 = it.ch * kDocsPerBundle;
       uint32_t b = bits[u];
-      const WaveScan ws = wave_scan_small(static_cast<uint32_t>(__builtin_popcount(b)));
-      const uint32_t total = ws.total;
-      uint32_t slot = ws.excl;
-      const uint32_t lane_doc = static_cast<uint32_t>(lane) * 32u;
-      while (b != 0u) {
-        const int lz = __builtin_clz(b);
-        my[slot++] = static_cast<uint16_t>(lane_doc + lz);
-        b &= ~(0x80000000u >> lz);
-      }
+      if (doc0 + kDocsPerBundle > num_docs) b &= valid_doc_mask(doc0 + lane_doc, num_docs);
+      const uint32_t pc = static_cast<uint32_t>(__builtin_popcount(b));
+      uint32_t total;
+      const uint32_t incl = wave_inclusive_sum(pc, &total);
+      uint16_t* sp = my + (incl - pc);
+      for (uint32_t r = __builtin_bitreverse32(b); r != 0u; r &= r - 1u)
+        *sp++ = static_cast<uint16_t>(lane_doc + static_cast<uint32_t>(__builtin_ctz(r)));
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const int64_t doc0 = ch * kDocsPerBundle;
-      Id* dst = ids + pos[u];
-      for (uint32_t i = lane; i < total; i += 64) dst[i] = static_cast<Id>(doc0 + my[i]);
+      write_run(my, total, lane, doc0, ids + pos[u]);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if (++ch == nch) ch = 0;
+      it.next(nch);
     }
   }
 }
@@ -334,11 +451,19 @@ extern "C" int st_bloom_compact_offsets(const int64_t* packed, int64_t num_queri
     ST_CHECK(packed != nullptr && workspace != nullptr, "null device pointer");
     int64_t* counts = static_cast<int64_t*>(workspace);
     const uint32_t* p32 = reinterpret_cast<const uint32_t*>(packed);
-    hipLaunchKernelGGL(compact_count_kernel,
-                       dim3(compact_grid(compact_count_kernel, items, kCountItems)),
-                       dim3(kCompactThreads), 0, s, p32, num_columns, nch, num_docs, items,
-                       counts);
-    check_launch("compact_count_kernel");
+    if (num_columns % kChunkWords == 0 && reinterpret_cast<uintptr_t>(packed) % 16 == 0) {
+      hipLaunchKernelGGL(compact_count_lines_kernel,
+                         dim3(compact_grid(compact_count_lines_kernel, (items + 3) / 4, kCountLines)),
+                         dim3(kCompactThreads), 0, s, reinterpret_cast<const u32x4*>(packed), nch,
+                         num_docs, items, counts);
+      check_launch("compact_count_lines_kernel");
+    } else {
+      hipLaunchKernelGGL(compact_count_kernel,
+                         dim3(compact_grid(compact_count_kernel, items, kCountItems)),
+                         dim3(kCompactThreads), 0, s, p32, num_columns, nch, num_docs, items,
+                         counts);
+      check_launch("compact_count_kernel");
+    }
     compact_scan_counts(counts, num_queries, nch, row_offsets, s);
   });
 }

@@ -10,7 +10,10 @@ tests/golden/make_golden.py full):
   queries): input digests (the generator itself), bundle_b_offsets,
   bloom_index, plan bytes, the packed search output, per-query match counts;
   the bool output equals the packed words bit for bit; the CSR row offsets of
-  the ids op are the running sums of the reference's match counts;
+  the ids op are the running sums of the reference's match counts, and its
+  ids, strictly ascending per row, each on a set bit of the reference-equal
+  packed output, are therefore exactly the set bits (also through
+  bloom_mask_to_ids on the packed output);
 * cfg4 (100M docs, build only): input digests, bundle_b_offsets and the
   5.9 GB bloom_index;
 * cfg5's fused search + filtered top-k on a doc prefix of its corpus, its
@@ -135,7 +138,31 @@ def test_full_size_build_and_search_vs_reference(cfg):
     want_ro = np.concatenate([[0], np.cumsum(d["match_counts"])])
     np.testing.assert_array_equal(ro.cpu().numpy(), want_ro)
     assert ids_out.numel() == want_ro[-1]
-    H.note(f"[full] {cfg}: bool output and CSR row offsets agree ({time.time() - t0:.0f}s)")
+    _check_ids_against_mask(ids_out, ro, packed, cspec.num_docs)
+    ids_m, ro_m = st.bloom_mask_to_ids(packed, cspec.num_docs)
+    assert torch.equal(ro_m, ro) and torch.equal(ids_m, ids_out), "mask -> ids differs from the fused ids op"
+    H.note(f"[full] {cfg}: bool output, CSR row offsets and every id agree ({time.time() - t0:.0f}s)")
+
+
+def _check_ids_against_mask(ids, ro, packed, num_docs):
+    """Pins CSR ids exactly, given row offsets equal to the reference's match
+    counts: within each row the ids ascend strictly, lie below num_docs and
+    name set bits of the packed output (doc d of a row at bit 63 - d % 64 of
+    word d // 64), so the row's ids are all of its set bits."""
+    n = ids.numel()
+    if n == 0:
+        return
+    counts = ro[1:] - ro[:-1]
+    rows = torch.repeat_interleave(torch.arange(counts.numel(), device=ids.device), counts)
+    d = ids.long()
+    assert int(d.min()) >= 0 and int(d.max()) < num_docs, "an id outside [0, num_docs)"
+    words = packed[rows, d // 64]
+    del rows
+    assert bool(((words >> (63 - d % 64)) & 1).bool().all()), "an id names a clear bit"
+    del words
+    starts = torch.zeros(n, dtype=torch.bool, device=ids.device)
+    starts[ro[:-1][counts > 0]] = True
+    assert bool(((d[1:] > d[:-1]) | starts[1:]).all()), "ids of a row not strictly ascending"
 
 
 @pytest.mark.timeout(900)
