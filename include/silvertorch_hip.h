@@ -370,7 +370,8 @@ int st_filtered_topk(const int64_t* packed, int64_t num_queries,
  * int32 doc ids.  1 <= dim <= 1280.  A cluster id outside
  * [0, num_offsets) or a negative length selects nothing.  workspace: device
  * memory of st_fused_kmean_ann_workspace_bytes(batch, probes) bytes (the
- * per-(row, probe) counts of passing docs).
+ * per-(row, probe) counts of passing docs, then the per-row totals and group
+ * starts that calls of 2,048 pairs or more use to spread the scoring).
  * ------------------------------------------------------------------------- */
 int64_t st_fused_kmean_ann_workspace_bytes(int64_t batch, int64_t probes);
 int st_kmean_ann_score_dtype(int emb_dtype, int64_t divisor_for_int8,

@@ -15,15 +15,17 @@
 // the score dtype, so every float score equals the reference CPU op's bit
 // for bit; int8 dot products are exact int32 sums.
 //
-// Two launches: kmean_count_kernel counts the passing docs of every (row,
-// probe); kmean_ann_kernel, one 512-thread workgroup per (row, probe),
-// starts at the row's count of the earlier probes, stages the query in LDS
-// as float64, takes its cluster's docs 4,096 at a time (8 per thread as
-// pass bits: the filter words shifted to the docs), lists the passing ones
-// in LDS in doc order (workgroup scan) and scores them, one doc per lane,
-// the rows staged through LDS with whole-line loads, into the next output
-// slots.  A heavy row is spread over its probes' workgroups.  Memory-bound
-// on the embedding rows read.
+// kmean_count_kernel counts the passing docs of every (row, probe).  Calls
+// of fewer than 2,048 pairs then run kmean_ann_kernel, one 512-thread
+// workgroup per (row, probe): it starts at the row's count of the earlier
+// probes, stages the query in LDS as float64, takes its cluster's docs 4,096
+// at a time (8 per thread as pass bits: the filter words shifted to the
+// docs), lists the passing ones in LDS in doc order (workgroup scan) and
+// scores them, one doc per lane, the rows staged through LDS with whole-line
+// loads, into the next output slots.  Larger calls take the balanced form
+// (ids listed per pair first, then the scoring spread over the chip by
+// groups of 64 slots; see kmean_groups_kernel).  Memory-bound on the
+// embedding rows read.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -33,8 +35,10 @@
 
 #include "st_common.hpp"
 #include "st_errors.hpp"
+#include "wave_ops.hpp"
 
 namespace st {
+int cu_count();
 namespace {
 
 constexpr int kKmThreads = 512;
@@ -489,6 +493,314 @@ __global__ __launch_bounds__(kKmThreads) __attribute__((amdgpu_waves_per_eu(4)))
   }
 }
 
+// ------------------------------------------------ balanced form (many pairs)
+//
+// Calls with at least kKmBalancedPairs (row, probe) pairs are split so that
+// the scoring work, not the pairs, is spread evenly: the passing docs per
+// query vary by orders of magnitude (a search filter passes 0-54% of a
+// cluster), and a workgroup or a wave per pair leaves the chip waiting on
+// the heaviest pairs.
+//   kmean_count_kernel   passing docs per (row, probe), as above;
+//   kmean_groups_kernel  one workgroup: per row its total, its filled slots
+//                        n_b = min(total, width) and its groups of 64 slots,
+//                        with the exclusive prefix of the groups over rows;
+//   kmean_list_kernel    one wave per (row, probe): lists the passing docs
+//                        (chunks of 1,024 docs, 16 per lane, offsets in LDS)
+//                        and writes their ids into the row's slots; the
+//                        row's padding is split over its probes' waves;
+//   kmean_score_kernel   a fixed grid of waves; wave w takes the groups
+//                        [G w / W, G (w + 1) / W) of the G in the call, reads
+//                        each group's 64 ids from the output and scores the
+//                        docs with the staged 64-byte slices of
+//                        kmean_ann_kernel, the loads of the next steps (and
+//                        the next group's ids) in flight while a slice is
+//                        summed.
+constexpr int kKmWaveThreads = 256;  // 4 waves per workgroup
+constexpr int kKmWaveDocsPerLane = 16;
+constexpr int kKmWaveChunk = 64 * kKmWaveDocsPerLane;
+constexpr int kKmWaveStage = 64 * kKmStageStride;
+constexpr int kKmRing = 4;  // groups whose ids and place are held per wave
+constexpr int kKmRingBytes = kKmRing * (64 * 4 + 32);  // ids, then a KmGroup (24 bytes) each
+constexpr int64_t kKmBalancedPairs = 2048;
+constexpr int64_t kKmBalancedMaxRows = 16384;  // rows the single-workgroup prefix takes
+constexpr int kKmWaveMaxLds = 65536;           // dynamic LDS of a score workgroup
+constexpr int kKmGroupsThreads = 1024;
+
+__host__ __device__ constexpr int km_query_bytes(int dim, bool i8) {
+  return ((i8 ? dim : 8 * dim) + 15) / 16 * 16;
+}
+__host__ __device__ constexpr int km_score_wave_lds(int dim, bool i8) {
+  return km_query_bytes(dim, i8) + kKmWaveStage + kKmRingBytes;
+}
+
+// Workspace of the balanced form after the batch x probes counts, int64:
+// row totals [batch], group starts [batch + 1].
+__host__ __device__ constexpr int64_t km_balanced_extra(int64_t batch) { return 2 * batch + 1; }
+
+__global__ __launch_bounds__(kKmGroupsThreads) void kmean_groups_kernel(
+    const int64_t* __restrict__ counts, int64_t batch, int64_t probes, int64_t width,
+    int64_t* __restrict__ rowtot, int64_t* __restrict__ gstart) {
+  __shared__ int64_t wave_tot[kKmGroupsThreads / 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int64_t carry = 0;
+  for (int64_t b0 = 0; b0 < batch; b0 += kKmGroupsThreads) {
+    const int64_t b = b0 + threadIdx.x;
+    int64_t groups = 0;
+    if (b < batch) {
+      int64_t total = 0;
+      for (int64_t p = 0; p < probes; ++p) total += counts[b * probes + p];
+      rowtot[b] = total;
+      groups = (min(total, width) + 63) / 64;
+    }
+    int64_t x = groups;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int64_t y = __shfl_up(x, off, 64);
+      if (lane >= off) x += y;
+    }
+    if (lane == 63) wave_tot[wave] = x;
+    __syncthreads();
+    int64_t before = 0, sum = 0;
+#pragma unroll
+    for (int j = 0; j < kKmGroupsThreads / 64; ++j) {
+      const int64_t t = wave_tot[j];
+      before += j < wave ? t : 0;
+      sum += t;
+    }
+    __syncthreads();
+    if (b < batch) gstart[b] = carry + before + x - groups;
+    carry += sum;
+  }
+  if (threadIdx.x == 0) gstart[batch] = carry;
+}
+
+template <int ST>
+__device__ __forceinline__ void km_pad(const KmArgs& a, int64_t at) {
+  if constexpr (ST == kKmF32) static_cast<float*>(a.scores)[at] = -3.402823466e38f;
+  if constexpr (ST == kKmF16) static_cast<uint16_t*>(a.scores)[at] = 0xFBFFu;
+  if constexpr (ST == kKmBF16) static_cast<uint16_t*>(a.scores)[at] = 0xFF7Fu;
+  if constexpr (ST == kKmI32) static_cast<int32_t*>(a.scores)[at] = INT32_MIN;
+  a.indices[at] = static_cast<int32_t>(a.invalid_index);
+}
+
+template <int ST>
+__global__ __launch_bounds__(kKmWaveThreads) void kmean_list_kernel(KmArgs a, const int64_t* counts,
+                                                                    const int64_t* rowtot,
+                                                                    int64_t pairs) {
+  __shared__ uint16_t lists[kKmWaveThreads / 64][kKmWaveChunk];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int64_t pair = static_cast<int64_t>(blockIdx.x) * (kKmWaveThreads / 64) + wv;
+  if (pair >= pairs) return;
+  uint16_t* list = lists[wv];
+  const int64_t b = pair / a.probes, p = pair % a.probes;
+  const int64_t out0 = b * a.max_per_row;
+  int64_t written = 0;  // the row's passing docs before this probe
+  for (int64_t q = lane; q < p; q += 64) written += counts[b * a.probes + q];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) written += __shfl_xor(written, off, 64);
+  KmProbe pr = km_probe(a, b, p);
+  bool none;
+  const int64_t* mask = km_mask_row(a, b, none);
+  if (none) pr.len = 0;
+  for (int64_t base = 0; base < pr.len && written < a.max_per_row; base += kKmWaveChunk) {
+    const int64_t i0 = base + static_cast<int64_t>(lane) * kKmWaveDocsPerLane;
+    const int n = static_cast<int>(min<int64_t>(max<int64_t>(pr.len - i0, 0), kKmWaveDocsPerLane));
+    uint64_t bits = pass_bits(mask, a.filter_cols, pr.start + i0, n, a.total_docs);
+    const uint32_t cnt = static_cast<uint32_t>(__popcll(bits));
+    uint32_t total;
+    uint32_t at = wave_inclusive_sum(cnt, &total) - cnt;
+    while (bits != 0) {  // this lane's passing docs, in order
+      const int j = __clzll(bits);
+      list[at++] = static_cast<uint16_t>(lane * kKmWaveDocsPerLane + j);
+      bits &= ~(0x8000000000000000ull >> j);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int64_t m = min<int64_t>(total, a.max_per_row - written);
+    for (int64_t i = lane; i < m; i += 64)
+      a.indices[out0 + written + i] = static_cast<int32_t>(pr.start + base + list[i]);
+    written += total;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();  // the list is refilled by the next chunk
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  // padding: slots [min(total, width), width) of the row, split over its probes
+  const int64_t lo = min(rowtot[b], a.max_per_row);
+  const int64_t share = (a.max_per_row - lo + a.probes - 1) / a.probes;
+  const int64_t s0 = lo + p * share, s1 = min(a.max_per_row, s0 + share);
+  for (int64_t s = s0 + lane; s < s1; s += 64) km_pad<ST>(a, out0 + s);
+}
+
+// Place of a group of 64 slots: row, first slot, filled slots in it.
+struct KmGroup {
+  int64_t b, s0;
+  int32_t n, pad;
+};
+static_assert(sizeof(KmGroup) <= 32, "a ring entry holds 32 bytes");
+
+template <int DT, int ST>
+__global__ __launch_bounds__(kKmWaveThreads) __attribute__((amdgpu_waves_per_eu(4))) void kmean_score_kernel(
+    KmArgs a, const int64_t* __restrict__ gstart, const int64_t* __restrict__ rowtot, int64_t batch) {
+  extern __shared__ __align__(16) char km_lds[];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int64_t nw = static_cast<int64_t>(gridDim.x) * (kKmWaveThreads / 64);
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * (kKmWaveThreads / 64) + wv;
+  const int64_t G = gstart[batch];
+  const int64_t g_lo = G * w / nw, g_hi = G * (w + 1) / nw;
+  if (g_lo >= g_hi) return;
+  const int dim = a.dim;
+  char* mine = km_lds + wv * km_score_wave_lds(dim, DT == kKmI8);
+  double* qd = reinterpret_cast<double*>(mine);
+  int8_t* qi = reinterpret_cast<int8_t*>(mine);
+  char* stg = mine + km_query_bytes(dim, DT == kKmI8);
+  int32_t* ring_ids = reinterpret_cast<int32_t*>(stg + kKmWaveStage);  // [kKmRing][64]
+  KmGroup* ring = reinterpret_cast<KmGroup*>(ring_ids + kKmRing * 64);
+
+  // row cursor of the next group to be placed: the largest row b with
+  // gstart[b] <= g (rows without groups have gstart[b] == gstart[b + 1])
+  int64_t cb = 0, hi = batch;
+  while (hi - cb > 1) {
+    const int64_t mid = (cb + hi) / 2;
+    if (gstart[mid] <= g_lo) cb = mid; else hi = mid;
+  }
+  int64_t c_start = gstart[cb], c_next = gstart[cb + 1];
+  int64_t c_fill = min(rowtot[cb], a.max_per_row);
+  auto place = [&](int64_t g) -> KmGroup {
+    while (g >= c_next) {
+      ++cb;
+      c_start = c_next;
+      c_next = gstart[cb + 1];
+      c_fill = -1;
+    }
+    if (c_fill < 0) c_fill = min(rowtot[cb], a.max_per_row);
+    const int64_t s0 = (g - c_start) * 64;
+    return KmGroup{cb, s0, static_cast<int32_t>(min<int64_t>(64, c_fill - s0)), 0};
+  };
+  // the next group's ids travel in a register, loaded one group ahead
+  KmGroup nxt = place(g_lo);
+  int32_t nid = lane < nxt.n ? a.indices[nxt.b * a.max_per_row + nxt.s0 + lane] : 0;
+  // group g enters: its ids and place go to the ring, group g + 1's ids are loaded
+  KmGroup lg{};  // the group whose rows are being loaded
+  auto enter = [&](int64_t g) {
+    lg = nxt;
+    ring_ids[(g & (kKmRing - 1)) * 64 + lane] = nid;
+    if (lane == 0) ring[g & (kKmRing - 1)] = lg;
+    if (g + 1 < g_hi) {
+      nxt = place(g + 1);
+      nid = lane < nxt.n ? a.indices[nxt.b * a.max_per_row + nxt.s0 + lane] : 0;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  int64_t qrow = -1;  // row whose query is staged
+  auto stage_query = [&](int64_t b) {
+    if constexpr (DT == kKmI8) {
+      const int8_t* q = static_cast<const int8_t*>(a.queries) + b * dim;
+      for (int d = lane; d < dim; d += 64) qi[d] = q[d];
+    } else {
+      const size_t es = DT == kKmF32 ? 4 : 2;
+      const char* q = static_cast<const char*>(a.queries) + static_cast<size_t>(b) * dim * es;
+      for (int d = lane; d < dim; d += 64) qd[d] = static_cast<double>(elem_f<DT>(q, d));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    qrow = b;
+  };
+  const size_t row_bytes = static_cast<size_t>(dim) * (DT == kKmF32 ? 4 : (DT == kKmI8 ? 1 : 2));
+  const char* emb = static_cast<const char*>(a.embeddings);
+  auto finish = [&](const KmGroup& gr, int32_t doc, double f64, int32_t i32) {
+    float f32h = 0.f;
+    if constexpr (DT == kKmI8) {
+      if (a.scale != nullptr)
+        f32h = static_cast<float>(i32) / half_to_float(a.scale[doc]);
+      else if (a.divisor != -1)
+        f32h = static_cast<float>(i32) / static_cast<float>(a.divisor);
+    }
+    put_score<DT, ST>(a.scores, gr.b * a.max_per_row + gr.s0 + lane, f64, i32, f32h);
+  };
+  const bool staged = (reinterpret_cast<uintptr_t>(emb) & 15u) == 0 && row_bytes % 16 == 0;
+  if (!staged) {
+    for (int64_t g = g_lo; g < g_hi; ++g) {
+      enter(g);
+      if (lg.b != qrow) stage_query(lg.b);
+      if (lane < lg.n) {
+        const int32_t doc = ring_ids[(g & (kKmRing - 1)) * 64 + lane];
+        const char* row = emb + static_cast<size_t>(doc) * row_bytes;
+        if constexpr (DT == kKmI8)
+          finish(lg, doc, 0.0, dot_i8(reinterpret_cast<const int8_t*>(row), qi, dim));
+        else
+          finish(lg, doc, dot_f64<DT>(row, qd, dim), 0);
+      }
+    }
+    return;
+  }
+  // step t = (group g_lo + t / nslices, 64-byte slice t % nslices)
+  const int pieces = static_cast<int>(row_bytes / 16);
+  const int per_slice = kKmSliceBytes / 16;
+  const int nslices = (pieces + per_slice - 1) / per_slice;
+  const int elems = DT == kKmF32 ? 4 : (DT == kKmI8 ? 16 : 8);  // per piece
+  const int64_t steps = (g_hi - g_lo) * nslices;
+  const int lr = lane >> 2, lp = lane & 3;  // load: row lr + 16 i, piece lp of the slice
+  auto load = [&](int64_t t, uint4 (&buf)[4]) {
+    const int64_t g = g_lo + t / nslices;
+    const int sl = static_cast<int>(t % nslices);
+    if (sl == 0) enter(g);
+    const int pc = sl * per_slice + lp;
+    const int32_t* ids = ring_ids + (g & (kKmRing - 1)) * 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int li = lr + 16 * i;
+      buf[i] = li < lg.n && pc < pieces
+                   ? *reinterpret_cast<const uint4*>(emb + static_cast<size_t>(ids[li]) * row_bytes +
+                                                     static_cast<size_t>(pc) * 16)
+                   : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  double acc = 0.0;
+  int32_t iacc = 0;
+  uint4 buf[kKmAhead][4];
+#pragma unroll
+  for (int j = 0; j < kKmAhead; ++j)
+    if (j < steps) load(j, buf[j]);
+  for (int64_t t0 = 0; t0 < steps; t0 += kKmAhead) {
+#pragma unroll
+    for (int j = 0; j < kKmAhead; ++j) {
+      const int64_t t = t0 + j;
+      if (t >= steps) break;
+      const int64_t g = g_lo + t / nslices;
+      const int sl = static_cast<int>(t % nslices);
+      const KmGroup gr = ring[g & (kKmRing - 1)];
+      if (sl == 0 && gr.b != qrow) stage_query(gr.b);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<uint4*>(stg + (lr + 16 * i) * kKmStageStride + lp * 16) = buf[j][i];
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      if (t + kKmAhead < steps) load(t + kKmAhead, buf[j]);
+      if (lane < gr.n) {
+#pragma unroll
+        for (int q = 0; q < per_slice; ++q) {
+          const int pc = sl * per_slice + q;
+          if (pc < pieces) {
+            const uint4 v = *reinterpret_cast<const uint4*>(stg + lane * kKmStageStride + q * 16);
+            acc_piece<DT>(v, qd, qi, pc * elems, acc, iacc);
+          }
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      if (sl == nslices - 1) {
+        if (lane < gr.n) finish(gr, ring_ids[(g & (kKmRing - 1)) * 64 + lane], acc, iacc);
+        acc = 0.0;
+        iacc = 0;
+      }
+    }
+  }
+}
+
 }  // namespace
 }  // namespace st
 
@@ -500,7 +812,10 @@ extern "C" int st_kmean_ann_score_dtype(int emb_dtype, int64_t divisor_for_int8,
 }
 
 extern "C" int64_t st_fused_kmean_ann_workspace_bytes(int64_t batch, int64_t probes) {
-  return batch > 0 && probes > 0 ? batch * probes * static_cast<int64_t>(sizeof(int64_t)) : 0;
+  using namespace st;
+  return batch > 0 && probes > 0
+             ? (batch * probes + km_balanced_extra(batch)) * static_cast<int64_t>(sizeof(int64_t))
+             : 0;
 }
 
 namespace st {
@@ -561,6 +876,39 @@ void kmean_run(const int64_t* cluster_offsets, int64_t num_offsets, const int64_
     const int64_t items = batch * probes, per = kKmCountThreads / 64;
     hipLaunchKernelGGL(kmean_count_kernel, dim3(static_cast<unsigned>((items + per - 1) / per)),
                        dim3(kKmCountThreads), 0, s, a, counts, items);
+  }
+  const int64_t pairs = batch * probes;
+  const int score_lds = (kKmWaveThreads / 64) * km_score_wave_lds(static_cast<int>(dim), emb_dtype == kKmI8);
+  if (probes > 0 && pairs >= kKmBalancedPairs && batch <= kKmBalancedMaxRows &&
+      score_lds <= kKmWaveMaxLds &&
+      (counts_capacity < 0 || pairs + km_balanced_extra(batch) <= counts_capacity)) {
+    int64_t* rowtot = counts + pairs;
+    int64_t* gstart = rowtot + batch;
+    hipLaunchKernelGGL(kmean_groups_kernel, dim3(1), dim3(kKmGroupsThreads), 0, s, counts, batch,
+                       probes, max_per_row, rowtot, gstart);
+    const dim3 lgrid(static_cast<unsigned>((pairs + 3) / 4)), wblock(kKmWaveThreads);
+    switch (st) {
+      case kKmF32: hipLaunchKernelGGL(kmean_list_kernel<kKmF32>, lgrid, wblock, 0, s, a, counts, rowtot, pairs); break;
+      case kKmF16: hipLaunchKernelGGL(kmean_list_kernel<kKmF16>, lgrid, wblock, 0, s, a, counts, rowtot, pairs); break;
+      case kKmBF16: hipLaunchKernelGGL(kmean_list_kernel<kKmBF16>, lgrid, wblock, 0, s, a, counts, rowtot, pairs); break;
+      default: hipLaunchKernelGGL(kmean_list_kernel<kKmI32>, lgrid, wblock, 0, s, a, counts, rowtot, pairs);
+    }
+    // a fixed grid: 16 waves per CU, every one resident
+    const dim3 sgrid(static_cast<unsigned>(4 * cu_count()));
+    switch (emb_dtype) {
+      case kKmF32: hipLaunchKernelGGL((kmean_score_kernel<kKmF32, kKmF32>), sgrid, wblock, score_lds, s, a, gstart, rowtot, batch); break;
+      case kKmF16: hipLaunchKernelGGL((kmean_score_kernel<kKmF16, kKmF16>), sgrid, wblock, score_lds, s, a, gstart, rowtot, batch); break;
+      case kKmBF16: hipLaunchKernelGGL((kmean_score_kernel<kKmBF16, kKmBF16>), sgrid, wblock, score_lds, s, a, gstart, rowtot, batch); break;
+      default:
+        if (st == kKmI32)
+          hipLaunchKernelGGL((kmean_score_kernel<kKmI8, kKmI32>), sgrid, wblock, score_lds, s, a, gstart, rowtot, batch);
+        else
+          hipLaunchKernelGGL((kmean_score_kernel<kKmI8, kKmF16>), sgrid, wblock, score_lds, s, a, gstart, rowtot, batch);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+      throw Error(ST_ERR_HIP, cat("fused_kmean_ann launch failed: ", hipGetErrorString(e)));
+    return;
   }
   const dim3 grid(static_cast<unsigned>(groups)), block(kKmThreads);
   switch (emb_dtype) {

@@ -137,6 +137,76 @@ def test_random_vs_oracle(dim, dtype, filtered, divisor, maxlen, seed):
     np.testing.assert_array_equal(ix.cpu().numpy(), want_i)
     np.testing.assert_array_equal(_bits(sc).view(np.uint8), want_s.view(np.uint8))
 
+# Calls of 2,048 (row, probe) pairs or more take the balanced form (ids
+# listed per pair, then scoring spread over the chip by groups of 64 slots:
+# kmean_list_kernel, kmean_score_kernel); smaller ones a workgroup per pair
+# (kmean_ann_kernel).  Rows are independent, so a large call must equal the
+# same rows called in slices of fewer pairs; three rows are also checked
+# against the oracle.  dim 1280 float32 exceeds the balanced form's LDS and
+# takes the workgroup form at both sizes.
+@pytest.mark.parametrize("dim,dtype,filtered,findex,divisor,width", [
+    (128, "bfloat16", True, False, -1, 6000), (17, "float32", True, True, -1, 3000),
+    (64, "float16", False, False, -1, 900), (32, "int8", True, False, -1, 5000),
+    (96, "int8", False, False, 7, 5000), (40, "bfloat16", True, True, -1, 200),
+    (1024, "float32", True, False, -1, 4000), (1280, "float32", False, False, -1, 2000)])
+def test_balanced_form_matches_slices_and_oracle(dim, dtype, filtered, findex, divisor, width):
+    rng = np.random.default_rng(dim * 7 + len(dtype) + width)
+    B, P_ = 512, 8
+    nclus = 24
+    sizes = rng.integers(0, 1500 if dim >= 1024 else 3000, nclus)
+    sizes[3] = 0
+    offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    n = int(offs[-1])
+    if dtype == "int8":
+        emb = rng.integers(-128, 128, (n, dim)).astype(np.int8)
+        q = rng.integers(-128, 128, (B, dim)).astype(np.int8)
+    else:
+        emb = rng.standard_normal((n, dim)).astype(np.float32)
+        q = rng.standard_normal((B, dim)).astype(np.float32)
+        if dtype == "float16":
+            emb, q = emb.astype(np.float16), q.astype(np.float16)
+        if dtype == "bfloat16":
+            emb, q = O.bf16_round(emb), O.bf16_round(q)
+    bf16 = dtype == "bfloat16"
+    cids = rng.integers(-1, nclus + 1, (B, P_)).astype(np.int64)  # ids outside the offsets select nothing
+    clen = np.where((cids >= 0) & (cids < nclus), sizes[np.clip(cids, 0, nclus - 1)], 5).astype(np.int64)
+    clen[rng.random((B, P_)) < 0.1] //= 3  # a prefix of the cluster
+    mask = fidx = None
+    if filtered:
+        mrows = 37 if findex else B
+        mask = rng.integers(-2**63, 2**63 - 1, (mrows, n // 64 + 1), dtype=np.int64)
+        mask &= rng.integers(-2**63, 2**63 - 1, mask.shape, dtype=np.int64)  # density 1/4
+        if findex:
+            fidx = rng.integers(-2, mrows + 2, B).astype(np.int64)  # some rows name no mask row
+    e_t, q_t = _t(emb, bf16), _t(q, bf16)
+    o_t = _t(offs)
+
+    def call(r0, r1):
+        kw = dict(divisor_for_int8=divisor, invalid_index_value=-3)
+        if filtered:
+            kw["filtering_bit_mask"] = _t(mask if findex else mask[r0:r1])
+            if findex:
+                kw["filtering_bit_index"] = _t(fidx[r0:r1])
+        return st.fused_kmean_ann(o_t, _t(cids[r0:r1]), _t(clen[r0:r1]), e_t, q_t[r0:r1], width, **kw)
+
+    H.note(f"[kmean balanced] dim={dim} {dtype} filtered={filtered} index={findex} width={width} docs={n}")
+    sc, ix = call(0, B)
+    for r0 in range(0, B, 128):  # 1,024 pairs per call: workgroup kernel
+        s2, i2 = call(r0, r0 + 128)
+        assert torch.equal(ix[r0:r0 + 128], i2), f"indices of rows {r0}.. differ between the kernels"
+        assert np.array_equal(_bits(sc[r0:r0 + 128]), _bits(s2)), f"scores of rows {r0}.. differ"
+    for b in (0, 201, B - 1):
+        m = None
+        if filtered:
+            m = mask[fidx[b]:fidx[b] + 1] if findex and 0 <= fidx[b] < mask.shape[0] else (
+                np.zeros((1, mask.shape[1]), np.int64) if findex else mask[b:b + 1])
+        ws, wi = O.fused_kmean_ann(offs, np.clip(cids[b:b + 1], 0, nclus - 1), np.where(
+            (cids[b:b + 1] >= 0) & (cids[b:b + 1] < nclus), clen[b:b + 1], 0), emb, q[b:b + 1], width,
+            filter_mask=m, invalid_index=-3, divisor=divisor, bf16=bf16)
+        np.testing.assert_array_equal(ix[b:b + 1].cpu().numpy(), wi)
+        np.testing.assert_array_equal(_bits(sc[b:b + 1]).view(np.uint8), ws.view(np.uint8))
+
+
 def test_search_mask_as_filter():
     """The packed output of bloom_index_search_batch filters the scoring, doc d
     at bit 63 - d % 64, as the reference CUDA op reads it."""

@@ -57,7 +57,9 @@ def _call(c, width, noalloc):
 @pytest.mark.parametrize("filtered", [False, True])
 def test_noalloc_matches_workspace_entry_point(filtered):
     rng = np.random.default_rng(31 + filtered)
-    for batch, probes, width in ((48, 6, 6400), (5, 3, 96)):  # second call smaller
+    # each call smaller than the one before; the first (4,096 pairs) takes the
+    # balanced form, whose group prefix also lives in the scratch array
+    for batch, probes, width in ((512, 8, 3000), (48, 6, 6400), (5, 3, 96)):
         c = _case(rng, batch, probes, 64, filtered)
         H.note(f"[noalloc] filtered={filtered} batch={batch} probes={probes} width={width} docs={c['n']}")
         want_s, want_i = _call(c, width, noalloc=False)
