@@ -323,6 +323,42 @@ __global__ __launch_bounds__(kKmCountThreads) void kmean_count_kernel(KmArgs a, 
   if (lane == 0) counts[item] = sum;
 }
 
+// Fills n elements of es bytes (2 or 4) at p with the element `word`
+// (its low es bytes): the elements before the first 16-byte boundary one by
+// one, then 16-byte stores, then the rest; thread t of nt.
+__device__ __forceinline__ void km_fill(char* p, int64_t n, int es, uint32_t word, int t, int nt) {
+  const int per = 16 / es;
+  int64_t head = static_cast<int64_t>(((16u - (reinterpret_cast<uintptr_t>(p) & 15u)) & 15u) / es);
+  if (head > n) head = n;
+  auto one = [&](char* q) {
+    if (es == 2) *reinterpret_cast<uint16_t*>(q) = static_cast<uint16_t>(word);
+    else *reinterpret_cast<uint32_t*>(q) = word;
+  };
+  if (t < head) one(p + t * es);
+  char* q = p + head * es;
+  const int64_t m = n - head, units = m / per;
+  const uint32_t w = es == 2 ? ((word & 0xFFFFu) | (word << 16)) : word;
+  for (int64_t u = t; u < units; u += nt) reinterpret_cast<uint4*>(q)[u] = make_uint4(w, w, w, w);
+  for (int64_t i = units * per + t; i < m; i += nt) one(q + i * es);
+}
+
+// Padding of slots [s0, s1) of the output row starting at out0: the score
+// dtype's most negative finite value (-FLT_MAX, -65504 for float16, 0xFF7F
+// for bfloat16) or INT32_MIN, and invalid_index.
+template <int ST>
+__device__ __forceinline__ void km_pad_range(const KmArgs& a, int64_t out0, int64_t s0, int64_t s1,
+                                             int t, int nt) {
+  if (s1 <= s0) return;
+  const int es = ST == kKmF16 || ST == kKmBF16 ? 2 : 4;
+  const uint32_t word = ST == kKmF32 ? 0xFF7FFFFFu
+                        : ST == kKmF16 ? 0xFBFFu
+                        : ST == kKmBF16 ? 0xFF7Fu
+                                        : 0x80000000u;
+  km_fill(static_cast<char*>(a.scores) + (out0 + s0) * es, s1 - s0, es, word, t, nt);
+  km_fill(reinterpret_cast<char*>(a.indices + out0 + s0), s1 - s0, 4,
+          static_cast<uint32_t>(static_cast<int32_t>(a.invalid_index)), t, nt);
+}
+
 // DT: embedding dtype; ST: score dtype.  One workgroup per (row, probe):
 // its first output slot is the row's passing docs of the earlier probes
 // (from counts); per chunk of 4,096 docs of the cluster every thread forms
@@ -481,16 +517,8 @@ __global__ __launch_bounds__(kKmThreads) __attribute__((amdgpu_waves_per_eu(4)))
     }
   }
   if (p != nprobes - 1) return;
-  // padding: the score dtype's most negative finite value (-FLT_MAX, -65504
-  // for float16, 0xFF7F for bfloat16 as the reference CUDA op pads,
-  // simple_index_mm.cuh:99-123) or INT32_MIN, and invalid_index
-  for (int64_t s = min(written, a.max_per_row) + tid; s < a.max_per_row; s += kKmThreads) {
-    if constexpr (ST == kKmF32) static_cast<float*>(a.scores)[out0 + s] = -3.402823466e38f;
-    if constexpr (ST == kKmF16) static_cast<uint16_t*>(a.scores)[out0 + s] = 0xFBFFu;
-    if constexpr (ST == kKmBF16) static_cast<uint16_t*>(a.scores)[out0 + s] = 0xFF7Fu;
-    if constexpr (ST == kKmI32) static_cast<int32_t*>(a.scores)[out0 + s] = INT32_MIN;
-    a.indices[out0 + s] = static_cast<int32_t>(a.invalid_index);
-  }
+  // padding (as the reference CUDA op pads, simple_index_mm.cuh:99-123)
+  km_pad_range<ST>(a, out0, min(written, a.max_per_row), a.max_per_row, tid, kKmThreads);
 }
 
 // ------------------------------------------------ balanced form (many pairs)
@@ -505,7 +533,7 @@ __global__ __launch_bounds__(kKmThreads) __attribute__((amdgpu_waves_per_eu(4)))
 //                        n_b = min(total, width) and its groups of 64 slots,
 //                        with the exclusive prefix of the groups over rows;
 //   kmean_list_kernel    one wave per (row, probe): lists the passing docs
-//                        (chunks of 1,024 docs, 16 per lane, offsets in LDS)
+//                        (chunks of 4,096 docs, 64 per lane, offsets in LDS)
 //                        and writes their ids into the row's slots; the
 //                        row's padding is split over its probes' waves;
 //   kmean_score_kernel   a fixed grid of waves; wave w takes the groups
@@ -516,11 +544,14 @@ __global__ __launch_bounds__(kKmThreads) __attribute__((amdgpu_waves_per_eu(4)))
 //                        the next group's ids) in flight while a slice is
 //                        summed.
 constexpr int kKmWaveThreads = 256;  // 4 waves per workgroup
-constexpr int kKmWaveDocsPerLane = 16;
+constexpr int kKmWaveDocsPerLane = 64;  // list pass: one 4,096-doc chunk per step
 constexpr int kKmWaveChunk = 64 * kKmWaveDocsPerLane;
 constexpr int kKmWaveStage = 64 * kKmStageStride;
 constexpr int kKmRing = 4;  // groups whose ids and place are held per wave
 constexpr int kKmRingBytes = kKmRing * (64 * 4 + 32);  // ids, then a KmGroup (24 bytes) each
+constexpr int kKmScoreAhead = 2;  // staging steps in flight per scoring wave (4 measured no faster)
+// the loads may run kKmScoreAhead groups ahead of the sums (one slice per row)
+static_assert(kKmRing > kKmScoreAhead && (kKmRing & (kKmRing - 1)) == 0, "ring size");
 constexpr int64_t kKmBalancedPairs = 2048;
 constexpr int64_t kKmBalancedMaxRows = 16384;  // rows the single-workgroup prefix takes
 constexpr int kKmWaveMaxLds = 65536;           // dynamic LDS of a score workgroup
@@ -575,15 +606,6 @@ __global__ __launch_bounds__(kKmGroupsThreads) void kmean_groups_kernel(
 }
 
 template <int ST>
-__device__ __forceinline__ void km_pad(const KmArgs& a, int64_t at) {
-  if constexpr (ST == kKmF32) static_cast<float*>(a.scores)[at] = -3.402823466e38f;
-  if constexpr (ST == kKmF16) static_cast<uint16_t*>(a.scores)[at] = 0xFBFFu;
-  if constexpr (ST == kKmBF16) static_cast<uint16_t*>(a.scores)[at] = 0xFF7Fu;
-  if constexpr (ST == kKmI32) static_cast<int32_t*>(a.scores)[at] = INT32_MIN;
-  a.indices[at] = static_cast<int32_t>(a.invalid_index);
-}
-
-template <int ST>
 __global__ __launch_bounds__(kKmWaveThreads) void kmean_list_kernel(KmArgs a, const int64_t* counts,
                                                                     const int64_t* rowtot,
                                                                     int64_t pairs) {
@@ -630,7 +652,7 @@ __global__ __launch_bounds__(kKmWaveThreads) void kmean_list_kernel(KmArgs a, co
   const int64_t lo = min(rowtot[b], a.max_per_row);
   const int64_t share = (a.max_per_row - lo + a.probes - 1) / a.probes;
   const int64_t s0 = lo + p * share, s1 = min(a.max_per_row, s0 + share);
-  for (int64_t s = s0 + lane; s < s1; s += 64) km_pad<ST>(a, out0 + s);
+  km_pad_range<ST>(a, out0, s0, s1, lane, 64);
 }
 
 // Place of a group of 64 slots: row, first slot, filled slots in it.
@@ -763,13 +785,13 @@ __global__ __launch_bounds__(kKmWaveThreads) __attribute__((amdgpu_waves_per_eu(
   };
   double acc = 0.0;
   int32_t iacc = 0;
-  uint4 buf[kKmAhead][4];
+  uint4 buf[kKmScoreAhead][4];
 #pragma unroll
-  for (int j = 0; j < kKmAhead; ++j)
+  for (int j = 0; j < kKmScoreAhead; ++j)
     if (j < steps) load(j, buf[j]);
-  for (int64_t t0 = 0; t0 < steps; t0 += kKmAhead) {
+  for (int64_t t0 = 0; t0 < steps; t0 += kKmScoreAhead) {
 #pragma unroll
-    for (int j = 0; j < kKmAhead; ++j) {
+    for (int j = 0; j < kKmScoreAhead; ++j) {
       const int64_t t = t0 + j;
       if (t >= steps) break;
       const int64_t g = g_lo + t / nslices;
@@ -780,7 +802,7 @@ __global__ __launch_bounds__(kKmWaveThreads) __attribute__((amdgpu_waves_per_eu(
       for (int i = 0; i < 4; ++i)
         *reinterpret_cast<uint4*>(stg + (lr + 16 * i) * kKmStageStride + lp * 16) = buf[j][i];
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      if (t + kKmAhead < steps) load(t + kKmAhead, buf[j]);
+      if (t + kKmScoreAhead < steps) load(t + kKmScoreAhead, buf[j]);
       if (lane < gr.n) {
 #pragma unroll
         for (int q = 0; q < per_slice; ++q) {
