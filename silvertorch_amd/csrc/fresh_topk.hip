@@ -475,6 +475,65 @@ __global__ __launch_bounds__(kSelectThreads) void fresh_select_kernel(FreshTopkA
     s_idx[i] = kNoIndex;
   }
   __syncthreads();
+  constexpr int B = score_bytes(kType);
+  auto emit = [&](int64_t j, uint32_t m) {
+    if (static_cast<int64_t>(m) >= N) m = 0;  // never: exactly k entries were taken
+    const int64_t o = row * k + j;
+    a.top_index[o] = static_cast<int64_t>(m);
+    a.from_fresh[o] = static_cast<int64_t>(m) < a.num_fresh ? 1 : 0;
+    const char* src = m < a.num_fresh ? static_cast<const char*>(fs) + static_cast<int64_t>(m) * B
+                                      : static_cast<const char*>(ms) + (static_cast<int64_t>(m) - a.num_fresh) * B;
+    char* dst = static_cast<char*>(a.top_scores) + o * B;
+    if constexpr (B == 8) {
+      *reinterpret_cast<uint64_t*>(dst) = *reinterpret_cast<const uint64_t*>(src);
+    } else if constexpr (B == 4) {
+      *reinterpret_cast<uint32_t*>(dst) = *reinterpret_cast<const uint32_t*>(src);
+    } else if constexpr (B == 2) {
+      *reinterpret_cast<uint16_t*>(dst) = *reinterpret_cast<const uint16_t*>(src);
+    } else {
+      *dst = *src;
+    }
+  };
+  if (n <= kSelectThreads) {
+    // bitonic sort with entry t in thread t's registers, best first: pairs
+    // at a stride below 64 meet within a wave (cross-lane shuffles), wider
+    // ones through LDS
+    uint64_t mk = 0ull;
+    uint32_t mi = kNoIndex;
+    if (tid < n) {
+      mk = s_key[tid];
+      mi = s_idx[tid];
+    }
+    for (int size = 2; size <= n; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        uint64_t pk;
+        uint32_t pi;
+        if (stride >= 64) {
+          __syncthreads();  // the previous exchange's readers are done
+          if (tid < n) {
+            s_key[tid] = mk;
+            s_idx[tid] = mi;
+          }
+          __syncthreads();
+          pk = tid < n ? s_key[tid ^ stride] : 0ull;
+          pi = tid < n ? s_idx[tid ^ stride] : kNoIndex;
+        } else {
+          pk = __shfl_xor(mk, stride, 64);
+          pi = __shfl_xor(mi, stride, 64);
+        }
+        // the lower thread of a pair keeps the entry that goes first in its
+        // size-block's direction (best first when (t & size) == 0)
+        const bool first = ((tid & stride) == 0) == ((tid & size) == 0);
+        const bool take = first ? before(pk, pi, mk, mi) : before(mk, mi, pk, pi);
+        if (tid < n && take) {
+          mk = pk;
+          mi = pi;
+        }
+      }
+    }
+    if (tid < k) emit(tid, mi);
+    return;
+  }
   // bitonic sort of s_key / s_idx [0, n), best first
   for (int size = 2; size <= n; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
@@ -495,26 +554,7 @@ __global__ __launch_bounds__(kSelectThreads) void fresh_select_kernel(FreshTopkA
       __syncthreads();
     }
   }
-  for (int64_t j = tid; j < k; j += kSelectThreads) {
-    uint32_t m = s_idx[j];
-    if (static_cast<int64_t>(m) >= N) m = 0;  // never: exactly k entries were taken
-    const int64_t o = row * k + j;
-    a.top_index[o] = static_cast<int64_t>(m);
-    a.from_fresh[o] = static_cast<int64_t>(m) < a.num_fresh ? 1 : 0;
-    constexpr int B = score_bytes(kType);
-    const char* src = m < a.num_fresh ? static_cast<const char*>(fs) + static_cast<int64_t>(m) * B
-                                      : static_cast<const char*>(ms) + (static_cast<int64_t>(m) - a.num_fresh) * B;
-    char* dst = static_cast<char*>(a.top_scores) + o * B;
-    if constexpr (B == 8) {
-      *reinterpret_cast<uint64_t*>(dst) = *reinterpret_cast<const uint64_t*>(src);
-    } else if constexpr (B == 4) {
-      *reinterpret_cast<uint32_t*>(dst) = *reinterpret_cast<const uint32_t*>(src);
-    } else if constexpr (B == 2) {
-      *reinterpret_cast<uint16_t*>(dst) = *reinterpret_cast<const uint16_t*>(src);
-    } else {
-      *dst = *src;
-    }
-  }
+  for (int64_t j = tid; j < k; j += kSelectThreads) emit(j, s_idx[j]);
 }
 
 template <int kType>
