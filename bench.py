@@ -504,6 +504,14 @@ def measure_search_cfg3(st, O):
         torch.cuda.synchronize()
         times.append(time.perf_counter() - t)
     secs = sorted(times)[1]
+    # back-to-back calls, as the headline's steps run: each call's host plan
+    # compile overlaps the previous call's kernels
+    n_b2b = 6
+    t = time.perf_counter()
+    for _ in range(n_b2b):
+        out = st.bloom_index_search_batch(bi, bo, pd, po, cspec.k, cspec.hash_k, False)
+    torch.cuda.synchronize()
+    step_secs = (time.perf_counter() - t) / n_b2b
     Q = len(queries)
     alg = bi.numel() * 8 + bo.numel() * 8 + pd.numel() + po.numel() * 8 + out.numel() * 8
     bbo = bo.cpu().numpy()
@@ -541,7 +549,8 @@ def measure_search_cfg3(st, O):
         ok &= bool(np.array_equal(out[:, bnd * 32:(bnd + 1) * 32].cpu().numpy(), want))
     w = np.diff(bbo)
     log(f"cfg3 search: {N} docs x {Q} queries, widths {w.min()}-{w.max()}, {secs * 1e3:.2f} ms op, "
-        f"{kernel_ms:.2f} ms kernels, sampled bundles bit-exact vs oracle: {ok}")
+        f"{step_secs * 1e3:.2f} ms per back-to-back step, {kernel_ms:.2f} ms kernels, "
+        f"sampled bundles bit-exact vs oracle: {ok}")
     if not ok:
         sys.exit("parity failure in sampled cfg3 bundles")
     return {
@@ -550,9 +559,11 @@ def measure_search_cfg3(st, O):
         "ms": secs * 1e3, "doc_queries_per_s": Q * N / secs,
         "algorithmic_bytes": alg, "achieved_gbs": alg / secs / 1e9,
         "frac_of_hbm_peak": alg / secs / 1e9 / HBM_PEAK_GBS,
+        "ms_per_step": step_secs * 1e3, "step_frac_of_hbm_peak": alg / step_secs / 1e9 / HBM_PEAK_GBS,
         "kernel_ms": kernel_ms, "kernel_gbs": alg / kernel_ms / 1e6,
         "kernel_frac_of_hbm_peak": alg / kernel_ms / 1e6 / HBM_PEAK_GBS,
-        "note": "ms: wall time of the op (plan compile, width binding, search kernels), median of 3; "
+        "note": "ms: wall time of one op call (plan compile, width binding, search kernels), median of 3; "
+                "ms_per_step: back-to-back op calls (6), each compiling and binding its plan; "
                 "kernel_ms: the search launches alone (host-bound plan, HIP events), median of 5",
     }
 
