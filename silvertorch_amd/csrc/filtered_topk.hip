@@ -19,10 +19,10 @@
 //
 // Selection is exact and runs in rounds over growing doc ranges: a scored
 // pair enters query q's candidate list when it passes the filter and its
-// score is at least thr[q]; after each round one workgroup per query sorts
-// its candidates (bitonic, in LDS) down to the best `topk` and sets thr[q] to
-// the score of the topk-th, so later rounds emit only pairs that can still
-// enter.  A candidate list has a fixed capacity; if any round overflows one,
+// score is at least thr[q]; after each round one workgroup per query keeps
+// the best `topk` of its candidates (a radix select in LDS; the last round
+// sorts them, bitonic) and sets thr[q] to the score of the topk-th, so later
+// rounds emit only pairs that can still enter.  A candidate list has a fixed capacity; if any round overflows one,
 // the whole selection is redone with rounds too small to overflow.
 #include <hip/hip_runtime.h>
 
@@ -409,8 +409,117 @@ __device__ void bitonic_sort_desc(uint64_t* keys, int size) {
   }
 }
 
-// One workgroup per query: keeps the best `topk` candidates (sorted), sets
-// the entry threshold, and on the last round writes the outputs.  The
+// Moves the best m = min(n, k) of the n distinct keys in keys[0, n) to
+// keys[0, m) in no particular order and returns m; *min_key receives the
+// smallest of them.  A radix select over the bits in which the keys differ
+// (8 bits a pass, one LDS histogram per wave) finds the lower bound L of the
+// best m (the m-th key itself, or the start of a digit bucket that holds
+// exactly the keys still needed), then the keys >= L are gathered.  Called
+// by the whole workgroup; the keys stay in LDS.
+__device__ uint32_t select_best(uint64_t* keys, uint32_t n, uint32_t k, uint64_t* min_key) {
+  constexpr int kWaves = kSelectThreads / 64;
+  __shared__ uint32_t hist[kWaves][256];
+  __shared__ uint64_t red_and[kWaves], red_or[kWaves];
+  __shared__ uint64_t s_prefix, s_min;
+  __shared__ uint32_t s_remaining, s_done, s_count;
+  __shared__ uint64_t picked[kMaxTopk];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t m = min(n, k);
+  uint64_t bound = 0ull;  // keys >= bound are the best m
+  if (n > k) {
+    uint64_t kand = ~0ull, kor = 0ull;
+    for (uint32_t i = tid; i < n; i += kSelectThreads) {
+      kand &= keys[i];
+      kor |= keys[i];
+    }
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) {
+      kand &= __shfl_xor(kand, d, 64);
+      kor |= __shfl_xor(kor, d, 64);
+    }
+    if (lane == 0) {
+      red_and[wave] = kand;
+      red_or[wave] = kor;
+    }
+    for (int i = tid; i < kWaves * 256; i += kSelectThreads) (&hist[0][0])[i] = 0u;
+    __syncthreads();
+    kand = ~0ull;
+    kor = 0ull;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      kand &= red_and[w];
+      kor |= red_or[w];
+    }
+    const uint64_t diff = kand ^ kor;  // nonzero: n > k >= 1 distinct keys
+    uint64_t prefix = kand & ~(~0ull >> __builtin_clzll(diff));
+    uint32_t remaining = k;
+    for (int shift = ((63 - __builtin_clzll(diff)) / 8) * 8; shift >= 0; shift -= 8) {
+      const uint64_t hi_mask = shift + 8 >= 64 ? 0ull : (~0ull << (shift + 8));
+      for (uint32_t i = tid; i < n; i += kSelectThreads) {
+        const uint64_t key = keys[i];
+        if ((key & hi_mask) == (prefix & hi_mask)) atomicAdd(&hist[wave][(key >> shift) & 0xFFu], 1u);
+      }
+      __syncthreads();
+      if (wave == 0) {
+        // bins from the top digit down: 4 per lane, lane 0 holding 255..252
+        uint32_t c[4], sum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          c[i] = 0;
+#pragma unroll
+          for (int w = 0; w < kWaves; ++w) c[i] += hist[w][255 - (lane * 4 + i)];
+          sum += c[i];
+        }
+        uint32_t incl = sum;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const uint32_t y = __shfl_up(incl, d, 64);
+          if (lane >= d) incl += y;
+        }
+        uint32_t run = incl - sum;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (run < remaining && run + c[i] >= remaining) {
+            const int digit = 255 - (lane * 4 + i);
+            s_prefix = (prefix & hi_mask) | (static_cast<uint64_t>(digit) << shift);
+            s_remaining = remaining - run;
+            s_done = run + c[i] == remaining ? 1u : 0u;  // the whole bucket is needed
+          }
+          run += c[i];
+        }
+      }
+      __syncthreads();
+      prefix = s_prefix;
+      remaining = s_remaining;
+      const bool done = s_done != 0u;
+      for (int i = tid; i < kWaves * 256; i += kSelectThreads) (&hist[0][0])[i] = 0u;
+      __syncthreads();
+      if (done) break;
+    }
+    bound = prefix;  // the bucket's lowest key, or the m-th key after the last pass
+  }
+  if (tid == 0) {
+    s_count = 0u;
+    s_min = ~0ull;
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < n; i += kSelectThreads) {
+    const uint64_t key = keys[i];
+    if (key >= bound) {
+      picked[atomicAdd(&s_count, 1u)] = key;
+      atomicMin(&s_min, key);
+    }
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < m; i += kSelectThreads) keys[i] = picked[i];
+  *min_key = s_min;
+  __syncthreads();
+  return m;
+}
+
+// One workgroup per query: keeps the best `topk` candidates (unordered
+// between rounds), sets the entry threshold, and on the last round writes
+// the outputs, sorted.  The
 // candidates are the kept best (slots [0, counts[q])) followed by the entries
 // of the round's nseg segments, gathered in that order.
 __global__ __launch_bounds__(kSelectThreads) void topk_select_kernel(
@@ -448,12 +557,31 @@ __global__ __launch_bounds__(kSelectThreads) void topk_select_kernel(
     return cand[kMaxTopk + static_cast<uint64_t>(lo) * st.seg + (w - start[lo])];
   };
   if (n <= static_cast<uint32_t>(kSelectSlots)) {
-    // One sort of the smallest power of two holding every candidate.
-    int size = 64;
-    while (size < static_cast<int>(n)) size <<= 1;
-    for (int i = threadIdx.x; i < size; i += kSelectThreads) keys[i] = i < static_cast<int>(n) ? at(i) : 0ull;
+    for (int i = threadIdx.x; i < static_cast<int>(n); i += kSelectThreads) keys[i] = at(i);
     __syncthreads();
-    bitonic_sort_desc(keys, size);
+    // the best min(n, topk) keys to the front of keys[], unordered; sorted
+    // on the last round
+    uint64_t sel_min = 0ull;
+    const uint32_t best = select_best(keys, n, static_cast<uint32_t>(topk), &sel_min);
+    if (final_round) {
+      int size = 64;
+      while (size < static_cast<int>(best)) size <<= 1;
+      for (int i = static_cast<int>(best) + threadIdx.x; i < size; i += kSelectThreads) keys[i] = 0ull;
+      __syncthreads();
+      bitonic_sort_desc(keys, size);
+      for (int64_t i = threadIdx.x; i < topk; i += kSelectThreads) {
+        const bool have = i < best;
+        out_ids[q * topk + i] = have ? static_cast<int64_t>(0xFFFFFFFFu - static_cast<uint32_t>(keys[i])) : -1;
+        out_scores[q * topk + i] = have ? from_ordered(static_cast<uint32_t>(keys[i] >> 32)) : -INFINITY;
+      }
+      return;
+    }
+    for (uint32_t i = threadIdx.x; i < best; i += kSelectThreads) cand[i] = keys[i];
+    if (threadIdx.x == 0) {
+      st.counts[q] = best;
+      st.thr[q] = best == topk ? from_ordered(static_cast<uint32_t>(sel_min >> 32)) : -INFINITY;
+    }
+    return;
   } else {
     // Keys 0 .. kSelectChunk-1 hold the best so far; each chunk of
     // candidates is sorted in behind them.
