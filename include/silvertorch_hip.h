@@ -436,10 +436,11 @@ int st_fresh_gather(const int64_t* top_index, int64_t rows, int64_t k,
  * for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
  * arguments and results as st_fused_kmean_ann minus `workspace`: the
- * per-(row, probe) counts go to a fixed device array of the library, one
- * copy per GPU (8 MiB, held until the process ends), so batch x probes must
- * not exceed ST_KMEAN_NOALLOC_MAX_PAIRS (larger calls are rejected before
- * any launch).  The device current on the calling thread must be the one
+ * per-(row, probe) counts (and, when they fit after them, the row totals and
+ * group starts of calls of 2,048 pairs or more) go to a fixed device array
+ * of the library, one copy per GPU (8 MiB, held until the process ends), so
+ * batch x probes must not exceed ST_KMEAN_NOALLOC_MAX_PAIRS (larger calls
+ * are rejected before any launch).  The device current on the calling thread must be the one
  * the buffers and the stream belong to.  Allocates nothing (no hipMalloc,
  * hipFree or allocating library call).  Calls that overlap on one GPU share
  * the array and race: serialise them (one stream, or events).

@@ -976,9 +976,11 @@ extern "C" int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_of
 // caller-provided workspace.  Its address is taken once per device with
 // hipGetSymbolAddress, on that device's first call; host code uses only that
 // address, never the array's name.  Every (row, probe) count is written by
-// kmean_count_kernel before kmean_ann_kernel reads it, so nothing needs
-// clearing between calls; calls that overlap on one GPU share the array and
-// race.
+// kmean_count_kernel before it is read, and in the balanced form every row
+// total and group start by kmean_groups_kernel (after the counts, when they
+// fit the array; otherwise the call takes the workgroup form), so nothing
+// needs clearing between calls; calls that overlap on one GPU share the
+// array and race.
 
 namespace st {
 namespace {
