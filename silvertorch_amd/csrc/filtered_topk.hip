@@ -48,9 +48,8 @@ constexpr int kScoreWaves = kScoreThreads / 64;
 constexpr int kQueryTile = 32;
 constexpr int kLdsBytes = 160 * 1024;
 constexpr int kSelectThreads = 256;
-constexpr int kSelectSlots = 4096;   // bitonic buffer: best 2048 + a chunk of 2048
-constexpr int kSelectChunk = kSelectSlots / 2;
-constexpr int kMaxTopk = kSelectChunk;
+constexpr int kSelectSlots = 4096;   // candidates gathered into LDS for the selection
+constexpr int kMaxTopk = 2048;
 constexpr uint32_t kCandidateCapacity = 32768;  // per query
 // A query's candidate list: the best kept so far in slots [0, kMaxTopk), then
 // one segment per scoring workgroup (at most kMaxSegments of them), each
@@ -409,14 +408,16 @@ __device__ void bitonic_sort_desc(uint64_t* keys, int size) {
   }
 }
 
-// Moves the best m = min(n, k) of the n distinct keys in keys[0, n) to
+// Writes the best m = min(n, k) of the n distinct keys key_at(0 .. n-1) to
 // keys[0, m) in no particular order and returns m; *min_key receives the
-// smallest of them.  A radix select over the bits in which the keys differ
+// smallest of them.  key_at may read keys[] itself (the keys are gathered
+// before keys[] is written).  A radix select over the bits in which the keys differ
 // (8 bits a pass, one LDS histogram per wave) finds the lower bound L of the
 // best m (the m-th key itself, or the start of a digit bucket that holds
 // exactly the keys still needed), then the keys >= L are gathered.  Called
 // by the whole workgroup; the keys stay in LDS.
-__device__ uint32_t select_best(uint64_t* keys, uint32_t n, uint32_t k, uint64_t* min_key) {
+template <typename Key>
+__device__ uint32_t select_best(Key key_at, uint64_t* keys, uint32_t n, uint32_t k, uint64_t* min_key) {
   constexpr int kWaves = kSelectThreads / 64;
   __shared__ uint32_t hist[kWaves][256];
   __shared__ uint64_t red_and[kWaves], red_or[kWaves];
@@ -429,8 +430,9 @@ __device__ uint32_t select_best(uint64_t* keys, uint32_t n, uint32_t k, uint64_t
   if (n > k) {
     uint64_t kand = ~0ull, kor = 0ull;
     for (uint32_t i = tid; i < n; i += kSelectThreads) {
-      kand &= keys[i];
-      kor |= keys[i];
+      const uint64_t key = key_at(i);
+      kand &= key;
+      kor |= key;
     }
 #pragma unroll
     for (int d = 32; d > 0; d >>= 1) {
@@ -456,7 +458,7 @@ __device__ uint32_t select_best(uint64_t* keys, uint32_t n, uint32_t k, uint64_t
     for (int shift = ((63 - __builtin_clzll(diff)) / 8) * 8; shift >= 0; shift -= 8) {
       const uint64_t hi_mask = shift + 8 >= 64 ? 0ull : (~0ull << (shift + 8));
       for (uint32_t i = tid; i < n; i += kSelectThreads) {
-        const uint64_t key = keys[i];
+        const uint64_t key = key_at(i);
         if ((key & hi_mask) == (prefix & hi_mask)) atomicAdd(&hist[wave][(key >> shift) & 0xFFu], 1u);
       }
       __syncthreads();
@@ -504,7 +506,7 @@ __device__ uint32_t select_best(uint64_t* keys, uint32_t n, uint32_t k, uint64_t
   }
   __syncthreads();
   for (uint32_t i = tid; i < n; i += kSelectThreads) {
-    const uint64_t key = keys[i];
+    const uint64_t key = key_at(i);
     if (key >= bound) {
       picked[atomicAdd(&s_count, 1u)] = key;
       atomicMin(&s_min, key);
@@ -556,49 +558,27 @@ __global__ __launch_bounds__(kSelectThreads) void topk_select_kernel(
     }
     return cand[kMaxTopk + static_cast<uint64_t>(lo) * st.seg + (w - start[lo])];
   };
+  // the best min(n, topk) to the front of keys[], unordered: candidates
+  // gathered into LDS when they fit (several radix passes read them), else
+  // read from their segments on each pass
+  uint64_t sel_min = 0ull;
+  uint32_t best;
   if (n <= static_cast<uint32_t>(kSelectSlots)) {
     for (int i = threadIdx.x; i < static_cast<int>(n); i += kSelectThreads) keys[i] = at(i);
     __syncthreads();
-    // the best min(n, topk) keys to the front of keys[], unordered; sorted
-    // on the last round
-    uint64_t sel_min = 0ull;
-    const uint32_t best = select_best(keys, n, static_cast<uint32_t>(topk), &sel_min);
-    if (final_round) {
-      int size = 64;
-      while (size < static_cast<int>(best)) size <<= 1;
-      for (int i = static_cast<int>(best) + threadIdx.x; i < size; i += kSelectThreads) keys[i] = 0ull;
-      __syncthreads();
-      bitonic_sort_desc(keys, size);
-      for (int64_t i = threadIdx.x; i < topk; i += kSelectThreads) {
-        const bool have = i < best;
-        out_ids[q * topk + i] = have ? static_cast<int64_t>(0xFFFFFFFFu - static_cast<uint32_t>(keys[i])) : -1;
-        out_scores[q * topk + i] = have ? from_ordered(static_cast<uint32_t>(keys[i] >> 32)) : -INFINITY;
-      }
-      return;
-    }
-    for (uint32_t i = threadIdx.x; i < best; i += kSelectThreads) cand[i] = keys[i];
-    if (threadIdx.x == 0) {
-      st.counts[q] = best;
-      st.thr[q] = best == topk ? from_ordered(static_cast<uint32_t>(sel_min >> 32)) : -INFINITY;
-    }
-    return;
+    best = select_best([&](uint32_t i) { return keys[i]; }, keys, n, static_cast<uint32_t>(topk), &sel_min);
   } else {
-    // Keys 0 .. kSelectChunk-1 hold the best so far; each chunk of
-    // candidates is sorted in behind them.
-    for (int i = threadIdx.x; i < kSelectChunk; i += kSelectThreads) keys[i] = 0ull;
-    for (uint32_t c0 = 0; c0 < n; c0 += kSelectChunk) {
-      for (int i = threadIdx.x; i < kSelectChunk; i += kSelectThreads)
-        keys[kSelectChunk + i] = c0 + i < n ? at(c0 + i) : 0ull;
-      __syncthreads();
-      bitonic_sort_desc(keys, kSelectSlots);
-    }
+    best = select_best(at, keys, n, static_cast<uint32_t>(topk), &sel_min);
   }
-  const uint32_t best = min(n, static_cast<uint32_t>(topk));
   if (final_round) {
+    int size = 64;
+    while (size < static_cast<int>(best)) size <<= 1;
+    for (int i = static_cast<int>(best) + threadIdx.x; i < size; i += kSelectThreads) keys[i] = 0ull;
+    __syncthreads();
+    bitonic_sort_desc(keys, size);
     for (int64_t i = threadIdx.x; i < topk; i += kSelectThreads) {
       const bool have = i < best;
-      out_ids[q * topk + i] = have ? static_cast<int64_t>(0xFFFFFFFFu - static_cast<uint32_t>(keys[i]))
-                                   : -1;
+      out_ids[q * topk + i] = have ? static_cast<int64_t>(0xFFFFFFFFu - static_cast<uint32_t>(keys[i])) : -1;
       out_scores[q * topk + i] = have ? from_ordered(static_cast<uint32_t>(keys[i] >> 32)) : -INFINITY;
     }
     return;
@@ -606,7 +586,7 @@ __global__ __launch_bounds__(kSelectThreads) void topk_select_kernel(
   for (uint32_t i = threadIdx.x; i < best; i += kSelectThreads) cand[i] = keys[i];
   if (threadIdx.x == 0) {
     st.counts[q] = best;
-    st.thr[q] = best == topk ? from_ordered(static_cast<uint32_t>(keys[topk - 1] >> 32)) : -INFINITY;
+    st.thr[q] = best == topk ? from_ordered(static_cast<uint32_t>(sel_min >> 32)) : -INFINITY;
   }
 }
 
