@@ -365,12 +365,37 @@ void prepare_partial_plan(PartialPlan& pp, const Tensor& plans_data, const Tenso
   pp.blob = host.to(dev, /*non_blocking=*/true);
 }
 
-// One index chunk: host-side layout (one copy of the cluster arrays to the
-// host: the response length sizes the output), then the kernel.
+// The cluster arrays of one chunk on the host (the response length sizes the
+// output): device tensors are copied into pinned memory without waiting, so
+// the copies overlap the host plan compile; the caller synchronises the
+// current stream (`pending`) before the layout reads them.
+struct PartialHost {
+  Tensor co, cl, pi;
+};
+
+Tensor host_copy(const Tensor& x, bool& pending) {
+  if (!x.is_cuda()) return x.contiguous();
+  // only the current device's stream is synchronised before the layout
+  if (x.device().index() != c10::hip::current_device()) return x.to(at::kCPU).contiguous();
+  Tensor h = at::empty(x.sizes(), x.options().device(at::kCPU).pinned_memory(true));
+  h.copy_(x, /*non_blocking=*/true);
+  pending = true;
+  return h;
+}
+
+PartialHost partial_host(const Tensor& offsets, const Tensor& lengths,
+                         const c10::optional<Tensor>& query_plan_index, bool& pending) {
+  PartialHost h;
+  h.co = host_copy(offsets.contiguous(), pending);
+  h.cl = host_copy(lengths.contiguous(), pending);
+  if (query_plan_index.has_value()) h.pi = host_copy(query_plan_index->contiguous(), pending);
+  return h;
+}
+
+// One index chunk: host-side layout from the chunk's cluster arrays (on the
+// host already), then the kernel.
 std::tuple<Tensor, Tensor, Tensor> partial_chunk(const PartialPlan& pp, const Tensor& index_in,
-                                                 const Tensor& bbo_in, const Tensor& offsets,
-                                                 const Tensor& lengths,
-                                                 const c10::optional<Tensor>& query_plan_index) {
+                                                 const Tensor& bbo_in, const PartialHost& host) {
   TORCH_CHECK(index_in.is_cuda(), "bloom_index must be a GPU tensor");
   TORCH_CHECK(bbo_in.scalar_type() == at::kLong, "bloom_bundle_b_offsets must be int64");
   TORCH_CHECK(bbo_in.device() == index_in.device(),
@@ -378,11 +403,12 @@ std::tuple<Tensor, Tensor, Tensor> partial_chunk(const PartialPlan& pp, const Te
   TORCH_CHECK(bbo_in.numel() >= 1, "bloom_bundle_b_offsets must hold at least one entry");
   const auto dev = index_in.device();
   const Tensor index = index_in.contiguous(), bbo = bbo_in.contiguous();
-  const int64_t rows = offsets.size(0), clusters = offsets.size(1), n = rows * clusters;
-  const Tensor co = offsets.to(at::kCPU).contiguous(), cl = lengths.to(at::kCPU).contiguous();
-  Tensor pi;
-  if (query_plan_index.has_value()) pi = query_plan_index->to(at::kCPU).contiguous();
-  Tensor cumsum = at::empty({n}, at::kInt), first = at::empty({n}, at::kChar);
+  const Tensor& co = host.co;
+  const Tensor& cl = host.cl;
+  const Tensor& pi = host.pi;
+  const int64_t rows = co.size(0), clusters = co.size(1), n = rows * clusters;
+  const auto pinned = at::TensorOptions().pinned_memory(true);
+  Tensor cumsum = at::empty({n}, pinned.dtype(at::kInt)), first = at::empty({n}, pinned.dtype(at::kChar));
   Tensor items = at::empty({std::max<int64_t>(n, 1) * static_cast<int64_t>(sizeof(st_partial_item))},
                            at::TensorOptions().dtype(at::kByte).pinned_memory(true));
   int64_t num_items = 0, total = 0;
@@ -405,7 +431,11 @@ std::tuple<Tensor, Tensor, Tensor> partial_chunk(const PartialPlan& pp, const Te
     // items_d is freed here; the caching allocator keeps it until the stream
     // has used it (record_stream semantics of the current stream)
   }
-  return {cumsum.to(dev), first.to(dev), mask};
+  return {cumsum.to(dev, /*non_blocking=*/true), first.to(dev, /*non_blocking=*/true), mask};
+}
+
+void sync_current_stream(at::Device dev) {
+  c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(dev.index()).synchronize();
 }
 
 std::tuple<Tensor, Tensor, Tensor> partial_gpu(const Tensor& bloom_index, const Tensor& bbo,
@@ -416,9 +446,12 @@ std::tuple<Tensor, Tensor, Tensor> partial_gpu(const Tensor& bloom_index, const 
   check_partial_args(bloom_index, offsets, lengths, query_plan_index, plans_offsets.numel() / 8);
   TORCH_CHECK(bloom_index.is_cuda(), "bloom_index must be a GPU tensor");
   c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(bloom_index.device());
+  bool pending = false;
+  const PartialHost host = partial_host(offsets, lengths, query_plan_index, pending);
   PartialPlan pp;
   prepare_partial_plan(pp, plans_data, plans_offsets, k, hash_k, bloom_index.device());
-  return partial_chunk(pp, bloom_index, bbo, offsets, lengths, query_plan_index);
+  if (pending) sync_current_stream(bloom_index.device());
+  return partial_chunk(pp, bloom_index, bbo, host);
 }
 
 std::tuple<Tensor, Tensor, Tensor> partial_cpu(const Tensor& bloom_index, const Tensor& bbo,
@@ -457,12 +490,15 @@ std::tuple<std::vector<Tensor>, std::vector<Tensor>, std::vector<Tensor>> partia
   const bool on_cpu = !indices[0].is_cuda();
   const at::Device dev = on_cpu ? gpu_for_cpu_call() : indices[0].device();
   c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(dev);
+  bool pending = false;
+  std::vector<PartialHost> hosts;
+  for (size_t i = 0; i < n; ++i) hosts.push_back(partial_host(offsets[i], lengths[i], query_plan_index, pending));
   PartialPlan pp;
   prepare_partial_plan(pp, plans_data, plans_offsets, k, hash_k, dev);
+  if (pending) sync_current_stream(dev);
   std::vector<Tensor> cs, fs, ms;
   for (size_t i = 0; i < n; ++i) {
-    auto [c, f, m] = partial_chunk(pp, indices[i].to(dev), bbos[i].to(dev), offsets[i], lengths[i],
-                                   query_plan_index);
+    auto [c, f, m] = partial_chunk(pp, indices[i].to(dev), bbos[i].to(dev), hosts[i]);
     if (on_cpu) {
       c = c.cpu();
       f = f.cpu();
