@@ -81,7 +81,10 @@ def _random_case(rng, n, dim, q, density):
 
 
 @pytest.mark.parametrize("dim", [64, 128, 256])
-@pytest.mark.parametrize("n,q,topk,density", [(1000, 5, 10, 0.5), (5000, 37, 100, 0.2), (3000, 64, 7, 0.002)])
+# (20000, 8, 100, 0.9): the first round's 8,192 docs give every query more
+# than 4,096 candidates, which the selection reads from their segments
+@pytest.mark.parametrize("n,q,topk,density", [(1000, 5, 10, 0.5), (5000, 37, 100, 0.2), (3000, 64, 7, 0.002),
+                                              (20000, 8, 100, 0.9)])
 def test_topk_random(dim, n, q, topk, density):
     rng = np.random.default_rng(dim + n + q)
     emb_bf, qv_bf, emb32, qv32, packed = _random_case(rng, n, dim, q, density)
@@ -93,8 +96,8 @@ def test_topk_random(dim, n, q, topk, density):
 
 def test_topk_rounds_and_query_chunks():
     """60k docs cross several selection rounds (first round 8192 docs, then
-    x8) and selections of more than one 2048-key chunk; 600 queries cross
-    the 512 queries one launch of the dim-128 kernel scores."""
+    x8), each keeping the best 100 of its candidates; 600 queries cross the
+    512 queries one launch of the dim-128 kernel scores."""
     rng = np.random.default_rng(7)
     emb_bf, qv_bf, emb32, qv32, packed = _random_case(rng, 60000, 128, 600, 0.3)
     H.note("[topk] 60000 docs x 600 queries")
