@@ -7,26 +7,8 @@
 
 namespace st {
 
-// Exclusive prefix and total over the wave of per-lane values below 64, by
-// bit slices: one ballot per bit, mbcnt for the lanes below, a scalar
-// popcount for the total.  No cross-lane data movement through LDS.
-struct WaveScan {
-  uint32_t excl, total;
-};
-
-__device__ __forceinline__ WaveScan wave_scan_small(uint32_t v) {
-  WaveScan r{0u, 0u};
-#pragma unroll
-  for (int k = 0; k < 6; ++k) {
-    const uint64_t m = __ballot((v >> k) & 1u);
-    r.excl += __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                        __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u))
-              << k;
-    r.total += static_cast<uint32_t>(__popcll(m)) << k;
-  }
-  return r;
-}
-
+// Total over the wave of per-lane values below 64, by bit slices: one
+// ballot per bit and a scalar popcount of it.
 __device__ __forceinline__ uint32_t wave_total_small(uint32_t v) {
   uint32_t t = 0;
 #pragma unroll
