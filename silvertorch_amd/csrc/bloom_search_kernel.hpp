@@ -640,7 +640,7 @@ __device__ __forceinline__ uint32_t u32x4_get(const u32x4& v, int i) {
 
 // Stores this lane's 16 bytes of packed output row `row` on the bundle (and,
 // in kOutCounts mode, the row's match count on the bundle, summed over the
-// lane's 16-lane group).  The u32s are, in order, the low and high halves of
+// lane's 16-lane group; called with the whole group active).  The u32s are, in order, the low and high halves of
 // words 2s and 2s + 1 (s = lane & 15); a word's high half holds its first 32
 // docs.
 template <int kOut>
@@ -653,14 +653,20 @@ __device__ __forceinline__ void store_quad(const SearchArgs& a, int lane, int64_
                                             bundle * 256 + s * 16);
   __builtin_nontemporal_store(v, dst);
   if constexpr (kOut == kOutCounts) {
-    const int64_t first = bundle * kDocsPerBundle + static_cast<int64_t>(s) * 128;
-    uint32_t n = __builtin_popcount(v.y & valid_doc_mask(first, a.num_docs)) +
-                 __builtin_popcount(v.x & valid_doc_mask(first + 32, a.num_docs)) +
-                 __builtin_popcount(v.w & valid_doc_mask(first + 64, a.num_docs)) +
-                 __builtin_popcount(v.z & valid_doc_mask(first + 96, a.num_docs));
-#pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) n += __shfl_xor(n, m, 16);
-    if (s == 0) a.counts[static_cast<int64_t>(row) * a.num_bundles + bundle] = n;
+    uint32_t n;
+    if ((bundle + 1) * kDocsPerBundle <= a.num_docs) {  // every doc of the bundle counts
+      n = __builtin_popcount(v.x) + __builtin_popcount(v.y) + __builtin_popcount(v.z) +
+          __builtin_popcount(v.w);
+    } else {
+      const int64_t first = bundle * kDocsPerBundle + static_cast<int64_t>(s) * 128;
+      n = __builtin_popcount(v.y & valid_doc_mask(first, a.num_docs)) +
+          __builtin_popcount(v.x & valid_doc_mask(first + 32, a.num_docs)) +
+          __builtin_popcount(v.w & valid_doc_mask(first + 64, a.num_docs)) +
+          __builtin_popcount(v.z & valid_doc_mask(first + 96, a.num_docs));
+    }
+    // the 16-lane group is one DPP row: its last lane holds the group's sum
+    n = row16_inclusive_sum(n);
+    if (s == 15) a.counts[static_cast<int64_t>(row) * a.num_bundles + bundle] = n;
   }
 }
 
