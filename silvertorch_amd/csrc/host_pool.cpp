@@ -14,6 +14,8 @@
 namespace st {
 namespace {
 
+thread_local bool t_in_job = false;  // this thread runs a pool job's fn
+
 class HostPool {
  public:
   static HostPool& get() {
@@ -23,8 +25,14 @@ class HostPool {
   // fn(i) for every i in [0, n), chunks of `chunk` taken in turn by the
   // workers and the caller; fn must not throw.
   void run(int64_t n, int64_t chunk, const std::function<void(int64_t)>& fn) {
+    // A call from inside a job (worker or caller) runs alone: the caller
+    // already holds job_mu_, and try_lock by the owner is undefined.
+    if (t_in_job || getpid() != pid_ || workers_ == 0) {
+      for (int64_t i = 0; i < n; ++i) fn(i);
+      return;
+    }
     std::unique_lock<std::mutex> busy(job_mu_, std::try_to_lock);
-    if (!busy.owns_lock() || getpid() != pid_ || workers_ == 0) {
+    if (!busy.owns_lock()) {
       for (int64_t i = 0; i < n; ++i) fn(i);
       return;
     }
@@ -52,12 +60,14 @@ class HostPool {
     for (int i = 0; i < workers_; ++i) std::thread([this] { loop(); }).detach();
   }
   void work() {
+    t_in_job = true;
     for (;;) {
       const int64_t b = next_.fetch_add(chunk_);
-      if (b >= n_) return;
+      if (b >= n_) break;
       const int64_t e = std::min(n_, b + chunk_);
       for (int64_t i = b; i < e; ++i) (*fn_)(i);
     }
+    t_in_job = false;
   }
   void loop() {
     uint64_t seen = 0;

@@ -1,8 +1,9 @@
 // A few host threads for the plan compiler and the query parser: workers
 // started on first use (ST_PLAN_THREADS sets the total, default
 // min(8, hardware threads), the caller included) that share one job at a
-// time with the calling thread.  A caller that finds the pool busy, or runs
-// in a child of the process that started it, does the work alone.
+// time with the calling thread.  A caller that finds the pool busy, calls
+// from inside a job's fn, or runs in a child of the process that started
+// it, does the work alone.
 #pragma once
 
 #include <cstdint>
