@@ -168,16 +168,44 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 // 0, 1, 2, ... (assign_one_bits_position, bloom_index_util.cuh:183-207).
 // b >= K always holds for bundles that have terms (b >= floor(K *
 // b_multiplier) >= K), so the loop ends.
+// The first K seeds are hashed unrolled with constant seeds and compared
+// pairwise; only when two of them collide (about K^2 / 2b of the keys) does
+// the key keep the first occurrence of each position, in seed order, and go
+// on with seeds K, K + 1, ... as the sequential search would.
 template <int K>
 __device__ __forceinline__ void build_positions(uint64_t mx, uint64_t my,
                                                 const FastMod64& fm,
                                                 uint32_t (&found)[K]) {
-  int cnt = 0;
-  uint64_t seed = 0;
   // The seed-independent rotations once per key; seeds stay far below
   // 2^27 (k distinct positions out of b >= k need few more than k seeds).
   const uint64_t rx = rotl64(mx, 27), ry = rotl64(my, 31);
   const bool small = fm.d < (1ull << 30);
+  bool distinct = true;
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const uint64_t h = murmur_finish_rot(rx, ry, static_cast<uint64_t>(j));
+    found[j] = small ? fast_mod_small(h, fm) : static_cast<uint32_t>(fast_mod(h, fm));
+#pragma unroll
+    for (int i = 0; i < j; ++i) distinct &= found[i] != found[j];
+  }
+  if (distinct) return;
+  uint32_t first[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) first[j] = found[j];
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    bool dup = false;
+#pragma unroll
+    for (int i = 0; i < j; ++i) dup |= first[i] == first[j];
+    if (!dup) {
+#pragma unroll
+      for (int s = 0; s < K; ++s)
+        if (s == cnt) found[s] = first[j];
+      ++cnt;
+    }
+  }
+  uint64_t seed = K;
   while (cnt < K) {
     const uint64_t h = seed < (1ull << 27) ? murmur_finish_rot(rx, ry, seed) : murmur_finish(mx, my, seed);
     ++seed;
