@@ -292,9 +292,9 @@ template <int K>
 __device__ __forceinline__ void scatter_value(const ScatterArgs& a, int lc,
                                               unsigned long long* tile,
                                               unsigned long long* gbase, const FastMod64& fm,
-                                              uint64_t mx, int64_t j, uint32_t col,
+                                              uint64_t mx, int64_t value, uint32_t col,
                                               unsigned long long bit) {
-  const uint64_t my = murmur_mix_y(static_cast<uint64_t>(a.values[j]));
+  const uint64_t my = murmur_mix_y(static_cast<uint64_t>(value));
   if constexpr (K > 0) {
     scatter_term<K>(a, lc, tile, gbase, fm, mx, my, col, bit);
   } else {
@@ -307,7 +307,10 @@ __device__ __forceinline__ void scatter_value(const ScatterArgs& a, int lc,
 // its values in an LDS map, then the threads take the group's values one
 // each (all lanes hash, value loads coalesce).  A group with more values than
 // the map holds walks them per slot instead.  The seed-independent half of
-// the feature id's hash comes from LDS.
+// the feature id's hash comes from LDS.  With one workgroup per CU nothing
+// else covers the workgroup's global-load waits, so the loads are issued a
+// step ahead: the next group's offsets during this group, the next value
+// of a thread before the current one is hashed.
 template <int K>
 __global__ __launch_bounds__(kBuildThreads) void scatter_kernel(ScatterArgs a) {
   __shared__ unsigned long long tile[kBuildTileWords];
@@ -356,31 +359,60 @@ __global__ __launch_bounds__(kBuildThreads) void scatter_kernel(ScatterArgs a) {
     for (int64_t w = tid; w < tw; w += kBuildThreads) tile[w] = 0;
     __syncthreads();
     const int64_t slot_lo = dlo * F, slot_hi = max<int64_t>(dhi, dlo) * F;
+    // the offsets a group reads: its slot's two and the group's two bounds
+    struct GroupOffsets {
+      int64_t o0, o1, g0, g1;
+    };
+    auto load_group = [&](int64_t g) {
+      GroupOffsets o{0, 0, 0, 0};
+      if (g >= slot_hi) return o;
+      const int64_t rel = g + tid;
+      if (rel < slot_hi) {
+        o.o0 = offs[rel];
+        o.o1 = offs[rel + 1];
+      }
+      o.g0 = offs[g];
+      o.g1 = offs[min<int64_t>(g + kBuildThreads, slot_hi)];
+      return o;
+    };
+    GroupOffsets next = load_group(b > 0 ? slot_lo : slot_hi);
     for (int64_t g = slot_lo; b > 0 && g < slot_hi; g += kBuildThreads) {
+      const GroupOffsets cur = next;
+      next = load_group(g + kBuildThreads);
       const int64_t rel = g + tid;
       const bool has_slot = rel < slot_hi;
-      const int64_t v0 = has_slot ? clampv(offs[rel]) : 0;
-      const int64_t v1 = has_slot ? clampv(offs[rel + 1]) : 0;
+      const int64_t v0 = has_slot ? clampv(cur.o0) : 0;
+      const int64_t v1 = has_slot ? clampv(cur.o1) : 0;
       const int64_t d = has_slot ? rel / F : 0;
       const int64_t f = has_slot ? rel - d * F : 0;
-      const int64_t gv0 = clampv(offs[g]);
-      const int64_t gv1 = clampv(offs[min<int64_t>(g + kBuildThreads, slot_hi)]);
+      const int64_t gv0 = clampv(cur.g0);
+      const int64_t gv1 = clampv(cur.g1);
       if (mappable && gv1 - gv0 <= kBuildValueMap) {  // uniform across the workgroup
+        // Value loads are clamped to the group's last value rather than
+        // predicated: with the same loads on every path the next value stays
+        // in flight while the current one is hashed.  The first is issued
+        // before the map is built.
+        const int64_t last = max<int64_t>(gv1 - 1, gv0);
+        const bool any = gv1 > gv0;  // uniform
+        int64_t j = gv0 + tid;
+        int64_t value = any ? a.values[min(j, last)] : 0;
         __syncthreads();  // previous group's readers are done with vmap
-        for (int64_t j = v0; j < v1; ++j)
-          vmap[j - gv0] = static_cast<uint32_t>(d) | (static_cast<uint32_t>(f) << 11);
+        for (int64_t i = v0; i < v1; ++i)
+          vmap[i - gv0] = static_cast<uint32_t>(d) | (static_cast<uint32_t>(f) << 11);
         __syncthreads();
-        for (int64_t j = gv0 + tid; j < gv1; j += kBuildThreads) {
+        for (; j < gv1; j += kBuildThreads) {
+          const int64_t value_next = a.values[min(j + kBuildThreads, last)];
           const uint32_t m = vmap[j - gv0];
           const uint32_t dd = m & 2047u;
-          scatter_value<K>(a, lc, tile, gbase, fm, mx_of(m >> 11), j, (dd >> 6) - c0,
+          scatter_value<K>(a, lc, tile, gbase, fm, mx_of(m >> 11), value, (dd >> 6) - c0,
                            1ull << (63 - (dd & 63)));
+          value = value_next;
         }
       } else if (v0 < v1) {
         const uint64_t mx = mx_of(f);
         for (int64_t j = v0; j < v1; ++j)
-          scatter_value<K>(a, lc, tile, gbase, fm, mx, j, static_cast<uint32_t>(d >> 6) - c0,
-                           1ull << (63 - (d & 63)));
+          scatter_value<K>(a, lc, tile, gbase, fm, mx, a.values[j],
+                           static_cast<uint32_t>(d >> 6) - c0, 1ull << (63 - (d & 63)));
       }
     }
     __syncthreads();
