@@ -257,9 +257,12 @@ def measure_partial(st, bi, bo, pd, po, k, hk, N, packed, steps):
     def step():
         return st.bloom_index_search_batch_return_partial_response(bi, bo, pd, po, co, cl, k, hk)
 
-    cs, first, mask = step()
-    torch.cuda.synchronize()
+    # as many untimed calls as timed ones: the op's pinned host blocks come
+    # from torch's host allocator, whose pool the first calls fill
     n = max(steps // 10, 5)
+    for _ in range(n):
+        cs, first, mask = step()
+    torch.cuda.synchronize()
     t = time.perf_counter()
     for _ in range(n):
         cs, first, mask = step()

@@ -171,6 +171,15 @@ int64_t st_search_plan_device_bytes(const st_search_plan* plan);
  * plans with two host-to-device copies per call,
  * bloom_index_search_cuda.cu:1043-1098). */
 int st_search_plan_upload_source(st_search_plan* plan, const void* pinned_host);
+/* Optional, with st_search_plan_upload_source: the search call's copy runs
+ * in st_search_plan_upload_groups(plan) workgroups, and each workgroup g,
+ * once its loads of `pinned_host` have returned, stores `value` to
+ * pinned_words[g] (pinned, device-accessible host memory, 8-byte aligned,
+ * that many words).  A caller that sees every word equal to `value` may
+ * reuse `pinned_host` without an event on the stream.  Null turns it off.
+ * No reference counterpart. */
+int st_search_plan_upload_signal(st_search_plan* plan, void* pinned_words, uint64_t value);
+int64_t st_search_plan_upload_groups(const st_search_plan* plan);
 int64_t st_search_plan_num_queries(const st_search_plan* plan);
 int64_t st_search_plan_blob_bytes(const st_search_plan* plan);
 const void* st_search_plan_blob(const st_search_plan* plan);

@@ -28,6 +28,8 @@ SIGNATURES = {
     "st_search_plan_prepare_device_binding": (ctypes.c_int, [_vp, _i64]),
     "st_search_plan_device_bytes": (_i64, [_vp]),
     "st_search_plan_upload_source": (ctypes.c_int, [_vp, _vp]),
+    "st_search_plan_upload_signal": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64]),
+    "st_search_plan_upload_groups": (_i64, [_vp]),
     "st_search_plan_num_queries": (_i64, [_vp]),
     "st_search_plan_blob_bytes": (_i64, [_vp]),
     "st_search_plan_blob": (_vp, [_vp]),

@@ -144,12 +144,16 @@ __device__ __forceinline__ void for_each_width(const int64_t* bbo, int64_t nb, F
 // counting sort; order within a slot is arbitrary) -- with `order_if_wide`
 // only when some slot width is wide (the wide-bundle kernel's order).  The
 // census reads only the bundle offsets, so it runs while the copy waits on
-// PCIe.
+// PCIe.  With `upload_done` set, each upload workgroup then stores
+// `upload_value` to upload_done[its index]: the host can reuse the pinned
+// source once every group's word holds the value (no event on the stream).
 constexpr int kUploadPerThread = 4;   // 16-byte pieces per thread of an upload group
+constexpr uint64_t kUploadGroupBytes = 16ull * kBindThreads * kUploadPerThread;
 
 __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
     const uint8_t* __restrict__ host_src, uint8_t* __restrict__ blob, int64_t upload_bytes,
-    uint32_t upload_groups, const int64_t* __restrict__ bbo, int64_t nb,
+    uint32_t upload_groups, unsigned long long* upload_done, unsigned long long upload_value,
+    const int64_t* __restrict__ bbo, int64_t nb,
     uint32_t* __restrict__ num_slots, int64_t* __restrict__ slot_width,
     uint32_t* __restrict__ bundle_slot, uint32_t* __restrict__ bundle_order,
     uint32_t order_if_wide) {
@@ -170,6 +174,14 @@ __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
       if (i < vec) reinterpret_cast<v4*>(blob)[i] = v[j];
     }
     if (blockIdx.x == 0 && tid < 16 && vec * 16 + tid < upload_bytes) blob[vec * 16 + tid] = host_src[vec * 16 + tid];
+    if (upload_done != nullptr) {
+      // every thread's loads of the source have returned (their data went
+      // into the stores above) before any thread passes the barrier
+      __syncthreads();
+      if (tid == 0)
+        __hip_atomic_store(upload_done + blockIdx.x, upload_value, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+    }
     return;
   }
   if (num_slots == nullptr) return;  // host-bound plan: nothing to bind
@@ -427,8 +439,8 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
   // (st_search_plan_upload_source), and the width census of a device-bound
   // plan: one launch, ahead of the search on the same stream.
   const uint64_t upload_bytes = plan->upload_source != nullptr ? plan->blob.size() : 0;
-  const uint32_t upload_groups = static_cast<uint32_t>(
-      (upload_bytes + 16ull * kBindThreads * kUploadPerThread - 1) / (16ull * kBindThreads * kUploadPerThread));
+  const uint32_t upload_groups =
+      static_cast<uint32_t>((upload_bytes + kUploadGroupBytes - 1) / kUploadGroupBytes);
   if (upload_bytes != 0 || plan->device_bind) {
     char* dev = const_cast<char*>(blob);
     // The visiting order is needed by batches outside the quad-lane path
@@ -443,6 +455,9 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
     hipLaunchKernelGGL(bind_prologue_kernel, dim3(upload_groups + (db ? 1 : 0)), dim3(kBindThreads), 0,
                        stream, static_cast<const uint8_t*>(plan->upload_device_src),
                        reinterpret_cast<uint8_t*>(dev), static_cast<int64_t>(upload_bytes), upload_groups,
+                       upload_bytes != 0 ? static_cast<unsigned long long*>(plan->upload_signal_device)
+                                         : nullptr,
+                       static_cast<unsigned long long>(plan->upload_signal_value),
                        bundle_b_offsets, num_bundles,
                        db ? reinterpret_cast<uint32_t*>(dev + plan->off_num_slots) : nullptr,
                        db ? reinterpret_cast<int64_t*>(dev + plan->off_slot_width) : nullptr,
@@ -569,6 +584,31 @@ extern "C" int st_search_plan_upload_source(st_search_plan* plan, const void* pi
     ST_CHECK(reinterpret_cast<uintptr_t>(dev) % 16 == 0, "the pinned plan buffer must be 16-byte aligned");
     plan->upload_source = pinned_host;
     plan->upload_device_src = dev;
+  });
+}
+
+extern "C" int64_t st_search_plan_upload_groups(const st_search_plan* plan) {
+  if (plan == nullptr || plan->upload_source == nullptr) return 0;
+  return static_cast<int64_t>((plan->blob.size() + st::kUploadGroupBytes - 1) / st::kUploadGroupBytes);
+}
+
+extern "C" int st_search_plan_upload_signal(st_search_plan* plan, void* pinned_words,
+                                            uint64_t value) {
+  using namespace st;
+  return guarded([&] {
+    ST_CHECK(plan != nullptr, "plan is null");
+    if (pinned_words == nullptr) {
+      plan->upload_signal_device = nullptr;
+      return;
+    }
+    ST_CHECK(reinterpret_cast<uintptr_t>(pinned_words) % 8 == 0,
+             "the pinned signal words must be 8-byte aligned");
+    void* dev = nullptr;
+    const hipError_t e = hipHostGetDevicePointer(&dev, pinned_words, 0);
+    ST_CHECK(e == hipSuccess, "the signal words are not pinned, device-accessible host memory (",
+             hipGetErrorString(e), ")");
+    plan->upload_signal_device = dev;
+    plan->upload_signal_value = value;
   });
 }
 

@@ -254,6 +254,11 @@ struct st_search_plan {
   // from this pinned host buffer (device address upload_device_src)
   const void* upload_source = nullptr;
   const void* upload_device_src = nullptr;
+  // set by st_search_plan_upload_signal: after copying its part of the blob
+  // each upload workgroup g stores upload_signal_value to
+  // upload_signal_device[g] (pinned host memory, device address)
+  void* upload_signal_device = nullptr;
+  uint64_t upload_signal_value = 0;
   // work table of the wide-bundle kernel (0: none), set by either binding
   uint64_t off_wide = 0;
   // host binding: every bundle has a slot and every slot width is wide

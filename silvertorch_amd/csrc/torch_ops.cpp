@@ -18,8 +18,12 @@
 #include <Python.h>
 #include <torch/library.h>
 
+#include <hip/hip_runtime_api.h>
+
 #include <algorithm>
 #include <cstring>
+#include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -142,6 +146,81 @@ struct PlanHolder {
   ~PlanHolder() { st_search_plan_destroy(p); }
 };
 
+// Pinned ring the search ops upload their plans from: kRingSlots slots of
+// kRingSlotBytes per device, allocated on first use and kept for the
+// process.  The search call's first kernel copies the plan out of its slot,
+// and each of its upload workgroups then stores the slot's use number to one
+// of the slot's signal words (st_search_plan_upload_signal): a slot is free
+// again once its words hold its last use number, with no event on the stream
+// (an event record costs the stream a few microseconds per call).  A plan
+// larger than a slot, or a call that finds every slot still in use, takes a
+// block of torch's pinned host allocator and its event instead.  A slot whose
+// call failed before its copy ran stays in use.
+constexpr int kRingSlots = 16;
+constexpr int64_t kRingSlotBytes = 256 << 10;
+constexpr int64_t kRingGroupBytes = 64 << 10;  // blob bytes per upload workgroup
+constexpr int kRingGroups = static_cast<int>(kRingSlotBytes / kRingGroupBytes);
+
+struct PlanRing {
+  std::mutex mu;
+  bool ready = false, failed = false;
+  uint8_t* data = nullptr;   // kRingSlots * kRingSlotBytes
+  uint64_t* words = nullptr; // kRingSlots * kRingGroups signal words
+  uint64_t last[kRingSlots] = {};  // use number of each slot's last upload
+  int groups[kRingSlots] = {};     // its upload workgroups
+  uint64_t uses = 0;
+  int next = 0;
+};
+
+PlanRing& plan_ring(int device) {
+  static std::mutex mu;
+  static std::vector<std::unique_ptr<PlanRing>> rings;
+  std::lock_guard<std::mutex> lk(mu);
+  if (static_cast<int>(rings.size()) <= device) rings.resize(device + 1);
+  if (!rings[device]) rings[device] = std::make_unique<PlanRing>();
+  return *rings[device];
+}
+
+// A free slot (its data pointer, signal words and new use number), or -1.
+int ring_acquire(PlanRing& r, int groups, uint8_t** data, uint64_t** words, uint64_t* use) {
+  std::lock_guard<std::mutex> lk(r.mu);
+  if (!r.ready && !r.failed) {
+    void* d = nullptr;
+    void* w = nullptr;
+    // fine-grained (coherent) host memory: the device reads each slot's new
+    // bytes over PCIe, not a cached copy of the slot's previous plan, and the
+    // host sees the signal words as the device stores them
+    if (hipHostMalloc(&d, kRingSlots * kRingSlotBytes, hipHostMallocCoherent) == hipSuccess &&
+        hipHostMalloc(&w, kRingSlots * kRingGroups * sizeof(uint64_t), hipHostMallocCoherent) ==
+            hipSuccess) {
+      std::memset(w, 0, kRingSlots * kRingGroups * sizeof(uint64_t));
+      r.data = static_cast<uint8_t*>(d);
+      r.words = static_cast<uint64_t*>(w);
+      r.ready = true;
+    } else {
+      if (d != nullptr) (void)hipHostFree(d);
+      (void)hipGetLastError();  // the fallback path serves every call
+      r.failed = true;
+    }
+  }
+  if (!r.ready) return -1;
+  for (int t = 0; t < kRingSlots; ++t) {
+    const int i = (r.next + t) % kRingSlots;
+    bool free = true;
+    for (int g = 0; g < r.groups[i]; ++g)
+      free &= __atomic_load_n(r.words + i * kRingGroups + g, __ATOMIC_ACQUIRE) >= r.last[i];
+    if (!free) continue;
+    r.next = (i + 1) % kRingSlots;
+    r.last[i] = ++r.uses;
+    r.groups[i] = groups;
+    *data = r.data + i * kRingSlotBytes;
+    *words = r.words + i * kRingGroups;
+    *use = r.last[i];
+    return i;
+  }
+  return -1;
+}
+
 // Checks, plan compilation, width binding and plan upload shared by the
 // search ops.
 struct PreparedSearch {
@@ -198,6 +277,22 @@ void prepare_search(PreparedSearch& ps, const Tensor& bloom_index_in,
   // this call's); the allocator reuses the pinned block only after that
   // stream has passed the call.
   const int64_t blob_bytes = st_search_plan_blob_bytes(ps.plan.p);
+  if (blob_bytes <= kRingSlotBytes) {
+    const int groups = static_cast<int>((blob_bytes + kRingGroupBytes - 1) / kRingGroupBytes);
+    uint8_t* slot = nullptr;
+    uint64_t* words = nullptr;
+    uint64_t use = 0;
+    if (ring_acquire(plan_ring(ps.index.device().index()), groups, &slot, &words, &use) >= 0) {
+      std::memcpy(slot, st_search_plan_blob(ps.plan.p), blob_bytes);
+      check_st(st_search_plan_upload_source(ps.plan.p, slot), "bloom_index_search_batch");
+      TORCH_CHECK(st_search_plan_upload_groups(ps.plan.p) == groups,
+                  "bloom_index_search_batch: plan upload group count mismatch");
+      check_st(st_search_plan_upload_signal(ps.plan.p, words, use), "bloom_index_search_batch");
+      ps.blob = at::empty({st_search_plan_device_bytes(ps.plan.p)},
+                          at::TensorOptions().dtype(at::kByte).device(ps.index.device()));
+      return;
+    }
+  }
   at::HostAllocator* host_alloc = at::getHostAllocator(at::kCUDA);
   at::DataPtr host = host_alloc->allocate(static_cast<size_t>(blob_bytes));
   std::memcpy(host.get(), st_search_plan_blob(ps.plan.p), blob_bytes);

@@ -437,6 +437,48 @@ def test_search_copies_its_plan_from_pinned_memory(bind):
         np.testing.assert_array_equal(got, O.unpack_bool(want) if bool_mask else want)
 
 
+def test_upload_signal_words_hold_the_value_after_the_copy():
+    """st_search_plan_upload_signal: a plan of 700 queries (a blob over
+    64 KB, so several upload workgroups) copied by the search call from
+    pinned memory; after the call each group's word holds the value, the
+    words past the group count keep their fill, and the output equals the
+    oracle's.  The torch ops reuse their pinned plan slots on these words."""
+    from silvertorch_amd import capi
+    from silvertorch_amd import synthetic as S
+
+    cspec, _ = S.CONFIGS["cfg2"]
+    docs = 20_000
+    corp = S.make_corpus(cspec, seed=5, num_docs=docs)
+    queries = S.make_queries(cspec, S.QuerySpec(700, "flat", 2, 6), seed=5)
+    index, bbo = H.build(corp.feature_ids, corp.feature_offsets, corp.feature_values, cspec.b_multiplier, cspec.k)
+    pd, po = _plans(queries, cspec.hash_k)
+    want = O.search_packed(index, bbo, pd, po, cspec.k, cspec.hash_k)
+    L = capi.lib()
+    plan = capi.SearchPlan(bytes(pd.tobytes()), po, cspec.k, cspec.hash_k)
+    nb = len(bbo) - 1
+    plan.prepare_device_binding(nb)
+    blob = plan.blob()
+    pinned = torch.frombuffer(bytearray(blob), dtype=torch.uint8).pin_memory()
+    capi.check(L.st_search_plan_upload_source(plan.handle, pinned.data_ptr()))
+    groups = L.st_search_plan_upload_groups(plan.handle)
+    H.note(f"[upload signal] blob={len(blob)} bytes groups={groups}")
+    assert groups == (len(blob) + 65535) // 65536 and groups >= 2
+    words = torch.full((groups + 2,), 7, dtype=torch.long).pin_memory()
+    value = 0x0123456789ABCDEF
+    capi.check(L.st_search_plan_upload_signal(plan.handle, words.data_ptr(), value))
+    blob_d = torch.full((plan.device_bytes,), 0xEE, dtype=torch.uint8, device="cuda")
+    idx_d = torch.as_tensor(index).cuda()
+    bbo_d = torch.as_tensor(bbo).cuda()
+    out = torch.empty((plan.num_queries, nb * 32), dtype=torch.long, device="cuda")
+    capi.check(L.st_bloom_index_search_batch(idx_d.data_ptr(), idx_d.numel(), bbo_d.data_ptr(), nb, plan.handle,
+                                             blob_d.data_ptr(), 0, out.data_ptr(),
+                                             torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert words[:groups].tolist() == [value] * groups
+    assert words[groups:].tolist() == [7, 7]
+    np.testing.assert_array_equal(out.cpu().numpy(), want)
+
+
 @pytest.mark.timeout(600)
 def test_more_distinct_widths_than_the_census_holds():
     """2100 bundles of 2100 distinct widths (1 .. 2102 rows: staged, column-
