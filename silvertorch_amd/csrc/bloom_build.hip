@@ -356,8 +356,6 @@ __global__ __launch_bounds__(kBuildThreads) void scatter_kernel(ScatterArgs a) {
                                 : doc1 - doc0;
     const uint32_t c0 = static_cast<uint32_t>(dlo >> 6);
     const int64_t tw = lc < 0 ? 0 : (b << lc);
-    for (int64_t w = tid; w < tw; w += kBuildThreads) tile[w] = 0;
-    __syncthreads();
     const int64_t slot_lo = dlo * F, slot_hi = max<int64_t>(dhi, dlo) * F;
     // the offsets a group reads: its slot's two and the group's two bounds
     struct GroupOffsets {
@@ -375,7 +373,10 @@ __global__ __launch_bounds__(kBuildThreads) void scatter_kernel(ScatterArgs a) {
       o.g1 = offs[min<int64_t>(g + kBuildThreads, slot_hi)];
       return o;
     };
+    // the first group's offsets are in flight while the tile is cleared
     GroupOffsets next = load_group(b > 0 ? slot_lo : slot_hi);
+    for (int64_t w = tid; w < tw; w += kBuildThreads) tile[w] = 0;
+    __syncthreads();
     for (int64_t g = slot_lo; b > 0 && g < slot_hi; g += kBuildThreads) {
       const GroupOffsets cur = next;
       next = load_group(g + kBuildThreads);
