@@ -61,6 +61,9 @@ def parse_args():
     p.add_argument("--no-topk", action="store_true", help="skip the cfg5 filter + top-k leg")
     p.add_argument("--no-build4", action="store_true", help="skip the cfg4 build-throughput leg")
     p.add_argument("--no-cfg3", action="store_true", help="skip the cfg3 wide-bundle search leg")
+    p.add_argument("--probe-pattern", action="store_true",
+                   help="only time the search kernel's HBM access pattern without its evaluation "
+                        "(silvertorch_amd/libst_probe.so) next to the search kernel, on cfg2's index")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 512 MiB device-to-device copy, 5 times: the known-size "
                         "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE readings")
@@ -77,6 +80,88 @@ def calibrate_copy():
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n, "launches": 5}), flush=True)
+
+
+def probe_pattern():
+    """The ceiling of the search kernel's access pattern on this part: the
+    probe kernel (csrc/pattern_probe.hip) moves cfg2's index through LDS tiles
+    and writes the packed output's 256-byte pieces with nothing between them,
+    with one or two tiles of loads in flight, and its loads or stores alone;
+    the search kernel itself is timed the same way (host-bound plan, HIP
+    events on the launching stream).  Prints one JSON line."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    import silvertorch_amd.ops._load_ops  # noqa: F401
+    from silvertorch_amd import capi
+    from silvertorch_amd import synthetic as S
+
+    st = torch.ops.st
+    dev = torch.device("cuda:0")
+    cspec, qspec = S.CONFIGS["cfg2"]
+    corp = S.make_corpus(cspec, seed=0)
+    queries = S.make_queries(cspec, qspec, seed=0)
+    bi, bo = st.bloom_index_build(torch.from_numpy(corp.feature_ids).to(dev),
+                                  torch.from_numpy(corp.feature_offsets).to(dev),
+                                  torch.from_numpy(corp.feature_values).to(dev), cspec.b_multiplier, cspec.k)
+    del corp
+    _, (pd, po) = st.parse_expression_query_batch(queries, torch.ones(1, dtype=torch.long), cspec.hash_k, True, 5)
+    Q, nb = len(queries), bo.numel() - 1
+    out = torch.empty((Q, nb * 32), dtype=torch.long, device=dev)
+    grid = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.empty(grid * 1024 * 16, dtype=torch.uint8, device=dev)
+    P = ctypes.CDLL(str(ROOT / "silvertorch_amd" / "libst_probe.so"))
+    P.st_probe_search_pattern.restype = ctypes.c_int
+    P.st_probe_search_pattern.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+                                          ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    P.st_probe_last_error.restype = ctypes.c_char_p
+    stream = torch.cuda.current_stream()
+    L = capi.lib()
+    plan = capi.SearchPlan(pd.numpy().tobytes(), po.numpy(), cspec.k, cspec.hash_k)
+    plan.bind_widths(bo.cpu().numpy())
+    blob = torch.frombuffer(bytearray(plan.blob()), dtype=torch.uint8).to(dev)
+
+    def run(fn, reps=20, warm=3):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for i in range(reps + warm):
+            if i >= warm:
+                ev[i - warm][0].record(stream)
+            fn()
+            if i >= warm:
+                ev[i - warm][1].record(stream)
+        torch.cuda.synchronize()
+        return float(np.median([a.elapsed_time(b) * 1e3 for a, b in ev]))
+
+    index_bytes, out_bytes = bi.numel() * 8, out.numel() * 8
+    res = {"probe": "search access pattern", "workload": f"cfg2: {nb} bundles, {Q} query rows",
+           "index_bytes": index_bytes, "output_bytes": out_bytes, "hbm_peak_gbs": HBM_PEAK_GBS, "runs": []}
+    for depth in (1, 2):
+        for mode, name, nbytes in ((0, "loads and stores", index_bytes + out_bytes), (1, "loads only", index_bytes),
+                                   (2, "stores only", out_bytes)):
+            def fn(depth=depth, mode=mode):
+                rc = P.st_probe_search_pattern(bi.data_ptr(), bi.numel(), bo.data_ptr(), nb, Q, out.data_ptr(),
+                                               sink.data_ptr(), depth, mode, grid, ctypes.c_void_p(stream.cuda_stream))
+                if rc != 0:
+                    raise RuntimeError(P.st_probe_last_error().decode())
+            us = run(fn)
+            res["runs"].append({"kernel": "pattern_probe_kernel", "tiles_in_flight": depth, "mode": name,
+                                "median_us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3,
+                                "frac": nbytes / us / 1e3 / HBM_PEAK_GBS})
+            log(f"probe: {depth} tile(s) in flight, {name}: {us:.1f} us, {nbytes / us / 1e3:.0f} GB/s")
+
+    def search():
+        capi.check(L.st_bloom_index_search_batch(bi.data_ptr(), bi.numel(), bo.data_ptr(), nb, plan.handle,
+                                                 blob.data_ptr(), 0, out.data_ptr(), stream.cuda_stream))
+    us = run(search)
+    nbytes = index_bytes + out_bytes
+    res["runs"].append({"kernel": "bloom_search_kernel", "mode": "search (packed, host-bound plan)",
+                        "median_us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3,
+                        "frac": nbytes / us / 1e3 / HBM_PEAK_GBS})
+    log(f"search kernel: {us:.1f} us, {nbytes / us / 1e3:.0f} GB/s")
+    print(json.dumps(res), flush=True)
 
 
 def host_cpu() -> tuple[str, int]:
@@ -679,6 +764,9 @@ def main():
     args = parse_args()
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.probe_pattern:
+        probe_pattern()
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",

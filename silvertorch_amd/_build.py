@@ -24,6 +24,9 @@ CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libsilvertorch_hip.so"
 EXT = PKG / "_C.so"
+# Measurement probe (bench.py --probe-pattern): the search kernel's memory
+# access pattern without its evaluation; not part of the product library.
+PROBE = PKG / "libst_probe.so"
 
 ARCH = os.environ.get("ST_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -137,12 +140,19 @@ def build_extension() -> Path:
     return EXT
 
 
+def build_probe() -> Path:
+    _run([HIPCC, *HIP_FLAGS, "-shared", str(CSRC / "pattern_probe.hip"), "-o", str(PROBE) + ".tmp"])
+    os.replace(str(PROBE) + ".tmp", PROBE)
+    return PROBE
+
+
 def build(jobs: int = os.cpu_count() or 8) -> None:
     build_library(jobs)
     build_extension()
+    build_probe()
 
 
 if __name__ == "__main__":
     INCREMENTAL = "--incremental" in sys.argv[1:]
     build()
-    print(f"built {LIB.relative_to(ROOT)} and {EXT.relative_to(ROOT)}")
+    print(f"built {LIB.relative_to(ROOT)}, {EXT.relative_to(ROOT)} and {PROBE.relative_to(ROOT)}")

@@ -481,10 +481,10 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
     }
   }
   // Wide bundles (kSearchTileRows < b <= kWideRows, width-bound) have their
-  // literal streams evaluated by the column-slice kernel, in packed mode;
-  // the per-batch kernels then skip those streams there.  With host-bound
-  // widths the launch is decided here; with device binding the kernel
-  // returns at once when no slot width is wide.
+  // literal streams evaluated by the column-slice phase, in packed mode; the
+  // per-batch kernels then skip those streams there.  With host-bound widths
+  // the phase is decided here; with device binding it ends at once when no
+  // slot width is wide.
   WideFn wide_fn = nullptr;
   if (bound && mode == kOutPacked && plan->off_wide != 0) {
     wide_fn = select_wide_kernel(plan->k_eff);
@@ -494,6 +494,36 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
       if (!any) wide_fn = nullptr;
     }
   }
+  // Which batches launch the per-batch kernel; the last of them also runs
+  // the wide-bundle phase (no launch of its own then).
+  std::vector<uint32_t> wide_flags(plan->batches.size(), 0u);
+  std::vector<char> launched(plan->batches.size(), 0);
+  size_t last_launch = plan->batches.size();
+  for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
+    const SearchBatch& bt = plan->batches[bi];
+    if (bt.generic) continue;
+    // 2 tells the kernel that every program of the batch is in the stream,
+    // so that wide bundles need nothing from it
+    if (wide_fn != nullptr) {
+      const auto* wo = reinterpret_cast<const uint32_t*>(plan->blob.data() + bt.off_wave);
+      const auto* sk = reinterpret_cast<const uint32_t*>(plan->blob.data() + bt.off_stream_skip);
+      bool all = true;
+      for (int w = 0; w < kSearchWaves; ++w) all &= wo[w + 1] - wo[w] == sk[w];
+      wide_flags[bi] = all ? 2u : 1u;
+    }
+    // Nothing for the per-batch kernel when the wide-bundle phase covers
+    // every bundle (known here with host-bound widths), unless it carries
+    // that phase.
+    launched[bi] = !(wide_flags[bi] == 2 && !plan->device_bind && plan->all_wide);
+    if (launched[bi]) last_launch = bi;
+  }
+  if (wide_fn != nullptr && last_launch == plan->batches.size()) {
+    // the last streamed batch launches only to carry the wide phase
+    for (size_t bi = 0; bi < plan->batches.size(); ++bi)
+      if (!plan->batches[bi].generic) last_launch = bi;
+    if (last_launch < plan->batches.size()) launched[last_launch] = 1;
+  }
+  const bool wide_in_search = wide_fn != nullptr && last_launch < plan->batches.size();
   for (size_t bi = 0; bi < plan->batches.size(); ++bi) {
     const SearchBatch& bt = plan->batches[bi];
     if (bt.generic) {
@@ -503,19 +533,11 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
                            counts, num_docs, stream);
       continue;
     }
-    // 2 tells the kernel that every program of the batch is in the stream,
-    // so that wide bundles need nothing from it
-    uint32_t wide_flag = 0;
-    if (wide_fn != nullptr) {
-      const auto* wo = reinterpret_cast<const uint32_t*>(plan->blob.data() + bt.off_wave);
-      const auto* sk = reinterpret_cast<const uint32_t*>(plan->blob.data() + bt.off_stream_skip);
-      bool all = true;
-      for (int w = 0; w < kSearchWaves; ++w) all &= wo[w + 1] - wo[w] == sk[w];
-      wide_flag = all ? 2u : 1u;
-    }
-    // Nothing for the per-batch kernel when the wide-bundle kernel covers
-    // every bundle (known here with host-bound widths).
-    if (wide_flag == 2 && !plan->device_bind && plan->all_wide) continue;
+    if (!launched[bi]) continue;
+    const bool carry_wide = wide_in_search && bi == last_launch;
+    // 3: a launch that only carries the wide phase (host-bound, all wide)
+    const uint32_t wide_flag =
+        carry_wide && wide_flags[bi] == 2 && !plan->device_bind && plan->all_wide ? 3u : wide_flags[bi];
     // Quad-lane stream evaluation when the batch's literal stream fits the
     // LDS area after the tile and a stream step holds whole quads (k <= 7).
     const int kk = std::max(plan->k_eff, 1);
@@ -538,19 +560,19 @@ void launch_search(const int64_t* bloom_index, int64_t bloom_index_numel,
         bound ? bt.stream_words : 0u, bound ? bt.stream_masks : 0u, bt.num_terms,
         static_cast<int32_t>(plan->hash_k),
         num_bundles * 32, out, counts, num_docs, wide_flag,
-        plan->device_bind ? at(plan->off_num_slots) : nullptr);
+        plan->device_bind ? at(plan->off_num_slots) : nullptr,
+        carry_wide ? at(plan->off_wide) : nullptr,
+        carry_wide ? at(plan->off_bundle_order) : nullptr,
+        carry_wide ? reinterpret_cast<const uint32_t*>(blob) : nullptr);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
       throw Error(ST_ERR_HIP, cat("search kernel launch failed: ", hipGetErrorString(e)));
   }
-  if (wide_fn != nullptr) {
+  if (wide_fn != nullptr && !wide_in_search) {
     hipLaunchKernelGGL(wide_fn, dim3(grid), dim3(kSearchThreads), 0, stream, bloom_index,
                        bloom_index_numel, bundle_b_offsets, num_bundles,
                        at(plan->off_bundle_slot), at(plan->off_bundle_order),
                        plan->device_bind ? at(plan->off_num_slots) : nullptr,
-                       plan->device_bind
-                           ? reinterpret_cast<const int64_t*>(blob + plan->off_slot_width)
-                           : nullptr,
                        reinterpret_cast<const uint32_t*>(blob), at(plan->off_wide),
                        num_bundles * 32, static_cast<int64_t*>(out));
     hipError_t e = hipGetLastError();

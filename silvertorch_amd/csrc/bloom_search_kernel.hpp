@@ -131,22 +131,24 @@ struct PartFilter {
 };
 
 // Issues this thread's share of the loads of the rows [start, start + b)
-// into `pre` (nothing when the bundle is wider than the LDS tile).
+// into `pre` (nothing when the bundle is wider than the LDS tile).  The
+// bound is one uniform limit on the 16-byte chunks (of a bundle whose rows
+// pass the end of the index, which only malformed offsets describe, the
+// chunks inside the index are loaded), so the per-load test is a 32-bit
+// compare.
 __device__ __forceinline__ void prefetch_tile(const SearchArgs& a, int64_t start, int64_t b,
                                               u32x4 (&pre)[kPrefetch]) {
   const int tid = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < kPrefetch; ++i) pre[i] = u32x4{0, 0, 0, 0};
-  if (b > kSearchTileRows) return;
-  const int64_t chunks = b * 16;
+  if (b > kSearchTileRows || start < 0) return;
+  const int64_t avail = (a.index_numel - start * 32) / 2;  // whole chunks left in the index
+  const int lim = static_cast<int>(b * 16 < avail ? b * 16 : (avail > 0 ? avail : 0));
   const u32x4* src = reinterpret_cast<const u32x4*>(a.index + start * 32);
 #pragma unroll
   for (int i = 0; i < kPrefetch; ++i) {
     const int c = tid + i * kSearchThreads;
-    // chunk c holds words start*32 + 2c and + 2c + 1
-    if (c < chunks && start * 32 + 2 * c + 1 < a.index_numel) {
-      pre[i] = __builtin_nontemporal_load(src + c);
-    }
+    if (c < lim) pre[i] = __builtin_nontemporal_load(src + c);
   }
 }
 
@@ -909,6 +911,14 @@ __device__ __forceinline__ void eval_queries(const SearchArgs& a, const RowSourc
   }
 }
 
+template <int K>
+__device__ __forceinline__ void wide_phase(
+    u32x4* tile, const int64_t* __restrict__ index, int64_t index_numel,
+    const int64_t* __restrict__ bundle_offsets, int64_t num_bundles,
+    const uint32_t* __restrict__ bundle_slot, const uint32_t* __restrict__ bundle_order,
+    const uint32_t* __restrict__ blob, const uint32_t* __restrict__ table, int64_t out_cols,
+    int64_t* __restrict__ out);
+
 // The arrays arrive as separate __restrict__ parameters (not inside
 // SearchArgs) so the compiler can prove the output stores never alias the
 // program and offset arrays and fetch those with scalar loads.
@@ -926,11 +936,14 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     uint32_t stream_masks,
     uint32_t num_terms, int32_t hash_k,
     int64_t out_cols, void* __restrict__ out, int64_t* __restrict__ counts, int64_t num_docs,
-    uint32_t wide_skip, const uint32_t* __restrict__ census) {
-  // wide_skip == 2: the wide-bundle kernel evaluates every program of this
+    uint32_t wide_skip, const uint32_t* __restrict__ census,
+    const uint32_t* __restrict__ wide_table, const uint32_t* __restrict__ wide_order,
+    const uint32_t* __restrict__ blob) {
+  // wide_skip == 2: the wide-bundle phase evaluates every program of this
   // batch on wide bundles; census[1] (device binding) says every bundle is
-  // one, so nothing is left for this launch
-  if (wide_skip == 2 && census != nullptr && as_const(census)[1] != 0u) return;
+  // one, so the search phase has nothing to do; 3: the host knows so
+  const bool search_phase =
+      wide_skip != 3 && !(wide_skip == 2 && census != nullptr && as_const(census)[1] != 0u);
   SearchArgs a;
   a.index = index;
   a.index_numel = index_numel;
@@ -1020,7 +1033,8 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
   };
   u32x4 pre[kPrefetch];
   u32x4 spre[kQuad ? kStreamPrefetch : 1];
-  BundleMeta cur = visit(0), nxt = visit(1);
+  const BundleMeta none{-1, 0, 0, kNoWidthSlot, 0, 1};
+  BundleMeta cur = search_phase ? visit(0) : none, nxt = search_phase ? visit(1) : none;
   if (cur.bundle >= 0) {
     prefetch_tile(a, cur.start, cur.b, pre);
     if (quad_bundle(cur)) prefetch_stream(cur, spre);
@@ -1178,6 +1192,15 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
     cur = nxt;
     nxt = after;
   }
+  // The wide-bundle phase (packed output, k <= 7) of the call's last search
+  // launch: skipped at once when the census found no wide slot width.
+  if constexpr (kOut == kOutPacked && K <= 7) {
+    if (wide_table != nullptr && (census == nullptr || as_const(census)[2] != 0u)) {
+      __syncthreads();  // the search phase's readers are done with the LDS
+      wide_phase<K>(reinterpret_cast<u32x4*>(tile), index, index_numel, bundle_offsets, num_bundles,
+                    bundle_slot, wide_order, blob, wide_table, out_cols, static_cast<int64_t*>(out));
+    }
+  }
 }
 
 // ------------------------------------------------ wide bundles, column slices
@@ -1200,6 +1223,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kWidePieces = kWideSliceBytes / 16;  // u32x4 per slice row
 constexpr int kWidePrefetch = kWideRows * kWidePieces / kSearchThreads;
 static_assert(kWidePrefetch * kSearchThreads == kWideRows * kWidePieces, "slice split");
+static_assert((kWideRows + 2) * kWidePieces <= (kSearchTileRows + 2) * 16,
+              "the search kernel's LDS tile holds the wide phase's slice tile");
 
 // LDS pointers (address space 3): reads through them are ds_read, and a
 // byte offset added to one is a 32-bit add.
@@ -1349,18 +1374,17 @@ __device__ __forceinline__ void wide_eval_group(const char* stream, const ST_CON
 // 128-byte index line are read by the same XCD at about the same time;
 // otherwise workgroup w takes bundles w, w + grid, ... with all slices.  Each
 // wave issues its share of the next slice's loads when it has evaluated the
-// current one.
-// `num_slots` (device binding; nullptr when the host decided to launch) lets
-// the kernel return at once when no slot width is wide (its word 2).
+// current one.  `tile` is the workgroup's LDS (kWideRows + 2 slice rows); the
+// phase runs as a kernel of its own (bloom_wide_kernel) or after the search
+// phase of a packed search launch (bloom_search_kernel), saving the call a
+// launch.
 template <int K>
-__global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
-    const int64_t* __restrict__ index, int64_t index_numel,
+__device__ __forceinline__ void wide_phase(
+    u32x4* tile, const int64_t* __restrict__ index, int64_t index_numel,
     const int64_t* __restrict__ bundle_offsets, int64_t num_bundles,
     const uint32_t* __restrict__ bundle_slot, const uint32_t* __restrict__ bundle_order,
-    const uint32_t* __restrict__ num_slots, const int64_t* __restrict__ slot_width,
     const uint32_t* __restrict__ blob, const uint32_t* __restrict__ table, int64_t out_cols,
     int64_t* __restrict__ out) {
-  __shared__ u32x4 tile[(kWideRows + 2) * kWidePieces];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const uint32_t wave = uniform(tid >> 6);
@@ -1369,8 +1393,6 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
   const ST_CONST uint32_t* border = as_const(bundle_order);
   const ST_CONST uint32_t* tab = as_const(table);
 
-  // the census's word: some slot width is wide
-  if (num_slots != nullptr && as_const(num_slots)[2] == 0u) return;
   if (tid < 2 * kWidePieces) {
     const uint32_t fill = tid < kWidePieces ? ~0u : 0u;
     tile[kWideOnesRow * kWidePieces + tid] = u32x4{fill, fill, fill, fill};
@@ -1460,11 +1482,28 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
   }
 }
 
+// The wide-bundle evaluation as a launch of its own (when no search launch
+// of the call carries it).  `num_slots` (device binding; nullptr when the
+// host decided to launch) lets it return at once when no slot width is wide
+// (its word 2).
+template <int K>
+__global__ __launch_bounds__(kSearchThreads) void bloom_wide_kernel(
+    const int64_t* __restrict__ index, int64_t index_numel,
+    const int64_t* __restrict__ bundle_offsets, int64_t num_bundles,
+    const uint32_t* __restrict__ bundle_slot, const uint32_t* __restrict__ bundle_order,
+    const uint32_t* __restrict__ num_slots, const uint32_t* __restrict__ blob,
+    const uint32_t* __restrict__ table, int64_t out_cols, int64_t* __restrict__ out) {
+  __shared__ u32x4 tile[(kWideRows + 2) * kWidePieces];
+  if (num_slots != nullptr && as_const(num_slots)[2] == 0u) return;
+  wide_phase<K>(tile, index, index_numel, bundle_offsets, num_bundles, bundle_slot, bundle_order,
+                blob, table, out_cols, out);
+}
+
 }  // namespace
 
 using WideFn = void (*)(const int64_t*, int64_t, const int64_t*, int64_t, const uint32_t*,
-                        const uint32_t*, const uint32_t*, const int64_t*, const uint32_t*,
-                        const uint32_t*, int64_t, int64_t*);
+                        const uint32_t*, const uint32_t*, const uint32_t*, const uint32_t*, int64_t,
+                        int64_t*);
 // The wide-bundle kernel of one K (nullptr for K > 7), defined in the
 // translation unit compiled with ST_SEARCH_K = K.
 template <int K>
@@ -1486,7 +1525,8 @@ using KernelFn = void (*)(const int64_t*, int64_t, const int64_t*, int64_t,
                           const uint32_t*, const uint32_t*, const uint32_t*, uint32_t,
                           const uint32_t*, const uint32_t*, uint32_t, uint32_t, uint32_t,
                           uint32_t, int32_t,
-                          int64_t, void*, int64_t*, int64_t, uint32_t, const uint32_t*);
+                          int64_t, void*, int64_t*, int64_t, uint32_t, const uint32_t*,
+                          const uint32_t*, const uint32_t*, const uint32_t*);
 
 // The kernels of one K (all output modes; the quad instance evaluates the
 // literal stream in quad lanes and needs a stream that fits the LDS and k <= 7),

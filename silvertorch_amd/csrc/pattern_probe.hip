@@ -1,0 +1,159 @@
+// Measurement probe, not part of the search path: the HBM access pattern of
+// the batched search kernel with its evaluation taken out, so that the
+// bandwidth this read/write mix reaches on the part can be measured on its
+// own (bench.py --probe-pattern).  Built into libst_probe.so, a library of
+// its own; nothing in the product calls it.
+//
+// The grid is the search kernel's: one 1024-thread workgroup per CU walks
+// bundles w, w + grid, ... in index order.  Per bundle it moves the bundle's
+// rows (b x 256 bytes, b <= 512) from HBM into an LDS tile through registers
+// with 16-byte non-temporal loads, and writes 256 bytes per query row of the
+// packed output (Q rows of 256 * num_bundles bytes), 16 bytes per lane, four
+// query rows per wave instruction: the search kernel's loads and stores with
+// nothing between them.  DEPTH register buffers are in flight: with DEPTH 1
+// the next bundle's loads go out when the current tile is in LDS (the search
+// kernel's form, whose registers hold one tile), with DEPTH 2 two bundles
+// ahead.  MODE 1 drops the stores (a 16-byte sink per workgroup keeps the
+// loads live), MODE 2 the loads.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#define PROBE_GLOBAL __attribute__((address_space(1)))
+
+constexpr int kThreads = 1024;
+constexpr int kTileRows = 512;
+constexpr int kPer = kTileRows * 16 / kThreads;  // u32x4 per thread per tile
+
+thread_local std::string g_error;
+
+// The tile's rows [start, start + b) from the uniform base; a bundle whose
+// rows would pass the end of the index loads nothing.
+__device__ __forceinline__ void load_tile(const u32x4* __restrict__ src, int64_t start,
+                                          int64_t b, int64_t numel, u32x4 (&pre)[kPer]) {
+  const int lim = (start + b) * 32 <= numel ? static_cast<int>(b * 16) : 0;
+  const u32x4* base = src + start * 16;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int c = static_cast<int>(threadIdx.x) + i * kThreads;
+    if (c < lim) pre[i] = __builtin_nontemporal_load(base + c);
+  }
+}
+
+template <int DEPTH, int MODE>
+__global__ __launch_bounds__(kThreads) void pattern_probe_kernel(
+    const int64_t* __restrict__ index, int64_t numel, const int64_t* __restrict__ bbo,
+    int64_t nb, int64_t Q, char* __restrict__ out, u32x4* __restrict__ sink) {
+  __shared__ u32x4 tile[(kTileRows + 2) * 16];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t grid = gridDim.x;
+  const u32x4* src = reinterpret_cast<const u32x4*>(index);
+  auto extent = [&](int64_t bnd, int64_t& start, int64_t& b) {
+    start = bbo[bnd];
+    b = bbo[bnd + 1] - start;
+    if (b < 0) b = 0;
+    if (b > kTileRows) b = kTileRows;
+  };
+  u32x4 pre[DEPTH][kPer];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    const int64_t bnd = blockIdx.x + d * grid;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) pre[d][i] = u32x4{1, 2, 3, 4};
+    if (MODE != 2 && bnd < nb) {
+      int64_t s, b;
+      extent(bnd, s, b);
+      load_tile(src, s, b, numel, pre[d]);
+    }
+  }
+  u32x4 acc{0, 0, 0, 0};
+  const int64_t row_bytes = nb * 256;
+  for (int64_t v = 0;; v += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int64_t bnd = blockIdx.x + (v + d) * grid;
+      if (bnd >= nb) {
+        if (MODE == 1) sink[blockIdx.x * kThreads + tid] = acc;
+        return;
+      }
+      int64_t s, b;
+      extent(bnd, s, b);
+      __syncthreads();  // the previous bundle's readers are done with the tile
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int c = tid + i * kThreads;
+        if (c < b * 16) tile[c] = pre[d][i];
+      }
+      const int64_t ahead = bnd + DEPTH * grid;
+      if (MODE != 2 && ahead < nb) {
+        int64_t s2, b2;
+        extent(ahead, s2, b2);
+        load_tile(src, s2, b2, numel, pre[d]);
+      }
+      __syncthreads();
+      const int rows = static_cast<int>(b > 0 ? b : 1);
+      if (MODE == 1) {
+        acc ^= tile[(tid * 7) % (rows * 16)];
+        continue;
+      }
+      // query rows wave * 4 + 64 j + (lane >> 4), 16 bytes per lane
+      for (int64_t q0 = wave * 4; q0 < Q; q0 += 64) {
+        const int64_t q = q0 + (lane >> 4);
+        if (q >= Q) continue;
+        const u32x4 val = tile[(static_cast<int>(q) * 16 + (lane & 15)) % (rows * 16)];
+        PROBE_GLOBAL u32x4* dst = (PROBE_GLOBAL u32x4*)(out + q * row_bytes + bnd * 256 + (lane & 15) * 16);
+        __builtin_nontemporal_store(val, dst);
+      }
+    }
+  }
+}
+
+template <int DEPTH, int MODE>
+hipError_t launch(const int64_t* index, int64_t numel, const int64_t* bbo, int64_t nb, int64_t Q,
+                  void* out, void* sink, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((pattern_probe_kernel<DEPTH, MODE>), dim3(grid), dim3(kThreads), 0, s, index,
+                     numel, bbo, nb, Q, static_cast<char*>(out), static_cast<u32x4*>(sink));
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// Runs the probe once on `stream`.  depth: 1 or 2; mode: 0 loads and stores,
+// 1 loads only, 2 stores only.  out: Q x num_bundles x 256 bytes; sink:
+// grid x 1024 x 16 bytes (mode 1).  Returns 0, or -1 with
+// st_probe_last_error() set.
+extern "C" int st_probe_search_pattern(const int64_t* index, int64_t numel,
+                                       const int64_t* bundle_b_offsets, int64_t num_bundles,
+                                       int64_t num_queries, void* out, void* sink, int depth,
+                                       int mode, int grid, void* stream) {
+  if (index == nullptr || bundle_b_offsets == nullptr || out == nullptr || sink == nullptr ||
+      num_bundles <= 0 || num_queries <= 0 || grid <= 0 || (depth != 1 && depth != 2) || mode < 0 ||
+      mode > 2) {
+    g_error = "st_probe_search_pattern: invalid arguments";
+    return -1;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  const int sel = depth * 3 + mode;
+  switch (sel) {
+    case 3: e = launch<1, 0>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
+    case 4: e = launch<1, 1>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
+    case 5: e = launch<1, 2>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
+    case 6: e = launch<2, 0>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
+    case 7: e = launch<2, 1>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
+    default: e = launch<2, 2>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
+  }
+  if (e != hipSuccess) {
+    g_error = std::string("st_probe_search_pattern: ") + hipGetErrorString(e);
+    return -1;
+  }
+  return 0;
+}
+
+extern "C" const char* st_probe_last_error() { return g_error.c_str(); }

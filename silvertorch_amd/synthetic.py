@@ -96,15 +96,23 @@ def _value_offset(spec: CorpusSpec, f: int) -> int:
     return spec.feature_offsets[f] if spec.feature_offsets else 0
 
 
-def _chunked(total: int, fill) -> None:
-    """Runs fill(chunk_index, lo, hi) over [0, total) in CHUNK pieces."""
+def _chunked(total: int, fill, progress=None, what: str = "") -> None:
+    """Runs fill(chunk_index, lo, hi) over [0, total) in CHUNK pieces; with
+    `progress`, reports each tenth of the chunks as it completes."""
     n_chunks = (total + CHUNK - 1) // CHUNK
     workers = max(1, min(16, os.cpu_count() or 1, n_chunks))
     with ThreadPoolExecutor(workers) as ex:
-        list(ex.map(lambda c: fill(c, c * CHUNK, min(total, (c + 1) * CHUNK)), range(n_chunks)))
+        futs = [ex.submit(fill, c, c * CHUNK, min(total, (c + 1) * CHUNK)) for c in range(n_chunks)]
+        step = max(1, n_chunks // 10)
+        for i, f in enumerate(futs):
+            f.result()
+            if progress is not None and ((i + 1) % step == 0 or i + 1 == n_chunks):
+                progress(f"{what}: {i + 1}/{n_chunks} chunks")
 
 
-def make_corpus(spec: CorpusSpec, seed: int = 0, num_docs: int | None = None) -> Corpus:
+def make_corpus(spec: CorpusSpec, seed: int = 0, num_docs: int | None = None, progress=None) -> Corpus:
+    """The seeded corpus of `spec` (its first `num_docs` docs); `progress`, if
+    given, is called with a short message as the generation advances."""
     n = spec.num_docs if num_docs is None else num_docs
     F = spec.num_features
     flat = np.empty(n * F, dtype=np.int64)
@@ -113,7 +121,7 @@ def make_corpus(spec: CorpusSpec, seed: int = 0, num_docs: int | None = None) ->
         flat[lo:hi] = np.random.default_rng([seed, STREAM_COUNTS, c]).integers(
             spec.count_lo, spec.count_hi + 1, hi - lo, dtype=np.int64)
 
-    _chunked(n * F, fill_counts)
+    _chunked(n * F, fill_counts, progress, "value counts")
     offsets = np.empty(n * F + 1, dtype=np.int64)
     offsets[0] = 0
     np.cumsum(flat, out=offsets[1:])
@@ -123,7 +131,7 @@ def make_corpus(spec: CorpusSpec, seed: int = 0, num_docs: int | None = None) ->
     def fill_values(c, lo, hi):
         values[lo:hi] = _draw_values(np.random.default_rng([seed, STREAM_VALUES, c]), hi - lo, spec, cdf)
 
-    _chunked(values.size, fill_values)
+    _chunked(values.size, fill_values, progress, "values")
     if spec.feature_offsets:
         feat_of_value = np.repeat(np.tile(np.arange(F), n), flat)
         values += np.asarray(spec.feature_offsets, dtype=np.int64)[feat_of_value]

@@ -14,6 +14,10 @@ tests/golden/make_golden.py full):
   ids, strictly ascending per row, each on a set bit of the reference-equal
   packed output, are therefore exactly the set bits (also through
   bloom_mask_to_ids on the packed output);
+* cfg3 (50M docs x 1,024 boolean trees with NOT, every bundle wider than
+  the LDS tile): input digests, bundle_b_offsets, the 10.7 GB bloom_index,
+  plan bytes, the 6.4 GB packed output and the per-query match counts, with
+  device-bound and host-bound plans;
 * cfg4 (100M docs, build only): input digests, bundle_b_offsets and the
   5.9 GB bloom_index;
 * cfg5's fused search + filtered top-k on a doc prefix of its corpus, its
@@ -57,7 +61,7 @@ def _corpus_on_device(cfg: str, t0: float):
     cspec, _ = S.CONFIGS[cfg]
     d = _digests()[cfg]
     H.note(f"[full] {cfg}: generating {cspec.num_docs} docs")
-    corp = S.make_corpus(cspec, seed=0)
+    corp = S.make_corpus(cspec, seed=0, progress=lambda m: H.note(f"[full] {cfg}: {m} ({time.time() - t0:.0f}s)"))
     assert corp.feature_values.size == d["num_values"], "the generator drew another corpus"
     assert S.digest(corp.feature_offsets) == d["inputs"]["offsets"], "feature_offsets differ from the reference's"
     assert S.digest(corp.feature_values) == d["inputs"]["values"], "feature_values differ from the reference's"
@@ -163,6 +167,61 @@ def _check_ids_against_mask(ids, ro, packed, num_docs):
     starts = torch.zeros(n, dtype=torch.bool, device=ids.device)
     starts[ro[:-1][counts > 0]] = True
     assert bool(((d[1:] > d[:-1]) | starts[1:]).all()), "ids of a row not strictly ascending"
+
+
+@pytest.mark.timeout(1500)
+def test_full_size_cfg3_build_and_search_vs_reference():
+    """cfg3 at full size: 50M docs x 16 features, k = 4, B_MULTIPLIER 10 (bundle
+    widths 1,600-1,920 rows: every bundle is wider than the search kernel's
+    LDS tile, so the column-slice wide-bundle phase evaluates it), 1,024
+    boolean trees with NOT.  Inputs, bundle_b_offsets, the 10.7 GB
+    bloom_index, plan bytes, the 6.4 GB packed output and every per-query
+    match count against the reference CPU ops' digests
+    (bloom_indexer.cpp:26-113, bloom_index_search.cpp:173-243); the search
+    runs through the op (device width binding), and once more from a plan
+    bound on the host through the C ABI, whose output must be the same."""
+    t0 = time.time()
+    cspec, ids, offs, vals = _corpus_on_device("cfg3", t0)
+    _, qspec = S.CONFIGS["cfg3"]
+    st = torch.ops.st
+    d = _digests()["cfg3"]
+    bi, bo = st.bloom_index_build(ids, offs, vals, cspec.b_multiplier, cspec.k)
+    torch.cuda.synchronize()
+    del ids, offs, vals
+    _check_build("cfg3", bi, bo, t0)
+
+    queries = S.make_queries(cspec, qspec, seed=0)
+    import hashlib
+
+    assert hashlib.sha256("\n".join(queries).encode()).hexdigest() == d["queries_sha256"]
+    _, (pd, po) = st.parse_expression_query_batch(queries, torch.ones(1, dtype=torch.long), cspec.hash_k, True, 5)
+    assert S.digest(pd.numpy()) == d["plans_data"] and S.digest(po.numpy()) == d["plans_offsets"], \
+        "plan bytes differ from the reference parser's"
+    packed = st.bloom_index_search_batch(bi, bo, pd, po, cspec.k, cspec.hash_k, False)
+    torch.cuda.synchronize()
+    assert list(packed.shape) == d["packed_shape"]
+    got = packed.cpu().numpy()
+    counts = S.match_counts(got, cspec.num_docs)
+    bad = [q for q, (a, b) in enumerate(zip(counts, d["match_counts"])) if a != b]
+    assert not bad, f"match counts differ from the reference's for queries {bad[:10]}"
+    assert S.digest(got) == d["packed"], "packed search output differs from the reference's"
+    del got
+    H.note(f"[full] cfg3: packed output {list(packed.shape)} of {len(queries)} trees equals the reference's "
+           f"({time.time() - t0:.0f}s)")
+
+    from silvertorch_amd import capi
+
+    plan = capi.SearchPlan(pd.numpy().tobytes(), po.numpy(), cspec.k, cspec.hash_k)
+    plan.bind_widths(bo.cpu().numpy())
+    blob = torch.frombuffer(bytearray(plan.blob()), dtype=torch.uint8).to(bi.device)
+    host_bound = torch.empty_like(packed)
+    nb = bo.numel() - 1
+    capi.check(capi.lib().st_bloom_index_search_batch(
+        bi.data_ptr(), bi.numel(), bo.data_ptr(), nb, plan.handle, blob.data_ptr(), 0, host_bound.data_ptr(),
+        torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert torch.equal(host_bound, packed), "the host-bound plan's output differs from the op's"
+    H.note(f"[full] cfg3: host-bound plan through the C ABI gives the same output ({time.time() - t0:.0f}s)")
 
 
 @pytest.mark.timeout(900)
