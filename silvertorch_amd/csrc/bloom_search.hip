@@ -132,6 +132,38 @@ __device__ __forceinline__ void for_each_width(const int64_t* bbo, int64_t nb, F
   }
 }
 
+// The bundle widths a thread visits, loaded once and kept in registers for
+// the census passes when they fit (nb <= kBindThreads * kBindChunk); the
+// passes over a larger index reload them.
+struct WidthRegs {
+  long long w[kBindChunk];
+  bool held;
+};
+
+__device__ __forceinline__ void load_widths(const int64_t* bbo, int64_t nb, WidthRegs& r) {
+  r.held = nb <= static_cast<int64_t>(kBindThreads) * kBindChunk;
+  if (!r.held) return;
+#pragma unroll
+  for (int j = 0; j < kBindChunk; ++j) {
+    const int64_t i = threadIdx.x + static_cast<int64_t>(j) * kBindThreads;
+    r.w[j] = i < nb ? bundle_width(bbo, i) : 0;
+  }
+}
+
+// for_each_width from the registers when they hold the widths.
+template <typename F>
+__device__ __forceinline__ void each_width(const int64_t* bbo, int64_t nb, const WidthRegs& r, F&& f) {
+  if (!r.held) {
+    for_each_width(bbo, nb, f);
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < kBindChunk; ++j) {
+    const int64_t i = threadIdx.x + static_cast<int64_t>(j) * kBindThreads;
+    if (i < nb) f(i, r.w[j]);
+  }
+}
+
 // Width binding of a device-bound plan (the host-side equivalent is
 // st_search_plan_bind_widths, search_plan.cpp), in two launches.
 //
@@ -196,6 +228,8 @@ __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
   __shared__ long long s_width[kMaxWidthSlots];
   __shared__ uint32_t cursor[kMaxWidthSlots + 1];
   __shared__ uint32_t any_wide;
+  WidthRegs wr;
+  load_widths(bbo, nb, wr);  // in flight while the table is cleared
   for (int e = tid; e < kCensusCap; e += kBindThreads) {
     keys[e] = kCensusEmpty;
     count[e] = 0u;
@@ -207,7 +241,7 @@ __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
   }
   if (tid <= kMaxWidthSlots) cursor[tid] = 0u;
   __syncthreads();
-  for_each_width(bbo, nb, [&](int64_t, long long w) {
+  each_width(bbo, nb, wr, [&](int64_t, long long w) {
     if (overflow) return;  // the outcome is decided
     const int e = census_find(keys, w, true);
     if (e >= 0) atomicAdd(count + e, 1u);
@@ -246,7 +280,7 @@ __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
   __syncthreads();
   const uint32_t ns = n < static_cast<uint32_t>(kMaxWidthSlots) ? n : kMaxWidthSlots;
   if (tid < static_cast<int>(ns)) slot_width[tid] = s_width[tid];
-  for_each_width(bbo, nb, [&](int64_t i, long long w) {
+  each_width(bbo, nb, wr, [&](int64_t i, long long w) {
     const int e = census_find(keys, w, false);
     const uint32_t sl = e >= 0 ? slot_of[e] : kNoWidthSlot;
     bundle_slot[i] = sl;
@@ -280,7 +314,7 @@ __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
   }
   __syncthreads();
   if (bundle_order != nullptr && (order_if_wide == 0u || any_wide != 0u)) {
-    for_each_width(bbo, nb, [&](int64_t i, long long w) {
+    each_width(bbo, nb, wr, [&](int64_t i, long long w) {
       const int e = census_find(keys, w, false);
       const uint32_t sl = e >= 0 ? slot_of[e] : kNoWidthSlot;
       const uint32_t at = atomicAdd(cursor + (sl == kNoWidthSlot ? kMaxWidthSlots : sl), 1u);
@@ -341,6 +375,17 @@ __global__ __launch_bounds__(kBindThreads) void bind_fill_kernel(
     const uint32_t s_lo = static_cast<uint32_t>(e[8]);
     const uint32_t s_hi = n_units != 0 ? s_lo + static_cast<uint32_t>(e[8] >> 32) : s_lo;
     if (words == 0) continue;
+    const uint32_t w0 = static_cast<uint32_t>(static_cast<uint64_t>(words) * part / parts);
+    const uint32_t w1 = static_cast<uint32_t>(static_cast<uint64_t>(words) * (part + 1) / parts);
+    // the part's first template words, loaded before the positions are
+    // resolved (they do not depend on them)
+    uint32_t c[kBindFillBatch], tw[kBindFillBatch];
+#pragma unroll
+    for (int j = 0; j < kBindFillBatch; ++j) {
+      const uint32_t i = w0 + tid + j * kBindThreads;
+      c[j] = i < w1 ? code[i] : kTmplCopy;
+      tw[j] = i < w1 ? tmpl[i] : 0u;
+    }
     __syncthreads();  // the previous batch's positions are no longer read
     for (uint32_t u = tid; u < n_terms; u += kBindThreads) {
       int16_t found[kMaxSearchK];
@@ -374,23 +419,23 @@ __global__ __launch_bounds__(kBindThreads) void bind_fill_kernel(
     }
     __syncthreads();
     uint32_t* dst = bound + static_cast<uint64_t>(sl) * words;
-    const uint32_t w0 = static_cast<uint32_t>(static_cast<uint64_t>(words) * part / parts);
-    const uint32_t w1 = static_cast<uint32_t>(static_cast<uint64_t>(words) * (part + 1) / parts);
     for (uint32_t i0 = w0; i0 < w1; i0 += kBindThreads * kBindFillBatch) {
-      // every load of the batch is issued before any value is used
-      uint32_t c[kBindFillBatch], t[kBindFillBatch];
+      // every load of the batch is issued before any value is used (the
+      // first batch's before the positions)
+      if (i0 != w0) {
 #pragma unroll
-      for (int j = 0; j < kBindFillBatch; ++j) {
-        const uint32_t i = i0 + tid + j * kBindThreads;
-        c[j] = i < w1 ? code[i] : kTmplCopy;
-        t[j] = i < w1 ? tmpl[i] : 0u;
+        for (int j = 0; j < kBindFillBatch; ++j) {
+          const uint32_t i = i0 + tid + j * kBindThreads;
+          c[j] = i < w1 ? code[i] : kTmplCopy;
+          tw[j] = i < w1 ? tmpl[i] : 0u;
+        }
       }
 #pragma unroll
       for (int j = 0; j < kBindFillBatch; ++j) {
         const uint32_t i = i0 + tid + j * kBindThreads;
         if (i >= w1) break;
         if (c[j] != kTmplCopy && i >= s_lo && i < s_hi) continue;  // the unit pass's
-        dst[i] = resolve(c[j], t[j]);
+        dst[i] = resolve(c[j], tw[j]);
       }
     }
     if (n_units == 0) continue;
