@@ -1360,9 +1360,12 @@ __device__ __forceinline__ void wide_eval_group(const char* stream, const ST_CON
   if (j + 1 < steps) wide_step<K, MASKS, WPL>(b1, tile_lane, res, acc);
   u32x4 v = res | acc;
   if (info & kSlotComplement) v = ~v;
+  // A plain (cached) store: the pair's other workgroup writes the other
+  // 64-byte half of the same 128-byte output line at about the same time,
+  // and the halves can meet in L2 (non-temporal stores went out as partial
+  // lines: 3% slower at cfg3).
   if (valid && (info & kSlotValid))
-    __builtin_nontemporal_store(
-        v, (ST_GLOBAL u32x4*)(out_lane + static_cast<int64_t>(info >> kSlotRowShift) * row_bytes));
+    *(ST_GLOBAL u32x4*)(out_lane + static_cast<int64_t>(info >> kSlotRowShift) * row_bytes) = v;
 }
 
 // Grid: 1024-thread workgroups, one per CU.  When the grid is a multiple

@@ -20,10 +20,12 @@ tests/golden/make_golden.py full):
   device-bound and host-bound plans;
 * cfg4 (100M docs, build only): input digests, bundle_b_offsets and the
   5.9 GB bloom_index;
-* cfg5's fused search + filtered top-k on a doc prefix of its corpus, its
-  512 queries and seeded embeddings, against the oracle's fp64 top-k under
-  the stated tolerance (ids equal except swaps between scores within 1e-3
-  relative; scores within 1e-3 of the fp64 score of the returned id).
+* cfg5's fused search + filtered top-k on all 20M docs (every query's
+  padding, filter and order; 16 sampled queries against an fp32 torch
+  reference of the same values), and on a doc prefix against the oracle's
+  fp64 top-k, under the stated tolerance (ids equal except swaps between
+  scores within 1e-3 relative; scores within 1e-3 of the fp64 score of the
+  returned id).
 """
 
 from __future__ import annotations
@@ -232,6 +234,82 @@ def test_full_size_cfg4_build_vs_reference():
     torch.cuda.synchronize()
     del ids, offs, vals
     _check_build("cfg4", bi, bo, t0)
+
+
+@pytest.mark.timeout(900)
+def test_full_size_cfg5_search_topk():
+    """bloom_index_search_topk on all 20M docs of cfg5 (the corpus whose
+    search output equals the reference's, test above), its 512 three-term
+    filters, bf16[128] doc embeddings N(0, 1/128) and queries N(0, 1) drawn
+    on the device (seeded torch), top-100.  For 16 queries spread over the
+    batch the result is checked against an fp32 torch reference of the same
+    bf16 values on the same filter (scores of every passing doc, -inf
+    elsewhere, torch.topk): ids equal except swaps between scores within
+    1e-3 relative, returned scores within 1e-3 of the fp64 score of the
+    returned id, scores non-increasing and equal scores in ascending id
+    order; for every query the ids pass its filter, are distinct, and the
+    -1 padding appears exactly when fewer than 100 docs pass."""
+    t0 = time.time()
+    cspec, ids, offs, vals = _corpus_on_device("cfg5", t0)
+    _, qspec = S.CONFIGS["cfg5"]
+    st = torch.ops.st
+    bi, bo = st.bloom_index_build(ids, offs, vals, cspec.b_multiplier, cspec.k)
+    del ids, offs, vals
+    queries = S.make_queries(cspec, qspec, seed=0)
+    _, (pd, po) = st.parse_expression_query_batch(queries, torch.ones(1, dtype=torch.long), cspec.hash_k, True, 5)
+    n, dim, topk = cspec.num_docs, 128, 100
+    emb, qv = S.make_embeddings_device(n, dim, len(queries), seed=0)
+    H.note(f"[full] cfg5 top-k: {n} docs x {len(queries)} queries, bf16[{dim}], top-{topk} "
+           f"({time.time() - t0:.0f}s)")
+    got_ids, got_sc = st.bloom_index_search_topk(bi, bo, pd, po, cspec.k, cspec.hash_k, emb, qv, n, topk)
+    packed = st.bloom_index_search_batch(bi, bo, pd, po, cspec.k, cspec.hash_k, False)
+    torch.cuda.synchronize()
+    assert S.digest(packed.cpu().numpy()) == _digests()["cfg5"]["packed"], "the filter differs from the reference's"
+    counts = torch.tensor(_digests()["cfg5"]["match_counts"])
+    # every query: padding exactly past the passing docs, ids pass the filter, distinct
+    have = (got_ids >= 0).sum(1).cpu()
+    assert torch.equal(have, torch.clamp(counts, max=topk)), "padding does not match the passing doc counts"
+    valid = got_ids >= 0
+    d = torch.where(valid, got_ids, torch.zeros_like(got_ids))
+    rows = torch.arange(len(queries), device=d.device)[:, None].expand_as(d)
+    bits = (packed[rows, d // 64] >> (63 - d % 64)) & 1
+    assert bool((bits.bool() | ~valid).all()), "a returned id fails its filter"
+    srt = torch.sort(torch.where(valid, got_ids, torch.full_like(got_ids, -1)), dim=1).values
+    assert bool(((srt[:, 1:] != srt[:, :-1]) | (srt[:, 1:] < 0)).all()), "duplicate ids"
+    sc = got_sc.cpu().numpy()
+    gi = got_ids.cpu().numpy()
+    for q in range(len(queries)):
+        m = int(have[q])
+        assert np.all(np.diff(sc[q, :m]) <= 0), "scores not non-increasing"
+        eq = np.diff(sc[q, :m]) == 0
+        assert np.all(np.diff(gi[q, :m])[eq] > 0), "equal scores not in ascending id order"
+    H.note(f"[full] cfg5 top-k: padding, filter, distinctness and order hold for all {len(queries)} queries "
+           f"({time.time() - t0:.0f}s)")
+    # fp32 reference for sampled queries
+    sample = list(range(0, len(queries), len(queries) // 16))[:16]
+    qf = qv[sample].float()
+    ref = torch.empty((len(sample), n), dtype=torch.float32, device=qv.device)
+    for r0 in range(0, n, 1 << 21):
+        r1 = min(n, r0 + (1 << 21))
+        ref[:, r0:r1] = (emb[r0:r1].float() @ qf.T).T
+    docs = torch.arange(n, device=qv.device)
+    for i, q in enumerate(sample):
+        passing = ((packed[q, docs // 64] >> (63 - docs % 64)) & 1).bool()
+        ref[i] = torch.where(passing, ref[i], torch.full_like(ref[i], -float("inf")))
+    want_sc, want_ids = torch.topk(ref, topk, dim=1)
+    want_sc, want_ids = want_sc.cpu().numpy(), want_ids.cpu().numpy()
+    emb_rows = emb[got_ids[sample].clamp(min=0)].float().cpu().numpy().astype(np.float64)
+    qf64 = qf.cpu().numpy().astype(np.float64)
+    for i, q in enumerate(sample):
+        m = int(have[q])
+        exact = emb_rows[i, :m] @ qf64[i]
+        np.testing.assert_allclose(sc[q, :m], exact, rtol=1e-3, atol=1e-6)
+        for j in range(m):
+            if gi[q, j] != want_ids[i, j]:
+                assert abs(exact[j] - want_sc[i, j]) <= 1e-3 * max(abs(want_sc[i, j]), 1e-6), \
+                    (q, j, gi[q, j], want_ids[i, j], exact[j], want_sc[i, j])
+    H.note(f"[full] cfg5 top-k: {len(sample)} sampled queries agree with the fp32 reference "
+           f"({time.time() - t0:.0f}s)")
 
 
 @pytest.mark.timeout(600)

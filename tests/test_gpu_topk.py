@@ -123,6 +123,44 @@ def test_topk_ties_overflow_and_safe_rounds(dim):
     assert (sc[0] == dim).all() and (ids[1] == -1).all() and np.isneginf(sc[1]).all()
 
 
+def test_topk_ties_at_the_boundary_go_to_lower_ids():
+    """300 docs share one embedding row whose score falls near rank 60 of the
+    top 100, so the boundary of the top 100 cuts through the group: equal
+    fp32 scores (the same row gives the same MFMA result in every tile), and
+    the kept members must be the group's lowest ids, in ascending order.  The
+    other scores are distinct with gaps far above the fp32 rounding, so here
+    the ids must equal the oracle's exactly (the tolerance's swaps cannot
+    hide a wrong tie rule)."""
+    rng = np.random.default_rng(2024)
+    n, dim, topk = 20000, 128, 100
+    emb = rng.normal(0, 1 / np.sqrt(dim), (n, dim)).astype(np.float32)
+    x = rng.normal(0, 1, dim).astype(np.float32)
+    qv = np.stack([x, x, x])
+    emb32 = _bf16(emb).float().numpy()
+    qv32 = _bf16(qv).float().numpy()
+    order = np.argsort(-(emb32.astype(np.float64) @ qv32[0].astype(np.float64)), kind="stable")
+    tie_row = emb32[order[60]].copy()
+    group = np.arange(17, n, 61)[:300]
+    emb32[group] = tie_row
+    emb_bf = _bf16(emb32)
+    cols = (n + 2047) // 2048 * 32
+    bits = np.ones((3, cols * 64), bool)
+    bits[1] = rng.random(cols * 64) < 0.5
+    bits[2] = rng.random(cols * 64) < 0.3
+    bits[1:, group] = True  # the whole group passes every filter
+    packed = np.packbits(bits, axis=1).view(">i8").astype(np.int64)
+    H.note("[topk] ties at the top-100 boundary")
+    ids, sc = _gpu_topk(packed, emb_bf, _bf16(qv32), n, topk)
+    want_ids, want_sc = O.filtered_topk(emb32, qv32, packed, topk)
+    for q in range(3):
+        in_group = np.isin(ids[q], group)
+        assert 0 < in_group.sum() < topk, "the boundary must cut through the tie group"
+        kept = ids[q][in_group]
+        assert kept.tolist() == sorted(group.tolist())[:len(kept)], "ties must go to the lowest ids, ascending"
+        assert len(set(sc[q][in_group].tolist())) == 1
+        np.testing.assert_array_equal(ids[q], want_ids[q])
+
+
 def test_topk_edge_cases():
     rng = np.random.default_rng(3)
     emb_bf, qv_bf, emb32, qv32, packed = _random_case(rng, 100, 64, 4, 0.5)
