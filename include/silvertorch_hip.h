@@ -451,8 +451,13 @@ int st_fresh_gather(const int64_t* top_index, int64_t rows, int64_t k,
  * batch x probes must not exceed ST_KMEAN_NOALLOC_MAX_PAIRS (larger calls
  * are rejected before any launch).  The device current on the calling thread must be the one
  * the buffers and the stream belong to.  Allocates nothing (no hipMalloc,
- * hipFree or allocating library call).  Calls that overlap on one GPU share
- * the array and race: serialise them (one stream, or events).
+ * hipFree or allocating library call).  Calls on one GPU share the array, so
+ * they never overlap: calls on one stream run in stream order, and a call on
+ * another stream than the device's previous call waits (hipStreamWaitEvent)
+ * for that call's event, recorded after every call; the event is created
+ * with the array's address on the device's first call.  Under graph capture,
+ * capture every call on one stream (a wait on an event recorded outside the
+ * capture is not part of the graph).
  * ------------------------------------------------------------------------- */
 #define ST_KMEAN_NOALLOC_MAX_PAIRS (1 << 20)
 int st_fused_kmean_ann_noalloc(const int64_t* cluster_offsets, int64_t num_offsets,

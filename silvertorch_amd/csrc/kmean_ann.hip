@@ -979,8 +979,12 @@ extern "C" int st_fused_kmean_ann(const int64_t* cluster_offsets, int64_t num_of
 // kmean_count_kernel before it is read, and in the balanced form every row
 // total and group start by kmean_groups_kernel (after the counts, when they
 // fit the array; otherwise the call takes the workgroup form), so nothing
-// needs clearing between calls; calls that overlap on one GPU share the
-// array and race.
+// needs clearing between calls.  Calls on one GPU share the array, so they
+// must not overlap: calls on one stream are ordered by the stream, and a call
+// on another stream than the device's previous call waits for that call (an
+// event, created with the scratch address on the device's first call and
+// recorded after every call; the host side of the calls is serialised by a
+// mutex so that no call slips between another's wait and its record).
 
 namespace st {
 namespace {
@@ -990,25 +994,41 @@ static_assert(kKmScratchItems == (int64_t{1} << 20), "the header's limit and the
 static __device__ __align__(256) int64_t scratch[kKmScratchItems];
 
 constexpr int kKmMaxDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kKmMaxDevices] = {};
+std::mutex g_scratch_mu;  // held for a whole call (see above)
 
-// The calling thread's current device's copy of `scratch`.
-int64_t* device_scratch() {
+// Per device: the address of its copy of `scratch`, the event recorded after
+// its last call and that call's stream.
+struct ScratchDevice {
+  void* ptr = nullptr;
+  hipEvent_t done = nullptr;
+  bool used = false;
+  hipStream_t last = nullptr;
+};
+ScratchDevice g_scratch[kKmMaxDevices];
+
+// The calling thread's current device's scratch state, set up on the
+// device's first call (g_scratch_mu held).
+ScratchDevice& device_scratch() {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) throw Error(ST_ERR_HIP, cat("hipGetDevice failed: ", hipGetErrorString(e)));
   ST_CHECK(dev >= 0 && dev < kKmMaxDevices, "device ordinal ", dev, " out of range");
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (g_scratch_ptr[dev] == nullptr) {
+  ScratchDevice& d = g_scratch[dev];
+  if (d.ptr == nullptr) {
     void* ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || ptr == nullptr)
       throw Error(ST_ERR_HIP, cat("hipGetSymbolAddress(scratch) failed on device ", dev, ": ",
                                   hipGetErrorString(e)));
-    g_scratch_ptr[dev] = ptr;
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess)
+      throw Error(ST_ERR_HIP, cat("hipEventCreateWithFlags failed on device ", dev, ": ",
+                                  hipGetErrorString(e)));
+    d.done = ev;
+    d.ptr = ptr;
   }
-  return static_cast<int64_t*>(g_scratch_ptr[dev]);
+  return d;
 }
 
 }  // namespace
@@ -1026,10 +1046,28 @@ extern "C" int st_fused_kmean_ann_noalloc(
     ST_CHECK(batch < 0 || probes <= 0 || batch <= kKmScratchItems / probes, "batch x probes = ", batch,
              " x ", probes, " exceeds the ", kKmScratchItems,
              " (row, probe) pairs of the no-allocation entry point's scratch");
-    int64_t* counts = batch > 0 && probes > 0 && max_per_row > 0 ? device_scratch() : nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    int64_t* counts = nullptr;
+    ScratchDevice* d = nullptr;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (batch > 0 && probes > 0 && max_per_row > 0) {
+      d = &device_scratch();
+      counts = static_cast<int64_t*>(d->ptr);
+      if (d->used && d->last != s) {  // the previous call, on another stream, first
+        const hipError_t e = hipStreamWaitEvent(s, d->done, 0);
+        if (e != hipSuccess)
+          throw Error(ST_ERR_HIP, cat("hipStreamWaitEvent failed: ", hipGetErrorString(e)));
+      }
+    }
     kmean_run(cluster_offsets, num_offsets, cluster_ids, cluster_length, batch, probes, embeddings,
               total_docs, dim, emb_dtype, queries, max_per_row, filter_mask, filter_rows, filter_cols,
               filter_index, per_embedding_scale, divisor_for_int8, invalid_index_value, counts,
               kKmScratchItems, scores, indices, stream);
+    if (d != nullptr) {
+      const hipError_t e = hipEventRecord(d->done, s);
+      if (e != hipSuccess) throw Error(ST_ERR_HIP, cat("hipEventRecord failed: ", hipGetErrorString(e)));
+      d->used = true;
+      d->last = s;
+    }
   });
 }

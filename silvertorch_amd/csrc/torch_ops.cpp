@@ -221,6 +221,26 @@ int ring_acquire(PlanRing& r, int groups, uint8_t** data, uint64_t** words, uint
   return -1;
 }
 
+}  // namespace
+
+// Test hook (not an operator): how many slots of `device`'s pinned plan ring
+// are free, or -1 when the ring has not been allocated.
+extern "C" int st_torch_plan_ring_free_slots(int device) {
+  PlanRing& r = plan_ring(device);
+  std::lock_guard<std::mutex> lk(r.mu);
+  if (!r.ready) return -1;
+  int n = 0;
+  for (int i = 0; i < kRingSlots; ++i) {
+    bool free = true;
+    for (int g = 0; g < r.groups[i]; ++g)
+      free &= __atomic_load_n(r.words + i * kRingGroups + g, __ATOMIC_ACQUIRE) >= r.last[i];
+    n += free ? 1 : 0;
+  }
+  return n;
+}
+
+namespace {
+
 // Checks, plan compilation, width binding and plan upload shared by the
 // search ops.
 struct PreparedSearch {
@@ -228,9 +248,19 @@ struct PreparedSearch {
   at::DataPtr host_blob;    // pinned copy the search call uploads from
   PlanHolder plan;
   int64_t Q = 0, nb = 0;
+  // The pinned ring slot the plan was copied into: the search call's upload
+  // workgroups free it; when the op fails before the search call is made
+  // (an allocation, a check), nothing will, and it is freed here.
+  uint64_t* ring_words = nullptr;
+  int ring_groups = 0;
+  uint64_t ring_use = 0;
+  bool handed_to_search = false;
   // Runs after the op's launches: the pinned block goes back to torch's host
   // allocator, which reuses it only once the stream has passed them.
   ~PreparedSearch() {
+    if (ring_words != nullptr && !handed_to_search)
+      for (int g = 0; g < ring_groups; ++g)
+        __atomic_store_n(ring_words + g, ring_use, __ATOMIC_RELEASE);
     if (!host_blob) return;
     const auto stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(index.device().index());
     at::getHostAllocator(at::kCUDA)->record_event(host_blob.get(), host_blob.get_context(),
@@ -283,6 +313,9 @@ void prepare_search(PreparedSearch& ps, const Tensor& bloom_index_in,
     uint64_t* words = nullptr;
     uint64_t use = 0;
     if (ring_acquire(plan_ring(ps.index.device().index()), groups, &slot, &words, &use) >= 0) {
+      ps.ring_words = words;
+      ps.ring_groups = groups;
+      ps.ring_use = use;
       std::memcpy(slot, st_search_plan_blob(ps.plan.p), blob_bytes);
       check_st(st_search_plan_upload_source(ps.plan.p, slot), "bloom_index_search_batch");
       TORCH_CHECK(st_search_plan_upload_groups(ps.plan.p) == groups,
@@ -317,6 +350,7 @@ Tensor search_gpu(const Tensor& bloom_index_in, const Tensor& bundle_b_offsets_i
                                at::TensorOptions().dtype(at::kBool).device(dev))
                    : at::empty({ps.Q, C}, at::TensorOptions().dtype(at::kLong).device(dev));
   if (ps.Q == 0 || ps.nb == 0) return out;
+  ps.handed_to_search = true;
   check_st(st_bloom_index_search_batch(ps.index.data_ptr<int64_t>(), ps.index.numel(),
                                        ps.bbo.data_ptr<int64_t>(), ps.nb, ps.plan.p,
                                        ps.blob.data_ptr(), return_bool_mask ? 1 : 0,
@@ -661,18 +695,22 @@ std::tuple<Tensor, Tensor> search_ids_gpu(const Tensor& bloom_index,
   TORCH_CHECK(num_docs >= 0, "num_docs must be non-negative, got ", num_docs);
   TORCH_CHECK(bloom_index.is_cuda(), "bloom_index must be a GPU tensor");
   c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(bloom_index.device());
+  {  // before the plan takes a pinned ring slot
+    const int64_t C = std::max<int64_t>(bundle_b_offsets.numel() - 1, 0) * ST_COLUMNS_PER_BUNDLE;
+    TORCH_CHECK(int64_ids || std::min(num_docs, C * ST_BITS_PER_COLUMN) <= INT32_MAX,
+                "int32 ids cannot hold doc ids up to ", num_docs, "; pass int64_ids=True");
+  }
   PreparedSearch ps;
   prepare_search(ps, bloom_index, bundle_b_offsets, plans_data, plans_offsets, k, hash_k);
   const auto dev = ps.index.device();
   const int64_t C = ps.nb * ST_COLUMNS_PER_BUNDLE;
-  TORCH_CHECK(int64_ids || std::min(num_docs, C * ST_BITS_PER_COLUMN) <= INT32_MAX,
-              "int32 ids cannot hold doc ids up to ", num_docs, "; pass int64_ids=True");
   auto opts = at::TensorOptions().device(dev);
   Tensor row_offsets = at::empty({ps.Q + 1}, opts.dtype(at::kLong));
   Tensor packed = at::empty({ps.Q, C}, opts.dtype(at::kLong));
   Tensor ws = at::empty({std::max<int64_t>(st_bloom_compact_workspace_bytes(ps.Q, C), 1)},
                         opts.dtype(at::kByte));
   void* stream = current_stream(ps.index);
+  ps.handed_to_search = true;
   check_st(st_bloom_index_search_batch_counts(
                ps.index.data_ptr<int64_t>(), ps.index.numel(), ps.bbo.data_ptr<int64_t>(),
                ps.nb, ps.plan.p, ps.blob.defined() ? ps.blob.data_ptr() : nullptr, num_docs,

@@ -551,3 +551,49 @@ def test_wide_bundle_slices_vs_oracle(k, neg, many):
     _, ro, packed = H.search_ids(index, bbo, pd, po, k, 7, n)
     np.testing.assert_array_equal(packed, want)
     np.testing.assert_array_equal(ro, O.compact(want, n)[1])
+
+
+def test_plan_ring_slots_survive_failed_calls():
+    """A search op that fails after its plan took a slot of the device's
+    pinned plan ring (here the bool output of 2^24 empty bundles for 16
+    queries, 512 GB, cannot be allocated) frees the slot itself, since no
+    upload workgroup will; the int32-ids check of the ids op fails before a
+    slot is taken.  After 20 failures of each kind every slot is free and a
+    search still runs and gives the same output."""
+    import ctypes
+    from pathlib import Path
+
+    st = torch.ops.st
+    ring = ctypes.CDLL(str(Path(__file__).resolve().parents[1] / "silvertorch_amd" / "_C.so"))
+    ring.st_torch_plan_ring_free_slots.restype = ctypes.c_int
+    ring.st_torch_plan_ring_free_slots.argtypes = [ctypes.c_int]
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(5)
+    n, F = 5000, 2
+    cnt = rng.integers(1, 3, (n, F))
+    offs = np.concatenate([[0], np.cumsum(cnt.reshape(-1))]).astype(np.int64)
+    vals = rng.integers(0, 30, int(offs[-1])).astype(np.int64)
+    bi, bo = st.bloom_index_build(torch.tensor([1, 2], dtype=torch.int32, device=dev),
+                                  torch.from_numpy(offs).to(dev), torch.from_numpy(vals).to(dev), 5.0, 3)
+    queries = [f"1:{i} OR 2:{i + 1}" for i in range(16)]
+    _, (pd, po) = st.parse_expression_query_batch(queries, torch.ones(1, dtype=torch.long), 7, True, 5)
+    want = st.bloom_index_search_batch(bi, bo, pd, po, 3, 7, False)
+    torch.cuda.synchronize()
+    assert ring.st_torch_plan_ring_free_slots(0) == 16
+    empty_index = torch.empty(0, dtype=torch.long, device=dev)
+    many_bundles = torch.zeros((1 << 24) + 1, dtype=torch.long, device=dev)
+    H.note("[ring] 20 calls failing after the plan upload was prepared")
+    for _ in range(20):
+        with pytest.raises(RuntimeError):
+            st.bloom_index_search_batch(empty_index, many_bundles, pd, po, 3, 7, True)
+    H.note("[ring] 20 calls failing the int32-ids check")
+    for _ in range(20):
+        with pytest.raises(RuntimeError, match="int32 ids cannot hold"):
+            st.bloom_index_search_batch_ids(empty_index, many_bundles[:(1 << 20) + 1], pd, po, 3, 7, 1 << 31)
+    torch.cuda.synchronize()
+    assert ring.st_torch_plan_ring_free_slots(0) == 16, "a failed call kept its pinned plan slot"
+    got = st.bloom_index_search_batch(bi, bo, pd, po, 3, 7, False)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    del many_bundles
+    torch.cuda.empty_cache()

@@ -2,7 +2,8 @@
 per-(row, probe) counts live in the library's fixed device array) against
 st_fused_kmean_ann with a caller workspace, through the C ABI: bit-identical
 scores and indices on two calls in a row, the second smaller, filtered and
-unfiltered; calls past the array's capacity are rejected."""
+unfiltered; calls past the array's capacity are rejected; calls on two
+streams do not race on the array."""
 
 from __future__ import annotations
 
@@ -85,3 +86,35 @@ def test_noalloc_rejects_more_pairs_than_its_scratch():
                                             None, None, -1, -9, sc.data_ptr(), ix.data_ptr(), stream))
     torch.cuda.synchronize()
     assert (ix.cpu() == -9).all()
+
+
+def test_noalloc_calls_on_two_streams_do_not_race():
+    """Two calls on two streams, issued back to back without any ordering by
+    the caller: the second waits for the first (the shared scratch array),
+    so both equal the workspace entry point's results."""
+    rng = np.random.default_rng(77)
+    a = _case(rng, 512, 8, 64, True)
+    b = _case(rng, 300, 7, 64, False)
+    want_a = _call(a, 3000, noalloc=False)
+    want_b = _call(b, 2000, noalloc=False)
+    L = capi.lib()
+    outs = []
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    H.note("[noalloc] two streams")
+    bufs = [(torch.full((c["batch"], w), 7, dtype=torch.int16, device="cuda"),
+             torch.full((c["batch"], w), 7, dtype=torch.int32, device="cuda")) for c, w in ((a, 3000), (b, 2000))]
+    torch.cuda.synchronize()  # the outputs' fills are done before either stream writes them
+    for (c, width, s), (sc, ix) in zip(((a, 3000, s1), (b, 2000, s2)), bufs):
+        B, P = c["batch"], c["probes"]
+        m = c["mask"]
+        capi.check(L.st_fused_kmean_ann_noalloc(
+            c["offs"].data_ptr(), c["offs"].numel(), c["cids"].data_ptr(), c["clen"].data_ptr(), B, P,
+            c["emb"].data_ptr(), c["n"], c["dim"], 2, c["q"].data_ptr(), width,
+            m.data_ptr() if m is not None else None, m.shape[0] if m is not None else 0,
+            m.shape[1] if m is not None else 0, None, None, -1, -1, sc.data_ptr(), ix.data_ptr(),
+            s.cuda_stream))
+        outs.append((sc, ix))
+    torch.cuda.synchronize()
+    for (sc, ix), (ws, wi) in zip(outs, (want_a, want_b)):
+        np.testing.assert_array_equal(ix.cpu().numpy(), wi)
+        np.testing.assert_array_equal(sc.cpu().numpy(), ws)
