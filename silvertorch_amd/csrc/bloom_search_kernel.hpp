@@ -1041,6 +1041,7 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
   }
 
   int64_t prev_b = -1;  // width whose term positions are in pos
+  uint32_t staged_slot = kNoWidthSlot;  // width slot whose literal stream is in pos
   const uint32_t s_begin = uniform(a.wave_off[wave]);
   const uint32_t s_end = uniform(a.wave_off[wave + 1]);
   const bool streamed = a.stream_words != 0;
@@ -1074,7 +1075,7 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
         if (c < chunks) tile[c] = pre[i];
       }
     }
-    if (quad_here) {  // the stream goes where unbound bundles keep positions
+    if (quad_here && slot != staged_slot) {  // the stream goes where unbound bundles keep positions
       const uint32_t chunks = a.stream_words / 4;
       u32x4* dst = reinterpret_cast<u32x4*>(pos);
 #pragma unroll
@@ -1082,15 +1083,19 @@ __global__ __launch_bounds__(kSearchThreads) void bloom_search_kernel(
         const uint32_t c = static_cast<uint32_t>(tid) + static_cast<uint32_t>(i) * kSearchThreads;
         if (c < chunks) dst[c] = spre[i];
       }
+      staged_slot = slot;
       prev_b = -1;
     }
+    // the positions of an unbound bundle replace the staged stream below
+    if (!skip && slot == kNoWidthSlot && b != prev_b) staged_slot = kNoWidthSlot;
     // The next bundle's loads go out as soon as this thread's registers are
     // in LDS, before the barrier, so the HBM queue is not left empty while the
-    // workgroup finishes storing the tile.
+    // workgroup finishes storing the tile.  Its stream is loaded only when
+    // another slot's is in LDS.
     const bool has_next = nxt.bundle >= 0;
     if (has_next) {
       prefetch_tile(a, nxt.start, nxt.b, pre);
-      if (quad_bundle(nxt)) prefetch_stream(nxt, spre);
+      if (quad_bundle(nxt) && nxt.slot != staged_slot) prefetch_stream(nxt, spre);
     }
     if (!skip && slot == kNoWidthSlot && b != prev_b) {
       const FastMod64 fm = make_fastmod_dev(static_cast<uint64_t>(b));
