@@ -85,10 +85,12 @@ def calibrate_copy():
 def probe_pattern():
     """The ceiling of the search kernel's access pattern on this part: the
     probe kernel (csrc/pattern_probe.hip) moves cfg2's index through LDS tiles
-    and writes the packed output's 256-byte pieces with nothing between them,
-    with one or two tiles of loads in flight, and its loads or stores alone;
-    the search kernel itself is timed the same way (host-bound plan, HIP
-    events on the launching stream).  Prints one JSON line."""
+    and writes the packed output with nothing between them, its loads or
+    stores alone, and the same with groups of 2 or 4 adjacent bundles per
+    workgroup visit (512- or 1,024-byte runs per query row instead of 256);
+    the search kernel itself is timed the same way (host-bound plan).  Each
+    figure is the mean over 20 back-to-back launches between one pair of HIP
+    events on the launching stream.  Prints one JSON line."""
     import ctypes
 
     import numpy as np
@@ -125,32 +127,38 @@ def probe_pattern():
     blob = torch.frombuffer(bytearray(plan.blob()), dtype=torch.uint8).to(dev)
 
     def run(fn, reps=20, warm=3):
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        for i in range(reps + warm):
-            if i >= warm:
-                ev[i - warm][0].record(stream)
+        # mean over `reps` back-to-back launches between one pair of events
+        for _ in range(warm):
             fn()
-            if i >= warm:
-                ev[i - warm][1].record(stream)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
         torch.cuda.synchronize()
-        return float(np.median([a.elapsed_time(b) * 1e3 for a, b in ev]))
+        return a.elapsed_time(b) * 1e3 / reps
 
     index_bytes, out_bytes = bi.numel() * 8, out.numel() * 8
     res = {"probe": "search access pattern", "workload": f"cfg2: {nb} bundles, {Q} query rows",
            "index_bytes": index_bytes, "output_bytes": out_bytes, "hbm_peak_gbs": HBM_PEAK_GBS, "runs": []}
-    for depth in (1, 2):
-        for mode, name, nbytes in ((0, "loads and stores", index_bytes + out_bytes), (1, "loads only", index_bytes),
-                                   (2, "stores only", out_bytes)):
-            def fn(depth=depth, mode=mode):
+    modes = {0: ("loads and stores", index_bytes + out_bytes), 1: ("loads only", index_bytes),
+             2: ("stores only", out_bytes)}
+    # bundles per group (contiguous bytes per query row / 256) and the modes timed
+    for grp, grp_modes in ((1, (0, 1, 2)), (2, (0, 2)), (4, (0, 2))):
+        for mode in grp_modes:
+            name, nbytes = modes[mode]
+
+            def fn(grp=grp, mode=mode):
                 rc = P.st_probe_search_pattern(bi.data_ptr(), bi.numel(), bo.data_ptr(), nb, Q, out.data_ptr(),
-                                               sink.data_ptr(), depth, mode, grid, ctypes.c_void_p(stream.cuda_stream))
+                                               sink.data_ptr(), grp, mode, grid, ctypes.c_void_p(stream.cuda_stream))
                 if rc != 0:
                     raise RuntimeError(P.st_probe_last_error().decode())
             us = run(fn)
-            res["runs"].append({"kernel": "pattern_probe_kernel", "tiles_in_flight": depth, "mode": name,
-                                "median_us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3,
+            res["runs"].append({"kernel": "pattern_probe_kernel", "bundles_per_group": grp,
+                                "bytes_per_query_row_run": 256 * grp, "mode": name,
+                                "mean_us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3,
                                 "frac": nbytes / us / 1e3 / HBM_PEAK_GBS})
-            log(f"probe: {depth} tile(s) in flight, {name}: {us:.1f} us, {nbytes / us / 1e3:.0f} GB/s")
+            log(f"probe: {256 * grp}-byte runs per query row, {name}: {us:.1f} us, {nbytes / us / 1e3:.0f} GB/s")
 
     def search():
         capi.check(L.st_bloom_index_search_batch(bi.data_ptr(), bi.numel(), bo.data_ptr(), nb, plan.handle,
@@ -158,7 +166,7 @@ def probe_pattern():
     us = run(search)
     nbytes = index_bytes + out_bytes
     res["runs"].append({"kernel": "bloom_search_kernel", "mode": "search (packed, host-bound plan)",
-                        "median_us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3,
+                        "mean_us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3,
                         "frac": nbytes / us / 1e3 / HBM_PEAK_GBS})
     log(f"search kernel: {us:.1f} us, {nbytes / us / 1e3:.0f} GB/s")
     print(json.dumps(res), flush=True)
@@ -838,8 +846,10 @@ def main():
         if not ok:
             sys.exit("parity failure in sampled bundles")
 
-    # Kernel-only timing through the C ABI: HIP events recorded on the stream
-    # the search kernel is launched on, bracketing only the launch.
+    # Kernel-only timing through the C ABI: `reps` back-to-back launches of the
+    # search kernel between one pair of HIP events recorded on the stream it
+    # is launched on (an event pair around each launch would add the
+    # dispatch latency of every launch, ~4 us, to the kernel's time).
     L = capi.lib()
     plan = capi.SearchPlan(pd.numpy().tobytes(), po.numpy(), k, hk)
     plan.bind_widths(bo.cpu().numpy())  # the op binds its plans to the bundle widths too
@@ -847,19 +857,19 @@ def main():
     kout = torch.empty_like(out)
     stream = torch.cuda.current_stream()
     reps = max(args.steps, 20)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
-    for i in range(reps + 3):
-        j = i - 3
-        if j >= 0:
-            starts[j].record(stream)
-        capi.check(L.st_bloom_index_search_batch(bi.data_ptr(), bi.numel(), bo.data_ptr(), nb, plan.handle,
-                                                 blob.data_ptr(), int(args.bool_mask), kout.data_ptr(),
-                                                 stream.cuda_stream))
-        if j >= 0:
-            ends[j].record(stream)
-    torch.cuda.synchronize()
-    kernel_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / reps
+
+    def kernel_only(mode, dst, n):
+        for i in range(n + 3):
+            if i == 3:
+                t0.record(stream)
+            capi.check(L.st_bloom_index_search_batch(bi.data_ptr(), bi.numel(), bo.data_ptr(), nb, plan.handle,
+                                                     blob.data_ptr(), mode, dst.data_ptr(), stream.cuda_stream))
+        t1.record(stream)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / n
+
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    kernel_ms = kernel_only(int(args.bool_mask), kout, reps)
     assert torch.equal(kout, out)
 
     # Bool output (the reference op's default, return_bool_mask=True): the
@@ -867,16 +877,7 @@ def main():
     bool_report = None
     if not args.bool_mask:
         bout = torch.empty((Q, nb * 2048), dtype=torch.bool, device=dev)
-        bev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
-        for i in range(23):
-            if i >= 3:
-                bev[i - 3][0].record(stream)
-            capi.check(L.st_bloom_index_search_batch(bi.data_ptr(), bi.numel(), bo.data_ptr(), nb, plan.handle,
-                                                     blob.data_ptr(), 1, bout.data_ptr(), stream.cuda_stream))
-            if i >= 3:
-                bev[i - 3][1].record(stream)
-        torch.cuda.synchronize()
-        bool_us = sum(x.elapsed_time(y) for x, y in bev) / len(bev) * 1e3
+        bool_us = kernel_only(1, bout, 20) * 1e3
         bytes_b = bi.numel() * 8 + bo.numel() * 8 + pd.numel() + po.numel() * 8 + bout.numel()
         # spot check against the packed words: bit 63 - i of word c is doc 64c + i
         words = kout[:, :4].cpu().numpy().view(np.uint64)
@@ -949,6 +950,8 @@ def main():
             "kernel": "bloom_search_kernel",
             "kernel_us": kernel_ms * 1e3,
             "algorithmic_bytes": alg_bytes,
+            "kernel_timing": f"mean of {reps} back-to-back launches between one pair of HIP events "
+                             "on the launching stream (host-bound plan)",
         },
         "cpu_baseline": baseline,
         "build": {"ms": build_s * 1e3, "docs_per_s": N / build_s, "workload": "cfg2 index build"},

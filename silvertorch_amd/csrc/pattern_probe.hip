@@ -5,16 +5,17 @@
 // its own; nothing in the product calls it.
 //
 // The grid is the search kernel's: one 1024-thread workgroup per CU walks
-// bundles w, w + grid, ... in index order.  Per bundle it moves the bundle's
-// rows (b x 256 bytes, b <= 512) from HBM into an LDS tile through registers
-// with 16-byte non-temporal loads, and writes 256 bytes per query row of the
-// packed output (Q rows of 256 * num_bundles bytes), 16 bytes per lane, four
-// query rows per wave instruction: the search kernel's loads and stores with
-// nothing between them.  DEPTH register buffers are in flight: with DEPTH 1
-// the next bundle's loads go out when the current tile is in LDS (the search
-// kernel's form, whose registers hold one tile), with DEPTH 2 two bundles
-// ahead.  MODE 1 drops the stores (a 16-byte sink per workgroup keeps the
-// loads live), MODE 2 the loads.
+// groups of RUN adjacent bundles, w, w + grid, ... .  Per bundle it moves the
+// bundle's rows (b x 256 bytes, b <= 512) from HBM into an LDS tile through
+// registers with 16-byte non-temporal loads, the next bundle's loads issued
+// as soon as the current tile is in LDS (the search kernel's form, whose
+// registers hold one tile).  After the group's last bundle it writes the
+// group's packed output: RUN * 256 contiguous bytes per query row (Q rows of
+// 256 * num_bundles bytes), 16 bytes per lane.  RUN 1 is the search kernel's
+// store pattern (four query rows per wave instruction); RUN 2 and 4 measure
+// whether longer runs per query row raise the write rate.  MODE 1 drops the
+// stores (a 16-byte sink per workgroup keeps the loads live), MODE 2 the
+// loads.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -44,7 +45,7 @@ __device__ __forceinline__ void load_tile(const u32x4* __restrict__ src, int64_t
   }
 }
 
-template <int DEPTH, int MODE>
+template <int RUN, int MODE>
 __global__ __launch_bounds__(kThreads) void pattern_probe_kernel(
     const int64_t* __restrict__ index, int64_t numel, const int64_t* __restrict__ bbo,
     int64_t nb, int64_t Q, char* __restrict__ out, u32x4* __restrict__ sink) {
@@ -60,94 +61,99 @@ __global__ __launch_bounds__(kThreads) void pattern_probe_kernel(
     if (b < 0) b = 0;
     if (b > kTileRows) b = kTileRows;
   };
-  u32x4 pre[DEPTH][kPer];
+  // bundle of step t of this workgroup's walk (-1: past the end)
+  auto bundle_at = [&](int64_t t) -> int64_t {
+    const int64_t bnd = (blockIdx.x + (t / RUN) * grid) * RUN + t % RUN;
+    return bnd < nb ? bnd : -1;
+  };
+  u32x4 pre[kPer];
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) {
-    const int64_t bnd = blockIdx.x + d * grid;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) pre[d][i] = u32x4{1, 2, 3, 4};
-    if (MODE != 2 && bnd < nb) {
-      int64_t s, b;
-      extent(bnd, s, b);
-      load_tile(src, s, b, numel, pre[d]);
-    }
+  for (int i = 0; i < kPer; ++i) pre[i] = u32x4{1, 2, 3, 4};
+  if (MODE != 2 && bundle_at(0) >= 0) {
+    int64_t s, b;
+    extent(bundle_at(0), s, b);
+    load_tile(src, s, b, numel, pre);
   }
   u32x4 acc{0, 0, 0, 0};
   const int64_t row_bytes = nb * 256;
-  for (int64_t v = 0;; v += DEPTH) {
+  constexpr int kRowsPerInsn = 4 / RUN;         // query rows one wave instruction covers
+  constexpr int kLanesPerRow = 64 / kRowsPerInsn;
+  for (int64_t t = 0;; ++t) {
+    const int64_t bnd = bundle_at(t);
+    if (bnd < 0) break;
+    int64_t s, b;
+    extent(bnd, s, b);
+    __syncthreads();  // the previous bundle's readers are done with the tile
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      const int64_t bnd = blockIdx.x + (v + d) * grid;
-      if (bnd >= nb) {
-        if (MODE == 1) sink[blockIdx.x * kThreads + tid] = acc;
-        return;
-      }
-      int64_t s, b;
-      extent(bnd, s, b);
-      __syncthreads();  // the previous bundle's readers are done with the tile
-#pragma unroll
-      for (int i = 0; i < kPer; ++i) {
-        const int c = tid + i * kThreads;
-        if (c < b * 16) tile[c] = pre[d][i];
-      }
-      const int64_t ahead = bnd + DEPTH * grid;
-      if (MODE != 2 && ahead < nb) {
-        int64_t s2, b2;
-        extent(ahead, s2, b2);
-        load_tile(src, s2, b2, numel, pre[d]);
-      }
-      __syncthreads();
-      const int rows = static_cast<int>(b > 0 ? b : 1);
-      if (MODE == 1) {
-        acc ^= tile[(tid * 7) % (rows * 16)];
-        continue;
-      }
-      // query rows wave * 4 + 64 j + (lane >> 4), 16 bytes per lane
-      for (int64_t q0 = wave * 4; q0 < Q; q0 += 64) {
-        const int64_t q = q0 + (lane >> 4);
-        if (q >= Q) continue;
-        const u32x4 val = tile[(static_cast<int>(q) * 16 + (lane & 15)) % (rows * 16)];
-        PROBE_GLOBAL u32x4* dst = (PROBE_GLOBAL u32x4*)(out + q * row_bytes + bnd * 256 + (lane & 15) * 16);
-        __builtin_nontemporal_store(val, dst);
-      }
+    for (int i = 0; i < kPer; ++i) {
+      const int c = tid + i * kThreads;
+      if (c < b * 16) tile[c] = pre[i];
+    }
+    const int64_t ahead = bundle_at(t + 1);
+    if (MODE != 2 && ahead >= 0) {
+      int64_t s2, b2;
+      extent(ahead, s2, b2);
+      load_tile(src, s2, b2, numel, pre);
+    }
+    __syncthreads();
+    const int rows = static_cast<int>(b > 0 ? b : 1);
+    if (MODE == 1) {
+      acc ^= tile[(tid * 7) % (rows * 16)];
+      continue;
+    }
+    // the group's stores follow its last bundle
+    if (t % RUN != RUN - 1 && ahead >= 0) continue;
+    const int64_t first = bnd - t % RUN;  // the group's first bundle
+    const int64_t run_bytes = (bnd - first + 1) * 256;
+    for (int64_t q0 = wave * kRowsPerInsn; q0 < Q; q0 += 16 * kRowsPerInsn) {
+      const int64_t q = q0 + lane / kLanesPerRow;
+      const int64_t off = static_cast<int64_t>(lane % kLanesPerRow) * 16;
+      if (q >= Q || off >= run_bytes) continue;
+      const u32x4 val = tile[(static_cast<int>(q) * 16 + (lane & 15)) % (rows * 16)];
+      PROBE_GLOBAL u32x4* dst = (PROBE_GLOBAL u32x4*)(out + q * row_bytes + first * 256 + off);
+      __builtin_nontemporal_store(val, dst);
     }
   }
+  if (MODE == 1) sink[blockIdx.x * kThreads + tid] = acc;
 }
 
-template <int DEPTH, int MODE>
+template <int RUN, int MODE>
 hipError_t launch(const int64_t* index, int64_t numel, const int64_t* bbo, int64_t nb, int64_t Q,
                   void* out, void* sink, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((pattern_probe_kernel<DEPTH, MODE>), dim3(grid), dim3(kThreads), 0, s, index,
+  hipLaunchKernelGGL((pattern_probe_kernel<RUN, MODE>), dim3(grid), dim3(kThreads), 0, s, index,
                      numel, bbo, nb, Q, static_cast<char*>(out), static_cast<u32x4*>(sink));
   return hipGetLastError();
 }
 
 }  // namespace
 
-// Runs the probe once on `stream`.  depth: 1 or 2; mode: 0 loads and stores,
-// 1 loads only, 2 stores only.  out: Q x num_bundles x 256 bytes; sink:
-// grid x 1024 x 16 bytes (mode 1).  Returns 0, or -1 with
-// st_probe_last_error() set.
+// Runs the probe once on `stream`.  run: adjacent bundles per group, 1, 2 or
+// 4; mode: 0 loads and stores, 1 loads only, 2 stores only.  out: Q x
+// num_bundles x 256 bytes; sink: grid x 1024 x 16 bytes (mode 1).  Returns 0,
+// or -1 with st_probe_last_error() set.
 extern "C" int st_probe_search_pattern(const int64_t* index, int64_t numel,
                                        const int64_t* bundle_b_offsets, int64_t num_bundles,
-                                       int64_t num_queries, void* out, void* sink, int depth,
+                                       int64_t num_queries, void* out, void* sink, int run,
                                        int mode, int grid, void* stream) {
   if (index == nullptr || bundle_b_offsets == nullptr || out == nullptr || sink == nullptr ||
-      num_bundles <= 0 || num_queries <= 0 || grid <= 0 || (depth != 1 && depth != 2) || mode < 0 ||
-      mode > 2) {
+      num_bundles <= 0 || num_queries <= 0 || grid <= 0 || (run != 1 && run != 2 && run != 4) ||
+      mode < 0 || mode > 2) {
     g_error = "st_probe_search_pattern: invalid arguments";
     return -1;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
-  const int sel = depth * 3 + mode;
+  const int sel = run * 3 + mode;
   switch (sel) {
     case 3: e = launch<1, 0>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
     case 4: e = launch<1, 1>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
     case 5: e = launch<1, 2>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
     case 6: e = launch<2, 0>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
     case 7: e = launch<2, 1>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
-    default: e = launch<2, 2>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
+    case 8: e = launch<2, 2>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
+    case 12: e = launch<4, 0>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
+    case 13: e = launch<4, 1>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
+    default: e = launch<4, 2>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
   }
   if (e != hipSuccess) {
     g_error = std::string("st_probe_search_pattern: ") + hipGetErrorString(e);

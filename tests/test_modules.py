@@ -99,3 +99,23 @@ def test_builder_from_features_moves_and_reloads(gpu):
     fresh = fresh.to(gpu)
     _, (pd, po) = FilterQueryParserModule(hash_k=4)(["1:1", "0:200 OR 2:5"], torch.ones(1, dtype=torch.long))
     assert torch.equal(fresh(pd, po, False), m(pd, po, False))
+
+
+def test_reference_import_paths_resolve_to_this_build():
+    """Code written against the reference imports silvertorch.ops._load_ops
+    and silvertorch.modules (silvertorch/ops/_load_ops.py:29-42,
+    silvertorch/modules/__init__.py); those paths give this build's ops and
+    classes."""
+    import silvertorch.ops._load_ops  # noqa: F401
+    import silvertorch_amd.modules as amd
+    from silvertorch.modules import (BloomIndexSearchModule as A, BloomIndexSearchModuleBuilder as B,
+                                     FilterQueryParserModule as C, FilterQueryParserModuleBuilder as D)
+    from silvertorch.modules.bloom_index_search_module_builder import BloomIndexSearchModuleBuilder
+    from silvertorch.modules.filter_query_parser_module import FilterQueryParserModule
+
+    assert (A, B, C, D) == (amd.BloomIndexSearchModule, amd.BloomIndexSearchModuleBuilder,
+                            amd.FilterQueryParserModule, amd.FilterQueryParserModuleBuilder)
+    assert BloomIndexSearchModuleBuilder is B and FilterQueryParserModule is C
+    assert hasattr(torch.ops.st, "bloom_index_build") and hasattr(torch.ops.st, "bloom_index_search_batch")
+    max_stack, _ = C(hash_k=7)(["0:0 AND 1:1"], torch.ones(1, dtype=torch.long))
+    assert max_stack == P.parse_batch(["0:0 AND 1:1"], 7, True, 5)[0]
