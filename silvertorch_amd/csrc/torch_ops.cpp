@@ -154,8 +154,9 @@ struct PlanHolder {
 // again once its words hold its last use number, with no event on the stream
 // (an event record costs the stream a few microseconds per call).  A plan
 // larger than a slot, or a call that finds every slot still in use, takes a
-// block of torch's pinned host allocator and its event instead.  A slot whose
-// call failed before its copy ran stays in use.
+// block of torch's pinned host allocator and its event instead.  An op that
+// fails before its search call frees its slot itself (PreparedSearch); a slot
+// whose search call failed before its copy ran stays in use.
 constexpr int kRingSlots = 16;
 constexpr int64_t kRingSlotBytes = 256 << 10;
 constexpr int64_t kRingGroupBytes = 64 << 10;  // blob bytes per upload workgroup
