@@ -170,8 +170,9 @@ __device__ __forceinline__ void each_width(const int64_t* bbo, int64_t nb, const
 // bind_prologue_kernel: workgroups [0, upload_groups) copy the plan's bytes
 // from pinned host memory into the device blob (when the caller left that
 // to the search call); workgroup `upload_groups` takes the census of the
-// bundle widths -- the kMaxWidthSlots most frequent widths get slots, ties
-// to the smaller width -- and writes the slot table, every bundle's slot
+// bundle widths -- every width gets a slot, in increasing width, when there
+// are at most kMaxWidthSlots of them, else the kMaxWidthSlots most frequent
+// do (ties to the smaller width) -- and writes the slot table, every bundle's slot
 // and, when `bundle_order` is given, a visiting order grouped by slot (a
 // counting sort; order within a slot is arbitrary) -- with `order_if_wide`
 // only when some slot width is wide (the wide-bundle kernel's order).  The
@@ -227,7 +228,7 @@ __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
   __shared__ uint32_t overflow;
   __shared__ long long s_width[kMaxWidthSlots];
   __shared__ uint32_t cursor[kMaxWidthSlots + 1];
-  __shared__ uint32_t any_wide;
+  __shared__ uint32_t any_wide, unslotted;
   WidthRegs wr;
   load_widths(bbo, nb, wr);  // in flight while the table is cleared
   for (int e = tid; e < kCensusCap; e += kBindThreads) {
@@ -238,14 +239,16 @@ __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
   if (tid == 0) {
     n_dense = 0u;
     overflow = 0u;
+    any_wide = 0u;
+    unslotted = 0u;
   }
   if (tid <= kMaxWidthSlots) cursor[tid] = 0u;
   __syncthreads();
+  // the distinct widths (no counts yet: with at most kMaxWidthSlots of them
+  // every width gets a slot and how often each occurs does not matter)
   each_width(bbo, nb, wr, [&](int64_t, long long w) {
     if (overflow) return;  // the outcome is decided
-    const int e = census_find(keys, w, true);
-    if (e >= 0) atomicAdd(count + e, 1u);
-    else overflow = 1u;
+    if (census_find(keys, w, true) < 0) overflow = 1u;
   });
   __syncthreads();
   if (overflow) {  // no slots: clear the table (census_find then finds nothing)
@@ -258,62 +261,82 @@ __global__ __launch_bounds__(kBindThreads) void bind_prologue_kernel(
       const uint32_t a = atomicAdd(&n_dense, 1u);
       dense[a] = static_cast<uint32_t>(e);
       dense_w[a] = w;
-      dense_c[a] = count[e];
     }
   }
   __syncthreads();
   const uint32_t n = n_dense;
+  // slot of each width: with more widths than slots, the kMaxWidthSlots
+  // most frequent (ties to the smaller width) after counting them;
+  // otherwise all of them in increasing width
+  const bool counted = n > static_cast<uint32_t>(kMaxWidthSlots);  // uniform
+  if (counted) {
+    each_width(bbo, nb, wr, [&](int64_t, long long w) {
+      atomicAdd(count + census_find(keys, w, false), 1u);  // every width is in the table
+    });
+    __syncthreads();
+    for (uint32_t a = tid; a < n; a += kBindThreads) dense_c[a] = count[dense[a]];
+    __syncthreads();
+  }
   for (uint32_t a = tid; a < n; a += kBindThreads) {
-    const uint32_t c = dense_c[a];
     const long long w = dense_w[a];
     uint32_t rank = 0;
+    if (counted) {
+      const uint32_t c = dense_c[a];
 #pragma unroll 8
-    for (uint32_t b = 0; b < n; ++b) {
-      const uint32_t cb = dense_c[b];
-      rank += (cb > c || (cb == c && dense_w[b] < w)) ? 1u : 0u;
+      for (uint32_t b = 0; b < n; ++b) {
+        const uint32_t cb = dense_c[b];
+        rank += (cb > c || (cb == c && dense_w[b] < w)) ? 1u : 0u;
+      }
+    } else {
+#pragma unroll 8
+      for (uint32_t b = 0; b < n; ++b) rank += dense_w[b] < w ? 1u : 0u;
     }
     if (rank < static_cast<uint32_t>(kMaxWidthSlots)) {
       slot_of[dense[a]] = rank;
       s_width[rank] = w;
+      if (wide_width(w)) any_wide = 1u;
     }
   }
   __syncthreads();
   const uint32_t ns = n < static_cast<uint32_t>(kMaxWidthSlots) ? n : kMaxWidthSlots;
   if (tid < static_cast<int>(ns)) slot_width[tid] = s_width[tid];
+  // the visiting order grouped by slot, when asked for (bucket counts only
+  // then)
+  const bool order = bundle_order != nullptr && (order_if_wide == 0u || any_wide != 0u);  // uniform
   each_width(bbo, nb, wr, [&](int64_t i, long long w) {
     const int e = census_find(keys, w, false);
     const uint32_t sl = e >= 0 ? slot_of[e] : kNoWidthSlot;
     bundle_slot[i] = sl;
-    atomicAdd(cursor + (sl == kNoWidthSlot ? kMaxWidthSlots : sl), 1u);
+    if (sl == kNoWidthSlot) unslotted = 1u;
+    if (order) atomicAdd(cursor + (sl == kNoWidthSlot ? kMaxWidthSlots : sl), 1u);
   });
   __syncthreads();
   static_assert(kMaxWidthSlots == 64, "one wave scans the slot buckets");
   if (tid < 64) {
     // num_slots[1]: every bundle has a slot, and every slot width is wide
     const bool narrow = tid < static_cast<int>(ns) && !wide_width(s_width[tid]);
-    const bool all_wide = __ballot(narrow) == 0ull && cursor[kMaxWidthSlots] == 0;
-    const bool wide = tid < static_cast<int>(ns) && wide_width(s_width[tid]);
-    const bool some_wide = __ballot(wide) != 0ull;
-    // bucket sizes -> bucket starts (exclusive scan over the wave; the
-    // unslotted bucket goes last)
-    const uint32_t c = cursor[tid];
-    uint32_t incl = c;
+    const bool all_wide = __ballot(narrow) == 0ull && unslotted == 0u;
+    if (order) {
+      // bucket sizes -> bucket starts (exclusive scan over the wave; the
+      // unslotted bucket goes last)
+      const uint32_t c = cursor[tid];
+      uint32_t incl = c;
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint32_t y = __shfl_up(incl, d, 64);
-      if (tid >= d) incl += y;
+      for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t y = __shfl_up(incl, d, 64);
+        if (tid >= d) incl += y;
+      }
+      cursor[tid] = incl - c;
+      if (tid == 63) cursor[kMaxWidthSlots] = incl;
     }
-    cursor[tid] = incl - c;
-    if (tid == 63) cursor[kMaxWidthSlots] = incl;
     if (tid == 0) {
       num_slots[0] = ns;
       num_slots[1] = all_wide ? 1u : 0u;
-      num_slots[2] = some_wide ? 1u : 0u;
-      any_wide = some_wide ? 1u : 0u;
+      num_slots[2] = any_wide;
     }
   }
-  __syncthreads();
-  if (bundle_order != nullptr && (order_if_wide == 0u || any_wide != 0u)) {
+  if (order) {
+    __syncthreads();
     each_width(bbo, nb, wr, [&](int64_t i, long long w) {
       const int e = census_find(keys, w, false);
       const uint32_t sl = e >= 0 ? slot_of[e] : kNoWidthSlot;
