@@ -409,7 +409,10 @@ __global__ __launch_bounds__(kBindThreads) void bind_fill_kernel(
       c[j] = i < w1 ? code[i] : kTmplCopy;
       tw[j] = i < w1 ? tmpl[i] : 0u;
     }
-    __syncthreads();  // the previous batch's positions are no longer read
+    // the previous batch's positions are no longer read (for the first batch
+    // no barrier: its wait for all loads would hold the hashes' loads behind
+    // the template words')
+    if (t != 0) __syncthreads();
     for (uint32_t u = tid; u < n_terms; u += kBindThreads) {
       int16_t found[kMaxSearchK];
       int cnt = 0;
