@@ -170,7 +170,6 @@ struct PlanRing {
   uint64_t last[kRingSlots] = {};  // use number of each slot's last upload
   int groups[kRingSlots] = {};     // its upload workgroups
   uint64_t uses = 0;
-  int next = 0;
 };
 
 PlanRing& plan_ring(int device) {
@@ -195,6 +194,10 @@ int ring_acquire(PlanRing& r, int groups, uint8_t** data, uint64_t** words, uint
         hipHostMalloc(&w, kRingSlots * kRingGroups * sizeof(uint64_t), hipHostMallocCoherent) ==
             hipSuccess) {
       std::memset(w, 0, kRingSlots * kRingGroups * sizeof(uint64_t));
+      // every page written once now: a page's first write faults it in on
+      // the host (~4 us per 4 KB page), which would otherwise land on the
+      // first call that uses each slot
+      std::memset(d, 0, kRingSlots * kRingSlotBytes);
       r.data = static_cast<uint8_t*>(d);
       r.words = static_cast<uint64_t*>(w);
       r.ready = true;
@@ -205,13 +208,13 @@ int ring_acquire(PlanRing& r, int groups, uint8_t** data, uint64_t** words, uint
     }
   }
   if (!r.ready) return -1;
-  for (int t = 0; t < kRingSlots; ++t) {
-    const int i = (r.next + t) % kRingSlots;
+  // the lowest free slot: calls reuse the few slots the calls in flight
+  // leave free, whose lines stay in the host's caches
+  for (int i = 0; i < kRingSlots; ++i) {
     bool free = true;
     for (int g = 0; g < r.groups[i]; ++g)
       free &= __atomic_load_n(r.words + i * kRingGroups + g, __ATOMIC_ACQUIRE) >= r.last[i];
     if (!free) continue;
-    r.next = (i + 1) % kRingSlots;
     r.last[i] = ++r.uses;
     r.groups[i] = groups;
     *data = r.data + i * kRingSlotBytes;
