@@ -83,6 +83,17 @@ __device__ __forceinline__ uint64_t score_key(const void* base, int64_t i) {
   }
 }
 
+// score_key of a 4-byte score from its bits.
+template <int kType>
+__device__ __forceinline__ uint64_t key_of_bits4(uint32_t u) {
+  if constexpr (kType == ST_SCORE_F32) {
+    return f32_key(u);
+  } else {
+    static_assert(kType == ST_SCORE_I32, "4-byte score type");
+    return static_cast<uint64_t>(static_cast<int64_t>(static_cast<int32_t>(u))) ^ 0x8000000000000000ull;
+  }
+}
+
 constexpr int score_bytes(int t) {
   return t == ST_SCORE_F64 || t == ST_SCORE_I64 ? 8
          : t == ST_SCORE_F32 || t == ST_SCORE_I32 ? 4
@@ -297,6 +308,8 @@ constexpr int kSelectThreads = 1024;
 constexpr int kSelectWaves = kSelectThreads / 64;
 constexpr int kSelectMaxPer = 16;  // keys per thread (64-bit, in registers)
 constexpr int kSelectMaxK = 4096;
+static_assert(kSelectMaxK >= 2 * kSelectThreads && (kSelectThreads & (kSelectThreads - 1)) == 0,
+              "the merge rounds' two run buffers fit s_key / s_idx");
 
 // Exclusive prefix sum over the workgroup of one value per thread (in
 // thread order); *total receives the sum.  Uses scratch[kSelectWaves + 1].
@@ -342,10 +355,35 @@ __global__ __launch_bounds__(kSelectThreads) void fresh_select_kernel(FreshTopkA
   // entries m = tid * kPer + j of the merged row
   uint64_t key[kPer];
   const int64_t m0 = static_cast<int64_t>(tid) * kPer;
+  bool vec = false;
+  if constexpr (score_bytes(kType) == 4 && kPer % 4 == 0) {
+    // 16-byte loads of 4 entries each (a thread's entries are consecutive,
+    // so 4-byte loads would put 64 lanes' accesses 4 * kPer bytes apart):
+    // each piece lies in one part when both parts' lengths are multiples of
+    // 4, and N is then one too
+    vec = a.num_fresh % 4 == 0 && a.num_main % 4 == 0 &&
+          (reinterpret_cast<uintptr_t>(fs) & 15u) == 0 && (reinterpret_cast<uintptr_t>(ms) & 15u) == 0;
+    if (vec) {
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int64_t m = m0 + j;
-    key[j] = m >= N ? 0ull : (m < a.num_fresh ? score_key<kType>(fs, m) : score_key<kType>(ms, m - a.num_fresh));
+      for (int u = 0; u < kPer / 4; ++u) {
+        const int64_t m = m0 + 4 * u;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (m < N)
+          v = *reinterpret_cast<const uint4*>(m < a.num_fresh
+                                                  ? static_cast<const uint32_t*>(fs) + m
+                                                  : static_cast<const uint32_t*>(ms) + (m - a.num_fresh));
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) key[4 * u + e] = m < N ? key_of_bits4<kType>(w[e]) : 0ull;
+      }
+    }
+  }
+  if (!vec) {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int64_t m = m0 + j;
+      key[j] = m >= N ? 0ull : (m < a.num_fresh ? score_key<kType>(fs, m) : score_key<kType>(ms, m - a.num_fresh));
+    }
   }
   // bits in which the row's keys differ
   uint64_t kand = ~0ull, kor = 0ull;
@@ -495,39 +533,68 @@ __global__ __launch_bounds__(kSelectThreads) void fresh_select_kernel(FreshTopkA
     }
   };
   if (n <= kSelectThreads) {
-    // bitonic sort with entry t in thread t's registers, best first: pairs
-    // at a stride below 64 meet within a wave (cross-lane shuffles), wider
-    // ones through LDS
+    // Entry t in thread t's registers.  Each wave sorts its 64 entries best
+    // first (bitonic, lanes exchange by shuffles); then the sorted runs are
+    // merged pairwise through LDS: an entry's place in the merged run is its
+    // place in its own run plus how many entries of the other run go before
+    // it (a binary search; entries of the second run also count the equal
+    // ones, so that equal entries -- the empty padding -- keep distinct
+    // places).
     uint64_t mk = 0ull;
     uint32_t mi = kNoIndex;
     if (tid < n) {
       mk = s_key[tid];
       mi = s_idx[tid];
     }
-    for (int size = 2; size <= n; size <<= 1) {
+    const int wn = n < 64 ? n : 64;
+    for (int size = 2; size <= wn; size <<= 1) {
+      const bool best_first = size == wn || (tid & size) == 0;
       for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        uint64_t pk;
-        uint32_t pi;
-        if (stride >= 64) {
-          __syncthreads();  // the previous exchange's readers are done
-          if (tid < n) {
-            s_key[tid] = mk;
-            s_idx[tid] = mi;
-          }
-          __syncthreads();
-          pk = tid < n ? s_key[tid ^ stride] : 0ull;
-          pi = tid < n ? s_idx[tid ^ stride] : kNoIndex;
-        } else {
-          pk = __shfl_xor(mk, stride, 64);
-          pi = __shfl_xor(mi, stride, 64);
-        }
+        const uint64_t pk = __shfl_xor(mk, stride, 64);
+        const uint32_t pi = __shfl_xor(mi, stride, 64);
         // the lower thread of a pair keeps the entry that goes first in its
-        // size-block's direction (best first when (t & size) == 0)
-        const bool first = ((tid & stride) == 0) == ((tid & size) == 0);
+        // block's direction
+        const bool first = ((tid & stride) == 0) == best_first;
         const bool take = first ? before(pk, pi, mk, mi) : before(mk, mi, pk, pi);
         if (tid < n && take) {
           mk = pk;
           mi = pi;
+        }
+      }
+    }
+    if (n > 64) {
+      // runs in s_key / s_idx [cur, cur + n), merged into the other half
+      int cur = 0;
+      __syncthreads();  // every thread has read its entry
+      if (tid < n) {
+        s_key[tid] = mk;
+        s_idx[tid] = mi;
+      }
+      __syncthreads();
+      for (int len = 64; len < n; len <<= 1) {
+        if (tid < n) {
+          const int pos = tid & (len - 1);
+          const int other = (tid & ~(len - 1)) ^ len;  // first entry of the other run
+          const bool second = (tid & len) != 0;
+          const uint64_t* ok = s_key + cur + other;
+          const uint32_t* oi = s_idx + cur + other;
+          int lo = 0, hi = len;  // entries of the other run that go first: [0, lo)
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            const bool goes_first = second ? !before(mk, mi, ok[mid], oi[mid])
+                                           : before(ok[mid], oi[mid], mk, mi);
+            if (goes_first) lo = mid + 1;
+            else hi = mid;
+          }
+          const int at = (cur ^ kSelectThreads) + (tid & ~(2 * len - 1)) + pos + lo;
+          s_key[at] = mk;
+          s_idx[at] = mi;
+        }
+        __syncthreads();
+        cur ^= kSelectThreads;
+        if (tid < n) {
+          mk = s_key[cur + tid];
+          mi = s_idx[cur + tid];
         }
       }
     }
