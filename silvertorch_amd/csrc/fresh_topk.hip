@@ -303,7 +303,9 @@ __global__ __launch_bounds__(kFreshThreads) void fresh_topk_kernel(FreshTopkArgs
 // bits in which the row's keys differ (8 bits a pass, histogram in LDS)
 // finds the k-th best key T and how many keys exceed it; the entries above
 // T and the lowest-indexed entries equal to T (as many as k needs) are
-// compacted in index order into LDS and sorted (bitonic) best first.
+// compacted in index order into LDS and sorted best first: up to 1,024 of
+// them as 64-entry runs sorted within each wave (bitonic, by shuffles) and
+// merged pairwise through LDS; more by a bitonic network in LDS.
 constexpr int kSelectThreads = 1024;
 constexpr int kSelectWaves = kSelectThreads / 64;
 constexpr int kSelectMaxPer = 16;  // keys per thread (64-bit, in registers)
