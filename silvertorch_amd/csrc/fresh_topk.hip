@@ -339,7 +339,7 @@ __device__ __forceinline__ uint32_t select_scan(uint32_t v, uint32_t* scratch, u
 
 template <int kType, int kPer>
 __global__ __launch_bounds__(kSelectThreads) void fresh_select_kernel(FreshTopkArgs a) {
-  __shared__ uint32_t hist[kSelectWaves][256];  // one histogram per wave
+  __shared__ __align__(16) uint32_t hist[kSelectWaves][256];  // one histogram per wave
   __shared__ uint32_t scan_scratch[kSelectWaves + 1];
   __shared__ uint64_t red_and[kSelectWaves], red_or[kSelectWaves];
   __shared__ uint64_t s_key[kSelectMaxK];
@@ -433,14 +433,16 @@ __global__ __launch_bounds__(kSelectThreads) void fresh_select_kernel(FreshTopkA
     __syncthreads();
     if (wave == 0) {
       // bins from the top digit down: 4 per lane, lane 0 holding 255..252
-      uint32_t c[4], sum = 0;
+      uint32_t c[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        c[i] = 0;
-#pragma unroll
-        for (int w = 0; w < kSelectWaves; ++w) c[i] += hist[w][255 - (lane * 4 + i)];
-        sum += c[i];
+      for (int w = 0; w < kSelectWaves; ++w) {  // bins 252 - 4 lane .. 255 - 4 lane at once
+        const uint4 h = *reinterpret_cast<const uint4*>(&hist[w][252 - lane * 4]);
+        c[0] += h.w;
+        c[1] += h.z;
+        c[2] += h.y;
+        c[3] += h.x;
       }
+      const uint32_t sum = c[0] + c[1] + c[2] + c[3];
       uint32_t incl = sum;
 #pragma unroll
       for (int d = 1; d < 64; d <<= 1) {
