@@ -15,7 +15,8 @@
 // store pattern (four query rows per wave instruction); RUN 2 and 4 measure
 // whether longer runs per query row raise the write rate.  MODE 1 drops the
 // stores (a 16-byte sink per workgroup keeps the loads live), MODE 2 the
-// loads.
+// loads.  Two streaming kernels give the part's contiguous read and write
+// rates for comparison.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -117,6 +118,34 @@ __global__ __launch_bounds__(kThreads) void pattern_probe_kernel(
   if (MODE == 1) sink[blockIdx.x * kThreads + tid] = acc;
 }
 
+// Reference points of the part: the index read as one contiguous stream
+// (non-temporal 16-byte loads, 8 per thread in flight, grid-stride) and the
+// output written as one contiguous stream (plain 16-byte stores), the two
+// forms that measured fastest for each on this part.
+__global__ __launch_bounds__(kThreads) void stream_read_kernel(const u32x4* __restrict__ src,
+                                                                int64_t n, u32x4* __restrict__ sink) {
+  u32x4 acc{0, 0, 0, 0};
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads * 8;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads * 8 + threadIdx.x; base < n;
+       base += stride) {
+    u32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t i = base + static_cast<int64_t>(j) * kThreads;
+      v[j] = i < n ? __builtin_nontemporal_load(src + i) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc ^= v[j];
+  }
+  sink[blockIdx.x * kThreads + threadIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(kThreads) void stream_write_kernel(u32x4* __restrict__ dst, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride)
+    *(PROBE_GLOBAL u32x4*)(dst + i) = u32x4{static_cast<uint32_t>(i), 1u, 2u, 3u};
+}
+
 template <int RUN, int MODE>
 hipError_t launch(const int64_t* index, int64_t numel, const int64_t* bbo, int64_t nb, int64_t Q,
                   void* out, void* sink, int grid, hipStream_t s) {
@@ -128,21 +157,37 @@ hipError_t launch(const int64_t* index, int64_t numel, const int64_t* bbo, int64
 }  // namespace
 
 // Runs the probe once on `stream`.  run: adjacent bundles per group, 1, 2 or
-// 4; mode: 0 loads and stores, 1 loads only, 2 stores only.  out: Q x
-// num_bundles x 256 bytes; sink: grid x 1024 x 16 bytes (mode 1).  Returns 0,
-// or -1 with st_probe_last_error() set.
+// 4; mode: 0 loads and stores, 1 loads only, 2 stores only, 3 the index read
+// as one stream, 4 the output written as one stream (run ignored for 3 and
+// 4).  out: Q x num_bundles x 256 bytes; sink: grid x 1024 x 16 bytes
+// (modes 1 and 3).  Returns 0, or -1 with st_probe_last_error() set.
 extern "C" int st_probe_search_pattern(const int64_t* index, int64_t numel,
                                        const int64_t* bundle_b_offsets, int64_t num_bundles,
                                        int64_t num_queries, void* out, void* sink, int run,
                                        int mode, int grid, void* stream) {
   if (index == nullptr || bundle_b_offsets == nullptr || out == nullptr || sink == nullptr ||
       num_bundles <= 0 || num_queries <= 0 || grid <= 0 || (run != 1 && run != 2 && run != 4) ||
-      mode < 0 || mode > 2) {
+      mode < 0 || mode > 4) {
     g_error = "st_probe_search_pattern: invalid arguments";
     return -1;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
+  if (mode == 3) {
+    hipLaunchKernelGGL(stream_read_kernel, dim3(grid), dim3(kThreads), 0, s,
+                       reinterpret_cast<const u32x4*>(index), numel / 2, static_cast<u32x4*>(sink));
+  } else if (mode == 4) {
+    hipLaunchKernelGGL(stream_write_kernel, dim3(grid), dim3(kThreads), 0, s,
+                       static_cast<u32x4*>(out), num_queries * num_bundles * 16);
+  }
+  if (mode >= 3) {
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+      g_error = std::string("st_probe_search_pattern: ") + hipGetErrorString(e);
+      return -1;
+    }
+    return 0;
+  }
   const int sel = run * 3 + mode;
   switch (sel) {
     case 3: e = launch<1, 0>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s); break;
