@@ -107,6 +107,8 @@ def _capi_topk(ms, fs, k, stype):
 @pytest.mark.parametrize("rows,nf,nm,k,levels", [
     (5, 30, 70, 25, 6),          # heavy ties
     (3, 0, 500, 500, 4),         # main only, k = the whole row
+    (4, 1001, 2999, 1000, 30),   # 1,024 kept: sorted runs merged; parts not multiples of 4
+    (4, 1000, 3000, 1000, 12),   # the same with 16-byte score loads (4-byte types)
     (4, 2000, 0, 64, 50),        # fresh only
     (2, 3000, 9000, 9000, 40),   # kept list in global memory, ties
     (3, 6000, 10384, 4096, 30),  # the largest row and k of the register selection
