@@ -539,22 +539,35 @@ __global__ __launch_bounds__(kKmThreads) __attribute__((amdgpu_waves_per_eu(4)))
 //   kmean_score_kernel   a fixed grid of waves; wave w takes the groups
 //                        [G w / W, G (w + 1) / W) of the G in the call, reads
 //                        each group's 64 ids from the output and scores the
-//                        docs with the staged 64-byte slices of
-//                        kmean_ann_kernel, the loads of the next steps (and
-//                        the next group's ids) in flight while a slice is
-//                        summed.
+//                        docs from 128-byte slices of their rows staged
+//                        through LDS as in kmean_ann_kernel, the loads of the
+//                        next step (and the next group's ids) in flight
+//                        while a slice is summed.
 constexpr int kKmWaveThreads = 256;  // 4 waves per workgroup
 constexpr int kKmWaveDocsPerLane = 64;  // list pass: one 4,096-doc chunk per step
 constexpr int kKmWaveChunk = 64 * kKmWaveDocsPerLane;
-constexpr int kKmWaveStage = 64 * kKmStageStride;
+// scoring stages kKmScoreSlice bytes of each of a group's 64 rows per step:
+// kKmScoreSlice / 16 lanes per row, 64 / (kKmScoreSlice / 16) rows per load
+// instruction, non-temporal; rows padded by 16 bytes so the lanes' 16-byte
+// reads of their own rows fall in distinct banks.  A slice is a whole 128-byte
+// line: with 64-byte slices a line's second half is read a step later from
+// L2, which then has to keep it (plain loads; non-temporal loads of 64-byte
+// slices fetch the line twice).
+constexpr int kKmScoreSlice = 128;
+constexpr int kKmScoreLanes = kKmScoreSlice / 16;
+constexpr int kKmScoreStride = kKmScoreSlice + 16;
+constexpr int kKmScoreThreads = 256;
+constexpr int kKmScorePerCu = 4;  // workgroups per CU at most (LDS permitting)
+constexpr int kKmWaveStage = 64 * kKmScoreStride;
 constexpr int kKmRing = 4;  // groups whose ids and place are held per wave
 constexpr int kKmRingBytes = kKmRing * (64 * 4 + 32);  // ids, then a KmGroup (24 bytes) each
-constexpr int kKmScoreAhead = 2;  // staging steps in flight per scoring wave (4 measured no faster)
+constexpr int kKmScoreAhead = 1;  // staging steps in flight per scoring wave (2 measured no faster)
 // the loads may run kKmScoreAhead groups ahead of the sums (one slice per row)
 static_assert(kKmRing > kKmScoreAhead && (kKmRing & (kKmRing - 1)) == 0, "ring size");
 constexpr int64_t kKmBalancedPairs = 2048;
 constexpr int64_t kKmBalancedMaxRows = 16384;  // rows the single-workgroup prefix takes
 constexpr int kKmWaveMaxLds = 65536;           // dynamic LDS of a score workgroup
+constexpr int kCuLdsBytes = 160 * 1024;        // LDS of a gfx950 CU
 constexpr int kKmGroupsThreads = 1024;
 
 __host__ __device__ constexpr int km_query_bytes(int dim, bool i8) {
@@ -656,6 +669,12 @@ __global__ __launch_bounds__(kKmWaveThreads) void kmean_list_kernel(KmArgs a, co
 }
 
 // Place of a group of 64 slots: row, first slot, filled slots in it.
+typedef uint32_t km_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 km_load_nt16(const char* p) {
+  const km_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const km_u32x4*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 struct KmGroup {
   int64_t b, s0;
   int32_t n, pad;
@@ -663,13 +682,13 @@ struct KmGroup {
 static_assert(sizeof(KmGroup) <= 32, "a ring entry holds 32 bytes");
 
 template <int DT, int ST>
-__global__ __launch_bounds__(kKmWaveThreads) __attribute__((amdgpu_waves_per_eu(4))) void kmean_score_kernel(
+__global__ __launch_bounds__(kKmScoreThreads) __attribute__((amdgpu_waves_per_eu(4))) void kmean_score_kernel(
     KmArgs a, const int64_t* __restrict__ gstart, const int64_t* __restrict__ rowtot, int64_t batch) {
   extern __shared__ __align__(16) char km_lds[];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int64_t nw = static_cast<int64_t>(gridDim.x) * (kKmWaveThreads / 64);
-  const int64_t w = static_cast<int64_t>(blockIdx.x) * (kKmWaveThreads / 64) + wv;
+  const int64_t nw = static_cast<int64_t>(gridDim.x) * (kKmScoreThreads / 64);
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * (kKmScoreThreads / 64) + wv;
   const int64_t G = gstart[batch];
   const int64_t g_lo = G * w / nw, g_hi = G * (w + 1) / nw;
   if (g_lo >= g_hi) return;
@@ -763,29 +782,31 @@ __global__ __launch_bounds__(kKmWaveThreads) __attribute__((amdgpu_waves_per_eu(
   }
   // step t = (group g_lo + t / nslices, 64-byte slice t % nslices)
   const int pieces = static_cast<int>(row_bytes / 16);
-  const int per_slice = kKmSliceBytes / 16;
+  constexpr int per_slice = kKmScoreLanes;
+  constexpr int rows_per_load = 64 / kKmScoreLanes;
   const int nslices = (pieces + per_slice - 1) / per_slice;
   const int elems = DT == kKmF32 ? 4 : (DT == kKmI8 ? 16 : 8);  // per piece
   const int64_t steps = (g_hi - g_lo) * nslices;
-  const int lr = lane >> 2, lp = lane & 3;  // load: row lr + 16 i, piece lp of the slice
-  auto load = [&](int64_t t, uint4 (&buf)[4]) {
+  // load: row lr + rows_per_load i, piece lp of the slice
+  const int lr = lane / kKmScoreLanes, lp = lane % kKmScoreLanes;
+  auto load = [&](int64_t t, uint4 (&buf)[kKmScoreLanes]) {
     const int64_t g = g_lo + t / nslices;
     const int sl = static_cast<int>(t % nslices);
     if (sl == 0) enter(g);
     const int pc = sl * per_slice + lp;
     const int32_t* ids = ring_ids + (g & (kKmRing - 1)) * 64;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int li = lr + 16 * i;
+    for (int i = 0; i < kKmScoreLanes; ++i) {
+      const int li = lr + rows_per_load * i;
       buf[i] = li < lg.n && pc < pieces
-                   ? *reinterpret_cast<const uint4*>(emb + static_cast<size_t>(ids[li]) * row_bytes +
-                                                     static_cast<size_t>(pc) * 16)
+                   ? km_load_nt16(emb + static_cast<size_t>(ids[li]) * row_bytes +
+                                  static_cast<size_t>(pc) * 16)
                    : make_uint4(0u, 0u, 0u, 0u);
     }
   };
   double acc = 0.0;
   int32_t iacc = 0;
-  uint4 buf[kKmScoreAhead][4];
+  uint4 buf[kKmScoreAhead][kKmScoreLanes];
 #pragma unroll
   for (int j = 0; j < kKmScoreAhead; ++j)
     if (j < steps) load(j, buf[j]);
@@ -799,8 +820,8 @@ __global__ __launch_bounds__(kKmWaveThreads) __attribute__((amdgpu_waves_per_eu(
       const KmGroup gr = ring[g & (kKmRing - 1)];
       if (sl == 0 && gr.b != qrow) stage_query(gr.b);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<uint4*>(stg + (lr + 16 * i) * kKmStageStride + lp * 16) = buf[j][i];
+      for (int i = 0; i < kKmScoreLanes; ++i)
+        *reinterpret_cast<uint4*>(stg + (lr + rows_per_load * i) * kKmScoreStride + lp * 16) = buf[j][i];
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
       if (t + kKmScoreAhead < steps) load(t + kKmScoreAhead, buf[j]);
       if (lane < gr.n) {
@@ -808,7 +829,7 @@ __global__ __launch_bounds__(kKmWaveThreads) __attribute__((amdgpu_waves_per_eu(
         for (int q = 0; q < per_slice; ++q) {
           const int pc = sl * per_slice + q;
           if (pc < pieces) {
-            const uint4 v = *reinterpret_cast<const uint4*>(stg + lane * kKmStageStride + q * 16);
+            const uint4 v = *reinterpret_cast<const uint4*>(stg + lane * kKmScoreStride + q * 16);
             acc_piece<DT>(v, qd, qi, pc * elems, acc, iacc);
           }
         }
@@ -900,7 +921,7 @@ void kmean_run(const int64_t* cluster_offsets, int64_t num_offsets, const int64_
                        dim3(kKmCountThreads), 0, s, a, counts, items);
   }
   const int64_t pairs = batch * probes;
-  const int score_lds = (kKmWaveThreads / 64) * km_score_wave_lds(static_cast<int>(dim), emb_dtype == kKmI8);
+  const int score_lds = (kKmScoreThreads / 64) * km_score_wave_lds(static_cast<int>(dim), emb_dtype == kKmI8);
   if (probes > 0 && pairs >= kKmBalancedPairs && batch <= kKmBalancedMaxRows &&
       score_lds <= kKmWaveMaxLds &&
       (counts_capacity < 0 || pairs + km_balanced_extra(batch) <= counts_capacity)) {
@@ -915,17 +936,19 @@ void kmean_run(const int64_t* cluster_offsets, int64_t num_offsets, const int64_
       case kKmBF16: hipLaunchKernelGGL(kmean_list_kernel<kKmBF16>, lgrid, wblock, 0, s, a, counts, rowtot, pairs); break;
       default: hipLaunchKernelGGL(kmean_list_kernel<kKmI32>, lgrid, wblock, 0, s, a, counts, rowtot, pairs);
     }
-    // a fixed grid: 16 waves per CU, every one resident
-    const dim3 sgrid(static_cast<unsigned>(4 * cu_count()));
+    // a fixed grid: as many workgroups per CU as its LDS holds, at most
+    // kKmScorePerCu, every one resident
+    const int per_cu = std::max(1, std::min(kKmScorePerCu, kCuLdsBytes / score_lds));
+    const dim3 sgrid(static_cast<unsigned>(per_cu * cu_count())), sblock(kKmScoreThreads);
     switch (emb_dtype) {
-      case kKmF32: hipLaunchKernelGGL((kmean_score_kernel<kKmF32, kKmF32>), sgrid, wblock, score_lds, s, a, gstart, rowtot, batch); break;
-      case kKmF16: hipLaunchKernelGGL((kmean_score_kernel<kKmF16, kKmF16>), sgrid, wblock, score_lds, s, a, gstart, rowtot, batch); break;
-      case kKmBF16: hipLaunchKernelGGL((kmean_score_kernel<kKmBF16, kKmBF16>), sgrid, wblock, score_lds, s, a, gstart, rowtot, batch); break;
+      case kKmF32: hipLaunchKernelGGL((kmean_score_kernel<kKmF32, kKmF32>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch); break;
+      case kKmF16: hipLaunchKernelGGL((kmean_score_kernel<kKmF16, kKmF16>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch); break;
+      case kKmBF16: hipLaunchKernelGGL((kmean_score_kernel<kKmBF16, kKmBF16>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch); break;
       default:
         if (st == kKmI32)
-          hipLaunchKernelGGL((kmean_score_kernel<kKmI8, kKmI32>), sgrid, wblock, score_lds, s, a, gstart, rowtot, batch);
+          hipLaunchKernelGGL((kmean_score_kernel<kKmI8, kKmI32>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch);
         else
-          hipLaunchKernelGGL((kmean_score_kernel<kKmI8, kKmF16>), sgrid, wblock, score_lds, s, a, gstart, rowtot, batch);
+          hipLaunchKernelGGL((kmean_score_kernel<kKmI8, kKmF16>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
