@@ -29,6 +29,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "../../include/silvertorch_hip.h"
 #include "st_common.hpp"
@@ -654,27 +655,63 @@ int64_t kept_length(int64_t k) {
 }
 
 // Gather of one data tensor: unit e of the output is unit e % D of the
-// source row chosen for output row e / D (D units per row).
-template <typename Idx, typename Elem>
-__global__ void fresh_gather_kernel(const int64_t* __restrict__ top_index, int64_t k,
-                                    int64_t total, const Idx* __restrict__ fresh_idx,
-                                    int64_t fresh_stride, const Idx* __restrict__ main_idx,
-                                    int64_t main_stride, int64_t num_fresh,
-                                    const Elem* __restrict__ fresh_data, int64_t fresh_rows,
-                                    const Elem* __restrict__ main_data, int64_t main_rows,
-                                    int64_t dim, Elem* __restrict__ out) {
-  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (e >= total) return;
-  const int64_t item = e / dim, d = e - item * dim;
-  const int64_t row = item / k;
-  const int64_t t = top_index[item];
-  const bool fresh = t < num_fresh;
-  int64_t src = fresh ? static_cast<int64_t>(fresh_idx[row * fresh_stride + t])
-                      : static_cast<int64_t>(main_idx[row * main_stride + (t - num_fresh)]);
-  const int64_t rows = fresh ? fresh_rows : main_rows;
-  if (src < 0 || src >= rows) src = 0;  // padded offsets read row 0
-  const Elem* data = fresh ? fresh_data : main_data;
-  out[e] = rows > 0 ? data[src * dim + d] : Elem{};
+// source row chosen for output row e / D (D units per row).  A thread moves
+// kGatherPer units a grid apart and issues every load (the top-k entry, the
+// index entry, the data unit) for all of them before its stores, so that
+// kGatherPer dependent load chains are in flight per thread (2 or 8 per
+// thread, or non-temporal row loads, measured slower).  Index arithmetic is
+// 32-bit when the unit count fits (Narrow).
+constexpr int kGatherPer = 4;
+constexpr int kGatherThreads = 256;
+
+template <typename Idx, typename Elem, bool Narrow>
+__global__ __launch_bounds__(kGatherThreads) void fresh_gather_kernel(
+    const int64_t* __restrict__ top_index, int64_t k, int64_t total,
+    const Idx* __restrict__ fresh_idx, int64_t fresh_stride, const Idx* __restrict__ main_idx,
+    int64_t main_stride, int64_t num_fresh, const Elem* __restrict__ fresh_data,
+    int64_t fresh_rows, const Elem* __restrict__ main_data, int64_t main_rows, int64_t dim,
+    Elem* __restrict__ out) {
+  using U = typename std::conditional<Narrow, uint32_t, int64_t>::type;
+  const U nt = static_cast<U>(gridDim.x) * kGatherThreads;
+  const U e0 = static_cast<U>(blockIdx.x) * kGatherThreads + threadIdx.x;
+  const U tot = static_cast<U>(total), D = static_cast<U>(dim), K = static_cast<U>(k);
+  int64_t t[kGatherPer];
+  U item[kGatherPer];
+#pragma unroll
+  for (int j = 0; j < kGatherPer; ++j) {
+    const U e = e0 + static_cast<U>(j) * nt;
+    item[j] = e / D;
+    t[j] = e < tot ? top_index[item[j]] : 0;
+  }
+  int64_t src[kGatherPer];
+#pragma unroll
+  for (int j = 0; j < kGatherPer; ++j) {
+    const U e = e0 + static_cast<U>(j) * nt;
+    const int64_t row = static_cast<int64_t>(item[j] / K);
+    const bool fresh = t[j] < num_fresh;
+    src[j] = e >= tot ? 0
+             : fresh  ? static_cast<int64_t>(fresh_idx[row * fresh_stride + t[j]])
+                      : static_cast<int64_t>(main_idx[row * main_stride + (t[j] - num_fresh)]);
+  }
+  Elem v[kGatherPer];
+#pragma unroll
+  for (int j = 0; j < kGatherPer; ++j) {
+    const U e = e0 + static_cast<U>(j) * nt;
+    const U d = e - item[j] * D;
+    const bool fresh = t[j] < num_fresh;
+    const int64_t rows = fresh ? fresh_rows : main_rows;
+    int64_t r = src[j];
+    if (r < 0 || r >= rows) r = 0;  // padded offsets read row 0
+    const Elem* data = fresh ? fresh_data : main_data;
+    v[j] = e < tot && rows > 0
+               ? data[r * static_cast<int64_t>(D) + static_cast<int64_t>(d)]
+               : Elem{};
+  }
+#pragma unroll
+  for (int j = 0; j < kGatherPer; ++j) {
+    const U e = e0 + static_cast<U>(j) * nt;
+    if (e < tot) out[e] = v[j];
+  }
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -695,15 +732,24 @@ void launch_gather_idx(const int64_t* top_index, int64_t rows, int64_t k, const 
   while (unit > 1 && (row_bytes % unit != 0 || align % unit != 0)) unit >>= 1;
   const int64_t units = row_bytes / unit;
   const int64_t total = rows * k * units;
-  const int threads = 256;
-  ST_CHECK((total + threads - 1) / threads <= 0x7FFFFFFF, "gather of ", total, " units is too large");
-  const dim3 grid(static_cast<unsigned>((total + threads - 1) / threads));
+  const int64_t per_block = static_cast<int64_t>(kGatherThreads) * kGatherPer;
+  ST_CHECK((total + per_block - 1) / per_block <= 0x7FFFFFFF, "gather of ", total, " units is too large");
+  const dim3 grid(static_cast<unsigned>((total + per_block - 1) / per_block));
+  // 32-bit arithmetic when every unit number a thread forms (below the
+  // grid's threads x kGatherPer) fits
+  const bool narrow = static_cast<int64_t>(grid.x) * per_block <= static_cast<int64_t>(UINT32_MAX);
   auto go = [&](auto tag) {
     using E = decltype(tag);
-    hipLaunchKernelGGL((fresh_gather_kernel<Idx, E>), grid, dim3(threads), 0, s, top_index, k,
-                       total, static_cast<const Idx*>(fi), fs, static_cast<const Idx*>(mi), ms,
-                       num_fresh, static_cast<const E*>(fd), frows, static_cast<const E*>(md),
-                       mrows, units, static_cast<E*>(out));
+    if (narrow)
+      hipLaunchKernelGGL((fresh_gather_kernel<Idx, E, true>), grid, dim3(kGatherThreads), 0, s,
+                         top_index, k, total, static_cast<const Idx*>(fi), fs,
+                         static_cast<const Idx*>(mi), ms, num_fresh, static_cast<const E*>(fd),
+                         frows, static_cast<const E*>(md), mrows, units, static_cast<E*>(out));
+    else
+      hipLaunchKernelGGL((fresh_gather_kernel<Idx, E, false>), grid, dim3(kGatherThreads), 0, s,
+                         top_index, k, total, static_cast<const Idx*>(fi), fs,
+                         static_cast<const Idx*>(mi), ms, num_fresh, static_cast<const E*>(fd),
+                         frows, static_cast<const E*>(md), mrows, units, static_cast<E*>(out));
   };
   switch (unit) {
     case 1: go(uint8_t{}); break;
