@@ -54,6 +54,13 @@ typedef int64_t i64x2_u __attribute__((ext_vector_type(2), aligned(8)));
 constexpr int kScanThreads = 1024;
 constexpr int kScanPerThread = 8;
 constexpr int kScanTile = kScanThreads * kScanPerThread;
+// the per-tile passes (reduce, apply) take tiles of kPartTile counts, 256
+// threads each, so that a call's tiles cover the CUs (cfg2: 610 tiles)
+constexpr int kPartThreads = 256;
+constexpr int kPartTile = kPartThreads * kScanPerThread;
+// up to this many tiles the apply pass sums the tile sums before its own
+// tile itself (no separate scan of the tile sums; at most ~4 MB of L2 reads)
+constexpr int64_t kPartPrefixTiles = 1024;
 
 // The lane's 32 doc bits of item (q, ch), masked to docs < num_docs; bit 31
 // is the lane's first doc, whose offset within the chunk is 32 * lane.
@@ -172,19 +179,27 @@ __device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* tota
   return before + x - v;
 }
 
-// Phase 1: sum of each tile of kScanTile counts.
-__global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(
+// Phase 1: sum of each tile of kPartTile counts (coalesced loads).
+__global__ __launch_bounds__(kPartThreads) void scan_reduce_kernel(
     const int64_t* __restrict__ data, int64_t n, int64_t* __restrict__ tile_sums) {
-  const int64_t start = static_cast<int64_t>(blockIdx.x) * kScanTile;
+  __shared__ int64_t wave_sum[kPartThreads / 64];
+  const int64_t start = static_cast<int64_t>(blockIdx.x) * kPartTile;
   int64_t s = 0;
 #pragma unroll
   for (int j = 0; j < kScanPerThread; ++j) {
-    const int64_t i = start + static_cast<int64_t>(j) * kScanThreads + threadIdx.x;
+    const int64_t i = start + static_cast<int64_t>(j) * kPartThreads + threadIdx.x;
     if (i < n) s += data[i];
   }
-  int64_t total;
-  block_exclusive_scan(s, &total);
-  if (threadIdx.x == 0) tile_sums[blockIdx.x] = total;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+  if ((threadIdx.x & 63) == 0) wave_sum[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t t = 0;
+#pragma unroll
+    for (int w = 0; w < kPartThreads / 64; ++w) t += wave_sum[w];
+    tile_sums[blockIdx.x] = t;
+  }
 }
 
 // Phase 2: exclusive scan of the tile sums in place (one workgroup); the
@@ -216,34 +231,86 @@ __global__ __launch_bounds__(kScanThreads) void scan_tiles_kernel(
 }
 
 // Phase 3: exclusive scan within each tile plus the tile's offset, in place;
-// items (q, 0) give row_offsets[q].
-__global__ __launch_bounds__(kScanThreads) void scan_apply_kernel(
+// items (q, 0) give row_offsets[q].  The tile goes through LDS so that the
+// global loads and stores are coalesced while each thread scans 8
+// consecutive counts; the LDS copy has one pad entry per 8 so that those
+// reads (72 bytes apart across lanes) spread over the banks.
+__device__ __forceinline__ int part_slot(int e) { return e + (e >> 3); }
+
+// With kPrefix the tile sums are not scanned beforehand: each workgroup
+// sums those of the tiles before its own (calls of at most kPartPrefixTiles
+// tiles), and the last one writes the total to row_offsets[num_queries].
+template <bool kPrefix>
+__global__ __launch_bounds__(kPartThreads) void scan_apply_kernel(
     int64_t* __restrict__ data, int64_t n, const int64_t* __restrict__ tile_offsets,
-    int64_t nch, int64_t* __restrict__ row_offsets) {
-  const int64_t start = static_cast<int64_t>(blockIdx.x) * kScanTile +
-                        static_cast<int64_t>(threadIdx.x) * kScanPerThread;
+    int64_t nch, int64_t* __restrict__ row_offsets, int64_t num_queries) {
+  __shared__ int64_t tile[kPartTile + kPartTile / 8];
+  __shared__ int64_t wave_tot[kPartThreads / 64];
+  __shared__ int64_t wave_pre[kPartThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t start = static_cast<int64_t>(blockIdx.x) * kPartTile;
+  if constexpr (kPrefix) {
+    int64_t pre = 0;
+    for (uint32_t t = tid; t < blockIdx.x; t += kPartThreads) pre += tile_offsets[t];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) pre += __shfl_xor(pre, off, 64);
+    if (lane == 0) wave_pre[wave] = pre;
+  }
+#pragma unroll
+  for (int j = 0; j < kScanPerThread; ++j) {
+    const int e = j * kPartThreads + tid;
+    tile[part_slot(e)] = start + e < n ? data[start + e] : 0;
+  }
+  __syncthreads();
   int64_t v[kScanPerThread];
   int64_t s = 0;
 #pragma unroll
   for (int j = 0; j < kScanPerThread; ++j) {
-    v[j] = start + j < n ? data[start + j] : 0;
+    v[j] = tile[part_slot(tid * kScanPerThread + j)];
     s += v[j];
   }
-  int64_t total;
-  int64_t run = tile_offsets[blockIdx.x] + block_exclusive_scan(s, &total);
-  int64_t q = start / nch, r = start - (start / nch) * nch;
+  int64_t x = s;  // inclusive scan of the thread sums over the wave
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int64_t y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) wave_tot[wave] = x;
+  __syncthreads();
+  int64_t base;
+  if constexpr (kPrefix) {
+    base = 0;
+#pragma unroll
+    for (int w = 0; w < kPartThreads / 64; ++w) base += wave_pre[w];
+    if (blockIdx.x == gridDim.x - 1 && tid == kPartThreads - 1) {
+      int64_t tot = base;
+#pragma unroll
+      for (int w = 0; w < kPartThreads / 64; ++w) tot += wave_tot[w];
+      row_offsets[num_queries] = tot;
+    }
+  } else {
+    base = tile_offsets[blockIdx.x];
+  }
+  int64_t run = base + x - s;
+#pragma unroll
+  for (int w = 0; w < kPartThreads / 64; ++w) run += w < wave ? wave_tot[w] : 0;
+  const int64_t first = start + static_cast<int64_t>(tid) * kScanPerThread;
+  int64_t q = first / nch, r = first - q * nch;
 #pragma unroll
   for (int j = 0; j < kScanPerThread; ++j) {
-    const int64_t i = start + j;
-    if (i < n) {
-      data[i] = run;
-      if (r == 0) row_offsets[q] = run;
-    }
+    if (first + j < n && r == 0) row_offsets[q] = run;
+    tile[part_slot(tid * kScanPerThread + j)] = run;
     run += v[j];
     if (++r == nch) {
       r = 0;
       ++q;
     }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kScanPerThread; ++j) {
+    const int e = j * kPartThreads + tid;
+    if (start + e < n) data[start + e] = tile[part_slot(e)];
   }
 }
 
@@ -406,16 +473,24 @@ void check_shape(int64_t num_queries, int64_t num_columns, int64_t num_docs) {
 void compact_scan_counts(int64_t* counts, int64_t num_queries, int64_t nch,
                          int64_t* row_offsets, hipStream_t s) {
   const int64_t items = num_queries * nch;
-  const int64_t tiles = (items + kScanTile - 1) / kScanTile;
+  const int64_t tiles = (items + kPartTile - 1) / kPartTile;
   int64_t* tile_sums = counts + items;
   hipLaunchKernelGGL(scan_reduce_kernel, dim3(static_cast<unsigned>(tiles)),
-                     dim3(kScanThreads), 0, s, counts, items, tile_sums);
+                     dim3(kPartThreads), 0, s, counts, items, tile_sums);
   check_launch("scan_reduce_kernel");
+  if (tiles <= kPartPrefixTiles) {
+    hipLaunchKernelGGL(scan_apply_kernel<true>, dim3(static_cast<unsigned>(tiles)),
+                       dim3(kPartThreads), 0, s, counts, items, tile_sums, nch, row_offsets,
+                       num_queries);
+    check_launch("scan_apply_kernel");
+    return;
+  }
   hipLaunchKernelGGL(scan_tiles_kernel, dim3(1), dim3(kScanThreads), 0, s, tile_sums, tiles,
                      row_offsets, num_queries);
   check_launch("scan_tiles_kernel");
-  hipLaunchKernelGGL(scan_apply_kernel, dim3(static_cast<unsigned>(tiles)),
-                     dim3(kScanThreads), 0, s, counts, items, tile_sums, nch, row_offsets);
+  hipLaunchKernelGGL(scan_apply_kernel<false>, dim3(static_cast<unsigned>(tiles)),
+                     dim3(kPartThreads), 0, s, counts, items, tile_sums, nch, row_offsets,
+                     num_queries);
   check_launch("scan_apply_kernel");
 }
 
@@ -430,7 +505,7 @@ void compact_zero_offsets(int64_t* row_offsets, int64_t n, hipStream_t s) {
 extern "C" int64_t st_bloom_compact_workspace_bytes(int64_t num_queries, int64_t num_columns) {
   if (num_queries <= 0 || num_columns <= 0) return 0;
   const int64_t items = num_queries * st::num_chunks(num_columns);
-  const int64_t tiles = (items + st::kScanTile - 1) / st::kScanTile;
+  const int64_t tiles = (items + st::kPartTile - 1) / st::kPartTile;
   return 8 * (items + tiles);
 }
 

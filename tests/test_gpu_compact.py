@@ -44,6 +44,45 @@ def test_compact_random_masks(shape, int64_ids):
             assert ids.dtype == (np.int64 if int64_ids else np.int32)
 
 
+def test_compact_more_tiles_than_the_folded_prefix_takes():
+    """1,100 queries x 1,920 chunks = 2.11 M chunk counts, more than the
+    1,024 scan tiles of 2,048 whose prefix the apply pass sums itself, so the
+    tile sums get their own scan pass.  The mask is built on the device from
+    planted ids (a few per row, some past num_docs, one row empty, one row
+    with a whole chunk set); the expected output is those ids in order."""
+    q, nch = 1100, 1920
+    c = 32 * nch
+    nd = c * 64 - 1000
+    rng = np.random.default_rng(11)
+    rows, ids = [], []
+    for r in range(q):
+        if r == 5:
+            chosen = np.arange(64 * 32 * 7, 64 * 32 * 8)  # chunk 7 full
+        elif r == 6:
+            chosen = np.zeros(0, np.int64)
+        else:
+            chosen = rng.choice(c * 64, size=int(rng.integers(1, 40)), replace=False)
+            if r % 97 == 0:
+                chosen = np.concatenate([chosen, np.arange(nd - 3, nd + 5)])
+        chosen = np.unique(chosen.astype(np.int64))
+        rows.append(np.full(chosen.size, r, np.int64))
+        ids.append(chosen)
+    rows, ids = np.concatenate(rows), np.concatenate(ids)
+    flat = torch.zeros(q * c, dtype=torch.long, device="cuda")
+    word = torch.as_tensor(rows * c + (ids >> 6)).cuda()
+    # distinct bits of one word sum to their OR (bit 63 is -2^63 in int64)
+    bit = torch.as_tensor(np.left_shift(np.uint64(1), (63 - (ids & 63)).astype(np.uint64)).view(np.int64)).cuda()
+    flat.index_add_(0, word, bit)
+    packed = flat.view(q, c)
+    H.note(f"[compact] planted ids q={q} c={c} num_docs={nd}")
+    got_ids, got_ro = H.compact(packed, nd)
+    keep = ids < nd
+    want_ids = ids[keep]
+    want_ro = np.concatenate([[0], np.cumsum(np.bincount(rows[keep], minlength=q))])
+    np.testing.assert_array_equal(got_ro, want_ro)
+    np.testing.assert_array_equal(got_ids.astype(np.int64), want_ids)
+
+
 def test_compact_cfg1_search_output():
     """The cfg1 search output (README-scale corpus, 32 queries) end to end."""
     from silvertorch_amd import synthetic as S
