@@ -673,7 +673,9 @@ __device__ __forceinline__ void store_quad(const SearchArgs& a, int lane, int64_
 }
 
 // Bool output of a quad: the four 2 KB rows of the wave's four programs,
-// each written as two 1 KB stores of 16 consecutive bytes per lane.  Lane l
+// each written as two 1 KB stores of 16 consecutive bytes per lane (plain
+// stores: at cfg2, whose bool output is 2.56 GB against 563 MB of index,
+// they measured 633-639 us against 646-649 us non-temporal).  Lane l
 // of a store covers docs 1024 j + 16 l .. +15, i.e. one half of a packed
 // 32-doc word that sits in another lane of the program's group: the four
 // components of that lane are fetched with ds_bpermute and the lane's one is
@@ -705,7 +707,7 @@ __device__ __forceinline__ void store_quad_bool(const SearchArgs& a, int lane, i
       o.y = (((y >> 4) & 0xFu) * 0x00204081u) & 0x01010101u;
       o.z = (((y >> 8) & 0xFu) * 0x00204081u) & 0x01010101u;
       o.w = (((y >> 12) & 0xFu) * 0x00204081u) & 0x01010101u;
-      __builtin_nontemporal_store(o, (ST_GLOBAL u32x4*)(base + 1024 * j + 16 * lane));
+      *(ST_GLOBAL u32x4*)(base + 1024 * j + 16 * lane) = o;
     }
   }
 }
