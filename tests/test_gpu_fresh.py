@@ -180,6 +180,49 @@ def test_op_gather_dtypes_and_clamping_vs_oracle(index_dtype):
         np.testing.assert_array_equal(conv(got), w, err_msg=x)
 
 
+def test_op_gather_many_keys_wide_rows_and_unaligned_data_vs_oracle():
+    """Ten keys, rows of 2,400 bytes (150 16-byte units), rows whose data
+    pointer is only 2-byte aligned (2-byte units), 1-byte rows, a dim-0
+    tensor, int64 ids."""
+    rng = np.random.default_rng(23)
+    R, nf, nm, k = 5, 30, 70, 40
+    ms = torch.from_numpy(rng.standard_normal((R, nm)).astype(np.float32))
+    fs = torch.from_numpy(rng.standard_normal((R, nf)).astype(np.float32))
+    mi = torch.from_numpy(rng.integers(-2, 25, (R, nm)))
+    fi = torch.from_numpy(rng.integers(-2, 9, (R, nf)))
+
+    def unaligned_bf16(rows, dim):  # contiguous, data pointer 2 bytes past a 16-byte boundary
+        base = torch.from_numpy(rng.standard_normal(rows * dim + 1).astype(np.float32)).to(torch.bfloat16).cuda()
+        return base[1:].view(rows, dim)
+
+    main = {"wide": torch.from_numpy(rng.standard_normal((24, 600)).astype(np.float32)).cuda(),
+            "bf_odd": unaligned_bf16(24, 7),
+            "u8": torch.from_numpy(rng.integers(0, 255, (24,)).astype(np.uint8)).cuda(),
+            "ids": torch.from_numpy(rng.integers(0, 2**40, (24,))).cuda(),
+            "zero": torch.zeros((24, 0), dtype=torch.float32).cuda()}
+    fresh = {"wide": torch.from_numpy(rng.standard_normal((8, 600)).astype(np.float32)).cuda(),
+             "bf_odd": unaligned_bf16(8, 7),
+             "u8": torch.from_numpy(rng.integers(0, 255, (8,)).astype(np.uint8)).cuda(),
+             "ids": torch.from_numpy(rng.integers(0, 2**40, (8,))).cuda(),
+             "zero": torch.zeros((8, 0), dtype=torch.float32).cuda()}
+    for j in range(5):
+        main[f"i32_{j}"] = torch.from_numpy(rng.integers(-99, 99, (24, j + 1)).astype(np.int32)).cuda()
+        fresh[f"i32_{j}"] = torch.from_numpy(rng.integers(-99, 99, (8, j + 1)).astype(np.int32)).cuda()
+    keys = list(main)
+    assert len(keys) == 10 and main["bf_odd"].data_ptr() % 16 == 2
+    _, ti, _, g = torch.ops.st.take_top_k_and_gather_from_main_and_fresh(
+        ms.cuda(), fs.cuda(), mi.cuda(), fi.cuda(), k, keys, [main[x] for x in keys],
+        [fresh[x] for x in keys], 1)
+    conv = lambda t: t.float().cpu().numpy() if t.dtype == torch.bfloat16 else t.cpu().numpy()  # noqa: E731
+    _, wi, _, wg = O.fresh_topk_gather(ms.numpy(), fs.numpy(), mi.numpy(), fi.numpy(), k,
+                                       [conv(main[x]) for x in keys], [conv(fresh[x]) for x in keys])
+    np.testing.assert_array_equal(ti.cpu().numpy(), wi)
+    for x, w in zip(keys, wg):
+        got = conv(g[x])
+        assert got.shape == tuple(w.shape), x
+        np.testing.assert_array_equal(got, w, err_msg=x)
+
+
 def test_op_argument_errors():
     st = torch.ops.st
     ms = torch.rand(2, 5, device="cuda")
