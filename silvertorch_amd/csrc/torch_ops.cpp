@@ -540,31 +540,34 @@ std::tuple<Tensor, Tensor, Tensor> partial_chunk(const PartialPlan& pp, const Te
   const Tensor& cl = host.cl;
   const Tensor& pi = host.pi;
   const int64_t rows = co.size(0), clusters = co.size(1), n = rows * clusters;
-  const auto pinned = at::TensorOptions().pinned_memory(true);
-  Tensor cumsum = at::empty({n}, pinned.dtype(at::kInt)), first = at::empty({n}, pinned.dtype(at::kChar));
-  Tensor items = at::empty({std::max<int64_t>(n, 1) * static_cast<int64_t>(sizeof(st_partial_item))},
-                           at::TensorOptions().dtype(at::kByte).pinned_memory(true));
+  // the work items, the column cumsum and the first bits in one pinned block
+  // and one copy to the device; the returned cumsum and first are views of
+  // the device block (one copy and allocation per call instead of three)
+  const int64_t items_bytes =
+      (std::max<int64_t>(n, 1) * static_cast<int64_t>(sizeof(st_partial_item)) + 15) / 16 * 16;
+  const int64_t off_cumsum = items_bytes, off_first = items_bytes + (4 * n + 15) / 16 * 16;
+  const int64_t block_bytes = off_first + std::max<int64_t>(n, 1);
+  Tensor host_block = at::empty({block_bytes}, at::TensorOptions().dtype(at::kByte).pinned_memory(true));
+  uint8_t* hb = host_block.data_ptr<uint8_t>();
   int64_t num_items = 0, total = 0;
   check_st(st_search_plan_partial_items(pp.plan.p, co.data_ptr<int64_t>(), cl.data_ptr<int64_t>(), rows,
                                         clusters, pi.defined() ? pi.data_ptr<int64_t>() : nullptr,
-                                        bbo.numel() - 1, cumsum.data_ptr<int32_t>(),
-                                        first.data_ptr<int8_t>(),
-                                        reinterpret_cast<st_partial_item*>(items.data_ptr()),
-                                        &num_items, &total),
+                                        bbo.numel() - 1, reinterpret_cast<int32_t*>(hb + off_cumsum),
+                                        reinterpret_cast<int8_t*>(hb + off_first),
+                                        reinterpret_cast<st_partial_item*>(hb), &num_items, &total),
            "bloom_index_search_batch_return_partial_response");
+  const Tensor block = host_block.to(dev, /*non_blocking=*/true);
   Tensor mask = at::empty({total}, at::TensorOptions().dtype(at::kLong).device(dev));
   if (num_items > 0) {
-    const Tensor items_d = items.to(dev, /*non_blocking=*/true);
     check_st(st_bloom_index_search_partial(index.data_ptr<int64_t>(), index.numel(),
                                            bbo.data_ptr<int64_t>(), bbo.numel() - 1, pp.plan.p,
                                            pp.blob.data_ptr(),
-                                           reinterpret_cast<const st_partial_item*>(items_d.data_ptr()),
+                                           reinterpret_cast<const st_partial_item*>(block.data_ptr()),
                                            num_items, mask.data_ptr<int64_t>(), current_stream(index)),
              "bloom_index_search_batch_return_partial_response");
-    // items_d is freed here; the caching allocator keeps it until the stream
-    // has used it (record_stream semantics of the current stream)
   }
-  return {cumsum.to(dev, /*non_blocking=*/true), first.to(dev, /*non_blocking=*/true), mask};
+  return {block.narrow(0, off_cumsum, 4 * n).view(at::kInt), block.narrow(0, off_first, n).view(at::kChar),
+          mask};
 }
 
 void sync_current_stream(at::Device dev) {
