@@ -32,6 +32,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <mutex>
+#include <type_traits>
 
 #include "st_common.hpp"
 #include "st_errors.hpp"
@@ -539,31 +540,33 @@ __global__ __launch_bounds__(kKmThreads) __attribute__((amdgpu_waves_per_eu(4)))
 //   kmean_score_kernel   a fixed grid of waves; wave w takes the groups
 //                        [G w / W, G (w + 1) / W) of the G in the call, reads
 //                        each group's 64 ids from the output and scores the
-//                        docs from 128-byte slices of their rows staged
-//                        through LDS as in kmean_ann_kernel, the loads of the
-//                        next step (and the next group's ids) in flight
-//                        while a slice is summed.
+//                        docs from 128-byte slices of their rows (64-byte
+//                        for the longest rows) staged through LDS as in
+//                        kmean_ann_kernel, the loads of the next step (and
+//                        the next group's ids) in flight while a slice is
+//                        summed.
 constexpr int kKmWaveThreads = 256;  // 4 waves per workgroup
 constexpr int kKmWaveDocsPerLane = 64;  // list pass: one 4,096-doc chunk per step
 constexpr int kKmWaveChunk = 64 * kKmWaveDocsPerLane;
-// scoring stages kKmScoreSlice bytes of each of a group's 64 rows per step:
-// kKmScoreSlice / 16 lanes per row, 64 / (kKmScoreSlice / 16) rows per load
-// instruction, non-temporal; rows padded by 16 bytes so the lanes' 16-byte
-// reads of their own rows fall in distinct banks.  A slice is a whole 128-byte
-// line: with 64-byte slices a line's second half is read a step later from
-// L2, which then has to keep it (plain loads; non-temporal loads of 64-byte
-// slices fetch the line twice).
-constexpr int kKmScoreSlice = 128;
-constexpr int kKmScoreLanes = kKmScoreSlice / 16;
-constexpr int kKmScoreStride = kKmScoreSlice + 16;
+// scoring stages SL bytes of each of a group's 64 rows per step (SL = 128 or
+// 64, a template parameter of kmean_score_kernel): SL / 16 lanes per row,
+// 64 / (SL / 16) rows per load instruction; rows padded by 16 bytes so the
+// lanes' 16-byte reads of their own rows fall in distinct banks.  A 128-byte
+// slice is a whole line, loaded non-temporal with one step in flight (2
+// measured no faster); with 64-byte slices a line's second half is read a
+// step later from L2, which then has to keep it, so those loads are plain
+// (non-temporal ones fetch the line twice), two steps in flight.  64-byte
+// slices serve the dims whose 128-byte tile leaves no room for the query.
 constexpr int kKmScoreThreads = 256;
 constexpr int kKmScorePerCu = 4;  // workgroups per CU at most (LDS permitting)
-constexpr int kKmWaveStage = 64 * kKmScoreStride;
+__host__ __device__ constexpr int km_score_stage(int slice) { return 64 * (slice + 16); }
 constexpr int kKmRing = 4;  // groups whose ids and place are held per wave
 constexpr int kKmRingBytes = kKmRing * (64 * 4 + 32);  // ids, then a KmGroup (24 bytes) each
-constexpr int kKmScoreAhead = 1;  // staging steps in flight per scoring wave (2 measured no faster)
-// the loads may run kKmScoreAhead groups ahead of the sums (one slice per row)
-static_assert(kKmRing > kKmScoreAhead && (kKmRing & (kKmRing - 1)) == 0, "ring size");
+__host__ __device__ constexpr int km_score_ahead(int slice) { return slice == 128 ? 1 : 2; }
+// the loads may run km_score_ahead groups ahead of the sums (one slice per row)
+static_assert(kKmRing > km_score_ahead(64) && kKmRing > km_score_ahead(128) &&
+                  (kKmRing & (kKmRing - 1)) == 0,
+              "ring size");
 constexpr int64_t kKmBalancedPairs = 2048;
 constexpr int64_t kKmBalancedMaxRows = 16384;  // rows the single-workgroup prefix takes
 constexpr int kKmWaveMaxLds = 65536;           // dynamic LDS of a score workgroup
@@ -573,8 +576,8 @@ constexpr int kKmGroupsThreads = 1024;
 __host__ __device__ constexpr int km_query_bytes(int dim, bool i8) {
   return ((i8 ? dim : 8 * dim) + 15) / 16 * 16;
 }
-__host__ __device__ constexpr int km_score_wave_lds(int dim, bool i8) {
-  return km_query_bytes(dim, i8) + kKmWaveStage + kKmRingBytes;
+__host__ __device__ constexpr int km_score_wave_lds(int dim, bool i8, int slice) {
+  return km_query_bytes(dim, i8) + km_score_stage(slice) + kKmRingBytes;
 }
 
 // Workspace of the balanced form after the batch x probes counts, int64:
@@ -681,7 +684,7 @@ struct KmGroup {
 };
 static_assert(sizeof(KmGroup) <= 32, "a ring entry holds 32 bytes");
 
-template <int DT, int ST>
+template <int DT, int ST, int SL>
 __global__ __launch_bounds__(kKmScoreThreads) __attribute__((amdgpu_waves_per_eu(4))) void kmean_score_kernel(
     KmArgs a, const int64_t* __restrict__ gstart, const int64_t* __restrict__ rowtot, int64_t batch) {
   extern __shared__ __align__(16) char km_lds[];
@@ -693,11 +696,12 @@ __global__ __launch_bounds__(kKmScoreThreads) __attribute__((amdgpu_waves_per_eu
   const int64_t g_lo = G * w / nw, g_hi = G * (w + 1) / nw;
   if (g_lo >= g_hi) return;
   const int dim = a.dim;
-  char* mine = km_lds + wv * km_score_wave_lds(dim, DT == kKmI8);
+  constexpr int kLanes = SL / 16, kStride = SL + 16, kAhead = km_score_ahead(SL);
+  char* mine = km_lds + wv * km_score_wave_lds(dim, DT == kKmI8, SL);
   double* qd = reinterpret_cast<double*>(mine);
   int8_t* qi = reinterpret_cast<int8_t*>(mine);
   char* stg = mine + km_query_bytes(dim, DT == kKmI8);
-  int32_t* ring_ids = reinterpret_cast<int32_t*>(stg + kKmWaveStage);  // [kKmRing][64]
+  int32_t* ring_ids = reinterpret_cast<int32_t*>(stg + km_score_stage(SL));  // [kKmRing][64]
   KmGroup* ring = reinterpret_cast<KmGroup*>(ring_ids + kKmRing * 64);
 
   // row cursor of the next group to be placed: the largest row b with
@@ -780,39 +784,41 @@ __global__ __launch_bounds__(kKmScoreThreads) __attribute__((amdgpu_waves_per_eu
     }
     return;
   }
-  // step t = (group g_lo + t / nslices, 64-byte slice t % nslices)
+  // step t = (group g_lo + t / nslices, SL-byte slice t % nslices)
   const int pieces = static_cast<int>(row_bytes / 16);
-  constexpr int per_slice = kKmScoreLanes;
-  constexpr int rows_per_load = 64 / kKmScoreLanes;
+  constexpr int per_slice = kLanes;
+  constexpr int rows_per_load = 64 / kLanes;
   const int nslices = (pieces + per_slice - 1) / per_slice;
   const int elems = DT == kKmF32 ? 4 : (DT == kKmI8 ? 16 : 8);  // per piece
   const int64_t steps = (g_hi - g_lo) * nslices;
   // load: row lr + rows_per_load i, piece lp of the slice
-  const int lr = lane / kKmScoreLanes, lp = lane % kKmScoreLanes;
-  auto load = [&](int64_t t, uint4 (&buf)[kKmScoreLanes]) {
+  const int lr = lane / kLanes, lp = lane % kLanes;
+  auto load = [&](int64_t t, uint4 (&buf)[kLanes]) {
     const int64_t g = g_lo + t / nslices;
     const int sl = static_cast<int>(t % nslices);
     if (sl == 0) enter(g);
     const int pc = sl * per_slice + lp;
     const int32_t* ids = ring_ids + (g & (kKmRing - 1)) * 64;
 #pragma unroll
-    for (int i = 0; i < kKmScoreLanes; ++i) {
+    for (int i = 0; i < kLanes; ++i) {
       const int li = lr + rows_per_load * i;
-      buf[i] = li < lg.n && pc < pieces
-                   ? km_load_nt16(emb + static_cast<size_t>(ids[li]) * row_bytes +
-                                  static_cast<size_t>(pc) * 16)
-                   : make_uint4(0u, 0u, 0u, 0u);
+      const char* src = emb + static_cast<size_t>(ids[li]) * row_bytes + static_cast<size_t>(pc) * 16;
+      if constexpr (SL == 128)
+        buf[i] = li < lg.n && pc < pieces ? km_load_nt16(src) : make_uint4(0u, 0u, 0u, 0u);
+      else
+        buf[i] = li < lg.n && pc < pieces ? *reinterpret_cast<const uint4*>(src)
+                                          : make_uint4(0u, 0u, 0u, 0u);
     }
   };
   double acc = 0.0;
   int32_t iacc = 0;
-  uint4 buf[kKmScoreAhead][kKmScoreLanes];
+  uint4 buf[kAhead][kLanes];
 #pragma unroll
-  for (int j = 0; j < kKmScoreAhead; ++j)
+  for (int j = 0; j < kAhead; ++j)
     if (j < steps) load(j, buf[j]);
-  for (int64_t t0 = 0; t0 < steps; t0 += kKmScoreAhead) {
+  for (int64_t t0 = 0; t0 < steps; t0 += kAhead) {
 #pragma unroll
-    for (int j = 0; j < kKmScoreAhead; ++j) {
+    for (int j = 0; j < kAhead; ++j) {
       const int64_t t = t0 + j;
       if (t >= steps) break;
       const int64_t g = g_lo + t / nslices;
@@ -820,16 +826,16 @@ __global__ __launch_bounds__(kKmScoreThreads) __attribute__((amdgpu_waves_per_eu
       const KmGroup gr = ring[g & (kKmRing - 1)];
       if (sl == 0 && gr.b != qrow) stage_query(gr.b);
 #pragma unroll
-      for (int i = 0; i < kKmScoreLanes; ++i)
-        *reinterpret_cast<uint4*>(stg + (lr + rows_per_load * i) * kKmScoreStride + lp * 16) = buf[j][i];
+      for (int i = 0; i < kLanes; ++i)
+        *reinterpret_cast<uint4*>(stg + (lr + rows_per_load * i) * kStride + lp * 16) = buf[j][i];
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      if (t + kKmScoreAhead < steps) load(t + kKmScoreAhead, buf[j]);
+      if (t + kAhead < steps) load(t + kAhead, buf[j]);
       if (lane < gr.n) {
 #pragma unroll
         for (int q = 0; q < per_slice; ++q) {
           const int pc = sl * per_slice + q;
           if (pc < pieces) {
-            const uint4 v = *reinterpret_cast<const uint4*>(stg + lane * kKmScoreStride + q * 16);
+            const uint4 v = *reinterpret_cast<const uint4*>(stg + lane * kStride + q * 16);
             acc_piece<DT>(v, qd, qi, pc * elems, acc, iacc);
           }
         }
@@ -921,7 +927,11 @@ void kmean_run(const int64_t* cluster_offsets, int64_t num_offsets, const int64_
                        dim3(kKmCountThreads), 0, s, a, counts, items);
   }
   const int64_t pairs = batch * probes;
-  const int score_lds = (kKmScoreThreads / 64) * km_score_wave_lds(static_cast<int>(dim), emb_dtype == kKmI8);
+  // 128-byte slices when their tile leaves room for the query, else 64-byte
+  const int waves = kKmScoreThreads / 64;
+  const bool i8 = emb_dtype == kKmI8;
+  const int slice = waves * km_score_wave_lds(static_cast<int>(dim), i8, 128) <= kKmWaveMaxLds ? 128 : 64;
+  const int score_lds = waves * km_score_wave_lds(static_cast<int>(dim), i8, slice);
   if (probes > 0 && pairs >= kKmBalancedPairs && batch <= kKmBalancedMaxRows &&
       score_lds <= kKmWaveMaxLds &&
       (counts_capacity < 0 || pairs + km_balanced_extra(batch) <= counts_capacity)) {
@@ -940,16 +950,23 @@ void kmean_run(const int64_t* cluster_offsets, int64_t num_offsets, const int64_
     // kKmScorePerCu, every one resident
     const int per_cu = std::max(1, std::min(kKmScorePerCu, kCuLdsBytes / score_lds));
     const dim3 sgrid(static_cast<unsigned>(per_cu * cu_count())), sblock(kKmScoreThreads);
-    switch (emb_dtype) {
-      case kKmF32: hipLaunchKernelGGL((kmean_score_kernel<kKmF32, kKmF32>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch); break;
-      case kKmF16: hipLaunchKernelGGL((kmean_score_kernel<kKmF16, kKmF16>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch); break;
-      case kKmBF16: hipLaunchKernelGGL((kmean_score_kernel<kKmBF16, kKmBF16>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch); break;
-      default:
-        if (st == kKmI32)
-          hipLaunchKernelGGL((kmean_score_kernel<kKmI8, kKmI32>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch);
-        else
-          hipLaunchKernelGGL((kmean_score_kernel<kKmI8, kKmF16>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch);
-    }
+    auto score = [&](auto sl) {
+      constexpr int SL = decltype(sl)::value;
+      switch (emb_dtype) {
+        case kKmF32: hipLaunchKernelGGL((kmean_score_kernel<kKmF32, kKmF32, SL>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch); break;
+        case kKmF16: hipLaunchKernelGGL((kmean_score_kernel<kKmF16, kKmF16, SL>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch); break;
+        case kKmBF16: hipLaunchKernelGGL((kmean_score_kernel<kKmBF16, kKmBF16, SL>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch); break;
+        default:
+          if (st == kKmI32)
+            hipLaunchKernelGGL((kmean_score_kernel<kKmI8, kKmI32, SL>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch);
+          else
+            hipLaunchKernelGGL((kmean_score_kernel<kKmI8, kKmF16, SL>), sgrid, sblock, score_lds, s, a, gstart, rowtot, batch);
+      }
+    };
+    if (slice == 128)
+      score(std::integral_constant<int, 128>{});
+    else
+      score(std::integral_constant<int, 64>{});
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
       throw Error(ST_ERR_HIP, cat("fused_kmean_ann launch failed: ", hipGetErrorString(e)));
