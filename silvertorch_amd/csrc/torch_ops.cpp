@@ -453,7 +453,8 @@ std::tuple<Tensor, Tensor, Tensor> column_info(const Tensor& offsets_in,
 
 struct PartialPlan {
   PlanHolder plan;
-  Tensor blob;  // device copy of the (unbound) plan blob
+  Tensor blob;  // device copy of the (unbound) plan blob; undefined when
+                // each chunk's block carries it (the single-chunk op)
 };
 
 void check_partial_args(const Tensor& bloom_index, const Tensor& offsets, const Tensor& lengths,
@@ -483,7 +484,7 @@ void check_partial_args(const Tensor& bloom_index, const Tensor& offsets, const 
 }
 
 void prepare_partial_plan(PartialPlan& pp, const Tensor& plans_data, const Tensor& plans_offsets,
-                          int64_t k, int64_t hash_k, at::Device dev) {
+                          int64_t k, int64_t hash_k, at::Device dev, bool upload) {
   TORCH_CHECK(plans_data.scalar_type() == at::kChar || plans_data.scalar_type() == at::kByte,
               "bloom_query_plans_data must be int8");
   TORCH_CHECK(plans_offsets.scalar_type() == at::kLong, "bloom_query_plans_offsets must be int64");
@@ -492,6 +493,7 @@ void prepare_partial_plan(PartialPlan& pp, const Tensor& plans_data, const Tenso
   check_st(st_search_plan_create(reinterpret_cast<const int8_t*>(pd.data_ptr()), pd.numel(),
                                  po.data_ptr<int64_t>(), po.numel(), k, hash_k, &pp.plan.p),
            "bloom_index_search_batch_return_partial_response");
+  if (!upload) return;
   const int64_t n = st_search_plan_blob_bytes(pp.plan.p);
   Tensor host = at::empty({std::max<int64_t>(n, 1)}, at::TensorOptions().dtype(at::kByte).pinned_memory(true));
   if (n) std::memcpy(host.data_ptr(), st_search_plan_blob(pp.plan.p), n);
@@ -540,29 +542,35 @@ std::tuple<Tensor, Tensor, Tensor> partial_chunk(const PartialPlan& pp, const Te
   const Tensor& cl = host.cl;
   const Tensor& pi = host.pi;
   const int64_t rows = co.size(0), clusters = co.size(1), n = rows * clusters;
-  // the work items, the column cumsum and the first bits in one pinned block
-  // and one copy to the device; the returned cumsum and first are views of
-  // the device block (one copy and allocation per call instead of three)
+  // the work items, the column cumsum and the first bits (and the plan blob
+  // when no device copy of it is shared) in one pinned block and one copy
+  // to the device; the returned cumsum and first are views of the device
+  // block (one copy and allocation per call instead of four)
+  const int64_t blob_bytes = pp.blob.defined() ? 0 : (st_search_plan_blob_bytes(pp.plan.p) + 15) / 16 * 16;
+  const int64_t off_items = blob_bytes;
   const int64_t items_bytes =
       (std::max<int64_t>(n, 1) * static_cast<int64_t>(sizeof(st_partial_item)) + 15) / 16 * 16;
-  const int64_t off_cumsum = items_bytes, off_first = items_bytes + (4 * n + 15) / 16 * 16;
+  const int64_t off_cumsum = off_items + items_bytes, off_first = off_cumsum + (4 * n + 15) / 16 * 16;
   const int64_t block_bytes = off_first + std::max<int64_t>(n, 1);
   Tensor host_block = at::empty({block_bytes}, at::TensorOptions().dtype(at::kByte).pinned_memory(true));
   uint8_t* hb = host_block.data_ptr<uint8_t>();
+  if (blob_bytes) std::memcpy(hb, st_search_plan_blob(pp.plan.p), st_search_plan_blob_bytes(pp.plan.p));
   int64_t num_items = 0, total = 0;
   check_st(st_search_plan_partial_items(pp.plan.p, co.data_ptr<int64_t>(), cl.data_ptr<int64_t>(), rows,
                                         clusters, pi.defined() ? pi.data_ptr<int64_t>() : nullptr,
                                         bbo.numel() - 1, reinterpret_cast<int32_t*>(hb + off_cumsum),
                                         reinterpret_cast<int8_t*>(hb + off_first),
-                                        reinterpret_cast<st_partial_item*>(hb), &num_items, &total),
+                                        reinterpret_cast<st_partial_item*>(hb + off_items), &num_items,
+                                        &total),
            "bloom_index_search_batch_return_partial_response");
   const Tensor block = host_block.to(dev, /*non_blocking=*/true);
   Tensor mask = at::empty({total}, at::TensorOptions().dtype(at::kLong).device(dev));
   if (num_items > 0) {
     check_st(st_bloom_index_search_partial(index.data_ptr<int64_t>(), index.numel(),
                                            bbo.data_ptr<int64_t>(), bbo.numel() - 1, pp.plan.p,
-                                           pp.blob.data_ptr(),
-                                           reinterpret_cast<const st_partial_item*>(block.data_ptr()),
+                                           pp.blob.defined() ? pp.blob.data_ptr() : block.data_ptr(),
+                                           reinterpret_cast<const st_partial_item*>(
+                                               block.data_ptr<uint8_t>() + off_items),
                                            num_items, mask.data_ptr<int64_t>(), current_stream(index)),
              "bloom_index_search_batch_return_partial_response");
   }
@@ -585,7 +593,8 @@ std::tuple<Tensor, Tensor, Tensor> partial_gpu(const Tensor& bloom_index, const 
   bool pending = false;
   const PartialHost host = partial_host(offsets, lengths, query_plan_index, pending);
   PartialPlan pp;
-  prepare_partial_plan(pp, plans_data, plans_offsets, k, hash_k, bloom_index.device());
+  prepare_partial_plan(pp, plans_data, plans_offsets, k, hash_k, bloom_index.device(),
+                       /*upload=*/false);
   if (pending) sync_current_stream(bloom_index.device());
   return partial_chunk(pp, bloom_index, bbo, host);
 }
@@ -630,7 +639,7 @@ std::tuple<std::vector<Tensor>, std::vector<Tensor>, std::vector<Tensor>> partia
   std::vector<PartialHost> hosts;
   for (size_t i = 0; i < n; ++i) hosts.push_back(partial_host(offsets[i], lengths[i], query_plan_index, pending));
   PartialPlan pp;
-  prepare_partial_plan(pp, plans_data, plans_offsets, k, hash_k, dev);
+  prepare_partial_plan(pp, plans_data, plans_offsets, k, hash_k, dev, /*upload=*/true);
   if (pending) sync_current_stream(dev);
   std::vector<Tensor> cs, fs, ms;
   for (size_t i = 0; i < n; ++i) {
