@@ -33,7 +33,7 @@
  *               returned column equals the full search's word there.
  *   compact     numpy nonzero on the unpacked mask.
  *   topk        brute-force numpy sort on tiny inputs.
- * Defined where the reference is undefined (documented in DESIGN.md):
+ * Defined where the reference is undefined (the HIP kernels do the same):
  *   a search term in a bundle of width 0 matches nothing (reference divides
  *   by zero); a row index that falls outside the index reads as zero.
  */
