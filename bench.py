@@ -143,9 +143,11 @@ def probe_pattern():
            "index_bytes": index_bytes, "output_bytes": out_bytes, "hbm_peak_gbs": HBM_PEAK_GBS, "runs": []}
     modes = {0: ("loads and stores", index_bytes + out_bytes), 1: ("loads only", index_bytes),
              2: ("stores only", out_bytes), 3: ("the index read as one stream", index_bytes),
-             4: ("the output written as one stream", out_bytes)}
+             4: ("the output written as one stream", out_bytes),
+             5: ("loads and stores, each wave's reads before its stores", index_bytes + out_bytes),
+             6: ("loads and stores, flat bundle walk (pattern_flat_kernel)", index_bytes + out_bytes)}
     # bundles per group (contiguous bytes per query row / 256) and the modes timed
-    for grp, grp_modes in ((1, (0, 1, 2, 3, 4)), (2, (0, 2)), (4, (0, 2))):
+    for grp, grp_modes in ((1, (0, 1, 2, 3, 4, 5, 6)), (2, (0, 2)), (4, (0, 2))):
         for mode in grp_modes:
             name, nbytes = modes[mode]
 
@@ -155,12 +157,13 @@ def probe_pattern():
                 if rc != 0:
                     raise RuntimeError(P.st_probe_last_error().decode())
             us = run(fn)
-            res["runs"].append({"kernel": "pattern_probe_kernel" if mode < 3 else
-                                ("stream_read_kernel" if mode == 3 else "stream_write_kernel"),
+            res["runs"].append({"kernel": "pattern_probe_kernel" if mode in (0, 1, 2, 5) else
+                                ("pattern_flat_kernel" if mode == 6 else
+                                 "stream_read_kernel" if mode == 3 else "stream_write_kernel"),
                                 "bundles_per_group": grp, "bytes_per_query_row_run": 256 * grp, "mode": name,
                                 "mean_us": us, "bytes": nbytes, "gbs": nbytes / us / 1e3,
                                 "frac": nbytes / us / 1e3 / HBM_PEAK_GBS})
-            if mode < 3:
+            if mode in (0, 1, 2, 5, 6):
                 log(f"probe: {256 * grp}-byte runs per query row, {name}: {us:.1f} us, {nbytes / us / 1e3:.0f} GB/s")
             else:
                 log(f"probe: {name}: {us:.1f} us, {nbytes / us / 1e3:.0f} GB/s")

@@ -15,7 +15,8 @@
 // store pattern (four query rows per wave instruction); RUN 2 and 4 measure
 // whether longer runs per query row raise the write rate.  MODE 1 drops the
 // stores (a 16-byte sink per workgroup keeps the loads live), MODE 2 the
-// loads.  Two streaming kernels give the part's contiguous read and write
+// loads; MODE 5 (RUN 1) issues each wave's four tile reads before its four
+// stores instead of reading and storing one query row at a time.  Two streaming kernels give the part's contiguous read and write
 // rates for comparison.
 #include <hip/hip_runtime.h>
 
@@ -106,6 +107,26 @@ __global__ __launch_bounds__(kThreads) void pattern_probe_kernel(
     if (t % RUN != RUN - 1 && ahead >= 0) continue;
     const int64_t first = bnd - t % RUN;  // the group's first bundle
     const int64_t run_bytes = (bnd - first + 1) * 256;
+    if constexpr (MODE == 5) {
+      // each wave's tile reads for four query rows first, then their four
+      // stores back to back
+      for (int64_t q0 = wave * kRowsPerInsn; q0 < Q; q0 += 64 * kRowsPerInsn) {
+        u32x4 val[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t q = q0 + 16 * kRowsPerInsn * j + lane / kLanesPerRow;
+          val[j] = tile[(static_cast<int>(q % Q) * 16 + (lane & 15)) % (rows * 16)];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t q = q0 + 16 * kRowsPerInsn * j + lane / kLanesPerRow;
+          const int64_t off = static_cast<int64_t>(lane % kLanesPerRow) * 16;
+          if (q >= Q || off >= run_bytes) continue;
+          __builtin_nontemporal_store(val[j], (PROBE_GLOBAL u32x4*)(out + q * row_bytes + first * 256 + off));
+        }
+      }
+      continue;
+    }
     for (int64_t q0 = wave * kRowsPerInsn; q0 < Q; q0 += 16 * kRowsPerInsn) {
       const int64_t q = q0 + lane / kLanesPerRow;
       const int64_t off = static_cast<int64_t>(lane % kLanesPerRow) * 16;
@@ -116,6 +137,61 @@ __global__ __launch_bounds__(kThreads) void pattern_probe_kernel(
     }
   }
   if (MODE == 1) sink[blockIdx.x * kThreads + tid] = acc;
+}
+
+// The same loads and stores (RUN 1) from a flatter loop: the workgroup walks
+// bundles blockIdx.x, + grid, ... directly, reads its four tile values per
+// lane, then stores them in one loop (MODE 6 of st_probe_search_pattern).
+__global__ __launch_bounds__(kThreads) void pattern_flat_kernel(
+    const int64_t* __restrict__ index, int64_t numel, const int64_t* __restrict__ bbo,
+    int64_t nb, int64_t Q, char* __restrict__ out) {
+  __shared__ u32x4 tile[(kTileRows + 2) * 16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const u32x4* src = reinterpret_cast<const u32x4*>(index);
+  auto extent = [&](int64_t bnd, int64_t& s, int64_t& b) {
+    s = bbo[bnd];
+    b = bbo[bnd + 1] - s;
+    if (b < 0) b = 0;
+    if (b > kTileRows) b = kTileRows;
+  };
+  u32x4 pre[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) pre[i] = u32x4{1, 2, 3, 4};
+  int64_t bnd = blockIdx.x;
+  if (bnd < nb) {
+    int64_t s, b;
+    extent(bnd, s, b);
+    load_tile(src, s, b, numel, pre);
+  }
+  const int64_t row_bytes = nb * 256;
+  for (; bnd < nb; bnd += gridDim.x) {
+    int64_t s, b;
+    extent(bnd, s, b);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = tid + i * kThreads;
+      if (c < b * 16) tile[c] = pre[i];
+    }
+    const int64_t nx = bnd + gridDim.x;
+    if (nx < nb) {
+      int64_t s2, b2;
+      extent(nx, s2, b2);
+      load_tile(src, s2, b2, numel, pre);
+    }
+    __syncthreads();
+    const int rows = static_cast<int>(b > 0 ? b : 1);
+    u32x4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      v[j] = tile[(static_cast<int>(wave * 4 + 64 * j + lane / 16) * 16 + (lane & 15)) % (rows * 16)];
+    int j = 0;
+    for (int64_t q0 = wave * 4; q0 < Q; q0 += 64, ++j) {
+      const int64_t q = q0 + lane / 16;
+      if (q < Q)
+        __builtin_nontemporal_store(v[j & 3], (PROBE_GLOBAL u32x4*)(out + q * row_bytes + bnd * 256 + (lane & 15) * 16));
+    }
+  }
 }
 
 // Reference points of the part: the index read as one contiguous stream
@@ -167,7 +243,7 @@ extern "C" int st_probe_search_pattern(const int64_t* index, int64_t numel,
                                        int mode, int grid, void* stream) {
   if (index == nullptr || bundle_b_offsets == nullptr || out == nullptr || sink == nullptr ||
       num_bundles <= 0 || num_queries <= 0 || grid <= 0 || (run != 1 && run != 2 && run != 4) ||
-      mode < 0 || mode > 4) {
+      mode < 0 || mode > 6 || (mode >= 5 && run != 1) || (mode == 6 && num_queries > 256)) {
     g_error = "st_probe_search_pattern: invalid arguments";
     return -1;
   }
@@ -180,8 +256,22 @@ extern "C" int st_probe_search_pattern(const int64_t* index, int64_t numel,
     hipLaunchKernelGGL(stream_write_kernel, dim3(grid), dim3(kThreads), 0, s,
                        static_cast<u32x4*>(out), num_queries * num_bundles * 16);
   }
-  if (mode >= 3) {
+  if (mode == 3 || mode == 4) {
     e = hipGetLastError();
+    if (e != hipSuccess) {
+      g_error = std::string("st_probe_search_pattern: ") + hipGetErrorString(e);
+      return -1;
+    }
+    return 0;
+  }
+  if (mode == 5 || mode == 6) {
+    if (mode == 5)
+      e = launch<1, 5>(index, numel, bundle_b_offsets, num_bundles, num_queries, out, sink, grid, s);
+    else {
+      hipLaunchKernelGGL(pattern_flat_kernel, dim3(grid), dim3(kThreads), 0, s, index, numel,
+                         bundle_b_offsets, num_bundles, num_queries, static_cast<char*>(out));
+      e = hipGetLastError();
+    }
     if (e != hipSuccess) {
       g_error = std::string("st_probe_search_pattern: ") + hipGetErrorString(e);
       return -1;
